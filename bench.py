@@ -1,0 +1,226 @@
+"""Benchmark of the DSALT sparse-attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c1|c4]
+
+A step is one HARD DSALT attention forward (the fused HIP kernel) over the packed batch
+of BASELINE.json config 2 (default): 4 x 2048 tokens, 16 heads x 64 head_dim,
+n_min 32, n_max 512, k_lmk 64, with q/k/v, windows and landmarks produced by a
+DSALTAttention module at random init (seed 1) from x ~ N(0, 1) [4, 2048, 1024].
+Inputs are resident in HBM before the timed region. Prints one JSON line.
+
+`roofline.achieved` counts only the FLOPs the sparse pattern needs: 4 * D * P, where
+P is the exact number of (query, key) pairs (band + admitted landmarks) counted on the
+host from the actual windows and landmarks. `cpu_baseline` times the reference's CPU
+fallback cost model (dense mask + fp32 SDPA, restated in oracle/) on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "dsalt-library_amd"))
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
+
+CONFIGS = {
+    # name: (batch, seq_len, d_model, heads, n_min, n_max, k_lmk, seed)
+    "c1": (1, 1024, 512, 8, 64, 256, 16, 0),
+    "c2": (4, 2048, 1024, 16, 32, 512, 64, 1),
+    "c4": (1, 16384, 2048, 16, 64, 1024, 128, 3),
+}
+
+
+def effective_pairs_hard(w: np.ndarray, lmk_pos: np.ndarray, cu: list[int]) -> int:
+    """Exact (query, key) pairs of the HARD pattern summed over heads: per query
+    min(w, i + 1) band keys plus the landmark slots p with 0 <= p <= i - w."""
+    H = lmk_pos.shape[0]
+    total = 0
+    for s in range(len(cu) - 1):
+        a, b = cu[s], cu[s + 1]
+        L = b - a
+        if L == 0:
+            continue
+        i = np.arange(L)
+        ws = w[a:b]
+        wi = np.where(ws >= 1, np.trunc(np.minimum(np.nan_to_num(ws, nan=1.0), 2 ** 30)), 1).astype(np.int64)
+        total += int(np.minimum(wi, i + 1).sum()) * H
+        pmax = np.sort(i - wi)  # landmark p admitted by query i iff p <= i - w(i)
+        for h in range(H):
+            p = lmk_pos[h, s]
+            p = p[(p >= 0) & (p < L)]
+            # number of queries admitting each p = #{i : i - w(i) >= p}
+            total += int((L - np.searchsorted(pmax, p, side="left")).sum())
+    return total
+
+
+def make_workload(cfg: str, device: torch.device):
+    from dsalt import _hip
+    from dsalt.modules import DSALTAttention
+    from dsalt.kernels.window_utils import apply_rotary_emb
+
+    B, L, d_model, H, n_min, n_max, k_lmk, seed = CONFIGS[cfg]
+    torch.manual_seed(seed)
+    mod = DSALTAttention(d_model, H, n_min, n_max, k_lmk, max_seq_len=L)
+    x = torch.randn(B, L, d_model)
+    mod = mod.to(device).eval()
+    T = B * L
+    xp = x.reshape(T, d_model).to(device)
+    cu = torch.arange(0, T + 1, L, dtype=torch.int32, device=device)
+    with torch.no_grad():
+        D = d_model // H
+        q = mod.q_proj(xp).view(T, H, D)
+        k = mod.k_proj(xp).view(T, H, D)
+        v = mod.v_proj(xp).view(T, H, D)
+        pos_ids = torch.arange(T, device=device) % L
+        cos, sin = mod.rope_cos[pos_ids].unsqueeze(1), mod.rope_sin[pos_ids].unsqueeze(1)
+        q, k = apply_rotary_emb(q, k, cos, sin)
+        q, k, v = (t.to(torch.bfloat16).contiguous() for t in (q, k, v))
+        w = mod._window_sizes(xp, floor=True)
+        from dsalt.kernels.selectors import _compute_landmark_indices
+        lmk, _, _ = _compute_landmark_indices(xp, mod.v_proj.weight, mod._alpha().float(), w, cu, k_lmk,
+                                              n_min, T, cu.tolist(), head_dim=D)
+    torch.cuda.synchronize()
+    return dict(q=q, k=k, v=v, w=w, lmk=lmk, cu=cu, T=T, H=H, D=D, B=B, L=L, k_lmk=k_lmk,
+                n_min=n_min, n_max=n_max, xp=xp, mod=mod)
+
+
+def time_launches(fn, steps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_baseline(wl, budget_s: float = 12.0):
+    """The reference's CPU fallback cost (dense HARD mask + fp32 SDPA), restated in
+    oracle/, timed on this host on one sequence of the workload (all heads)."""
+    from oracle import dsalt_oracle as orc
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    L = wl["L"]
+    q32, k32, v32 = (wl[n][:L].float().cpu() for n in ("q", "k", "v"))
+    w = wl["w"][:L].float().cpu().numpy()
+    pos = wl["lmk"][:, :1].cpu().numpy()
+    cu = [0, L]
+    orc.cpu_baseline_hard(q32, k32, v32, w, pos, cu)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        orc.cpu_baseline_hard(q32, k32, v32, w, pos, cu)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 20:
+            break
+    return {"value": reps * L / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} x 1 sequence of {L} tokens, {wl['H']} heads (dense mask + fp32 SDPA)"}
+
+
+def load_traffic(cfg: str):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE, if recorded."""
+    path = os.path.join(ROOT, "profiles", f"fwd_{cfg}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f)
+    return rec.get("hbm_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from dsalt import _hip
+
+    dev = torch.device("cuda", 0)
+    wl = make_workload(args.config, dev)
+    q, k, v, w, lmk, cu = wl["q"], wl["k"], wl["v"], wl["w"], wl["lmk"], wl["cu"]
+    T, H, D = wl["T"], wl["H"], wl["D"]
+    out = torch.empty_like(q)
+    lse = torch.empty((T, H), device=dev, dtype=torch.float32)
+    scale = 1.0 / math.sqrt(D)
+
+    def step():
+        _hip.fwd(_hip.MODE_HARD, q, k, v, w, lmk, None, cu, scale, out=out, lse=lse)
+
+    ms = time_launches(step, args.steps, args.warmup)
+
+    # selection + quantisation (the rest of the inference hot path), reported alongside
+    from dsalt.kernels.landmark_tokens_ker import hybrid_scores_per_head
+    with torch.no_grad():
+        mod = wl["mod"]
+        scores, _, _ = hybrid_scores_per_head(wl["xp"], mod.v_proj.weight, mod._alpha().float(), H, D)
+        w_cont = mod._window_continuous(wl["xp"]).float()
+    sel_ms = time_launches(lambda: _hip.select_landmarks(scores, w, cu, wl["k_lmk"]), 20, 3)
+    qz_ms = time_launches(lambda: _hip.quantize_windows(w_cont), 20, 3)
+
+    P = effective_pairs_hard(w.float().cpu().numpy(), lmk.cpu().numpy(), cu.cpu().tolist())
+    flops = 4.0 * D * P
+    bytes_alg = 2 * T * H * D * 4 + 4 * T * H + 4 * T + 8 * H * wl["B"] * wl["k_lmk"]
+    t_s = ms * 1e-3
+    tflops = flops / t_s / 1e12
+    traffic = load_traffic(args.config)
+
+    res = {
+        "metric": "DSALT attn fwd tokens/s & % bf16 MFMA peak (16h×64d, seq 2048)",
+        "value": T / t_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (DSALTAttention random init, x ~ N(0,1))",
+        "config": {
+            "workload": f"{args.config}: HARD DSALT attention forward, packed {wl['B']}x{wl['L']} tokens, "
+                        f"{H} heads x {D} head_dim, n_min {wl['n_min']}, n_max {wl['n_max']}, k_lmk {wl['k_lmk']}",
+            "tokens": T, "heads": H, "head_dim": D, "seqs": wl["B"], "seq_len": wl["L"],
+            "k_lmk": wl["k_lmk"], "pairs": P, "keys_per_query": P / (T * H),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": tflops,
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": tflops / MFMA_BF16_PEAK_TFLOPS,
+            "traffic": traffic,
+            "hbm_algorithmic_GBs": bytes_alg / t_s / 1e9,
+            "hbm_frac": bytes_alg / t_s / 1e9 / HBM_PEAK_GBS,
+        },
+        "select_ms": sel_ms,
+        "quantize_ms": qz_ms,
+        "path_ms": ms + sel_ms + qz_ms,
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(wl)
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,166 @@
+// extern "C" entry points of libdsalt_hip.so: host-side argument validation, error
+// reporting and dispatch to the kernel launchers. Declared in include/dsalt_hip.h.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Shared checks of a packed [T, H, D] 16-bit tensor read/written with 16-byte
+// (or `vec_elems`-element) vector accesses along D.
+int check_tensor(const char *name, const void *p, int64_t st, int64_t sh, int vec_elems) {
+    if (!p) return fail(DSALT_ERR_INVALID, "%s is NULL", name);
+    if (!aligned(p, vec_elems * 2))
+        return fail(DSALT_ERR_INVALID, "%s must be %d-byte aligned", name, vec_elems * 2);
+    if (st < 0 || sh < 0 || st % vec_elems || sh % vec_elems)
+        return fail(DSALT_ERR_INVALID, "%s strides (t=%lld, h=%lld) must be non-negative multiples of %d",
+                    name, (long long)st, (long long)sh, vec_elems);
+    return DSALT_OK;
+}
+
+int check_common(int mode, int dtype, int T, int S, int H, int D, int k, const int32_t *cu,
+                 const float *w, const int64_t *lmk_pos) {
+    if (mode != DSALT_MODE_HARD && mode != DSALT_MODE_SOFT)
+        return fail(DSALT_ERR_INVALID, "mode must be DSALT_MODE_HARD or DSALT_MODE_SOFT (got %d)", mode);
+    if (dtype != DSALT_DTYPE_BF16 && dtype != DSALT_DTYPE_F16)
+        return fail(DSALT_ERR_INVALID, "dtype must be DSALT_DTYPE_BF16 or DSALT_DTYPE_F16 (got %d)", dtype);
+    if (T < 0) return fail(DSALT_ERR_INVALID, "total_len must be >= 0 (got %d)", T);
+    if (S < 1) return fail(DSALT_ERR_INVALID, "num_seqs must be >= 1 (got %d)", S);
+    if (H < 1) return fail(DSALT_ERR_INVALID, "n_heads must be >= 1 (got %d)", H);
+    if (D != 64 && D != 128)
+        return fail(DSALT_ERR_UNSUPPORTED, "head_dim must be 64 or 128 (got %d)", D);
+    if (k < 0 || k > DSALT_MAX_K_LMK)
+        return fail(DSALT_ERR_UNSUPPORTED, "k_lmk must be in [0, %d] (got %d)", DSALT_MAX_K_LMK, k);
+    if (!cu) return fail(DSALT_ERR_INVALID, "cu_seqlens is NULL");
+    if (!w) return fail(DSALT_ERR_INVALID, "w (window sizes) is NULL");
+    if (k > 0 && !lmk_pos) return fail(DSALT_ERR_INVALID, "lmk_pos is NULL while k_lmk = %d", k);
+    const int64_t blocks = (int64_t)dsalt::block_upper_bound(T, S, dsalt::kFwdBM) * H;
+    if (blocks > (int64_t)INT32_MAX / 2)
+        return fail(DSALT_ERR_UNSUPPORTED, "problem too large: %lld query blocks", (long long)blocks);
+    return DSALT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsalt_abi_version(void) { return DSALT_ABI_VERSION; }
+const char *dsalt_last_error(void) { return g_err; }
+size_t dsalt_fwd_args_size(void) { return sizeof(dsalt_fwd_args); }
+size_t dsalt_bwd_args_size(void) { return sizeof(dsalt_bwd_args); }
+size_t dsalt_select_args_size(void) { return sizeof(dsalt_select_args); }
+
+int dsalt_fwd_check(const dsalt_fwd_args *a) {
+    if (!a) return fail(DSALT_ERR_INVALID, "args is NULL");
+    int rc = check_common(a->mode, a->dtype, a->total_len, a->num_seqs, a->n_heads, a->head_dim,
+                          a->k_lmk, a->cu_seqlens, a->w, a->lmk_pos);
+    if (rc) return rc;
+    if ((rc = check_tensor("q", a->q, a->q_stride_t, a->q_stride_h, 8))) return rc;
+    if ((rc = check_tensor("k", a->k, a->k_stride_t, a->k_stride_h, 8))) return rc;
+    if ((rc = check_tensor("v", a->v, a->v_stride_t, a->v_stride_h, 8))) return rc;
+    if ((rc = check_tensor("out", a->out, a->out_stride_t, a->out_stride_h, 4))) return rc;
+    if (!a->lse) return fail(DSALT_ERR_INVALID, "lse is NULL");
+    if (a->mode == DSALT_MODE_SOFT && !(a->tau_win > 0.f))
+        return fail(DSALT_ERR_INVALID, "tau_win must be > 0 (got %g)", (double)a->tau_win);
+    if (!(a->scale == a->scale)) return fail(DSALT_ERR_INVALID, "scale is NaN");
+    return DSALT_OK;
+}
+
+int dsalt_fwd(const dsalt_fwd_args *a, void *stream) {
+    int rc = dsalt_fwd_check(a);
+    if (rc) return rc;
+    hipError_t e = dsalt::launch_fwd(*a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(DSALT_ERR_LAUNCH, "dsalt_fwd launch failed: %s", hipGetErrorString(e));
+    return DSALT_OK;
+}
+
+int dsalt_select_check(const dsalt_select_args *a) {
+    if (!a) return fail(DSALT_ERR_INVALID, "args is NULL");
+    if (a->total_len < 0) return fail(DSALT_ERR_INVALID, "total_len must be >= 0");
+    if (a->num_seqs < 1) return fail(DSALT_ERR_INVALID, "num_seqs must be >= 1");
+    if (a->n_heads < 1) return fail(DSALT_ERR_INVALID, "n_heads must be >= 1");
+    if (a->k_lmk < 0 || a->k_lmk > DSALT_MAX_K_LMK)
+        return fail(DSALT_ERR_UNSUPPORTED, "k_lmk must be in [0, %d] (got %d)", DSALT_MAX_K_LMK, a->k_lmk);
+    if (!a->scores || !a->w || !a->cu_seqlens || (!a->lmk_pos && a->k_lmk > 0))
+        return fail(DSALT_ERR_INVALID, "scores, w, cu_seqlens and lmk_pos must be non-NULL");
+    if ((int64_t)a->num_seqs * a->n_heads > (int64_t)INT32_MAX)
+        return fail(DSALT_ERR_UNSUPPORTED, "too many (head, sequence) pairs");
+    return DSALT_OK;
+}
+
+int dsalt_select_landmarks(const dsalt_select_args *a, void *stream) {
+    int rc = dsalt_select_check(a);
+    if (rc) return rc;
+    hipError_t e = dsalt::launch_select(*a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess)
+        return fail(DSALT_ERR_LAUNCH, "dsalt_select_landmarks launch failed: %s", hipGetErrorString(e));
+    return DSALT_OK;
+}
+
+int dsalt_quantize_windows(const float *w_cont, int64_t n, float *w_out, int32_t *w_int_out,
+                           void *stream) {
+    if (n < 0) return fail(DSALT_ERR_INVALID, "n must be >= 0");
+    if (n > 0 && !w_cont) return fail(DSALT_ERR_INVALID, "w_cont is NULL");
+    hipError_t e = dsalt::launch_quantize(w_cont, n, w_out, w_int_out, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess)
+        return fail(DSALT_ERR_LAUNCH, "dsalt_quantize_windows launch failed: %s", hipGetErrorString(e));
+    return DSALT_OK;
+}
+
+int64_t dsalt_bwd_workspace_size(int32_t total_len, int32_t num_seqs, int32_t n_heads,
+                                 int32_t head_dim, int32_t k_lmk) {
+    if (total_len < 0 || num_seqs < 1 || n_heads < 1 || k_lmk < 0) return -1;
+    return dsalt::bwd_workspace_bytes(total_len, num_seqs, n_heads, head_dim, k_lmk);
+}
+
+int dsalt_bwd_check(const dsalt_bwd_args *a) {
+    if (!a) return fail(DSALT_ERR_INVALID, "args is NULL");
+    int rc = check_common(a->mode, a->dtype, a->total_len, a->num_seqs, a->n_heads, a->head_dim,
+                          a->k_lmk, a->cu_seqlens, a->w, a->lmk_pos);
+    if (rc) return rc;
+    if ((rc = check_tensor("q", a->q, a->q_stride_t, a->q_stride_h, 8))) return rc;
+    if ((rc = check_tensor("k", a->k, a->k_stride_t, a->k_stride_h, 8))) return rc;
+    if ((rc = check_tensor("v", a->v, a->v_stride_t, a->v_stride_h, 8))) return rc;
+    if ((rc = check_tensor("out", a->out, a->out_stride_t, a->out_stride_h, 8))) return rc;
+    if ((rc = check_tensor("dout", a->dout, a->dout_stride_t, a->dout_stride_h, 8))) return rc;
+    if ((rc = check_tensor("dq", a->dq, a->dq_stride_t, a->dq_stride_h, 4))) return rc;
+    if ((rc = check_tensor("dk", a->dk, a->dk_stride_t, a->dk_stride_h, 4))) return rc;
+    if ((rc = check_tensor("dv", a->dv, a->dv_stride_t, a->dv_stride_h, 4))) return rc;
+    if (!a->lse) return fail(DSALT_ERR_INVALID, "lse is NULL");
+    if (a->mode == DSALT_MODE_SOFT && !(a->tau_win > 0.f))
+        return fail(DSALT_ERR_INVALID, "tau_win must be > 0 (got %g)", (double)a->tau_win);
+    const int64_t need = dsalt::bwd_workspace_bytes(a->total_len, a->num_seqs, a->n_heads, a->head_dim,
+                                                    a->k_lmk);
+    if (need > 0) {
+        if (!a->workspace) return fail(DSALT_ERR_INVALID, "workspace is NULL (%lld bytes needed)", (long long)need);
+        if (a->workspace_bytes < need)
+            return fail(DSALT_ERR_INVALID, "workspace too small: %lld < %lld bytes",
+                        (long long)a->workspace_bytes, (long long)need);
+        if (!aligned(a->workspace, 256)) return fail(DSALT_ERR_INVALID, "workspace must be 256-byte aligned");
+    }
+    return DSALT_OK;
+}
+
+int dsalt_bwd(const dsalt_bwd_args *a, void *stream) {
+    int rc = dsalt_bwd_check(a);
+    if (rc) return rc;
+    hipError_t e = dsalt::launch_bwd(*a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(DSALT_ERR_LAUNCH, "dsalt_bwd launch failed: %s", hipGetErrorString(e));
+    return DSALT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,147 @@
+// Device-side building blocks shared by the gfx950 DSALT kernels: MFMA wrappers for
+// bf16/fp16, wave64 reductions, the packed-sequence block lookup and launch constants.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <limits.h>
+
+namespace dsalt {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+template <typename To, typename From>
+__device__ __forceinline__ To bitcast(const From &x) {
+    static_assert(sizeof(To) == sizeof(From), "bitcast size mismatch");
+    return __builtin_bit_cast(To, x);
+}
+
+// 16-bit element types. Storage is always raw uint16_t; `vec8` is the MFMA operand of
+// v_mfma_f32_32x32x16_{bf16,f16}: 8 consecutive K-elements of one M row (A) or one N
+// column (B) per lane, lane l covering row/column l%32 and K-elements (l/32)*8..+7.
+struct BF16 {
+    typedef bf16x8 vec8;
+    static __device__ __forceinline__ f32x16 mfma(vec8 a, vec8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    // Round-to-nearest-even pack of two fp32 values (v_cvt_pk_bf16_f32).
+    static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+        bf16x2 v = {(__bf16)lo, (__bf16)hi};
+        return bitcast<uint32_t>(v);
+    }
+    static __device__ __forceinline__ float to_f32(uint16_t x) {
+        return __uint_as_float(((uint32_t)x) << 16);
+    }
+};
+
+struct F16 {
+    typedef f16x8 vec8;
+    static __device__ __forceinline__ f32x16 mfma(vec8 a, vec8 b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+        f16x2 v = {(_Float16)lo, (_Float16)hi};
+        return bitcast<uint32_t>(v);
+    }
+    static __device__ __forceinline__ float to_f32(uint16_t x) {
+        return (float)bitcast<_Float16>(x);
+    }
+};
+
+// Row index (within a 32-row MFMA block) of accumulator register r of a lane in half
+// `hh` (= lane / 32): the 32x32 accumulator holds, for column lane%32, the rows
+// (r/4)*8 + hh*4 + r%4. acc_row_const() is the part that does not depend on the lane.
+__device__ __forceinline__ constexpr int acc_row_const(int r) { return (r >> 2) * 8 + (r & 3); }
+
+// ---- wave64 reductions (all lanes receive the result) ----------------------------
+__device__ __forceinline__ int wave_min(int x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = min(x, __shfl_xor(x, o));
+    return x;
+}
+__device__ __forceinline__ int wave_max(int x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x = max(x, __shfl_xor(x, o));
+    return x;
+}
+__device__ __forceinline__ int wave_sum(int x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+__device__ __forceinline__ float wave_sumf(float x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+    }
+    return x;
+}
+
+// Combine the two 32-lane halves of a wave (lanes l and l^32 hold the same query
+// column in the 32x32 MFMA layout): v_permlane32_swap returns both halves, so one
+// swap plus one VALU op gives the pair maximum / sum in every lane.
+__device__ __forceinline__ float half_max(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// Map a linear block index `target` over all (sequence, block-in-sequence) pairs of a
+// packed batch (blocks of `bm` tokens, sequence s owning ceil(L_s / bm) blocks) to its
+// pair, scanning cu_seqlens 64 sequences at a time with a wave prefix sum. Every lane
+// returns the same answer; false when `target` is past the last block. This replaces a
+// host-built block map, so launches need no device-to-host synchronisation.
+__device__ __forceinline__ bool find_block(const int32_t *__restrict__ cu, int num_seqs, int target,
+                                           int bm, int lane, int &seq, int &blk) {
+    for (int base = 0; base < num_seqs; base += 64) {
+        const int s = base + lane;
+        int nb = 0;
+        if (s < num_seqs) {
+            const int len = cu[s + 1] - cu[s];
+            nb = len > 0 ? (len + bm - 1) / bm : 0;
+        }
+        const int incl = wave_incl_scan(nb, lane);
+        const int total = __shfl(incl, 63);
+        if (target < total) {
+            const unsigned long long m = __ballot(incl > target);
+            const int first = __ffsll((long long)m) - 1;
+            const int incl_f = __shfl(incl, first);
+            const int nb_f = __shfl(nb, first);
+            seq = base + first;
+            blk = target - (incl_f - nb_f);
+            return true;
+        }
+        target -= total;
+    }
+    return false;
+}
+
+// Workgroup index remap for the 8 XCDs of MI355X. Consecutive hardware workgroup ids
+// are dispatched round-robin over the XCDs; remapping them so that each XCD receives a
+// contiguous range of logical ids keeps neighbouring query/key blocks (which share
+// K/V rows) on the same XCD and therefore in the same L2. `grid` must be a multiple of 8.
+__device__ __forceinline__ int xcd_remap(int bid, int grid) {
+    const int per = grid >> 3;
+    return (bid & 7) * per + (bid >> 3);
+}
+
+}  // namespace dsalt

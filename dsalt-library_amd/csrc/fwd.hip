@@ -1,0 +1,434 @@
+// Fused DSALT sparse-attention forward for gfx950 (HARD and SOFT semantics).
+//
+// Reference semantics: _dsalt_fwd_kernel (dsalt/kernels/dsalt_triton_attn.py:27-169) and
+// _train_fwd_kernel (dsalt/kernels/dsalt_triton_train.py:74-214); the landmark K/V
+// gather of _build_landmark_kv (dsalt/kernels/selectors.py:137-159) is done in-kernel.
+//
+// Design (one workgroup = 4 waves = 128 consecutive queries of one (sequence, head)):
+//  * Each wave owns 32 queries and computes S^T = K . Q^T with v_mfma_f32_32x32x16, so
+//    a lane holds ONE query (column lane%32) and 16 keys per 32-key block: the row max
+//    is an in-register max plus one v_permlane32_swap between the two lane halves, and
+//    P^T converts in place into the B operand of O^T += V^T . P^T (no data movement).
+//  * K tiles (64 keys) are staged row-major in LDS, V tiles transposed (V^T), double
+//    buffered, with the next tile's global loads in flight during the current tile's
+//    MFMAs. Rows are padded so that the MFMA operand reads are bank-conflict free.
+//  * The workgroup streams the union of its waves' key ranges
+//    [min_i(i - w_i + 1), max_i i]; a wave skips tiles outside its own range, and tiles
+//    that lie inside every row's band core take a mask-free path.
+//  * Landmark K/V rows are gathered straight from K/V into the same tile buffers after
+//    the band, with per-slot admission (p <= p_max(i)) and per-slot logit bias.
+//  * Online softmax in base 2 with a stale maximum: the running max is only raised (and
+//    O rescaled) when a tile exceeds it by more than 2^8, which keeps P <= 256.
+//  * The workgroup -> (head, sequence, block) map is computed in-kernel from cu_seqlens
+//    and remapped across the 8 XCDs, so launches need no host-side block map.
+#include "common.h"
+#include "launch.h"
+
+namespace dsalt {
+namespace {
+
+constexpr int kKPad = 8;          // K tile row = D + 8 halves: conflict-free b128 reads
+constexpr int kVPad = 4;          // V^T tile row = 64 + 4 halves: conflict-free b64 reads
+constexpr float kStaleMax = 8.0f;  // allowed growth of the row max before a rescale (log2)
+enum { kHard = 0, kSoft = 1 };
+
+struct FwdParams {
+    const uint16_t *q, *k, *v;
+    uint16_t *o;
+    float *lse;
+    const float *w;
+    const int64_t *lmk_pos;
+    const float *lmk_bias;
+    const int32_t *cu;
+    int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lse_st, lse_sh, w_st;
+    int64_t lp_sh, lp_ss, lp_sk, lb_sh, lb_ss, lb_sk;
+    int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid;
+    float scale_log2, inv_tau, win_edge;
+};
+
+template <typename DT, int D, int MODE>
+__global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
+    typedef typename DT::vec8 vec8;
+    constexpr int BN = kFwdBN;
+    constexpr int KS = D / 16;              // MFMA k-steps over the head dim
+    constexpr int ND = D / 32;              // 32-row blocks of O^T
+    constexpr int CPR = D / 8;              // 16-byte chunks per K/V row
+    constexpr int PER_T = BN * CPR / 256;   // chunks per thread per tile
+
+    __shared__ __align__(16) uint16_t ks[2][BN][D + kKPad];
+    __shared__ __align__(16) uint16_t vt[2][D][BN + kVPad];
+    __shared__ int s_red[4][3];
+    __shared__ int s_ltile[DSALT_MAX_K_LMK / BN];
+    __shared__ int s_nlt;
+    extern __shared__ int s_dyn[];
+    int *s_lpos = s_dyn;
+    float *s_lbias = reinterpret_cast<float *>(s_dyn + p.k_pad);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ql = lane & 31, hh = lane >> 5;
+
+    // ---- workgroup -> (head, sequence, query block) -----------------------------------
+    const int logical = xcd_remap(blockIdx.x, p.grid);
+    const int head = logical / p.n_qblk;
+    if (head >= p.n_heads) return;
+    int seq, blk;
+    if (!find_block(p.cu, p.num_seqs, logical - head * p.n_qblk, kFwdBM, lane, seq, blk)) return;
+    const int seq_start = p.cu[seq];
+    const int seq_len = p.cu[seq + 1] - seq_start;
+    const int i = blk * kFwdBM + wave * 32 + ql;  // query offset inside the sequence
+    const bool qvalid = i < seq_len;
+    const int64_t tok_i = (int64_t)seq_start + i;
+
+    // ---- Q (B operand: query column ql, head-dim chunk hh*8 of every 16) ---------------
+    vec8 qv[KS];
+    {
+        const uint16_t *qp = p.q + tok_i * p.q_st + (int64_t)head * p.q_sh + hh * 8;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            uint4 raw = make_uint4(0, 0, 0, 0);
+            if (qvalid) raw = *reinterpret_cast<const uint4 *>(qp + s * 16);
+            qv[s] = bitcast<vec8>(raw);
+        }
+    }
+
+    // ---- per-query key ranges -----------------------------------------------------------
+    // lo: first band key; corelo: first key of the zero-bias core; pmax: largest
+    // admissible landmark position (-1: none). All inclusive, relative to the sequence.
+    const float wv = qvalid ? p.w[tok_i * p.w_st] : 0.f;
+    int lo, corelo, pmax;
+    float wc = wv;
+    if (MODE == kHard) {
+        // w = max(1, trunc(w)); NaN -> 1 (dsalt_triton_attn.py:69-70, :282)
+        const int wi = (wv >= 1.f) ? (int)fminf(wv, 1073741824.f) : 1;
+        lo = max(0, i - wi + 1);
+        corelo = lo;
+        pmax = lo - 1;  // p <= i - w  <=>  p < i - w + 1 (dsalt_triton_attn.py:133-135)
+    } else {
+        // band 0 <= i-j <= w~  <=>  j >= i - floor(w~) (dsalt_triton_train.py:147-150)
+        lo = (wc >= 0.f) ? max(0, i - (int)floorf(fminf(wc, 1073741824.f))) : i + 1;
+        // core i-j <= w~ - win_edge, the difference taken in fp32 (:154)
+        const float wce = wc - p.win_edge;
+        corelo = (wce >= 0.f) ? i - (int)floorf(fminf(wce, 1073741824.f)) : i + 1;
+        corelo = max(corelo, lo);
+        // landmark: p <= i and (float)p < (float)i - w~ (:183-185)  <=>  p <= ceil(t)-1
+        const float t = (float)i - wc;
+        pmax = (t == t) ? (int)fminf(fmaxf(ceilf(fminf(t, 1073741824.f)) - 1.f, -1.f), (float)i) : -1;
+    }
+    const int wlo = wave_min(qvalid ? lo : INT_MAX);
+    const int whi = wave_max(qvalid ? i : -1);
+    const int wclo = wave_max(qvalid ? corelo : INT_MIN);
+    const int wchi = wave_min(qvalid ? i : INT_MAX);
+    const int wpmax = wave_max(qvalid ? pmax : -1);
+
+    // ---- landmark slots -> LDS (invalid / out-of-sequence slots become INT_MAX) --------
+    for (int s = tid; s < p.k_pad; s += 256) {
+        int pos = INT_MAX;
+        float b = 0.f;
+        if (s < p.k_lmk) {
+            const int64_t pp = p.lmk_pos[head * p.lp_sh + seq * p.lp_ss + s * p.lp_sk];
+            if (pp >= 0 && pp < seq_len) {
+                pos = (int)pp;
+                if (p.lmk_bias) b = p.lmk_bias[head * p.lb_sh + seq * p.lb_ss + s * p.lb_sk] * kLog2e;
+            }
+        }
+        s_lpos[s] = pos;
+        s_lbias[s] = b;
+    }
+    if (lane == 0) {
+        s_red[wave][0] = wlo;
+        s_red[wave][1] = whi;
+        s_red[wave][2] = wpmax;
+    }
+    __syncthreads();
+    const int glo = min(min(s_red[0][0], s_red[1][0]), min(s_red[2][0], s_red[3][0]));
+    const int ghi = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
+    const int gpmax = max(max(s_red[0][2], s_red[1][2]), max(s_red[2][2], s_red[3][2]));
+    if (wave == 0) {  // landmark tiles holding at least one admissible position
+        int n = 0;
+        for (int lt = 0; lt < p.k_pad / BN; ++lt) {
+            if (wave_min(s_lpos[lt * BN + lane]) <= gpmax) {
+                if (lane == 0) s_ltile[n] = lt;
+                ++n;
+            }
+        }
+        if (lane == 0) s_nlt = n;
+    }
+    __syncthreads();
+    const int nb = (ghi >= glo) ? (ghi - glo) / BN + 1 : 0;
+    const int nt = nb + s_nlt;
+
+    // ---- tile staging -------------------------------------------------------------------
+    uint4 kr[PER_T], vr[PER_T];
+    auto load_tile = [&](int t) {
+        const bool band = t < nb;
+        const int tb = glo + t * BN;
+        const int lt = band ? 0 : s_ltile[t - nb];
+#pragma unroll
+        for (int u = 0; u < PER_T; ++u) {
+            const int c = tid + u * 256;
+            const int row = c / CPR, col = c % CPR;
+            int key;
+            bool ok;
+            if (band) {
+                key = tb + row;
+                ok = key < seq_len;
+            } else {
+                key = s_lpos[lt * BN + row];
+                ok = key != INT_MAX;
+            }
+            uint4 kx = make_uint4(0, 0, 0, 0), vx = kx;
+            if (ok) {
+                const int64_t tok = (int64_t)seq_start + key;
+                kx = *reinterpret_cast<const uint4 *>(p.k + tok * p.k_st + (int64_t)head * p.k_sh + col * 8);
+                vx = *reinterpret_cast<const uint4 *>(p.v + tok * p.v_st + (int64_t)head * p.v_sh + col * 8);
+            }
+            kr[u] = kx;
+            vr[u] = vx;
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < PER_T; ++u) {
+            const int c = tid + u * 256;
+            const int row = c / CPR, col = c % CPR;
+            *reinterpret_cast<uint4 *>(&ks[buf][row][col * 8]) = kr[u];
+            const uint16_t *e = reinterpret_cast<const uint16_t *>(&vr[u]);
+#pragma unroll
+            for (int x = 0; x < 8; ++x) vt[buf][col * 8 + x][row] = e[x];
+        }
+    };
+
+    f32x16 oacc[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[d][r] = 0.f;
+    float m2 = -INFINITY, lsum = 0.f;
+    const float c = p.scale_log2;
+
+    if (nt > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    __syncthreads();
+
+    for (int t = 0; t < nt; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < nt) load_tile(t + 1);
+
+        const bool band = t < nb;
+        const int tb = glo + t * BN;
+        int lt = 0;
+        bool active;
+        if (band) {
+            active = (tb <= whi) && (tb + BN - 1 >= wlo);
+        } else {
+            lt = s_ltile[t - nb];
+            active = wave_min(s_lpos[lt * BN + lane]) <= wpmax;
+        }
+        if (active) {
+            // S^T (64 keys x 32 queries) = K . Q^T
+            f32x16 sacc[2];
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                f32x16 acc;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+                for (int s = 0; s < KS; ++s) {
+                    const vec8 a = bitcast<vec8>(
+                        *reinterpret_cast<const uint4 *>(&ks[buf][rb * 32 + ql][s * 16 + hh * 8]));
+                    acc = DT::mfma(a, qv[s], acc);
+                }
+                sacc[rb] = acc;
+            }
+
+            // masks and biases; `scaled` = values already in log2 logit units
+            bool scaled = false;
+            if (band) {
+                // key offset in the tile of (rb, r) = rb*32 + acc_row_const(r) + hh*4
+                const int A = i - tb - hh * 4;   // key <= i       <=> cst <= A
+                const int B = lo - tb - hh * 4;  // key >= lo      <=> cst >= B
+                const bool need_lo = tb < wclo;
+                const bool need_hi = tb + BN - 1 > wchi;
+                if (MODE == kHard) {
+                    if (need_lo || need_hi) {
+#pragma unroll
+                        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const int cst = rb * 32 + acc_row_const(r);
+                                if (cst > A || cst < B) sacc[rb][r] = -INFINITY;
+                            }
+                    }
+                } else {
+                    if (need_lo) {
+                        const int Bc = corelo - tb - hh * 4;  // key >= corelo <=> cst >= Bc
+#pragma unroll
+                        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const int cst = rb * 32 + acc_row_const(r);
+                                float x = sacc[rb][r] * c;
+                                if (cst < Bc) {
+                                    // log sigmoid((w~ - d)/tau) in log2 units, d = i - key
+                                    const float z = (wc - (float)(A - cst)) * p.inv_tau;
+                                    x -= fast_log2(1.f + fast_exp2(-z * kLog2e));
+                                }
+                                sacc[rb][r] = (cst > A || cst < B) ? -INFINITY : x;
+                            }
+                        scaled = true;
+                    } else if (need_hi) {
+#pragma unroll
+                        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const int cst = rb * 32 + acc_row_const(r);
+                                if (cst > A) sacc[rb][r] = -INFINITY;
+                            }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int slot = lt * BN + rb * 32 + acc_row_const(r) + hh * 4;
+                        const int pos = s_lpos[slot];
+                        sacc[rb][r] = (pos <= pmax) ? fmaf(sacc[rb][r], c, s_lbias[slot]) : -INFINITY;
+                    }
+                scaled = true;
+            }
+
+            // online softmax (base 2, stale maximum)
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[rb][r]);
+            tmax = half_max(tmax);
+            const float tm2 = scaled ? tmax : tmax * c;
+            if (tm2 > m2 + kStaleMax) {
+                const float alpha = fast_exp2(m2 - tm2);
+                lsum *= alpha;
+#pragma unroll
+                for (int d = 0; d < ND; ++d)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
+                m2 = tm2;
+            }
+            const float mu = (m2 == -INFINITY) ? 0.f : m2;
+            uint32_t pk[2][8];
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float e0, e1;
+                    if (scaled) {
+                        e0 = fast_exp2(sacc[rb][2 * j] - mu);
+                        e1 = fast_exp2(sacc[rb][2 * j + 1] - mu);
+                    } else {
+                        e0 = fast_exp2(fmaf(sacc[rb][2 * j], c, -mu));
+                        e1 = fast_exp2(fmaf(sacc[rb][2 * j + 1], c, -mu));
+                    }
+                    lsum += e0 + e1;
+                    pk[rb][j] = DT::pack2(e0, e1);
+                }
+
+            // O^T (D x 32 queries) += V^T . P^T ; k-step kk covers tile keys kk*16..+15
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int rb = kk >> 1, g = kk & 1;
+                const vec8 b = bitcast<vec8>(
+                    make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
+#pragma unroll
+                for (int d = 0; d < ND; ++d) {
+                    const uint16_t *row = &vt[buf][d * 32 + ql][kk * 16 + hh * 4];
+                    const uint2 lo8 = *reinterpret_cast<const uint2 *>(row);
+                    const uint2 hi8 = *reinterpret_cast<const uint2 *>(row + 8);
+                    const vec8 a = bitcast<vec8>(make_uint4(lo8.x, lo8.y, hi8.x, hi8.y));
+                    oacc[d] = DT::mfma(a, b, oacc[d]);
+                }
+            }
+        }
+
+        if (t + 1 < nt) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln 2 --------------------------------
+    const float ltot = half_sum(lsum);
+    const bool nonempty = ltot > 1e-9f;
+    const float inv = nonempty ? 1.f / ltot : 0.f;
+    if (qvalid) {
+        uint16_t *op = p.o + tok_i * p.o_st + (int64_t)head * p.o_sh;
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int dd = d * 32 + g * 8 + hh * 4;
+                uint2 val;
+                val.x = DT::pack2(oacc[d][g * 4 + 0] * inv, oacc[d][g * 4 + 1] * inv);
+                val.y = DT::pack2(oacc[d][g * 4 + 2] * inv, oacc[d][g * 4 + 3] * inv);
+                *reinterpret_cast<uint2 *>(op + dd) = val;
+            }
+        if (hh == 0)
+            p.lse[tok_i * p.lse_st + (int64_t)head * p.lse_sh] =
+                nonempty ? (m2 + fast_log2(ltot)) * kLn2 : -INFINITY;
+    }
+}
+
+template <typename DT, int D, int MODE>
+hipError_t launch_typed(const FwdParams &p, size_t dyn, hipStream_t stream) {
+    hipLaunchKernelGGL((fwd_kernel<DT, D, MODE>), dim3(p.grid), dim3(256), dyn, stream, p);
+    return hipGetLastError();
+}
+
+template <typename DT>
+hipError_t launch_dt(const FwdParams &p, int head_dim, int mode, size_t dyn, hipStream_t stream) {
+    if (head_dim == 64)
+        return mode == DSALT_MODE_HARD ? launch_typed<DT, 64, kHard>(p, dyn, stream)
+                                       : launch_typed<DT, 64, kSoft>(p, dyn, stream);
+    return mode == DSALT_MODE_HARD ? launch_typed<DT, 128, kHard>(p, dyn, stream)
+                                   : launch_typed<DT, 128, kSoft>(p, dyn, stream);
+}
+
+}  // namespace
+
+hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream) {
+    if (a.total_len == 0) return hipSuccess;
+    FwdParams p;
+    p.q = static_cast<const uint16_t *>(a.q);
+    p.k = static_cast<const uint16_t *>(a.k);
+    p.v = static_cast<const uint16_t *>(a.v);
+    p.o = static_cast<uint16_t *>(a.out);
+    p.lse = a.lse;
+    p.w = a.w;
+    p.lmk_pos = a.lmk_pos;
+    p.lmk_bias = a.lmk_bias;
+    p.cu = a.cu_seqlens;
+    p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
+    p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;
+    p.v_st = a.v_stride_t; p.v_sh = a.v_stride_h;
+    p.o_st = a.out_stride_t; p.o_sh = a.out_stride_h;
+    p.lse_st = a.lse_stride_t; p.lse_sh = a.lse_stride_h;
+    p.w_st = a.w_stride;
+    p.lp_sh = a.lmk_pos_stride_h; p.lp_ss = a.lmk_pos_stride_s; p.lp_sk = a.lmk_pos_stride_k;
+    p.lb_sh = a.lmk_bias_stride_h; p.lb_ss = a.lmk_bias_stride_s; p.lb_sk = a.lmk_bias_stride_k;
+    p.total_len = a.total_len;
+    p.num_seqs = a.num_seqs;
+    p.n_heads = a.n_heads;
+    p.k_lmk = a.k_lmk;
+    p.k_pad = (a.k_lmk + kFwdBN - 1) / kFwdBN * kFwdBN;
+    p.n_qblk = block_upper_bound(a.total_len, a.num_seqs, kFwdBM);
+    const int64_t blocks = (int64_t)p.n_qblk * a.n_heads;
+    p.grid = (int)((blocks + 7) / 8 * 8);
+    p.scale_log2 = a.scale * kLog2e;
+    p.inv_tau = 1.f / a.tau_win;
+    p.win_edge = a.win_edge;
+    const size_t dyn = (size_t)p.k_pad * (sizeof(int) + sizeof(float));
+    if (a.dtype == DSALT_DTYPE_BF16) return launch_dt<BF16>(p, a.head_dim, a.mode, dyn, stream);
+    return launch_dt<F16>(p, a.head_dim, a.mode, dyn, stream);
+}
+
+}  // namespace dsalt

@@ -1,0 +1,29 @@
+// Internal interface between the C-ABI layer (api.hip) and the kernel translation
+// units. Arguments arrive here already validated.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include "../../include/dsalt_hip.h"
+
+namespace dsalt {
+
+// Forward: one workgroup of 4 waves owns kFwdBM consecutive queries of one
+// (sequence, head); each wave owns 32 of them. Key tiles hold kFwdBN keys.
+constexpr int kFwdBM = 128;
+constexpr int kFwdBN = 64;
+
+hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream);
+hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream);
+hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream);
+hipError_t launch_quantize(const float *w_cont, int64_t n, float *w_out, int32_t *w_int,
+                           hipStream_t stream);
+
+// Number of query blocks of `bm` tokens over a packed batch, as an upper bound that is
+// computable without reading cu_seqlens: sum_s ceil(L_s/bm) <= ceil(T/bm) + S.
+inline int block_upper_bound(int total_len, int num_seqs, int bm) {
+    return (total_len + bm - 1) / bm + num_seqs;
+}
+
+int64_t bwd_workspace_bytes(int total_len, int num_seqs, int n_heads, int head_dim, int k_lmk);
+
+}  // namespace dsalt

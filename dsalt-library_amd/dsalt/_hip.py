@@ -1,0 +1,338 @@
+"""ctypes binding of libdsalt_hip.so (the gfx950 HIP kernels behind the DSALT API).
+
+The structures below mirror include/dsalt_hip.h field by field; ``check_abi()``
+compares their sizes with the library's own ``sizeof``. Every call runs on the
+current torch stream of the tensors' device and never synchronises. There is no
+fallback: a missing library or a non-GPU tensor raises ``DsaltError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import c_float, c_int32, c_int64, c_size_t, c_void_p
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdsalt_hip.so")
+
+DSALT_OK = 0
+MODE_HARD = 0
+MODE_SOFT = 1
+DTYPE_BF16 = 0
+DTYPE_F16 = 1
+MAX_K_LMK = 1024
+ABI_VERSION = 1
+
+_DTYPES = {torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
+
+
+class DsaltError(RuntimeError):
+    """Raised for invalid arguments, a missing library or a failed launch."""
+
+
+class FwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("mode", c_int32), ("dtype", c_int32), ("total_len", c_int32), ("num_seqs", c_int32),
+        ("n_heads", c_int32), ("head_dim", c_int32), ("k_lmk", c_int32), ("reserved0", c_int32),
+        ("q", c_void_p), ("q_stride_t", c_int64), ("q_stride_h", c_int64),
+        ("k", c_void_p), ("k_stride_t", c_int64), ("k_stride_h", c_int64),
+        ("v", c_void_p), ("v_stride_t", c_int64), ("v_stride_h", c_int64),
+        ("out", c_void_p), ("out_stride_t", c_int64), ("out_stride_h", c_int64),
+        ("lse", c_void_p), ("lse_stride_t", c_int64), ("lse_stride_h", c_int64),
+        ("w", c_void_p), ("w_stride", c_int64),
+        ("lmk_pos", c_void_p), ("lmk_pos_stride_h", c_int64), ("lmk_pos_stride_s", c_int64),
+        ("lmk_pos_stride_k", c_int64),
+        ("lmk_bias", c_void_p), ("lmk_bias_stride_h", c_int64), ("lmk_bias_stride_s", c_int64),
+        ("lmk_bias_stride_k", c_int64),
+        ("cu_seqlens", c_void_p),
+        ("scale", c_float), ("tau_win", c_float), ("win_edge", c_float), ("reserved1", c_float),
+    ]
+
+
+class BwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("mode", c_int32), ("dtype", c_int32), ("total_len", c_int32), ("num_seqs", c_int32),
+        ("n_heads", c_int32), ("head_dim", c_int32), ("k_lmk", c_int32), ("reserved0", c_int32),
+        ("q", c_void_p), ("q_stride_t", c_int64), ("q_stride_h", c_int64),
+        ("k", c_void_p), ("k_stride_t", c_int64), ("k_stride_h", c_int64),
+        ("v", c_void_p), ("v_stride_t", c_int64), ("v_stride_h", c_int64),
+        ("out", c_void_p), ("out_stride_t", c_int64), ("out_stride_h", c_int64),
+        ("lse", c_void_p), ("lse_stride_t", c_int64), ("lse_stride_h", c_int64),
+        ("dout", c_void_p), ("dout_stride_t", c_int64), ("dout_stride_h", c_int64),
+        ("w", c_void_p), ("w_stride", c_int64),
+        ("lmk_pos", c_void_p), ("lmk_pos_stride_h", c_int64), ("lmk_pos_stride_s", c_int64),
+        ("lmk_pos_stride_k", c_int64),
+        ("lmk_bias", c_void_p), ("lmk_bias_stride_h", c_int64), ("lmk_bias_stride_s", c_int64),
+        ("lmk_bias_stride_k", c_int64),
+        ("cu_seqlens", c_void_p),
+        ("dq", c_void_p), ("dq_stride_t", c_int64), ("dq_stride_h", c_int64),
+        ("dk", c_void_p), ("dk_stride_t", c_int64), ("dk_stride_h", c_int64),
+        ("dv", c_void_p), ("dv_stride_t", c_int64), ("dv_stride_h", c_int64),
+        ("d_lmk_bias", c_void_p), ("d_w", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_int64),
+        ("scale", c_float), ("tau_win", c_float), ("win_edge", c_float), ("reserved1", c_float),
+    ]
+
+
+class SelectArgs(ctypes.Structure):
+    _fields_ = [
+        ("total_len", c_int32), ("num_seqs", c_int32), ("n_heads", c_int32), ("k_lmk", c_int32),
+        ("scores", c_void_p), ("scores_stride_t", c_int64), ("scores_stride_h", c_int64),
+        ("w", c_void_p), ("w_stride", c_int64),
+        ("cu_seqlens", c_void_p),
+        ("lmk_pos", c_void_p),
+    ]
+
+
+EXPORTED_SYMBOLS = (
+    "dsalt_fwd", "dsalt_fwd_check", "dsalt_bwd", "dsalt_bwd_check", "dsalt_bwd_workspace_size",
+    "dsalt_select_landmarks", "dsalt_select_check", "dsalt_quantize_windows",
+    "dsalt_abi_version", "dsalt_last_error", "dsalt_fwd_args_size", "dsalt_bwd_args_size",
+    "dsalt_select_args_size",
+)
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libdsalt_hip.so once; raise DsaltError when it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise DsaltError(
+            f"{LIB_PATH} is missing: build it with `python dsalt-library_amd/build.py` "
+            "(the DSALT path has no non-HIP fallback)")
+    h = ctypes.CDLL(LIB_PATH)
+    for name, argtypes in (
+        ("dsalt_fwd", [ctypes.POINTER(FwdArgs), c_void_p]),
+        ("dsalt_fwd_check", [ctypes.POINTER(FwdArgs)]),
+        ("dsalt_bwd", [ctypes.POINTER(BwdArgs), c_void_p]),
+        ("dsalt_bwd_check", [ctypes.POINTER(BwdArgs)]),
+        ("dsalt_select_landmarks", [ctypes.POINTER(SelectArgs), c_void_p]),
+        ("dsalt_select_check", [ctypes.POINTER(SelectArgs)]),
+        ("dsalt_quantize_windows", [c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
+    ):
+        fn = getattr(h, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    h.dsalt_bwd_workspace_size.argtypes = [c_int32] * 5
+    h.dsalt_bwd_workspace_size.restype = c_int64
+    h.dsalt_abi_version.restype = ctypes.c_int
+    h.dsalt_last_error.restype = ctypes.c_char_p
+    for n in ("dsalt_fwd_args_size", "dsalt_bwd_args_size", "dsalt_select_args_size"):
+        getattr(h, n).restype = c_size_t
+    _lib = h
+    check_abi()
+    return h
+
+
+def check_abi() -> None:
+    h = lib()
+    if h.dsalt_abi_version() != ABI_VERSION:
+        raise DsaltError(f"ABI version mismatch: library {h.dsalt_abi_version()} vs binding {ABI_VERSION}")
+    for struct, fn in ((FwdArgs, h.dsalt_fwd_args_size), (BwdArgs, h.dsalt_bwd_args_size),
+                       (SelectArgs, h.dsalt_select_args_size)):
+        if ctypes.sizeof(struct) != fn():
+            raise DsaltError(f"{struct.__name__} layout mismatch: {ctypes.sizeof(struct)} vs {fn()} bytes")
+
+
+def _raise(rc: int, what: str) -> None:
+    if rc != DSALT_OK:
+        msg = lib().dsalt_last_error().decode(errors="replace")
+        raise DsaltError(f"{what} failed (code {rc}): {msg}")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def require_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise DsaltError(
+                f"the DSALT HIP path needs tensors on a ROCm GPU, got a tensor on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise DsaltError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise DsaltError("no tensor given")
+    return dev
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def compute_dtype(dtype: torch.dtype) -> torch.dtype:
+    """bf16/fp16 compute as is; anything else computes in fp16, as the reference's
+    kernels do (dsalt/kernels/dsalt_triton_attn.py:266)."""
+    return dtype if dtype in _DTYPES else torch.float16
+
+
+def as_kernel_operand(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """[T,H,D] operand with unit stride on D, 16-byte aligned rows (copy only if needed)."""
+    if t.dtype != dtype:
+        t = t.to(dtype)
+    ok = (t.dim() == 3 and t.stride(2) == 1 and t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0
+          and t.data_ptr() % 16 == 0)
+    return t if ok else t.contiguous()
+
+
+def _f32_vec(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.float32 else t.float()
+
+
+def _cu_i32(cu: torch.Tensor) -> torch.Tensor:
+    if cu.dtype != torch.int32 or not cu.is_contiguous():
+        cu = cu.to(torch.int32).contiguous()
+    return cu
+
+
+def fwd(mode: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, w: torch.Tensor,
+        lmk_pos: torch.Tensor | None, lmk_bias: torch.Tensor | None, cu_seqlens: torch.Tensor,
+        scale: float, tau_win: float = 1.0, win_edge: float = 4.0,
+        out: torch.Tensor | None = None, lse: torch.Tensor | None = None):
+    """Sparse-attention forward. q/k/v must already be kernel operands (see
+    ``as_kernel_operand``). Returns (out [T,H,D] in q.dtype, lse [T,H] fp32)."""
+    dev = require_gpu(q, k, v, w, cu_seqlens)
+    T, H, D = q.shape
+    if k.shape != q.shape or v.shape != q.shape:
+        raise DsaltError(f"q/k/v shapes differ: {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise DsaltError(f"q/k/v must share a bf16/fp16 dtype, got {q.dtype} {k.dtype} {v.dtype}")
+    cu = _cu_i32(cu_seqlens)
+    S = cu.shape[0] - 1
+    w = _f32_vec(w)
+    if w.dim() != 1 or w.shape[0] != T:
+        raise DsaltError(f"w must be [T={T}], got {tuple(w.shape)}")
+    kl = 0
+    if lmk_pos is not None:
+        if lmk_pos.dim() != 3 or lmk_pos.shape[0] != H or lmk_pos.shape[1] != S:
+            raise DsaltError(f"landmark positions must be [H={H}, S={S}, k], got {tuple(lmk_pos.shape)}")
+        if lmk_pos.dtype != torch.int64:
+            lmk_pos = lmk_pos.long()
+        kl = lmk_pos.shape[2]
+        if lmk_bias is not None:
+            if lmk_bias.shape != lmk_pos.shape:
+                raise DsaltError(f"landmark bias shape {tuple(lmk_bias.shape)} != {tuple(lmk_pos.shape)}")
+            lmk_bias = _f32_vec(lmk_bias)
+    if out is None:
+        out = torch.empty((T, H, D), device=dev, dtype=q.dtype)
+    if lse is None:
+        lse = torch.empty((T, H), device=dev, dtype=torch.float32)
+    a = FwdArgs()
+    a.mode, a.dtype, a.total_len, a.num_seqs = mode, _DTYPES[q.dtype], T, S
+    a.n_heads, a.head_dim, a.k_lmk = H, D, kl
+    a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
+    a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
+    a.out, a.out_stride_t, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    a.lse, a.lse_stride_t, a.lse_stride_h = lse.data_ptr(), lse.stride(0), lse.stride(1)
+    a.w, a.w_stride = w.data_ptr(), w.stride(0)
+    if kl > 0:
+        a.lmk_pos = lmk_pos.data_ptr()
+        a.lmk_pos_stride_h, a.lmk_pos_stride_s, a.lmk_pos_stride_k = lmk_pos.stride()
+        if lmk_bias is not None:
+            a.lmk_bias = lmk_bias.data_ptr()
+            a.lmk_bias_stride_h, a.lmk_bias_stride_s, a.lmk_bias_stride_k = lmk_bias.stride()
+    a.cu_seqlens = cu.data_ptr()
+    a.scale, a.tau_win, a.win_edge = float(scale), float(tau_win), float(win_edge)
+    _raise(lib().dsalt_fwd(ctypes.byref(a), stream_handle(dev)), "dsalt_fwd")
+    return out, lse
+
+
+def bwd_workspace_size(T: int, S: int, H: int, D: int, k: int) -> int:
+    n = lib().dsalt_bwd_workspace_size(T, S, H, D, k)
+    if n < 0:
+        raise DsaltError("invalid sizes for dsalt_bwd_workspace_size")
+    return int(n)
+
+
+def bwd(mode: int, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, scale: float,
+        tau_win: float = 1.0, win_edge: float = 4.0, need_dw: bool = False):
+    """Sparse-attention backward. Returns (dq, dk, dv, d_lmk_bias [H,S,k] fp32 or None,
+    d_w [T] fp32 or None); dq/dk/dv are in q.dtype."""
+    dev = require_gpu(q, k, v, out, lse, dout, w, cu_seqlens)
+    T, H, D = q.shape
+    cu = _cu_i32(cu_seqlens)
+    S = cu.shape[0] - 1
+    w = _f32_vec(w)
+    dout = as_kernel_operand(dout, q.dtype)
+    kl = 0 if lmk_pos is None else lmk_pos.shape[2]
+    if lmk_pos is not None and lmk_pos.dtype != torch.int64:
+        lmk_pos = lmk_pos.long()
+    if lmk_bias is not None:
+        lmk_bias = _f32_vec(lmk_bias)
+    dq = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dk = torch.empty_like(q, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(q, memory_format=torch.contiguous_format)
+    d_bias = torch.empty((H, S, kl), device=dev, dtype=torch.float32) if kl > 0 else None
+    d_w = torch.empty((T,), device=dev, dtype=torch.float32) if need_dw else None
+    ws_bytes = bwd_workspace_size(T, S, H, D, kl)
+    ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+    a = BwdArgs()
+    a.mode, a.dtype, a.total_len, a.num_seqs = mode, _DTYPES[q.dtype], T, S
+    a.n_heads, a.head_dim, a.k_lmk = H, D, kl
+    a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
+    a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
+    a.out, a.out_stride_t, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+    a.lse, a.lse_stride_t, a.lse_stride_h = lse.data_ptr(), lse.stride(0), lse.stride(1)
+    a.dout, a.dout_stride_t, a.dout_stride_h = dout.data_ptr(), dout.stride(0), dout.stride(1)
+    a.w, a.w_stride = w.data_ptr(), w.stride(0)
+    if kl > 0:
+        a.lmk_pos = lmk_pos.data_ptr()
+        a.lmk_pos_stride_h, a.lmk_pos_stride_s, a.lmk_pos_stride_k = lmk_pos.stride()
+        if lmk_bias is not None:
+            a.lmk_bias = lmk_bias.data_ptr()
+            a.lmk_bias_stride_h, a.lmk_bias_stride_s, a.lmk_bias_stride_k = lmk_bias.stride()
+        a.d_lmk_bias = d_bias.data_ptr()
+    a.cu_seqlens = cu.data_ptr()
+    a.dq, a.dq_stride_t, a.dq_stride_h = dq.data_ptr(), dq.stride(0), dq.stride(1)
+    a.dk, a.dk_stride_t, a.dk_stride_h = dk.data_ptr(), dk.stride(0), dk.stride(1)
+    a.dv, a.dv_stride_t, a.dv_stride_h = dv.data_ptr(), dv.stride(0), dv.stride(1)
+    a.d_w = _ptr(d_w)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
+    a.scale, a.tau_win, a.win_edge = float(scale), float(tau_win), float(win_edge)
+    _raise(lib().dsalt_bwd(ctypes.byref(a), stream_handle(dev)), "dsalt_bwd")
+    return dq, dk, dv, d_bias, d_w
+
+
+def select_landmarks(scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Tensor,
+                     k_lmk: int) -> torch.Tensor:
+    """Top-k landmark positions [H, S, k] int64 (ascending, -1 padded) from fp32 scores [T, H]."""
+    dev = require_gpu(scores, w, cu_seqlens)
+    if scores.dtype != torch.float32:
+        raise DsaltError(f"scores must be float32, got {scores.dtype}")
+    T, H = scores.shape
+    cu = _cu_i32(cu_seqlens)
+    S = cu.shape[0] - 1
+    w = _f32_vec(w)
+    out = torch.empty((H, S, k_lmk), device=dev, dtype=torch.int64)
+    if k_lmk == 0:
+        return out
+    a = SelectArgs()
+    a.total_len, a.num_seqs, a.n_heads, a.k_lmk = T, S, H, k_lmk
+    a.scores, a.scores_stride_t, a.scores_stride_h = scores.data_ptr(), scores.stride(0), scores.stride(1)
+    a.w, a.w_stride = w.data_ptr(), w.stride(0)
+    a.cu_seqlens = cu.data_ptr()
+    a.lmk_pos = out.data_ptr()
+    _raise(lib().dsalt_select_landmarks(ctypes.byref(a), stream_handle(dev)), "dsalt_select_landmarks")
+    return out
+
+
+def quantize_windows(w_cont: torch.Tensor, want_int: bool = False):
+    """w = max(1, floor(w~)) as float32 (NaN stays NaN); optionally also as int32."""
+    dev = require_gpu(w_cont)
+    w_cont = _f32_vec(w_cont).contiguous()
+    n = w_cont.numel()
+    wq = torch.empty_like(w_cont)
+    wi = torch.empty(w_cont.shape, device=dev, dtype=torch.int32) if want_int else None
+    _raise(lib().dsalt_quantize_windows(w_cont.data_ptr(), n, wq.data_ptr(), _ptr(wi), stream_handle(dev)),
+           "dsalt_quantize_windows")
+    return (wq, wi) if want_int else wq

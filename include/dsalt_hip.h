@@ -1,0 +1,196 @@
+/*
+ * dsalt_hip.h - C ABI of the gfx950 (MI355X) DSALT sparse-attention library
+ * (libdsalt_hip.so).
+ *
+ * DSALT attention: query i of a packed sequence attends to its causal local window
+ * plus k content-selected landmark tokens of its sequence. Two semantics exist:
+ *
+ *   HARD (inference):  band  j in [i - w(i) + 1, i],  w(i) = max(1, trunc(w[i]))
+ *                      landmark p admitted iff 0 <= p <= i - w(i); logit bias lmk_bias[slot]
+ *   SOFT (training):   band  0 <= d = i - j <= w~(i)  (fp32 compare), logit bias 0 in the
+ *                      core d <= w~ - win_edge, log sigmoid((w~ - d) / tau_win) on the edge;
+ *                      landmark p admitted iff p <= i and (float)p < (float)i - w~(i);
+ *                      logit bias lmk_logw[slot]
+ *
+ * Logits are q.k * scale (+ bias); softmax is computed online in fp32; O is stored in
+ * the input dtype and LSE = max + log(sum) in fp32 (natural log; -inf for empty rows,
+ * whose O is 0).
+ *
+ * Conventions shared by every entry point:
+ *   - All tensors are device pointers on the current HIP device. Packed token-major
+ *     tensors are [T, H, D] with unit stride along D; strides are given in ELEMENTS.
+ *   - Landmark positions are int64 [H, S, k], relative to the sequence start; -1 (or any
+ *     value outside [0, L_s)) marks an empty slot.
+ *   - cu_seqlens is int32 [S + 1], non-decreasing, cu_seqlens[0] = 0, cu_seqlens[S] = T.
+ *   - `stream` is a hipStream_t (NULL = default stream). Calls are asynchronous on that
+ *     stream, never synchronise and never allocate memory; the backward takes its scratch
+ *     memory from a caller-provided workspace.
+ *   - Every function returns DSALT_OK (0) or an error code; dsalt_last_error() returns a
+ *     thread-local message describing the most recent failure on the calling thread.
+ *   - Argument validation is host-side only (no device reads), so it also runs on a
+ *     machine without a GPU (the *_check functions).
+ */
+#ifndef DSALT_HIP_H
+#define DSALT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSALT_ABI_VERSION 1
+
+enum {
+    DSALT_OK = 0,
+    DSALT_ERR_INVALID = 1,     /* bad argument (shape, stride, alignment, null pointer) */
+    DSALT_ERR_UNSUPPORTED = 2, /* valid request this build does not support (e.g. D=96) */
+    DSALT_ERR_LAUNCH = 3,      /* the HIP runtime rejected a kernel launch */
+};
+
+enum { DSALT_DTYPE_BF16 = 0, DSALT_DTYPE_F16 = 1 };
+enum { DSALT_MODE_HARD = 0, DSALT_MODE_SOFT = 1 };
+
+/* Largest k_lmk the kernels accept (landmark slots per head and sequence). */
+#define DSALT_MAX_K_LMK 1024
+
+/*
+ * Fused sparse-attention forward.
+ * Replaces the Triton launches of
+ *   _dsalt_fwd_kernel  (dsalt/kernels/dsalt_triton_attn.py:27-169, launched at :184-209)
+ *   _train_fwd_kernel  (dsalt/kernels/dsalt_triton_train.py:74-214, launched at :629-645)
+ * The landmark K/V gather of _build_landmark_kv (dsalt/kernels/selectors.py:137-159) and
+ * the packed block map of _build_seq_block_map (selectors.py:37-67) happen inside the
+ * kernel; `out` is written in the input dtype without a prior memset.
+ */
+typedef struct dsalt_fwd_args {
+    int32_t mode;      /* DSALT_MODE_HARD or DSALT_MODE_SOFT */
+    int32_t dtype;     /* DSALT_DTYPE_* of q, k, v and out */
+    int32_t total_len; /* T */
+    int32_t num_seqs;  /* S >= 1 */
+    int32_t n_heads;   /* H >= 1 */
+    int32_t head_dim;  /* D, 64 or 128 */
+    int32_t k_lmk;     /* landmark slots per (head, sequence), 0..DSALT_MAX_K_LMK */
+    int32_t reserved0;
+    const void *q;
+    int64_t q_stride_t, q_stride_h;
+    const void *k;
+    int64_t k_stride_t, k_stride_h;
+    const void *v;
+    int64_t v_stride_t, v_stride_h;
+    void *out;
+    int64_t out_stride_t, out_stride_h;
+    float *lse; /* [T, H] fp32 */
+    int64_t lse_stride_t, lse_stride_h;
+    const float *w; /* [T]: HARD window sizes, SOFT continuous windows w~ */
+    int64_t w_stride;
+    const int64_t *lmk_pos; /* [H, S, k]; may be NULL when k_lmk == 0 */
+    int64_t lmk_pos_stride_h, lmk_pos_stride_s, lmk_pos_stride_k;
+    const float *lmk_bias; /* [H, S, k] fp32 (HARD lmk_bias, SOFT lmk_logw); NULL = 0 */
+    int64_t lmk_bias_stride_h, lmk_bias_stride_s, lmk_bias_stride_k;
+    const int32_t *cu_seqlens; /* [S + 1] */
+    float scale;               /* logit scale, normally 1/sqrt(D) */
+    float tau_win;             /* SOFT only */
+    float win_edge;            /* SOFT only */
+    float reserved1;
+} dsalt_fwd_args;
+
+int dsalt_fwd(const dsalt_fwd_args *args, void *stream);
+/* Validation of dsalt_fwd's arguments without launching anything. */
+int dsalt_fwd_check(const dsalt_fwd_args *args);
+
+/*
+ * Sparse-attention backward (both modes): dQ, dK, dV, the landmark-bias gradient and,
+ * in SOFT mode, the gradient with respect to the continuous window (summed over heads).
+ * Replaces
+ *   _train_bwd_preprocess / _train_bwd_dkdv_kernel / _train_bwd_kernel
+ *       (dsalt/kernels/dsalt_triton_train.py:220-481, launched at :693-745) and the
+ *       d_w.sum(1) of :748
+ *   dsalt_triton_backward (dsalt/kernels/dsalt_triton_bwd.py:219-324) with its kernels
+ *       _dsalt_bwd_preprocess / _dsalt_bwd_kernel (:17-216).
+ * Deterministic: no atomics; every output element is written by exactly one thread.
+ */
+typedef struct dsalt_bwd_args {
+    int32_t mode, dtype, total_len, num_seqs, n_heads, head_dim, k_lmk, reserved0;
+    const void *q;
+    int64_t q_stride_t, q_stride_h;
+    const void *k;
+    int64_t k_stride_t, k_stride_h;
+    const void *v;
+    int64_t v_stride_t, v_stride_h;
+    const void *out; /* forward output (input dtype) */
+    int64_t out_stride_t, out_stride_h;
+    const float *lse; /* forward LSE [T, H] */
+    int64_t lse_stride_t, lse_stride_h;
+    const void *dout; /* upstream gradient, input dtype */
+    int64_t dout_stride_t, dout_stride_h;
+    const float *w;
+    int64_t w_stride;
+    const int64_t *lmk_pos;
+    int64_t lmk_pos_stride_h, lmk_pos_stride_s, lmk_pos_stride_k;
+    const float *lmk_bias;
+    int64_t lmk_bias_stride_h, lmk_bias_stride_s, lmk_bias_stride_k;
+    const int32_t *cu_seqlens;
+    void *dq; /* [T, H, D] input dtype */
+    int64_t dq_stride_t, dq_stride_h;
+    void *dk;
+    int64_t dk_stride_t, dk_stride_h;
+    void *dv;
+    int64_t dv_stride_t, dv_stride_h;
+    float *d_lmk_bias; /* [H, S, k] contiguous fp32; may be NULL */
+    float *d_w;        /* [T] fp32, SOFT only; may be NULL */
+    void *workspace;   /* >= dsalt_bwd_workspace_size(...) bytes, 256-byte aligned */
+    int64_t workspace_bytes;
+    float scale, tau_win, win_edge, reserved1;
+} dsalt_bwd_args;
+
+int64_t dsalt_bwd_workspace_size(int32_t total_len, int32_t num_seqs, int32_t n_heads,
+                                 int32_t head_dim, int32_t k_lmk);
+int dsalt_bwd(const dsalt_bwd_args *args, void *stream);
+int dsalt_bwd_check(const dsalt_bwd_args *args);
+
+/*
+ * Landmark top-k selection.
+ * Replaces the covered mask, the per-(head, sequence) torch.topk and the -1 fill of
+ * _compute_landmark_indices (dsalt/kernels/selectors.py:105-134).
+ * Token j at offset o inside its sequence is a candidate iff o >= trunc(w[j]). For each
+ * (head, sequence) the min(k, L) largest scores are taken (NaN ranks above +inf, which
+ * ranks above every finite score; equal scores: the lower position wins). Selected
+ * finite-score positions are written in ascending order, followed by -1 in every
+ * remaining slot (the reference's -inf/NaN/+inf slots also become -1).
+ */
+typedef struct dsalt_select_args {
+    int32_t total_len, num_seqs, n_heads, k_lmk;
+    const float *scores; /* [T, H] fp32 */
+    int64_t scores_stride_t, scores_stride_h;
+    const float *w; /* [T] window sizes */
+    int64_t w_stride;
+    const int32_t *cu_seqlens;
+    int64_t *lmk_pos; /* out: [H, S, k] contiguous int64 */
+} dsalt_select_args;
+
+int dsalt_select_landmarks(const dsalt_select_args *args, void *stream);
+int dsalt_select_check(const dsalt_select_args *args);
+
+/*
+ * Window quantisation w = max(1, floor(w~)) (NaN stays NaN), the floor/clamp of
+ * DSALTAttention._window_sizes(floor=True) and of _train_selectors
+ * (dsalt/modules/dsalt_attention.py:277-284, :471). Either output may be NULL; the
+ * int32 output holds 1 for NaN inputs, as the kernels' own clamp does.
+ */
+int dsalt_quantize_windows(const float *w_cont, int64_t n, float *w_out, int32_t *w_int_out,
+                           void *stream);
+
+int dsalt_abi_version(void);
+const char *dsalt_last_error(void);
+/* sizeof of the argument structs as compiled into the library (ABI layout check). */
+size_t dsalt_fwd_args_size(void);
+size_t dsalt_bwd_args_size(void);
+size_t dsalt_select_args_size(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSALT_HIP_H */

@@ -1,0 +1,364 @@
+"""CPU oracle for the DSALT sparse-attention hot path. TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this
+module, and only as the checker (or the timed CPU baseline) - never as a product code
+path. It restates, on the CPU, the reference algorithm of LeonardoCofone/dsalt-library
+(files cited relative to the reference root):
+
+  hybrid_scores          dsalt/kernels/landmark_tokens_ker.py:45-61
+  window_continuous      dsalt/modules/dsalt_attention.py:270-275
+  quantize_windows       dsalt/modules/dsalt_attention.py:277-284, :471
+  select_landmarks       dsalt/kernels/selectors.py:105-134 (numpy, exact)
+  attention_hard         dsalt/kernels/dsalt_triton_attn.py:69-169 (the HARD set; equal to
+                         the _last_P mask of dsalt_attention.py:668-692)
+  attention_soft         dsalt/kernels/dsalt_triton_train.py:116-214 with the exact band of
+                         the dense reference dsalt_attention.py:520-563
+  gradients              torch autograd through attention_hard / attention_soft in fp64
+                         (the formulas of dsalt_triton_train.py:302-383, :439-476)
+  cpu_baseline_hard      the reference's CPU fallback cost model: dense per-sequence mask +
+                         F.scaled_dot_product_attention in fp32 (dsalt_attention.py:95-144,
+                         dsalt/kernels/sparse_attn.py:29-57), with the HARD kernel's mask
+
+Pinning (tests/test_oracle.py): closed forms and library routines - causal attention via
+F.scaled_dot_product_attention(is_causal=True) when k = 0 and the window covers the
+sequence; O_i = V_i for w = 1, k = 0; the constant-landmark-bias reweighting closed
+form; the soft edge against F.logsigmoid; selection against a brute-force Python sort
+and against torch.topk as sets; scores against numpy's mean/std(ddof=1); gradients
+against finite differences (torch.autograd.gradcheck) - and the committed golden
+fixtures of tests/golden/. The reference ships no golden vectors of its own.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+# ---------------------------------------------------------------------------------------
+# selectors
+# ---------------------------------------------------------------------------------------
+
+
+def hybrid_scores(x: torch.Tensor, W_V: torch.Tensor, alpha: torch.Tensor, n_heads: int, dh: int):
+    """(scores [T,H], z_x [T], z_v [T,H]); landmark_tokens_ker.py:45-61."""
+    T = x.shape[0]
+    x_norm = x.norm(dim=-1).float()
+    z_x = (x_norm - x_norm.mean()) / x_norm.std().clamp(min=1e-6)
+    n_kv = W_V.shape[0] // dh
+    xwv = (x @ W_V.T).view(T, n_kv, dh).norm(dim=-1).float()
+    z_v = (xwv - xwv.mean(0, keepdim=True)) / xwv.std(0, keepdim=True).clamp(min=1e-6)
+    if n_kv != n_heads:
+        z_v = z_v.repeat_interleave(n_heads // n_kv, dim=1)
+    scores = alpha * z_v + (1.0 - alpha) * z_x.unsqueeze(1)
+    return scores, z_x, z_v
+
+
+def window_continuous(win_logits: torch.Tensor, n_min: int, n_max: int) -> torch.Tensor:
+    """w~ = n_min + sigmoid(logit) * (n_max - n_min); dsalt_attention.py:270-275."""
+    return n_min + torch.sigmoid(win_logits) * (n_max - n_min)
+
+
+def quantize_windows(w_cont: np.ndarray | torch.Tensor) -> np.ndarray:
+    """w = max(1, floor(w~)) in fp32, NaN kept (torch clamp semantics)."""
+    w = np.asarray(w_cont.detach().cpu().numpy() if torch.is_tensor(w_cont) else w_cont, dtype=np.float32)
+    out = np.maximum(np.floor(w), np.float32(1.0))
+    out[np.isnan(w)] = np.nan
+    return out.astype(np.float32)
+
+
+def _rank_order(vals: np.ndarray) -> np.ndarray:
+    """Indices of `vals` from the best to the worst pick: NaN first, then descending
+    value (-0 == +0), ties broken by the lower index."""
+    idx = np.arange(vals.shape[0])
+    isnan = np.isnan(vals)
+    v = np.where(isnan, 0.0, vals).astype(np.float64)
+    # lexsort: last key is primary
+    return np.lexsort((idx, -v, ~isnan))
+
+
+def select_landmarks(scores: np.ndarray, w: np.ndarray, cu: np.ndarray, k: int) -> np.ndarray:
+    """Landmark positions [H, S, k] int64 of selectors.py:105-134 with the build's
+    deterministic slot order: selected finite positions ascending, then -1.
+
+    Token j at offset o is covered when o < trunc(w_j) (its score becomes -inf); each
+    (head, sequence) takes the top min(k, L) scores (NaN > +inf > finite, lower index
+    first on ties); non-finite picks (NaN, +/-inf) become -1.
+    """
+    scores = np.asarray(scores, dtype=np.float32)
+    w = np.asarray(w, dtype=np.float32)
+    cu = np.asarray(cu, dtype=np.int64)
+    T, H = scores.shape
+    S = cu.shape[0] - 1
+    out = np.full((H, S, k), -1, dtype=np.int64)
+    for s in range(S):
+        a, b = int(cu[s]), int(cu[s + 1])
+        L = b - a
+        if L <= 0 or k == 0:
+            continue
+        off = np.arange(L)
+        with np.errstate(invalid="ignore"):
+            covered = (off + 1).astype(np.float32) <= w[a:b]  # off < trunc(w)
+        k_eff = min(k, L)
+        for h in range(H):
+            vals = scores[a:b, h].copy()
+            vals[covered] = -np.inf
+            order = _rank_order(vals)[:k_eff]
+            picked = order[np.isfinite(vals[order])]
+            picked.sort()
+            out[h, s, :picked.shape[0]] = picked
+    return out
+
+
+def _covered(o: int, wv: float) -> bool:
+    """Token at offset o is covered when o < trunc(w); NaN covers nothing, +inf all."""
+    if math.isnan(wv):
+        return False
+    if math.isinf(wv):
+        return wv > 0
+    return o < math.trunc(wv)
+
+
+def select_landmarks_bruteforce(scores, w, cu, k):
+    """Pure-Python version of select_landmarks (one full sort per (head, sequence) by an
+    explicit comparison key), used to pin the vectorised one on small inputs."""
+    scores = np.asarray(scores, dtype=np.float32)
+    w = [float(v) for v in np.asarray(w, dtype=np.float32)]
+    cu = [int(c) for c in cu]
+    H = scores.shape[1]
+    S = len(cu) - 1
+    res = np.full((H, S, k), -1, dtype=np.int64)
+    for s in range(S):
+        a, b = cu[s], cu[s + 1]
+        L = b - a
+        for h in range(H):
+            cand = []
+            for o in range(L):
+                v = -math.inf if _covered(o, w[a + o]) else float(scores[a + o, h])
+                cand.append((0, 0.0, o, v) if math.isnan(v) else (1, -v, o, v))
+            cand.sort()
+            picked = sorted(o for _, _, o, v in cand[:min(k, L)] if math.isfinite(v))
+            res[h, s, :len(picked)] = picked
+    return res
+
+
+# ---------------------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------------------
+
+
+def _seq_attention(qs, ks, vs, band_bias, band_ok, lk, lv, lmk_logit_bias, lmk_ok, scale):
+    """Softmax over [band keys | landmark slots] for one sequence, all heads.
+
+    qs [H,R,D] (R query rows), ks/vs [H,L,D]; band_bias [R,L] or scalar; band_ok [R,L]
+    bool; lk/lv [H,k,D]; lmk_logit_bias [H,1,k]; lmk_ok [H,R,k] bool.
+    Returns (O [H,R,D], LSE [H,R])."""
+    logits_b = torch.matmul(qs, ks.transpose(-1, -2)) * scale + band_bias
+    logits_b = logits_b.masked_fill(~band_ok, float("-inf"))
+    parts = [logits_b]
+    if lk is not None:
+        logits_l = torch.matmul(qs, lk.transpose(-1, -2)) * scale + lmk_logit_bias
+        logits_l = logits_l.masked_fill(~lmk_ok, float("-inf"))
+        parts.append(logits_l)
+    logits = torch.cat(parts, dim=-1)
+    lse = torch.logsumexp(logits, dim=-1)
+    nonempty = torch.isfinite(lse)
+    lse_safe = torch.where(nonempty, lse, torch.zeros_like(lse))
+    p = torch.exp(logits - lse_safe.unsqueeze(-1))
+    L = ks.shape[1]
+    o = torch.matmul(p[..., :L], vs)
+    if lk is not None:
+        o = o + torch.matmul(p[..., L:], lv)
+    return o, lse
+
+
+def _gather_landmarks(ks, vs, pos_hk, L):
+    valid = (pos_hk >= 0) & (pos_hk < L)
+    pc = pos_hk.clamp(0, max(L - 1, 0))
+    idx = pc.unsqueeze(-1).expand(-1, -1, ks.shape[-1])
+    lk = torch.gather(ks, 1, idx)
+    lv = torch.gather(vs, 1, idx)
+    return lk, lv, valid
+
+
+def attention_hard(q, k, v, w, lmk_pos, lmk_bias, cu, scale=None, rows=None):
+    """HARD sparse attention (dsalt_triton_attn.py:69-169).
+
+    q/k/v [T,H,D] (any float dtype; computed in their dtype, use fp64 for the oracle);
+    w [T] window sizes, w(i) = max(1, trunc(w)); lmk_pos [H,S,k] int; lmk_bias [H,S,k]
+    or None. Band: j in [i-w+1, i]; landmark slot p: 0 <= p <= i - w, logit bias
+    lmk_bias. Returns (O [T,H,D], LSE [T,H]) with O = 0, LSE = -inf on empty rows.
+    Differentiable in q, k, v and lmk_bias. ``rows=(r0, r1)`` restricts every sequence
+    to its query offsets [r0, r1) (the outputs then hold only those rows).
+    """
+    T, H, D = q.shape
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    cu = [int(c) for c in (cu.tolist() if torch.is_tensor(cu) else cu)]
+    S = len(cu) - 1
+    kl = 0 if lmk_pos is None else lmk_pos.shape[-1]
+    w_np = np.asarray(w.detach().cpu().numpy() if torch.is_tensor(w) else w, dtype=np.float32)
+    outs, lses = [], []
+    for s in range(S):
+        a, b = cu[s], cu[s + 1]
+        L = b - a
+        if L == 0:
+            continue
+        r0, r1 = (0, L) if rows is None else (min(rows[0], L), min(rows[1], L))
+        if r1 <= r0:
+            continue
+        qs = q[a + r0:a + r1].transpose(0, 1)
+        ks, vs = (t[a:b].transpose(0, 1) for t in (k, v))
+        ws = w_np[a + r0:a + r1]
+        with np.errstate(invalid="ignore"):
+            wi = np.where(ws >= 1, np.trunc(np.minimum(ws, 2 ** 30)), 1).astype(np.int64)
+        wi_t = torch.from_numpy(wi)
+        i = torch.arange(r0, r1)
+        j = torch.arange(L)
+        lo = i - wi_t + 1
+        band_ok = (j[None, :] <= i[:, None]) & (j[None, :] >= lo[:, None])
+        lk = lv = lb = lmk_ok = None
+        if kl > 0:
+            pos = lmk_pos[:, s, :].to(torch.long).cpu()
+            lk, lv, valid = _gather_landmarks(ks, vs, pos, L)
+            lmk_ok = valid[:, None, :] & (pos[:, None, :] < lo[None, :, None])
+            lb = (lmk_bias[:, s, :].unsqueeze(1).to(q.dtype) if lmk_bias is not None
+                  else torch.zeros((H, 1, kl), dtype=q.dtype))
+        o, lse = _seq_attention(qs, ks, vs, 0.0, band_ok, lk, lv, lb, lmk_ok, scale)
+        outs.append(o.transpose(0, 1))
+        lses.append(lse.transpose(0, 1))
+    if not outs:
+        return q.new_zeros((0, H, D)), q.new_zeros((0, H))
+    return torch.cat(outs, 0), torch.cat(lses, 0)
+
+
+def attention_soft(q, k, v, w_cont, lmk_pos, lmk_logw, cu, tau_win=1.0, win_edge=4.0, scale=None,
+                   rows=None):
+    """SOFT sparse attention (dsalt_triton_train.py:116-214).
+
+    Band 0 <= d = i - j <= w~(i) (fp32 compare), bias 0 when d <= w~ - win_edge (fp32
+    difference) else log sigmoid((w~ - d)/tau_win); landmark p admitted when p <= i and
+    (float)p < (float)i - w~(i), bias lmk_logw. Differentiable in q, k, v, lmk_logw and
+    w_cont (through the edge bias only; the set membership is a step function).
+    ``rows=(r0, r1)`` restricts every sequence to its query offsets [r0, r1).
+    """
+    T, H, D = q.shape
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    cu = [int(c) for c in (cu.tolist() if torch.is_tensor(cu) else cu)]
+    S = len(cu) - 1
+    kl = 0 if lmk_pos is None else lmk_pos.shape[-1]
+    w32_all = w_cont.detach().to(torch.float32).cpu()
+    outs, lses = [], []
+    for s in range(S):
+        a, b = cu[s], cu[s + 1]
+        L = b - a
+        if L == 0:
+            continue
+        r0, r1 = (0, L) if rows is None else (min(rows[0], L), min(rows[1], L))
+        if r1 <= r0:
+            continue
+        qs = q[a + r0:a + r1].transpose(0, 1)
+        ks, vs = (t[a:b].transpose(0, 1) for t in (k, v))
+        w32 = w32_all[a + r0:a + r1]
+        w_hi = w_cont[a + r0:a + r1].to(q.dtype)
+        i = torch.arange(r0, r1)
+        j = torch.arange(L)
+        d32 = (i[:, None] - j[None, :]).to(torch.float32)
+        band_ok = (j[None, :] <= i[:, None]) & (d32 <= w32[:, None])
+        core = d32 <= (w32 - torch.tensor(win_edge, dtype=torch.float32))[:, None]
+        z = (w_hi[:, None] - d32.to(q.dtype)) / tau_win
+        edge = F.logsigmoid(z)
+        band_bias = torch.where(core, torch.zeros_like(edge), edge)
+        band_bias = torch.where(band_ok, band_bias, torch.zeros_like(band_bias))
+        lk = lv = lb = lmk_ok = None
+        if kl > 0:
+            pos = lmk_pos[:, s, :].to(torch.long).cpu()
+            lk, lv, valid = _gather_landmarks(ks, vs, pos, L)
+            thr = i.to(torch.float32) - w32  # (float)i - w~
+            lmk_ok = (valid[:, None, :] & (pos[:, None, :] <= i[None, :, None])
+                      & (pos.to(torch.float32)[:, None, :] < thr[None, :, None]))
+            lw = lmk_logw[:, s, :].to(q.dtype)
+            lb = torch.where(torch.isfinite(lw), lw, torch.zeros_like(lw)).unsqueeze(1)
+            lmk_ok = lmk_ok & torch.isfinite(lw)[:, None, :]
+        o, lse = _seq_attention(qs, ks, vs, band_bias, band_ok, lk, lv, lb, lmk_ok, scale)
+        outs.append(o.transpose(0, 1))
+        lses.append(lse.transpose(0, 1))
+    if not outs:
+        return q.new_zeros((0, H, D)), q.new_zeros((0, H))
+    return torch.cat(outs, 0), torch.cat(lses, 0)
+
+
+def effective_pairs(mode: str, w, lmk_pos, cu, H: int) -> int:
+    """Exact number of (query, key) pairs of the sparse pattern (band + admitted
+    landmark slots), summed over heads: the P of F_fwd = 4*D*P."""
+    cu = [int(c) for c in (cu.tolist() if torch.is_tensor(cu) else cu)]
+    w = np.asarray(w.detach().cpu().numpy() if torch.is_tensor(w) else w, dtype=np.float32)
+    pos = None if lmk_pos is None else np.asarray(lmk_pos.detach().cpu().numpy() if torch.is_tensor(lmk_pos) else lmk_pos)
+    total = 0
+    for s in range(len(cu) - 1):
+        a, b = cu[s], cu[s + 1]
+        L = b - a
+        if L == 0:
+            continue
+        i = np.arange(L)
+        ws = w[a:b]
+        if mode == "hard":
+            with np.errstate(invalid="ignore"):
+                wi = np.where(ws >= 1, np.trunc(np.minimum(ws, 2 ** 30)), 1).astype(np.int64)
+            band = np.minimum(wi, i + 1)
+            pmax = i - wi  # admissible p <= pmax
+        else:
+            with np.errstate(invalid="ignore"):
+                fw = np.where(ws >= 0, np.floor(np.minimum(ws, 2 ** 30)), -1).astype(np.int64)
+            band = np.clip(np.minimum(fw + 1, i + 1), 0, None)
+            t = i.astype(np.float32) - ws
+            with np.errstate(invalid="ignore"):
+                pmax = np.where(np.isnan(t), -1, np.minimum(i, np.ceil(t).astype(np.int64) - 1))
+        total += int(band.sum()) * H
+        if pos is not None and pos.shape[-1] > 0:
+            for h in range(H):
+                p = pos[h, s]
+                p = p[(p >= 0) & (p < L)]
+                if p.size:
+                    total += int((p[None, :] <= pmax[:, None]).sum())
+    return total
+
+
+# ---------------------------------------------------------------------------------------
+# CPU baseline: the reference's dense masked-SDPA fallback, restated
+# ---------------------------------------------------------------------------------------
+
+
+def hard_mask(L: int, w: np.ndarray, pos_hk: np.ndarray) -> torch.Tensor:
+    """[H, L, L] boolean HARD mask of one sequence: band [i-w+1, i] plus landmark
+    columns p <= i - w (the set of dsalt_triton_attn.py:100-135)."""
+    i = torch.arange(L)
+    with np.errstate(invalid="ignore"):
+        wi = torch.from_numpy(np.where(w >= 1, np.trunc(np.minimum(w, 2 ** 30)), 1).astype(np.int64))
+    lo = i - wi + 1
+    band = (i[None, :] <= i[:, None]) & (i[None, :] >= lo[:, None])
+    H = pos_hk.shape[0]
+    col = torch.zeros((H, L + 1), dtype=torch.bool)
+    p = torch.from_numpy(np.where((pos_hk >= 0) & (pos_hk < L), pos_hk, L).astype(np.int64))
+    col.scatter_(1, p, True)
+    lmk = col[:, None, :L] & (i[None, None, :] < lo[None, :, None])
+    return band.unsqueeze(0) | lmk
+
+
+def cpu_baseline_hard(q32, k32, v32, w, lmk_pos, cu, seqs=None):
+    """Dense masked SDPA in fp32 on the CPU for the listed sequences (default: all):
+    per sequence, build the [H,L,L] HARD mask as an additive -inf mask and run
+    F.scaled_dot_product_attention - the cost model of the reference's CPU path.
+    Returns the list of per-sequence outputs [L,H,D]."""
+    cu = [int(c) for c in cu]
+    w = np.asarray(w, dtype=np.float32)
+    pos = np.asarray(lmk_pos)
+    outs = []
+    for s in (range(len(cu) - 1) if seqs is None else seqs):
+        a, b = cu[s], cu[s + 1]
+        L = b - a
+        mask = hard_mask(L, w[a:b], pos[:, s, :])
+        additive = torch.zeros(mask.shape, dtype=torch.float32).masked_fill_(~mask, float("-inf"))
+        qs, ks, vs = (t[a:b].transpose(0, 1).unsqueeze(0) for t in (q32, k32, v32))
+        o = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=additive.unsqueeze(0))
+        outs.append(o.squeeze(0).transpose(0, 1))
+    return outs

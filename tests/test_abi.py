@@ -1,0 +1,112 @@
+"""The C-ABI library: it loads, exports every function include/dsalt_hip.h declares, its
+argument structs match the ctypes mirror, and host-side validation rejects bad
+arguments. No device memory is touched (validation reads no device data). CPU only."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import dsalt._hip as hip
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dsalt_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(dsalt_\w+)\s*\(", text, re.M)))
+
+
+def test_library_built_and_loads():
+    assert os.path.exists(hip.LIB_PATH), "run dsalt-library_amd/build.py"
+    hip.lib()
+    hip.check_abi()
+
+
+def test_exports_every_declared_symbol():
+    names = declared_functions()
+    assert len(names) >= 13
+    lib = ctypes.CDLL(hip.LIB_PATH)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(hip.EXPORTED_SYMBOLS) <= set(names)
+
+
+def test_struct_sizes():
+    lib = hip.lib()
+    assert ctypes.sizeof(hip.FwdArgs) == lib.dsalt_fwd_args_size()
+    assert ctypes.sizeof(hip.BwdArgs) == lib.dsalt_bwd_args_size()
+    assert ctypes.sizeof(hip.SelectArgs) == lib.dsalt_select_args_size()
+
+
+def _fake_fwd(**kw):
+    a = hip.FwdArgs()
+    a.mode, a.dtype, a.total_len, a.num_seqs, a.n_heads, a.head_dim, a.k_lmk = 0, 0, 256, 2, 4, 64, 16
+    base = 0x10000000
+    for i, name in enumerate(("q", "k", "v", "out", "lse", "w", "lmk_pos", "cu_seqlens")):
+        setattr(a, name, base + i * 0x100000)
+    a.q_stride_t = a.k_stride_t = a.v_stride_t = a.out_stride_t = 4 * 64
+    a.q_stride_h = a.k_stride_h = a.v_stride_h = a.out_stride_h = 64
+    a.lse_stride_t, a.lse_stride_h, a.w_stride = 4, 1, 1
+    a.lmk_pos_stride_h, a.lmk_pos_stride_s, a.lmk_pos_stride_k = 32, 16, 1
+    a.scale, a.tau_win, a.win_edge = 0.125, 1.0, 4.0
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _check(a):
+    lib = hip.lib()
+    rc = lib.dsalt_fwd_check(ctypes.byref(a))
+    return rc, lib.dsalt_last_error().decode()
+
+
+def test_fwd_check_accepts_valid_args():
+    assert _check(_fake_fwd()) == (0, "") or _check(_fake_fwd())[0] == 0
+
+
+@pytest.mark.parametrize("field,value,code,needle", [
+    ("head_dim", 96, 2, "head_dim"),
+    ("mode", 7, 1, "mode"),
+    ("dtype", 5, 1, "dtype"),
+    ("k_lmk", 5000, 2, "k_lmk"),
+    ("num_seqs", 0, 1, "num_seqs"),
+    ("q", None, 1, "q is NULL"),
+    ("lmk_pos", None, 1, "lmk_pos"),
+    ("q", 0x10000008, 1, "aligned"),
+    ("k_stride_t", 250, 1, "strides"),
+    ("tau_win", 0.0, 1, "tau_win"),
+])
+def test_fwd_check_rejects(field, value, code, needle):
+    kw = {field: value}
+    if field == "tau_win":
+        kw["mode"] = 1
+    rc, msg = _check(_fake_fwd(**kw))
+    assert rc == code and needle in msg, (rc, msg)
+
+
+def test_bwd_workspace_and_check():
+    lib = hip.lib()
+    assert lib.dsalt_bwd_workspace_size(1024, 2, 8, 64, 16) >= 0
+    assert lib.dsalt_bwd_workspace_size(-1, 2, 8, 64, 16) == -1
+    a = hip.BwdArgs()
+    a.mode, a.dtype, a.total_len, a.num_seqs, a.n_heads, a.head_dim = 0, 0, 128, 1, 2, 128
+    assert lib.dsalt_bwd_check(ctypes.byref(a)) != 0
+
+
+def test_select_check():
+    lib = hip.lib()
+    a = hip.SelectArgs()
+    a.total_len, a.num_seqs, a.n_heads, a.k_lmk = 100, 1, 2, 2000
+    a.scores, a.w, a.cu_seqlens, a.lmk_pos = 0x1000, 0x2000, 0x3000, 0x4000
+    assert lib.dsalt_select_check(ctypes.byref(a)) == 2
+    a.k_lmk = 16
+    assert lib.dsalt_select_check(ctypes.byref(a)) == 0
+
+
+def test_cpu_tensors_raise():
+    import torch
+    q = torch.zeros(8, 1, 64, dtype=torch.bfloat16)
+    with pytest.raises(hip.DsaltError, match="ROCm GPU"):
+        hip.fwd(0, q, q, q, torch.ones(8), None, None, torch.tensor([0, 8], dtype=torch.int32), 0.125)

@@ -1,0 +1,230 @@
+"""Forward parity: HIP sparse attention (through the C ABI via dsalt._hip) against the
+fp64 CPU oracle on the same bf16/fp16 inputs. Tolerance (north star): max-abs 2e-2 and
+relative L2 1e-2 of the outputs; LSE within 2e-2 and -inf exactly on empty rows."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import dsalt._hip as hip
+from oracle import dsalt_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, REL_L2, LSE_ABS = 2e-2, 1e-2, 2e-2
+
+
+def close(got, ref, what, max_abs=MAX_ABS, rel_l2=REL_L2):
+    got, ref = got.double().cpu(), ref.double().cpu()
+    diff = got - ref
+    ma = diff.abs().max().item() if diff.numel() else 0.0
+    rl = (diff.norm() / ref.norm().clamp_min(1e-30)).item() if diff.numel() else 0.0
+    assert ma <= max_abs and rl <= rel_l2, f"{what}: max-abs {ma:.3e}, rel-L2 {rl:.3e}"
+
+
+def lse_close(got, ref, what):
+    got, ref = got.double().cpu(), ref.double().cpu()
+    fin = torch.isfinite(ref)
+    assert torch.equal(torch.isfinite(got), fin), f"{what}: empty-row pattern differs"
+    if fin.any():
+        d = (got[fin] - ref[fin]).abs().max().item()
+        assert d <= LSE_ABS, f"{what}: LSE max-abs {d:.3e}"
+
+
+def make_inputs(lens, H, D, k, mode, seed, dtype=torch.bfloat16, n_min=8, n_max=64,
+                lmk_kind="random"):
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T, S = int(cu[-1]), len(lens)
+    q, kk, v = (torch.randn(T, H, D, generator=g).to(dtype) for _ in range(3))
+    w_cont = (n_min + torch.rand(T, generator=g) * (n_max - n_min)).float()
+    w = w_cont.floor().clamp(min=1) if mode == hip.MODE_HARD else w_cont
+    pos = np.full((H, S, k), -1, dtype=np.int64)
+    for h in range(H):
+        for s, L in enumerate(lens):
+            if L == 0 or k == 0:
+                continue
+            if lmk_kind == "random":
+                c = rng.choice(L, size=min(k, L), replace=False)
+                pos[h, s, :len(c)] = c  # unsorted
+            elif lmk_kind == "messy":  # unsorted, duplicates, -1 holes, out-of-range
+                c = rng.integers(-2, L + 3, size=k)
+                pos[h, s] = c
+    pos = torch.from_numpy(pos)
+    if mode == hip.MODE_HARD:
+        bias = torch.randn(H, S, k, generator=g)
+    else:
+        bias = torch.nn.functional.logsigmoid(torch.randn(H, S, k, generator=g) / 2)
+        bias = torch.where(pos >= 0, bias, torch.full_like(bias, float("-inf")))
+    return q, kk, v, w, pos, bias, torch.from_numpy(cu).to(torch.int32)
+
+
+def run_hip(mode, q, k, v, w, pos, bias, cu, **kw):
+    dev = torch.device("cuda", 0)
+    qd, kd, vd = (t.to(dev) for t in (q, k, v))
+    posd = pos.to(dev) if pos is not None and pos.shape[-1] > 0 else None
+    biasd = bias.to(dev) if posd is not None and bias is not None else None
+    out, lse = hip.fwd(mode, qd, kd, vd, w.to(dev), posd, biasd, cu.to(dev), 1.0 / math.sqrt(q.shape[-1]), **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu(), lse.cpu()
+
+
+def run_oracle(mode, q, k, v, w, pos, bias, cu, rows=None, **kw):
+    q64, k64, v64 = (t.double() for t in (q, k, v))
+    if mode == hip.MODE_HARD:
+        return orc.attention_hard(q64, k64, v64, w, pos, None if bias is None else bias.double(), cu.tolist(),
+                                  rows=rows)
+    return orc.attention_soft(q64, k64, v64, w.double(), pos, None if bias is None else bias.double(),
+                              cu.tolist(), rows=rows, **kw)
+
+
+CASES = [
+    # lens, H, D, k, n_min, n_max, lmk_kind
+    ([1, 2, 3, 130], 2, 64, 5, 1, 9, "random"),
+    ([300, 77, 513], 3, 128, 20, 8, 96, "random"),
+    ([200, 0, 129], 2, 64, 100, 4, 40, "messy"),
+    ([64, 191], 2, 128, 0, 1, 300, "random"),
+    ([1024], 8, 64, 16, 64, 256, "random"),
+]
+
+
+@pytest.mark.parametrize("mode", [hip.MODE_HARD, hip.MODE_SOFT], ids=["hard", "soft"])
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_fwd_matches_oracle(mode, case):
+    lens, H, D, k, n_min, n_max, kind = CASES[case]
+    print(f"fwd case={case} mode={mode} lens={lens} H={H} D={D} k={k}", flush=True)
+    q, kk, v, w, pos, bias, cu = make_inputs(lens, H, D, k, mode, seed=case, n_min=n_min, n_max=n_max,
+                                             lmk_kind=kind)
+    out, lse = run_hip(mode, q, kk, v, w, pos, bias, cu)
+    o_ref, l_ref = run_oracle(mode, q, kk, v, w, pos, bias, cu)
+    close(out, o_ref, f"out case {case}")
+    lse_close(lse, l_ref, f"lse case {case}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_fwd_dtypes(dtype):
+    lens, H, D, k = [257, 100], 2, 64, 12
+    q, kk, v, w, pos, bias, cu = make_inputs(lens, H, D, k, hip.MODE_HARD, seed=7, dtype=dtype, n_max=120)
+    out, lse = run_hip(hip.MODE_HARD, q, kk, v, w, pos, bias, cu)
+    o_ref, l_ref = run_oracle(hip.MODE_HARD, q, kk, v, w, pos, bias, cu)
+    close(out, o_ref, f"out {dtype}")
+    lse_close(lse, l_ref, f"lse {dtype}")
+
+
+def test_fwd_soft_edges_and_empty_rows():
+    # integral w~ (exact band j >= i - w~), negative w~ (empty band), tiny w~ (edge only)
+    lens, H, D, k = [150], 2, 64, 8
+    q, kk, v, w, pos, bias, cu = make_inputs(lens, H, D, k, hip.MODE_SOFT, seed=8, n_min=2, n_max=30)
+    w = w.clone()
+    w[::3] = w[::3].floor()           # integral windows
+    w[5:20] = -3.0                     # no band keys
+    w[20:30] = 0.5                     # only d = 0, on the soft edge
+    out, lse = run_hip(hip.MODE_SOFT, q, kk, v, w, pos, bias, cu, tau_win=0.7, win_edge=3.0)
+    o_ref, l_ref = run_oracle(hip.MODE_SOFT, q, kk, v, w, pos, bias, cu, tau_win=0.7, win_edge=3.0)
+    close(out, o_ref, "soft edges")
+    lse_close(lse, l_ref, "soft edges lse")
+
+
+def test_fwd_full_window_equals_causal_sdpa():
+    lens, H, D = [333], 4, 128
+    q, kk, v, _, _, _, cu = make_inputs(lens, H, D, 0, hip.MODE_HARD, seed=9)
+    w = torch.full((333,), 1e6)
+    out, _ = run_hip(hip.MODE_HARD, q, kk, v, w, None, None, cu)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        *(t.double().transpose(0, 1) for t in (q, kk, v)), is_causal=True).transpose(0, 1)
+    close(out, ref, "causal")
+
+
+def test_fwd_strided_operands():
+    # q/k/v as views of one [T, 3, H, D] buffer (row stride 3*H*D), output written in place
+    T, H, D = 300, 4, 64
+    g = torch.Generator().manual_seed(10)
+    qkv = torch.randn(T, 3, H, D, generator=g).to(torch.bfloat16)
+    q, kk, v = qkv[:, 0], qkv[:, 1], qkv[:, 2]
+    cu = torch.tensor([0, 120, 300], dtype=torch.int32)
+    w = (torch.rand(T, generator=g) * 50 + 1).floor()
+    pos = torch.stack([torch.stack([torch.randperm(120, generator=g)[:10], torch.randperm(180, generator=g)[:10]])
+                       for _ in range(H)])
+    bias = torch.randn(H, 2, 10, generator=g)
+    dev = torch.device("cuda", 0)
+    qkv_d = qkv.to(dev)
+    out = torch.empty(T, H, 2 * D, device=dev, dtype=torch.bfloat16)[:, :, :D]  # strided output
+    o, lse = hip.fwd(hip.MODE_HARD, qkv_d[:, 0], qkv_d[:, 1], qkv_d[:, 2], w.to(dev), pos.to(dev), bias.to(dev),
+                     cu.to(dev), 1.0 / math.sqrt(D), out=out)
+    torch.cuda.synchronize()
+    o_ref, _ = run_oracle(hip.MODE_HARD, q, kk, v, w, pos, bias, cu)
+    close(o.float().cpu(), o_ref, "strided")
+
+
+@pytest.mark.parametrize("cfg", ["c2", "c4"])
+def test_fwd_headline_shapes_on_row_subsets(cfg):
+    # full-size launches; the oracle checks a window of query rows of every sequence
+    if cfg == "c2":
+        lens, H, D, k, n_min, n_max, rows = [2048] * 4, 16, 64, 64, 32, 512, (1536, 1792)
+    else:
+        lens, H, D, k, n_min, n_max, rows = [16384], 16, 128, 128, 64, 1024, (15872, 16128)
+    print(f"fwd headline {cfg}", flush=True)
+    q, kk, v, w, pos, bias, cu = make_inputs(lens, H, D, k, hip.MODE_HARD, seed=11, n_min=n_min, n_max=n_max)
+    out, lse = run_hip(hip.MODE_HARD, q, kk, v, w, pos, bias, cu)
+    o_ref, l_ref = run_oracle(hip.MODE_HARD, q, kk, v, w, pos, bias, cu, rows=rows)
+    sel = torch.cat([torch.arange(int(cu[s]) + rows[0], int(cu[s]) + rows[1]) for s in range(len(lens))])
+    close(out[sel], o_ref, cfg)
+    lse_close(lse[sel], l_ref, cfg + " lse")
+
+
+# ------------------------------------------------------------------- selection
+
+def _select_case(seed, lens, H, tie=True):
+    rng = np.random.default_rng(seed)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(cu[-1])
+    scores = rng.standard_normal((T, H)).astype(np.float32)
+    if tie:
+        scores = np.round(scores * 4) / 4
+        scores[rng.random((T, H)) < 0.02] = np.nan
+        scores[rng.random((T, H)) < 0.02] = np.inf
+        scores[rng.random((T, H)) < 0.02] = -np.inf
+        scores[rng.random((T, H)) < 0.02] = -0.0
+    w = (rng.random(T) * 60).astype(np.float32)
+    w[rng.random(T) < 0.02] = np.nan
+    return scores, w, cu
+
+
+@pytest.mark.parametrize("lens,H,k", [
+    ([50, 0, 7, 300], 4, 16),
+    ([2048] * 4, 16, 64),
+    ([1448, 783, 749, 1864, 1814, 555, 722, 1355], 16, 64),
+    ([20000, 33], 2, 128),     # longer than the LDS key cache
+    ([5, 900], 3, 1024),
+])
+@pytest.mark.parametrize("tie", [True, False], ids=["ties", "distinct"])
+def test_select_bit_exact(lens, H, k, tie):
+    print(f"select lens={lens[:3]} H={H} k={k} tie={tie}", flush=True)
+    scores, w, cu = _select_case(len(lens) * 31 + k, lens, H, tie)
+    dev = torch.device("cuda", 0)
+    got = hip.select_landmarks(torch.from_numpy(scores).to(dev), torch.from_numpy(w).to(dev),
+                               torch.from_numpy(cu).to(torch.int32).to(dev), k).cpu().numpy()
+    np.testing.assert_array_equal(got, orc.select_landmarks(scores, w, cu, k))
+
+
+def test_select_strided_scores():
+    scores, w, cu = _select_case(5, [100, 60], 8)
+    dev = torch.device("cuda", 0)
+    big = torch.zeros(scores.shape[0], 16, device=dev)
+    big[:, ::2] = torch.from_numpy(scores).to(dev)
+    got = hip.select_landmarks(big[:, ::2], torch.from_numpy(w).to(dev), torch.from_numpy(cu).int().to(dev), 9)
+    np.testing.assert_array_equal(got.cpu().numpy(), orc.select_landmarks(scores, w, cu, 9))
+
+
+def test_quantize_bit_exact():
+    rng = np.random.default_rng(1)
+    w = np.concatenate([rng.random(10000).astype(np.float32) * 600 - 50,
+                        np.array([np.nan, 1.0, 0.999999, 2 ** 31, -np.inf, np.inf], dtype=np.float32)])
+    dev = torch.device("cuda", 0)
+    wq, wi = hip.quantize_windows(torch.from_numpy(w).to(dev), want_int=True)
+    ref = orc.quantize_windows(w)
+    np.testing.assert_array_equal(wq.cpu().numpy(), ref)
+    exp_i = np.where(w >= 1, np.minimum(np.floor(np.nan_to_num(w, posinf=2 ** 30)), 2 ** 30), 1).astype(np.int32)
+    np.testing.assert_array_equal(wi.cpu().numpy(), exp_i)
