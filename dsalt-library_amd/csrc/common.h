@@ -135,6 +135,49 @@ __device__ __forceinline__ bool find_block(const int32_t *__restrict__ cu, int n
     return false;
 }
 
+enum { kHard = 0, kSoft = 1 };
+
+// Key ranges of query offset i (all inclusive, relative to its sequence) given its
+// window value wv:
+//   lo     first band key           HARD: max(0, i - w + 1), w = max(1, trunc(wv)), NaN -> 1
+//                                   SOFT: max(0, i - floor(w~)); i + 1 (empty) if w~ < 0 / NaN
+//   corelo first zero-bias key      HARD: lo; SOFT: i - floor(w~ - win_edge) (fp32 difference),
+//                                   i + 1 when that difference is negative
+//   pmax   largest admissible landmark position (-1: none)
+//                                   HARD: p <= i - w            (dsalt_triton_attn.py:133-135)
+//                                   SOFT: p <= i and (float)p < (float)i - w~ (dsalt_triton_train.py:183-185)
+// The SOFT band 0 <= i-j <= w~ (dsalt_triton_train.py:147-150) is j >= i - floor(w~) for
+// integer j, and the core test d <= w~ - win_edge (:154) is j >= i - floor(w~ - win_edge).
+template <int MODE>
+__device__ __forceinline__ void query_ranges(int i, float wv, float win_edge, int &lo, int &corelo,
+                                             int &pmax) {
+    if (MODE == kHard) {
+        const int wi = (wv >= 1.f) ? (int)fminf(wv, 1073741824.f) : 1;
+        lo = max(0, i - wi + 1);
+        corelo = lo;
+        pmax = lo - 1;
+    } else {
+        lo = (wv >= 0.f) ? max(0, i - (int)floorf(fminf(wv, 1073741824.f))) : i + 1;
+        const float wce = wv - win_edge;
+        corelo = (wce >= 0.f) ? i - (int)floorf(fminf(wce, 1073741824.f)) : i + 1;
+        corelo = max(corelo, lo);
+        const float t = (float)i - wv;  // p admissible <=> p <= ceil(t) - 1 (and p <= i)
+        pmax = (t == t) ? (int)fminf(fmaxf(ceilf(fminf(t, 1073741824.f)) - 1.f, -1.f), (float)i) : -1;
+    }
+}
+
+// Soft window edge of key distance d for continuous window w~: returns
+// log2(sigmoid(z)) with z = (w~ - d) / tau (the logit bias log sigmoid(z) in log2 units,
+// dsalt_triton_train.py:152-155) and, through `one_minus_sig`, 1 - sigmoid(z), which is
+// tau * d(log sigmoid(z))/d w~ (dsalt_triton_train.py:370-373).
+__device__ __forceinline__ float soft_edge_log2(float wc, float d, float inv_tau, float &one_minus_sig) {
+    const float z = (wc - d) * inv_tau;
+    const float e = __builtin_amdgcn_exp2f(-z * kLog2e);  // exp(-z)
+    const float onep = 1.f + e;
+    one_minus_sig = e / onep;
+    return -__builtin_amdgcn_logf(onep);
+}
+
 // Workgroup index remap for the 8 XCDs of MI355X. Consecutive hardware workgroup ids
 // are dispatched round-robin over the XCDs; remapping them so that each XCD receives a
 // contiguous range of logical ids keeps neighbouring query/key blocks (which share

@@ -30,8 +30,6 @@ namespace {
 constexpr int kKPad = 8;          // K tile row = D + 8 halves: conflict-free b128 reads
 constexpr int kVPad = 4;          // V^T tile row = 64 + 4 halves: conflict-free b64 reads
 constexpr float kStaleMax = 8.0f;  // allowed growth of the row max before a rescale (log2)
-enum { kHard = 0, kSoft = 1 };
-
 struct FwdParams {
     const uint16_t *q, *k, *v;
     uint16_t *o;
@@ -95,25 +93,9 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     // lo: first band key; corelo: first key of the zero-bias core; pmax: largest
     // admissible landmark position (-1: none). All inclusive, relative to the sequence.
     const float wv = qvalid ? p.w[tok_i * p.w_st] : 0.f;
+    const float wc = wv;
     int lo, corelo, pmax;
-    float wc = wv;
-    if (MODE == kHard) {
-        // w = max(1, trunc(w)); NaN -> 1 (dsalt_triton_attn.py:69-70, :282)
-        const int wi = (wv >= 1.f) ? (int)fminf(wv, 1073741824.f) : 1;
-        lo = max(0, i - wi + 1);
-        corelo = lo;
-        pmax = lo - 1;  // p <= i - w  <=>  p < i - w + 1 (dsalt_triton_attn.py:133-135)
-    } else {
-        // band 0 <= i-j <= w~  <=>  j >= i - floor(w~) (dsalt_triton_train.py:147-150)
-        lo = (wc >= 0.f) ? max(0, i - (int)floorf(fminf(wc, 1073741824.f))) : i + 1;
-        // core i-j <= w~ - win_edge, the difference taken in fp32 (:154)
-        const float wce = wc - p.win_edge;
-        corelo = (wce >= 0.f) ? i - (int)floorf(fminf(wce, 1073741824.f)) : i + 1;
-        corelo = max(corelo, lo);
-        // landmark: p <= i and (float)p < (float)i - w~ (:183-185)  <=>  p <= ceil(t)-1
-        const float t = (float)i - wc;
-        pmax = (t == t) ? (int)fminf(fmaxf(ceilf(fminf(t, 1073741824.f)) - 1.f, -1.f), (float)i) : -1;
-    }
+    query_ranges<MODE>(i, wv, p.win_edge, lo, corelo, pmax);
     const int wlo = wave_min(qvalid ? lo : INT_MAX);
     const int whi = wave_max(qvalid ? i : -1);
     const int wclo = wave_max(qvalid ? corelo : INT_MIN);
@@ -270,10 +252,9 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
                             for (int r = 0; r < 16; ++r) {
                                 const int cst = rb * 32 + acc_row_const(r);
                                 float x = sacc[rb][r] * c;
-                                if (cst < Bc) {
-                                    // log sigmoid((w~ - d)/tau) in log2 units, d = i - key
-                                    const float z = (wc - (float)(A - cst)) * p.inv_tau;
-                                    x -= fast_log2(1.f + fast_exp2(-z * kLog2e));
+                                if (cst < Bc) {  // soft edge, d = i - key = A - cst
+                                    float oms;
+                                    x += soft_edge_log2(wc, (float)(A - cst), p.inv_tau, oms);
                                 }
                                 sacc[rb][r] = (cst > A || cst < B) ? -INFINITY : x;
                             }
