@@ -147,6 +147,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="first run 3 plain device copies of this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)",
@@ -156,6 +158,14 @@ def main():
     from dsalt import _hip
 
     dev = torch.device("cuda", 0)
+    if args.copy_calib_mib > 0:
+        n = args.copy_calib_mib * (1 << 20) // 4
+        src = torch.randn(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     wl = make_workload(args.config, dev)
     q, k, v, w, lmk, cu = wl["q"], wl["k"], wl["v"], wl["w"], wl["lmk"], wl["cu"]
     T, H, D = wl["T"], wl["H"], wl["D"]
@@ -163,9 +173,7 @@ def main():
     lse = torch.empty((T, H), device=dev, dtype=torch.float32)
     scale = 1.0 / math.sqrt(D)
 
-    def step():
-        _hip.fwd(_hip.MODE_HARD, q, k, v, w, lmk, None, cu, scale, out=out, lse=lse)
-
+    step = _hip.FwdLauncher(_hip.MODE_HARD, q, k, v, w, lmk, None, cu, scale, out=out, lse=lse)
     ms = time_launches(step, args.steps, args.warmup)
 
     # selection + quantisation (the rest of the inference hot path), reported alongside

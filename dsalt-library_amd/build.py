@@ -24,6 +24,7 @@ HIPCC_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-ffp-contract=fast", "-Wall", "-Wno-unused-result",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",  # MFMA C/D in VGPRs: no accvgpr copies for softmax
 ]
 
 

@@ -72,7 +72,12 @@ int dsalt_fwd_check(const dsalt_fwd_args *a) {
     if ((rc = check_tensor("q", a->q, a->q_stride_t, a->q_stride_h, 8))) return rc;
     if ((rc = check_tensor("k", a->k, a->k_stride_t, a->k_stride_h, 8))) return rc;
     if ((rc = check_tensor("v", a->v, a->v_stride_t, a->v_stride_h, 8))) return rc;
-    if ((rc = check_tensor("out", a->out, a->out_stride_t, a->out_stride_h, 4))) return rc;
+    if (a->out_dtype != a->dtype && a->out_dtype != DSALT_DTYPE_F32)
+        return fail(DSALT_ERR_INVALID, "out_dtype must equal dtype or be DSALT_DTYPE_F32 (got %d)", a->out_dtype);
+    {  // rows are written 4 elements at a time; check_tensor counts 16-bit elements
+        const int64_t m = a->out_dtype == DSALT_DTYPE_F32 ? 2 : 1;
+        if ((rc = check_tensor("out", a->out, a->out_stride_t * m, a->out_stride_h * m, (int)(4 * m)))) return rc;
+    }
     if (!a->lse) return fail(DSALT_ERR_INVALID, "lse is NULL");
     if (a->mode == DSALT_MODE_SOFT && !(a->tau_win > 0.f))
         return fail(DSALT_ERR_INVALID, "tau_win must be > 0 (got %g)", (double)a->tau_win);
@@ -135,11 +140,21 @@ int dsalt_bwd_check(const dsalt_bwd_args *a) {
     if ((rc = check_tensor("q", a->q, a->q_stride_t, a->q_stride_h, 8))) return rc;
     if ((rc = check_tensor("k", a->k, a->k_stride_t, a->k_stride_h, 8))) return rc;
     if ((rc = check_tensor("v", a->v, a->v_stride_t, a->v_stride_h, 8))) return rc;
-    if ((rc = check_tensor("out", a->out, a->out_stride_t, a->out_stride_h, 8))) return rc;
+    if (a->out_dtype != a->dtype && a->out_dtype != DSALT_DTYPE_F32)
+        return fail(DSALT_ERR_INVALID, "out_dtype must equal dtype or be DSALT_DTYPE_F32 (got %d)", a->out_dtype);
+    {  // O rows are read 8 elements at a time (16 bytes in 16-bit types, 32 in fp32)
+        const int64_t m = a->out_dtype == DSALT_DTYPE_F32 ? 2 : 1;
+        if ((rc = check_tensor("out", a->out, a->out_stride_t * m, a->out_stride_h * m, 8))) return rc;
+    }
     if ((rc = check_tensor("dout", a->dout, a->dout_stride_t, a->dout_stride_h, 8))) return rc;
-    if ((rc = check_tensor("dq", a->dq, a->dq_stride_t, a->dq_stride_h, 4))) return rc;
-    if ((rc = check_tensor("dk", a->dk, a->dk_stride_t, a->dk_stride_h, 4))) return rc;
-    if ((rc = check_tensor("dv", a->dv, a->dv_stride_t, a->dv_stride_h, 4))) return rc;
+    if (a->grad_dtype != a->dtype && a->grad_dtype != DSALT_DTYPE_F32)
+        return fail(DSALT_ERR_INVALID, "grad_dtype must equal dtype or be DSALT_DTYPE_F32 (got %d)", a->grad_dtype);
+    // gradient rows are written 4 elements at a time (8 bytes in 16-bit types, 16 in fp32)
+    const int gv = a->grad_dtype == DSALT_DTYPE_F32 ? 8 : 4;  // check_tensor counts 16-bit elements
+    const int64_t gm = a->grad_dtype == DSALT_DTYPE_F32 ? 2 : 1;
+    if ((rc = check_tensor("dq", a->dq, a->dq_stride_t * gm, a->dq_stride_h * gm, gv))) return rc;
+    if ((rc = check_tensor("dk", a->dk, a->dk_stride_t * gm, a->dk_stride_h * gm, gv))) return rc;
+    if ((rc = check_tensor("dv", a->dv, a->dv_stride_t * gm, a->dv_stride_h * gm, gv))) return rc;
     if (!a->lse) return fail(DSALT_ERR_INVALID, "lse is NULL");
     if (a->mode == DSALT_MODE_SOFT && !(a->tau_win > 0.f))
         return fail(DSALT_ERR_INVALID, "tau_win must be > 0 (got %g)", (double)a->tau_win);

@@ -1,17 +1,894 @@
-// Sparse-attention backward for gfx950 (placeholder until the kernels land).
+// DSALT sparse-attention backward for gfx950 (HARD and SOFT semantics), deterministic
+// and atomic-free.
+//
+// Reference semantics: _train_bwd_preprocess / _train_bwd_kernel / _train_bwd_dkdv_kernel
+// (dsalt/kernels/dsalt_triton_train.py:220-481) and _dsalt_bwd_preprocess /
+// _dsalt_bwd_kernel (dsalt/kernels/dsalt_triton_bwd.py:17-216):
+//   P = exp(logit - LSE), dP = dO . V^T, Delta_i = sum_d O_i dO_i, dS = P (dP - Delta)
+//   dQ = scale * dS K, dK = scale * dS^T Q, dV = P^T dO
+//   d_bias[h,s,slot] = sum_i dS[i, slot]                                   (:325-327)
+//   d_w~[i] = sum_h sum_{edge keys j} dS[i, j] (1 - sigmoid(z_ij)) / tau_win  (:370-373, :748)
+// The reference adds landmark dK/dV, d_bias and d_w~ with atomics; here every output
+// element is produced by exactly one thread, in a fixed order.
+//
+// Kernels, launched in this order on one stream:
+//   prep    one workgroup per 128-token block: Delta for all heads, and the smallest band
+//           start of the block (bounds the key-parallel query scan of `kv`).
+//   lmk_kv  key-parallel over landmark slots: one workgroup per (head, sequence, 64 slots);
+//           4 waves = 2 slot groups x 2 query sub-blocks scan the sequence's queries in
+//           64-query LDS tiles. Writes landmark dK/dV partials (workspace) and d_bias.
+//   dq      query-parallel, 4 waves x 32 queries per workgroup, the forward's tiling (band
+//           tiles, then gathered landmark tiles); S^T, dP^T and dQ^T on MFMA. Writes dQ and
+//           the per-head soft-edge d_w~ (workspace).
+//   kv      key-parallel band dK/dV, 4 waves x 32 keys per workgroup, scanning 64-query LDS
+//           tiles from the key block to the last query block whose band reaches it; adds
+//           the landmark partials of keys that are landmark positions; its head-0
+//           workgroups also reduce d_w~ over heads.
+// Every MFMA is v_mfma_f32_32x32x16 with operands in the layouts of the forward kernel:
+// a lane owns one column (query or key) of each 32x32 block and 16 rows of it.
 #include "common.h"
 #include "launch.h"
 
 namespace dsalt {
+namespace {
+
+constexpr int kPad8 = 8;  // row-major tile row padding (halves): conflict-free b128 reads
+constexpr int kPad4 = 4;  // transposed tile row padding (halves): conflict-free b64 reads
+constexpr int kBM = 128;  // queries (dq) / keys (kv) per workgroup; prep block size
+constexpr int kTN = 64;   // keys per tile (dq) / queries per tile (kv, lmk_kv)
+
+struct BwdParams {
+    const uint16_t *q, *k, *v, *dout;
+    const void *o;  // forward output: fp32 if o_f32, else the compute dtype
+    const float *lse, *w;
+    const int64_t *lmk_pos;
+    const float *lmk_bias;
+    const int32_t *cu;
+    void *dq, *dk, *dv;  // gradient outputs: fp32 if grad_f32, else the compute dtype
+    float *d_bias, *d_w;
+    float *ws_delta;         // [T*H]
+    int *ws_minlo;           // [n_qblk]
+    float *ws_dwh;           // [T*H] or null
+    float *ws_ldk, *ws_ldv;  // [H*S*k_pad*D] or null
+    int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, do_st, do_sh, lse_st, lse_sh, w_st;
+    int64_t lp_sh, lp_ss, lp_sk, lb_sh, lb_ss, lb_sk;
+    int64_t dq_st, dq_sh, dk_st, dk_sh, dv_st, dv_sh;
+    int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid_q, n_lgrp, grad_f32, o_f32;
+    float scale, scale_log2, inv_tau, win_edge;
+};
+
+__device__ __forceinline__ uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+// A operand of a k-step over 16 tokens from a transposed tile row: 4 tokens at `at` and
+// 4 at `at + 8` (the token order of the packed P/dS registers, see the forward kernel).
+template <typename vec8>
+__device__ __forceinline__ vec8 ld_tr_operand(const uint16_t *at) {
+    const uint2 a = *reinterpret_cast<const uint2 *>(at);
+    const uint2 b = *reinterpret_cast<const uint2 *>(at + 8);
+    return bitcast<vec8>(make_uint4(a.x, a.y, b.x, b.y));
+}
+
+// Store D/32 transposed 32x32 accumulator blocks (lane = row token, registers = head-dim
+// (r/4)*8 + hh*4 + r%4) times `mul` as one row of a gradient tensor: fp32 when `f32`,
+// else the 16-bit compute dtype.
+template <typename DT, int ND>
+__device__ __forceinline__ void store_row(void *base, int64_t off, bool f32, const f32x16 (&acc)[ND],
+                                          float mul, int hh) {
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int dd = d * 32 + g * 8 + hh * 4;
+            if (f32) {
+                *reinterpret_cast<float4 *>(static_cast<float *>(base) + off + dd) =
+                    make_float4(acc[d][g * 4] * mul, acc[d][g * 4 + 1] * mul, acc[d][g * 4 + 2] * mul,
+                                acc[d][g * 4 + 3] * mul);
+            } else {
+                uint2 val;
+                val.x = DT::pack2(acc[d][g * 4 + 0] * mul, acc[d][g * 4 + 1] * mul);
+                val.y = DT::pack2(acc[d][g * 4 + 2] * mul, acc[d][g * 4 + 3] * mul);
+                *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(base) + off + dd) = val;
+            }
+        }
+}
+
+template <typename DT>
+__device__ __forceinline__ void pack_block(const f32x16 &x, uint32_t (&pk)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pk[j] = DT::pack2(x[2 * j], x[2 * j + 1]);
+}
+
+// ==================================================================================
+// prep: Delta = rowsum(O * dO) for all heads and the block's smallest band start
+// ==================================================================================
+template <typename DT, int D, int MODE>
+__global__ void __launch_bounds__(256) bwd_prep_kernel(const BwdParams p) {
+    __shared__ int s_min[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int seq, blk;
+    if (!find_block(p.cu, p.num_seqs, blockIdx.x, kBM, lane, seq, blk)) return;
+    const int seq_start = p.cu[seq];
+    const int seq_len = p.cu[seq + 1] - seq_start;
+    const int base = blk * kBM;
+    const int nvalid = min(kBM, seq_len - base);
+
+    int lo = INT_MAX;
+    if (tid < nvalid) {
+        const int i = base + tid;
+        int corelo, pmax;
+        query_ranges<MODE>(i, p.w[((int64_t)seq_start + i) * p.w_st], p.win_edge, lo, corelo, pmax);
+    }
+    lo = wave_min(lo);
+    if (lane == 0) s_min[wave] = lo;
+
+    // Delta uses O as stored (fp32 when the forward wrote fp32) and dO in the compute dtype
+    // (dsalt_triton_train.py:673-674)
+    constexpr int G = D / 8;  // lanes per (token, head) pair, 8 elements each
+    const int H = p.n_heads;
+    const int npairs = nvalid * H;
+    const int c = tid % G;
+    for (int pp = tid / G; pp < npairs; pp += 256 / G) {
+        const int t = pp / H, h = pp - t * H;
+        const int64_t tok = (int64_t)seq_start + base + t;
+        const int64_t ooff = tok * p.o_st + (int64_t)h * p.o_sh + c * 8;
+        const uint4 d8 = ld16(p.dout + tok * p.do_st + (int64_t)h * p.do_sh + c * 8);
+        const uint16_t *de = reinterpret_cast<const uint16_t *>(&d8);
+        float of[8];
+        if (p.o_f32) {
+            const float4 a = *reinterpret_cast<const float4 *>(static_cast<const float *>(p.o) + ooff);
+            const float4 b = *reinterpret_cast<const float4 *>(static_cast<const float *>(p.o) + ooff + 4);
+            of[0] = a.x; of[1] = a.y; of[2] = a.z; of[3] = a.w;
+            of[4] = b.x; of[5] = b.y; of[6] = b.z; of[7] = b.w;
+        } else {
+            const uint4 o8 = ld16(static_cast<const uint16_t *>(p.o) + ooff);
+            const uint16_t *oe = reinterpret_cast<const uint16_t *>(&o8);
+#pragma unroll
+            for (int x = 0; x < 8; ++x) of[x] = DT::to_f32(oe[x]);
+        }
+        float acc = 0.f;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) acc = fmaf(of[x], DT::to_f32(de[x]), acc);
+#pragma unroll
+        for (int o = G / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+        if (c == 0) p.ws_delta[tok * H + h] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) p.ws_minlo[blockIdx.x] = min(min(s_min[0], s_min[1]), min(s_min[2], s_min[3]));
+}
+
+// ==================================================================================
+// dq: query-parallel dQ (band + landmarks) and per-head soft-edge d_w~
+// ==================================================================================
+template <typename DT, int D, int MODE>
+__global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
+    typedef typename DT::vec8 vec8;
+    constexpr int BN = kTN;
+    constexpr int KS = D / 16, ND = D / 32, CPR = D / 8, PER_T = BN * CPR / 256;
+
+    __shared__ __align__(16) uint16_t ks[2][BN][D + kPad8];
+    __shared__ __align__(16) uint16_t vs[2][BN][D + kPad8];
+    __shared__ __align__(16) uint16_t kt[2][D][BN + kPad4];
+    __shared__ int s_red[4][3];
+    __shared__ int s_ltile[DSALT_MAX_K_LMK / BN];
+    __shared__ int s_nlt;
+    extern __shared__ int s_dyn[];
+    int *s_lpos = s_dyn;
+    float *s_lbias = reinterpret_cast<float *>(s_dyn + p.k_pad);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ql = lane & 31, hh = lane >> 5;
+    const int logical = xcd_remap(blockIdx.x, p.grid_q);
+    const int head = logical / p.n_qblk;
+    if (head >= p.n_heads) return;
+    int seq, blk;
+    if (!find_block(p.cu, p.num_seqs, logical - head * p.n_qblk, kBM, lane, seq, blk)) return;
+    const int seq_start = p.cu[seq];
+    const int seq_len = p.cu[seq + 1] - seq_start;
+    const int i = blk * kBM + wave * 32 + ql;
+    const bool qvalid = i < seq_len;
+    const int64_t tok_i = (int64_t)seq_start + i;
+
+    vec8 qv[KS], dov[KS];
+    {
+        const uint16_t *qp = p.q + tok_i * p.q_st + (int64_t)head * p.q_sh + hh * 8;
+        const uint16_t *dp = p.dout + tok_i * p.do_st + (int64_t)head * p.do_sh + hh * 8;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            uint4 a = make_uint4(0, 0, 0, 0), b = a;
+            if (qvalid) {
+                a = ld16(qp + s * 16);
+                b = ld16(dp + s * 16);
+            }
+            qv[s] = bitcast<vec8>(a);
+            dov[s] = bitcast<vec8>(b);
+        }
+    }
+    const float lsev = qvalid ? p.lse[tok_i * p.lse_st + (int64_t)head * p.lse_sh] : -INFINITY;
+    const float lse2 = (lsev == -INFINITY) ? INFINITY : lsev * kLog2e;  // +inf: every P is 0
+    const float delta = qvalid ? p.ws_delta[tok_i * p.n_heads + head] : 0.f;
+
+    const float wc = qvalid ? p.w[tok_i * p.w_st] : 0.f;
+    int lo, corelo, pmax;
+    query_ranges<MODE>(i, wc, p.win_edge, lo, corelo, pmax);
+    const int wlo = wave_min(qvalid ? lo : INT_MAX);
+    const int whi = wave_max(qvalid ? i : -1);
+    const int wclo = wave_max(qvalid ? corelo : INT_MIN);
+    const int wchi = wave_min(qvalid ? i : INT_MAX);
+    const int wpmax = wave_max(qvalid ? pmax : -1);
+
+    for (int s = tid; s < p.k_pad; s += 256) {
+        int pos = INT_MAX;
+        float b = 0.f;
+        if (s < p.k_lmk) {
+            const int64_t pp = p.lmk_pos[head * p.lp_sh + seq * p.lp_ss + s * p.lp_sk];
+            if (pp >= 0 && pp < seq_len) {
+                pos = (int)pp;
+                if (p.lmk_bias) b = p.lmk_bias[head * p.lb_sh + seq * p.lb_ss + s * p.lb_sk] * kLog2e;
+            }
+        }
+        s_lpos[s] = pos;
+        s_lbias[s] = b;
+    }
+    if (lane == 0) {
+        s_red[wave][0] = wlo;
+        s_red[wave][1] = whi;
+        s_red[wave][2] = wpmax;
+    }
+    __syncthreads();
+    const int glo = min(min(s_red[0][0], s_red[1][0]), min(s_red[2][0], s_red[3][0]));
+    const int ghi = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
+    const int gpmax = max(max(s_red[0][2], s_red[1][2]), max(s_red[2][2], s_red[3][2]));
+    if (wave == 0) {
+        int n = 0;
+        for (int lt = 0; lt < p.k_pad / BN; ++lt) {
+            if (wave_min(s_lpos[lt * BN + lane]) <= gpmax) {
+                if (lane == 0) s_ltile[n] = lt;
+                ++n;
+            }
+        }
+        if (lane == 0) s_nlt = n;
+    }
+    __syncthreads();
+    const int nb = (ghi >= glo) ? (ghi - glo) / BN + 1 : 0;
+    const int nt = nb + s_nlt;
+
+    uint4 kr[PER_T], vr[PER_T];
+    auto load_tile = [&](int t) {
+        const bool band = t < nb;
+        const int tb = glo + t * BN;
+        const int lt = band ? 0 : s_ltile[t - nb];
+#pragma unroll
+        for (int u = 0; u < PER_T; ++u) {
+            const int c = tid + u * 256;
+            const int row = c / CPR, col = c % CPR;
+            const int key = band ? tb + row : s_lpos[lt * BN + row];
+            const bool ok = band ? key < seq_len : key != INT_MAX;
+            uint4 kx = make_uint4(0, 0, 0, 0), vx = kx;
+            if (ok) {
+                const int64_t tok = (int64_t)seq_start + key;
+                kx = ld16(p.k + tok * p.k_st + (int64_t)head * p.k_sh + col * 8);
+                vx = ld16(p.v + tok * p.v_st + (int64_t)head * p.v_sh + col * 8);
+            }
+            kr[u] = kx;
+            vr[u] = vx;
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < PER_T; ++u) {
+            const int c = tid + u * 256;
+            const int row = c / CPR, col = c % CPR;
+            *reinterpret_cast<uint4 *>(&ks[buf][row][col * 8]) = kr[u];
+            *reinterpret_cast<uint4 *>(&vs[buf][row][col * 8]) = vr[u];
+            const uint16_t *e = reinterpret_cast<const uint16_t *>(&kr[u]);
+#pragma unroll
+            for (int x = 0; x < 8; ++x) kt[buf][col * 8 + x][row] = e[x];
+        }
+    };
+
+    f32x16 dqacc[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dqacc[d][r] = 0.f;
+    float dw = 0.f;
+    const float c = p.scale_log2;
+
+    if (nt > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    __syncthreads();
+    for (int t = 0; t < nt; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < nt) load_tile(t + 1);
+        const bool band = t < nb;
+        const int tb = glo + t * BN;
+        int lt = 0;
+        bool active;
+        if (band) {
+            active = (tb <= whi) && (tb + BN - 1 >= wlo);
+        } else {
+            lt = s_ltile[t - nb];
+            active = wave_min(s_lpos[lt * BN + lane]) <= wpmax;
+        }
+        if (active) {
+            f32x16 sacc[2], pacc[2];
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+                f32x16 a0, a1;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) a0[r] = a1[r] = 0.f;
+#pragma unroll
+                for (int s = 0; s < KS; ++s) {
+                    const vec8 ka = bitcast<vec8>(ld16(&ks[buf][rb * 32 + ql][s * 16 + hh * 8]));
+                    const vec8 va = bitcast<vec8>(ld16(&vs[buf][rb * 32 + ql][s * 16 + hh * 8]));
+                    a0 = DT::mfma(ka, qv[s], a0);
+                    a1 = DT::mfma(va, dov[s], a1);
+                }
+                sacc[rb] = a0;
+                pacc[rb] = a1;
+            }
+            // dS (into sacc): P = exp2(logit2 - lse2) on admitted pairs, dS = P (dP - Delta)
+            if (band) {
+                const int A = i - tb - hh * 4;
+                const int B = lo - tb - hh * 4;
+                const bool need_lo = tb < wclo;
+                const bool need_hi = tb + BN - 1 > wchi;
+                if (MODE == kSoft && need_lo) {
+                    const int Bc = corelo - tb - hh * 4;
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int cst = rb * 32 + acc_row_const(r);
+                            float oms;
+                            const float edge = soft_edge_log2(wc, (float)(A - cst), p.inv_tau, oms);
+                            const bool ok = (cst <= A) & (cst >= B);
+                            const bool is_edge = (cst < Bc) & ok;  // exp(-z) may overflow elsewhere
+                            const float x = fmaf(sacc[rb][r], c, is_edge ? edge : 0.f);
+                            const float pr = ok ? fast_exp2(x - lse2) : 0.f;
+                            const float ds = pr * (pacc[rb][r] - delta);
+                            dw += is_edge ? ds * oms : 0.f;
+                            sacc[rb][r] = ds;
+                        }
+                } else {
+                    const int Bm = (need_lo) ? B : INT_MIN;
+                    const int Am = (need_hi) ? A : INT_MAX;
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int cst = rb * 32 + acc_row_const(r);
+                            const bool ok = (cst <= Am) & (cst >= Bm);
+                            const float pr = ok ? fast_exp2(fmaf(sacc[rb][r], c, -lse2)) : 0.f;
+                            sacc[rb][r] = pr * (pacc[rb][r] - delta);
+                        }
+                }
+            } else {
+#pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int slot = lt * BN + rb * 32 + g * 8 + hh * 4;
+                        const int4 pos = *reinterpret_cast<const int4 *>(&s_lpos[slot]);
+                        const float4 bia = *reinterpret_cast<const float4 *>(&s_lbias[slot]);
+                        const int pp[4] = {pos.x, pos.y, pos.z, pos.w};
+                        const float bb[4] = {bia.x, bia.y, bia.z, bia.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int r = g * 4 + e;
+                            const float pr =
+                                (pp[e] <= pmax) ? fast_exp2(fmaf(sacc[rb][r], c, bb[e] - lse2)) : 0.f;
+                            sacc[rb][r] = pr * (pacc[rb][r] - delta);
+                        }
+                    }
+            }
+            // dQ^T (D x 32 queries) += K^T . dS^T
+            uint32_t pk[2][8];
+            pack_block<DT>(sacc[0], pk[0]);
+            pack_block<DT>(sacc[1], pk[1]);
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int rb = kk >> 1, g = kk & 1;
+                const vec8 b = bitcast<vec8>(
+                    make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
+#pragma unroll
+                for (int d = 0; d < ND; ++d)
+                    dqacc[d] = DT::mfma(ld_tr_operand<vec8>(&kt[buf][d * 32 + ql][kk * 16 + hh * 4]), b, dqacc[d]);
+            }
+        }
+        if (t + 1 < nt) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (qvalid) store_row<DT, ND>(p.dq, tok_i * p.dq_st + (int64_t)head * p.dq_sh, p.grad_f32, dqacc, p.scale, hh);
+    if (MODE == kSoft && p.ws_dwh) {
+        const float dwt = half_sum(dw) * p.inv_tau;
+        if (hh == 0 && qvalid) p.ws_dwh[tok_i * p.n_heads + head] = dwt;
+    }
+}
+
+// ==================================================================================
+// kv (LMK = false): key-parallel band dK/dV;  lmk_kv (LMK = true): landmark dK/dV + d_bias
+// ==================================================================================
+template <int D>
+struct KvSmem {
+    uint16_t qs[2][kTN][D + kPad8];
+    uint16_t qt[2][D][kTN + kPad4];
+    uint16_t dos[2][kTN][D + kPad8];
+    uint16_t dot[2][D][kTN + kPad4];
+    float lse2[2][kTN];
+    float del[2][kTN];
+    int lo[2][kTN];   // band start (LMK: largest admissible landmark position)
+    int clo[2][kTN];  // SOFT: core start
+    float wc[2][kTN];
+    int sb[2][2][4];  // per buffer and 32-query sub-block: min lo, max lo, max corelo, max pmax
+    int misc[8];
+};
+
+template <typename DT, int D, int MODE, bool LMK>
+__global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
+    typedef typename DT::vec8 vec8;
+    constexpr int QT = kTN;
+    constexpr int KS = D / 16, ND = D / 32, CPR = D / 8, PER_T = QT * CPR / 256;
+    __shared__ __align__(16) KvSmem<D> sm;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ql = lane & 31, hh = lane >> 5;
+
+    int head, seq, kblk = 0, gbase = 0, q_begin, q_end, slot = 0, sbw = 0, kw = 0;
+    int key = INT_MAX;  // this lane's key position in the sequence (INT_MAX: none)
+    float kbias2 = 0.f;
+    if (!LMK) {
+        const int logical = xcd_remap(blockIdx.x, p.grid_q);
+        head = logical / p.n_qblk;
+        if (head >= p.n_heads) return;
+        const int target = logical - head * p.n_qblk;
+        if (!find_block(p.cu, p.num_seqs, target, kBM, lane, seq, kblk)) return;
+        gbase = target - kblk;
+    } else {
+        const int per_head = p.num_seqs * p.n_lgrp;
+        head = blockIdx.x / per_head;
+        const int rem = blockIdx.x - head * per_head;
+        seq = rem / p.n_lgrp;
+        const int gp = rem - seq * p.n_lgrp;
+        sbw = wave & 1;
+        slot = gp * 64 + (wave >> 1) * 32 + ql;
+    }
+    const int seq_start = p.cu[seq];
+    const int seq_len = p.cu[seq + 1] - seq_start;
+
+    if (!LMK) {
+        const int kb = kblk * kBM;
+        kw = kb + wave * 32;
+        if (kw + ql < seq_len) key = kw + ql;
+        // last 128-query block whose smallest band start reaches this key block
+        const int nbs = (seq_len + kBM - 1) / kBM;
+        int last = kblk;
+        for (int b = kblk + 1 + tid; b < nbs; b += 256)
+            if (p.ws_minlo[gbase + b] <= kb + kBM - 1) last = max(last, b);
+        last = wave_max(last);
+        if (lane == 0) sm.misc[wave] = last;
+        __syncthreads();
+        last = max(max(sm.misc[0], sm.misc[1]), max(sm.misc[2], sm.misc[3]));
+        q_begin = kb;
+        q_end = min(seq_len, (last + 1) * kBM);
+    } else {
+        if (slot < p.k_lmk) {
+            const int64_t pp = p.lmk_pos[head * p.lp_sh + seq * p.lp_ss + slot * p.lp_sk];
+            if (pp >= 0 && pp < seq_len) {
+                key = (int)pp;
+                if (p.lmk_bias) kbias2 = p.lmk_bias[head * p.lb_sh + seq * p.lb_ss + slot * p.lb_sk] * kLog2e;
+            }
+        }
+        // queries admitting a landmark p satisfy q >= p
+        const int mn = wave_min(key);
+        if (lane == 0) sm.misc[wave] = mn;
+        __syncthreads();
+        const int gmin = min(min(sm.misc[0], sm.misc[1]), min(sm.misc[2], sm.misc[3]));
+        q_begin = (gmin == INT_MAX) ? seq_len : gmin;
+        q_end = seq_len;
+    }
+    const bool kvalid = key != INT_MAX;
+    const int wkmin = LMK ? wave_min(key) : kw;
+    const int wkmax = LMK ? wave_max(kvalid ? key : -1) : min(kw + 31, seq_len - 1);
+
+    // this lane's key row as the B operand of S = Q K^T and dP = dO V^T
+    vec8 kreg[KS], vreg[KS];
+    {
+        const int64_t tok = (int64_t)seq_start + (kvalid ? key : 0);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            uint4 a = make_uint4(0, 0, 0, 0), b = a;
+            if (kvalid) {
+                a = ld16(p.k + tok * p.k_st + (int64_t)head * p.k_sh + s * 16 + hh * 8);
+                b = ld16(p.v + tok * p.v_st + (int64_t)head * p.v_sh + s * 16 + hh * 8);
+            }
+            kreg[s] = bitcast<vec8>(a);
+            vreg[s] = bitcast<vec8>(b);
+        }
+    }
+
+    const int ntile = (q_end > q_begin) ? (q_end - q_begin + QT - 1) / QT : 0;
+    uint4 qr[PER_T], dr[PER_T];
+    float pl = INFINITY, pd = 0.f, pw = 0.f;
+    int plo = INT_MAX, pclo = INT_MAX, ppm = -1;
+    auto load_tile = [&](int t) {
+        const int q0 = q_begin + t * QT;
+#pragma unroll
+        for (int u = 0; u < PER_T; ++u) {
+            const int c = tid + u * 256;
+            const int row = c / CPR, col = c % CPR;
+            const int q = q0 + row;
+            uint4 a = make_uint4(0, 0, 0, 0), b = a;
+            if (q < seq_len) {
+                const int64_t tok = (int64_t)seq_start + q;
+                a = ld16(p.q + tok * p.q_st + (int64_t)head * p.q_sh + col * 8);
+                b = ld16(p.dout + tok * p.do_st + (int64_t)head * p.do_sh + col * 8);
+            }
+            qr[u] = a;
+            dr[u] = b;
+        }
+        if (tid < QT) {
+            const int q = q0 + tid;
+            pl = INFINITY;
+            pd = 0.f;
+            pw = 0.f;
+            plo = INT_MAX;
+            pclo = INT_MAX;
+            ppm = -1;
+            if (q < seq_len) {
+                const int64_t tok = (int64_t)seq_start + q;
+                const float lv = p.lse[tok * p.lse_st + (int64_t)head * p.lse_sh];
+                pl = (lv == -INFINITY) ? INFINITY : lv * kLog2e;
+                pd = p.ws_delta[tok * p.n_heads + head];
+                pw = p.w[tok * p.w_st];
+                query_ranges<MODE>(q, pw, p.win_edge, plo, pclo, ppm);
+            }
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < PER_T; ++u) {
+            const int c = tid + u * 256;
+            const int row = c / CPR, col = c % CPR;
+            *reinterpret_cast<uint4 *>(&sm.qs[buf][row][col * 8]) = qr[u];
+            *reinterpret_cast<uint4 *>(&sm.dos[buf][row][col * 8]) = dr[u];
+            const uint16_t *e = reinterpret_cast<const uint16_t *>(&qr[u]);
+            const uint16_t *f = reinterpret_cast<const uint16_t *>(&dr[u]);
+#pragma unroll
+            for (int x = 0; x < 8; ++x) {
+                sm.qt[buf][col * 8 + x][row] = e[x];
+                sm.dot[buf][col * 8 + x][row] = f[x];
+            }
+        }
+        if (tid < QT) {  // wave 0: per-query parameters and per-sub-block summaries
+            sm.lse2[buf][tid] = pl;
+            sm.del[buf][tid] = pd;
+            sm.lo[buf][tid] = LMK ? ppm : plo;
+            sm.clo[buf][tid] = pclo;
+            sm.wc[buf][tid] = pw;
+            const bool v = plo != INT_MAX;
+            int mnlo = v ? plo : INT_MAX, mxlo = v ? plo : INT_MIN, mxclo = v ? pclo : INT_MIN, mxpm = ppm;
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) {  // within each 32-lane half
+                mnlo = min(mnlo, __shfl_xor(mnlo, o));
+                mxlo = max(mxlo, __shfl_xor(mxlo, o));
+                mxclo = max(mxclo, __shfl_xor(mxclo, o));
+                mxpm = max(mxpm, __shfl_xor(mxpm, o));
+            }
+            if ((tid & 31) == 0) {
+                sm.sb[buf][tid >> 5][0] = mnlo;
+                sm.sb[buf][tid >> 5][1] = mxlo;
+                sm.sb[buf][tid >> 5][2] = mxclo;
+                sm.sb[buf][tid >> 5][3] = mxpm;
+            }
+        }
+    };
+
+    f32x16 dk[ND], dv[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dk[d][r] = dv[d][r] = 0.f;
+    float dbias = 0.f;
+    const float c = p.scale_log2;
+
+    if (ntile > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    __syncthreads();
+    for (int t = 0; t < ntile; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < ntile) load_tile(t + 1);
+#pragma unroll
+        for (int sbi = 0; sbi < (LMK ? 1 : 2); ++sbi) {
+            const int sb = LMK ? sbw : sbi;
+            const int qsb = q_begin + t * QT + sb * 32;  // first query of the sub-block
+            bool skip = qsb >= seq_len;
+            if (!LMK) skip = skip || (qsb + 31 < kw) || (sm.sb[buf][sb][0] > wkmax);
+            else skip = skip || (sm.sb[buf][sb][3] < wkmin);
+            if (skip) continue;
+
+            // S and dP (32 queries x 32 keys): lane = key column, registers = query rows
+            f32x16 sacc, pacc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const vec8 qa = bitcast<vec8>(ld16(&sm.qs[buf][sb * 32 + ql][s * 16 + hh * 8]));
+                const vec8 da = bitcast<vec8>(ld16(&sm.dos[buf][sb * 32 + ql][s * 16 + hh * 8]));
+                sacc = DT::mfma(qa, kreg[s], sacc);
+                pacc = DT::mfma(da, vreg[s], pacc);
+            }
+            // register r holds query q = qsb + hh*4 + acc_row_const(r) of the lane's key
+            const int Cj = (kvalid ? key : INT_MAX / 2) - qsb - hh * 4;  // q >= key <=> cst >= Cj
+            const bool need_hi = LMK || (qsb < wkmax);
+            const bool need_lo = LMK || (sm.sb[buf][sb][1] > wkmin);
+            const bool need_edge = (MODE == kSoft) && !LMK && (sm.sb[buf][sb][2] > wkmin);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int qi = sb * 32 + g * 8 + hh * 4;
+                const float4 l4 = *reinterpret_cast<const float4 *>(&sm.lse2[buf][qi]);
+                const float4 d4 = *reinterpret_cast<const float4 *>(&sm.del[buf][qi]);
+                const int4 o4 = *reinterpret_cast<const int4 *>(&sm.lo[buf][qi]);
+                const float la[4] = {l4.x, l4.y, l4.z, l4.w};
+                const float da[4] = {d4.x, d4.y, d4.z, d4.w};
+                const int oa[4] = {o4.x, o4.y, o4.z, o4.w};
+                int ca[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX};
+                float wa[4] = {0.f, 0.f, 0.f, 0.f};
+                if (need_edge) {
+                    const int4 c4 = *reinterpret_cast<const int4 *>(&sm.clo[buf][qi]);
+                    const float4 w4 = *reinterpret_cast<const float4 *>(&sm.wc[buf][qi]);
+                    ca[0] = c4.x; ca[1] = c4.y; ca[2] = c4.z; ca[3] = c4.w;
+                    wa[0] = w4.x; wa[1] = w4.y; wa[2] = w4.z; wa[3] = w4.w;
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = g * 4 + e;
+                    const int cst = acc_row_const(r);
+                    float pr;
+                    if (LMK) {
+                        // landmark admitted: key <= pmax(q) (key = INT_MAX when the slot is empty)
+                        pr = (key <= oa[e]) ? fast_exp2(fmaf(sacc[r], c, kbias2 - la[e])) : 0.f;
+                    } else {
+                        const bool ok = (!need_hi | (cst >= Cj)) & (!need_lo | (oa[e] <= key)) & kvalid;
+                        float x = fmaf(sacc[r], c, -la[e]);
+                        if (MODE == kSoft && need_edge) {
+                            float oms;
+                            const float edge = soft_edge_log2(wa[e], (float)(cst - Cj), p.inv_tau, oms);
+                            x += (key < ca[e]) ? edge : 0.f;
+                        }
+                        pr = ok ? fast_exp2(x) : 0.f;
+                    }
+                    const float ds = pr * (pacc[r] - da[e]);
+                    if (LMK) dbias += ds;
+                    sacc[r] = pr;
+                    pacc[r] = ds;
+                }
+            }
+            uint32_t pkp[8], pks[8];
+            pack_block<DT>(sacc, pkp);
+            pack_block<DT>(pacc, pks);
+            // dV^T += dO^T . P ; dK^T += Q^T . dS   (k-steps over the 32 queries)
+#pragma unroll
+            for (int g = 0; g < 2; ++g) {
+                const vec8 bp = bitcast<vec8>(make_uint4(pkp[g * 4], pkp[g * 4 + 1], pkp[g * 4 + 2], pkp[g * 4 + 3]));
+                const vec8 bs = bitcast<vec8>(make_uint4(pks[g * 4], pks[g * 4 + 1], pks[g * 4 + 2], pks[g * 4 + 3]));
+#pragma unroll
+                for (int d = 0; d < ND; ++d) {
+                    const int col = sb * 32 + g * 16 + hh * 4;
+                    dv[d] = DT::mfma(ld_tr_operand<vec8>(&sm.dot[buf][d * 32 + ql][col]), bp, dv[d]);
+                    dk[d] = DT::mfma(ld_tr_operand<vec8>(&sm.qt[buf][d * 32 + ql][col]), bs, dk[d]);
+                }
+            }
+        }
+        if (t + 1 < ntile) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (!LMK) {
+        // landmark contributions of keys that are landmark positions (computed by lmk_kv)
+        if (p.ws_ldk) {
+            const size_t base = ((size_t)head * p.num_seqs + seq) * p.k_pad;
+            for (int s0 = 0; s0 < p.k_lmk; s0 += 64) {
+                int pos = -1;
+                if (s0 + lane < p.k_lmk) {
+                    const int64_t pp = p.lmk_pos[head * p.lp_sh + seq * p.lp_ss + (s0 + lane) * p.lp_sk];
+                    if (pp >= kw && pp < min(kw + 32, seq_len)) pos = (int)pp;
+                }
+                unsigned long long m = __ballot(pos >= 0);
+                while (m) {
+                    const int b = __ffsll((long long)m) - 1;
+                    m &= m - 1;
+                    const int pb = __shfl(pos, b);
+                    if (key == pb) {
+                        const float *gk = p.ws_ldk + (base + s0 + b) * D;
+                        const float *gv = p.ws_ldv + (base + s0 + b) * D;
+#pragma unroll
+                        for (int d = 0; d < ND; ++d)
+#pragma unroll
+                            for (int g = 0; g < 4; ++g) {
+                                const int dd = d * 32 + g * 8 + hh * 4;
+                                const float4 a = *reinterpret_cast<const float4 *>(gk + dd);
+                                const float4 b4 = *reinterpret_cast<const float4 *>(gv + dd);
+                                dk[d][g * 4 + 0] += a.x; dk[d][g * 4 + 1] += a.y;
+                                dk[d][g * 4 + 2] += a.z; dk[d][g * 4 + 3] += a.w;
+                                dv[d][g * 4 + 0] += b4.x; dv[d][g * 4 + 1] += b4.y;
+                                dv[d][g * 4 + 2] += b4.z; dv[d][g * 4 + 3] += b4.w;
+                            }
+                    }
+                }
+            }
+        }
+        if (kvalid) {
+            const int64_t tok = (int64_t)seq_start + key;
+            store_row<DT, ND>(p.dk, tok * p.dk_st + (int64_t)head * p.dk_sh, p.grad_f32, dk, p.scale, hh);
+            store_row<DT, ND>(p.dv, tok * p.dv_st + (int64_t)head * p.dv_sh, p.grad_f32, dv, 1.f, hh);
+        }
+        if (MODE == kSoft && p.d_w && p.ws_dwh && head == 0 && tid < kBM) {
+            const int tq = kblk * kBM + tid;
+            if (tq < seq_len) {
+                const int64_t tok = (int64_t)seq_start + tq;
+                float acc = 0.f;
+                for (int h = 0; h < p.n_heads; ++h) acc += p.ws_dwh[tok * p.n_heads + h];
+                p.d_w[tok] = acc;
+            }
+        }
+    } else {
+        // combine the two query sub-blocks of each slot group (waves 2g+1 into 2g), fixed order
+        float *red = reinterpret_cast<float *>(&sm.qs[0][0][0]);
+        constexpr int PER_LANE = 2 * ND * 16 + 1;
+        static_assert(2 * 64 * PER_LANE * 4 <= sizeof(sm.qs) + sizeof(sm.qt), "reduction scratch");
+        const int g = wave >> 1;
+        float *mine = red + (size_t)(g * 64 + lane) * PER_LANE;
+        if (sbw == 1) {
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    mine[d * 16 + r] = dk[d][r];
+                    mine[ND * 16 + d * 16 + r] = dv[d][r];
+                }
+            mine[2 * ND * 16] = dbias;
+        }
+        __syncthreads();
+        if (sbw == 0) {
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    dk[d][r] += mine[d * 16 + r];
+                    dv[d][r] += mine[ND * 16 + d * 16 + r];
+                }
+            dbias += mine[2 * ND * 16];
+            const float db = half_sum(dbias);
+            const size_t row = ((size_t)head * p.num_seqs + seq) * p.k_pad + slot;
+            float *gk = p.ws_ldk + row * D;
+            float *gv = p.ws_ldv + row * D;
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int gg = 0; gg < 4; ++gg) {
+                    const int dd = d * 32 + gg * 8 + hh * 4;
+                    *reinterpret_cast<float4 *>(gk + dd) =
+                        make_float4(dk[d][gg * 4], dk[d][gg * 4 + 1], dk[d][gg * 4 + 2], dk[d][gg * 4 + 3]);
+                    *reinterpret_cast<float4 *>(gv + dd) =
+                        make_float4(dv[d][gg * 4], dv[d][gg * 4 + 1], dv[d][gg * 4 + 2], dv[d][gg * 4 + 3]);
+                }
+            if (hh == 0 && slot < p.k_lmk && p.d_bias)
+                p.d_bias[((size_t)head * p.num_seqs + seq) * p.k_lmk + slot] = db;
+        }
+    }
+}
+
+struct WsLayout {
+    size_t delta, minlo, dwh, ldk, ldv, total;
+};
+
+WsLayout ws_layout(int T, int S, int H, int D, int k) {
+    auto al = [](size_t x) { return (x + 255) / 256 * 256; };
+    WsLayout L;
+    size_t off = 0;
+    L.delta = off;
+    off += al((size_t)T * H * 4);
+    L.minlo = off;
+    off += al((size_t)block_upper_bound(T, S, kBM) * 4);
+    L.dwh = off;
+    off += al((size_t)T * H * 4);
+    const size_t kp = (size_t)((k + 63) / 64 * 64);
+    L.ldk = off;
+    off += al((size_t)H * S * kp * D * 4);
+    L.ldv = off;
+    off += al((size_t)H * S * kp * D * 4);
+    L.total = off;
+    return L;
+}
+
+template <typename DT, int D, int MODE>
+hipError_t launch_typed(const BwdParams &p, hipStream_t stream) {
+    hipLaunchKernelGGL((bwd_prep_kernel<DT, D, MODE>), dim3(p.n_qblk), dim3(256), 0, stream, p);
+    if (p.k_lmk > 0)
+        hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, true>), dim3(p.n_heads * p.num_seqs * p.n_lgrp), dim3(256),
+                           0, stream, p);
+    const size_t dyn = (size_t)p.k_pad * (sizeof(int) + sizeof(float));
+    hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE>), dim3(p.grid_q), dim3(256), dyn, stream, p);
+    hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false>), dim3(p.grid_q), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+template <typename DT>
+hipError_t launch_dt(const BwdParams &p, int head_dim, int mode, hipStream_t stream) {
+    if (head_dim == 64)
+        return mode == DSALT_MODE_HARD ? launch_typed<DT, 64, kHard>(p, stream)
+                                       : launch_typed<DT, 64, kSoft>(p, stream);
+    return mode == DSALT_MODE_HARD ? launch_typed<DT, 128, kHard>(p, stream)
+                                   : launch_typed<DT, 128, kSoft>(p, stream);
+}
+
+}  // namespace
 
 int64_t bwd_workspace_bytes(int total_len, int num_seqs, int n_heads, int head_dim, int k_lmk) {
-    (void)total_len; (void)num_seqs; (void)n_heads; (void)head_dim; (void)k_lmk;
-    return 0;
+    return (int64_t)ws_layout(total_len, num_seqs, n_heads, head_dim, k_lmk).total;
 }
 
 hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream) {
-    (void)a; (void)stream;
-    return hipErrorNotSupported;
+    if (a.total_len == 0) {
+        return hipSuccess;
+    }
+    const WsLayout L = ws_layout(a.total_len, a.num_seqs, a.n_heads, a.head_dim, a.k_lmk);
+    char *ws = static_cast<char *>(a.workspace);
+    BwdParams p;
+    p.q = static_cast<const uint16_t *>(a.q);
+    p.k = static_cast<const uint16_t *>(a.k);
+    p.v = static_cast<const uint16_t *>(a.v);
+    p.o = a.out;
+    p.o_f32 = a.out_dtype == DSALT_DTYPE_F32;
+    p.dout = static_cast<const uint16_t *>(a.dout);
+    p.lse = a.lse;
+    p.w = a.w;
+    p.lmk_pos = a.lmk_pos;
+    p.lmk_bias = a.lmk_bias;
+    p.cu = a.cu_seqlens;
+    p.dq = a.dq;
+    p.dk = a.dk;
+    p.dv = a.dv;
+    p.grad_f32 = a.grad_dtype == DSALT_DTYPE_F32;
+    p.d_bias = a.d_lmk_bias;
+    p.d_w = (a.mode == DSALT_MODE_SOFT) ? a.d_w : nullptr;
+    p.ws_delta = reinterpret_cast<float *>(ws + L.delta);
+    p.ws_minlo = reinterpret_cast<int *>(ws + L.minlo);
+    p.ws_dwh = p.d_w ? reinterpret_cast<float *>(ws + L.dwh) : nullptr;
+    p.ws_ldk = a.k_lmk > 0 ? reinterpret_cast<float *>(ws + L.ldk) : nullptr;
+    p.ws_ldv = a.k_lmk > 0 ? reinterpret_cast<float *>(ws + L.ldv) : nullptr;
+    p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
+    p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;
+    p.v_st = a.v_stride_t; p.v_sh = a.v_stride_h;
+    p.o_st = a.out_stride_t; p.o_sh = a.out_stride_h;
+    p.do_st = a.dout_stride_t; p.do_sh = a.dout_stride_h;
+    p.lse_st = a.lse_stride_t; p.lse_sh = a.lse_stride_h;
+    p.w_st = a.w_stride;
+    p.lp_sh = a.lmk_pos_stride_h; p.lp_ss = a.lmk_pos_stride_s; p.lp_sk = a.lmk_pos_stride_k;
+    p.lb_sh = a.lmk_bias_stride_h; p.lb_ss = a.lmk_bias_stride_s; p.lb_sk = a.lmk_bias_stride_k;
+    p.dq_st = a.dq_stride_t; p.dq_sh = a.dq_stride_h;
+    p.dk_st = a.dk_stride_t; p.dk_sh = a.dk_stride_h;
+    p.dv_st = a.dv_stride_t; p.dv_sh = a.dv_stride_h;
+    p.total_len = a.total_len;
+    p.num_seqs = a.num_seqs;
+    p.n_heads = a.n_heads;
+    p.k_lmk = a.k_lmk;
+    p.k_pad = (a.k_lmk + 63) / 64 * 64;
+    p.n_lgrp = p.k_pad / 64;
+    p.n_qblk = block_upper_bound(a.total_len, a.num_seqs, kBM);
+    p.grid_q = (int)(((int64_t)p.n_qblk * a.n_heads + 7) / 8 * 8);
+    p.scale = a.scale;
+    p.scale_log2 = a.scale * kLog2e;
+    p.inv_tau = 1.f / a.tau_win;
+    p.win_edge = a.win_edge;
+    if (a.dtype == DSALT_DTYPE_BF16) return launch_dt<BF16>(p, a.head_dim, a.mode, stream);
+    return launch_dt<F16>(p, a.head_dim, a.mode, stream);
 }
 
 }  // namespace dsalt

@@ -24,6 +24,8 @@
 #include "common.h"
 #include "launch.h"
 
+#include <type_traits>
+
 namespace dsalt {
 namespace {
 
@@ -32,7 +34,7 @@ constexpr int kVPad = 4;          // V^T tile row = 64 + 4 halves: conflict-free
 constexpr float kStaleMax = 8.0f;  // allowed growth of the row max before a rescale (log2)
 struct FwdParams {
     const uint16_t *q, *k, *v;
-    uint16_t *o;
+    void *o;  // [T,H,D]: fp32 if out_f32, else the compute dtype
     float *lse;
     const float *w;
     const int64_t *lmk_pos;
@@ -40,7 +42,7 @@ struct FwdParams {
     const int32_t *cu;
     int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lse_st, lse_sh, w_st;
     int64_t lp_sh, lp_ss, lp_sk, lb_sh, lb_ss, lb_sk;
-    int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid;
+    int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid, out_f32;
     float scale_log2, inv_tau, win_edge;
 };
 
@@ -180,6 +182,55 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
         }
     };
 
+    // Online-softmax update of one 64-key tile (sacc: raw q.k or log2-unit logits, -inf
+    // where masked) followed by O^T += V^T . P^T from LDS buffer `buf`.
+    auto softmax_pv_impl = [&](auto scaled_tag, f32x16 (&sacc)[2], f32x16 (&oacc)[ND], float &m2,
+                               float &lsum, float c, int buf, int ql, int hh) {
+        constexpr bool SCALED = decltype(scaled_tag)::value;
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[rb][r]);
+        tmax = half_max(tmax);
+        const float tm2 = SCALED ? tmax : tmax * c;
+        if (tm2 > m2 + kStaleMax) {
+            const float alpha = fast_exp2(m2 - tm2);
+            lsum *= alpha;
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
+            m2 = tm2;
+        }
+        const float mu = (m2 == -INFINITY) ? 0.f : m2;
+        uint32_t pk[2][8];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float e0 = SCALED ? fast_exp2(sacc[rb][2 * j] - mu) : fast_exp2(fmaf(sacc[rb][2 * j], c, -mu));
+                const float e1 = SCALED ? fast_exp2(sacc[rb][2 * j + 1] - mu)
+                                        : fast_exp2(fmaf(sacc[rb][2 * j + 1], c, -mu));
+                lsum += e0 + e1;
+                pk[rb][j] = DT::pack2(e0, e1);
+            }
+        // O^T (D x 32 queries) += V^T . P^T ; k-step kk covers tile keys kk*16..+15
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int rb = kk >> 1, g = kk & 1;
+            const vec8 b = bitcast<vec8>(
+                make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
+#pragma unroll
+            for (int d = 0; d < ND; ++d) {
+                const uint16_t *row = &vt[buf][d * 32 + ql][kk * 16 + hh * 4];
+                const uint2 lo8 = *reinterpret_cast<const uint2 *>(row);
+                const uint2 hi8 = *reinterpret_cast<const uint2 *>(row + 8);
+                const vec8 a = bitcast<vec8>(make_uint4(lo8.x, lo8.y, hi8.x, hi8.y));
+                oacc[d] = DT::mfma(a, b, oacc[d]);
+            }
+        }
+    };
     f32x16 oacc[ND];
 #pragma unroll
     for (int d = 0; d < ND; ++d)
@@ -225,111 +276,74 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
                 sacc[rb] = acc;
             }
 
-            // masks and biases; `scaled` = values already in log2 logit units
-            bool scaled = false;
+            // masks and biases, then softmax + PV. Two wave-uniform variants: `raw` keeps
+            // q.k in sacc (scale folded into the exponent), `scaled` holds log2-unit logits
+            // (needed when a per-key bias is present: soft window edge or landmarks).
             if (band) {
                 // key offset in the tile of (rb, r) = rb*32 + acc_row_const(r) + hh*4
                 const int A = i - tb - hh * 4;   // key <= i       <=> cst <= A
                 const int B = lo - tb - hh * 4;  // key >= lo      <=> cst >= B
                 const bool need_lo = tb < wclo;
                 const bool need_hi = tb + BN - 1 > wchi;
-                if (MODE == kHard) {
-                    if (need_lo || need_hi) {
+                if (MODE == kSoft && need_lo) {
+                    const int Bc = corelo - tb - hh * 4;  // key >= corelo <=> cst >= Bc
 #pragma unroll
-                        for (int rb = 0; rb < 2; ++rb)
+                    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-                            for (int r = 0; r < 16; ++r) {
-                                const int cst = rb * 32 + acc_row_const(r);
-                                if (cst > A || cst < B) sacc[rb][r] = -INFINITY;
-                            }
-                    }
+                        for (int r = 0; r < 16; ++r) {
+                            const int cst = rb * 32 + acc_row_const(r);
+                            float x = sacc[rb][r] * c;
+                            float oms;
+                            const float edge = soft_edge_log2(wc, (float)(A - cst), p.inv_tau, oms);
+                            x += (cst < Bc) ? edge : 0.f;  // soft edge, d = i - key = A - cst
+                            sacc[rb][r] = ((cst <= A) & (cst >= B)) ? x : -INFINITY;
+                        }
+                    softmax_pv_impl(std::true_type{}, sacc, oacc, m2, lsum, c, buf, ql, hh);
                 } else {
-                    if (need_lo) {
-                        const int Bc = corelo - tb - hh * 4;  // key >= corelo <=> cst >= Bc
+                    if (need_lo && need_hi) {
 #pragma unroll
                         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
                             for (int r = 0; r < 16; ++r) {
                                 const int cst = rb * 32 + acc_row_const(r);
-                                float x = sacc[rb][r] * c;
-                                if (cst < Bc) {  // soft edge, d = i - key = A - cst
-                                    float oms;
-                                    x += soft_edge_log2(wc, (float)(A - cst), p.inv_tau, oms);
-                                }
-                                sacc[rb][r] = (cst > A || cst < B) ? -INFINITY : x;
+                                sacc[rb][r] = ((cst <= A) & (cst >= B)) ? sacc[rb][r] : -INFINITY;
                             }
-                        scaled = true;
+                    } else if (need_lo) {
+#pragma unroll
+                        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const int cst = rb * 32 + acc_row_const(r);
+                                sacc[rb][r] = (cst >= B) ? sacc[rb][r] : -INFINITY;
+                            }
                     } else if (need_hi) {
 #pragma unroll
                         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
                             for (int r = 0; r < 16; ++r) {
                                 const int cst = rb * 32 + acc_row_const(r);
-                                if (cst > A) sacc[rb][r] = -INFINITY;
+                                sacc[rb][r] = (cst <= A) ? sacc[rb][r] : -INFINITY;
                             }
                     }
+                    softmax_pv_impl(std::false_type{}, sacc, oacc, m2, lsum, c, buf, ql, hh);
                 }
             } else {
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int slot = lt * BN + rb * 32 + acc_row_const(r) + hh * 4;
-                        const int pos = s_lpos[slot];
-                        sacc[rb][r] = (pos <= pmax) ? fmaf(sacc[rb][r], c, s_lbias[slot]) : -INFINITY;
+                    for (int g = 0; g < 4; ++g) {
+                        const int slot = lt * BN + rb * 32 + g * 8 + hh * 4;
+                        const int4 pos = *reinterpret_cast<const int4 *>(&s_lpos[slot]);
+                        const float4 bia = *reinterpret_cast<const float4 *>(&s_lbias[slot]);
+                        const int pp[4] = {pos.x, pos.y, pos.z, pos.w};
+                        const float bb[4] = {bia.x, bia.y, bia.z, bia.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int r = g * 4 + e;
+                            sacc[rb][r] = (pp[e] <= pmax) ? fmaf(sacc[rb][r], c, bb[e]) : -INFINITY;
+                        }
                     }
-                scaled = true;
-            }
-
-            // online softmax (base 2, stale maximum)
-            float tmax = -INFINITY;
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[rb][r]);
-            tmax = half_max(tmax);
-            const float tm2 = scaled ? tmax : tmax * c;
-            if (tm2 > m2 + kStaleMax) {
-                const float alpha = fast_exp2(m2 - tm2);
-                lsum *= alpha;
-#pragma unroll
-                for (int d = 0; d < ND; ++d)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
-                m2 = tm2;
-            }
-            const float mu = (m2 == -INFINITY) ? 0.f : m2;
-            uint32_t pk[2][8];
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    float e0, e1;
-                    if (scaled) {
-                        e0 = fast_exp2(sacc[rb][2 * j] - mu);
-                        e1 = fast_exp2(sacc[rb][2 * j + 1] - mu);
-                    } else {
-                        e0 = fast_exp2(fmaf(sacc[rb][2 * j], c, -mu));
-                        e1 = fast_exp2(fmaf(sacc[rb][2 * j + 1], c, -mu));
-                    }
-                    lsum += e0 + e1;
-                    pk[rb][j] = DT::pack2(e0, e1);
-                }
-
-            // O^T (D x 32 queries) += V^T . P^T ; k-step kk covers tile keys kk*16..+15
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const int rb = kk >> 1, g = kk & 1;
-                const vec8 b = bitcast<vec8>(
-                    make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
-#pragma unroll
-                for (int d = 0; d < ND; ++d) {
-                    const uint16_t *row = &vt[buf][d * 32 + ql][kk * 16 + hh * 4];
-                    const uint2 lo8 = *reinterpret_cast<const uint2 *>(row);
-                    const uint2 hi8 = *reinterpret_cast<const uint2 *>(row + 8);
-                    const vec8 a = bitcast<vec8>(make_uint4(lo8.x, lo8.y, hi8.x, hi8.y));
-                    oacc[d] = DT::mfma(a, b, oacc[d]);
-                }
+                softmax_pv_impl(std::true_type{}, sacc, oacc, m2, lsum, c, buf, ql, hh);
             }
         }
 
@@ -342,16 +356,22 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     const bool nonempty = ltot > 1e-9f;
     const float inv = nonempty ? 1.f / ltot : 0.f;
     if (qvalid) {
-        uint16_t *op = p.o + tok_i * p.o_st + (int64_t)head * p.o_sh;
+        const int64_t ooff = tok_i * p.o_st + (int64_t)head * p.o_sh;
 #pragma unroll
         for (int d = 0; d < ND; ++d)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int dd = d * 32 + g * 8 + hh * 4;
-                uint2 val;
-                val.x = DT::pack2(oacc[d][g * 4 + 0] * inv, oacc[d][g * 4 + 1] * inv);
-                val.y = DT::pack2(oacc[d][g * 4 + 2] * inv, oacc[d][g * 4 + 3] * inv);
-                *reinterpret_cast<uint2 *>(op + dd) = val;
+                const float o0 = oacc[d][g * 4 + 0] * inv, o1 = oacc[d][g * 4 + 1] * inv;
+                const float o2 = oacc[d][g * 4 + 2] * inv, o3 = oacc[d][g * 4 + 3] * inv;
+                if (p.out_f32) {
+                    *reinterpret_cast<float4 *>(static_cast<float *>(p.o) + ooff + dd) = make_float4(o0, o1, o2, o3);
+                } else {
+                    uint2 val;
+                    val.x = DT::pack2(o0, o1);
+                    val.y = DT::pack2(o2, o3);
+                    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(p.o) + ooff + dd) = val;
+                }
             }
         if (hh == 0)
             p.lse[tok_i * p.lse_st + (int64_t)head * p.lse_sh] =
@@ -382,7 +402,8 @@ hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream) {
     p.q = static_cast<const uint16_t *>(a.q);
     p.k = static_cast<const uint16_t *>(a.k);
     p.v = static_cast<const uint16_t *>(a.v);
-    p.o = static_cast<uint16_t *>(a.out);
+    p.o = a.out;
+    p.out_f32 = a.out_dtype == DSALT_DTYPE_F32;
     p.lse = a.lse;
     p.w = a.w;
     p.lmk_pos = a.lmk_pos;

@@ -2,9 +2,10 @@
 
 Forward: one HIP launch (fused band + landmark attention, in-kernel landmark gather,
 no output memset). Backward: one ``dsalt_bwd`` call (deterministic, atomic-free).
-Saved for backward: the kernel operands, O in the compute dtype and the fp32 LSE,
-as DSALTAttentionFunction / DSALTTrainFunction do (dsalt_triton_attn.py:300,
-dsalt_triton_train.py:647).
+Saved for backward: the kernel operands, O and the fp32 LSE, as DSALTAttentionFunction /
+DSALTTrainFunction do (dsalt_triton_attn.py:300, dsalt_triton_train.py:647). The
+``dsalt.kernels`` entry points return O in fp32 (like the reference); the kernel writes
+it in fp32 directly, and the backward's Delta = rowsum(O * dO) then uses the unrounded O.
 """
 from __future__ import annotations
 
@@ -15,7 +16,8 @@ import torch
 from .. import _hip
 
 
-def _forward(ctx, mode: int, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens, tau_win, win_edge):
+def _forward(ctx, mode: int, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens, tau_win, win_edge,
+             out_f32: bool = False):
     _hip.require_gpu(q, k, v, w, cu_seqlens)
     if q.dim() != 3:
         raise _hip.DsaltError(f"q must be packed [T, H, D], got {tuple(q.shape)}")
@@ -29,7 +31,8 @@ def _forward(ctx, mode: int, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens, tau_win,
     if lmk_pos is not None and lmk_pos.shape[-1] > 0:
         lp = lmk_pos.detach()
     lb = None if (lmk_bias is None or lp is None) else lmk_bias.detach().float()
-    out, lse = _hip.fwd(mode, q_c, k_c, v_c, w_f, lp, lb, cu_seqlens, scale, tau_win, win_edge)
+    out, lse = _hip.fwd(mode, q_c, k_c, v_c, w_f, lp, lb, cu_seqlens, scale, tau_win, win_edge,
+                        out_dtype=torch.float32 if out_f32 else None)
     ctx.save_for_backward(q_c, k_c, v_c, out, lse, lp, lb, w_f, cu_seqlens)
     ctx.dsalt_mode = mode
     ctx.dsalt_scale = scale
@@ -42,10 +45,13 @@ def _forward(ctx, mode: int, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens, tau_win,
 
 def _backward(ctx, grad_out, need_dw: bool):
     q_c, k_c, v_c, out, lse, lp, lb, w_f, cu = ctx.saved_tensors
+    od = ctx.dsalt_q_dtype
+    # gradients come back in q's dtype; fp32 inputs (computed in fp16) get fp32 gradients
+    # written directly by the kernels
+    gdt = torch.float32 if od == torch.float32 else q_c.dtype
     dq, dk, dv, d_bias, d_w = _hip.bwd(
         ctx.dsalt_mode, q_c, k_c, v_c, out, lse, grad_out, w_f, lp, lb, cu,
-        ctx.dsalt_scale, ctx.dsalt_tau, ctx.dsalt_edge, need_dw=need_dw)
-    od = ctx.dsalt_q_dtype
+        ctx.dsalt_scale, ctx.dsalt_tau, ctx.dsalt_edge, need_dw=need_dw, grad_dtype=gdt)
     return (dq.to(od), dk.to(od), dv.to(od),
             None if d_bias is None else d_bias.to(od),
             None if d_w is None else d_w.to(od))

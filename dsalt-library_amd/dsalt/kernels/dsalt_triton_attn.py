@@ -31,9 +31,8 @@ from .selectors import (  # noqa: F401  (re-exported like the reference, :18-24)
 class DSALTAttentionFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, lmk_indices, lmk_bias, w_sizes, cu_seqlens):
-        out = _sparse._forward(ctx, _hip.MODE_HARD, q, k, v, lmk_indices, lmk_bias, w_sizes,
-                               cu_seqlens, 1.0, 4.0)
-        return out.float()
+        return _sparse._forward(ctx, _hip.MODE_HARD, q, k, v, lmk_indices, lmk_bias, w_sizes,
+                                cu_seqlens, 1.0, 4.0, out_f32=True)
 
     @staticmethod
     def backward(ctx, grad_out):

@@ -42,9 +42,9 @@ def dsalt_triton_backward(
     lp = lmk_pos if lmk_pos is not None and lmk_pos.shape[-1] > 0 else None
     dq, dk, dv, d_bias, _ = _hip.bwd(_hip.MODE_HARD, q_c, k_c, v_c, o_c, lse.float(), grad_out,
                                      w_sizes, lp, None if lp is None else lmk_bias, cu_seqlens,
-                                     float(scale))
+                                     float(scale), grad_dtype=torch.float32)
     if d_bias is None:
         H, S = q.shape[1], cu_seqlens.shape[0] - 1
         d_bias = torch.zeros((H, S, 0 if lmk_pos is None else lmk_pos.shape[-1]),
                              device=q.device, dtype=torch.float32)
-    return dq.float(), dk.float(), dv.float(), d_bias
+    return dq, dk, dv, d_bias

@@ -28,9 +28,8 @@ class DSALTTrainFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, lmk_pos, lmk_logw, w_cont, cu_seqlens, tau_win, win_edge, n_max,
                 cu_list=None):
-        out = _sparse._forward(ctx, _hip.MODE_SOFT, q, k, v, lmk_pos, lmk_logw, w_cont,
-                               cu_seqlens, float(tau_win), float(win_edge))
-        return out.float()
+        return _sparse._forward(ctx, _hip.MODE_SOFT, q, k, v, lmk_pos, lmk_logw, w_cont,
+                                cu_seqlens, float(tau_win), float(win_edge), out_f32=True)
 
     @staticmethod
     def backward(ctx, grad_out):

@@ -49,7 +49,7 @@ enum {
     DSALT_ERR_LAUNCH = 3,      /* the HIP runtime rejected a kernel launch */
 };
 
-enum { DSALT_DTYPE_BF16 = 0, DSALT_DTYPE_F16 = 1 };
+enum { DSALT_DTYPE_BF16 = 0, DSALT_DTYPE_F16 = 1, DSALT_DTYPE_F32 = 2 /* outputs and gradients only */ };
 enum { DSALT_MODE_HARD = 0, DSALT_MODE_SOFT = 1 };
 
 /* Largest k_lmk the kernels accept (landmark slots per head and sequence). */
@@ -62,7 +62,8 @@ enum { DSALT_MODE_HARD = 0, DSALT_MODE_SOFT = 1 };
  *   _train_fwd_kernel  (dsalt/kernels/dsalt_triton_train.py:74-214, launched at :629-645)
  * The landmark K/V gather of _build_landmark_kv (dsalt/kernels/selectors.py:137-159) and
  * the packed block map of _build_seq_block_map (selectors.py:37-67) happen inside the
- * kernel; `out` is written in the input dtype without a prior memset.
+ * kernel; `out` is written (no prior memset) in the input dtype, or in fp32 when
+ * out_dtype = DSALT_DTYPE_F32 (the reference's entry points return O as fp32).
  */
 typedef struct dsalt_fwd_args {
     int32_t mode;      /* DSALT_MODE_HARD or DSALT_MODE_SOFT */
@@ -72,7 +73,7 @@ typedef struct dsalt_fwd_args {
     int32_t n_heads;   /* H >= 1 */
     int32_t head_dim;  /* D, 64 or 128 */
     int32_t k_lmk;     /* landmark slots per (head, sequence), 0..DSALT_MAX_K_LMK */
-    int32_t reserved0;
+    int32_t out_dtype; /* element type of out: `dtype` or DSALT_DTYPE_F32 */
     const void *q;
     int64_t q_stride_t, q_stride_h;
     const void *k;
@@ -112,14 +113,17 @@ int dsalt_fwd_check(const dsalt_fwd_args *args);
  * Deterministic: no atomics; every output element is written by exactly one thread.
  */
 typedef struct dsalt_bwd_args {
-    int32_t mode, dtype, total_len, num_seqs, n_heads, head_dim, k_lmk, reserved0;
+    int32_t mode, dtype, total_len, num_seqs, n_heads, head_dim, k_lmk;
+    int32_t grad_dtype; /* dq/dk/dv element type: `dtype` or DSALT_DTYPE_F32 */
+    int32_t out_dtype;  /* element type of the saved forward output: `dtype` or DSALT_DTYPE_F32 */
+    int32_t reserved0;
     const void *q;
     int64_t q_stride_t, q_stride_h;
     const void *k;
     int64_t k_stride_t, k_stride_h;
     const void *v;
     int64_t v_stride_t, v_stride_h;
-    const void *out; /* forward output (input dtype) */
+    const void *out; /* forward output [T, H, D] in out_dtype */
     int64_t out_stride_t, out_stride_h;
     const float *lse; /* forward LSE [T, H] */
     int64_t lse_stride_t, lse_stride_h;
@@ -132,7 +136,7 @@ typedef struct dsalt_bwd_args {
     const float *lmk_bias;
     int64_t lmk_bias_stride_h, lmk_bias_stride_s, lmk_bias_stride_k;
     const int32_t *cu_seqlens;
-    void *dq; /* [T, H, D] input dtype */
+    void *dq; /* [T, H, D] in grad_dtype */
     int64_t dq_stride_t, dq_stride_h;
     void *dk;
     int64_t dk_stride_t, dk_stride_h;

@@ -228,3 +228,17 @@ def test_quantize_bit_exact():
     np.testing.assert_array_equal(wq.cpu().numpy(), ref)
     exp_i = np.where(w >= 1, np.minimum(np.floor(np.nan_to_num(w, posinf=2 ** 30)), 2 ** 30), 1).astype(np.int32)
     np.testing.assert_array_equal(wi.cpu().numpy(), exp_i)
+
+
+@pytest.mark.parametrize("mode", [hip.MODE_HARD, hip.MODE_SOFT], ids=["hard", "soft"])
+def test_fwd_fp32_output(mode):
+    lens, H, D, k = [300, 45], 3, 128, 10
+    q, kk, v, w, pos, bias, cu = make_inputs(lens, H, D, k, mode, seed=12, n_min=4, n_max=80)
+    dev = torch.device("cuda", 0)
+    out, lse = hip.fwd(mode, q.to(dev), kk.to(dev), v.to(dev), w.to(dev), pos.to(dev), bias.to(dev), cu.to(dev),
+                       1.0 / math.sqrt(D), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32
+    o_ref, l_ref = run_oracle(mode, q, kk, v, w, pos, bias, cu)
+    close(out.cpu(), o_ref, "fp32 out")
+    lse_close(lse.cpu(), l_ref, "fp32 out lse")
