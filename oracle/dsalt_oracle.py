@@ -362,3 +362,106 @@ def cpu_baseline_hard(q32, k32, v32, w, lmk_pos, cu, seqs=None):
         o = F.scaled_dot_product_attention(qs, ks, vs, attn_mask=additive.unsqueeze(0))
         outs.append(o.squeeze(0).transpose(0, 1))
     return outs
+
+
+# ---------------------------------------------------------------------------------------
+# module composition (training, packed): dsalt/modules/dsalt_attention.py:565-608 with
+# _train_selectors (:457-487) and the dense SOFT attention of _packed_train (:489-563)
+# ---------------------------------------------------------------------------------------
+
+
+def rope_cache(seq_len: int, head_dim: int, base: float = 10000.0, scale: float = 1.0, dtype=torch.float64):
+    """(cos, sin) [seq_len, head_dim]: half-split RoPE, positions divided by `scale`
+    (dsalt/kernels/window_utils.py:91-107)."""
+    theta = 1.0 / (base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    pos = torch.arange(seq_len, dtype=torch.float32) / scale
+    emb = torch.cat([torch.outer(pos, theta)] * 2, dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+def rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    half = x.shape[-1] // 2
+    return x * cos + torch.cat([-x[..., half:], x[..., :half]], dim=-1) * sin
+
+
+def module_train_forward(params: dict, cfg: dict, x: torch.Tensor, cu, tau_win=1.0, tau_lmk=2.0,
+                         win_edge=4.0):
+    """Packed training forward of DSALTAttention from its parameters (names as in
+    named_parameters()). Differentiable in x and the parameters (leaf tensors in
+    `params`). Returns (out [T, d_model], selectors (w_cont, lmk_pos, lmk_logw))."""
+    cu = [int(c) for c in cu]
+    T, d_model = x.shape
+    H = cfg["n_heads"]
+    D = d_model // H
+    n_kv = cfg.get("n_kv_heads") or H
+
+    def lin(name, inp):
+        y = inp @ params[name + ".weight"].T
+        b = params.get(name + ".bias")
+        return y if b is None else y + b
+
+    q = lin("q_proj", x).view(T, H, D)
+    k = lin("k_proj", x).view(T, n_kv, D)
+    v = lin("v_proj", x).view(T, n_kv, D)
+    cos, sin = rope_cache(cfg["max_seq_len"], D, cfg.get("rope_base", 10000.0), cfg.get("yarn_scale", 1.0),
+                          dtype=x.dtype)
+    pos_ids = torch.cat([torch.arange(cu[s + 1] - cu[s]) for s in range(len(cu) - 1)])
+    c, s_ = cos[pos_ids].unsqueeze(1), sin[pos_ids].unsqueeze(1)
+    q, k = rotate(q, c, s_), rotate(k, c, s_)
+    if n_kv != H:
+        rep = H // n_kv
+        k = k.unsqueeze(2).expand(T, n_kv, rep, D).reshape(T, H, D)
+        v = v.unsqueeze(2).expand(T, n_kv, rep, D).reshape(T, H, D)
+
+    w_cont = cfg["n_min"] + torch.sigmoid(lin("win_gate", x).squeeze(-1)) * (cfg["n_max"] - cfg["n_min"])
+    alpha = torch.sigmoid(params["alpha_w"])
+    with torch.no_grad():
+        w_disc = quantize_windows(w_cont.detach().float())
+        s32, _, _ = hybrid_scores(x.detach().float(), params["v_proj.weight"].detach().float(),
+                                  alpha.detach().float(), H, D)
+        lmk_pos = torch.from_numpy(select_landmarks(s32.numpy(), w_disc, np.array(cu), cfg["k_lmk"]))
+    scores, _, _ = hybrid_scores(x, params["v_proj.weight"], alpha, H, D)
+    starts = torch.tensor(cu[:-1])
+    abs_pos = starts[None, :, None] + lmk_pos.clamp(min=0)
+    s_sel = scores[abs_pos, torch.arange(H)[:, None, None]]
+    lmk_logw = torch.log(torch.sigmoid(s_sel / tau_lmk).clamp(min=1e-20))
+    lmk_logw = torch.where(lmk_pos >= 0, lmk_logw, torch.full_like(lmk_logw, float("-inf")))
+    o, _ = attention_soft(q, k, v, w_cont, lmk_pos, lmk_logw, cu, tau_win=tau_win, win_edge=win_edge)
+    out = o.reshape(T, d_model) @ params["out_proj.weight"].T
+    return out, (w_cont, lmk_pos, lmk_logw)
+
+
+def module_eval_forward(params: dict, cfg: dict, x: torch.Tensor, cu):
+    """Packed inference forward of DSALTAttention (dsalt_attention.py:610-625): floor-
+    quantised windows, landmark top-k on fp32 scores, HARD attention with zero landmark
+    bias, out_proj. Returns (out, (w_sizes, lmk_pos))."""
+    cu = [int(c) for c in cu]
+    T, d_model = x.shape
+    H = cfg["n_heads"]
+    D = d_model // H
+    n_kv = cfg.get("n_kv_heads") or H
+
+    def lin(name, inp):
+        y = inp @ params[name + ".weight"].T
+        b = params.get(name + ".bias")
+        return y if b is None else y + b
+
+    q = lin("q_proj", x).view(T, H, D)
+    k = lin("k_proj", x).view(T, n_kv, D)
+    v = lin("v_proj", x).view(T, n_kv, D)
+    cos, sin = rope_cache(cfg["max_seq_len"], D, cfg.get("rope_base", 10000.0), cfg.get("yarn_scale", 1.0),
+                          dtype=x.dtype)
+    pos_ids = torch.cat([torch.arange(cu[s + 1] - cu[s]) for s in range(len(cu) - 1)])
+    c, s_ = cos[pos_ids].unsqueeze(1), sin[pos_ids].unsqueeze(1)
+    q, k = rotate(q, c, s_), rotate(k, c, s_)
+    if n_kv != H:
+        rep = H // n_kv
+        k = k.unsqueeze(2).expand(T, n_kv, rep, D).reshape(T, H, D)
+        v = v.unsqueeze(2).expand(T, n_kv, rep, D).reshape(T, H, D)
+    w_cont = cfg["n_min"] + torch.sigmoid(lin("win_gate", x).squeeze(-1)) * (cfg["n_max"] - cfg["n_min"])
+    w_sizes = quantize_windows(w_cont.detach().float())
+    alpha = torch.sigmoid(params["alpha_w"]).detach().float()
+    s32, _, _ = hybrid_scores(x.detach().float(), params["v_proj.weight"].detach().float(), alpha, H, D)
+    lmk_pos = torch.from_numpy(select_landmarks(s32.numpy(), w_sizes, np.array(cu), cfg["k_lmk"]))
+    o, _ = attention_hard(q, k, v, w_sizes, lmk_pos, None, cu)
+    return o.reshape(T, d_model) @ params["out_proj.weight"].T, (w_sizes, lmk_pos)

@@ -1,0 +1,75 @@
+"""Writes golden vectors of the reference's DSALTAttention module composition.
+
+Run in the build container only (where the reference checkout exists):
+
+    TORCHDYNAMO_DISABLE=1 python tests/golden/make_golden.py [/path/to/reference]
+
+What it pins: the part no closed form covers - the module composition of
+dsalt/modules/dsalt_attention.py in training mode on packed uniform-length input
+(q/k/v projections -> RoPE -> _train_selectors (continuous window, landmark top-k,
+soft landmark weight) -> the dense SOFT attention of _packed_train ->
+out_proj), and the gradients of the output with respect to x and every parameter.
+On a CPU the reference takes its dense path (_packed_train, :489-563), which is the
+reference's own definition of the training kernel's math. TORCHDYNAMO_DISABLE=1 runs
+its torch.compile'd RoPE eagerly.
+
+Each fixture is an .npz (no pickles) holding the config, the parameters, the inputs,
+the upstream gradient and the reference's outputs and gradients.
+"""
+from __future__ import annotations
+
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+CASES = {
+    "module_train_mha": dict(d_model=128, n_heads=2, n_min=4, n_max=40, k_lmk=8, max_seq_len=256,
+                             n_kv_heads=None, qkv_bias=False, yarn_scale=1.0, rope_base=10000.0,
+                             lens=[64, 64], seed=0),
+    "module_train_gqa": dict(d_model=128, n_heads=2, n_min=2, n_max=24, k_lmk=5, max_seq_len=128,
+                             n_kv_heads=1, qkv_bias=True, yarn_scale=2.0, rope_base=500.0,
+                             lens=[48, 48, 48], seed=1),
+}
+
+
+def main(ref_root: str) -> None:
+    os.environ.setdefault("TORCHDYNAMO_DISABLE", "1")
+    sys.path.insert(0, ref_root)
+    import torch
+    from dsalt.modules.dsalt_attention import DSALTAttention
+
+    for name, cfg in CASES.items():
+        torch.manual_seed(cfg["seed"])
+        mod = DSALTAttention(cfg["d_model"], cfg["n_heads"], cfg["n_min"], cfg["n_max"], cfg["k_lmk"],
+                             cfg["max_seq_len"], yarn_scale=cfg["yarn_scale"], n_kv_heads=cfg["n_kv_heads"],
+                             qkv_bias=cfg["qkv_bias"], rope_base=cfg["rope_base"])
+        T = sum(cfg["lens"])
+        x = torch.randn(T, cfg["d_model"])
+        cu_list = [0]
+        for L in cfg["lens"]:
+            cu_list.append(cu_list[-1] + L)
+        cu = torch.tensor(cu_list, dtype=torch.int32)
+        mod.train()
+        with torch.no_grad():
+            w_cont, lmk_pos, lmk_logw = mod._train_selectors(x, cu, T, x.device, cu_list)
+        xg = x.clone().requires_grad_()
+        out, _ = mod(xg, cu_seqlens=cu)
+        dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(100 + cfg["seed"]))
+        out.backward(dout)
+        arrays = {"config": np.array(json.dumps(cfg)), "x": x.numpy(), "cu": cu.numpy(),
+                  "out": out.detach().numpy(), "dout": dout.numpy(), "grad.x": xg.grad.numpy(),
+                  "w_cont": w_cont.numpy(), "lmk_pos": lmk_pos.numpy(), "lmk_logw": lmk_logw.numpy()}
+        for pname, p in mod.named_parameters():
+            arrays["p." + pname] = p.detach().numpy()
+            arrays["grad." + pname] = p.grad.numpy()
+        path = os.path.join(HERE, name + ".npz")
+        np.savez_compressed(path, **arrays)
+        print(f"wrote {path} ({os.path.getsize(path)} bytes)")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
