@@ -9,9 +9,11 @@
 //    a lane holds ONE query (column lane%32) and 16 keys per 32-key block: the row max
 //    is an in-register max plus one v_permlane32_swap between the two lane halves, and
 //    P^T converts in place into the B operand of O^T += V^T . P^T (no data movement).
-//  * K tiles (64 keys) are staged row-major in LDS, V tiles transposed (V^T), double
-//    buffered, with the next tile's global loads in flight during the current tile's
-//    MFMAs. Rows are padded so that the MFMA operand reads are bank-conflict free.
+//  * K and V tiles (64 keys) go global -> LDS with direct loads (global_load_lds_dwordx4,
+//    no register staging) into a ring of NSTAGE buffers: loads run NSTAGE-1 tiles ahead
+//    of the MFMAs, so their latency is hidden even at low occupancy. K is read row-major, V with the transposing
+//    ds_read_b64_tr_b16 (the PV operand needs keys along K); both tiles are XOR-swizzled
+//    so that either read pattern is bank-conflict free (tiles.h).
 //  * The workgroup streams the union of its waves' key ranges
 //    [min_i(i - w_i + 1), max_i i]; a wave skips tiles outside its own range, and tiles
 //    that lie inside every row's band core take a mask-free path.
@@ -23,14 +25,13 @@
 //    and remapped across the 8 XCDs, so launches need no host-side block map.
 #include "common.h"
 #include "launch.h"
+#include "tiles.h"
 
 #include <type_traits>
 
 namespace dsalt {
 namespace {
 
-constexpr int kKPad = 8;          // K tile row = D + 8 halves: conflict-free b128 reads
-constexpr int kVPad = 4;          // V^T tile row = 64 + 4 halves: conflict-free b64 reads
 constexpr float kStaleMax = 8.0f;  // allowed growth of the row max before a rescale (log2)
 struct FwdParams {
     const uint16_t *q, *k, *v;
@@ -52,17 +53,18 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     constexpr int BN = kFwdBN;
     constexpr int KS = D / 16;              // MFMA k-steps over the head dim
     constexpr int ND = D / 32;              // 32-row blocks of O^T
-    constexpr int CPR = D / 8;              // 16-byte chunks per K/V row
-    constexpr int PER_T = BN * CPR / 256;   // chunks per thread per tile
+    constexpr int TB = Tile64<D>::BYTES;
+    constexpr int NSTAGE = D == 64 ? 4 : 3;                 // LDS ring depth
+    constexpr int LPT = 2 * Tile64<D>::LOADS_PER_WAVE;     // load instructions per tile per wave
 
-    __shared__ __align__(16) uint16_t ks[2][BN][D + kKPad];
-    __shared__ __align__(16) uint16_t vt[2][D][BN + kVPad];
+    __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][K, V]
     __shared__ int s_red[4][3];
     __shared__ int s_ltile[DSALT_MAX_K_LMK / BN];
     __shared__ int s_nlt;
     extern __shared__ int s_dyn[];
-    int *s_lpos = s_dyn;
-    float *s_lbias = reinterpret_cast<float *>(s_dyn + p.k_pad);
+    int *s_lpos = s_dyn;                                          // INT_MAX: empty slot
+    float *s_lbias = reinterpret_cast<float *>(s_dyn + p.k_pad);  // log2-unit bias
+    int *s_lrow = s_dyn + 2 * p.k_pad;                            // row to load (0 if empty)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 31, hh = lane >> 5;
@@ -117,6 +119,7 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
         }
         s_lpos[s] = pos;
         s_lbias[s] = b;
+        s_lrow[s] = pos == INT_MAX ? 0 : pos;
     }
     if (lane == 0) {
         s_red[wave][0] = wlo;
@@ -141,45 +144,21 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     const int nb = (ghi >= glo) ? (ghi - glo) / BN + 1 : 0;
     const int nt = nb + s_nlt;
 
-    // ---- tile staging -------------------------------------------------------------------
-    uint4 kr[PER_T], vr[PER_T];
-    auto load_tile = [&](int t) {
+    // ---- tile staging: direct global -> LDS loads ----------------------------------------
+    // Out-of-range band rows and empty landmark slots load a real row of the sequence
+    // (so every address is valid); the masks give those keys probability 0.
+    const char *kbase = reinterpret_cast<const char *>(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh);
+    const char *vbase = reinterpret_cast<const char *>(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh);
+    const int64_t kst = p.k_st * 2, vst = p.v_st * 2;
+    auto issue_tile = [&](int t, int buf) {
         const bool band = t < nb;
-        const int tb = glo + t * BN;
-        const int lt = band ? 0 : s_ltile[t - nb];
-#pragma unroll
-        for (int u = 0; u < PER_T; ++u) {
-            const int c = tid + u * 256;
-            const int row = c / CPR, col = c % CPR;
-            int key;
-            bool ok;
-            if (band) {
-                key = tb + row;
-                ok = key < seq_len;
-            } else {
-                key = s_lpos[lt * BN + row];
-                ok = key != INT_MAX;
-            }
-            uint4 kx = make_uint4(0, 0, 0, 0), vx = kx;
-            if (ok) {
-                const int64_t tok = (int64_t)seq_start + key;
-                kx = *reinterpret_cast<const uint4 *>(p.k + tok * p.k_st + (int64_t)head * p.k_sh + col * 8);
-                vx = *reinterpret_cast<const uint4 *>(p.v + tok * p.v_st + (int64_t)head * p.v_sh + col * 8);
-            }
-            kr[u] = kx;
-            vr[u] = vx;
-        }
-    };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int u = 0; u < PER_T; ++u) {
-            const int c = tid + u * 256;
-            const int row = c / CPR, col = c % CPR;
-            *reinterpret_cast<uint4 *>(&ks[buf][row][col * 8]) = kr[u];
-            const uint16_t *e = reinterpret_cast<const uint16_t *>(&vr[u]);
-#pragma unroll
-            for (int x = 0; x < 8; ++x) vt[buf][col * 8 + x][row] = e[x];
-        }
+        const int key0 = glo + t * BN;                 // band: key of tile row 0
+        const int *lrow = s_lrow + (band ? 0 : s_ltile[t - nb] * BN);
+        auto key_of = [&](int row) -> int64_t {
+            return band ? (int64_t)min(key0 + row, seq_len - 1) : (int64_t)lrow[row];
+        };
+        tile_load_async<D, kSwzRow>(s_tiles[buf][0], wave, lane, [&](int row) { return kbase + key_of(row) * kst; });
+        tile_load_async<D, kSwzTr>(s_tiles[buf][1], wave, lane, [&](int row) { return vbase + key_of(row) * vst; });
     };
 
     // Online-softmax update of one 64-key tile (sacc: raw q.k or log2-unit logits, -inf
@@ -223,10 +202,7 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
                 make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
 #pragma unroll
             for (int d = 0; d < ND; ++d) {
-                const uint16_t *row = &vt[buf][d * 32 + ql][kk * 16 + hh * 4];
-                const uint2 lo8 = *reinterpret_cast<const uint2 *>(row);
-                const uint2 hi8 = *reinterpret_cast<const uint2 *>(row + 8);
-                const vec8 a = bitcast<vec8>(make_uint4(lo8.x, lo8.y, hi8.x, hi8.y));
+                const vec8 a = bitcast<vec8>(tile_read_tr<D>(s_tiles[buf][1], kk * 16, d * 32, lane));
                 oacc[d] = DT::mfma(a, b, oacc[d]);
             }
         }
@@ -239,15 +215,17 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     float m2 = -INFINITY, lsum = 0.f;
     const float c = p.scale_log2;
 
-    if (nt > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
+    // prologue: tiles 0 .. NSTAGE-2 in flight; wait for tile 0
+    for (int t = 0; t < NSTAGE - 1; ++t)
+        if (t < nt) issue_tile(t, t);
+    if (nt >= NSTAGE - 1) tile_wait_loads<(NSTAGE - 2) * LPT>();
+    else tile_wait_loads<0>();
     __syncthreads();
 
+    int buf = 0;
     for (int t = 0; t < nt; ++t) {
-        const int buf = t & 1;
-        if (t + 1 < nt) load_tile(t + 1);
+        // refill the stage read in iteration t-1 (every wave passed the barrier after it)
+        if (t + NSTAGE - 1 < nt) issue_tile(t + NSTAGE - 1, buf == 0 ? NSTAGE - 1 : buf - 1);
 
         const bool band = t < nb;
         const int tb = glo + t * BN;
@@ -269,8 +247,7 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
                 for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 #pragma unroll
                 for (int s = 0; s < KS; ++s) {
-                    const vec8 a = bitcast<vec8>(
-                        *reinterpret_cast<const uint4 *>(&ks[buf][rb * 32 + ql][s * 16 + hh * 8]));
+                    const vec8 a = bitcast<vec8>(tile_read_row16<D>(s_tiles[buf][0], rb * 32 + ql, 2 * s + hh));
                     acc = DT::mfma(a, qv[s], acc);
                 }
                 sacc[rb] = acc;
@@ -347,8 +324,11 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
             }
         }
 
-        if (t + 1 < nt) store_tile(buf ^ 1);
+        // tile t+1 must have landed; tiles t+2 .. t+NSTAGE-1 may stay in flight
+        if (t + NSTAGE - 1 < nt) tile_wait_loads<(NSTAGE - 2) * LPT>();
+        else tile_wait_loads<0>();
         __syncthreads();
+        buf = (buf + 1 == NSTAGE) ? 0 : buf + 1;
     }
 
     // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln 2 --------------------------------
@@ -428,7 +408,7 @@ hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream) {
     p.scale_log2 = a.scale * kLog2e;
     p.inv_tau = 1.f / a.tau_win;
     p.win_edge = a.win_edge;
-    const size_t dyn = (size_t)p.k_pad * (sizeof(int) + sizeof(float));
+    const size_t dyn = (size_t)p.k_pad * (2 * sizeof(int) + sizeof(float));
     if (a.dtype == DSALT_DTYPE_BF16) return launch_dt<BF16>(p, a.head_dim, a.mode, dyn, stream);
     return launch_dt<F16>(p, a.head_dim, a.mode, dyn, stream);
 }
