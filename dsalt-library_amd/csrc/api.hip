@@ -82,6 +82,8 @@ int dsalt_fwd_check(const dsalt_fwd_args *a) {
     if (a->mode == DSALT_MODE_SOFT && !(a->tau_win > 0.f))
         return fail(DSALT_ERR_INVALID, "tau_win must be > 0 (got %g)", (double)a->tau_win);
     if (!(a->scale == a->scale)) return fail(DSALT_ERR_INVALID, "scale is NaN");
+    if (a->scale == 0.f || !(fabsf(a->scale) < INFINITY))
+        return fail(DSALT_ERR_UNSUPPORTED, "scale must be finite and non-zero (got %g)", (double)a->scale);
     return DSALT_OK;
 }
 

@@ -105,35 +105,71 @@ __device__ __forceinline__ float half_sum(float x) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
-// Map a linear block index `target` over all (sequence, block-in-sequence) pairs of a
-// packed batch (blocks of `bm` tokens, sequence s owning ceil(L_s / bm) blocks) to its
-// pair, scanning cu_seqlens 64 sequences at a time with a wave prefix sum. Every lane
-// returns the same answer; false when `target` is past the last block. This replaces a
-// host-built block map, so launches need no device-to-host synchronisation.
+// Workgroup ids over the query (or key) blocks of a packed batch. Sequence s (start
+// cu[s], length L_s) owns the ceil(L_s / bm) consecutive ids starting at
+// first(s) = floor(cu[s] / bm) + s. first() is strictly increasing and the ranges are
+// disjoint; the largest id is at most ceil(T / bm) + S - 2, so a grid of
+// block_upper_bound(T, S, bm) ids covers every block, and the ids in the gaps between
+// ranges map to no block (false). The lookup is one coalesced load of 64 cu_seqlens
+// entries and a ballot per 64 sequences - no prefix sum and no host-side block map,
+// so launches need no device-to-host synchronisation. Every lane returns the same
+// (wave-uniform) answer, with the sequence's start and length.
 __device__ __forceinline__ bool find_block(const int32_t *__restrict__ cu, int num_seqs, int target,
-                                           int bm, int lane, int &seq, int &blk) {
+                                           int bm, int lane, int &seq, int &blk, int &seq_start,
+                                           int &seq_len) {
+    int cand = -1, cand_first = 0, cand_start = 0, cand_end = 0;
     for (int base = 0; base < num_seqs; base += 64) {
         const int s = base + lane;
-        int nb = 0;
+        int c0 = 0, c1 = 0, first = INT_MAX;
         if (s < num_seqs) {
-            const int len = cu[s + 1] - cu[s];
-            nb = len > 0 ? (len + bm - 1) / bm : 0;
+            c0 = cu[s];
+            c1 = cu[s + 1];
+            first = c0 / bm + s;
         }
-        const int incl = wave_incl_scan(nb, lane);
-        const int total = __shfl(incl, 63);
-        if (target < total) {
-            const unsigned long long m = __ballot(incl > target);
-            const int first = __ffsll((long long)m) - 1;
-            const int incl_f = __shfl(incl, first);
-            const int nb_f = __shfl(nb, first);
-            seq = base + first;
-            blk = target - (incl_f - nb_f);
-            return true;
-        }
-        target -= total;
+        const unsigned long long m = __ballot(first <= target);  // a prefix of the lanes
+        if (m == 0) break;
+        const int last = 63 - __clzll((long long)m);
+        cand = base + last;
+        cand_first = __builtin_amdgcn_readlane(first, last);
+        cand_start = __builtin_amdgcn_readlane(c0, last);
+        cand_end = __builtin_amdgcn_readlane(c1, last);
+        if (last < 63) break;
     }
-    return false;
+    if (cand < 0) return false;
+    const int len = cand_end - cand_start;
+    if (target - cand_first >= (len + bm - 1) / bm) return false;
+    seq = cand;
+    blk = target - cand_first;
+    seq_start = cand_start;
+    seq_len = len;
+    return true;
 }
+__device__ __forceinline__ bool find_block(const int32_t *__restrict__ cu, int num_seqs, int target,
+                                           int bm, int lane, int &seq, int &blk) {
+    int start, len;
+    return find_block(cu, num_seqs, target, bm, lane, seq, blk, start, len);
+}
+
+// Wave-uniform reductions over all 64 lanes without LDS: DPP quad/row permutations
+// reduce each row of 16 lanes, then the four row results are read as scalars.
+template <typename Op>
+__device__ __forceinline__ int wave_reduce_dpp(int x, Op op) {
+    x = op(x, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+    x = op(x, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+    x = op(x, __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    x = op(x, __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false));  // row_mirror
+    const int r0 = __builtin_amdgcn_readlane(x, 0), r1 = __builtin_amdgcn_readlane(x, 16);
+    const int r2 = __builtin_amdgcn_readlane(x, 32), r3 = __builtin_amdgcn_readlane(x, 48);
+    return op(op(r0, r1), op(r2, r3));
+}
+struct MinOp {
+    __device__ __forceinline__ int operator()(int a, int b) const { return min(a, b); }
+};
+struct MaxOp {
+    __device__ __forceinline__ int operator()(int a, int b) const { return max(a, b); }
+};
+__device__ __forceinline__ int wave_min_u(int x) { return wave_reduce_dpp(x, MinOp()); }
+__device__ __forceinline__ int wave_max_u(int x) { return wave_reduce_dpp(x, MaxOp()); }
 
 enum { kHard = 0, kSoft = 1 };
 

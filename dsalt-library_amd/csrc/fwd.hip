@@ -33,6 +33,8 @@ namespace dsalt {
 namespace {
 
 constexpr float kStaleMax = 8.0f;  // allowed growth of the row max before a rescale (log2)
+constexpr uint32_t kNegInfBits = 0xff800000u;
+
 struct FwdParams {
     const uint16_t *q, *k, *v;
     void *o;  // [T,H,D]: fp32 if out_f32, else the compute dtype
@@ -44,8 +46,28 @@ struct FwdParams {
     int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lse_st, lse_sh, w_st;
     int64_t lp_sh, lp_ss, lp_sk, lb_sh, lb_ss, lb_sk;
     int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid, out_f32;
-    float scale_log2, inv_tau, win_edge;
+    uint32_t q_sign;  // 0x80008000 when scale < 0 (Q is negated on load and |scale| used)
+    float c;          // |scale| * log2(e): raw q.k -> log2-unit logit
+    float inv_c;      // 1 / c: log2-unit (or natural, times log2 e) bias -> raw units
+    float inv_tau, win_edge;
 };
+
+// Bit (rb*16 + r) of a lane's 32-bit tile mask stands for accumulator element
+// sacc[rb][r], i.e. tile row rb*32 + acc_row_const(r) + hh*4. The row offset
+// rb*32 + acc_row_const(r) increases with the bit index, so the elements whose offset
+// is <= a form a prefix of the bits.
+__device__ __forceinline__ uint32_t rows_le(int a) {
+    if (a < 0) return 0u;
+    const int n = min(32, 4 * (a >> 3) + min((a & 7) + 1, 4));
+    return n >= 32 ? 0xffffffffu : (1u << n) - 1u;
+}
+
+// x if bit j of `mask` is set, else -inf. With j a compile-time constant this is
+// v_bfe_i32 + v_bfi_b32: no compare into a lane-mask SGPR (and no hazard wait after it).
+__device__ __forceinline__ float keep_if(uint32_t mask, int j, float x) {
+    const uint32_t m = (uint32_t)((int32_t)(mask << (31 - j)) >> 31);
+    return __uint_as_float((m & __float_as_uint(x)) | (~m & kNegInfBits));
+}
 
 template <typename DT, int D, int MODE>
 __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
@@ -59,11 +81,10 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
 
     __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][K, V]
     __shared__ int s_red[4][3];
-    __shared__ int s_ltile[DSALT_MAX_K_LMK / BN];
-    __shared__ int s_nlt;
+    __shared__ int s_ltmin[DSALT_MAX_K_LMK / BN];  // smallest position in each landmark tile
     extern __shared__ int s_dyn[];
     int *s_lpos = s_dyn;                                          // INT_MAX: empty slot
-    float *s_lbias = reinterpret_cast<float *>(s_dyn + p.k_pad);  // log2-unit bias
+    float *s_lbias = reinterpret_cast<float *>(s_dyn + p.k_pad);  // raw-unit bias
     int *s_lrow = s_dyn + 2 * p.k_pad;                            // row to load (0 if empty)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -73,11 +94,11 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     const int logical = xcd_remap(blockIdx.x, p.grid);
     const int head = logical / p.n_qblk;
     if (head >= p.n_heads) return;
-    int seq, blk;
-    if (!find_block(p.cu, p.num_seqs, logical - head * p.n_qblk, kFwdBM, lane, seq, blk)) return;
-    const int seq_start = p.cu[seq];
-    const int seq_len = p.cu[seq + 1] - seq_start;
-    const int i = blk * kFwdBM + wave * 32 + ql;  // query offset inside the sequence
+    int seq, blk, seq_start, seq_len;
+    if (!find_block(p.cu, p.num_seqs, logical - head * p.n_qblk, kFwdBM, lane, seq, blk, seq_start, seq_len))
+        return;
+    const int wq0 = blk * kFwdBM + wave * 32;  // first query of this wave
+    const int i = wq0 + ql;                    // query offset inside the sequence
     const bool qvalid = i < seq_len;
     const int64_t tok_i = (int64_t)seq_start + i;
 
@@ -89,6 +110,7 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
         for (int s = 0; s < KS; ++s) {
             uint4 raw = make_uint4(0, 0, 0, 0);
             if (qvalid) raw = *reinterpret_cast<const uint4 *>(qp + s * 16);
+            raw.x ^= p.q_sign; raw.y ^= p.q_sign; raw.z ^= p.q_sign; raw.w ^= p.q_sign;
             qv[s] = bitcast<vec8>(raw);
         }
     }
@@ -97,16 +119,16 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     // lo: first band key; corelo: first key of the zero-bias core; pmax: largest
     // admissible landmark position (-1: none). All inclusive, relative to the sequence.
     const float wv = qvalid ? p.w[tok_i * p.w_st] : 0.f;
-    const float wc = wv;
     int lo, corelo, pmax;
     query_ranges<MODE>(i, wv, p.win_edge, lo, corelo, pmax);
-    const int wlo = wave_min(qvalid ? lo : INT_MAX);
-    const int whi = wave_max(qvalid ? i : -1);
-    const int wclo = wave_max(qvalid ? corelo : INT_MIN);
-    const int wchi = wave_min(qvalid ? i : INT_MAX);
-    const int wpmax = wave_max(qvalid ? pmax : -1);
+    const int wlo = wave_min_u(qvalid ? lo : INT_MAX);
+    const int wclo = wave_max_u(qvalid ? corelo : INT_MIN);
+    const int wpmax = wave_max_u(qvalid ? pmax : -1);
+    const int whi = min(wq0 + 31, seq_len - 1);  // last valid query of the wave
+    const int wchi = wq0;                        // first query of the wave
 
     // ---- landmark slots -> LDS (invalid / out-of-sequence slots become INT_MAX) --------
+    // k_pad is a multiple of 64, so iteration j of wave w covers landmark tile 4j + w.
     for (int s = tid; s < p.k_pad; s += 256) {
         int pos = INT_MAX;
         float b = 0.f;
@@ -114,35 +136,29 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
             const int64_t pp = p.lmk_pos[head * p.lp_sh + seq * p.lp_ss + s * p.lp_sk];
             if (pp >= 0 && pp < seq_len) {
                 pos = (int)pp;
-                if (p.lmk_bias) b = p.lmk_bias[head * p.lb_sh + seq * p.lb_ss + s * p.lb_sk] * kLog2e;
+                if (p.lmk_bias) b = p.lmk_bias[head * p.lb_sh + seq * p.lb_ss + s * p.lb_sk] * (kLog2e * p.inv_c);
             }
         }
         s_lpos[s] = pos;
         s_lbias[s] = b;
         s_lrow[s] = pos == INT_MAX ? 0 : pos;
+        const int tmin = wave_min_u(pos);
+        if (lane == 0) s_ltmin[s >> 6] = tmin;
     }
     if (lane == 0) {
         s_red[wave][0] = wlo;
-        s_red[wave][1] = whi;
+        s_red[wave][1] = wq0 < seq_len ? whi : -1;
         s_red[wave][2] = wpmax;
     }
     __syncthreads();
     const int glo = min(min(s_red[0][0], s_red[1][0]), min(s_red[2][0], s_red[3][0]));
     const int ghi = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
     const int gpmax = max(max(s_red[0][2], s_red[1][2]), max(s_red[2][2], s_red[3][2]));
-    if (wave == 0) {  // landmark tiles holding at least one admissible position
-        int n = 0;
-        for (int lt = 0; lt < p.k_pad / BN; ++lt) {
-            if (wave_min(s_lpos[lt * BN + lane]) <= gpmax) {
-                if (lane == 0) s_ltile[n] = lt;
-                ++n;
-            }
-        }
-        if (lane == 0) s_nlt = n;
-    }
-    __syncthreads();
+    // landmark tiles holding at least one position admissible for the workgroup
+    const int n_lt = p.k_pad / BN;
+    const uint64_t lmask = __ballot(lane < n_lt && s_ltmin[lane < n_lt ? lane : 0] <= gpmax);
     const int nb = (ghi >= glo) ? (ghi - glo) / BN + 1 : 0;
-    const int nt = nb + s_nlt;
+    const int nt = nb + __popcll(lmask);
 
     // ---- tile staging: direct global -> LDS loads ----------------------------------------
     // Out-of-range band rows and empty landmark slots load a real row of the sequence
@@ -150,77 +166,39 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     const char *kbase = reinterpret_cast<const char *>(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh);
     const char *vbase = reinterpret_cast<const char *>(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh);
     const int64_t kst = p.k_st * 2, vst = p.v_st * 2;
+    const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
+    uint64_t lm_issue = lmask, lm_comp = lmask;  // landmark tiles not yet issued / computed
     auto issue_tile = [&](int t, int buf) {
         const bool band = t < nb;
-        const int key0 = glo + t * BN;                 // band: key of tile row 0
-        const int *lrow = s_lrow + (band ? 0 : s_ltile[t - nb] * BN);
+        const int key0 = glo + t * BN;  // band: key of tile row 0
+        int lt = 0;
+        if (!band) {
+            lt = __builtin_ctzll(lm_issue);
+            lm_issue &= lm_issue - 1;
+        }
+        const int *lrow = s_lrow + lt * BN;
         auto key_of = [&](int row) -> int64_t {
             return band ? (int64_t)min(key0 + row, seq_len - 1) : (int64_t)lrow[row];
         };
-        tile_load_async<D, kSwzRow>(s_tiles[buf][0], wave, lane, [&](int row) { return kbase + key_of(row) * kst; });
-        tile_load_async<D, kSwzTr>(s_tiles[buf][1], wave, lane, [&](int row) { return vbase + key_of(row) * vst; });
+        const uint32_t kl = tiles_lds + buf * (2 * TB);
+        tile_load_async<D, kSwzRow>(kl, wave, lane, [&](int row) { return kbase + key_of(row) * kst; });
+        tile_load_async<D, kSwzTr>(kl + TB, wave, lane, [&](int row) { return vbase + key_of(row) * vst; });
     };
 
-    // Online-softmax update of one 64-key tile (sacc: raw q.k or log2-unit logits, -inf
-    // where masked) followed by O^T += V^T . P^T from LDS buffer `buf`.
-    auto softmax_pv_impl = [&](auto scaled_tag, f32x16 (&sacc)[2], f32x16 (&oacc)[ND], float &m2,
-                               float &lsum, float c, int buf, int ql, int hh) {
-        constexpr bool SCALED = decltype(scaled_tag)::value;
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sacc[rb][r]);
-        tmax = half_max(tmax);
-        const float tm2 = SCALED ? tmax : tmax * c;
-        if (tm2 > m2 + kStaleMax) {
-            const float alpha = fast_exp2(m2 - tm2);
-            lsum *= alpha;
-#pragma unroll
-            for (int d = 0; d < ND; ++d)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
-            m2 = tm2;
-        }
-        const float mu = (m2 == -INFINITY) ? 0.f : m2;
-        uint32_t pk[2][8];
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float e0 = SCALED ? fast_exp2(sacc[rb][2 * j] - mu) : fast_exp2(fmaf(sacc[rb][2 * j], c, -mu));
-                const float e1 = SCALED ? fast_exp2(sacc[rb][2 * j + 1] - mu)
-                                        : fast_exp2(fmaf(sacc[rb][2 * j + 1], c, -mu));
-                lsum += e0 + e1;
-                pk[rb][j] = DT::pack2(e0, e1);
-            }
-        // O^T (D x 32 queries) += V^T . P^T ; k-step kk covers tile keys kk*16..+15
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            const int rb = kk >> 1, g = kk & 1;
-            const vec8 b = bitcast<vec8>(
-                make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
-#pragma unroll
-            for (int d = 0; d < ND; ++d) {
-                const vec8 a = bitcast<vec8>(tile_read_tr<D>(s_tiles[buf][1], kk * 16, d * 32, lane));
-                oacc[d] = DT::mfma(a, b, oacc[d]);
-            }
-        }
-    };
     f32x16 oacc[ND];
 #pragma unroll
     for (int d = 0; d < ND; ++d)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[d][r] = 0.f;
-    float m2 = -INFINITY, lsum = 0.f;
-    const float c = p.scale_log2;
+    float m2 = -INFINITY;       // running max (log2 units), stale by at most kStaleMax
+    float lsum0 = 0.f, lsum1 = 0.f;
+    const float c = p.c;
 
     // prologue: tiles 0 .. NSTAGE-2 in flight; wait for tile 0
     for (int t = 0; t < NSTAGE - 1; ++t)
         if (t < nt) issue_tile(t, t);
-    if (nt >= NSTAGE - 1) tile_wait_loads<(NSTAGE - 2) * LPT>();
-    else tile_wait_loads<0>();
-    __syncthreads();
+    if (nt >= NSTAGE - 1) tile_barrier<(NSTAGE - 2) * LPT>();
+    else tile_barrier<0>();
 
     int buf = 0;
     for (int t = 0; t < nt; ++t) {
@@ -234,11 +212,14 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
         if (band) {
             active = (tb <= whi) && (tb + BN - 1 >= wlo);
         } else {
-            lt = s_ltile[t - nb];
-            active = wave_min(s_lpos[lt * BN + lane]) <= wpmax;
+            lt = __builtin_ctzll(lm_comp);
+            lm_comp &= lm_comp - 1;
+            active = s_ltmin[lt] <= wpmax;
         }
         if (active) {
-            // S^T (64 keys x 32 queries) = K . Q^T
+            const char *ktile = s_tiles[buf][0];
+            const char *vtile = s_tiles[buf][1];
+            // S^T (64 keys x 32 queries) = K . Q^T, raw q.k
             f32x16 sacc[2];
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
@@ -247,62 +228,38 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
                 for (int r = 0; r < 16; ++r) acc[r] = 0.f;
 #pragma unroll
                 for (int s = 0; s < KS; ++s) {
-                    const vec8 a = bitcast<vec8>(tile_read_row16<D>(s_tiles[buf][0], rb * 32 + ql, 2 * s + hh));
+                    const vec8 a = bitcast<vec8>(tile_read_row16<D>(ktile, rb * 32 + ql, 2 * s + hh));
                     acc = DT::mfma(a, qv[s], acc);
                 }
                 sacc[rb] = acc;
             }
 
-            // masks and biases, then softmax + PV. Two wave-uniform variants: `raw` keeps
-            // q.k in sacc (scale folded into the exponent), `scaled` holds log2-unit logits
-            // (needed when a per-key bias is present: soft window edge or landmarks).
+            // masks and per-key biases, folded into the raw scores (bias / c)
             if (band) {
-                // key offset in the tile of (rb, r) = rb*32 + acc_row_const(r) + hh*4
+                // element (rb, r) is key tb + rb*32 + acc_row_const(r) + hh*4 =: tb + hh*4 + cst
                 const int A = i - tb - hh * 4;   // key <= i       <=> cst <= A
                 const int B = lo - tb - hh * 4;  // key >= lo      <=> cst >= B
                 const bool need_lo = tb < wclo;
                 const bool need_hi = tb + BN - 1 > wchi;
                 if (MODE == kSoft && need_lo) {
                     const int Bc = corelo - tb - hh * 4;  // key >= corelo <=> cst >= Bc
+                    const float wc = wv;
 #pragma unroll
                     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
                             const int cst = rb * 32 + acc_row_const(r);
-                            float x = sacc[rb][r] * c;
                             float oms;
                             const float edge = soft_edge_log2(wc, (float)(A - cst), p.inv_tau, oms);
-                            x += (cst < Bc) ? edge : 0.f;  // soft edge, d = i - key = A - cst
+                            const float x = sacc[rb][r] + ((cst < Bc) ? edge * p.inv_c : 0.f);
                             sacc[rb][r] = ((cst <= A) & (cst >= B)) ? x : -INFINITY;
                         }
-                    softmax_pv_impl(std::true_type{}, sacc, oacc, m2, lsum, c, buf, ql, hh);
-                } else {
-                    if (need_lo && need_hi) {
+                } else if (need_lo | need_hi) {
+                    const uint32_t keep = rows_le(A) & ~rows_le(B - 1);
 #pragma unroll
-                        for (int rb = 0; rb < 2; ++rb)
+                    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-                            for (int r = 0; r < 16; ++r) {
-                                const int cst = rb * 32 + acc_row_const(r);
-                                sacc[rb][r] = ((cst <= A) & (cst >= B)) ? sacc[rb][r] : -INFINITY;
-                            }
-                    } else if (need_lo) {
-#pragma unroll
-                        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                            for (int r = 0; r < 16; ++r) {
-                                const int cst = rb * 32 + acc_row_const(r);
-                                sacc[rb][r] = (cst >= B) ? sacc[rb][r] : -INFINITY;
-                            }
-                    } else if (need_hi) {
-#pragma unroll
-                        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                            for (int r = 0; r < 16; ++r) {
-                                const int cst = rb * 32 + acc_row_const(r);
-                                sacc[rb][r] = (cst <= A) ? sacc[rb][r] : -INFINITY;
-                            }
-                    }
-                    softmax_pv_impl(std::false_type{}, sacc, oacc, m2, lsum, c, buf, ql, hh);
+                        for (int r = 0; r < 16; ++r) sacc[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r]);
                 }
             } else {
 #pragma unroll
@@ -317,22 +274,69 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int r = g * 4 + e;
-                            sacc[rb][r] = (pp[e] <= pmax) ? fmaf(sacc[rb][r], c, bb[e]) : -INFINITY;
+                            sacc[rb][r] = (pp[e] <= pmax) ? sacc[rb][r] + bb[e] : -INFINITY;
                         }
                     }
-                softmax_pv_impl(std::true_type{}, sacc, oacc, m2, lsum, c, buf, ql, hh);
+            }
+
+            // ---- online softmax (base 2, stale max) ----------------------------------
+            float t0 = fmaxf(fmaxf(sacc[0][0], sacc[0][1]), sacc[0][2]);
+            float t1 = fmaxf(fmaxf(sacc[0][3], sacc[0][4]), sacc[0][5]);
+            float t2 = fmaxf(fmaxf(sacc[1][0], sacc[1][1]), sacc[1][2]);
+            float t3 = fmaxf(fmaxf(sacc[1][3], sacc[1][4]), sacc[1][5]);
+#pragma unroll
+            for (int r = 6; r < 16; r += 2) {
+                t0 = fmaxf(fmaxf(t0, sacc[0][r]), sacc[0][r + 1]);
+                t2 = fmaxf(fmaxf(t2, sacc[1][r]), sacc[1][r + 1]);
+            }
+            const float tmax = half_max(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)));
+            const float tm2 = tmax * c;
+            if (tm2 > m2 + kStaleMax) {
+                const float alpha = fast_exp2(m2 - tm2);
+                lsum0 *= alpha;
+                lsum1 *= alpha;
+#pragma unroll
+                for (int d = 0; d < ND; ++d)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
+                m2 = tm2;
+            }
+            const float mu = (m2 == -INFINITY) ? 0.f : m2;
+            // P in fp32: its row sum (fp32, unrounded, as the LSE needs it) and its
+            // 16-bit rounding (the PV operand)
+            uint32_t pk[2][8];
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float e0 = fast_exp2(fmaf(sacc[rb][2 * j], c, -mu));
+                    const float e1 = fast_exp2(fmaf(sacc[rb][2 * j + 1], c, -mu));
+                    if (j & 1) lsum1 += e0 + e1;
+                    else lsum0 += e0 + e1;
+                    pk[rb][j] = DT::pack2(e0, e1);
+                }
+            // O^T (D x 32 queries) += V^T . P^T ; k-step kk covers tile keys kk*16..+15
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                const int rb = kk >> 1, g = kk & 1;
+                const vec8 b = bitcast<vec8>(
+                    make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
+#pragma unroll
+                for (int d = 0; d < ND; ++d) {
+                    const vec8 a = bitcast<vec8>(tile_read_tr<D>(vtile, kk * 16, d * 32, lane));
+                    oacc[d] = DT::mfma(a, b, oacc[d]);
+                }
             }
         }
 
         // tile t+1 must have landed; tiles t+2 .. t+NSTAGE-1 may stay in flight
-        if (t + NSTAGE - 1 < nt) tile_wait_loads<(NSTAGE - 2) * LPT>();
-        else tile_wait_loads<0>();
-        __syncthreads();
+        if (t + NSTAGE - 1 < nt) tile_barrier<(NSTAGE - 2) * LPT>();
+        else tile_barrier<0>();
         buf = (buf + 1 == NSTAGE) ? 0 : buf + 1;
     }
 
     // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln 2 --------------------------------
-    const float ltot = half_sum(lsum);
+    const float ltot = half_sum(lsum0 + lsum1);
     const bool nonempty = ltot > 1e-9f;
     const float inv = nonempty ? 1.f / ltot : 0.f;
     if (qvalid) {
@@ -405,7 +409,9 @@ hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream) {
     p.n_qblk = block_upper_bound(a.total_len, a.num_seqs, kFwdBM);
     const int64_t blocks = (int64_t)p.n_qblk * a.n_heads;
     p.grid = (int)((blocks + 7) / 8 * 8);
-    p.scale_log2 = a.scale * kLog2e;
+    p.q_sign = a.scale < 0.f ? 0x80008000u : 0u;
+    p.c = fabsf(a.scale) * kLog2e;
+    p.inv_c = 1.f / p.c;
     p.inv_tau = 1.f / a.tau_win;
     p.win_edge = a.win_edge;
     const size_t dyn = (size_t)p.k_pad * (2 * sizeof(int) + sizeof(float));

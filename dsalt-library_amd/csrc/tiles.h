@@ -1,6 +1,12 @@
 // LDS tiles of 64 rows x D 16-bit elements (rows are tokens: keys or queries), filled
 // with direct global->LDS loads (global_load_lds_dwordx4, gfx950) and read back as
-// v_mfma_f32_32x32x16 operands. Rows are unpadded; the 16-byte chunks of each row are
+// v_mfma_f32_32x32x16 operands.
+//
+// The direct loads are issued through inline asm and completed with explicit
+// s_waitcnt vmcnt(N) + s_barrier (tile_barrier): when the compiler sees an LDS DMA it
+// must assume every later LDS read may alias it and every workgroup fence must drain
+// it, so it emits s_waitcnt vmcnt(0) before each tile read and each __syncthreads -
+// which would wait for the tiles being prefetched as well and serialise the ring. Rows are unpadded; the 16-byte chunks of each row are
 // XOR-swizzled so that the two read patterns are bank-conflict free:
 //   swz_row  : chunk ^ (row & 7)          row-major operand reads (16 B per lane, 8
 //                                         consecutive rows, same logical chunk)
@@ -13,8 +19,6 @@
 namespace dsalt {
 
 typedef short shortx4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) const void gbl_cvoid;
 
 enum { kSwzRow = 0, kSwzTr = 1 };
 
@@ -31,12 +35,24 @@ struct Tile64 {
     static constexpr int LOADS_PER_WAVE = 64 * CPR / 256;  // 64-lane load instructions per wave
 };
 
-// This wave's share of the direct loads of one tile (4 waves cover the tile). Physical
-// chunk slot g holds logical chunk (g % CPR) ^ swz(row) of row g / CPR; `row_src(row)`
-// returns the byte address of that row's element 0 in global memory (always a valid
-// address: callers clamp out-of-range rows onto a real row and mask them later).
+// Byte address in LDS of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+
+// global_load_lds_dwordx4: lane i's 16 bytes at `src` land at LDS byte m0 + 16 * i.
+// `lds` must be wave-uniform (it is moved into m0).
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
+// This wave's share of the direct loads of one tile (4 waves cover the tile): LPW load
+// instructions, counted by vmcnt. Physical chunk slot g holds logical chunk
+// (g % CPR) ^ swz(row) of row g / CPR; `row_src(row)` returns the byte address of that
+// row's element 0 in global memory (always a valid address: callers clamp out-of-range
+// rows onto a real row and mask them later). `tile_lds` = lds_addr(tile), wave-uniform.
 template <int D, int SWZ, typename RowSrc>
-__device__ __forceinline__ void tile_load_async(char *tile, int wave, int lane, RowSrc row_src) {
+__device__ __forceinline__ void tile_load_async(uint32_t tile_lds, int wave, int lane, RowSrc row_src) {
     constexpr int CPR = Tile64<D>::CPR, LPW = Tile64<D>::LOADS_PER_WAVE;
 #pragma unroll
     for (int u = 0; u < LPW; ++u) {
@@ -44,18 +60,18 @@ __device__ __forceinline__ void tile_load_async(char *tile, int wave, int lane, 
         const int g = slot0 + lane;
         const int row = g / CPR;
         const int c = (g % CPR) ^ tile_swz<SWZ>(row);
-        const char *src = row_src(row) + c * 16;
-        __builtin_amdgcn_global_load_lds((gbl_cvoid *)src, (lds_void *)(tile + slot0 * 16), 16, 0, 0);
+        dma16(row_src(row) + c * 16, __builtin_amdgcn_readfirstlane(tile_lds + slot0 * 16));
     }
 }
 
 // Wait until at most N of this wave's vector-memory operations are outstanding (they
-// complete in issue order for this counter), i.e. until every direct load issued
-// before the last N has landed in LDS. A workgroup barrier must follow before other
-// waves read the data.
+// complete in issue order), i.e. until every direct load issued before the last N has
+// landed in LDS, drain this wave's LDS operations, then synchronise the workgroup: after
+// it every wave may read what every wave's completed loads wrote, and every wave's
+// earlier LDS reads are done (their buffers may be refilled).
 template <int N>
-__device__ __forceinline__ void tile_wait_loads() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+__device__ __forceinline__ void tile_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 // Row-major operand read: 16 bytes = logical chunk c of `row` (8 consecutive elements).

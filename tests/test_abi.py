@@ -77,6 +77,8 @@ def test_fwd_check_accepts_valid_args():
     ("q", 0x10000008, 1, "aligned"),
     ("k_stride_t", 250, 1, "strides"),
     ("tau_win", 0.0, 1, "tau_win"),
+    ("scale", 0.0, 2, "scale"),
+    ("scale", float("inf"), 2, "scale"),
 ])
 def test_fwd_check_rejects(field, value, code, needle):
     kw = {field: value}

@@ -75,7 +75,7 @@ def run_oracle(mode, q, k, v, w, pos, bias, cu, rows=None, **kw):
     q64, k64, v64 = (t.double() for t in (q, k, v))
     if mode == hip.MODE_HARD:
         return orc.attention_hard(q64, k64, v64, w, pos, None if bias is None else bias.double(), cu.tolist(),
-                                  rows=rows)
+                                  rows=rows, **kw)
     return orc.attention_soft(q64, k64, v64, w.double(), pos, None if bias is None else bias.double(),
                               cu.tolist(), rows=rows, **kw)
 
@@ -172,6 +172,36 @@ def test_fwd_headline_shapes_on_row_subsets(cfg):
     sel = torch.cat([torch.arange(int(cu[s]) + rows[0], int(cu[s]) + rows[1]) for s in range(len(lens))])
     close(out[sel], o_ref, cfg)
     lse_close(lse[sel], l_ref, cfg + " lse")
+
+
+def test_fwd_many_sequences():
+    # more than 64 sequences (the block lookup scans cu_seqlens 64 entries at a time),
+    # empty ones included, lengths not multiples of the 128-query block
+    rng = np.random.default_rng(13)
+    lens = [int(x) for x in rng.integers(0, 70, size=150)]
+    lens[3] = lens[77] = lens[149] = 0
+    lens[64] = 300
+    for mode in (hip.MODE_HARD, hip.MODE_SOFT):
+        print(f"fwd many sequences mode={mode}", flush=True)
+        q, kk, v, w, pos, bias, cu = make_inputs(lens, 2, 64, 6, mode, seed=13, n_min=2, n_max=40)
+        out, lse = run_hip(mode, q, kk, v, w, pos, bias, cu)
+        o_ref, l_ref = run_oracle(mode, q, kk, v, w, pos, bias, cu)
+        close(out, o_ref, f"many sequences {mode}")
+        lse_close(lse, l_ref, f"many sequences {mode} lse")
+
+
+@pytest.mark.parametrize("mode", [hip.MODE_HARD, hip.MODE_SOFT], ids=["hard", "soft"])
+def test_fwd_negative_scale(mode):
+    lens, H, D, k = [200, 61], 2, 64, 9
+    q, kk, v, w, pos, bias, cu = make_inputs(lens, H, D, k, mode, seed=14, n_min=4, n_max=90)
+    dev = torch.device("cuda", 0)
+    scale = -0.3
+    out, lse = hip.fwd(mode, q.to(dev), kk.to(dev), v.to(dev), w.to(dev), pos.to(dev), bias.to(dev), cu.to(dev),
+                       scale, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    o_ref, l_ref = run_oracle(mode, q, kk, v, w, pos, bias, cu, scale=scale)
+    close(out.cpu(), o_ref, "negative scale")
+    lse_close(lse.cpu(), l_ref, "negative scale lse")
 
 
 # ------------------------------------------------------------------- selection
