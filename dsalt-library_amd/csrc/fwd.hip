@@ -57,9 +57,8 @@ struct FwdParams {
 // rb*32 + acc_row_const(r) increases with the bit index, so the elements whose offset
 // is <= a form a prefix of the bits.
 __device__ __forceinline__ uint32_t rows_le(int a) {
-    if (a < 0) return 0u;
-    const int n = min(32, 4 * (a >> 3) + min((a & 7) + 1, 4));
-    return n >= 32 ? 0xffffffffu : (1u << n) - 1u;
+    const int n = min(max(4 * (a >> 3) + min((a & 7) + 1, 4), 0), 32);  // 0 for a < 0
+    return (uint32_t)((1ull << n) - 1ull);
 }
 
 // x if bit j of `mask` is set, else -inf. With j a compile-time constant this is
@@ -76,31 +75,60 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     constexpr int KS = D / 16;              // MFMA k-steps over the head dim
     constexpr int ND = D / 32;              // 32-row blocks of O^T
     constexpr int TB = Tile64<D>::BYTES;
-    constexpr int NSTAGE = D == 64 ? 4 : 3;                 // LDS ring depth
+    constexpr int NSTAGE = 4;                              // LDS ring depth (tiles)
     constexpr int LPT = 2 * Tile64<D>::LOADS_PER_WAVE;     // load instructions per tile per wave
 
     __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][K, V]
-    __shared__ int s_red[4][3];
+    __shared__ int s_red[4][2];
     __shared__ int s_ltmin[DSALT_MAX_K_LMK / BN];  // smallest position in each landmark tile
     extern __shared__ int s_dyn[];
     int *s_lpos = s_dyn;                                          // INT_MAX: empty slot
     float *s_lbias = reinterpret_cast<float *>(s_dyn + p.k_pad);  // raw-unit bias
     int *s_lrow = s_dyn + 2 * p.k_pad;                            // row to load (0 if empty)
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // `wave` through readfirstlane: the compiler then knows it is wave-uniform, so every
+    // per-wave decision below is a scalar branch (no exec masking, no register merges).
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
 
     // ---- workgroup -> (head, sequence, query block) -----------------------------------
+    // Blocks run last-first inside a head: late blocks have the widest key ranges, and
+    // starting them first shortens the tail of the launch.
     const int logical = xcd_remap(blockIdx.x, p.grid);
     const int head = logical / p.n_qblk;
     if (head >= p.n_heads) return;
     int seq, blk, seq_start, seq_len;
-    if (!find_block(p.cu, p.num_seqs, logical - head * p.n_qblk, kFwdBM, lane, seq, blk, seq_start, seq_len))
+    if (!find_block(p.cu, p.num_seqs, p.n_qblk - 1 - (logical - head * p.n_qblk), kFwdBM, lane, seq, blk,
+                    seq_start, seq_len))
         return;
     const int wq0 = blk * kFwdBM + wave * 32;  // first query of this wave
     const int i = wq0 + ql;                    // query offset inside the sequence
     const bool qvalid = i < seq_len;
     const int64_t tok_i = (int64_t)seq_start + i;
+    const int ghi = min(blk * kFwdBM + kFwdBM - 1, seq_len - 1);  // last query of the workgroup
+
+    // ---- tile staging: direct global -> LDS loads ----------------------------------------
+    // Band tiles run from the diagonal down: tile t holds keys ghi-63-64t .. ghi-64t, so
+    // the first tiles are known before the windows are read and their loads overlap the
+    // setup. Landmark tiles follow the band tiles. K/V rows are read through buffer
+    // resources whose range is this (sequence, head): rows below the sequence start
+    // (wrapped offsets) read as zeros, empty landmark slots load row 0; the masks give
+    // all of them probability 0.
+    const uint32_t kst = (uint32_t)p.k_st * 2u, vst = (uint32_t)p.v_st * 2u;  // row strides (bytes)
+    const i32x4 krs = buffer_rsrc(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh, (uint32_t)seq_len * kst);
+    const i32x4 vrs = buffer_rsrc(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh, (uint32_t)seq_len * vst);
+    const TileLanes<D, kSwzRow> klanes(wave, lane, kst);
+    const TileLanes<D, kSwzTr> vlanes(wave, lane, vst);
+    const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
+    auto band_key0 = [&](int t) { return ghi - (BN - 1) - t * BN; };
+    auto issue_band = [&](int t) {
+        const int key0 = band_key0(t);
+        const uint32_t kl = tiles_lds + (t & (NSTAGE - 1)) * (2 * TB);
+        klanes.load_band(kl, wave, krs, (uint32_t)key0 * kst);  // wraps when key0 < 0
+        vlanes.load_band(kl + TB, wave, vrs, (uint32_t)key0 * vst);
+    };
+#pragma unroll
+    for (int t = 0; t < NSTAGE - 1; ++t) issue_band(t);
 
     // ---- Q (B operand: query column ql, head-dim chunk hh*8 of every 16) ---------------
     vec8 qv[KS];
@@ -147,42 +175,55 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     }
     if (lane == 0) {
         s_red[wave][0] = wlo;
-        s_red[wave][1] = wq0 < seq_len ? whi : -1;
-        s_red[wave][2] = wpmax;
+        s_red[wave][1] = wpmax;
     }
     __syncthreads();
     const int glo = min(min(s_red[0][0], s_red[1][0]), min(s_red[2][0], s_red[3][0]));
-    const int ghi = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
-    const int gpmax = max(max(s_red[0][2], s_red[1][2]), max(s_red[2][2], s_red[3][2]));
+    const int gpmax = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
     // landmark tiles holding at least one position admissible for the workgroup
     const int n_lt = p.k_pad / BN;
     const uint64_t lmask = __ballot(lane < n_lt && s_ltmin[lane < n_lt ? lane : 0] <= gpmax);
-    const int nb = (ghi >= glo) ? (ghi - glo) / BN + 1 : 0;
+    // band tiles (at least the NSTAGE-1 issued above; extra ones are inactive)
+    const int nb = max((ghi - glo) / BN + 1, NSTAGE - 1);
     const int nt = nb + __popcll(lmask);
-
-    // ---- tile staging: direct global -> LDS loads ----------------------------------------
-    // Out-of-range band rows and empty landmark slots load a real row of the sequence
-    // (so every address is valid); the masks give those keys probability 0.
-    const char *kbase = reinterpret_cast<const char *>(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh);
-    const char *vbase = reinterpret_cast<const char *>(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh);
-    const int64_t kst = p.k_st * 2, vst = p.v_st * 2;
-    const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
-    uint64_t lm_issue = lmask, lm_comp = lmask;  // landmark tiles not yet issued / computed
-    auto issue_tile = [&](int t, int buf) {
-        const bool band = t < nb;
-        const int key0 = glo + t * BN;  // band: key of tile row 0
-        int lt = 0;
-        if (!band) {
-            lt = __builtin_ctzll(lm_issue);
-            lm_issue &= lm_issue - 1;
+    auto lmk_tile = [&](int t) {  // landmark tile of iteration t >= nb: (t-nb)-th set bit
+        uint64_t m = lmask;
+        for (int j = nb; j < t; ++j) m &= m - 1;
+        return (int)__builtin_ctzll(m);
+    };
+    auto issue_tile = [&](int t) {
+        if (t < nb) {
+            issue_band(t);
+        } else {
+            const int *lrow = s_lrow + lmk_tile(t) * BN;
+            const uint32_t kl = tiles_lds + (t & (NSTAGE - 1)) * (2 * TB);
+            klanes.load_gather(kl, wave, krs, kst, lrow);
+            vlanes.load_gather(kl + TB, wave, vrs, vst, lrow);
         }
-        const int *lrow = s_lrow + lt * BN;
-        auto key_of = [&](int row) -> int64_t {
-            return band ? (int64_t)min(key0 + row, seq_len - 1) : (int64_t)lrow[row];
-        };
-        const uint32_t kl = tiles_lds + buf * (2 * TB);
-        tile_load_async<D, kSwzRow>(kl, wave, lane, [&](int row) { return kbase + key_of(row) * kst; });
-        tile_load_async<D, kSwzTr>(kl + TB, wave, lane, [&](int row) { return vbase + key_of(row) * vst; });
+    };
+    auto tile_active = [&](int t) {  // wave-uniform
+        if (t < nb) {
+            const int tb = band_key0(t);
+            return (tb <= whi) && (tb + BN - 1 >= wlo);
+        }
+        return s_ltmin[lmk_tile(t)] <= wpmax;
+    };
+
+    // S^T (64 keys x 32 queries) = K . Q^T, raw q.k, from the K tile of stage `stage`
+    auto qk_tile = [&](int stage, f32x16 (&sacc)[2]) {
+        const char *ktile = s_tiles[stage][0];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            f32x16 acc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const vec8 a = bitcast<vec8>(tile_read_row16<D>(ktile, rb * 32 + ql, 2 * s + hh));
+                acc = DT::mfma(a, qv[s], acc);
+            }
+            sacc[rb] = acc;
+        }
     };
 
     f32x16 oacc[ND];
@@ -194,145 +235,143 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     float lsum0 = 0.f, lsum1 = 0.f;
     const float c = p.c;
 
-    // prologue: tiles 0 .. NSTAGE-2 in flight; wait for tile 0
-    for (int t = 0; t < NSTAGE - 1; ++t)
-        if (t < nt) issue_tile(t, t);
-    if (nt >= NSTAGE - 1) tile_barrier<(NSTAGE - 2) * LPT>();
-    else tile_barrier<0>();
-
-    int buf = 0;
-    for (int t = 0; t < nt; ++t) {
-        // refill the stage read in iteration t-1 (every wave passed the barrier after it)
-        if (t + NSTAGE - 1 < nt) issue_tile(t + NSTAGE - 1, buf == 0 ? NSTAGE - 1 : buf - 1);
-
-        const bool band = t < nb;
-        const int tb = glo + t * BN;
-        int lt = 0;
-        bool active;
-        if (band) {
-            active = (tb <= whi) && (tb + BN - 1 >= wlo);
-        } else {
-            lt = __builtin_ctzll(lm_comp);
-            lm_comp &= lm_comp - 1;
-            active = s_ltmin[lt] <= wpmax;
+    // online-softmax update with the scores of one tile (raw units, -inf where masked)
+    // and O^T += V^T . P^T from the V tile of stage `stage`
+    auto softmax_pv = [&](f32x16 (&sacc)[2], int stage) {
+        float t0 = fmaxf(fmaxf(sacc[0][0], sacc[0][1]), sacc[0][2]);
+        float t1 = fmaxf(fmaxf(sacc[0][3], sacc[0][4]), sacc[0][5]);
+        float t2 = fmaxf(fmaxf(sacc[1][0], sacc[1][1]), sacc[1][2]);
+        float t3 = fmaxf(fmaxf(sacc[1][3], sacc[1][4]), sacc[1][5]);
+#pragma unroll
+        for (int r = 6; r < 16; r += 2) {
+            t0 = fmaxf(fmaxf(t0, sacc[0][r]), sacc[0][r + 1]);
+            t2 = fmaxf(fmaxf(t2, sacc[1][r]), sacc[1][r + 1]);
         }
-        if (active) {
-            const char *ktile = s_tiles[buf][0];
-            const char *vtile = s_tiles[buf][1];
-            // S^T (64 keys x 32 queries) = K . Q^T, raw q.k
-            f32x16 sacc[2];
+        const float tmax = half_max(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)));
+        const float tm2 = tmax * c;
+        const bool raise = tm2 > m2 + kStaleMax;
+        if (__builtin_amdgcn_ballot_w64(raise)) {  // wave-uniform branch: rare after the first tile
+            const float alpha = raise ? fast_exp2(m2 - tm2) : 1.f;
+            lsum0 *= alpha;
+            lsum1 *= alpha;
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-                f32x16 acc;
+            for (int d = 0; d < ND; ++d)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+                for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
+            m2 = raise ? tm2 : m2;
+        }
+        const float mu = (m2 == -INFINITY) ? 0.f : m2;
+        // P in fp32: its row sum (fp32, unrounded, as the LSE needs it) and its 16-bit
+        // rounding (the PV operand)
+        uint32_t pk[2][8];
 #pragma unroll
-                for (int s = 0; s < KS; ++s) {
-                    const vec8 a = bitcast<vec8>(tile_read_row16<D>(ktile, rb * 32 + ql, 2 * s + hh));
-                    acc = DT::mfma(a, qv[s], acc);
-                }
-                sacc[rb] = acc;
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float e0 = fast_exp2(fmaf(sacc[rb][2 * j], c, -mu));
+                const float e1 = fast_exp2(fmaf(sacc[rb][2 * j + 1], c, -mu));
+                if (j & 1) lsum1 += e0 + e1;
+                else lsum0 += e0 + e1;
+                pk[rb][j] = DT::pack2(e0, e1);
             }
+        // O^T (D x 32 queries) += V^T . P^T ; k-step kk covers tile keys kk*16..+15
+        const char *vtile = s_tiles[stage][1];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int rb = kk >> 1, g = kk & 1;
+            const vec8 b = bitcast<vec8>(
+                make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
+#pragma unroll
+            for (int d = 0; d < ND; ++d) {
+                const vec8 a = bitcast<vec8>(tile_read_tr<D>(vtile, kk * 16, d * 32, lane));
+                oacc[d] = DT::mfma(a, b, oacc[d]);
+            }
+        }
+    };
 
-            // masks and per-key biases, folded into the raw scores (bias / c)
-            if (band) {
-                // element (rb, r) is key tb + rb*32 + acc_row_const(r) + hh*4 =: tb + hh*4 + cst
-                const int A = i - tb - hh * 4;   // key <= i       <=> cst <= A
-                const int B = lo - tb - hh * 4;  // key >= lo      <=> cst >= B
-                const bool need_lo = tb < wclo;
-                const bool need_hi = tb + BN - 1 > wchi;
-                if (MODE == kSoft && need_lo) {
-                    const int Bc = corelo - tb - hh * 4;  // key >= corelo <=> cst >= Bc
-                    const float wc = wv;
-#pragma unroll
-                    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int cst = rb * 32 + acc_row_const(r);
-                            float oms;
-                            const float edge = soft_edge_log2(wc, (float)(A - cst), p.inv_tau, oms);
-                            const float x = sacc[rb][r] + ((cst < Bc) ? edge * p.inv_c : 0.f);
-                            sacc[rb][r] = ((cst <= A) & (cst >= B)) ? x : -INFINITY;
-                        }
-                } else if (need_lo | need_hi) {
-                    const uint32_t keep = rows_le(A) & ~rows_le(B - 1);
-#pragma unroll
-                    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) sacc[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r]);
-                }
-            } else {
+    // masks / biases of tile t folded into its raw scores (bias / c), then softmax + PV.
+    // Each variant calls its own copy of softmax_pv, so the masked scores never have
+    // to be merged back into the registers of the unmasked ones.
+    auto tile_update = [&](int t, f32x16 (&sacc)[2]) {
+        const int stage = t & (NSTAGE - 1);
+        if (t < nb) {
+            const int tb = band_key0(t);
+            // element (rb, r) is key tb + rb*32 + acc_row_const(r) + hh*4 =: tb + hh*4 + cst
+            const int A = i - tb - hh * 4;   // key <= i       <=> cst <= A
+            const int B = lo - tb - hh * 4;  // key >= lo      <=> cst >= B
+            const bool need_lo = tb < wclo;
+            const bool need_hi = tb + BN - 1 > wchi;
+            if (MODE == kSoft && need_lo) {
+                const int Bc = corelo - tb - hh * 4;  // key >= corelo <=> cst >= Bc
+                f32x16 x[2];
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int slot = lt * BN + rb * 32 + g * 8 + hh * 4;
-                        const int4 pos = *reinterpret_cast<const int4 *>(&s_lpos[slot]);
-                        const float4 bia = *reinterpret_cast<const float4 *>(&s_lbias[slot]);
-                        const int pp[4] = {pos.x, pos.y, pos.z, pos.w};
-                        const float bb[4] = {bia.x, bia.y, bia.z, bia.w};
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int r = g * 4 + e;
-                            sacc[rb][r] = (pp[e] <= pmax) ? sacc[rb][r] + bb[e] : -INFINITY;
-                        }
+                    for (int r = 0; r < 16; ++r) {
+                        const int cst = rb * 32 + acc_row_const(r);
+                        float oms;
+                        const float edge = soft_edge_log2(wv, (float)(A - cst), p.inv_tau, oms);
+                        const float y = sacc[rb][r] + ((cst < Bc) ? edge * p.inv_c : 0.f);
+                        x[rb][r] = ((cst <= A) & (cst >= B)) ? y : -INFINITY;
                     }
-            }
-
-            // ---- online softmax (base 2, stale max) ----------------------------------
-            float t0 = fmaxf(fmaxf(sacc[0][0], sacc[0][1]), sacc[0][2]);
-            float t1 = fmaxf(fmaxf(sacc[0][3], sacc[0][4]), sacc[0][5]);
-            float t2 = fmaxf(fmaxf(sacc[1][0], sacc[1][1]), sacc[1][2]);
-            float t3 = fmaxf(fmaxf(sacc[1][3], sacc[1][4]), sacc[1][5]);
+                softmax_pv(x, stage);
+            } else if (need_lo | need_hi) {
+                const uint32_t keep = rows_le(A) & ~rows_le(B - 1);
+                f32x16 x[2];
 #pragma unroll
-            for (int r = 6; r < 16; r += 2) {
-                t0 = fmaxf(fmaxf(t0, sacc[0][r]), sacc[0][r + 1]);
-                t2 = fmaxf(fmaxf(t2, sacc[1][r]), sacc[1][r + 1]);
-            }
-            const float tmax = half_max(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)));
-            const float tm2 = tmax * c;
-            if (tm2 > m2 + kStaleMax) {
-                const float alpha = fast_exp2(m2 - tm2);
-                lsum0 *= alpha;
-                lsum1 *= alpha;
+                for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-                for (int d = 0; d < ND; ++d)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
-                m2 = tm2;
+                    for (int r = 0; r < 16; ++r) x[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r]);
+                softmax_pv(x, stage);
+            } else {
+                softmax_pv(sacc, stage);
             }
-            const float mu = (m2 == -INFINITY) ? 0.f : m2;
-            // P in fp32: its row sum (fp32, unrounded, as the LSE needs it) and its
-            // 16-bit rounding (the PV operand)
-            uint32_t pk[2][8];
+        } else {
+            const int lt = lmk_tile(t);
+            f32x16 x[2];
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float e0 = fast_exp2(fmaf(sacc[rb][2 * j], c, -mu));
-                    const float e1 = fast_exp2(fmaf(sacc[rb][2 * j + 1], c, -mu));
-                    if (j & 1) lsum1 += e0 + e1;
-                    else lsum0 += e0 + e1;
-                    pk[rb][j] = DT::pack2(e0, e1);
-                }
-            // O^T (D x 32 queries) += V^T . P^T ; k-step kk covers tile keys kk*16..+15
+                for (int g = 0; g < 4; ++g) {
+                    const int slot = lt * BN + rb * 32 + g * 8 + hh * 4;
+                    const int4 pos = *reinterpret_cast<const int4 *>(&s_lpos[slot]);
+                    const float4 bia = *reinterpret_cast<const float4 *>(&s_lbias[slot]);
+                    const int pp[4] = {pos.x, pos.y, pos.z, pos.w};
+                    const float bb[4] = {bia.x, bia.y, bia.z, bia.w};
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const int rb = kk >> 1, g = kk & 1;
-                const vec8 b = bitcast<vec8>(
-                    make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
-#pragma unroll
-                for (int d = 0; d < ND; ++d) {
-                    const vec8 a = bitcast<vec8>(tile_read_tr<D>(vtile, kk * 16, d * 32, lane));
-                    oacc[d] = DT::mfma(a, b, oacc[d]);
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = g * 4 + e;
+                        x[rb][r] = (pp[e] <= pmax) ? sacc[rb][r] + bb[e] : -INFINITY;
+                    }
                 }
-            }
+            softmax_pv(x, stage);
         }
+    };
 
-        // tile t+1 must have landed; tiles t+2 .. t+NSTAGE-1 may stay in flight
-        if (t + NSTAGE - 1 < nt) tile_barrier<(NSTAGE - 2) * LPT>();
+    // ---- software-pipelined tile loop ----------------------------------------------------
+    // Iteration t: refill the ring with tile t+3, issue S for tile t+1 (its MFMAs run
+    // while this wave does the softmax of tile t), softmax + PV of tile t, then wait
+    // until tile t+2 has landed. The ring holds tiles t (V in use), t+1 (K in use),
+    // t+2 (landing) and t+3 (in flight); tile t+3 reuses the stage of tile t-1, whose V
+    // every wave finished reading before the barrier that ended iteration t-1.
+    // nt >= NSTAGE - 1 = 3, and tiles 0..2 were issued during the setup.
+    auto step = [&](int t, f32x16 (&cur)[2], f32x16 (&nxt)[2], bool act_cur) -> bool {
+        if (t + NSTAGE - 1 < nt) issue_tile(t + NSTAGE - 1);
+        const bool act_nxt = (t + 1 < nt) && tile_active(t + 1);
+        if (t + 1 < nt) qk_tile((t + 1) & (NSTAGE - 1), nxt);  // also for inactive tiles: no
+                                                                 // register copies between buffers
+        if (act_cur) tile_update(t, cur);
+        if (t + NSTAGE - 1 < nt) tile_barrier<LPT>();
         else tile_barrier<0>();
-        buf = (buf + 1 == NSTAGE) ? 0 : buf + 1;
+        return act_nxt;
+    };
+    f32x16 sA[2], sB[2];
+    tile_barrier<LPT>();  // tiles 0 and 1 landed (tile 2 may be in flight)
+    bool act = tile_active(0);
+    qk_tile(0, sA);
+    for (int t = 0; t < nt; t += 2) {
+        act = step(t, sA, sB, act);
+        if (t + 1 < nt) act = step(t + 1, sB, sA, act);
     }
 
     // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln 2 --------------------------------

@@ -40,29 +40,64 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
 }
 
-// global_load_lds_dwordx4: lane i's 16 bytes at `src` land at LDS byte m0 + 16 * i.
-// `lds` must be wave-uniform (it is moved into m0).
-__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
-    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource (V#) over `bytes` bytes at `base`: loads at byte offsets >= bytes
+// (including offsets that wrapped below 0) are out of range and return zeros instead of
+// faulting. Word 3 is the gfx9 default (32-bit dwords, no swizzle, no stride).
+__device__ __forceinline__ i32x4 buffer_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    i32x4 r;
+    r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+    r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+    r.w = 0x00020000;
+    return r;
+}
+
+// buffer_load_dwordx4 ... lds: lane i's 16 bytes at byte offset voff of the buffer land
+// at LDS byte m0 + 16 * i. `lds` must be wave-uniform (it is moved into m0).
+__device__ __forceinline__ void dma16(uint32_t voff, i32x4 rsrc, uint32_t lds) {
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
 }
 
 // This wave's share of the direct loads of one tile (4 waves cover the tile): LPW load
-// instructions, counted by vmcnt. Physical chunk slot g holds logical chunk
-// (g % CPR) ^ swz(row) of row g / CPR; `row_src(row)` returns the byte address of that
-// row's element 0 in global memory (always a valid address: callers clamp out-of-range
-// rows onto a real row and mask them later). `tile_lds` = lds_addr(tile), wave-uniform.
-template <int D, int SWZ, typename RowSrc>
-__device__ __forceinline__ void tile_load_async(uint32_t tile_lds, int wave, int lane, RowSrc row_src) {
-    constexpr int CPR = Tile64<D>::CPR, LPW = Tile64<D>::LOADS_PER_WAVE;
+// instructions per tile, counted by vmcnt. Physical chunk slot g holds logical chunk
+// (g % CPR) ^ swz(row) of tile row g / CPR. The per-lane parts (tile row, byte offset of
+// the row and chunk for a given row stride) are computed once; a band tile then costs
+// one add per load, a gathered tile one multiply-add.
+template <int D, int SWZ>
+struct TileLanes {
+    static constexpr int CPR = D / 8, LPW = Tile64<D>::LOADS_PER_WAVE;
+    int row[LPW];
+    uint32_t chunk_off[LPW];  // byte offset of the lane's chunk inside its row
+    uint32_t lane_off[LPW];   // row * stride + chunk_off
+    __device__ __forceinline__ TileLanes(int wave, int lane, uint32_t stride) {
 #pragma unroll
-    for (int u = 0; u < LPW; ++u) {
-        const int slot0 = (wave * LPW + u) * 64;
-        const int g = slot0 + lane;
-        const int row = g / CPR;
-        const int c = (g % CPR) ^ tile_swz<SWZ>(row);
-        dma16(row_src(row) + c * 16, __builtin_amdgcn_readfirstlane(tile_lds + slot0 * 16));
+        for (int u = 0; u < LPW; ++u) {
+            const int g = (wave * LPW + u) * 64 + lane;
+            row[u] = g / CPR;
+            chunk_off[u] = (uint32_t)(((g % CPR) ^ tile_swz<SWZ>(row[u])) << 4);
+            lane_off[u] = (uint32_t)row[u] * stride + chunk_off[u];
+        }
     }
-}
+    __device__ __forceinline__ static uint32_t lds_slot(uint32_t tile_lds, int wave, int u) {
+        return __builtin_amdgcn_readfirstlane(tile_lds + (wave * LPW + u) * 64 * 16);
+    }
+    // Rows row0 .. row0+63 (row0 * stride = base_off, may wrap below 0) into the tile at
+    // LDS byte tile_lds (wave-uniform).
+    __device__ __forceinline__ void load_band(uint32_t tile_lds, int wave, i32x4 rsrc, uint32_t base_off) const {
+#pragma unroll
+        for (int u = 0; u < LPW; ++u) dma16(base_off + lane_off[u], rsrc, lds_slot(tile_lds, wave, u));
+    }
+    // Tile row r from buffer row rows[r].
+    __device__ __forceinline__ void load_gather(uint32_t tile_lds, int wave, i32x4 rsrc, uint32_t stride,
+                                                const int *rows) const {
+#pragma unroll
+        for (int u = 0; u < LPW; ++u)
+            dma16((uint32_t)rows[row[u]] * stride + chunk_off[u], rsrc, lds_slot(tile_lds, wave, u));
+    }
+};
 
 // Wait until at most N of this wave's vector-memory operations are outstanding (they
 // complete in issue order), i.e. until every direct load issued before the last N has
