@@ -84,6 +84,11 @@ int dsalt_fwd_check(const dsalt_fwd_args *a) {
     if (!(a->scale == a->scale)) return fail(DSALT_ERR_INVALID, "scale is NaN");
     if (a->scale == 0.f || !(fabsf(a->scale) < INFINITY))
         return fail(DSALT_ERR_UNSUPPORTED, "scale must be finite and non-zero (got %g)", (double)a->scale);
+    // K/V rows of one sequence are addressed with 32-bit byte offsets
+    const int64_t row_bytes = 2 * (a->k_stride_t > a->v_stride_t ? a->k_stride_t : a->v_stride_t);
+    if ((int64_t)a->total_len * row_bytes >= ((int64_t)1 << 32))
+        return fail(DSALT_ERR_UNSUPPORTED, "a sequence's K/V rows must span < 4 GiB (total_len %d x row stride %lld B)",
+                    a->total_len, (long long)row_bytes);
     return DSALT_OK;
 }
 

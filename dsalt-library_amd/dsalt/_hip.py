@@ -253,7 +253,9 @@ def _fwd_args(mode, q, k, v, w, lmk_pos, lmk_bias, cu_seqlens, scale, tau_win, w
     if out is None:
         out = torch.empty((T, H, D), device=dev, dtype=odt)
     if lse is None:
-        lse = torch.empty((T, H), device=dev, dtype=torch.float32)
+        # [T, H] view of head-major storage: a workgroup (one head, consecutive tokens)
+        # then writes its LSE values contiguously
+        lse = torch.empty((H, T), device=dev, dtype=torch.float32).t()
     a = FwdArgs()
     a.mode, a.dtype, a.total_len, a.num_seqs = mode, _DTYPES[q.dtype], T, S
     a.n_heads, a.head_dim, a.k_lmk = H, D, kl

@@ -64,6 +64,9 @@ enum { DSALT_MODE_HARD = 0, DSALT_MODE_SOFT = 1 };
  * the packed block map of _build_seq_block_map (selectors.py:37-67) happen inside the
  * kernel; `out` is written (no prior memset) in the input dtype, or in fp32 when
  * out_dtype = DSALT_DTYPE_F32 (the reference's entry points return O as fp32).
+ * Limits: `scale` finite and non-zero (a negative scale is applied by negating Q);
+ * total_len x max(k, v row stride) x 2 bytes < 4 GiB (K/V rows of a sequence are
+ * addressed with 32-bit offsets). Both are checked and return DSALT_ERR_UNSUPPORTED.
  */
 typedef struct dsalt_fwd_args {
     int32_t mode;      /* DSALT_MODE_HARD or DSALT_MODE_SOFT */

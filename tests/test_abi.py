@@ -79,6 +79,7 @@ def test_fwd_check_accepts_valid_args():
     ("tau_win", 0.0, 1, "tau_win"),
     ("scale", 0.0, 2, "scale"),
     ("scale", float("inf"), 2, "scale"),
+    ("k_stride_t", 1 << 30, 2, "4 GiB"),
 ])
 def test_fwd_check_rejects(field, value, code, needle):
     kw = {field: value}
