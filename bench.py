@@ -96,6 +96,101 @@ def make_workload(cfg: str, device: torch.device):
                 n_min=n_min, n_max=n_max, xp=xp, mod=mod)
 
 
+def effective_pairs_soft(w_cont: np.ndarray, lmk_pos: np.ndarray, cu: list[int]) -> int:
+    """Exact (query, key) pairs of the SOFT pattern summed over heads: per query
+    min(floor(w~), i) + 1 band keys (none when w~ < 0) plus the landmark slots p with
+    p <= i and p < i - w~ (fp32 compare)."""
+    H = lmk_pos.shape[0]
+    total = 0
+    for s in range(len(cu) - 1):
+        a, b = cu[s], cu[s + 1]
+        L = b - a
+        if L == 0:
+            continue
+        i = np.arange(L)
+        ws = w_cont[a:b].astype(np.float32)
+        with np.errstate(invalid="ignore"):
+            band = np.where(ws >= 0, np.minimum(np.floor(np.minimum(ws, 2.0 ** 30)), i) + 1, 0)
+        total += int(band.sum()) * H
+        thr = (i.astype(np.float32) - ws)  # p admitted iff p < thr (and p <= i)
+        for h in range(H):
+            p = lmk_pos[h, s]
+            p = np.sort(p[(p >= 0) & (p < L)]).astype(np.float32)
+            if p.size == 0:
+                continue
+            cnt = np.searchsorted(p, np.where(np.isnan(thr), -np.inf, thr), side="left")  # p < thr
+            cnt = np.minimum(cnt, np.searchsorted(p, i.astype(np.float32), side="right"))  # p <= i
+            total += int(cnt.sum())
+    return total
+
+
+def make_train_workload(device: torch.device):
+    """BASELINE config 3: eight sequences with lengths numpy.random.seed(2);
+    randint(256, 2049, 8) packed into one stream (T = 9290), DSALTAttention(1024, 16, 32,
+    512, 64) at random init (seed 2), x ~ N(0, 1), dO ~ N(0, 1); the SOFT (training)
+    selection and attention inputs the module produces."""
+    from dsalt.modules import DSALTAttention
+    from dsalt.kernels.window_utils import apply_rotary_emb
+
+    np.random.seed(2)
+    lens = [int(x) for x in np.random.randint(256, 2049, 8)]
+    d_model, H, n_min, n_max, k_lmk = 1024, 16, 32, 512, 64
+    torch.manual_seed(2)
+    mod = DSALTAttention(d_model, H, n_min, n_max, k_lmk, max_seq_len=2048).to(device).train()
+    T = sum(lens)
+    x = torch.randn(T, d_model).to(device)
+    cu_list = [0]
+    for L in lens:
+        cu_list.append(cu_list[-1] + L)
+    cu = torch.tensor(cu_list, dtype=torch.int32, device=device)
+    D = d_model // H
+    with torch.no_grad():
+        w_cont, lmk_pos, lmk_logw = mod._train_selectors(x, cu, T, device, cu_list)
+        q = mod.q_proj(x).view(T, H, D)
+        k = mod.k_proj(x).view(T, H, D)
+        v = mod.v_proj(x).view(T, H, D)
+        pos_ids = torch.cat([torch.arange(L, device=device) for L in lens])
+        cos, sin = mod.rope_cos[pos_ids].unsqueeze(1), mod.rope_sin[pos_ids].unsqueeze(1)
+        q, k = apply_rotary_emb(q, k, cos, sin)
+        q, k, v = (t.to(torch.bfloat16).contiguous() for t in (q, k, v))
+    dout = torch.randn(T, H, D, generator=torch.Generator().manual_seed(102)).to(torch.bfloat16).to(device)
+    torch.cuda.synchronize()
+    return dict(q=q, k=k, v=v, w=w_cont.float().contiguous(), lmk=lmk_pos, logw=lmk_logw.float().contiguous(),
+                cu=cu, cu_list=cu_list, T=T, H=H, D=D, lens=lens, k_lmk=k_lmk, dout=dout)
+
+
+def measure_backward(device: torch.device, steps: int = 20, warmup: int = 3) -> dict:
+    """SOFT forward and backward (dQ, dK, dV, d_lmk_logw, d_w~) at config 3, bf16 in and out."""
+    from dsalt import _hip
+
+    wl = make_train_workload(device)
+    q, k, v, T, H, D = wl["q"], wl["k"], wl["v"], wl["T"], wl["H"], wl["D"]
+    scale = 1.0 / math.sqrt(D)
+    fwd = _hip.FwdLauncher(_hip.MODE_SOFT, q, k, v, wl["w"], wl["lmk"], wl["logw"], wl["cu"], scale)
+    fwd_ms = time_launches(fwd, steps, warmup)
+    bwd = _hip.BwdLauncher(_hip.MODE_SOFT, q, k, v, fwd.out, fwd.lse, wl["dout"], wl["w"], wl["lmk"], wl["logw"],
+                           wl["cu"], scale, need_dw=True)
+    bwd_ms = time_launches(bwd, steps, warmup)
+    P = effective_pairs_soft(wl["w"].cpu().numpy(), wl["lmk"].cpu().numpy(), wl["cu_list"])
+    t_b, t_f = bwd_ms * 1e-3, fwd_ms * 1e-3
+    bytes_bwd = 2 * T * H * D * 8 + 8 * T * H  # read Q, K, V, O, dO; write dQ, dK, dV (16-bit); LSE, Delta
+    bytes_fwd = 2 * T * H * D * 4 + 4 * T * H + 4 * T + 12 * H * len(wl["lens"]) * wl["k_lmk"]
+    return {
+        "workload": f"c3: SOFT DSALT attention forward + backward, {len(wl['lens'])} packed sequences "
+                    f"(T = {T}), {H} heads x {D} head_dim, n_min 32, n_max 512, k_lmk 64, bf16",
+        "pairs": P,
+        "fwd_ms": fwd_ms,
+        "bwd_ms": bwd_ms,
+        "fwd_tflops": 4.0 * D * P / t_f / 1e12,
+        "bwd_tflops": 10.0 * D * P / t_b / 1e12,
+        "bwd_mfma_frac": 10.0 * D * P / t_b / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "bwd_hbm_GBs": bytes_bwd / t_b / 1e9,
+        "bwd_hbm_frac": bytes_bwd / t_b / 1e9 / HBM_PEAK_GBS,
+        "fwd_hbm_GBs": bytes_fwd / t_f / 1e9,
+        "tokens_per_s_fwd_bwd": T / (t_f + t_b),
+    }
+
+
 def time_launches(fn, steps: int, warmup: int) -> float:
     for _ in range(warmup):
         fn()
@@ -150,6 +245,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-backward", action="store_true", help="skip the config-3 backward measurement")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -237,6 +333,8 @@ def main():
         "quantize_ms": qz_ms,
         "path_ms": ms + sel_ms + qz_ms,
     }
+    if not args.no_backward:
+        res["backward"] = measure_backward(dev)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(wl)
     print(json.dumps(res))

@@ -291,6 +291,31 @@ def bwd(mode: int, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, sc
     """Sparse-attention backward. Returns (dq, dk, dv, d_lmk_bias [H,S,k] fp32 or None,
     d_w [T] fp32 or None); dq/dk/dv are in ``grad_dtype`` (q.dtype or torch.float32,
     default q.dtype)."""
+    launcher = BwdLauncher(mode, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, scale,
+                           tau_win, win_edge, need_dw, grad_dtype)
+    launcher()
+    return launcher.results
+
+
+class BwdLauncher:
+    """A backward launch with its argument block, outputs and workspace built once;
+    calling it re-launches on the current stream with the same buffers."""
+
+    def __init__(self, mode: int, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, scale: float,
+                 tau_win: float = 1.0, win_edge: float = 4.0, need_dw: bool = False,
+                 grad_dtype: torch.dtype | None = None):
+        self.args, self._keep, self.results, self.device = _bwd_args(
+            mode, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, scale, tau_win, win_edge,
+            need_dw, grad_dtype)
+        self._fn = lib().dsalt_bwd
+        self._ref = ctypes.byref(self.args)
+
+    def __call__(self) -> None:
+        _raise(self._fn(self._ref, stream_handle(self.device)), "dsalt_bwd")
+
+
+def _bwd_args(mode, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, scale, tau_win, win_edge,
+              need_dw, grad_dtype):
     dev = require_gpu(q, k, v, out, lse, dout, w, cu_seqlens)
     T, H, D = q.shape
     cu = _cu_i32(cu_seqlens)
@@ -340,8 +365,8 @@ def bwd(mode: int, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, sc
     a.d_w = _ptr(d_w)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
     a.scale, a.tau_win, a.win_edge = float(scale), float(tau_win), float(win_edge)
-    _raise(lib().dsalt_bwd(ctypes.byref(a), stream_handle(dev)), "dsalt_bwd")
-    return dq, dk, dv, d_bias, d_w
+    keep = (q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu, ws)  # must outlive the args
+    return a, keep, (dq, dk, dv, d_bias, d_w), dev
 
 
 def select_landmarks(scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Tensor,
