@@ -12,18 +12,20 @@
 // element is produced by exactly one thread, in a fixed order.
 //
 // Kernels, launched in this order on one stream:
-//   prep    one workgroup per 128-token block: Delta for all heads, and the smallest band
-//           start of the block (bounds the key-parallel query scan of `kv`).
-//   lmk_kv  key-parallel over landmark slots: one workgroup per (head, sequence, 64 slots);
-//           4 waves = 2 slot groups x 2 query sub-blocks scan the sequence's queries in
-//           64-query LDS tiles. Writes landmark dK/dV partials (workspace) and d_bias.
+//   prep    one workgroup per (128-token block, head): Delta, and (head 0) the smallest
+//           band start of the block (bounds the key-parallel query scan of `kv`).
+//   lmk_kv  key-parallel over landmark slots: one workgroup per (head, 64 slots, chunk of
+//           512 queries of one sequence); 4 waves = 2 slot groups x 2 query sub-blocks scan
+//           the chunk's queries in 64-query LDS tiles. Writes landmark dK/dV and d_bias
+//           partials per chunk (workspace).
 //   dq      query-parallel, 4 waves x 32 queries per workgroup, the forward's tiling (band
 //           tiles, then gathered landmark tiles); S^T, dP^T and dQ^T on MFMA. Writes dQ and
 //           the per-head soft-edge d_w~ (workspace).
 //   kv      key-parallel band dK/dV, 4 waves x 32 keys per workgroup, scanning 64-query LDS
 //           tiles from the key block to the last query block whose band reaches it; adds
-//           the landmark partials of keys that are landmark positions; its head-0
-//           workgroups also reduce d_w~ over heads.
+//           the landmark partials (over the sequence's chunks) of keys that are landmark
+//           positions; its head-0 workgroups reduce d_w~ over heads.
+//   dbias   d_lmk_bias = sum of the lmk_kv chunk partials, one workgroup per (head, seq).
 // Every MFMA is v_mfma_f32_32x32x16 with operands in the layouts of the forward kernel:
 // a lane owns one column (query or key) of each 32x32 block and 16 rows of it.
 #include "common.h"
@@ -36,6 +38,7 @@ constexpr int kPad8 = 8;  // row-major tile row padding (halves): conflict-free 
 constexpr int kPad4 = 4;  // transposed tile row padding (halves): conflict-free b64 reads
 constexpr int kBM = 128;  // queries (dq) / keys (kv) per workgroup; prep block size
 constexpr int kTN = 64;   // keys per tile (dq) / queries per tile (kv, lmk_kv)
+constexpr int kLC = 512;  // queries per lmk_kv chunk (chunks are numbered like query blocks)
 
 struct BwdParams {
     const uint16_t *q, *k, *v, *dout;
@@ -49,11 +52,12 @@ struct BwdParams {
     float *ws_delta;         // [T*H]
     int *ws_minlo;           // [n_qblk]
     float *ws_dwh;           // [T*H] or null
-    float *ws_ldk, *ws_ldv;  // [H*S*k_pad*D] or null
+    float *ws_ldk, *ws_ldv;  // landmark dK/dV partials [H][n_lchunk][k_pad][D] or null
+    float *ws_ldb;           // landmark d_bias partials [H][n_lchunk][k_pad] or null
     int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, do_st, do_sh, lse_st, lse_sh, w_st;
     int64_t lp_sh, lp_ss, lp_sk, lb_sh, lb_ss, lb_sk;
     int64_t dq_st, dq_sh, dk_st, dk_sh, dv_st, dv_sh;
-    int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid_q, n_lgrp, grad_f32, o_f32;
+    int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid_q, n_lgrp, n_lchunk, grad_f32, o_f32;
     float scale, scale_log2, inv_tau, win_edge;
 };
 
@@ -99,61 +103,64 @@ __device__ __forceinline__ void pack_block(const f32x16 &x, uint32_t (&pk)[8]) {
 }
 
 // ==================================================================================
-// prep: Delta = rowsum(O * dO) for all heads and the block's smallest band start
+// prep: Delta = rowsum(O * dO), one workgroup per (128-token block, head), two threads
+// per token; the head-0 workgroup of a block also records the block's smallest band start
 // ==================================================================================
 template <typename DT, int D, int MODE>
 __global__ void __launch_bounds__(256) bwd_prep_kernel(const BwdParams p) {
     __shared__ int s_min[4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int seq, blk;
-    if (!find_block(p.cu, p.num_seqs, blockIdx.x, kBM, lane, seq, blk)) return;
-    const int seq_start = p.cu[seq];
-    const int seq_len = p.cu[seq + 1] - seq_start;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int head = blockIdx.x % p.n_heads;
+    const int bidx = blockIdx.x / p.n_heads;
+    int seq, blk, seq_start, seq_len;
+    if (!find_block(p.cu, p.num_seqs, bidx, kBM, lane, seq, blk, seq_start, seq_len)) return;
     const int base = blk * kBM;
-    const int nvalid = min(kBM, seq_len - base);
-
-    int lo = INT_MAX;
-    if (tid < nvalid) {
-        const int i = base + tid;
-        int corelo, pmax;
-        query_ranges<MODE>(i, p.w[((int64_t)seq_start + i) * p.w_st], p.win_edge, lo, corelo, pmax);
-    }
-    lo = wave_min(lo);
-    if (lane == 0) s_min[wave] = lo;
+    const int t = tid >> 1, half = tid & 1;
+    const bool valid = base + t < seq_len;
+    const int64_t tok = (int64_t)seq_start + base + t;
 
     // Delta uses O as stored (fp32 when the forward wrote fp32) and dO in the compute dtype
     // (dsalt_triton_train.py:673-674)
-    constexpr int G = D / 8;  // lanes per (token, head) pair, 8 elements each
-    const int H = p.n_heads;
-    const int npairs = nvalid * H;
-    const int c = tid % G;
-    for (int pp = tid / G; pp < npairs; pp += 256 / G) {
-        const int t = pp / H, h = pp - t * H;
-        const int64_t tok = (int64_t)seq_start + base + t;
-        const int64_t ooff = tok * p.o_st + (int64_t)h * p.o_sh + c * 8;
-        const uint4 d8 = ld16(p.dout + tok * p.do_st + (int64_t)h * p.do_sh + c * 8);
-        const uint16_t *de = reinterpret_cast<const uint16_t *>(&d8);
-        float of[8];
-        if (p.o_f32) {
-            const float4 a = *reinterpret_cast<const float4 *>(static_cast<const float *>(p.o) + ooff);
-            const float4 b = *reinterpret_cast<const float4 *>(static_cast<const float *>(p.o) + ooff + 4);
-            of[0] = a.x; of[1] = a.y; of[2] = a.z; of[3] = a.w;
-            of[4] = b.x; of[5] = b.y; of[6] = b.z; of[7] = b.w;
-        } else {
-            const uint4 o8 = ld16(static_cast<const uint16_t *>(p.o) + ooff);
-            const uint16_t *oe = reinterpret_cast<const uint16_t *>(&o8);
+    constexpr int HALF = D / 2;  // elements per thread
+    float acc = 0.f;
+    if (valid) {
+        const int64_t ooff = tok * p.o_st + (int64_t)head * p.o_sh + half * HALF;
+        const uint16_t *dp = p.dout + tok * p.do_st + (int64_t)head * p.do_sh + half * HALF;
 #pragma unroll
-            for (int x = 0; x < 8; ++x) of[x] = DT::to_f32(oe[x]);
+        for (int c = 0; c < HALF / 8; ++c) {
+            const uint4 d8 = ld16(dp + c * 8);
+            const uint16_t *de = reinterpret_cast<const uint16_t *>(&d8);
+            float of[8];
+            if (p.o_f32) {
+                const float4 x = *reinterpret_cast<const float4 *>(static_cast<const float *>(p.o) + ooff + c * 8);
+                const float4 y = *reinterpret_cast<const float4 *>(static_cast<const float *>(p.o) + ooff + c * 8 + 4);
+                of[0] = x.x; of[1] = x.y; of[2] = x.z; of[3] = x.w;
+                of[4] = y.x; of[5] = y.y; of[6] = y.z; of[7] = y.w;
+            } else {
+                const uint4 o8 = ld16(static_cast<const uint16_t *>(p.o) + ooff + c * 8);
+                const uint16_t *oe = reinterpret_cast<const uint16_t *>(&o8);
+#pragma unroll
+                for (int x = 0; x < 8; ++x) of[x] = DT::to_f32(oe[x]);
+            }
+#pragma unroll
+            for (int x = 0; x < 8; ++x) acc = fmaf(of[x], DT::to_f32(de[x]), acc);
         }
-        float acc = 0.f;
-#pragma unroll
-        for (int x = 0; x < 8; ++x) acc = fmaf(of[x], DT::to_f32(de[x]), acc);
-#pragma unroll
-        for (int o = G / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-        if (c == 0) p.ws_delta[tok * H + h] = acc;
     }
-    __syncthreads();
-    if (tid == 0) p.ws_minlo[blockIdx.x] = min(min(s_min[0], s_min[1]), min(s_min[2], s_min[3]));
+    acc += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc), 0xB1, 0xF, 0xF, false));  // + partner
+    if (valid && half == 0) p.ws_delta[tok * p.n_heads + head] = acc;
+
+    if (head == 0) {  // smallest band start of the block
+        int lo = INT_MAX;
+        if (tid < kBM && base + tid < seq_len) {
+            const int i = base + tid;
+            int corelo, pmax;
+            query_ranges<MODE>(i, p.w[((int64_t)seq_start + i) * p.w_st], p.win_edge, lo, corelo, pmax);
+        }
+        lo = wave_min_u(lo);
+        if (lane == 0) s_min[wave] = lo;
+        __syncthreads();
+        if (tid == 0) p.ws_minlo[bidx] = min(min(s_min[0], s_min[1]), min(s_min[2], s_min[3]));
+    }
 }
 
 // ==================================================================================
@@ -437,7 +444,7 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int ql = lane & 31, hh = lane >> 5;
 
-    int head, seq, kblk = 0, gbase = 0, q_begin, q_end, slot = 0, sbw = 0, kw = 0;
+    int head, seq, kblk = 0, gbase = 0, q_begin, q_end, slot = 0, sbw = 0, kw = 0, lcid = 0, lchunk = 0;
     int key = INT_MAX;  // this lane's key position in the sequence (INT_MAX: none)
     float kbias2 = 0.f;
     if (!LMK) {
@@ -448,11 +455,13 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
         if (!find_block(p.cu, p.num_seqs, target, kBM, lane, seq, kblk)) return;
         gbase = target - kblk;
     } else {
-        const int per_head = p.num_seqs * p.n_lgrp;
+        // workgroup = (head, 64-slot group, query chunk); chunk ids follow find_block
+        const int per_head = p.n_lgrp * p.n_lchunk;
         head = blockIdx.x / per_head;
         const int rem = blockIdx.x - head * per_head;
-        seq = rem / p.n_lgrp;
-        const int gp = rem - seq * p.n_lgrp;
+        const int gp = rem / p.n_lchunk;
+        lcid = rem - gp * p.n_lchunk;
+        if (!find_block(p.cu, p.num_seqs, lcid, kLC, lane, seq, lchunk)) return;
         sbw = wave & 1;
         slot = gp * 64 + (wave >> 1) * 32 + ql;
     }
@@ -487,8 +496,8 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
         if (lane == 0) sm.misc[wave] = mn;
         __syncthreads();
         const int gmin = min(min(sm.misc[0], sm.misc[1]), min(sm.misc[2], sm.misc[3]));
-        q_begin = (gmin == INT_MAX) ? seq_len : gmin;
-        q_end = seq_len;
+        q_end = min(seq_len, (lchunk + 1) * kLC);
+        q_begin = (gmin == INT_MAX) ? q_end : min(max(gmin, lchunk * kLC), q_end);
     }
     const bool kvalid = key != INT_MAX;
     const int wkmin = LMK ? wave_min(key) : kw;
@@ -522,7 +531,7 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
             const int row = c / CPR, col = c % CPR;
             const int q = q0 + row;
             uint4 a = make_uint4(0, 0, 0, 0), b = a;
-            if (q < seq_len) {
+            if (q < q_end) {  // queries past q_end belong to another workgroup
                 const int64_t tok = (int64_t)seq_start + q;
                 a = ld16(p.q + tok * p.q_st + (int64_t)head * p.q_sh + col * 8);
                 b = ld16(p.dout + tok * p.do_st + (int64_t)head * p.do_sh + col * 8);
@@ -538,7 +547,7 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
             plo = INT_MAX;
             pclo = INT_MAX;
             ppm = -1;
-            if (q < seq_len) {
+            if (q < q_end) {  // queries past q_end belong to another workgroup
                 const int64_t tok = (int64_t)seq_start + q;
                 const float lv = p.lse[tok * p.lse_st + (int64_t)head * p.lse_sh];
                 pl = (lv == -INFINITY) ? INFINITY : lv * kLog2e;
@@ -607,7 +616,7 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
         for (int sbi = 0; sbi < (LMK ? 1 : 2); ++sbi) {
             const int sb = LMK ? sbw : sbi;
             const int qsb = q_begin + t * QT + sb * 32;  // first query of the sub-block
-            bool skip = qsb >= seq_len;
+            bool skip = qsb >= q_end;
             if (!LMK) skip = skip || (qsb + 31 < kw) || (sm.sb[buf][sb][0] > wkmax);
             else skip = skip || (sm.sb[buf][sb][3] < wkmin);
             if (skip) continue;
@@ -690,9 +699,10 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
     }
 
     if (!LMK) {
-        // landmark contributions of keys that are landmark positions (computed by lmk_kv)
+        // landmark contributions of keys that are landmark positions (computed by lmk_kv
+        // per query chunk; summed here over the sequence's chunks in a fixed order)
         if (p.ws_ldk) {
-            const size_t base = ((size_t)head * p.num_seqs + seq) * p.k_pad;
+            const int c_first = seq_start / kLC + seq, n_ch = (seq_len + kLC - 1) / kLC;
             for (int s0 = 0; s0 < p.k_lmk; s0 += 64) {
                 int pos = -1;
                 if (s0 + lane < p.k_lmk) {
@@ -705,20 +715,23 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
                     m &= m - 1;
                     const int pb = __shfl(pos, b);
                     if (key == pb) {
-                        const float *gk = p.ws_ldk + (base + s0 + b) * D;
-                        const float *gv = p.ws_ldv + (base + s0 + b) * D;
+                        for (int ch = 0; ch < n_ch; ++ch) {
+                            const size_t row = ((size_t)head * p.n_lchunk + c_first + ch) * p.k_pad + s0 + b;
+                            const float *gk = p.ws_ldk + row * D;
+                            const float *gv = p.ws_ldv + row * D;
 #pragma unroll
-                        for (int d = 0; d < ND; ++d)
+                            for (int d = 0; d < ND; ++d)
 #pragma unroll
-                            for (int g = 0; g < 4; ++g) {
-                                const int dd = d * 32 + g * 8 + hh * 4;
-                                const float4 a = *reinterpret_cast<const float4 *>(gk + dd);
-                                const float4 b4 = *reinterpret_cast<const float4 *>(gv + dd);
-                                dk[d][g * 4 + 0] += a.x; dk[d][g * 4 + 1] += a.y;
-                                dk[d][g * 4 + 2] += a.z; dk[d][g * 4 + 3] += a.w;
-                                dv[d][g * 4 + 0] += b4.x; dv[d][g * 4 + 1] += b4.y;
-                                dv[d][g * 4 + 2] += b4.z; dv[d][g * 4 + 3] += b4.w;
-                            }
+                                for (int g = 0; g < 4; ++g) {
+                                    const int dd = d * 32 + g * 8 + hh * 4;
+                                    const float4 a = *reinterpret_cast<const float4 *>(gk + dd);
+                                    const float4 b4 = *reinterpret_cast<const float4 *>(gv + dd);
+                                    dk[d][g * 4 + 0] += a.x; dk[d][g * 4 + 1] += a.y;
+                                    dk[d][g * 4 + 2] += a.z; dk[d][g * 4 + 3] += a.w;
+                                    dv[d][g * 4 + 0] += b4.x; dv[d][g * 4 + 1] += b4.y;
+                                    dv[d][g * 4 + 2] += b4.z; dv[d][g * 4 + 3] += b4.w;
+                                }
+                        }
                     }
                 }
             }
@@ -765,7 +778,7 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
                 }
             dbias += mine[2 * ND * 16];
             const float db = half_sum(dbias);
-            const size_t row = ((size_t)head * p.num_seqs + seq) * p.k_pad + slot;
+            const size_t row = ((size_t)head * p.n_lchunk + lcid) * p.k_pad + slot;
             float *gk = p.ws_ldk + row * D;
             float *gv = p.ws_ldv + row * D;
 #pragma unroll
@@ -778,14 +791,26 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
                     *reinterpret_cast<float4 *>(gv + dd) =
                         make_float4(dv[d][gg * 4], dv[d][gg * 4 + 1], dv[d][gg * 4 + 2], dv[d][gg * 4 + 3]);
                 }
-            if (hh == 0 && slot < p.k_lmk && p.d_bias)
-                p.d_bias[((size_t)head * p.num_seqs + seq) * p.k_lmk + slot] = db;
+            if (hh == 0) p.ws_ldb[row] = db;
         }
     }
 }
 
+// d_bias[h, s, slot] = sum over the query chunks of sequence s of the lmk_kv partials
+// (fixed order; zero for empty sequences). One workgroup of 64 threads per (head, sequence).
+__global__ void __launch_bounds__(64) bwd_dbias_kernel(const BwdParams p) {
+    const int head = blockIdx.x / p.num_seqs, seq = blockIdx.x - head * p.num_seqs;
+    const int seq_start = p.cu[seq], seq_len = p.cu[seq + 1] - seq_start;
+    const int c_first = seq_start / kLC + seq, n_ch = (seq_len + kLC - 1) / kLC;
+    for (int sl = threadIdx.x; sl < p.k_lmk; sl += 64) {
+        float acc = 0.f;
+        for (int ch = 0; ch < n_ch; ++ch) acc += p.ws_ldb[((size_t)head * p.n_lchunk + c_first + ch) * p.k_pad + sl];
+        p.d_bias[((size_t)head * p.num_seqs + seq) * p.k_lmk + sl] = acc;
+    }
+}
+
 struct WsLayout {
-    size_t delta, minlo, dwh, ldk, ldv, total;
+    size_t delta, minlo, dwh, ldk, ldv, ldb, total;
 };
 
 WsLayout ws_layout(int T, int S, int H, int D, int k) {
@@ -799,20 +824,26 @@ WsLayout ws_layout(int T, int S, int H, int D, int k) {
     L.dwh = off;
     off += al((size_t)T * H * 4);
     const size_t kp = (size_t)((k + 63) / 64 * 64);
+    const size_t nch = (size_t)block_upper_bound(T, S, kLC);
     L.ldk = off;
-    off += al((size_t)H * S * kp * D * 4);
+    off += al((size_t)H * nch * kp * D * 4);
     L.ldv = off;
-    off += al((size_t)H * S * kp * D * 4);
+    off += al((size_t)H * nch * kp * D * 4);
+    L.ldb = off;
+    off += al((size_t)H * nch * kp * 4);
     L.total = off;
     return L;
 }
 
 template <typename DT, int D, int MODE>
 hipError_t launch_typed(const BwdParams &p, hipStream_t stream) {
-    hipLaunchKernelGGL((bwd_prep_kernel<DT, D, MODE>), dim3(p.n_qblk), dim3(256), 0, stream, p);
-    if (p.k_lmk > 0)
-        hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, true>), dim3(p.n_heads * p.num_seqs * p.n_lgrp), dim3(256),
+    hipLaunchKernelGGL((bwd_prep_kernel<DT, D, MODE>), dim3(p.n_qblk * p.n_heads), dim3(256), 0, stream, p);
+    if (p.k_lmk > 0) {
+        hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, true>), dim3(p.n_heads * p.n_lgrp * p.n_lchunk), dim3(256),
                            0, stream, p);
+        if (p.d_bias)
+            hipLaunchKernelGGL(bwd_dbias_kernel, dim3(p.n_heads * p.num_seqs), dim3(64), 0, stream, p);
+    }
     const size_t dyn = (size_t)p.k_pad * (sizeof(int) + sizeof(float));
     hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE>), dim3(p.grid_q), dim3(256), dyn, stream, p);
     hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false>), dim3(p.grid_q), dim3(256), 0, stream, p);
@@ -863,6 +894,7 @@ hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream) {
     p.ws_dwh = p.d_w ? reinterpret_cast<float *>(ws + L.dwh) : nullptr;
     p.ws_ldk = a.k_lmk > 0 ? reinterpret_cast<float *>(ws + L.ldk) : nullptr;
     p.ws_ldv = a.k_lmk > 0 ? reinterpret_cast<float *>(ws + L.ldv) : nullptr;
+    p.ws_ldb = a.k_lmk > 0 ? reinterpret_cast<float *>(ws + L.ldb) : nullptr;
     p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
     p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;
     p.v_st = a.v_stride_t; p.v_sh = a.v_stride_h;
@@ -881,6 +913,7 @@ hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream) {
     p.k_lmk = a.k_lmk;
     p.k_pad = (a.k_lmk + 63) / 64 * 64;
     p.n_lgrp = p.k_pad / 64;
+    p.n_lchunk = block_upper_bound(a.total_len, a.num_seqs, kLC);
     p.n_qblk = block_upper_bound(a.total_len, a.num_seqs, kBM);
     p.grid_q = (int)(((int64_t)p.n_qblk * a.n_heads + 7) / 8 * 8);
     p.scale = a.scale;
