@@ -30,6 +30,7 @@
 // a lane owns one column (query or key) of each 32x32 block and 16 rows of it.
 #include "common.h"
 #include "launch.h"
+#include "tiles.h"
 
 namespace dsalt {
 namespace {
@@ -166,35 +167,61 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(const BwdParams p) {
 // ==================================================================================
 // dq: query-parallel dQ (band + landmarks) and per-head soft-edge d_w~
 // ==================================================================================
+// The forward's structure: one workgroup = 4 waves x 32 queries of one (sequence, head);
+// K and V tiles of 64 keys stream through a 4-stage LDS ring by direct global->LDS loads
+// (band tiles from the diagonal down, then the gathered landmark tiles). Per tile a wave
+// computes S^T = K.Q^T and dP^T = V.dO^T (lane = query column), P = 2^(S c + bias - lse2)
+// on admitted pairs, dS = P (dP - Delta), and dQ^T += K^T.dS^T with K read transposed.
 template <typename DT, int D, int MODE>
 __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     typedef typename DT::vec8 vec8;
     constexpr int BN = kTN;
-    constexpr int KS = D / 16, ND = D / 32, CPR = D / 8, PER_T = BN * CPR / 256;
+    constexpr int KS = D / 16, ND = D / 32;
+    constexpr int TB = Tile64<D>::BYTES;
+    constexpr int NSTAGE = 4;
+    constexpr int LPT = 2 * Tile64<D>::LOADS_PER_WAVE;
 
-    __shared__ __align__(16) uint16_t ks[2][BN][D + kPad8];
-    __shared__ __align__(16) uint16_t vs[2][BN][D + kPad8];
-    __shared__ __align__(16) uint16_t kt[2][D][BN + kPad4];
-    __shared__ int s_red[4][3];
-    __shared__ int s_ltile[DSALT_MAX_K_LMK / BN];
-    __shared__ int s_nlt;
+    __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][K, V], both row-swizzled
+    __shared__ int s_red[4][2];
+    __shared__ int s_ltmin[DSALT_MAX_K_LMK / BN];
     extern __shared__ int s_dyn[];
-    int *s_lpos = s_dyn;
-    float *s_lbias = reinterpret_cast<float *>(s_dyn + p.k_pad);
+    int *s_lpos = s_dyn;                                          // INT_MAX: empty slot
+    float *s_lbias = reinterpret_cast<float *>(s_dyn + p.k_pad);  // log2 units
+    int *s_lrow = s_dyn + 2 * p.k_pad;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
     const int logical = xcd_remap(blockIdx.x, p.grid_q);
     const int head = logical / p.n_qblk;
     if (head >= p.n_heads) return;
-    int seq, blk;
-    if (!find_block(p.cu, p.num_seqs, logical - head * p.n_qblk, kBM, lane, seq, blk)) return;
-    const int seq_start = p.cu[seq];
-    const int seq_len = p.cu[seq + 1] - seq_start;
-    const int i = blk * kBM + wave * 32 + ql;
+    int seq, blk, seq_start, seq_len;
+    if (!find_block(p.cu, p.num_seqs, p.n_qblk - 1 - (logical - head * p.n_qblk), kBM, lane, seq, blk, seq_start,
+                    seq_len))
+        return;
+    const int wq0 = blk * kBM + wave * 32;
+    const int i = wq0 + ql;
     const bool qvalid = i < seq_len;
     const int64_t tok_i = (int64_t)seq_start + i;
+    const int ghi = min(blk * kBM + kBM - 1, seq_len - 1);
 
+    // ---- tile staging (band tiles from the diagonal down, then landmark tiles) ---------
+    const uint32_t kst = (uint32_t)p.k_st * 2u, vst = (uint32_t)p.v_st * 2u;
+    const i32x4 krs = buffer_rsrc(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh, (uint32_t)seq_len * kst);
+    const i32x4 vrs = buffer_rsrc(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh, (uint32_t)seq_len * vst);
+    const TileLanes<D, kSwzRow> klanes(wave, lane, kst);
+    const TileLanes<D, kSwzRow> vlanes(wave, lane, vst);
+    const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
+    auto band_key0 = [&](int t) { return ghi - (BN - 1) - t * BN; };
+    auto issue_band = [&](int t) {
+        const int key0 = band_key0(t);
+        const uint32_t kl = tiles_lds + (t & (NSTAGE - 1)) * (2 * TB);
+        klanes.load_band(kl, wave, krs, (uint32_t)key0 * kst);  // wraps when key0 < 0
+        vlanes.load_band(kl + TB, wave, vrs, (uint32_t)key0 * vst);
+    };
+#pragma unroll
+    for (int t = 0; t < NSTAGE - 1; ++t) issue_band(t);
+
+    // ---- this lane's query: Q and dO as B operands, LSE, Delta, ranges ------------------
     vec8 qv[KS], dov[KS];
     {
         const uint16_t *qp = p.q + tok_i * p.q_st + (int64_t)head * p.q_sh + hh * 8;
@@ -213,15 +240,14 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     const float lsev = qvalid ? p.lse[tok_i * p.lse_st + (int64_t)head * p.lse_sh] : -INFINITY;
     const float lse2 = (lsev == -INFINITY) ? INFINITY : lsev * kLog2e;  // +inf: every P is 0
     const float delta = qvalid ? p.ws_delta[tok_i * p.n_heads + head] : 0.f;
-
     const float wc = qvalid ? p.w[tok_i * p.w_st] : 0.f;
     int lo, corelo, pmax;
     query_ranges<MODE>(i, wc, p.win_edge, lo, corelo, pmax);
-    const int wlo = wave_min(qvalid ? lo : INT_MAX);
-    const int whi = wave_max(qvalid ? i : -1);
-    const int wclo = wave_max(qvalid ? corelo : INT_MIN);
-    const int wchi = wave_min(qvalid ? i : INT_MAX);
-    const int wpmax = wave_max(qvalid ? pmax : -1);
+    const int wlo = wave_min_u(qvalid ? lo : INT_MAX);
+    const int wclo = wave_max_u(qvalid ? corelo : INT_MIN);
+    const int wpmax = wave_max_u(qvalid ? pmax : -1);
+    const int whi = min(wq0 + 31, seq_len - 1);
+    const int wchi = wq0;
 
     for (int s = tid; s < p.k_pad; s += 256) {
         int pos = INT_MAX;
@@ -235,61 +261,34 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
         }
         s_lpos[s] = pos;
         s_lbias[s] = b;
+        s_lrow[s] = pos == INT_MAX ? 0 : pos;
+        const int tmin = wave_min_u(pos);
+        if (lane == 0) s_ltmin[s >> 6] = tmin;
     }
     if (lane == 0) {
         s_red[wave][0] = wlo;
-        s_red[wave][1] = whi;
-        s_red[wave][2] = wpmax;
+        s_red[wave][1] = wpmax;
     }
     __syncthreads();
     const int glo = min(min(s_red[0][0], s_red[1][0]), min(s_red[2][0], s_red[3][0]));
-    const int ghi = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
-    const int gpmax = max(max(s_red[0][2], s_red[1][2]), max(s_red[2][2], s_red[3][2]));
-    if (wave == 0) {
-        int n = 0;
-        for (int lt = 0; lt < p.k_pad / BN; ++lt) {
-            if (wave_min(s_lpos[lt * BN + lane]) <= gpmax) {
-                if (lane == 0) s_ltile[n] = lt;
-                ++n;
-            }
-        }
-        if (lane == 0) s_nlt = n;
-    }
-    __syncthreads();
-    const int nb = (ghi >= glo) ? (ghi - glo) / BN + 1 : 0;
-    const int nt = nb + s_nlt;
-
-    uint4 kr[PER_T], vr[PER_T];
-    auto load_tile = [&](int t) {
-        const bool band = t < nb;
-        const int tb = glo + t * BN;
-        const int lt = band ? 0 : s_ltile[t - nb];
-#pragma unroll
-        for (int u = 0; u < PER_T; ++u) {
-            const int c = tid + u * 256;
-            const int row = c / CPR, col = c % CPR;
-            const int key = band ? tb + row : s_lpos[lt * BN + row];
-            const bool ok = band ? key < seq_len : key != INT_MAX;
-            uint4 kx = make_uint4(0, 0, 0, 0), vx = kx;
-            if (ok) {
-                const int64_t tok = (int64_t)seq_start + key;
-                kx = ld16(p.k + tok * p.k_st + (int64_t)head * p.k_sh + col * 8);
-                vx = ld16(p.v + tok * p.v_st + (int64_t)head * p.v_sh + col * 8);
-            }
-            kr[u] = kx;
-            vr[u] = vx;
-        }
+    const int gpmax = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
+    const int n_lt = p.k_pad / BN;
+    const uint64_t lmask = __ballot(lane < n_lt && s_ltmin[lane < n_lt ? lane : 0] <= gpmax);
+    const int nb = max((ghi - glo) / BN + 1, NSTAGE - 1);
+    const int nt = nb + __popcll(lmask);
+    auto lmk_tile = [&](int t) {
+        uint64_t m = lmask;
+        for (int j = nb; j < t; ++j) m &= m - 1;
+        return (int)__builtin_ctzll(m);
     };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int u = 0; u < PER_T; ++u) {
-            const int c = tid + u * 256;
-            const int row = c / CPR, col = c % CPR;
-            *reinterpret_cast<uint4 *>(&ks[buf][row][col * 8]) = kr[u];
-            *reinterpret_cast<uint4 *>(&vs[buf][row][col * 8]) = vr[u];
-            const uint16_t *e = reinterpret_cast<const uint16_t *>(&kr[u]);
-#pragma unroll
-            for (int x = 0; x < 8; ++x) kt[buf][col * 8 + x][row] = e[x];
+    auto issue_tile = [&](int t) {
+        if (t < nb) {
+            issue_band(t);
+        } else {
+            const int *lrow = s_lrow + lmk_tile(t) * BN;
+            const uint32_t kl = tiles_lds + (t & (NSTAGE - 1)) * (2 * TB);
+            klanes.load_gather(kl, wave, krs, kst, lrow);
+            vlanes.load_gather(kl + TB, wave, vrs, vst, lrow);
         }
     };
 
@@ -301,26 +300,44 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     float dw = 0.f;
     const float c = p.scale_log2;
 
-    if (nt > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
-    __syncthreads();
-    for (int t = 0; t < nt; ++t) {
-        const int buf = t & 1;
-        if (t + 1 < nt) load_tile(t + 1);
-        const bool band = t < nb;
-        const int tb = glo + t * BN;
-        int lt = 0;
-        bool active;
-        if (band) {
-            active = (tb <= whi) && (tb + BN - 1 >= wlo);
-        } else {
-            lt = s_ltile[t - nb];
-            active = wave_min(s_lpos[lt * BN + lane]) <= wpmax;
+    // dS = P (dP - Delta) from shifted logits x (log2 units incl. biases, -inf where not
+    // admitted), then dQ^T += K^T . dS^T with K of stage `stage` read transposed
+    auto ds_dq = [&](f32x16 (&x)[2], const f32x16 (&pacc)[2], int stage) {
+        uint32_t pk[2][8];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float p0 = fast_exp2(x[rb][2 * j] - lse2), p1 = fast_exp2(x[rb][2 * j + 1] - lse2);
+                pk[rb][j] = DT::pack2(p0 * (pacc[rb][2 * j] - delta), p1 * (pacc[rb][2 * j + 1] - delta));
+            }
+        const char *ktile = s_tiles[stage][0];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int rb = kk >> 1, g = kk & 1;
+            const vec8 b = bitcast<vec8>(
+                make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
+#pragma unroll
+            for (int d = 0; d < ND; ++d) {
+                const vec8 a = bitcast<vec8>(tile_read_tr<D, kSwzRow>(ktile, kk * 16, d * 32, lane));
+                dqacc[d] = DT::mfma(a, b, dqacc[d]);
+            }
         }
+    };
+
+    tile_barrier<LPT>();  // tiles 0 and 1 landed (tile 2 may be in flight)
+    for (int t = 0; t < nt; ++t) {
+        if (t + NSTAGE - 1 < nt) issue_tile(t + NSTAGE - 1);
+        const int stage = t & (NSTAGE - 1);
+        const bool band = t < nb;
+        const int tb = band ? band_key0(t) : 0;
+        const int lt = band ? 0 : lmk_tile(t);
+        const bool active = band ? ((tb <= whi) && (tb + BN - 1 >= wlo)) : (s_ltmin[lt] <= wpmax);
         if (active) {
+            // S^T = K . Q^T and dP^T = V . dO^T (64 keys x 32 queries)
             f32x16 sacc[2], pacc[2];
+            const char *ktile = s_tiles[stage][0];
+            const char *vtile = s_tiles[stage][1];
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
                 f32x16 a0, a1;
@@ -328,22 +345,23 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
                 for (int r = 0; r < 16; ++r) a0[r] = a1[r] = 0.f;
 #pragma unroll
                 for (int s = 0; s < KS; ++s) {
-                    const vec8 ka = bitcast<vec8>(ld16(&ks[buf][rb * 32 + ql][s * 16 + hh * 8]));
-                    const vec8 va = bitcast<vec8>(ld16(&vs[buf][rb * 32 + ql][s * 16 + hh * 8]));
+                    const vec8 ka = bitcast<vec8>(tile_read_row16<D>(ktile, rb * 32 + ql, 2 * s + hh));
+                    const vec8 va = bitcast<vec8>(tile_read_row16<D>(vtile, rb * 32 + ql, 2 * s + hh));
                     a0 = DT::mfma(ka, qv[s], a0);
                     a1 = DT::mfma(va, dov[s], a1);
                 }
                 sacc[rb] = a0;
                 pacc[rb] = a1;
             }
-            // dS (into sacc): P = exp2(logit2 - lse2) on admitted pairs, dS = P (dP - Delta)
             if (band) {
-                const int A = i - tb - hh * 4;
-                const int B = lo - tb - hh * 4;
+                // element (rb, r) is key tb + rb*32 + acc_row_const(r) + hh*4 =: tb + hh*4 + cst
+                const int A = i - tb - hh * 4;   // key <= i  <=> cst <= A
+                const int B = lo - tb - hh * 4;  // key >= lo <=> cst >= B
                 const bool need_lo = tb < wclo;
                 const bool need_hi = tb + BN - 1 > wchi;
                 if (MODE == kSoft && need_lo) {
                     const int Bc = corelo - tb - hh * 4;
+                    f32x16 x[2];
 #pragma unroll
                     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -353,26 +371,30 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
                             const float edge = soft_edge_log2(wc, (float)(A - cst), p.inv_tau, oms);
                             const bool ok = (cst <= A) & (cst >= B);
                             const bool is_edge = (cst < Bc) & ok;  // exp(-z) may overflow elsewhere
-                            const float x = fmaf(sacc[rb][r], c, is_edge ? edge : 0.f);
-                            const float pr = ok ? fast_exp2(x - lse2) : 0.f;
-                            const float ds = pr * (pacc[rb][r] - delta);
-                            dw += is_edge ? ds * oms : 0.f;
-                            sacc[rb][r] = ds;
+                            const float y = fmaf(sacc[rb][r], c, is_edge ? edge : 0.f);
+                            x[rb][r] = ok ? y : -INFINITY;
+                            const float pr = ok ? fast_exp2(y - lse2) : 0.f;
+                            dw += is_edge ? pr * (pacc[rb][r] - delta) * oms : 0.f;
                         }
-                } else {
-                    const int Bm = (need_lo) ? B : INT_MIN;
-                    const int Am = (need_hi) ? A : INT_MAX;
+                    ds_dq(x, pacc, stage);
+                } else if (need_lo | need_hi) {
+                    const uint32_t keep = rows_le(A) & ~rows_le(B - 1);
+                    f32x16 x[2];
 #pragma unroll
                     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int cst = rb * 32 + acc_row_const(r);
-                            const bool ok = (cst <= Am) & (cst >= Bm);
-                            const float pr = ok ? fast_exp2(fmaf(sacc[rb][r], c, -lse2)) : 0.f;
-                            sacc[rb][r] = pr * (pacc[rb][r] - delta);
-                        }
+                        for (int r = 0; r < 16; ++r) x[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r] * c);
+                    ds_dq(x, pacc, stage);
+                } else {
+                    f32x16 x[2];
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) x[rb][r] = sacc[rb][r] * c;
+                    ds_dq(x, pacc, stage);
                 }
             } else {
+                f32x16 x[2];
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -385,28 +407,15 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int r = g * 4 + e;
-                            const float pr =
-                                (pp[e] <= pmax) ? fast_exp2(fmaf(sacc[rb][r], c, bb[e] - lse2)) : 0.f;
-                            sacc[rb][r] = pr * (pacc[rb][r] - delta);
+                            x[rb][r] = (pp[e] <= pmax) ? fmaf(sacc[rb][r], c, bb[e]) : -INFINITY;
                         }
                     }
-            }
-            // dQ^T (D x 32 queries) += K^T . dS^T
-            uint32_t pk[2][8];
-            pack_block<DT>(sacc[0], pk[0]);
-            pack_block<DT>(sacc[1], pk[1]);
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const int rb = kk >> 1, g = kk & 1;
-                const vec8 b = bitcast<vec8>(
-                    make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
-#pragma unroll
-                for (int d = 0; d < ND; ++d)
-                    dqacc[d] = DT::mfma(ld_tr_operand<vec8>(&kt[buf][d * 32 + ql][kk * 16 + hh * 4]), b, dqacc[d]);
+                ds_dq(x, pacc, stage);
             }
         }
-        if (t + 1 < nt) store_tile(buf ^ 1);
-        __syncthreads();
+        // tile t+1 must have landed; tiles t+2 .. t+NSTAGE-1 may stay in flight
+        if (t + NSTAGE - 1 < nt) tile_barrier<(NSTAGE - 2) * LPT>();
+        else tile_barrier<0>();
     }
 
     if (qvalid) store_row<DT, ND>(p.dq, tok_i * p.dq_st + (int64_t)head * p.dq_sh, p.grad_f32, dqacc, p.scale, hh);
@@ -441,7 +450,7 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
     constexpr int KS = D / 16, ND = D / 32, CPR = D / 8, PER_T = QT * CPR / 256;
     __shared__ __align__(16) KvSmem<D> sm;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
 
     int head, seq, kblk = 0, gbase = 0, q_begin, q_end, slot = 0, sbw = 0, kw = 0, lcid = 0, lchunk = 0;
@@ -844,7 +853,7 @@ hipError_t launch_typed(const BwdParams &p, hipStream_t stream) {
         if (p.d_bias)
             hipLaunchKernelGGL(bwd_dbias_kernel, dim3(p.n_heads * p.num_seqs), dim3(64), 0, stream, p);
     }
-    const size_t dyn = (size_t)p.k_pad * (sizeof(int) + sizeof(float));
+    const size_t dyn = (size_t)p.k_pad * (2 * sizeof(int) + sizeof(float));
     hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE>), dim3(p.grid_q), dim3(256), dyn, stream, p);
     hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false>), dim3(p.grid_q), dim3(256), 0, stream, p);
     return hipGetLastError();

@@ -33,7 +33,6 @@ namespace dsalt {
 namespace {
 
 constexpr float kStaleMax = 8.0f;  // allowed growth of the row max before a rescale (log2)
-constexpr uint32_t kNegInfBits = 0xff800000u;
 
 struct FwdParams {
     const uint16_t *q, *k, *v;
@@ -51,22 +50,6 @@ struct FwdParams {
     float inv_c;      // 1 / c: log2-unit (or natural, times log2 e) bias -> raw units
     float inv_tau, win_edge;
 };
-
-// Bit (rb*16 + r) of a lane's 32-bit tile mask stands for accumulator element
-// sacc[rb][r], i.e. tile row rb*32 + acc_row_const(r) + hh*4. The row offset
-// rb*32 + acc_row_const(r) increases with the bit index, so the elements whose offset
-// is <= a form a prefix of the bits.
-__device__ __forceinline__ uint32_t rows_le(int a) {
-    const int n = min(max(4 * (a >> 3) + min((a & 7) + 1, 4), 0), 32);  // 0 for a < 0
-    return (uint32_t)((1ull << n) - 1ull);
-}
-
-// x if bit j of `mask` is set, else -inf. With j a compile-time constant this is
-// v_bfe_i32 + v_bfi_b32: no compare into a lane-mask SGPR (and no hazard wait after it).
-__device__ __forceinline__ float keep_if(uint32_t mask, int j, float x) {
-    const uint32_t m = (uint32_t)((int32_t)(mask << (31 - j)) >> 31);
-    return __uint_as_float((m & __float_as_uint(x)) | (~m & kNegInfBits));
-}
 
 template <typename DT, int D, int MODE>
 __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {

@@ -122,18 +122,38 @@ __device__ __forceinline__ uint4 tile_read_row16(const char *tile, int row, int 
 // ds_read_b64_tr_b16 gives lane l element l%4 of the 8-byte chunks addressed by lanes
 // 16*(l/16) + 4e + (l%16)/4, e = 0..3; each lane therefore addresses row
 // row0 + (l/32)*4 + ((l%16)/4) and the 4 columns col0 + 16*((l/16)%2) + 4*(l%4).
-template <int D>
+// The tile is conflict-free for this pattern with the kSwzTr swizzle; a kSwzRow tile
+// (read both ways) serves it with 2-way bank conflicts.
+template <int D, int SWZ = kSwzTr>
 __device__ __forceinline__ uint4 tile_read_tr(const char *tile, int row0, int col0, int lane) {
     const int row = row0 + ((lane >> 5) << 2) + ((lane >> 2) & 3);
     const int col = col0 + (((lane >> 4) & 1) << 4) + ((lane & 3) << 2);
     const int c = col >> 3, half = (col >> 2) & 1;
-    const char *a = tile + row * Tile64<D>::ROWB + ((c ^ tile_swz<kSwzTr>(row)) << 4) + (half << 3);
+    const char *a = tile + row * Tile64<D>::ROWB + ((c ^ tile_swz<SWZ>(row)) << 4) + (half << 3);
     const shortx4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) shortx4 *)a);
-    // row + 8 has the same swizzle ((row & 3) unchanged)
+    // row + 8 has the same swizzle (row & 7 and row & 3 unchanged)
     const shortx4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (__attribute__((address_space(3))) shortx4 *)(a + 8 * Tile64<D>::ROWB));
     const uint2 l2 = bitcast<uint2>(lo), h2 = bitcast<uint2>(hi);
     return make_uint4(l2.x, l2.y, h2.x, h2.y);
+}
+
+constexpr uint32_t kNegInfBits = 0xff800000u;
+
+// Bit (rb*16 + r) of a lane's 32-bit tile mask stands for accumulator element
+// sacc[rb][r], i.e. tile row rb*32 + acc_row_const(r) + hh*4. The row offset
+// rb*32 + acc_row_const(r) increases with the bit index, so the elements whose offset
+// is <= a form a prefix of the bits.
+__device__ __forceinline__ uint32_t rows_le(int a) {
+    const int n = min(max(4 * (a >> 3) + min((a & 7) + 1, 4), 0), 32);  // 0 for a < 0
+    return (uint32_t)((1ull << n) - 1ull);
+}
+
+// x if bit j of `mask` is set, else -inf. With j a compile-time constant this is
+// v_bfe_i32 + v_bfi_b32: no compare into a lane-mask SGPR (and no hazard wait after it).
+__device__ __forceinline__ float keep_if(uint32_t mask, int j, float x) {
+    const uint32_t m = (uint32_t)((int32_t)(mask << (31 - j)) >> 31);
+    return __uint_as_float((m & __float_as_uint(x)) | (~m & kNegInfBits));
 }
 
 }  // namespace dsalt
