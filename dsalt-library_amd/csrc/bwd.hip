@@ -41,6 +41,22 @@ constexpr int kBM = 128;  // queries (dq) / keys (kv) per workgroup; prep block 
 constexpr int kTN = 64;   // keys per tile (dq) / queries per tile (kv, lmk_kv)
 constexpr int kLC = 512;  // queries per lmk_kv chunk (chunks are numbered like query blocks)
 
+// Per-(head, query) record written by prep and streamed by kv next to the Q / dO tiles,
+// field-major ([H][field][T]) so that one 64-query tile of a field is one 256-byte
+// direct load. Integer fields are encoded so that an all-zero record (what an
+// out-of-range load returns) admits no key: lo and corelo as INT_MAX - x, pmax as x + 1.
+enum {
+    kRecLse2 = 0,    // LSE * log2(e), +inf for empty rows (float)
+    kRecDelta = 1,   // rowsum(O * dO) (float)
+    kRecLo = 2,      // INT_MAX - first band key
+    kRecClo = 3,     // INT_MAX - first zero-bias band key (SOFT core start)
+    kRecPmax = 4,    // largest admissible landmark position + 1
+    kRecWc = 5,      // window w~ (float)
+    kRecGLo = 6,     // INT_MAX - min lo over the query's 32-query group
+    kRecGClo = 7,    // INT_MAX - max corelo over the query's 32-query group
+    kRecFields = 8
+};
+
 struct BwdParams {
     const uint16_t *q, *k, *v, *dout;
     const void *o;  // forward output: fp32 if o_f32, else the compute dtype
@@ -50,7 +66,7 @@ struct BwdParams {
     const int32_t *cu;
     void *dq, *dk, *dv;  // gradient outputs: fp32 if grad_f32, else the compute dtype
     float *d_bias, *d_w;
-    float *ws_delta;         // [T*H]
+    float *ws_qrec;          // per-query records [H][kRecFields][T] (see bwd_prep_kernel)
     int *ws_minlo;           // [n_qblk]
     float *ws_dwh;           // [T*H] or null
     float *ws_ldk, *ws_ldv;  // landmark dK/dV partials [H][n_lchunk][k_pad][D] or null
@@ -104,8 +120,9 @@ __device__ __forceinline__ void pack_block(const f32x16 &x, uint32_t (&pk)[8]) {
 }
 
 // ==================================================================================
-// prep: Delta = rowsum(O * dO), one workgroup per (128-token block, head), two threads
-// per token; the head-0 workgroup of a block also records the block's smallest band start
+// prep: one workgroup per (128-token block, head), two threads per token: Delta =
+// rowsum(O * dO) and the token's per-query record; the head-0 workgroup of a block also
+// records the block's smallest band start
 // ==================================================================================
 template <typename DT, int D, int MODE>
 __global__ void __launch_bounds__(256) bwd_prep_kernel(const BwdParams p) {
@@ -148,17 +165,33 @@ __global__ void __launch_bounds__(256) bwd_prep_kernel(const BwdParams p) {
         }
     }
     acc += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc), 0xB1, 0xF, 0xF, false));  // + partner
-    if (valid && half == 0) p.ws_delta[tok * p.n_heads + head] = acc;
+
+    // ranges of this token (both threads of a token compute them; wave w holds the
+    // 32-token group w of the block)
+    int lo = INT_MAX, corelo = INT_MAX, pmax = -1;
+    float wv = 0.f;
+    if (valid) {
+        wv = p.w[tok * p.w_st];
+        query_ranges<MODE>(base + t, wv, p.win_edge, lo, corelo, pmax);
+    }
+    const int glo = wave_min_u(lo);
+    const int gclo = wave_max_u(valid ? corelo : INT_MIN);
+    if (valid && half == 0) {
+        const float lv = p.lse[tok * p.lse_st + (int64_t)head * p.lse_sh];
+        float *rec = p.ws_qrec + (size_t)head * kRecFields * p.total_len + tok;
+        const size_t T = (size_t)p.total_len;
+        rec[kRecLse2 * T] = (lv == -INFINITY) ? INFINITY : lv * kLog2e;
+        rec[kRecDelta * T] = acc;
+        reinterpret_cast<int *>(rec)[kRecLo * T] = INT_MAX - lo;
+        reinterpret_cast<int *>(rec)[kRecClo * T] = INT_MAX - corelo;
+        reinterpret_cast<int *>(rec)[kRecPmax * T] = pmax + 1;
+        rec[kRecWc * T] = wv;
+        reinterpret_cast<int *>(rec)[kRecGLo * T] = INT_MAX - glo;
+        reinterpret_cast<int *>(rec)[kRecGClo * T] = INT_MAX - gclo;
+    }
 
     if (head == 0) {  // smallest band start of the block
-        int lo = INT_MAX;
-        if (tid < kBM && base + tid < seq_len) {
-            const int i = base + tid;
-            int corelo, pmax;
-            query_ranges<MODE>(i, p.w[((int64_t)seq_start + i) * p.w_st], p.win_edge, lo, corelo, pmax);
-        }
-        lo = wave_min_u(lo);
-        if (lane == 0) s_min[wave] = lo;
+        if (lane == 0) s_min[wave] = glo;
         __syncthreads();
         if (tid == 0) p.ws_minlo[bidx] = min(min(s_min[0], s_min[1]), min(s_min[2], s_min[3]));
     }
@@ -239,7 +272,7 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     }
     const float lsev = qvalid ? p.lse[tok_i * p.lse_st + (int64_t)head * p.lse_sh] : -INFINITY;
     const float lse2 = (lsev == -INFINITY) ? INFINITY : lsev * kLog2e;  // +inf: every P is 0
-    const float delta = qvalid ? p.ws_delta[tok_i * p.n_heads + head] : 0.f;
+    const float delta = qvalid ? p.ws_qrec[((size_t)head * kRecFields + kRecDelta) * p.total_len + tok_i] : 0.f;
     const float wc = qvalid ? p.w[tok_i * p.w_st] : 0.f;
     int lo, corelo, pmax;
     query_ranges<MODE>(i, wc, p.win_edge, lo, corelo, pmax);
@@ -428,40 +461,39 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
 // ==================================================================================
 // kv (LMK = false): key-parallel band dK/dV;  lmk_kv (LMK = true): landmark dK/dV + d_bias
 // ==================================================================================
-template <int D>
-struct KvSmem {
-    uint16_t qs[2][kTN][D + kPad8];
-    uint16_t qt[2][D][kTN + kPad4];
-    uint16_t dos[2][kTN][D + kPad8];
-    uint16_t dot[2][D][kTN + kPad4];
-    float lse2[2][kTN];
-    float del[2][kTN];
-    int lo[2][kTN];   // band start (LMK: largest admissible landmark position)
-    int clo[2][kTN];  // SOFT: core start
-    float wc[2][kTN];
-    int sb[2][2][4];  // per buffer and 32-query sub-block: min lo, max lo, max corelo, max pmax
-    int misc[8];
-};
-
+// A wave owns 32 keys (band: consecutive keys; LMK: 32 landmark slots) held in registers
+// as B operands, and streams 64-query tiles of Q, dO and the per-query records through a
+// 4-stage LDS ring (direct global->LDS loads, one barrier per tile). Per 32-query
+// sub-block: S = Q.K^T and dP = dO.V^T (lane = key column, registers = query rows),
+// P = 2^(S c + bias - lse2) on admitted pairs, dS = P (dP - Delta), then dV^T += dO^T.P
+// and dK^T += Q^T.dS with Q and dO read transposed.
 template <typename DT, int D, int MODE, bool LMK>
 __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
     typedef typename DT::vec8 vec8;
-    constexpr int QT = kTN;
-    constexpr int KS = D / 16, ND = D / 32, CPR = D / 8, PER_T = QT * CPR / 256;
-    __shared__ __align__(16) KvSmem<D> sm;
+    constexpr int QT = kTN;  // queries per tile
+    constexpr int KS = D / 16, ND = D / 32;
+    constexpr int TB = Tile64<D>::BYTES;
+    constexpr int NSTAGE = 4;
+    constexpr int RB = QT * 4;                                   // bytes of one record field per tile
+    constexpr int LPT = 2 * Tile64<D>::LOADS_PER_WAVE + 2;       // Q, dO, and 2 record fields per wave
+    static_assert(kRecFields == 8, "4 waves x 2 fields");
+
+    __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][Q, dO], row-swizzled
+    __shared__ __align__(16) char s_rec[NSTAGE][kRecFields][RB];
+    __shared__ int s_misc[8];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
 
-    int head, seq, kblk = 0, gbase = 0, q_begin, q_end, slot = 0, sbw = 0, kw = 0, lcid = 0, lchunk = 0;
+    int head, seq, seq_start, seq_len, kblk = 0, gbase = 0, q_begin, q_end, slot = 0, sbw = 0, kw = 0, lcid = 0;
     int key = INT_MAX;  // this lane's key position in the sequence (INT_MAX: none)
     float kbias2 = 0.f;
     if (!LMK) {
         const int logical = xcd_remap(blockIdx.x, p.grid_q);
         head = logical / p.n_qblk;
         if (head >= p.n_heads) return;
-        const int target = logical - head * p.n_qblk;
-        if (!find_block(p.cu, p.num_seqs, target, kBM, lane, seq, kblk)) return;
+        const int target = p.n_qblk - 1 - (logical - head * p.n_qblk);
+        if (!find_block(p.cu, p.num_seqs, target, kBM, lane, seq, kblk, seq_start, seq_len)) return;
         gbase = target - kblk;
     } else {
         // workgroup = (head, 64-slot group, query chunk); chunk ids follow find_block
@@ -470,12 +502,13 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
         const int rem = blockIdx.x - head * per_head;
         const int gp = rem / p.n_lchunk;
         lcid = rem - gp * p.n_lchunk;
-        if (!find_block(p.cu, p.num_seqs, lcid, kLC, lane, seq, lchunk)) return;
+        int lchunk;
+        if (!find_block(p.cu, p.num_seqs, lcid, kLC, lane, seq, lchunk, seq_start, seq_len)) return;
         sbw = wave & 1;
         slot = gp * 64 + (wave >> 1) * 32 + ql;
+        q_begin = lchunk * kLC;  // refined below
+        q_end = min(seq_len, (lchunk + 1) * kLC);
     }
-    const int seq_start = p.cu[seq];
-    const int seq_len = p.cu[seq + 1] - seq_start;
 
     if (!LMK) {
         const int kb = kblk * kBM;
@@ -486,10 +519,10 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
         int last = kblk;
         for (int b = kblk + 1 + tid; b < nbs; b += 256)
             if (p.ws_minlo[gbase + b] <= kb + kBM - 1) last = max(last, b);
-        last = wave_max(last);
-        if (lane == 0) sm.misc[wave] = last;
+        last = wave_max_u(last);
+        if (lane == 0) s_misc[wave] = last;
         __syncthreads();
-        last = max(max(sm.misc[0], sm.misc[1]), max(sm.misc[2], sm.misc[3]));
+        last = max(max(s_misc[0], s_misc[1]), max(s_misc[2], s_misc[3]));
         q_begin = kb;
         q_end = min(seq_len, (last + 1) * kBM);
     } else {
@@ -500,17 +533,18 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
                 if (p.lmk_bias) kbias2 = p.lmk_bias[head * p.lb_sh + seq * p.lb_ss + slot * p.lb_sk] * kLog2e;
             }
         }
-        // queries admitting a landmark p satisfy q >= p
-        const int mn = wave_min(key);
-        if (lane == 0) sm.misc[wave] = mn;
+        // queries admitting a landmark p satisfy q > p: start at the first 64-query tile
+        // of the chunk that holds a query after the smallest position
+        const int mn = wave_min_u(key);
+        if (lane == 0) s_misc[wave] = mn;
         __syncthreads();
-        const int gmin = min(min(sm.misc[0], sm.misc[1]), min(sm.misc[2], sm.misc[3]));
-        q_end = min(seq_len, (lchunk + 1) * kLC);
-        q_begin = (gmin == INT_MAX) ? q_end : min(max(gmin, lchunk * kLC), q_end);
+        const int gmin = min(min(s_misc[0], s_misc[1]), min(s_misc[2], s_misc[3]));
+        if (gmin == INT_MAX || gmin >= q_end) q_begin = q_end;
+        else if (gmin > q_begin) q_begin += (gmin - q_begin) / QT * QT;
     }
     const bool kvalid = key != INT_MAX;
-    const int wkmin = LMK ? wave_min(key) : kw;
-    const int wkmax = LMK ? wave_max(kvalid ? key : -1) : min(kw + 31, seq_len - 1);
+    const int wkmin = LMK ? wave_min_u(key) : kw;
+    const int wkmax = LMK ? wave_max_u(kvalid ? key : -1) : min(kw + 31, seq_len - 1);
 
     // this lane's key row as the B operand of S = Q K^T and dP = dO V^T
     vec8 kreg[KS], vreg[KS];
@@ -528,82 +562,38 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
         }
     }
 
+    // ---- tile staging: Q, dO and 8 record fields of 64 queries per tile ----------------
+    const uint32_t qst = (uint32_t)p.q_st * 2u, dst = (uint32_t)p.do_st * 2u;
+    const i32x4 qrs = buffer_rsrc(p.q + (int64_t)seq_start * p.q_st + (int64_t)head * p.q_sh, (uint32_t)seq_len * qst);
+    const i32x4 drs = buffer_rsrc(p.dout + (int64_t)seq_start * p.do_st + (int64_t)head * p.do_sh,
+                                  (uint32_t)seq_len * dst);
+    // records of this head: field f of query q at byte (f * T + seq_start + q) * 4; queries
+    // at or past seq_len get an out-of-range offset (zeros: admit nothing)
+    const i32x4 rrs = buffer_rsrc(p.ws_qrec + (size_t)head * kRecFields * p.total_len,
+                                  (uint32_t)(kRecFields * p.total_len * 4));
+    const TileLanes<D, kSwzRow> qlanes(wave, lane, qst);
+    const TileLanes<D, kSwzRow> dlanes(wave, lane, dst);
+    const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
+    const uint32_t rec_lds = lds_addr(&s_rec[0][0][0]);
     const int ntile = (q_end > q_begin) ? (q_end - q_begin + QT - 1) / QT : 0;
-    uint4 qr[PER_T], dr[PER_T];
-    float pl = INFINITY, pd = 0.f, pw = 0.f;
-    int plo = INT_MAX, pclo = INT_MAX, ppm = -1;
-    auto load_tile = [&](int t) {
+    auto issue_tile = [&](int t) {
         const int q0 = q_begin + t * QT;
+        const int st = t & (NSTAGE - 1);
+        const uint32_t tl = tiles_lds + st * (2 * TB);
+        qlanes.load_band(tl, wave, qrs, (uint32_t)q0 * qst);
+        dlanes.load_band(tl + TB, wave, drs, (uint32_t)q0 * dst);
+        const int q = q0 + lane;
 #pragma unroll
-        for (int u = 0; u < PER_T; ++u) {
-            const int c = tid + u * 256;
-            const int row = c / CPR, col = c % CPR;
-            const int q = q0 + row;
-            uint4 a = make_uint4(0, 0, 0, 0), b = a;
-            if (q < q_end) {  // queries past q_end belong to another workgroup
-                const int64_t tok = (int64_t)seq_start + q;
-                a = ld16(p.q + tok * p.q_st + (int64_t)head * p.q_sh + col * 8);
-                b = ld16(p.dout + tok * p.do_st + (int64_t)head * p.do_sh + col * 8);
-            }
-            qr[u] = a;
-            dr[u] = b;
-        }
-        if (tid < QT) {
-            const int q = q0 + tid;
-            pl = INFINITY;
-            pd = 0.f;
-            pw = 0.f;
-            plo = INT_MAX;
-            pclo = INT_MAX;
-            ppm = -1;
-            if (q < q_end) {  // queries past q_end belong to another workgroup
-                const int64_t tok = (int64_t)seq_start + q;
-                const float lv = p.lse[tok * p.lse_st + (int64_t)head * p.lse_sh];
-                pl = (lv == -INFINITY) ? INFINITY : lv * kLog2e;
-                pd = p.ws_delta[tok * p.n_heads + head];
-                pw = p.w[tok * p.w_st];
-                query_ranges<MODE>(q, pw, p.win_edge, plo, pclo, ppm);
-            }
+        for (int u = 0; u < 2; ++u) {
+            const int f = wave * 2 + u;
+            const uint32_t off = (q < seq_len) ? (uint32_t)(((size_t)f * p.total_len + seq_start + q) * 4) : 0xFFFFFF00u;
+            asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(off), "s"(rrs),
+                         "{m0}"(__builtin_amdgcn_readfirstlane(rec_lds + (st * kRecFields + f) * RB))
+                         : "memory");
         }
     };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int u = 0; u < PER_T; ++u) {
-            const int c = tid + u * 256;
-            const int row = c / CPR, col = c % CPR;
-            *reinterpret_cast<uint4 *>(&sm.qs[buf][row][col * 8]) = qr[u];
-            *reinterpret_cast<uint4 *>(&sm.dos[buf][row][col * 8]) = dr[u];
-            const uint16_t *e = reinterpret_cast<const uint16_t *>(&qr[u]);
-            const uint16_t *f = reinterpret_cast<const uint16_t *>(&dr[u]);
-#pragma unroll
-            for (int x = 0; x < 8; ++x) {
-                sm.qt[buf][col * 8 + x][row] = e[x];
-                sm.dot[buf][col * 8 + x][row] = f[x];
-            }
-        }
-        if (tid < QT) {  // wave 0: per-query parameters and per-sub-block summaries
-            sm.lse2[buf][tid] = pl;
-            sm.del[buf][tid] = pd;
-            sm.lo[buf][tid] = LMK ? ppm : plo;
-            sm.clo[buf][tid] = pclo;
-            sm.wc[buf][tid] = pw;
-            const bool v = plo != INT_MAX;
-            int mnlo = v ? plo : INT_MAX, mxlo = v ? plo : INT_MIN, mxclo = v ? pclo : INT_MIN, mxpm = ppm;
-#pragma unroll
-            for (int o = 16; o > 0; o >>= 1) {  // within each 32-lane half
-                mnlo = min(mnlo, __shfl_xor(mnlo, o));
-                mxlo = max(mxlo, __shfl_xor(mxlo, o));
-                mxclo = max(mxclo, __shfl_xor(mxclo, o));
-                mxpm = max(mxpm, __shfl_xor(mxpm, o));
-            }
-            if ((tid & 31) == 0) {
-                sm.sb[buf][tid >> 5][0] = mnlo;
-                sm.sb[buf][tid >> 5][1] = mxlo;
-                sm.sb[buf][tid >> 5][2] = mxclo;
-                sm.sb[buf][tid >> 5][3] = mxpm;
-            }
-        }
-    };
+    auto rec_i = [&](int st, int f, int q) -> const int * { return reinterpret_cast<const int *>(&s_rec[st][f][q * 4]); };
+    auto rec_f = [&](int st, int f, int q) -> const float * { return reinterpret_cast<const float *>(&s_rec[st][f][q * 4]); };
 
     f32x16 dk[ND], dv[ND];
 #pragma unroll
@@ -612,22 +602,29 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
         for (int r = 0; r < 16; ++r) dk[d][r] = dv[d][r] = 0.f;
     float dbias = 0.f;
     const float c = p.scale_log2;
+    const int nkey = INT_MAX - (kvalid ? key : INT_MAX / 2);  // lo(q) <= key <=> rec lo >= nkey
 
-    if (ntile > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
-    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NSTAGE - 1; ++t)
+        if (t < ntile) issue_tile(t);
+    if (ntile >= NSTAGE - 1) tile_barrier<(NSTAGE - 2) * LPT>();
+    else tile_barrier<0>();
+
     for (int t = 0; t < ntile; ++t) {
-        const int buf = t & 1;
-        if (t + 1 < ntile) load_tile(t + 1);
+        if (t + NSTAGE - 1 < ntile) issue_tile(t + NSTAGE - 1);
+        const int st = t & (NSTAGE - 1);
+        const char *qtile = s_tiles[st][0];
+        const char *dtile = s_tiles[st][1];
 #pragma unroll
         for (int sbi = 0; sbi < (LMK ? 1 : 2); ++sbi) {
             const int sb = LMK ? sbw : sbi;
             const int qsb = q_begin + t * QT + sb * 32;  // first query of the sub-block
+            // group summaries of the sub-block (wave-uniform LDS reads)
+            const int gmin_lo = INT_MAX - *rec_i(st, kRecGLo, sb * 32);
+            const int gmax_clo = INT_MAX - *rec_i(st, kRecGClo, sb * 32);
             bool skip = qsb >= q_end;
-            if (!LMK) skip = skip || (qsb + 31 < kw) || (sm.sb[buf][sb][0] > wkmax);
-            else skip = skip || (sm.sb[buf][sb][3] < wkmin);
+            if (!LMK) skip = skip || (qsb + 31 < kw) || (gmin_lo > wkmax);
+            else skip = skip || (gmax_clo <= wkmin);  // pmax < corelo
             if (skip) continue;
 
             // S and dP (32 queries x 32 keys): lane = key column, registers = query rows
@@ -636,60 +633,63 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
             for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
-                const vec8 qa = bitcast<vec8>(ld16(&sm.qs[buf][sb * 32 + ql][s * 16 + hh * 8]));
-                const vec8 da = bitcast<vec8>(ld16(&sm.dos[buf][sb * 32 + ql][s * 16 + hh * 8]));
+                const vec8 qa = bitcast<vec8>(tile_read_row16<D>(qtile, sb * 32 + ql, 2 * s + hh));
+                const vec8 da = bitcast<vec8>(tile_read_row16<D>(dtile, sb * 32 + ql, 2 * s + hh));
                 sacc = DT::mfma(qa, kreg[s], sacc);
                 pacc = DT::mfma(da, vreg[s], pacc);
             }
             // register r holds query q = qsb + hh*4 + acc_row_const(r) of the lane's key
             const int Cj = (kvalid ? key : INT_MAX / 2) - qsb - hh * 4;  // q >= key <=> cst >= Cj
             const bool need_hi = LMK || (qsb < wkmax);
-            const bool need_lo = LMK || (sm.sb[buf][sb][1] > wkmin);
-            const bool need_edge = (MODE == kSoft) && !LMK && (sm.sb[buf][sb][2] > wkmin);
+            const bool need_lo = LMK || (gmax_clo > wkmin);
+            const bool need_edge = (MODE == kSoft) && !LMK && need_lo;
+            uint32_t pkp[8], pks[8];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int qi = sb * 32 + g * 8 + hh * 4;
-                const float4 l4 = *reinterpret_cast<const float4 *>(&sm.lse2[buf][qi]);
-                const float4 d4 = *reinterpret_cast<const float4 *>(&sm.del[buf][qi]);
-                const int4 o4 = *reinterpret_cast<const int4 *>(&sm.lo[buf][qi]);
+                const float4 l4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecLse2, qi));
+                const float4 d4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecDelta, qi));
+                const int4 o4 = *reinterpret_cast<const int4 *>(rec_i(st, LMK ? kRecPmax : kRecLo, qi));
                 const float la[4] = {l4.x, l4.y, l4.z, l4.w};
                 const float da[4] = {d4.x, d4.y, d4.z, d4.w};
                 const int oa[4] = {o4.x, o4.y, o4.z, o4.w};
-                int ca[4] = {INT_MAX, INT_MAX, INT_MAX, INT_MAX};
+                int ca[4] = {0, 0, 0, 0};
                 float wa[4] = {0.f, 0.f, 0.f, 0.f};
                 if (need_edge) {
-                    const int4 c4 = *reinterpret_cast<const int4 *>(&sm.clo[buf][qi]);
-                    const float4 w4 = *reinterpret_cast<const float4 *>(&sm.wc[buf][qi]);
+                    const int4 c4 = *reinterpret_cast<const int4 *>(rec_i(st, kRecClo, qi));
+                    const float4 w4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecWc, qi));
                     ca[0] = c4.x; ca[1] = c4.y; ca[2] = c4.z; ca[3] = c4.w;
                     wa[0] = w4.x; wa[1] = w4.y; wa[2] = w4.z; wa[3] = w4.w;
                 }
+                float pr4[4], ds4[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int r = g * 4 + e;
                     const int cst = acc_row_const(r);
                     float pr;
                     if (LMK) {
-                        // landmark admitted: key <= pmax(q) (key = INT_MAX when the slot is empty)
-                        pr = (key <= oa[e]) ? fast_exp2(fmaf(sacc[r], c, kbias2 - la[e])) : 0.f;
+                        // landmark admitted: key <= pmax(q) <=> key < rec pmax (key = INT_MAX when empty)
+                        pr = (key < oa[e]) ? fast_exp2(fmaf(sacc[r], c, kbias2 - la[e])) : 0.f;
                     } else {
-                        const bool ok = (!need_hi | (cst >= Cj)) & (!need_lo | (oa[e] <= key)) & kvalid;
+                        const bool ok = (!need_hi | (cst >= Cj)) & (!need_lo | (oa[e] >= nkey)) & kvalid;
                         float x = fmaf(sacc[r], c, -la[e]);
                         if (MODE == kSoft && need_edge) {
                             float oms;
                             const float edge = soft_edge_log2(wa[e], (float)(cst - Cj), p.inv_tau, oms);
-                            x += (key < ca[e]) ? edge : 0.f;
+                            x += (nkey > ca[e]) ? edge : 0.f;  // key < corelo(q)
                         }
                         pr = ok ? fast_exp2(x) : 0.f;
                     }
                     const float ds = pr * (pacc[r] - da[e]);
                     if (LMK) dbias += ds;
-                    sacc[r] = pr;
-                    pacc[r] = ds;
+                    pr4[e] = pr;
+                    ds4[e] = ds;
                 }
+                pkp[g * 2] = DT::pack2(pr4[0], pr4[1]);
+                pkp[g * 2 + 1] = DT::pack2(pr4[2], pr4[3]);
+                pks[g * 2] = DT::pack2(ds4[0], ds4[1]);
+                pks[g * 2 + 1] = DT::pack2(ds4[2], ds4[3]);
             }
-            uint32_t pkp[8], pks[8];
-            pack_block<DT>(sacc, pkp);
-            pack_block<DT>(pacc, pks);
             // dV^T += dO^T . P ; dK^T += Q^T . dS   (k-steps over the 32 queries)
 #pragma unroll
             for (int g = 0; g < 2; ++g) {
@@ -697,14 +697,14 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
                 const vec8 bs = bitcast<vec8>(make_uint4(pks[g * 4], pks[g * 4 + 1], pks[g * 4 + 2], pks[g * 4 + 3]));
 #pragma unroll
                 for (int d = 0; d < ND; ++d) {
-                    const int col = sb * 32 + g * 16 + hh * 4;
-                    dv[d] = DT::mfma(ld_tr_operand<vec8>(&sm.dot[buf][d * 32 + ql][col]), bp, dv[d]);
-                    dk[d] = DT::mfma(ld_tr_operand<vec8>(&sm.qt[buf][d * 32 + ql][col]), bs, dk[d]);
+                    dv[d] = DT::mfma(bitcast<vec8>(tile_read_tr<D, kSwzRow>(dtile, sb * 32 + g * 16, d * 32, lane)), bp, dv[d]);
+                    dk[d] = DT::mfma(bitcast<vec8>(tile_read_tr<D, kSwzRow>(qtile, sb * 32 + g * 16, d * 32, lane)), bs, dk[d]);
                 }
             }
         }
-        if (t + 1 < ntile) store_tile(buf ^ 1);
-        __syncthreads();
+        // tile t+1 must have landed; tiles t+2 .. t+NSTAGE-1 may stay in flight
+        if (t + NSTAGE - 1 < ntile) tile_barrier<(NSTAGE - 2) * LPT>();
+        else tile_barrier<0>();
     }
 
     if (!LMK) {
@@ -760,10 +760,11 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
             }
         }
     } else {
-        // combine the two query sub-blocks of each slot group (waves 2g+1 into 2g), fixed order
-        float *red = reinterpret_cast<float *>(&sm.qs[0][0][0]);
+        // combine the two query sub-blocks of each slot group (waves 2g+1 into 2g), fixed
+        // order, through LDS (the tile ring is idle after the last barrier)
+        float *red = reinterpret_cast<float *>(&s_tiles[0][0][0]);
         constexpr int PER_LANE = 2 * ND * 16 + 1;
-        static_assert(2 * 64 * PER_LANE * 4 <= sizeof(sm.qs) + sizeof(sm.qt), "reduction scratch");
+        static_assert(2 * 64 * PER_LANE * 4 <= sizeof(s_tiles), "reduction scratch");
         const int g = wave >> 1;
         float *mine = red + (size_t)(g * 64 + lane) * PER_LANE;
         if (sbw == 1) {
@@ -819,15 +820,15 @@ __global__ void __launch_bounds__(64) bwd_dbias_kernel(const BwdParams p) {
 }
 
 struct WsLayout {
-    size_t delta, minlo, dwh, ldk, ldv, ldb, total;
+    size_t qrec, minlo, dwh, ldk, ldv, ldb, total;
 };
 
 WsLayout ws_layout(int T, int S, int H, int D, int k) {
     auto al = [](size_t x) { return (x + 255) / 256 * 256; };
     WsLayout L;
     size_t off = 0;
-    L.delta = off;
-    off += al((size_t)T * H * 4);
+    L.qrec = off;
+    off += al((size_t)H * kRecFields * T * 4);
     L.minlo = off;
     off += al((size_t)block_upper_bound(T, S, kBM) * 4);
     L.dwh = off;
@@ -898,7 +899,7 @@ hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream) {
     p.grad_f32 = a.grad_dtype == DSALT_DTYPE_F32;
     p.d_bias = a.d_lmk_bias;
     p.d_w = (a.mode == DSALT_MODE_SOFT) ? a.d_w : nullptr;
-    p.ws_delta = reinterpret_cast<float *>(ws + L.delta);
+    p.ws_qrec = reinterpret_cast<float *>(ws + L.qrec);
     p.ws_minlo = reinterpret_cast<int *>(ws + L.minlo);
     p.ws_dwh = p.d_w ? reinterpret_cast<float *>(ws + L.dwh) : nullptr;
     p.ws_ldk = a.k_lmk > 0 ? reinterpret_cast<float *>(ws + L.ldk) : nullptr;
