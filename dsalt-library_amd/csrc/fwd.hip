@@ -110,26 +110,69 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
         klanes.load_band(kl, wave, krs, (uint32_t)key0 * kst);  // wraps when key0 < 0
         vlanes.load_band(kl + TB, wave, vrs, (uint32_t)key0 * vst);
     };
-#pragma unroll
-    for (int t = 0; t < NSTAGE - 1; ++t) issue_band(t);
-
-    // ---- Q (B operand: query column ql, head-dim chunk hh*8 of every 16) ---------------
+    // ---- global loads of the setup, issued before the first tile loads: loads complete
+    // in issue order, so waiting for these does not wait for the tiles ----------------
+    // Invalid lanes load a clamped valid row (their results are never stored), so no
+    // load sits in a divergent branch (which would make the compiler wait on it early).
     vec8 qv[KS];
     {
-        const uint16_t *qp = p.q + tok_i * p.q_st + (int64_t)head * p.q_sh + hh * 8;
+        const int64_t tq = qvalid ? tok_i : (int64_t)seq_start + seq_len - 1;
+        const uint16_t *qp = p.q + tq * p.q_st + (int64_t)head * p.q_sh + hh * 8;
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            uint4 raw = make_uint4(0, 0, 0, 0);
-            if (qvalid) raw = *reinterpret_cast<const uint4 *>(qp + s * 16);
-            raw.x ^= p.q_sign; raw.y ^= p.q_sign; raw.z ^= p.q_sign; raw.w ^= p.q_sign;
-            qv[s] = bitcast<vec8>(raw);
+        for (int s = 0; s < KS; ++s) qv[s] = bitcast<vec8>(*reinterpret_cast<const uint4 *>(qp + s * 16));
+    }
+    const float wraw = p.w[(qvalid ? tok_i : (int64_t)seq_start + seq_len - 1) * p.w_st];
+    // landmark slots s = tid + 256 j (k_pad <= DSALT_MAX_K_LMK = 4 * 256)
+    constexpr int LMK_PER_THREAD = DSALT_MAX_K_LMK / 256;
+    int64_t lpp[LMK_PER_THREAD];
+    float lbb[LMK_PER_THREAD];
+#pragma unroll
+    for (int j = 0; j < LMK_PER_THREAD; ++j) {
+        lpp[j] = -1;
+        lbb[j] = 0.f;
+        if (256 * j < p.k_lmk) {  // wave-uniform
+            const int s = min(tid + 256 * j, p.k_lmk - 1);
+            lpp[j] = p.lmk_pos[head * p.lp_sh + seq * p.lp_ss + s * p.lp_sk];
+            if (p.lmk_bias) lbb[j] = p.lmk_bias[head * p.lb_sh + seq * p.lb_ss + s * p.lb_sk];
         }
+    }
+    // the first NSTAGE-1 band tiles through the compiler builtin, so that the waits for
+    // the loads above count them (in-loop refills use inline asm, see tiles.h); rows
+    // below the sequence start are clamped to row 0
+    {
+        const char *kb = reinterpret_cast<const char *>(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh);
+        const char *vb = reinterpret_cast<const char *>(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh);
+#pragma unroll
+        for (int t = 0; t < NSTAGE - 1; ++t) {
+            const int key0 = band_key0(t);
+            char *kt = s_tiles[t][0];
+            char *vt = s_tiles[t][1];
+#pragma unroll
+            for (int u = 0; u < Tile64<D>::LOADS_PER_WAVE; ++u) {
+                const int slot0 = (wave * Tile64<D>::LOADS_PER_WAVE + u) * 64;
+                const int64_t key = max(key0 + klanes.row[u], 0);
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void *)(kb + key * kst + klanes.chunk_off[u]),
+                    (__attribute__((address_space(3))) void *)(kt + slot0 * 16), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void *)(vb + key * vst + vlanes.chunk_off[u]),
+                    (__attribute__((address_space(3))) void *)(vt + slot0 * 16), 16, 0, 0);
+            }
+        }
+    }
+
+    // ---- Q (B operand: query column ql, head-dim chunk hh*8 of every 16) ---------------
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        uint4 raw = bitcast<uint4>(qv[s]);
+        raw.x ^= p.q_sign; raw.y ^= p.q_sign; raw.z ^= p.q_sign; raw.w ^= p.q_sign;
+        qv[s] = bitcast<vec8>(raw);
     }
 
     // ---- per-query key ranges -----------------------------------------------------------
     // lo: first band key; corelo: first key of the zero-bias core; pmax: largest
     // admissible landmark position (-1: none). All inclusive, relative to the sequence.
-    const float wv = qvalid ? p.w[tok_i * p.w_st] : 0.f;
+    const float wv = qvalid ? wraw : 0.f;
     int lo, corelo, pmax;
     query_ranges<MODE>(i, wv, p.win_edge, lo, corelo, pmax);
     const int wlo = wave_min_u(qvalid ? lo : INT_MAX);
@@ -139,28 +182,28 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     const int wchi = wq0;                        // first query of the wave
 
     // ---- landmark slots -> LDS (invalid / out-of-sequence slots become INT_MAX) --------
-    // k_pad is a multiple of 64, so iteration j of wave w covers landmark tile 4j + w.
-    for (int s = tid; s < p.k_pad; s += 256) {
-        int pos = INT_MAX;
-        float b = 0.f;
-        if (s < p.k_lmk) {
-            const int64_t pp = p.lmk_pos[head * p.lp_sh + seq * p.lp_ss + s * p.lp_sk];
-            if (pp >= 0 && pp < seq_len) {
-                pos = (int)pp;
-                if (p.lmk_bias) b = p.lmk_bias[head * p.lb_sh + seq * p.lb_ss + s * p.lb_sk] * (kLog2e * p.inv_c);
+    // k_pad is a multiple of 64, so slot block j of wave w is landmark tile 4j + w.
+#pragma unroll
+    for (int j = 0; j < LMK_PER_THREAD; ++j) {
+        const int s = tid + 256 * j;
+        if (256 * j < p.k_pad) {  // wave-uniform (k_pad is a multiple of 64)
+            if (s < p.k_pad) {
+                const bool ok = s < p.k_lmk && lpp[j] >= 0 && lpp[j] < seq_len;
+                const int pos = ok ? (int)lpp[j] : INT_MAX;
+                s_lpos[s] = pos;
+                s_lbias[s] = ok ? lbb[j] * (kLog2e * p.inv_c) : 0.f;
+                s_lrow[s] = ok ? pos : 0;
+                const int tmin = wave_min_u(pos);
+                if (lane == 0) s_ltmin[s >> 6] = tmin;
             }
         }
-        s_lpos[s] = pos;
-        s_lbias[s] = b;
-        s_lrow[s] = pos == INT_MAX ? 0 : pos;
-        const int tmin = wave_min_u(pos);
-        if (lane == 0) s_ltmin[s >> 6] = tmin;
     }
     if (lane == 0) {
         s_red[wave][0] = wlo;
         s_red[wave][1] = wpmax;
     }
-    __syncthreads();
+    // LDS writes visible to the workgroup; the tile loads stay in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     const int glo = min(min(s_red[0][0], s_red[1][0]), min(s_red[2][0], s_red[3][0]));
     const int gpmax = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
     // landmark tiles holding at least one position admissible for the workgroup
