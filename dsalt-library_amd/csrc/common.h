@@ -223,4 +223,65 @@ __device__ __forceinline__ int xcd_remap(int bid, int grid) {
     return (bid & 7) * per + (bid >> 3);
 }
 
+// (head, rank) of hardware workgroup `bid` in a grid of n_heads x n_rank items (grid a
+// multiple of 8). When n_heads is a multiple of 8, XCD x = bid % 8 owns the heads
+// [x * n_heads / 8, (x + 1) * n_heads / 8) (their K/V rows stay in one L2) and receives
+// its items rank-major, the heads interleaved: rank 0 of every head first. Otherwise XCD
+// x owns a contiguous range of head-major items. `head` may be >= n_heads for padding.
+__device__ __forceinline__ void head_rank(int bid, int grid, int n_heads, int n_rank, int &head, int &rank) {
+    if ((n_heads & 7) == 0) {
+        const int hpx = n_heads >> 3, j = bid >> 3;
+        head = (bid & 7) * hpx + j % hpx;
+        rank = j / hpx;
+    } else {
+        const int logical = xcd_remap(bid, grid);
+        head = logical / n_rank;
+        rank = logical - head * n_rank;
+    }
+}
+
+struct AddOp {
+    __device__ __forceinline__ int operator()(int a, int b) const { return a + b; }
+};
+__device__ __forceinline__ int wave_sum_u(int x) { return wave_reduce_dpp(x, AddOp()); }
+
+// Block of rank `rank` (0 <= rank < n_rank) when the blocks of all sequences are taken
+// in decreasing block index, ties in increasing sequence order: the late blocks of the
+// sequences, whose key ranges are the longest, are dispatched first and the short
+// first blocks of every sequence last, which shortens the tail of a launch. Ranks past
+// the number of blocks map to no block (false). Level b (block index b) holds the
+// sequences with more than b blocks; C(b) = sum_s max(0, nblk_s - b) ranks lie at levels
+// >= b, so the level of `rank` is the largest b with C(b) > rank (binary search over
+// DPP wave sums) and its sequence is the (rank - C(b+1))-th of that level. One lane per
+// sequence: more than 64 sequences use find_block over reversed ids instead.
+__device__ __forceinline__ bool find_block_desc(const int32_t *__restrict__ cu, int num_seqs, int rank, int n_rank,
+                                                int bm, int lane, int &seq, int &blk, int &seq_start,
+                                                int &seq_len) {
+    if (num_seqs > 64)
+        return find_block(cu, num_seqs, n_rank - 1 - rank, bm, lane, seq, blk, seq_start, seq_len);
+    int c0 = 0, c1 = 0, nblk = 0;
+    if (lane < num_seqs) {
+        c0 = cu[lane];
+        c1 = cu[lane + 1];
+        nblk = max(c1 - c0 + bm - 1, 0) / bm;
+    }
+    if (rank >= wave_sum_u(nblk)) return false;
+    int lo = 0, hi = wave_max_u(nblk);  // C(lo) > rank >= C(hi) = 0
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (wave_sum_u(max(nblk - mid, 0)) > rank) lo = mid;
+        else hi = mid;
+    }
+    const int j = rank - wave_sum_u(max(nblk - lo - 1, 0));
+    const unsigned long long level = __ballot(nblk > lo);
+    const int before = __builtin_amdgcn_mbcnt_hi((uint32_t)(level >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)level, 0u));
+    const int s = __builtin_ctzll(__ballot(((level >> lane) & 1ull) && before == j));
+    seq = s;
+    blk = lo;
+    seq_start = __builtin_amdgcn_readlane(c0, s);
+    seq_len = __builtin_amdgcn_readlane(c1, s) - seq_start;
+    return true;
+}
+
 }  // namespace dsalt

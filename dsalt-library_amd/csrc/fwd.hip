@@ -15,14 +15,20 @@
 //    ds_read_b64_tr_b16 (the PV operand needs keys along K); both tiles are XOR-swizzled
 //    so that either read pattern is bank-conflict free (tiles.h).
 //  * The workgroup streams the union of its waves' key ranges
-//    [min_i(i - w_i + 1), max_i i]; a wave skips tiles outside its own range, and tiles
-//    that lie inside every row's band core take a mask-free path.
+//    [min_i(i - w_i + 1), max_i i]. Each tile iteration is branch-free: the band mask
+//    (keys outside [lo_i, i], which also covers tiles outside a wave's range) is applied
+//    to every tile, so that the softmax VALU work of tile t and the S = K Q^T MFMAs of
+//    tile t+1 form one basic block, as do the O += P V MFMAs of tile t and the mask and
+//    row max of tile t+1; sched_group_barrier interleaves MFMA and VALU inside each.
 //  * Landmark K/V rows are gathered straight from K/V into the same tile buffers after
-//    the band, with per-slot admission (p <= p_max(i)) and per-slot logit bias.
+//    the band, with per-slot admission (p <= p_max(i)) and per-slot logit bias applied
+//    in place by a rare (wave-uniform) branch, as is the SOFT edge bias of band tiles
+//    that reach below a row's core.
 //  * Online softmax in base 2 with a stale maximum: the running max is only raised (and
 //    O rescaled) when a tile exceeds it by more than 2^8, which keeps P <= 256.
 //  * The workgroup -> (head, sequence, block) map is computed in-kernel from cu_seqlens
-//    and remapped across the 8 XCDs, so launches need no host-side block map.
+//    (no host-side block map): each XCD owns whole heads, and blocks arrive in
+//    decreasing block index so that the long late blocks start first.
 #include "common.h"
 #include "launch.h"
 #include "tiles.h"
@@ -52,7 +58,7 @@ struct FwdParams {
 };
 
 template <typename DT, int D, int MODE>
-__global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
+__global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
     typedef typename DT::vec8 vec8;
     constexpr int BN = kFwdBN;
     constexpr int KS = D / 16;              // MFMA k-steps over the head dim
@@ -75,15 +81,13 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     const int ql = lane & 31, hh = lane >> 5;
 
     // ---- workgroup -> (head, sequence, query block) -----------------------------------
-    // Blocks run last-first inside a head: late blocks have the widest key ranges, and
-    // starting them first shortens the tail of the launch.
-    const int logical = xcd_remap(blockIdx.x, p.grid);
-    const int head = logical / p.n_qblk;
+    // Blocks are dispatched in decreasing block index: late blocks have the widest key
+    // ranges, and starting them first shortens the tail of the launch.
+    int head, rank;
+    head_rank(blockIdx.x, p.grid, p.n_heads, p.n_qblk, head, rank);
     if (head >= p.n_heads) return;
     int seq, blk, seq_start, seq_len;
-    if (!find_block(p.cu, p.num_seqs, p.n_qblk - 1 - (logical - head * p.n_qblk), kFwdBM, lane, seq, blk,
-                    seq_start, seq_len))
-        return;
+    if (!find_block_desc(p.cu, p.num_seqs, rank, p.n_qblk, kFwdBM, lane, seq, blk, seq_start, seq_len)) return;
     const int wq0 = blk * kFwdBM + wave * 32;  // first query of this wave
     const int i = wq0 + ql;                    // query offset inside the sequence
     const bool qvalid = i < seq_len;
@@ -178,7 +182,6 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     const int wlo = wave_min_u(qvalid ? lo : INT_MAX);
     const int wclo = wave_max_u(qvalid ? corelo : INT_MIN);
     const int wpmax = wave_max_u(qvalid ? pmax : -1);
-    const int whi = min(wq0 + 31, seq_len - 1);  // last valid query of the wave
     const int wchi = wq0;                        // first query of the wave
 
     // ---- landmark slots -> LDS (invalid / out-of-sequence slots become INT_MAX) --------
@@ -227,13 +230,6 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
             vlanes.load_gather(kl + TB, wave, vrs, vst, lrow);
         }
     };
-    auto tile_active = [&](int t) {  // wave-uniform
-        if (t < nb) {
-            const int tb = band_key0(t);
-            return (tb <= whi) && (tb + BN - 1 >= wlo);
-        }
-        return s_ltmin[lmk_tile(t)] <= wpmax;
-    };
 
     // S^T (64 keys x 32 queries) = K . Q^T, raw q.k, from the K tile of stage `stage`
     auto qk_tile = [&](int stage, f32x16 (&sacc)[2]) {
@@ -257,39 +253,14 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
     for (int d = 0; d < ND; ++d)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[d][r] = 0.f;
-    float m2 = -INFINITY;       // running max (log2 units), stale by at most kStaleMax
+    float m2 = -INFINITY;  // running max (log2 units), stale by at most kStaleMax
+    float mu = 0.f;        // exponent offset: m2, or 0 while m2 is -inf
     float lsum0 = 0.f, lsum1 = 0.f;
     const float c = p.c;
 
-    // online-softmax update with the scores of one tile (raw units, -inf where masked)
-    // and O^T += V^T . P^T from the V tile of stage `stage`
-    auto softmax_pv = [&](f32x16 (&sacc)[2], int stage) {
-        float t0 = fmaxf(fmaxf(sacc[0][0], sacc[0][1]), sacc[0][2]);
-        float t1 = fmaxf(fmaxf(sacc[0][3], sacc[0][4]), sacc[0][5]);
-        float t2 = fmaxf(fmaxf(sacc[1][0], sacc[1][1]), sacc[1][2]);
-        float t3 = fmaxf(fmaxf(sacc[1][3], sacc[1][4]), sacc[1][5]);
-#pragma unroll
-        for (int r = 6; r < 16; r += 2) {
-            t0 = fmaxf(fmaxf(t0, sacc[0][r]), sacc[0][r + 1]);
-            t2 = fmaxf(fmaxf(t2, sacc[1][r]), sacc[1][r + 1]);
-        }
-        const float tmax = half_max(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)));
-        const float tm2 = tmax * c;
-        const bool raise = tm2 > m2 + kStaleMax;
-        if (__builtin_amdgcn_ballot_w64(raise)) {  // wave-uniform branch: rare after the first tile
-            const float alpha = raise ? fast_exp2(m2 - tm2) : 1.f;
-            lsum0 *= alpha;
-            lsum1 *= alpha;
-#pragma unroll
-            for (int d = 0; d < ND; ++d)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
-            m2 = raise ? tm2 : m2;
-        }
-        const float mu = (m2 == -INFINITY) ? 0.f : m2;
-        // P in fp32: its row sum (fp32, unrounded, as the LSE needs it) and its 16-bit
-        // rounding (the PV operand)
-        uint32_t pk[2][8];
+    // P = exp2(S * c - mu) of one tile: fp32 row sums (unrounded, as the LSE needs them)
+    // and the 16-bit P^T operand. Masked scores are -inf and give 0.
+    auto exp_pack = [&](const f32x16 (&sacc)[2], uint32_t (&pk)[2][8]) {
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -300,7 +271,9 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
                 else lsum0 += e0 + e1;
                 pk[rb][j] = DT::pack2(e0, e1);
             }
-        // O^T (D x 32 queries) += V^T . P^T ; k-step kk covers tile keys kk*16..+15
+    };
+    // O^T (D x 32 queries) += V^T . P^T ; k-step kk covers tile keys kk*16..+15
+    auto pv = [&](const uint32_t (&pk)[2][8], int stage) {
         const char *vtile = s_tiles[stage][1];
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
@@ -314,47 +287,12 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
             }
         }
     };
-
-    // masks / biases of tile t folded into its raw scores (bias / c), then softmax + PV.
-    // Each variant calls its own copy of softmax_pv, so the masked scores never have
-    // to be merged back into the registers of the unmasked ones.
-    auto tile_update = [&](int t, f32x16 (&sacc)[2]) {
-        const int stage = t & (NSTAGE - 1);
-        if (t < nb) {
-            const int tb = band_key0(t);
-            // element (rb, r) is key tb + rb*32 + acc_row_const(r) + hh*4 =: tb + hh*4 + cst
-            const int A = i - tb - hh * 4;   // key <= i       <=> cst <= A
-            const int B = lo - tb - hh * 4;  // key >= lo      <=> cst >= B
-            const bool need_lo = tb < wclo;
-            const bool need_hi = tb + BN - 1 > wchi;
-            if (MODE == kSoft && need_lo) {
-                const int Bc = corelo - tb - hh * 4;  // key >= corelo <=> cst >= Bc
-                f32x16 x[2];
-#pragma unroll
-                for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int cst = rb * 32 + acc_row_const(r);
-                        float oms;
-                        const float edge = soft_edge_log2(wv, (float)(A - cst), p.inv_tau, oms);
-                        const float y = sacc[rb][r] + ((cst < Bc) ? edge * p.inv_c : 0.f);
-                        x[rb][r] = ((cst <= A) & (cst >= B)) ? y : -INFINITY;
-                    }
-                softmax_pv(x, stage);
-            } else if (need_lo | need_hi) {
-                const uint32_t keep = rows_le(A) & ~rows_le(B - 1);
-                f32x16 x[2];
-#pragma unroll
-                for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) x[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r]);
-                softmax_pv(x, stage);
-            } else {
-                softmax_pv(sacc, stage);
-            }
-        } else {
+    // Per-element adjustments that only some tiles need, applied in place to the raw
+    // scores of tile t (t < nt): landmark admission (p <= p_max(i)) and bias, and the
+    // SOFT edge bias of band tiles that reach below a row's core.
+    auto adjust = [&](int t, f32x16 (&sacc)[2]) {
+        if (t >= nb) {
             const int lt = lmk_tile(t);
-            f32x16 x[2];
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -367,37 +305,118 @@ __global__ void __launch_bounds__(256) fwd_kernel(const FwdParams p) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int r = g * 4 + e;
-                        x[rb][r] = (pp[e] <= pmax) ? sacc[rb][r] + bb[e] : -INFINITY;
+                        sacc[rb][r] = (pp[e] <= pmax) ? sacc[rb][r] + bb[e] : -INFINITY;
                     }
                 }
-            softmax_pv(x, stage);
+        } else if (MODE == kSoft && band_key0(t) < wclo) {
+            const int tb = band_key0(t);
+            const int A = i - tb - hh * 4;
+            const int Bc = corelo - tb - hh * 4;  // key >= corelo <=> cst >= Bc
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int cst = rb * 32 + acc_row_const(r);
+                    float oms;
+                    const float edge = soft_edge_log2(wv, (float)(A - cst), p.inv_tau, oms);
+                    sacc[rb][r] += (cst < Bc) ? edge * p.inv_c : 0.f;
+                }
+        }
+    };
+    // Band mask of tile t (keys outside [lo, i]; all kept for landmark tiles) applied in
+    // place, branch-free; returns the tile's masked row max (raw units, -inf if empty).
+    // Element (rb, r) is key tb + rb*32 + acc_row_const(r) + hh*4 =: tb + hh*4 + cst.
+    auto mask_max = [&](int t, f32x16 (&sacc)[2]) -> float {
+        const int tb = band_key0(t);
+        const int A = i - tb - hh * 4;   // key <= i  <=> cst <= A
+        const int B = lo - tb - hh * 4;  // key >= lo <=> cst >= B
+        const uint32_t band = rows_le(A) & ~rows_le(B - 1);
+        const uint32_t keep = (t < nb) ? band : 0xffffffffu;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r]);
+        float t0 = fmaxf(fmaxf(sacc[0][0], sacc[0][1]), sacc[0][2]);
+        float t1 = fmaxf(fmaxf(sacc[0][3], sacc[0][4]), sacc[0][5]);
+        float t2 = fmaxf(fmaxf(sacc[1][0], sacc[1][1]), sacc[1][2]);
+        float t3 = fmaxf(fmaxf(sacc[1][3], sacc[1][4]), sacc[1][5]);
+#pragma unroll
+        for (int r = 6; r < 16; r += 2) {
+            t0 = fmaxf(fmaxf(t0, sacc[0][r]), sacc[0][r + 1]);
+            t2 = fmaxf(fmaxf(t2, sacc[1][r]), sacc[1][r + 1]);
+        }
+        return half_max(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)));
+    };
+    // Raise the running max when the tile max exceeds it by more than kStaleMax
+    // (wave-uniform branch, rare after the first tile): O and l are rescaled to it.
+    auto rescale = [&](float tmax) {
+        const float tm2 = tmax * c;
+        const bool raise = tm2 > m2 + kStaleMax;
+        if (__builtin_amdgcn_ballot_w64(raise)) {
+            const float alpha = raise ? fast_exp2(m2 - tm2) : 1.f;
+            lsum0 *= alpha;
+            lsum1 *= alpha;
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
+            m2 = raise ? tm2 : m2;
+            mu = (m2 == -INFINITY) ? 0.f : m2;
         }
     };
 
     // ---- software-pipelined tile loop ----------------------------------------------------
-    // Iteration t: refill the ring with tile t+3, issue S for tile t+1 (its MFMAs run
-    // while this wave does the softmax of tile t), softmax + PV of tile t, then wait
-    // until tile t+2 has landed. The ring holds tiles t (V in use), t+1 (K in use),
-    // t+2 (landing) and t+3 (in flight); tile t+3 reuses the stage of tile t-1, whose V
-    // every wave finished reading before the barrier that ended iteration t-1.
-    // nt >= NSTAGE - 1 = 3, and tiles 0..2 were issued during the setup.
-    auto step = [&](int t, f32x16 (&cur)[2], f32x16 (&nxt)[2], bool act_cur) -> bool {
+    // Iteration t: refill the ring with tile t+3; part A: P of tile t (VALU) interleaved
+    // with S of tile t+1 (MFMA); part B: O += P V of tile t (MFMA) interleaved with the
+    // masks and row max of tile t+1 (VALU); then the max update and a wait until tile
+    // t+2 has landed. The ring holds tiles t (V in use), t+1 (K in use), t+2 (landing)
+    // and t+3 (in flight); tile t+3 reuses the stage of tile t-1, whose V every wave
+    // finished reading before the barrier that ended iteration t-1. Tiles outside a
+    // wave's key range are fully masked (P = 0) rather than skipped, which keeps the
+    // iteration branch-free. nt >= NSTAGE - 1 = 3, and tiles 0..2 were issued during the
+    // setup. The last iteration computes S of a tile that does not exist (stale LDS
+    // stage) and ignores it.
+    auto step = [&](int t, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
         if (t + NSTAGE - 1 < nt) issue_tile(t + NSTAGE - 1);
-        const bool act_nxt = (t + 1 < nt) && tile_active(t + 1);
-        if (t + 1 < nt) qk_tile((t + 1) & (NSTAGE - 1), nxt);  // also for inactive tiles: no
-                                                                 // register copies between buffers
-        if (act_cur) tile_update(t, cur);
+        uint32_t pk[2][8];
+        qk_tile((t + 1) & (NSTAGE - 1), nxt);
+        exp_pack(cur, pk);
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);   // K operand reads
+        __builtin_amdgcn_sched_group_barrier(0x402, 16, 0);  // VALU / transcendental
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x402, 14, 0);  // VALU / transcendental
+        }
+        // keep P and the row sums in part A (otherwise they sink past the branch below)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(pk[rb][j]));
+        asm volatile("" : "+v"(lsum0), "+v"(lsum1));
+        const bool more = t + 1 < nt;
+        if (more) adjust(t + 1, nxt);
+        pv(pk, t & (NSTAGE - 1));
+        const float tmax = mask_max(t + 1, nxt);
+        __builtin_amdgcn_sched_group_barrier(0x100, 16, 1);  // V operand reads
+        __builtin_amdgcn_sched_group_barrier(0x002, 12, 1);  // VALU
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 1);  // VALU
+        }
+        rescale(more ? tmax : -INFINITY);
         if (t + NSTAGE - 1 < nt) tile_barrier<LPT>();
         else tile_barrier<0>();
-        return act_nxt;
     };
     f32x16 sA[2], sB[2];
     tile_barrier<LPT>();  // tiles 0 and 1 landed (tile 2 may be in flight)
-    bool act = tile_active(0);
     qk_tile(0, sA);
+    adjust(0, sA);
+    rescale(mask_max(0, sA));
     for (int t = 0; t < nt; t += 2) {
-        act = step(t, sA, sB, act);
-        if (t + 1 < nt) act = step(t + 1, sB, sA, act);
+        step(t, sA, sB);
+        if (t + 1 < nt) step(t + 1, sB, sA);
     }
 
     // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln 2 --------------------------------

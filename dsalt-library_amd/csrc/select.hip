@@ -6,17 +6,20 @@
 // quantisation is DSALTAttention._window_sizes(floor=True) / the floor+clamp of
 // _train_selectors (dsalt/modules/dsalt_attention.py:277-284, :471).
 //
-// Design: one 256-thread workgroup per (head, sequence).
+// Design: one 1024-thread workgroup per (head, sequence).
 //  * Each score becomes a 32-bit key whose unsigned order is the score order
 //    (NaN > +inf > finite > ..., -0 folded onto +0); covered tokens and -inf get key 0,
 //    which marks "not a candidate". Keys are cached in LDS for L <= 16384.
-//  * If more than k_eff candidates exist, an MSB-first radix select (4 passes of 8-bit
-//    digits; LDS histogram, one wave scans the 256 bins) finds the exact k_eff-th key
-//    `thr` and how many keys equal to it are still needed.
-//  * A final ordered pass emits the selected positions in ascending order with two
-//    workgroup prefix scans per 256-token chunk: keys > thr, plus the first `need_eq`
-//    keys == thr by position (ties: lower position wins). NaN/+inf picks occupy their
-//    slot but are not emitted; every slot after the last emitted one is -1.
+//  * If more than k_eff candidates exist, an MSB-first radix select over key - min_key
+//    (8-bit digits starting at the top bit of the candidates' key range, so that the
+//    first LDS histogram is not concentrated on a few exponent values; one wave scans
+//    the 256 bins) finds the exact k_eff-th key `thr` and how many keys equal to it are
+//    still needed.
+//  * A final ordered pass emits the selected positions in ascending order: each thread
+//    owns a contiguous run of positions, and one workgroup scan of (finite keys > thr,
+//    keys == thr) gives every thread its first output slot. Keys == thr are taken by
+//    position (ties: lower position wins). NaN/+inf picks occupy their slot but are not
+//    emitted; every slot after the last emitted one is -1.
 // Fully deterministic; integer-exact with respect to the fp32 scores.
 #include "common.h"
 #include "launch.h"
@@ -24,7 +27,8 @@
 namespace dsalt {
 namespace {
 
-constexpr int kSelThreads = 256;
+constexpr int kSelThreads = 1024;
+constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kSelCache = 16384;               // keys cached in LDS (64 KB)
 constexpr uint32_t kKeyPosInf = 0xFF800000u;   // key of +inf; finite keys are below it
 
@@ -38,6 +42,7 @@ struct SelParams {
     int num_seqs, n_heads, k;
 };
 
+// Order-preserving 32-bit key of an fp32 score (unsigned order = score order).
 __device__ __forceinline__ uint32_t order_key(float s) {
     if (s != s) return 0xFFFFFFFFu;       // NaN ranks above everything (torch.topk)
     if (s == -INFINITY) return 0u;        // never a finite pick: treated as not selectable
@@ -46,25 +51,57 @@ __device__ __forceinline__ uint32_t order_key(float s) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Exclusive prefix sum over the 256 threads of the workgroup; `total` gets the sum.
-__device__ __forceinline__ int block_excl_scan(int x, int lane, int wave, int *s_tot, int &total) {
-    const int incl = wave_incl_scan(x, lane);
-    if (lane == 63) s_tot[wave] = incl;
-    __syncthreads();
-    const int w0 = s_tot[0], w1 = s_tot[1], w2 = s_tot[2], w3 = s_tot[3];
-    const int off = (wave > 0 ? w0 : 0) + (wave > 1 ? w1 : 0) + (wave > 2 ? w2 : 0);
-    total = w0 + w1 + w2 + w3;
-    __syncthreads();
-    return off + incl - x;
+// Inclusive prefix sum over the 64 lanes of a wave with DPP (rows of 16 by row_shr,
+// then row_bcast15 / row_bcast31 across rows); no LDS traffic.
+__device__ __forceinline__ int wave_incl_scan_dpp(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
+    return x;
 }
 
+// Workgroup-wide exclusive prefix sums of two counters (thread order = tid order).
+__device__ __forceinline__ void block_excl_scan2(int a, int b, int lane, int wave, int (*s_w)[2], int &ea,
+                                                 int &eb, int &ta, int &tb) {
+    const int ia = wave_incl_scan_dpp(a), ib = wave_incl_scan_dpp(b);
+    if (lane == 63) {
+        s_w[wave][0] = ia;
+        s_w[wave][1] = ib;
+    }
+    __syncthreads();
+    int oa = 0, ob = 0;
+    ta = 0;
+    tb = 0;
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) {
+        const int xa = s_w[w][0], xb = s_w[w][1];
+        if (w < wave) {
+            oa += xa;
+            ob += xb;
+        }
+        ta += xa;
+        tb += xb;
+    }
+    ea = oa + ia - a;
+    eb = ob + ib - b;
+    __syncthreads();
+}
+
+// One workgroup of 1024 threads per (head, sequence). The key pass and the histogram
+// passes stride over positions (j = tid + 1024 i: coalesced loads, conflict-free LDS);
+// for the emission thread t owns the contiguous positions [t*C, t*C + C)
+// (C = ceil(L / 1024)), which keeps the output in position order with one workgroup scan.
 __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) {
     __shared__ uint32_t s_keys[kSelCache];
     __shared__ int s_hist[256];
-    __shared__ int s_tot[4];
+    __shared__ int s_w[kSelWaves][2];
+    __shared__ uint32_t s_mm[kSelWaves][2];
     __shared__ int s_bc[2];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int head = blockIdx.x / p.num_seqs;
     const int seq = blockIdx.x - head * p.num_seqs;
     const int start = p.cu[seq];
@@ -72,6 +109,8 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
     int64_t *out = p.out + ((int64_t)head * p.num_seqs + seq) * p.k;
     const int k_eff = min(p.k, max(L, 0));
     const bool cached = L <= kSelCache;
+    const int C = (max(L, 0) + kSelThreads - 1) / kSelThreads;
+    const int j0 = tid * C, j1 = min(j0 + C, max(L, 0));
 
     auto make_key = [&](int j) -> uint32_t {
         const int64_t tok = (int64_t)start + j;
@@ -82,27 +121,48 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
     };
     auto key_at = [&](int j) -> uint32_t { return cached ? s_keys[j] : make_key(j); };
 
-    // pass 0: keys and candidate count
+    // pass 0: keys, candidate count and the candidates' key range
     int cnt = 0;
+    uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
     for (int j = tid; j < L; j += kSelThreads) {
         const uint32_t key = make_key(j);
         if (cached) s_keys[j] = key;
-        cnt += key != 0u;
+        if (key != 0u) {
+            ++cnt;
+            kmin = min(kmin, key);
+            kmax = max(kmax, key);
+        }
     }
-    int ncand;
-    (void)block_excl_scan(cnt, lane, wave, s_tot, ncand);
+    kmin = (uint32_t)wave_min_u((int)(kmin ^ 0x80000000u)) ^ 0x80000000u;  // unsigned via sign flip
+    kmax = (uint32_t)wave_max_u((int)(kmax ^ 0x80000000u)) ^ 0x80000000u;
+    if (lane == 0) {
+        s_mm[wave][0] = kmin;
+        s_mm[wave][1] = kmax;
+    }
+    int e0, e1, ncand, unused;
+    block_excl_scan2(cnt, 0, lane, wave, s_w, e0, e1, ncand, unused);  // its barriers publish s_mm
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) {
+        kmin = min(kmin, s_mm[w][0]);
+        kmax = max(kmax, s_mm[w][1]);
+    }
 
     uint32_t thr = 0u;  // select key > thr, plus the first need_eq keys == thr
     int need_eq = 0;
     if (k_eff > 0 && ncand > k_eff) {
+        // MSB-first radix select on rel = key - kmin, 8-bit digits from the top set bit of
+        // the candidates' range (the first digit is spread over the whole histogram)
+        const uint32_t range = kmax - kmin;
+        const int nbits = range ? 32 - __clz((int)range) : 0;
         uint32_t prefix = 0u, pmask = 0u;
         int remaining = k_eff;
-        for (int shift = 24; shift >= 0; shift -= 8) {
-            s_hist[tid] = 0;
+        for (int shift = max(nbits - 8, 0);; shift = max(shift - 8, 0)) {
+            if (tid < 256) s_hist[tid] = 0;
             __syncthreads();
             for (int j = tid; j < L; j += kSelThreads) {
                 const uint32_t key = key_at(j);
-                if (key != 0u && (key & pmask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1);
+                const uint32_t rel = key - kmin;
+                if (key != 0u && (rel & pmask) == prefix) atomicAdd(&s_hist[(rel >> shift) & 255u], 1);
             }
             __syncthreads();
             if (wave == 0) {
@@ -110,7 +170,7 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
                 const int c0 = s_hist[255 - 4 * lane], c1 = s_hist[254 - 4 * lane];
                 const int c2 = s_hist[253 - 4 * lane], c3 = s_hist[252 - 4 * lane];
                 const int sum4 = c0 + c1 + c2 + c3;
-                const int incl = wave_incl_scan(sum4, lane);
+                const int incl = wave_incl_scan_dpp(sum4);
                 const int excl = incl - sum4;
                 if (excl < remaining && incl >= remaining) {
                     int cum = excl, d;
@@ -133,30 +193,43 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
             pmask |= 0xFFu << shift;
             remaining -= s_bc[1];
             __syncthreads();
+            if (shift == 0) break;
         }
-        thr = prefix;
+        thr = kmin + prefix;
         need_eq = remaining;
     }
 
-    // ordered emission
-    int run_eq = 0, run_out = 0;
+    // ordered emission: emitted slots before this thread = finite keys > thr before it plus
+    // the equal keys selected before it (equal keys are selected in position order)
     if (k_eff > 0) {
-        for (int base = 0; base < L; base += kSelThreads) {
-            const int j = base + tid;
-            const uint32_t key = j < L ? key_at(j) : 0u;
-            const int is_gt = key > thr;
-            const int is_eq = (need_eq > 0) && (key == thr);
-            int eq_tot, out_tot;
-            const int eq_rank = run_eq + block_excl_scan(is_eq, lane, wave, s_tot, eq_tot);
-            const bool sel = is_gt || (is_eq && eq_rank < need_eq);
-            const int emit = sel && key < kKeyPosInf;
-            const int slot = run_out + block_excl_scan(emit, lane, wave, s_tot, out_tot);
-            if (emit && slot < p.k) out[slot] = j;
-            run_eq += eq_tot;
-            run_out += out_tot;
+        int n_gt = 0, n_eq = 0;
+        for (int j = j0; j < j1; ++j) {
+            const uint32_t key = key_at(j);
+            n_gt += (key > thr) && (key < kKeyPosInf);
+            n_eq += (need_eq > 0) && (key == thr);
         }
+        int gt_before, eq_before, gt_tot, eq_tot;
+        block_excl_scan2(n_gt, n_eq, lane, wave, s_w, gt_before, eq_before, gt_tot, eq_tot);
+        const bool thr_finite = thr < kKeyPosInf;
+        int slot = gt_before + (thr_finite ? min(eq_before, need_eq) : 0);
+        int eq_rank = eq_before;
+        for (int j = j0; j < j1; ++j) {
+            const uint32_t key = key_at(j);
+            bool emit = (key > thr) && (key < kKeyPosInf);
+            if ((need_eq > 0) && (key == thr)) {
+                emit = thr_finite && eq_rank < need_eq;
+                ++eq_rank;
+            }
+            if (emit) {
+                if (slot < p.k) out[slot] = j;
+                ++slot;
+            }
+        }
+        const int total = gt_tot + (thr_finite ? min(eq_tot, need_eq) : 0);
+        for (int s2 = total + tid; s2 < p.k; s2 += kSelThreads) out[s2] = -1;
+    } else {
+        for (int s2 = tid; s2 < p.k; s2 += kSelThreads) out[s2] = -1;
     }
-    for (int s = run_out + tid; s < p.k; s += kSelThreads) out[s] = -1;
 }
 
 __global__ void quantize_kernel(const float *__restrict__ w, int64_t n, float *__restrict__ wq,
