@@ -159,7 +159,7 @@ def make_train_workload(device: torch.device):
                 cu=cu, cu_list=cu_list, T=T, H=H, D=D, lens=lens, k_lmk=k_lmk, dout=dout)
 
 
-def measure_backward(device: torch.device, steps: int = 20, warmup: int = 3) -> dict:
+def measure_backward(device: torch.device, steps: int = 50, warmup: int = 20) -> dict:
     """SOFT forward and backward (dQ, dK, dV, d_lmk_logw, d_w~) at config 3, bf16 in and out."""
     from dsalt import _hip
 
@@ -241,8 +241,10 @@ def load_traffic(cfg: str):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    # the GPU clock ramps up over the first ~10 ms of back-to-back launches: the default
+    # warmup (about 20 ms of forwards) makes the timed steps run at the sustained clock
+    ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-backward", action="store_true", help="skip the config-3 backward measurement")
