@@ -32,6 +32,8 @@
 #include "launch.h"
 #include "tiles.h"
 
+#include <type_traits>
+
 namespace dsalt {
 namespace {
 
@@ -40,6 +42,8 @@ constexpr int kPad4 = 4;  // transposed tile row padding (halves): conflict-free
 constexpr int kBM = 128;  // queries (dq) / keys (kv) per workgroup; prep block size
 constexpr int kTN = 64;   // keys per tile (dq) / queries per tile (kv, lmk_kv)
 constexpr int kLC = 512;  // queries per lmk_kv chunk (chunks are numbered like query blocks)
+
+enum { kCoreTile = 0, kEdgeTile = 1, kLmkTile = 2 };  // tile kinds of the dq loop phases
 
 // Per-(head, query) record written by prep and streamed by kv next to the Q / dO tiles,
 // field-major ([H][field][T]) so that one 64-query tile of a field is one 256-byte
@@ -335,15 +339,7 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
 
     // dS = P (dP - Delta) from shifted logits x (log2 units incl. biases, -inf where not
     // admitted), then dQ^T += K^T . dS^T with K of stage `stage` read transposed
-    auto ds_dq = [&](f32x16 (&x)[2], const f32x16 (&pacc)[2], int stage) {
-        uint32_t pk[2][8];
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float p0 = fast_exp2(x[rb][2 * j] - lse2), p1 = fast_exp2(x[rb][2 * j + 1] - lse2);
-                pk[rb][j] = DT::pack2(p0 * (pacc[rb][2 * j] - delta), p1 * (pacc[rb][2 * j + 1] - delta));
-            }
+    auto dq_mfma = [&](const uint32_t (&pk)[2][8], int stage) {
         const char *ktile = s_tiles[stage][0];
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
@@ -357,15 +353,31 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
             }
         }
     };
+    auto ds_dq = [&](f32x16 (&x)[2], const f32x16 (&pacc)[2], int stage) {
+        uint32_t pk[2][8];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float p0 = fast_exp2(x[rb][2 * j] - lse2), p1 = fast_exp2(x[rb][2 * j + 1] - lse2);
+                pk[rb][j] = DT::pack2(p0 * (pacc[rb][2 * j] - delta), p1 * (pacc[rb][2 * j + 1] - delta));
+            }
+        dq_mfma(pk, stage);
+    };
 
-    tile_barrier<LPT>();  // tiles 0 and 1 landed (tile 2 may be in flight)
-    for (int t = 0; t < nt; ++t) {
+    // ---- tile loop, in phases of one tile kind: band tiles inside every row's core
+    // (keep mask only), SOFT band tiles that reach below a row's core start (a suffix of
+    // the band tiles; edge bias and d_w~), landmark tiles (bias, admission). A tile's
+    // work is one basic block: S^T/dP^T of the lower 32 keys (MFMA), then the masks, P
+    // and dS of that half (VALU) under the S^T/dP^T MFMAs of the upper half, then the
+    // upper half's VALU work under the dQ^T MFMAs of the lower half.
+    auto tile = [&](int t, auto kind) {
+        constexpr int KIND = decltype(kind)::value;
         if (t + NSTAGE - 1 < nt) issue_tile(t + NSTAGE - 1);
         const int stage = t & (NSTAGE - 1);
-        const bool band = t < nb;
-        const int tb = band ? band_key0(t) : 0;
-        const int lt = band ? 0 : lmk_tile(t);
-        const bool active = band ? ((tb <= whi) && (tb + BN - 1 >= wlo)) : (s_ltmin[lt] <= wpmax);
+        const int tb = KIND != kLmkTile ? band_key0(t) : 0;
+        const int lt = KIND == kLmkTile ? lmk_tile(t) : 0;
+        const bool active = KIND != kLmkTile ? ((tb <= whi) && (tb + BN - 1 >= wlo)) : (s_ltmin[lt] <= wpmax);
         if (active) {
             // S^T = K . Q^T and dP^T = V . dO^T (64 keys x 32 queries)
             f32x16 sacc[2], pacc[2];
@@ -386,48 +398,9 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
                 sacc[rb] = a0;
                 pacc[rb] = a1;
             }
-            if (band) {
-                // element (rb, r) is key tb + rb*32 + acc_row_const(r) + hh*4 =: tb + hh*4 + cst
-                const int A = i - tb - hh * 4;   // key <= i  <=> cst <= A
-                const int B = lo - tb - hh * 4;  // key >= lo <=> cst >= B
-                const bool need_lo = tb < wclo;
-                const bool need_hi = tb + BN - 1 > wchi;
-                if (MODE == kSoft && need_lo) {
-                    const int Bc = corelo - tb - hh * 4;
-                    f32x16 x[2];
-#pragma unroll
-                    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int cst = rb * 32 + acc_row_const(r);
-                            float oms;
-                            const float edge = soft_edge_log2(wc, (float)(A - cst), p.inv_tau, oms);
-                            const bool ok = (cst <= A) & (cst >= B);
-                            const bool is_edge = (cst < Bc) & ok;  // exp(-z) may overflow elsewhere
-                            const float y = fmaf(sacc[rb][r], c, is_edge ? edge : 0.f);
-                            x[rb][r] = ok ? y : -INFINITY;
-                            const float pr = ok ? fast_exp2(y - lse2) : 0.f;
-                            dw += is_edge ? pr * (pacc[rb][r] - delta) * oms : 0.f;
-                        }
-                    ds_dq(x, pacc, stage);
-                } else if (need_lo | need_hi) {
-                    const uint32_t keep = rows_le(A) & ~rows_le(B - 1);
-                    f32x16 x[2];
-#pragma unroll
-                    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) x[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r] * c);
-                    ds_dq(x, pacc, stage);
-                } else {
-                    f32x16 x[2];
-#pragma unroll
-                    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) x[rb][r] = sacc[rb][r] * c;
-                    ds_dq(x, pacc, stage);
-                }
-            } else {
-                f32x16 x[2];
+            // logits in log2 units with biases, -inf where not admitted
+            f32x16 x[2];
+            if constexpr (KIND == kLmkTile) {
 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -443,13 +416,80 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
                             x[rb][r] = (pp[e] <= pmax) ? fmaf(sacc[rb][r], c, bb[e]) : -INFINITY;
                         }
                     }
-                ds_dq(x, pacc, stage);
+            } else {
+                // element (rb, r) is key tb + rb*32 + acc_row_const(r) + hh*4 =: tb + hh*4 + cst
+                const int A = i - tb - hh * 4;   // key <= i  <=> cst <= A
+                const int B = lo - tb - hh * 4;  // key >= lo <=> cst >= B
+                if constexpr (MODE == kSoft && KIND == kEdgeTile) {
+                    // edge bias, P, dS and the d_w~ term fused per element: dS (1 - sigma) on
+                    // edge keys; the edge terms are only formed where they are used
+                    // (exp(-z) may overflow elsewhere)
+                    const int Bc = corelo - tb - hh * 4;
+                    uint32_t pk[2][8];
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            float ds2[2];
+#pragma unroll
+                            for (int h2 = 0; h2 < 2; ++h2) {
+                                const int r = 2 * j + h2;
+                                const int cst = rb * 32 + acc_row_const(r);
+                                const bool ok = (cst <= A) & (cst >= B);
+                                const bool is_edge = (cst < Bc) & ok;
+                                const float z = ((float)wc - (float)(A - cst)) * p.inv_tau;
+                                const float e = fast_exp2(is_edge ? -z * kLog2e : 0.f);  // exp(-z)
+                                const float onep = 1.f + e;
+                                const float edge = is_edge ? -fast_log2(onep) : 0.f;  // log2 sigmoid(z)
+                                const float y = fmaf(sacc[rb][r], c, edge);
+                                const float pr = ok ? fast_exp2(y - lse2) : 0.f;
+                                const float dsv = pr * (pacc[rb][r] - delta);
+                                dw += is_edge ? dsv * (e * __builtin_amdgcn_rcpf(onep)) : 0.f;
+                                ds2[h2] = dsv;
+                            }
+                            pk[rb][j] = DT::pack2(ds2[0], ds2[1]);
+                        }
+                    dq_mfma(pk, stage);
+                } else {
+                    const uint32_t keep = rows_le(A) & ~rows_le(B - 1);
+#pragma unroll
+                    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) x[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r] * c);
+                }
+            }
+            if constexpr (KIND != kEdgeTile) ds_dq(x, pacc, stage);
+            if constexpr (KIND != kEdgeTile) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // K/V reads, lower half
+                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // S^T/dP^T MFMAs, lower half
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // K/V reads, upper half
+#pragma unroll
+                for (int m = 0; m < 8; ++m) {  // upper-half MFMAs under lower-half VALU
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x402, 12, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // K^T reads
+#pragma unroll
+                for (int m = 0; m < 8; ++m) {  // dQ^T MFMAs under upper-half VALU
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x402, 10, 0);
+                }
             }
         }
         // tile t+1 must have landed; tiles t+2 .. t+NSTAGE-1 may stay in flight
         if (t + NSTAGE - 1 < nt) tile_barrier<(NSTAGE - 2) * LPT>();
         else tile_barrier<0>();
-    }
+    };
+    // band tiles inside every row's core: tile t holds keys ghi-63-64t .. ghi-64t, all
+    // >= wclo for t <= (ghi-63-wclo)/64
+    const int n_core = MODE == kSoft ? min(nb, (ghi - 63 - wclo >= 0) ? (ghi - 63 - wclo) / BN + 1 : 0) : nb;
+
+    tile_barrier<LPT>();  // tiles 0 and 1 landed (tile 2 may be in flight)
+    int t = 0;
+    for (; t < n_core; ++t) tile(t, std::integral_constant<int, kCoreTile>());
+    if constexpr (MODE == kSoft)
+        for (; t < nb; ++t) tile(t, std::integral_constant<int, kEdgeTile>());
+    for (; t < nt; ++t) tile(t, std::integral_constant<int, kLmkTile>());
 
     if (qvalid) store_row<DT, ND>(p.dq, tok_i * p.dq_st + (int64_t)head * p.dq_sh, p.grad_f32, dqacc, p.scale, hh);
     if (MODE == kSoft && p.ws_dwh) {
