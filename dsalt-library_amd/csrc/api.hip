@@ -165,6 +165,9 @@ int dsalt_bwd_check(const dsalt_bwd_args *a) {
     if (!a->lse) return fail(DSALT_ERR_INVALID, "lse is NULL");
     if (a->mode == DSALT_MODE_SOFT && !(a->tau_win > 0.f))
         return fail(DSALT_ERR_INVALID, "tau_win must be > 0 (got %g)", (double)a->tau_win);
+    if (!(a->scale == a->scale)) return fail(DSALT_ERR_INVALID, "scale is NaN");
+    if (a->scale == 0.f || !(fabsf(a->scale) < INFINITY))
+        return fail(DSALT_ERR_UNSUPPORTED, "scale must be finite and non-zero (got %g)", (double)a->scale);
     const int64_t need = dsalt::bwd_workspace_bytes(a->total_len, a->num_seqs, a->n_heads, a->head_dim,
                                                     a->k_lmk);
     if (need > 0) {

@@ -80,6 +80,7 @@ struct BwdParams {
     int64_t dq_st, dq_sh, dk_st, dk_sh, dv_st, dv_sh;
     int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid_q, n_lgrp, n_lchunk, grad_f32, o_f32;
     float scale, scale_log2, inv_tau, win_edge;
+    float inv_c2;  // 1 / scale_log2: log2-unit bias -> raw q.k units
 };
 
 __device__ __forceinline__ uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
@@ -508,7 +509,7 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
 // P = 2^(S c + bias - lse2) on admitted pairs, dS = P (dP - Delta), then dV^T += dO^T.P
 // and dK^T += Q^T.dS with Q and dO read transposed.
 template <typename DT, int D, int MODE, bool LMK>
-__global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
+__global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
     typedef typename DT::vec8 vec8;
     constexpr int QT = kTN;  // queries per tile
     constexpr int KS = D / 16, ND = D / 32;
@@ -650,101 +651,223 @@ __global__ void __launch_bounds__(256) bwd_kv_kernel(const BwdParams p) {
     if (ntile >= NSTAGE - 1) tile_barrier<(NSTAGE - 2) * LPT>();
     else tile_barrier<0>();
 
-    for (int t = 0; t < ntile; ++t) {
-        if (t + NSTAGE - 1 < ntile) issue_tile(t + NSTAGE - 1);
-        const int st = t & (NSTAGE - 1);
-        const char *qtile = s_tiles[st][0];
-        const char *dtile = s_tiles[st][1];
+    // dV^T += dO^T . P ; dK^T += Q^T . dS   (k-steps over the 32 queries of sub-block sb)
+    auto kv_mfma = [&](const char *qtile, const char *dtile, int sb, const uint32_t (&pkp)[8],
+                       const uint32_t (&pks)[8]) {
 #pragma unroll
-        for (int sbi = 0; sbi < (LMK ? 1 : 2); ++sbi) {
-            const int sb = LMK ? sbw : sbi;
-            const int qsb = q_begin + t * QT + sb * 32;  // first query of the sub-block
-            // group summaries of the sub-block (wave-uniform LDS reads)
-            const int gmin_lo = INT_MAX - *rec_i(st, kRecGLo, sb * 32);
-            const int gmax_clo = INT_MAX - *rec_i(st, kRecGClo, sb * 32);
-            bool skip = qsb >= q_end;
-            if (!LMK) skip = skip || (qsb + 31 < kw) || (gmin_lo > wkmax);
-            else skip = skip || (gmax_clo <= wkmin);  // pmax < corelo
-            if (skip) continue;
-
-            // S and dP (32 queries x 32 keys): lane = key column, registers = query rows
-            f32x16 sacc, pacc;
+        for (int g = 0; g < 2; ++g) {
+            const vec8 bp = bitcast<vec8>(make_uint4(pkp[g * 4], pkp[g * 4 + 1], pkp[g * 4 + 2], pkp[g * 4 + 3]));
+            const vec8 bs = bitcast<vec8>(make_uint4(pks[g * 4], pks[g * 4 + 1], pks[g * 4 + 2], pks[g * 4 + 3]));
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
-#pragma unroll
-            for (int s = 0; s < KS; ++s) {
-                const vec8 qa = bitcast<vec8>(tile_read_row16<D>(qtile, sb * 32 + ql, 2 * s + hh));
-                const vec8 da = bitcast<vec8>(tile_read_row16<D>(dtile, sb * 32 + ql, 2 * s + hh));
-                sacc = DT::mfma(qa, kreg[s], sacc);
-                pacc = DT::mfma(da, vreg[s], pacc);
-            }
-            // register r holds query q = qsb + hh*4 + acc_row_const(r) of the lane's key
-            const int Cj = (kvalid ? key : INT_MAX / 2) - qsb - hh * 4;  // q >= key <=> cst >= Cj
-            const bool need_hi = LMK || (qsb < wkmax);
-            const bool need_lo = LMK || (gmax_clo > wkmin);
-            const bool need_edge = (MODE == kSoft) && !LMK && need_lo;
-            uint32_t pkp[8], pks[8];
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int qi = sb * 32 + g * 8 + hh * 4;
-                const float4 l4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecLse2, qi));
-                const float4 d4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecDelta, qi));
-                const int4 o4 = *reinterpret_cast<const int4 *>(rec_i(st, LMK ? kRecPmax : kRecLo, qi));
-                const float la[4] = {l4.x, l4.y, l4.z, l4.w};
-                const float da[4] = {d4.x, d4.y, d4.z, d4.w};
-                const int oa[4] = {o4.x, o4.y, o4.z, o4.w};
-                int ca[4] = {0, 0, 0, 0};
-                float wa[4] = {0.f, 0.f, 0.f, 0.f};
-                if (need_edge) {
-                    const int4 c4 = *reinterpret_cast<const int4 *>(rec_i(st, kRecClo, qi));
-                    const float4 w4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecWc, qi));
-                    ca[0] = c4.x; ca[1] = c4.y; ca[2] = c4.z; ca[3] = c4.w;
-                    wa[0] = w4.x; wa[1] = w4.y; wa[2] = w4.z; wa[3] = w4.w;
-                }
-                float pr4[4], ds4[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = g * 4 + e;
-                    const int cst = acc_row_const(r);
-                    float pr;
-                    if (LMK) {
-                        // landmark admitted: key <= pmax(q) <=> key < rec pmax (key = INT_MAX when empty)
-                        pr = (key < oa[e]) ? fast_exp2(fmaf(sacc[r], c, kbias2 - la[e])) : 0.f;
-                    } else {
-                        const bool ok = (!need_hi | (cst >= Cj)) & (!need_lo | (oa[e] >= nkey)) & kvalid;
-                        float x = fmaf(sacc[r], c, -la[e]);
-                        if (MODE == kSoft && need_edge) {
-                            float oms;
-                            const float edge = soft_edge_log2(wa[e], (float)(cst - Cj), p.inv_tau, oms);
-                            x += (nkey > ca[e]) ? edge : 0.f;  // key < corelo(q)
-                        }
-                        pr = ok ? fast_exp2(x) : 0.f;
-                    }
-                    const float ds = pr * (pacc[r] - da[e]);
-                    if (LMK) dbias += ds;
-                    pr4[e] = pr;
-                    ds4[e] = ds;
-                }
-                pkp[g * 2] = DT::pack2(pr4[0], pr4[1]);
-                pkp[g * 2 + 1] = DT::pack2(pr4[2], pr4[3]);
-                pks[g * 2] = DT::pack2(ds4[0], ds4[1]);
-                pks[g * 2 + 1] = DT::pack2(ds4[2], ds4[3]);
-            }
-            // dV^T += dO^T . P ; dK^T += Q^T . dS   (k-steps over the 32 queries)
-#pragma unroll
-            for (int g = 0; g < 2; ++g) {
-                const vec8 bp = bitcast<vec8>(make_uint4(pkp[g * 4], pkp[g * 4 + 1], pkp[g * 4 + 2], pkp[g * 4 + 3]));
-                const vec8 bs = bitcast<vec8>(make_uint4(pks[g * 4], pks[g * 4 + 1], pks[g * 4 + 2], pks[g * 4 + 3]));
-#pragma unroll
-                for (int d = 0; d < ND; ++d) {
-                    dv[d] = DT::mfma(bitcast<vec8>(tile_read_tr<D, kSwzRow>(dtile, sb * 32 + g * 16, d * 32, lane)), bp, dv[d]);
-                    dk[d] = DT::mfma(bitcast<vec8>(tile_read_tr<D, kSwzRow>(qtile, sb * 32 + g * 16, d * 32, lane)), bs, dk[d]);
-                }
+            for (int d = 0; d < ND; ++d) {
+                dv[d] = DT::mfma(bitcast<vec8>(tile_read_tr<D, kSwzRow>(dtile, sb * 32 + g * 16, d * 32, lane)), bp, dv[d]);
+                dk[d] = DT::mfma(bitcast<vec8>(tile_read_tr<D, kSwzRow>(qtile, sb * 32 + g * 16, d * 32, lane)), bs, dk[d]);
             }
         }
-        // tile t+1 must have landed; tiles t+2 .. t+NSTAGE-1 may stay in flight
-        if (t + NSTAGE - 1 < ntile) tile_barrier<(NSTAGE - 2) * LPT>();
-        else tile_barrier<0>();
+    };
+    // S and dP (32 queries x 32 keys) of sub-block sb: lane = key column, registers = query rows
+    auto sdp_mfma = [&](const char *qtile, const char *dtile, int sb, f32x16 &sacc, f32x16 &pacc) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const vec8 qa = bitcast<vec8>(tile_read_row16<D>(qtile, sb * 32 + ql, 2 * s + hh));
+            const vec8 da = bitcast<vec8>(tile_read_row16<D>(dtile, sb * 32 + ql, 2 * s + hh));
+            sacc = DT::mfma(qa, kreg[s], sacc);
+            pacc = DT::mfma(da, vreg[s], pacc);
+        }
+    };
+
+    if (!LMK) {
+        // Band: one basic block per 64-query tile. S/dP of both 32-query sub-blocks, the
+        // masks, P and dS of sub-block 0 (VALU) under the S/dP MFMAs of sub-block 1, and
+        // sub-block 1's VALU work under the dV/dK MFMAs of sub-block 0. The band masks
+        // (q >= key, lo(q) <= key) are branch-free; a sub-block without admitted pairs is
+        // fully masked, a tile without any is skipped. SOFT edge biases (key < corelo(q))
+        // are added in place by a wave-uniform branch.
+        for (int t = 0; t < ntile; ++t) {
+            if (t + NSTAGE - 1 < ntile) issue_tile(t + NSTAGE - 1);
+            const int st = t & (NSTAGE - 1);
+            const char *qtile = s_tiles[st][0];
+            const char *dtile = s_tiles[st][1];
+            const int q0 = q_begin + t * QT;
+            bool live[2], edge[2];
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+                const int qsb = q0 + sb * 32;
+                const int gmin_lo = INT_MAX - *rec_i(st, kRecGLo, sb * 32);
+                const int gmax_clo = INT_MAX - *rec_i(st, kRecGClo, sb * 32);
+                live[sb] = !((qsb >= q_end) || (qsb + 31 < kw) || (gmin_lo > wkmax));
+                edge[sb] = (MODE == kSoft) && live[sb] && (gmax_clo > wkmin);
+            }
+            if (live[0] | live[1]) {
+                f32x16 sacc[2], pacc[2];
+                sdp_mfma(qtile, dtile, 0, sacc[0], pacc[0]);
+                sdp_mfma(qtile, dtile, 1, sacc[1], pacc[1]);
+                if (MODE == kSoft) {
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb) {
+                        if (!edge[sb]) continue;
+                        const int qsb = q0 + sb * 32;
+                        const int Cj = (kvalid ? key : INT_MAX / 2) - qsb - hh * 4;
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            const int qi = sb * 32 + g * 8 + hh * 4;
+                            const int4 c4 = *reinterpret_cast<const int4 *>(rec_i(st, kRecClo, qi));
+                            const float4 w4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecWc, qi));
+                            const int ca[4] = {c4.x, c4.y, c4.z, c4.w};
+                            const float wa[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const int r = g * 4 + e;
+                                float oms;
+                                const float eb = soft_edge_log2(wa[e], (float)(acc_row_const(r) - Cj), p.inv_tau, oms);
+                                // raw-score units: the logit is sacc * c + eb
+                                sacc[sb][r] += (nkey > ca[e]) ? eb * p.inv_c2 : 0.f;  // key < corelo(q)
+                            }
+                        }
+                    }
+                }
+                uint32_t pkp[2][8], pks[2][8];
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    const int qsb = q0 + sb * 32;
+                    const int Cj = (kvalid ? key : INT_MAX / 2) - qsb - hh * 4;  // q >= key <=> cst >= Cj
+                    const bool kv_ok = kvalid & live[sb];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int qi = sb * 32 + g * 8 + hh * 4;
+                        float4 l4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecLse2, qi));
+                        float4 d4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecDelta, qi));
+                        int4 o4 = *reinterpret_cast<const int4 *>(rec_i(st, kRecLo, qi));
+                        // whole 16-byte reads, taken unconditionally (otherwise the compiler
+                        // splits them and sinks the parts into per-element branches)
+                        asm volatile("" : "+v"(l4.x), "+v"(l4.y), "+v"(l4.z), "+v"(l4.w), "+v"(d4.x), "+v"(d4.y),
+                                     "+v"(d4.z), "+v"(d4.w), "+v"(o4.x), "+v"(o4.y), "+v"(o4.z), "+v"(o4.w));
+                        const float la[4] = {l4.x, l4.y, l4.z, l4.w};
+                        const float da[4] = {d4.x, d4.y, d4.z, d4.w};
+                        const int oa[4] = {o4.x, o4.y, o4.z, o4.w};
+                        float pr4[4], ds4[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int r = g * 4 + e;
+                            const bool ok = (acc_row_const(r) >= Cj) & (oa[e] >= nkey) & kv_ok;
+                            // masked before the exp (exp2(-inf) = 0): a select, never a branch
+                            const float pr = fast_exp2(ok ? fmaf(sacc[sb][r], c, -la[e]) : -INFINITY);
+                            pr4[e] = pr;
+                            ds4[e] = pr * (pacc[sb][r] - da[e]);
+                        }
+                        pkp[sb][g * 2] = DT::pack2(pr4[0], pr4[1]);
+                        pkp[sb][g * 2 + 1] = DT::pack2(pr4[2], pr4[3]);
+                        pks[sb][g * 2] = DT::pack2(ds4[0], ds4[1]);
+                        pks[sb][g * 2 + 1] = DT::pack2(ds4[2], ds4[3]);
+                    }
+                }
+                kv_mfma(qtile, dtile, 0, pkp[0], pks[0]);
+                kv_mfma(qtile, dtile, 1, pkp[1], pks[1]);
+            }
+            // tile t+1 must have landed; tiles t+2 .. t+NSTAGE-1 may stay in flight
+            if (t + NSTAGE - 1 < ntile) tile_barrier<(NSTAGE - 2) * LPT>();
+            else tile_barrier<0>();
+        }
+    } else {
+    for (int t = 0; t < ntile; ++t) {
+            if (t + NSTAGE - 1 < ntile) issue_tile(t + NSTAGE - 1);
+            const int st = t & (NSTAGE - 1);
+            const char *qtile = s_tiles[st][0];
+            const char *dtile = s_tiles[st][1];
+    #pragma unroll
+            for (int sbi = 0; sbi < (LMK ? 1 : 2); ++sbi) {
+                const int sb = LMK ? sbw : sbi;
+                const int qsb = q_begin + t * QT + sb * 32;  // first query of the sub-block
+                // group summaries of the sub-block (wave-uniform LDS reads)
+                const int gmin_lo = INT_MAX - *rec_i(st, kRecGLo, sb * 32);
+                const int gmax_clo = INT_MAX - *rec_i(st, kRecGClo, sb * 32);
+                bool skip = qsb >= q_end;
+                if (!LMK) skip = skip || (qsb + 31 < kw) || (gmin_lo > wkmax);
+                else skip = skip || (gmax_clo <= wkmin);  // pmax < corelo
+                if (skip) continue;
+    
+                // S and dP (32 queries x 32 keys): lane = key column, registers = query rows
+                f32x16 sacc, pacc;
+    #pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[r] = pacc[r] = 0.f;
+    #pragma unroll
+                for (int s = 0; s < KS; ++s) {
+                    const vec8 qa = bitcast<vec8>(tile_read_row16<D>(qtile, sb * 32 + ql, 2 * s + hh));
+                    const vec8 da = bitcast<vec8>(tile_read_row16<D>(dtile, sb * 32 + ql, 2 * s + hh));
+                    sacc = DT::mfma(qa, kreg[s], sacc);
+                    pacc = DT::mfma(da, vreg[s], pacc);
+                }
+                // register r holds query q = qsb + hh*4 + acc_row_const(r) of the lane's key
+                const int Cj = (kvalid ? key : INT_MAX / 2) - qsb - hh * 4;  // q >= key <=> cst >= Cj
+                const bool need_hi = LMK || (qsb < wkmax);
+                const bool need_lo = LMK || (gmax_clo > wkmin);
+                const bool need_edge = (MODE == kSoft) && !LMK && need_lo;
+                uint32_t pkp[8], pks[8];
+    #pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int qi = sb * 32 + g * 8 + hh * 4;
+                    const float4 l4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecLse2, qi));
+                    const float4 d4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecDelta, qi));
+                    const int4 o4 = *reinterpret_cast<const int4 *>(rec_i(st, LMK ? kRecPmax : kRecLo, qi));
+                    const float la[4] = {l4.x, l4.y, l4.z, l4.w};
+                    const float da[4] = {d4.x, d4.y, d4.z, d4.w};
+                    const int oa[4] = {o4.x, o4.y, o4.z, o4.w};
+                    int ca[4] = {0, 0, 0, 0};
+                    float wa[4] = {0.f, 0.f, 0.f, 0.f};
+                    if (need_edge) {
+                        const int4 c4 = *reinterpret_cast<const int4 *>(rec_i(st, kRecClo, qi));
+                        const float4 w4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecWc, qi));
+                        ca[0] = c4.x; ca[1] = c4.y; ca[2] = c4.z; ca[3] = c4.w;
+                        wa[0] = w4.x; wa[1] = w4.y; wa[2] = w4.z; wa[3] = w4.w;
+                    }
+                    float pr4[4], ds4[4];
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = g * 4 + e;
+                        const int cst = acc_row_const(r);
+                        float pr;
+                        if (LMK) {
+                            // landmark admitted: key <= pmax(q) <=> key < rec pmax (key = INT_MAX when empty)
+                            pr = (key < oa[e]) ? fast_exp2(fmaf(sacc[r], c, kbias2 - la[e])) : 0.f;
+                        } else {
+                            const bool ok = (!need_hi | (cst >= Cj)) & (!need_lo | (oa[e] >= nkey)) & kvalid;
+                            float x = fmaf(sacc[r], c, -la[e]);
+                            if (MODE == kSoft && need_edge) {
+                                float oms;
+                                const float edge = soft_edge_log2(wa[e], (float)(cst - Cj), p.inv_tau, oms);
+                                x += (nkey > ca[e]) ? edge : 0.f;  // key < corelo(q)
+                            }
+                            pr = ok ? fast_exp2(x) : 0.f;
+                        }
+                        const float ds = pr * (pacc[r] - da[e]);
+                        if (LMK) dbias += ds;
+                        pr4[e] = pr;
+                        ds4[e] = ds;
+                    }
+                    pkp[g * 2] = DT::pack2(pr4[0], pr4[1]);
+                    pkp[g * 2 + 1] = DT::pack2(pr4[2], pr4[3]);
+                    pks[g * 2] = DT::pack2(ds4[0], ds4[1]);
+                    pks[g * 2 + 1] = DT::pack2(ds4[2], ds4[3]);
+                }
+                // dV^T += dO^T . P ; dK^T += Q^T . dS   (k-steps over the 32 queries)
+    #pragma unroll
+                for (int g = 0; g < 2; ++g) {
+                    const vec8 bp = bitcast<vec8>(make_uint4(pkp[g * 4], pkp[g * 4 + 1], pkp[g * 4 + 2], pkp[g * 4 + 3]));
+                    const vec8 bs = bitcast<vec8>(make_uint4(pks[g * 4], pks[g * 4 + 1], pks[g * 4 + 2], pks[g * 4 + 3]));
+    #pragma unroll
+                    for (int d = 0; d < ND; ++d) {
+                        dv[d] = DT::mfma(bitcast<vec8>(tile_read_tr<D, kSwzRow>(dtile, sb * 32 + g * 16, d * 32, lane)), bp, dv[d]);
+                        dk[d] = DT::mfma(bitcast<vec8>(tile_read_tr<D, kSwzRow>(qtile, sb * 32 + g * 16, d * 32, lane)), bs, dk[d]);
+                    }
+                }
+            }
+            // tile t+1 must have landed; tiles t+2 .. t+NSTAGE-1 may stay in flight
+            if (t + NSTAGE - 1 < ntile) tile_barrier<(NSTAGE - 2) * LPT>();
+            else tile_barrier<0>();
+        }
+    
     }
 
     if (!LMK) {
@@ -968,6 +1091,7 @@ hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream) {
     p.grid_q = (int)(((int64_t)p.n_qblk * a.n_heads + 7) / 8 * 8);
     p.scale = a.scale;
     p.scale_log2 = a.scale * kLog2e;
+    p.inv_c2 = 1.f / p.scale_log2;
     p.inv_tau = 1.f / a.tau_win;
     p.win_edge = a.win_edge;
     if (a.dtype == DSALT_DTYPE_BF16) return launch_dt<BF16>(p, a.head_dim, a.mode, stream);
