@@ -98,6 +98,33 @@ def test_bwd_workspace_and_check():
     assert lib.dsalt_bwd_check(ctypes.byref(a)) != 0
 
 
+def _fake_bwd(**kw):
+    a = hip.BwdArgs()
+    a.mode, a.dtype, a.total_len, a.num_seqs, a.n_heads, a.head_dim, a.k_lmk = 0, 0, 256, 2, 4, 64, 16
+    base = 0x10000000
+    names = ("q", "k", "v", "out", "lse", "dout", "w", "lmk_pos", "cu_seqlens", "dq", "dk", "dv", "workspace")
+    for i, name in enumerate(names):
+        setattr(a, name, base + i * 0x1000000)
+    for t in ("q", "k", "v", "out", "dout", "dq", "dk", "dv"):
+        setattr(a, t + "_stride_t", 4 * 64)
+        setattr(a, t + "_stride_h", 64)
+    a.lse_stride_t, a.lse_stride_h, a.w_stride = 4, 1, 1
+    a.lmk_pos_stride_h, a.lmk_pos_stride_s, a.lmk_pos_stride_k = 32, 16, 1
+    a.workspace_bytes = 1 << 30
+    a.scale, a.tau_win, a.win_edge = 0.125, 1.0, 4.0
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("value", [0.0, float("inf"), float("nan")])
+def test_bwd_check_rejects_bad_scale(value):
+    lib = hip.lib()
+    assert lib.dsalt_bwd_check(ctypes.byref(_fake_bwd())) == 0, lib.dsalt_last_error().decode()
+    rc = lib.dsalt_bwd_check(ctypes.byref(_fake_bwd(scale=value)))
+    assert rc != 0 and "scale" in lib.dsalt_last_error().decode()
+
+
 def test_select_check():
     lib = hip.lib()
     a = hip.SelectArgs()
