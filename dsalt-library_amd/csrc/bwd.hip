@@ -12,15 +12,15 @@
 // element is produced by exactly one thread, in a fixed order.
 //
 // Kernels, launched in this order on one stream:
-//   prep    one workgroup per (128-token block, head): Delta, and (head 0) the smallest
-//           band start of the block (bounds the key-parallel query scan of `kv`).
+//   dq      query-parallel, 4 waves x 32 queries per workgroup, the forward's tiling (band
+//           tiles, then gathered landmark tiles); S^T, dP^T and dQ^T on MFMA. Computes
+//           Delta = rowsum(O * dO) for its queries and writes dQ, the per-head soft-edge
+//           d_w~, the per-query records of the key-parallel passes and (head 0) the
+//           block's smallest band start, which bounds the query scan of `kv` (workspace).
 //   lmk_kv  key-parallel over landmark slots: one workgroup per (head, 64 slots, chunk of
 //           512 queries of one sequence); 4 waves = 2 slot groups x 2 query sub-blocks scan
 //           the chunk's queries in 64-query LDS tiles. Writes landmark dK/dV and d_bias
 //           partials per chunk (workspace).
-//   dq      query-parallel, 4 waves x 32 queries per workgroup, the forward's tiling (band
-//           tiles, then gathered landmark tiles); S^T, dP^T and dQ^T on MFMA. Writes dQ and
-//           the per-head soft-edge d_w~ (workspace).
 //   kv      key-parallel band dK/dV, 4 waves x 32 keys per workgroup, scanning 64-query LDS
 //           tiles from the key block to the last query block whose band reaches it; adds
 //           the landmark partials (over the sequence's chunks) of keys that are landmark
@@ -39,13 +39,13 @@ namespace {
 
 constexpr int kPad8 = 8;  // row-major tile row padding (halves): conflict-free b128 reads
 constexpr int kPad4 = 4;  // transposed tile row padding (halves): conflict-free b64 reads
-constexpr int kBM = 128;  // queries (dq) / keys (kv) per workgroup; prep block size
+constexpr int kBM = 128;  // queries (dq) / keys (kv) per workgroup
 constexpr int kTN = 64;   // keys per tile (dq) / queries per tile (kv, lmk_kv)
 constexpr int kLC = 512;  // queries per lmk_kv chunk (chunks are numbered like query blocks)
 
 enum { kCoreTile = 0, kEdgeTile = 1, kLmkTile = 2 };  // tile kinds of the dq loop phases
 
-// Per-(head, query) record written by prep and streamed by kv next to the Q / dO tiles,
+// Per-(head, query) record written by dq and streamed by kv next to the Q / dO tiles,
 // field-major ([H][field][T]) so that one 64-query tile of a field is one 256-byte
 // direct load. Integer fields are encoded so that an all-zero record (what an
 // out-of-range load returns) admits no key: lo and corelo as INT_MAX - x, pmax as x + 1.
@@ -70,7 +70,7 @@ struct BwdParams {
     const int32_t *cu;
     void *dq, *dk, *dv;  // gradient outputs: fp32 if grad_f32, else the compute dtype
     float *d_bias, *d_w;
-    float *ws_qrec;          // per-query records [H][kRecFields][T] (see bwd_prep_kernel)
+    float *ws_qrec;          // per-query records [H][kRecFields][T], written by bwd_dq_kernel
     int *ws_minlo;           // [n_qblk]
     float *ws_dwh;           // [T*H] or null
     float *ws_ldk, *ws_ldv;  // landmark dK/dV partials [H][n_lchunk][k_pad][D] or null
@@ -125,84 +125,6 @@ __device__ __forceinline__ void pack_block(const f32x16 &x, uint32_t (&pk)[8]) {
 }
 
 // ==================================================================================
-// prep: one workgroup per (128-token block, head), two threads per token: Delta =
-// rowsum(O * dO) and the token's per-query record; the head-0 workgroup of a block also
-// records the block's smallest band start
-// ==================================================================================
-template <typename DT, int D, int MODE>
-__global__ void __launch_bounds__(256) bwd_prep_kernel(const BwdParams p) {
-    __shared__ int s_min[4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int head = blockIdx.x % p.n_heads;
-    const int bidx = blockIdx.x / p.n_heads;
-    int seq, blk, seq_start, seq_len;
-    if (!find_block(p.cu, p.num_seqs, bidx, kBM, lane, seq, blk, seq_start, seq_len)) return;
-    const int base = blk * kBM;
-    const int t = tid >> 1, half = tid & 1;
-    const bool valid = base + t < seq_len;
-    const int64_t tok = (int64_t)seq_start + base + t;
-
-    // Delta uses O as stored (fp32 when the forward wrote fp32) and dO in the compute dtype
-    // (dsalt_triton_train.py:673-674)
-    constexpr int HALF = D / 2;  // elements per thread
-    float acc = 0.f;
-    if (valid) {
-        const int64_t ooff = tok * p.o_st + (int64_t)head * p.o_sh + half * HALF;
-        const uint16_t *dp = p.dout + tok * p.do_st + (int64_t)head * p.do_sh + half * HALF;
-#pragma unroll
-        for (int c = 0; c < HALF / 8; ++c) {
-            const uint4 d8 = ld16(dp + c * 8);
-            const uint16_t *de = reinterpret_cast<const uint16_t *>(&d8);
-            float of[8];
-            if (p.o_f32) {
-                const float4 x = *reinterpret_cast<const float4 *>(static_cast<const float *>(p.o) + ooff + c * 8);
-                const float4 y = *reinterpret_cast<const float4 *>(static_cast<const float *>(p.o) + ooff + c * 8 + 4);
-                of[0] = x.x; of[1] = x.y; of[2] = x.z; of[3] = x.w;
-                of[4] = y.x; of[5] = y.y; of[6] = y.z; of[7] = y.w;
-            } else {
-                const uint4 o8 = ld16(static_cast<const uint16_t *>(p.o) + ooff + c * 8);
-                const uint16_t *oe = reinterpret_cast<const uint16_t *>(&o8);
-#pragma unroll
-                for (int x = 0; x < 8; ++x) of[x] = DT::to_f32(oe[x]);
-            }
-#pragma unroll
-            for (int x = 0; x < 8; ++x) acc = fmaf(of[x], DT::to_f32(de[x]), acc);
-        }
-    }
-    acc += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc), 0xB1, 0xF, 0xF, false));  // + partner
-
-    // ranges of this token (both threads of a token compute them; wave w holds the
-    // 32-token group w of the block)
-    int lo = INT_MAX, corelo = INT_MAX, pmax = -1;
-    float wv = 0.f;
-    if (valid) {
-        wv = p.w[tok * p.w_st];
-        query_ranges<MODE>(base + t, wv, p.win_edge, lo, corelo, pmax);
-    }
-    const int glo = wave_min_u(lo);
-    const int gclo = wave_max_u(valid ? corelo : INT_MIN);
-    if (valid && half == 0) {
-        const float lv = p.lse[tok * p.lse_st + (int64_t)head * p.lse_sh];
-        float *rec = p.ws_qrec + (size_t)head * kRecFields * p.total_len + tok;
-        const size_t T = (size_t)p.total_len;
-        rec[kRecLse2 * T] = (lv == -INFINITY) ? INFINITY : lv * kLog2e;
-        rec[kRecDelta * T] = acc;
-        reinterpret_cast<int *>(rec)[kRecLo * T] = INT_MAX - lo;
-        reinterpret_cast<int *>(rec)[kRecClo * T] = INT_MAX - corelo;
-        reinterpret_cast<int *>(rec)[kRecPmax * T] = pmax + 1;
-        rec[kRecWc * T] = wv;
-        reinterpret_cast<int *>(rec)[kRecGLo * T] = INT_MAX - glo;
-        reinterpret_cast<int *>(rec)[kRecGClo * T] = INT_MAX - gclo;
-    }
-
-    if (head == 0) {  // smallest band start of the block
-        if (lane == 0) s_min[wave] = glo;
-        __syncthreads();
-        if (tid == 0) p.ws_minlo[bidx] = min(min(s_min[0], s_min[1]), min(s_min[2], s_min[3]));
-    }
-}
-
-// ==================================================================================
 // dq: query-parallel dQ (band + landmarks) and per-head soft-edge d_w~
 // ==================================================================================
 // The forward's structure: one workgroup = 4 waves x 32 queries of one (sequence, head);
@@ -233,9 +155,8 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     const int head = logical / p.n_qblk;
     if (head >= p.n_heads) return;
     int seq, blk, seq_start, seq_len;
-    if (!find_block(p.cu, p.num_seqs, p.n_qblk - 1 - (logical - head * p.n_qblk), kBM, lane, seq, blk, seq_start,
-                    seq_len))
-        return;
+    const int target = p.n_qblk - 1 - (logical - head * p.n_qblk);
+    if (!find_block(p.cu, p.num_seqs, target, kBM, lane, seq, blk, seq_start, seq_len)) return;
     const int wq0 = blk * kBM + wave * 32;
     const int i = wq0 + ql;
     const bool qvalid = i < seq_len;
@@ -277,12 +198,56 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     }
     const float lsev = qvalid ? p.lse[tok_i * p.lse_st + (int64_t)head * p.lse_sh] : -INFINITY;
     const float lse2 = (lsev == -INFINITY) ? INFINITY : lsev * kLog2e;  // +inf: every P is 0
-    const float delta = qvalid ? p.ws_qrec[((size_t)head * kRecFields + kRecDelta) * p.total_len + tok_i] : 0.f;
+    // Delta_i = sum_d O_i dO_i with O as stored (fp32 when the forward wrote fp32) and dO
+    // in the compute dtype (dsalt_triton_train.py:673-674): this lane holds the dims
+    // s*16 + hh*8 .. +7 of dO (its B operand), the other half-wave the rest
+    float delta;
+    {
+        float acc = 0.f;
+        if (qvalid) {
+            const int64_t ooff = tok_i * p.o_st + (int64_t)head * p.o_sh + hh * 8;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const uint4 d8 = bitcast<uint4>(dov[s]);
+                const uint16_t *de = reinterpret_cast<const uint16_t *>(&d8);
+                float of[8];
+                if (p.o_f32) {
+                    const float *op = static_cast<const float *>(p.o) + ooff + s * 16;
+                    const float4 x = *reinterpret_cast<const float4 *>(op);
+                    const float4 y = *reinterpret_cast<const float4 *>(op + 4);
+                    of[0] = x.x; of[1] = x.y; of[2] = x.z; of[3] = x.w;
+                    of[4] = y.x; of[5] = y.y; of[6] = y.z; of[7] = y.w;
+                } else {
+                    const uint4 o8 = ld16(static_cast<const uint16_t *>(p.o) + ooff + s * 16);
+                    const uint16_t *oe = reinterpret_cast<const uint16_t *>(&o8);
+#pragma unroll
+                    for (int x = 0; x < 8; ++x) of[x] = DT::to_f32(oe[x]);
+                }
+#pragma unroll
+                for (int x = 0; x < 8; ++x) acc = fmaf(of[x], DT::to_f32(de[x]), acc);
+            }
+        }
+        delta = half_sum(acc);
+    }
     const float wc = qvalid ? p.w[tok_i * p.w_st] : 0.f;
     int lo, corelo, pmax;
     query_ranges<MODE>(i, wc, p.win_edge, lo, corelo, pmax);
     const int wlo = wave_min_u(qvalid ? lo : INT_MAX);
     const int wclo = wave_max_u(qvalid ? corelo : INT_MIN);
+    // per-query records for the key-parallel passes (field-major [H][field][T]; the wave
+    // is the query's 32-query group) and, from head 0, the block's smallest band start
+    if (qvalid && hh == 0) {
+        float *rec = p.ws_qrec + (size_t)head * kRecFields * p.total_len + tok_i;
+        const size_t T = (size_t)p.total_len;
+        rec[kRecLse2 * T] = lse2;
+        rec[kRecDelta * T] = delta;
+        reinterpret_cast<int *>(rec)[kRecLo * T] = INT_MAX - lo;
+        reinterpret_cast<int *>(rec)[kRecClo * T] = INT_MAX - corelo;
+        reinterpret_cast<int *>(rec)[kRecPmax * T] = pmax + 1;
+        rec[kRecWc * T] = wc;
+        reinterpret_cast<int *>(rec)[kRecGLo * T] = INT_MAX - wlo;
+        reinterpret_cast<int *>(rec)[kRecGClo * T] = INT_MAX - wclo;
+    }
     const int wpmax = wave_max_u(qvalid ? pmax : -1);
     const int whi = min(wq0 + 31, seq_len - 1);
     const int wchi = wq0;
@@ -310,6 +275,7 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     __syncthreads();
     const int glo = min(min(s_red[0][0], s_red[1][0]), min(s_red[2][0], s_red[3][0]));
     const int gpmax = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
+    if (head == 0 && tid == 0) p.ws_minlo[target] = glo;  // bounds the query scan of the kv pass
     const int n_lt = p.k_pad / BN;
     const uint64_t lmask = __ballot(lane < n_lt && s_ltmin[lane < n_lt ? lane : 0] <= gpmax);
     const int nb = max((ghi - glo) / BN + 1, NSTAGE - 1);
@@ -1010,15 +976,15 @@ WsLayout ws_layout(int T, int S, int H, int D, int k) {
 
 template <typename DT, int D, int MODE>
 hipError_t launch_typed(const BwdParams &p, hipStream_t stream) {
-    hipLaunchKernelGGL((bwd_prep_kernel<DT, D, MODE>), dim3(p.n_qblk * p.n_heads), dim3(256), 0, stream, p);
+    // dq writes the per-query records that the key-parallel passes stream
+    const size_t dyn = (size_t)p.k_pad * (2 * sizeof(int) + sizeof(float));
+    hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE>), dim3(p.grid_q), dim3(256), dyn, stream, p);
     if (p.k_lmk > 0) {
         hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, true>), dim3(p.n_heads * p.n_lgrp * p.n_lchunk), dim3(256),
                            0, stream, p);
         if (p.d_bias)
             hipLaunchKernelGGL(bwd_dbias_kernel, dim3(p.n_heads * p.num_seqs), dim3(64), 0, stream, p);
     }
-    const size_t dyn = (size_t)p.k_pad * (2 * sizeof(int) + sizeof(float));
-    hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE>), dim3(p.grid_q), dim3(256), dyn, stream, p);
     hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false>), dim3(p.grid_q), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
