@@ -191,6 +191,27 @@ def measure_backward(device: torch.device, steps: int = 50, warmup: int = 20) ->
     }
 
 
+def time_graph(fn, per_graph: int = 50, replays: int = 10) -> float:
+    """Per-launch time of `fn` from a HIP graph of `per_graph` captured launches, replayed
+    `replays` times: kernels shorter than the host's launch cost are timed on the GPU
+    alone. `fn` must launch on the current stream and must not allocate or memset."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (replays * per_graph)
+
+
 def time_launches(fn, steps: int, warmup: int) -> float:
     for _ in range(warmup):
         fn()
@@ -283,8 +304,28 @@ def main():
         mod = wl["mod"]
         scores, _, _ = hybrid_scores_per_head(wl["xp"], mod.v_proj.weight, mod._alpha().float(), H, D)
         w_cont = mod._window_continuous(wl["xp"]).float()
-    sel_ms = time_launches(lambda: _hip.select_landmarks(scores, w, cu, wl["k_lmk"]), 20, 3)
-    qz_ms = time_launches(lambda: _hip.quantize_windows(w_cont), 20, 3)
+    sel = _hip.SelectLauncher(scores, w, cu, wl["k_lmk"])
+    sel_ms = time_graph(sel)
+    qz_ms = time_graph(_hip.QuantizeLauncher(w_cont))
+    bytes_sel = 4 * T * H + 4 * T + 4 * (wl["B"] + 1) + 8 * H * wl["B"] * wl["k_lmk"]
+
+    # cold HBM: launches rotate over input sets whose total (> 512 MB) exceeds the
+    # 256 MB last-level cache, so every launch reads Q, K and V from HBM
+    n_sets = max(2, int(math.ceil(544e6 / (4 * q.numel() * 2))))
+    sets = []
+    for _ in range(n_sets):
+        qs, ks, vs = q.clone(), k.clone(), v.clone()
+        os_ = torch.empty_like(q)
+        ls = torch.empty((H, T), device=dev, dtype=torch.float32).t()
+        sets.append(_hip.FwdLauncher(_hip.MODE_HARD, qs, ks, vs, w, lmk, None, cu, scale, out=os_, lse=ls))
+    rot = [0]
+
+    def cold_step():
+        sets[rot[0] % n_sets]()
+        rot[0] += 1
+
+    cold_ms = time_launches(cold_step, max(args.steps, 4 * n_sets), 2 * n_sets)
+    del sets
 
     P = effective_pairs_hard(w.float().cpu().numpy(), lmk.cpu().numpy(), cu.cpu().tolist())
     flops = 4.0 * D * P
@@ -331,7 +372,16 @@ def main():
             "flops_per_launch": flops,
         },
         "bytes_per_launch": bytes_alg,
+        # the same forward with every launch on a different input set (> 512 MB in total)
+        "cold": {
+            "ms_per_step": cold_ms,
+            "tokens_per_s": T / (cold_ms * 1e-3),
+            "mfma_frac": flops / (cold_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "hbm_frac": bytes_alg / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "input_sets": n_sets,
+        },
         "select_ms": sel_ms,
+        "select": {"us": sel_ms * 1e3, "GB/s": bytes_sel / (sel_ms * 1e-3) / 1e9, "bytes": bytes_sel},
         "quantize_ms": qz_ms,
         "path_ms": ms + sel_ms + qz_ms,
     }

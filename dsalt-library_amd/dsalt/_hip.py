@@ -392,6 +392,48 @@ def select_landmarks(scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Te
     return out
 
 
+class SelectLauncher:
+    """select_landmarks with its argument block built once: each call launches the
+    selection kernel on the current stream (for timing loops); `out` holds the result."""
+
+    def __init__(self, scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Tensor, k_lmk: int):
+        self.device = require_gpu(scores, w, cu_seqlens)
+        if scores.dtype != torch.float32:
+            raise DsaltError(f"scores must be float32, got {scores.dtype}")
+        T, H = scores.shape
+        self._cu = _cu_i32(cu_seqlens)
+        self._w = _f32_vec(w)
+        self._scores = scores
+        S = self._cu.shape[0] - 1
+        self.out = torch.empty((H, S, k_lmk), device=self.device, dtype=torch.int64)
+        a = SelectArgs()
+        a.total_len, a.num_seqs, a.n_heads, a.k_lmk = T, S, H, k_lmk
+        a.scores, a.scores_stride_t, a.scores_stride_h = scores.data_ptr(), scores.stride(0), scores.stride(1)
+        a.w, a.w_stride = self._w.data_ptr(), self._w.stride(0)
+        a.cu_seqlens = self._cu.data_ptr()
+        a.lmk_pos = self.out.data_ptr()
+        self._args = a
+        self._ref = ctypes.byref(a)
+        self._fn = lib().dsalt_select_landmarks
+
+    def __call__(self) -> None:
+        _raise(self._fn(self._ref, stream_handle(self.device)), "dsalt_select_landmarks")
+
+
+class QuantizeLauncher:
+    """quantize_windows with the buffers allocated once (for timing loops)."""
+
+    def __init__(self, w_cont: torch.Tensor):
+        self.device = require_gpu(w_cont)
+        self._w = _f32_vec(w_cont).contiguous()
+        self.out = torch.empty_like(self._w)
+        self._fn = lib().dsalt_quantize_windows
+
+    def __call__(self) -> None:
+        _raise(self._fn(self._w.data_ptr(), self._w.numel(), self.out.data_ptr(), None, stream_handle(self.device)),
+               "dsalt_quantize_windows")
+
+
 def quantize_windows(w_cont: torch.Tensor, want_int: bool = False):
     """w = max(1, floor(w~)) as float32 (NaN stays NaN); optionally also as int32."""
     dev = require_gpu(w_cont)
