@@ -272,3 +272,34 @@ def test_fwd_fp32_output(mode):
     o_ref, l_ref = run_oracle(mode, q, kk, v, w, pos, bias, cu)
     close(out.cpu(), o_ref, "fp32 out")
     lse_close(lse.cpu(), l_ref, "fp32 out lse")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("mode", [hip.MODE_HARD, hip.MODE_SOFT], ids=["hard", "soft"])
+@pytest.mark.parametrize("case", ["large", "small", "tiny", "underflow"])
+def test_fwd_extreme_logits(mode, case, dtype):
+    """Logits far from 0: tile sums beyond the 16-bit range ("large"), row totals of
+    about 2^-40 ("small": kept as they are in bf16), about 2^-72 ("tiny") and P that all
+    underflow in fp32 ("underflow") must still match the oracle."""
+    print(f"extreme logits mode={mode} case={case} dtype={dtype}", flush=True)
+    lens, H, D, k = [200, 77], 2, 64, 8
+    q, kk, v, w, pos, bias, cu = make_inputs(lens, H, D, k, mode, seed=21, dtype=dtype, n_min=4, n_max=90)
+    scale = 1.0 / math.sqrt(D)
+    if case == "large":
+        scale = 8.0
+    else:
+        # Q and K along opposite directions: every q.k is about -a^2
+        a = {"small": 15.0, "tiny": 20.0, "underflow": 40.0}[case]
+        g = torch.Generator().manual_seed(5)
+        u = torch.randn(D, generator=g)
+        u = u / u.norm()
+        q = (a * u + 0.1 * torch.randn(q.shape, generator=g)).to(dtype)
+        kk = (-a * u + 0.1 * torch.randn(kk.shape, generator=g)).to(dtype)
+    dev = torch.device("cuda", 0)
+    out, lse = hip.fwd(mode, q.to(dev), kk.to(dev), v.to(dev), w.to(dev), pos.to(dev), bias.to(dev), cu.to(dev),
+                       scale, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    o_ref, l_ref = run_oracle(mode, q, kk, v, w, pos, bias, cu, scale=scale)
+    assert torch.isfinite(out).all()
+    close(out.cpu(), o_ref, f"extreme {case}")
+    lse_close(lse.cpu(), l_ref, f"extreme {case} lse")
