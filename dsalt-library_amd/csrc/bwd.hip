@@ -770,7 +770,7 @@ __global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
                 const bool need_hi = LMK || (qsb < wkmax);
                 const bool need_lo = LMK || (gmax_clo > wkmin);
                 const bool need_edge = (MODE == kSoft) && !LMK && need_lo;
-                uint32_t pkp[8], pks[8];
+                uint32_t pkp[8], pks[8], plo[8], slo[8];
     #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int qi = sb * 32 + g * 8 + hh * 4;
@@ -816,16 +816,30 @@ __global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
                     pkp[g * 2 + 1] = DT::pack2(pr4[2], pr4[3]);
                     pks[g * 2] = DT::pack2(ds4[0], ds4[1]);
                     pks[g * 2 + 1] = DT::pack2(ds4[2], ds4[3]);
+                    // rounding remainders x - 16bit(x) (exact in fp32), rounded in turn
+                    plo[g * 2] = DT::pack2(pr4[0] - DT::lo_f32(pkp[g * 2]), pr4[1] - DT::hi_f32(pkp[g * 2]));
+                    plo[g * 2 + 1] = DT::pack2(pr4[2] - DT::lo_f32(pkp[g * 2 + 1]), pr4[3] - DT::hi_f32(pkp[g * 2 + 1]));
+                    slo[g * 2] = DT::pack2(ds4[0] - DT::lo_f32(pks[g * 2]), ds4[1] - DT::hi_f32(pks[g * 2]));
+                    slo[g * 2 + 1] = DT::pack2(ds4[2] - DT::lo_f32(pks[g * 2 + 1]), ds4[3] - DT::hi_f32(pks[g * 2 + 1]));
                 }
-                // dV^T += dO^T . P ; dK^T += Q^T . dS   (k-steps over the 32 queries)
+                // dV^T += dO^T . P ; dK^T += Q^T . dS   (k-steps over the 32 queries). A
+                // landmark key sums over every query of its sequence, so P and dS enter as
+                // 16-bit high part + 16-bit remainder (relative error ~2^-17 instead of
+                // ~2^-9 of a single rounding); the operand read is shared by both MFMAs.
     #pragma unroll
                 for (int g = 0; g < 2; ++g) {
                     const vec8 bp = bitcast<vec8>(make_uint4(pkp[g * 4], pkp[g * 4 + 1], pkp[g * 4 + 2], pkp[g * 4 + 3]));
                     const vec8 bs = bitcast<vec8>(make_uint4(pks[g * 4], pks[g * 4 + 1], pks[g * 4 + 2], pks[g * 4 + 3]));
+                    const vec8 bpl = bitcast<vec8>(make_uint4(plo[g * 4], plo[g * 4 + 1], plo[g * 4 + 2], plo[g * 4 + 3]));
+                    const vec8 bsl = bitcast<vec8>(make_uint4(slo[g * 4], slo[g * 4 + 1], slo[g * 4 + 2], slo[g * 4 + 3]));
     #pragma unroll
                     for (int d = 0; d < ND; ++d) {
-                        dv[d] = DT::mfma(bitcast<vec8>(tile_read_tr<D, kSwzRow>(dtile, sb * 32 + g * 16, d * 32, lane)), bp, dv[d]);
-                        dk[d] = DT::mfma(bitcast<vec8>(tile_read_tr<D, kSwzRow>(qtile, sb * 32 + g * 16, d * 32, lane)), bs, dk[d]);
+                        const vec8 ad = bitcast<vec8>(tile_read_tr<D, kSwzRow>(dtile, sb * 32 + g * 16, d * 32, lane));
+                        const vec8 aq = bitcast<vec8>(tile_read_tr<D, kSwzRow>(qtile, sb * 32 + g * 16, d * 32, lane));
+                        dv[d] = DT::mfma(ad, bp, dv[d]);
+                        dk[d] = DT::mfma(aq, bs, dk[d]);
+                        dv[d] = DT::mfma(ad, bpl, dv[d]);
+                        dk[d] = DT::mfma(aq, bsl, dk[d]);
                     }
                 }
             }

@@ -39,6 +39,9 @@ struct BF16 {
     static __device__ __forceinline__ float to_f32(uint16_t x) {
         return __uint_as_float(((uint32_t)x) << 16);
     }
+    // the low / high element of a packed pair
+    static __device__ __forceinline__ float lo_f32(uint32_t x) { return __uint_as_float(x << 16); }
+    static __device__ __forceinline__ float hi_f32(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
 };
 
 struct F16 {
@@ -53,6 +56,8 @@ struct F16 {
     static __device__ __forceinline__ float to_f32(uint16_t x) {
         return (float)bitcast<_Float16>(x);
     }
+    static __device__ __forceinline__ float lo_f32(uint32_t x) { return to_f32((uint16_t)x); }
+    static __device__ __forceinline__ float hi_f32(uint32_t x) { return to_f32((uint16_t)(x >> 16)); }
 };
 
 // Row index (within a 32-row MFMA block) of accumulator register r of a lane in half

@@ -9,7 +9,8 @@
 //    a lane holds ONE query (column lane%32) and 16 keys per 32-key block: the row max
 //    is an in-register max plus one v_permlane32_swap between the two lane halves, and
 //    P^T converts in place into the B operand of O^T += V^T . P^T (no data movement).
-//  * K and V tiles (64 keys) go global -> LDS with direct loads (global_load_lds_dwordx4,
+//  * K and V tiles (BN = 64 keys at D = 64, 32 at D = 128: 8 KB each of K and V either
+//    way) go global -> LDS with direct loads (global_load_lds_dwordx4,
 //    no register staging) into a ring of NSTAGE buffers: loads run NSTAGE-1 tiles ahead
 //    of the MFMAs, so their latency is hidden even at low occupancy. K is read row-major, V with the transposing
 //    ds_read_b64_tr_b16 (the PV operand needs keys along K); both tiles are XOR-swizzled
@@ -60,12 +61,14 @@ struct FwdParams {
 template <typename DT, int D, int MODE>
 __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
     typedef typename DT::vec8 vec8;
-    constexpr int BN = kFwdBN;
+    constexpr int BN = fwd_bn(D);           // keys per tile
+    constexpr int NRB = BN / 32;            // 32-key row blocks of S^T per tile
     constexpr int KS = D / 16;              // MFMA k-steps over the head dim
     constexpr int ND = D / 32;              // 32-row blocks of O^T
-    constexpr int TB = Tile64<D>::BYTES;
-    constexpr int NSTAGE = 4;                              // LDS ring depth (tiles)
-    constexpr int LPT = 2 * Tile64<D>::LOADS_PER_WAVE;     // load instructions per tile per wave
+    typedef TileN<D, BN> Tile;
+    constexpr int TB = Tile::BYTES;
+    constexpr int NSTAGE = 4;                          // LDS ring depth (tiles)
+    constexpr int LPT = 2 * Tile::LOADS_PER_WAVE;      // load instructions per tile per wave
 
     __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][K, V]
     __shared__ int s_red[4][2];
@@ -95,7 +98,7 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
     const int ghi = min(blk * kFwdBM + kFwdBM - 1, seq_len - 1);  // last query of the workgroup
 
     // ---- tile staging: direct global -> LDS loads ----------------------------------------
-    // Band tiles run from the diagonal down: tile t holds keys ghi-63-64t .. ghi-64t, so
+    // Band tiles run from the diagonal down: tile t holds keys ghi-BN+1-BN*t .. ghi-BN*t, so
     // the first tiles are known before the windows are read and their loads overlap the
     // setup. Landmark tiles follow the band tiles. K/V rows are read through buffer
     // resources whose range is this (sequence, head): rows below the sequence start
@@ -104,8 +107,8 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
     const uint32_t kst = (uint32_t)p.k_st * 2u, vst = (uint32_t)p.v_st * 2u;  // row strides (bytes)
     const i32x4 krs = buffer_rsrc(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh, (uint32_t)seq_len * kst);
     const i32x4 vrs = buffer_rsrc(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh, (uint32_t)seq_len * vst);
-    const TileLanes<D, kSwzRow> klanes(wave, lane, kst);
-    const TileLanes<D, kSwzTr> vlanes(wave, lane, vst);
+    const TileLanes<D, kSwzRow, BN> klanes(wave, lane, kst);
+    const TileLanes<D, kSwzTr, BN> vlanes(wave, lane, vst);
     const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
     auto band_key0 = [&](int t) { return ghi - (BN - 1) - t * BN; };
     auto issue_band = [&](int t) {
@@ -152,8 +155,8 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
             char *kt = s_tiles[t][0];
             char *vt = s_tiles[t][1];
 #pragma unroll
-            for (int u = 0; u < Tile64<D>::LOADS_PER_WAVE; ++u) {
-                const int slot0 = (wave * Tile64<D>::LOADS_PER_WAVE + u) * 64;
+            for (int u = 0; u < Tile::LOADS_PER_WAVE; ++u) {
+                const int slot0 = (wave * Tile::LOADS_PER_WAVE + u) * 64;
                 const int64_t key = max(key0 + klanes.row[u], 0);
                 __builtin_amdgcn_global_load_lds(
                     (const __attribute__((address_space(1))) void *)(kb + key * kst + klanes.chunk_off[u]),
@@ -185,7 +188,8 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
     const int wchi = wq0;                        // first query of the wave
 
     // ---- landmark slots -> LDS (invalid / out-of-sequence slots become INT_MAX) --------
-    // k_pad is a multiple of 64, so slot block j of wave w is landmark tile 4j + w.
+    // k_pad is a multiple of 64: slot block j of wave w (64 slots) is landmark tile 4j + w
+    // when BN = 64, tiles 8j + 2w and 8j + 2w + 1 when BN = 32.
 #pragma unroll
     for (int j = 0; j < LMK_PER_THREAD; ++j) {
         const int s = tid + 256 * j;
@@ -196,8 +200,17 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
                 s_lpos[s] = pos;
                 s_lbias[s] = ok ? lbb[j] * (kLog2e * p.inv_c) : 0.f;
                 s_lrow[s] = ok ? pos : 0;
-                const int tmin = wave_min_u(pos);
-                if (lane == 0) s_ltmin[s >> 6] = tmin;
+                if (BN == 64) {
+                    const int tmin = wave_min_u(pos);
+                    if (lane == 0) s_ltmin[s >> 6] = tmin;
+                } else {
+                    const int tlo = wave_min_u(hh == 0 ? pos : INT_MAX);
+                    const int thi = wave_min_u(hh == 1 ? pos : INT_MAX);
+                    if (lane == 0) {
+                        s_ltmin[s >> 5] = tlo;
+                        s_ltmin[(s >> 5) + 1] = thi;
+                    }
+                }
             }
         }
     }
@@ -231,11 +244,11 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
         }
     };
 
-    // S^T (64 keys x 32 queries) = K . Q^T, raw q.k, from the K tile of stage `stage`
-    auto qk_tile = [&](int stage, f32x16 (&sacc)[2]) {
+    // S^T (BN keys x 32 queries) = K . Q^T, raw q.k, from the K tile of stage `stage`
+    auto qk_tile = [&](int stage, f32x16 (&sacc)[NRB]) {
         const char *ktile = s_tiles[stage][0];
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
+        for (int rb = 0; rb < NRB; ++rb) {
             f32x16 acc;
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[r] = 0.f;
@@ -260,9 +273,9 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
 
     // P = exp2(S * c - mu) of one tile: fp32 row sums (unrounded, as the LSE needs them)
     // and the 16-bit P^T operand. Masked scores are -inf and give 0.
-    auto exp_pack = [&](const f32x16 (&sacc)[2], uint32_t (&pk)[2][8]) {
+    auto exp_pack = [&](const f32x16 (&sacc)[NRB], uint32_t (&pk)[NRB][8]) {
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+        for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float e0 = fast_exp2(fmaf(sacc[rb][2 * j], c, -mu));
@@ -273,10 +286,10 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
             }
     };
     // O^T (D x 32 queries) += V^T . P^T ; k-step kk covers tile keys kk*16..+15
-    auto pv = [&](const uint32_t (&pk)[2][8], int stage) {
+    auto pv = [&](const uint32_t (&pk)[NRB][8], int stage) {
         const char *vtile = s_tiles[stage][1];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
+        for (int kk = 0; kk < 2 * NRB; ++kk) {
             const int rb = kk >> 1, g = kk & 1;
             const vec8 b = bitcast<vec8>(
                 make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
@@ -290,11 +303,11 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
     // Per-element adjustments that only some tiles need, applied in place to the raw
     // scores of tile t (t < nt): landmark admission (p <= p_max(i)) and bias, and the
     // SOFT edge bias of band tiles that reach below a row's core.
-    auto adjust = [&](int t, f32x16 (&sacc)[2]) {
+    auto adjust = [&](int t, f32x16 (&sacc)[NRB]) {
         if (t >= nb) {
             const int lt = lmk_tile(t);
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
+            for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int slot = lt * BN + rb * 32 + g * 8 + hh * 4;
@@ -313,7 +326,7 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
             const int A = i - tb - hh * 4;
             const int Bc = corelo - tb - hh * 4;  // key >= corelo <=> cst >= Bc
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
+            for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int cst = rb * 32 + acc_row_const(r);
@@ -326,26 +339,33 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
     // Band mask of tile t (keys outside [lo, i]; all kept for landmark tiles) applied in
     // place, branch-free; returns the tile's masked row max (raw units, -inf if empty).
     // Element (rb, r) is key tb + rb*32 + acc_row_const(r) + hh*4 =: tb + hh*4 + cst.
-    auto mask_max = [&](int t, f32x16 (&sacc)[2]) -> float {
+    auto mask_max = [&](int t, f32x16 (&sacc)[NRB]) -> float {
         const int tb = band_key0(t);
         const int A = i - tb - hh * 4;   // key <= i  <=> cst <= A
         const int B = lo - tb - hh * 4;  // key >= lo <=> cst >= B
         const uint32_t band = rows_le(A) & ~rows_le(B - 1);
         const uint32_t keep = (t < nb) ? band : 0xffffffffu;
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+        for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r]);
-        float t0 = fmaxf(fmaxf(sacc[0][0], sacc[0][1]), sacc[0][2]);
-        float t1 = fmaxf(fmaxf(sacc[0][3], sacc[0][4]), sacc[0][5]);
-        float t2 = fmaxf(fmaxf(sacc[1][0], sacc[1][1]), sacc[1][2]);
-        float t3 = fmaxf(fmaxf(sacc[1][3], sacc[1][4]), sacc[1][5]);
+        // v_max3 trees, two chains per row block
+        float tm[2 * NRB];
 #pragma unroll
-        for (int r = 6; r < 16; r += 2) {
-            t0 = fmaxf(fmaxf(t0, sacc[0][r]), sacc[0][r + 1]);
-            t2 = fmaxf(fmaxf(t2, sacc[1][r]), sacc[1][r + 1]);
+        for (int rb = 0; rb < NRB; ++rb) {
+            tm[2 * rb] = fmaxf(fmaxf(sacc[rb][0], sacc[rb][1]), sacc[rb][2]);
+            tm[2 * rb + 1] = fmaxf(fmaxf(sacc[rb][3], sacc[rb][4]), sacc[rb][5]);
         }
-        return half_max(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)));
+#pragma unroll
+        for (int r = 6; r < 16; r += 2)
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb) {
+                float &x = tm[2 * rb + (NRB == 1 ? ((r >> 1) & 1) : 0)];
+                x = fmaxf(fmaxf(x, sacc[rb][r]), sacc[rb][r + 1]);
+            }
+        float mx = fmaxf(tm[0], tm[1]);
+        if constexpr (NRB == 2) mx = fmaxf(mx, fmaxf(tm[2], tm[3]));
+        return half_max(mx);
     };
     // Raise the running max when the tile max exceeds it by more than kStaleMax
     // (wave-uniform branch, rare after the first tile): O and l are rescaled to it.
@@ -376,21 +396,27 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
     // iteration branch-free. nt >= NSTAGE - 1 = 3, and tiles 0..2 were issued during the
     // setup. The last iteration computes S of a tile that does not exist (stale LDS
     // stage) and ignores it.
-    auto step = [&](int t, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+    // MFMAs and operand reads of the two parts of an iteration, and the VALU instructions
+    // placed after each MFMA (part A: exp / sum / pack, ~56 per row block; part B: masks
+    // and max, ~40 per row block)
+    constexpr int NQK = KS * NRB, NPV = 2 * ND * NRB;
+    constexpr int VALU_A = (NRB * 56 - 16 + NQK - 1) / NQK + 2;
+    constexpr int VALU_B = (NRB * 32 + NPV - 1) / NPV;
+    auto step = [&](int t, f32x16 (&cur)[NRB], f32x16 (&nxt)[NRB]) {
         if (t + NSTAGE - 1 < nt) issue_tile(t + NSTAGE - 1);
-        uint32_t pk[2][8];
+        uint32_t pk[NRB][8];
         qk_tile((t + 1) & (NSTAGE - 1), nxt);
         exp_pack(cur, pk);
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);   // K operand reads
-        __builtin_amdgcn_sched_group_barrier(0x402, 16, 0);  // VALU / transcendental
+        __builtin_amdgcn_sched_group_barrier(0x100, NQK, 0);  // K operand reads
+        __builtin_amdgcn_sched_group_barrier(0x402, 16, 0);   // VALU / transcendental
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x402, 14, 0);  // VALU / transcendental
+        for (int m = 0; m < NQK; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x402, VALU_A, 0);  // VALU / transcendental
         }
         // keep P and the row sums in part A (otherwise they sink past the branch below)
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+        for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
             for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(pk[rb][j]));
         asm volatile("" : "+v"(lsum0), "+v"(lsum1));
@@ -398,18 +424,18 @@ __global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
         if (more) adjust(t + 1, nxt);
         pv(pk, t & (NSTAGE - 1));
         const float tmax = mask_max(t + 1, nxt);
-        __builtin_amdgcn_sched_group_barrier(0x100, 16, 1);  // V operand reads
-        __builtin_amdgcn_sched_group_barrier(0x002, 12, 1);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * NPV, 1);  // V operand reads
+        __builtin_amdgcn_sched_group_barrier(0x002, 12, 1);       // VALU
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 8, 1);  // VALU
+        for (int m = 0; m < NPV; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);       // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, VALU_B, 1);  // VALU
         }
         rescale(more ? tmax : -INFINITY);
         if (t + NSTAGE - 1 < nt) tile_barrier<LPT>();
         else tile_barrier<0>();
     };
-    f32x16 sA[2], sB[2];
+    f32x16 sA[NRB], sB[NRB];
     tile_barrier<LPT>();  // tiles 0 and 1 landed (tile 2 may be in flight)
     qk_tile(0, sA);
     adjust(0, sA);

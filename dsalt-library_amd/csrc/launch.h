@@ -8,9 +8,12 @@
 namespace dsalt {
 
 // Forward: one workgroup of 4 waves owns kFwdBM consecutive queries of one
-// (sequence, head); each wave owns 32 of them. Key tiles hold kFwdBN keys.
+// (sequence, head); each wave owns 32 of them. Key tiles hold fwd_bn(D) keys: 64 at
+// D = 64, 32 at D = 128 (the same LDS bytes and MFMA work per tile). Landmark slots are
+// padded to a multiple of kFwdBN = 64, which every tile size divides.
 constexpr int kFwdBM = 128;
 constexpr int kFwdBN = 64;
+constexpr int fwd_bn(int head_dim) { return head_dim == 64 ? 64 : 32; }
 
 hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream);
 hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream);

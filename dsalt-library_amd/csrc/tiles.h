@@ -1,4 +1,4 @@
-// LDS tiles of 64 rows x D 16-bit elements (rows are tokens: keys or queries), filled
+// LDS tiles of ROWS (64 or 32) rows x D 16-bit elements (rows are tokens: keys or queries), filled
 // with direct global->LDS loads (global_load_lds_dwordx4, gfx950) and read back as
 // v_mfma_f32_32x32x16 operands.
 //
@@ -27,13 +27,16 @@ __device__ __forceinline__ int tile_swz(int row) {
     return SWZ == kSwzRow ? (row & 7) : ((row & 3) << 1);
 }
 
-template <int D>
-struct Tile64 {
-    static constexpr int CPR = D / 8;                    // 16-byte chunks per row
-    static constexpr int ROWB = D * 2;                   // bytes per row
-    static constexpr int BYTES = 64 * ROWB;              // bytes per tile
-    static constexpr int LOADS_PER_WAVE = 64 * CPR / 256;  // 64-lane load instructions per wave
+template <int D, int ROWS = 64>
+struct TileN {
+    static constexpr int CPR = D / 8;                        // 16-byte chunks per row
+    static constexpr int ROWB = D * 2;                       // bytes per row
+    static constexpr int BYTES = ROWS * ROWB;                // bytes per tile
+    static constexpr int LOADS_PER_WAVE = ROWS * CPR / 256;  // 64-lane load instructions per wave
+    static_assert(ROWS * CPR % 256 == 0, "4 waves x 64 lanes must cover the tile's 16-byte chunks");
 };
+template <int D>
+using Tile64 = TileN<D, 64>;
 
 // Byte address in LDS of a pointer into a __shared__ array.
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
@@ -66,9 +69,9 @@ __device__ __forceinline__ void dma16(uint32_t voff, i32x4 rsrc, uint32_t lds) {
 // (g % CPR) ^ swz(row) of tile row g / CPR. The per-lane parts (tile row, byte offset of
 // the row and chunk for a given row stride) are computed once; a band tile then costs
 // one add per load, a gathered tile one multiply-add.
-template <int D, int SWZ>
+template <int D, int SWZ, int ROWS = 64>
 struct TileLanes {
-    static constexpr int CPR = D / 8, LPW = Tile64<D>::LOADS_PER_WAVE;
+    static constexpr int CPR = D / 8, LPW = TileN<D, ROWS>::LOADS_PER_WAVE;
     int row[LPW];
     uint32_t chunk_off[LPW];  // byte offset of the lane's chunk inside its row
     uint32_t lane_off[LPW];   // row * stride + chunk_off
@@ -84,7 +87,7 @@ struct TileLanes {
     __device__ __forceinline__ static uint32_t lds_slot(uint32_t tile_lds, int wave, int u) {
         return __builtin_amdgcn_readfirstlane(tile_lds + (wave * LPW + u) * 64 * 16);
     }
-    // Rows row0 .. row0+63 (row0 * stride = base_off, may wrap below 0) into the tile at
+    // Rows row0 .. row0+ROWS-1 (row0 * stride = base_off, may wrap below 0) into the tile at
     // LDS byte tile_lds (wave-uniform).
     __device__ __forceinline__ void load_band(uint32_t tile_lds, int wave, i32x4 rsrc, uint32_t base_off) const {
 #pragma unroll
