@@ -9,10 +9,11 @@
 //    a lane holds ONE query (column lane%32) and 16 keys per 32-key block: the row max
 //    is an in-register max plus one v_permlane32_swap between the two lane halves, and
 //    P^T converts in place into the B operand of O^T += V^T . P^T (no data movement).
-//  * K and V tiles (BN = 64 keys at D = 64, 32 at D = 128: 8 KB each of K and V either
-//    way) go global -> LDS with direct loads (global_load_lds_dwordx4,
-//    no register staging) into a ring of NSTAGE buffers: loads run NSTAGE-1 tiles ahead
-//    of the MFMAs, so their latency is hidden even at low occupancy. K is read row-major, V with the transposing
+//  * K and V tiles (BN = 32 keys: 4 KB each at D = 64, 8 KB at D = 128) go global ->
+//    LDS with direct loads (global_load_lds_dwordx4, no register staging) into a ring
+//    of NSTAGE buffers: loads run NSTAGE-1 tiles ahead of the MFMAs. The small tiles
+//    keep the LDS ring and the S / P registers small enough for 3 workgroups per CU at
+//    D = 64 and 2 at D = 128. K is read row-major, V with the transposing
 //    ds_read_b64_tr_b16 (the PV operand needs keys along K); both tiles are XOR-swizzled
 //    so that either read pattern is bank-conflict free (tiles.h).
 //  * The workgroup streams the union of its waves' key ranges
@@ -59,7 +60,7 @@ struct FwdParams {
 };
 
 template <typename DT, int D, int MODE>
-__global__ void __launch_bounds__(256, 2) fwd_kernel(const FwdParams p) {
+__global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const FwdParams p) {
     typedef typename DT::vec8 vec8;
     constexpr int BN = fwd_bn(D);           // keys per tile
     constexpr int NRB = BN / 32;            // 32-key row blocks of S^T per tile
