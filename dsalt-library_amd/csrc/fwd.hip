@@ -4,7 +4,8 @@
 // _train_fwd_kernel (dsalt/kernels/dsalt_triton_train.py:74-214); the landmark K/V
 // gather of _build_landmark_kv (dsalt/kernels/selectors.py:137-159) is done in-kernel.
 //
-// Design (one workgroup = 4 waves = 128 consecutive queries of one (sequence, head)):
+// Design (one workgroup = fwd_waves(D) waves of 32 consecutive queries each, of one
+// (sequence, head)):
 //  * Each wave owns 32 queries and computes S^T = K . Q^T with v_mfma_f32_32x32x16, so
 //    a lane holds ONE query (column lane%32) and 16 keys per 32-key block: the row max
 //    is an in-register max plus one v_permlane32_swap between the two lane halves, and
@@ -60,19 +61,22 @@ struct FwdParams {
 };
 
 template <typename DT, int D, int MODE>
-__global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const FwdParams p) {
+__global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_kernel(const FwdParams p) {
     typedef typename DT::vec8 vec8;
+    constexpr int NW = fwd_waves(D);        // waves per workgroup
+    constexpr int BM = 32 * NW;             // queries per workgroup
+    constexpr int NT = 64 * NW;             // threads per workgroup
     constexpr int BN = fwd_bn(D);           // keys per tile
     constexpr int NRB = BN / 32;            // 32-key row blocks of S^T per tile
     constexpr int KS = D / 16;              // MFMA k-steps over the head dim
     constexpr int ND = D / 32;              // 32-row blocks of O^T
-    typedef TileN<D, BN> Tile;
+    typedef TileN<D, BN, NW> Tile;
     constexpr int TB = Tile::BYTES;
-    constexpr int NSTAGE = 4;                          // LDS ring depth (tiles)
+    constexpr int NSTAGE = fwd_stages(D);              // LDS ring depth (tiles)
     constexpr int LPT = 2 * Tile::LOADS_PER_WAVE;      // load instructions per tile per wave
 
     __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][K, V]
-    __shared__ int s_red[4][2];
+    __shared__ int s_red[NW][2];
     __shared__ int s_ltmin[DSALT_MAX_K_LMK / BN];  // smallest position in each landmark tile
     extern __shared__ int s_dyn[];
     int *s_lpos = s_dyn;                                          // INT_MAX: empty slot
@@ -91,12 +95,12 @@ __global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const F
     head_rank(blockIdx.x, p.grid, p.n_heads, p.n_qblk, head, rank);
     if (head >= p.n_heads) return;
     int seq, blk, seq_start, seq_len;
-    if (!find_block_desc(p.cu, p.num_seqs, rank, p.n_qblk, kFwdBM, lane, seq, blk, seq_start, seq_len)) return;
-    const int wq0 = blk * kFwdBM + wave * 32;  // first query of this wave
+    if (!find_block_desc(p.cu, p.num_seqs, rank, p.n_qblk, BM, lane, seq, blk, seq_start, seq_len)) return;
+    const int wq0 = blk * BM + wave * 32;      // first query of this wave
     const int i = wq0 + ql;                    // query offset inside the sequence
     const bool qvalid = i < seq_len;
     const int64_t tok_i = (int64_t)seq_start + i;
-    const int ghi = min(blk * kFwdBM + kFwdBM - 1, seq_len - 1);  // last query of the workgroup
+    const int ghi = min(blk * BM + BM - 1, seq_len - 1);  // last query of the workgroup
 
     // ---- tile staging: direct global -> LDS loads ----------------------------------------
     // Band tiles run from the diagonal down: tile t holds keys ghi-BN+1-BN*t .. ghi-BN*t, so
@@ -108,13 +112,14 @@ __global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const F
     const uint32_t kst = (uint32_t)p.k_st * 2u, vst = (uint32_t)p.v_st * 2u;  // row strides (bytes)
     const i32x4 krs = buffer_rsrc(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh, (uint32_t)seq_len * kst);
     const i32x4 vrs = buffer_rsrc(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh, (uint32_t)seq_len * vst);
-    const TileLanes<D, kSwzRow, BN> klanes(wave, lane, kst);
-    const TileLanes<D, kSwzTr, BN> vlanes(wave, lane, vst);
+    const TileLanes<D, kSwzRow, BN, NW> klanes(wave, lane, kst);
+    const TileLanes<D, kSwzTr, BN, NW> vlanes(wave, lane, vst);
     const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
     auto band_key0 = [&](int t) { return ghi - (BN - 1) - t * BN; };
+    auto stage_of = [](int t) { return t % NSTAGE; };  // t >= 0, wave-uniform
     auto issue_band = [&](int t) {
         const int key0 = band_key0(t);
-        const uint32_t kl = tiles_lds + (t & (NSTAGE - 1)) * (2 * TB);
+        const uint32_t kl = tiles_lds + stage_of(t) * (2 * TB);
         klanes.load_band(kl, wave, krs, (uint32_t)key0 * kst);  // wraps when key0 < 0
         vlanes.load_band(kl + TB, wave, vrs, (uint32_t)key0 * vst);
     };
@@ -130,16 +135,16 @@ __global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const F
         for (int s = 0; s < KS; ++s) qv[s] = bitcast<vec8>(*reinterpret_cast<const uint4 *>(qp + s * 16));
     }
     const float wraw = p.w[(qvalid ? tok_i : (int64_t)seq_start + seq_len - 1) * p.w_st];
-    // landmark slots s = tid + 256 j (k_pad <= DSALT_MAX_K_LMK = 4 * 256)
-    constexpr int LMK_PER_THREAD = DSALT_MAX_K_LMK / 256;
+    // landmark slots s = tid + NT j (k_pad <= DSALT_MAX_K_LMK)
+    constexpr int LMK_PER_THREAD = DSALT_MAX_K_LMK / NT;
     int64_t lpp[LMK_PER_THREAD];
     float lbb[LMK_PER_THREAD];
 #pragma unroll
     for (int j = 0; j < LMK_PER_THREAD; ++j) {
         lpp[j] = -1;
         lbb[j] = 0.f;
-        if (256 * j < p.k_lmk) {  // wave-uniform
-            const int s = min(tid + 256 * j, p.k_lmk - 1);
+        if (NT * j < p.k_lmk) {  // wave-uniform
+            const int s = min(tid + NT * j, p.k_lmk - 1);
             lpp[j] = p.lmk_pos[head * p.lp_sh + seq * p.lp_ss + s * p.lp_sk];
             if (p.lmk_bias) lbb[j] = p.lmk_bias[head * p.lb_sh + seq * p.lb_ss + s * p.lb_sk];
         }
@@ -189,12 +194,12 @@ __global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const F
     const int wchi = wq0;                        // first query of the wave
 
     // ---- landmark slots -> LDS (invalid / out-of-sequence slots become INT_MAX) --------
-    // k_pad is a multiple of 64: slot block j of wave w (64 slots) is landmark tile 4j + w
-    // when BN = 64, tiles 8j + 2w and 8j + 2w + 1 when BN = 32.
+    // k_pad is a multiple of 64: slot block j of wave w (64 slots from s = 64 (NW j + w))
+    // is landmark tile s / 64 when BN = 64, tiles s / 32 and s / 32 + 1 when BN = 32.
 #pragma unroll
     for (int j = 0; j < LMK_PER_THREAD; ++j) {
-        const int s = tid + 256 * j;
-        if (256 * j < p.k_pad) {  // wave-uniform (k_pad is a multiple of 64)
+        const int s = tid + NT * j;
+        if (NT * j < p.k_pad) {  // wave-uniform (k_pad is a multiple of 64)
             if (s < p.k_pad) {
                 const bool ok = s < p.k_lmk && lpp[j] >= 0 && lpp[j] < seq_len;
                 const int pos = ok ? (int)lpp[j] : INT_MAX;
@@ -221,8 +226,12 @@ __global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const F
     }
     // LDS writes visible to the workgroup; the tile loads stay in flight
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    const int glo = min(min(s_red[0][0], s_red[1][0]), min(s_red[2][0], s_red[3][0]));
-    const int gpmax = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
+    int glo = s_red[0][0], gpmax = s_red[0][1];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+        glo = min(glo, s_red[w][0]);
+        gpmax = max(gpmax, s_red[w][1]);
+    }
     // landmark tiles holding at least one position admissible for the workgroup
     const int n_lt = p.k_pad / BN;
     const uint64_t lmask = __ballot(lane < n_lt && s_ltmin[lane < n_lt ? lane : 0] <= gpmax);
@@ -239,7 +248,7 @@ __global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const F
             issue_band(t);
         } else {
             const int *lrow = s_lrow + lmk_tile(t) * BN;
-            const uint32_t kl = tiles_lds + (t & (NSTAGE - 1)) * (2 * TB);
+            const uint32_t kl = tiles_lds + stage_of(t) * (2 * TB);
             klanes.load_gather(kl, wave, krs, kst, lrow);
             vlanes.load_gather(kl + TB, wave, vrs, vst, lrow);
         }
@@ -394,8 +403,9 @@ __global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const F
     // and t+3 (in flight); tile t+3 reuses the stage of tile t-1, whose V every wave
     // finished reading before the barrier that ended iteration t-1. Tiles outside a
     // wave's key range are fully masked (P = 0) rather than skipped, which keeps the
-    // iteration branch-free. nt >= NSTAGE - 1 = 3, and tiles 0..2 were issued during the
-    // setup. The last iteration computes S of a tile that does not exist (stale LDS
+    // iteration branch-free. nt >= NSTAGE - 1, and tiles 0 .. NSTAGE-2 were issued during
+    // the setup. With NSTAGE = 3, tile t+2 is issued at the start of iteration t and must
+    // have landed at its end. The last iteration computes S of a tile that does not exist (stale LDS
     // stage) and ignores it.
     // MFMAs and operand reads of the two parts of an iteration, and the VALU instructions
     // placed after each MFMA (part A: exp / sum / pack, ~56 per row block; part B: masks
@@ -406,7 +416,7 @@ __global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const F
     auto step = [&](int t, f32x16 (&cur)[NRB], f32x16 (&nxt)[NRB]) {
         if (t + NSTAGE - 1 < nt) issue_tile(t + NSTAGE - 1);
         uint32_t pk[NRB][8];
-        qk_tile((t + 1) & (NSTAGE - 1), nxt);
+        qk_tile(stage_of(t + 1), nxt);
         exp_pack(cur, pk);
         __builtin_amdgcn_sched_group_barrier(0x100, NQK, 0);  // K operand reads
         __builtin_amdgcn_sched_group_barrier(0x402, 16, 0);   // VALU / transcendental
@@ -423,7 +433,7 @@ __global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const F
         asm volatile("" : "+v"(lsum0), "+v"(lsum1));
         const bool more = t + 1 < nt;
         if (more) adjust(t + 1, nxt);
-        pv(pk, t & (NSTAGE - 1));
+        pv(pk, stage_of(t));
         const float tmax = mask_max(t + 1, nxt);
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * NPV, 1);  // V operand reads
         __builtin_amdgcn_sched_group_barrier(0x002, 12, 1);       // VALU
@@ -433,11 +443,11 @@ __global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const F
             __builtin_amdgcn_sched_group_barrier(0x002, VALU_B, 1);  // VALU
         }
         rescale(more ? tmax : -INFINITY);
-        if (t + NSTAGE - 1 < nt) tile_barrier<LPT>();
+        if (t + NSTAGE - 1 < nt) tile_barrier<(NSTAGE - 3) * LPT>();
         else tile_barrier<0>();
     };
     f32x16 sA[NRB], sB[NRB];
-    tile_barrier<LPT>();  // tiles 0 and 1 landed (tile 2 may be in flight)
+    tile_barrier<(NSTAGE - 3) * LPT>();  // tiles 0 and 1 landed (tile 2 may be in flight)
     qk_tile(0, sA);
     adjust(0, sA);
     rescale(mask_max(0, sA));
@@ -476,7 +486,7 @@ __global__ void __launch_bounds__(256, fwd_waves_per_simd(D)) fwd_kernel(const F
 
 template <typename DT, int D, int MODE>
 hipError_t launch_typed(const FwdParams &p, size_t dyn, hipStream_t stream) {
-    hipLaunchKernelGGL((fwd_kernel<DT, D, MODE>), dim3(p.grid), dim3(256), dyn, stream, p);
+    hipLaunchKernelGGL((fwd_kernel<DT, D, MODE>), dim3(p.grid), dim3(64 * fwd_waves(D)), dyn, stream, p);
     return hipGetLastError();
 }
 
@@ -517,7 +527,7 @@ hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream) {
     p.n_heads = a.n_heads;
     p.k_lmk = a.k_lmk;
     p.k_pad = (a.k_lmk + kFwdBN - 1) / kFwdBN * kFwdBN;
-    p.n_qblk = block_upper_bound(a.total_len, a.num_seqs, kFwdBM);
+    p.n_qblk = block_upper_bound(a.total_len, a.num_seqs, fwd_bm(a.head_dim));
     const int64_t blocks = (int64_t)p.n_qblk * a.n_heads;
     p.grid = (int)((blocks + 7) / 8 * 8);
     p.q_sign = a.scale < 0.f ? 0x80008000u : 0u;

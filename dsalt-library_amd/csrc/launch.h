@@ -7,16 +7,20 @@
 
 namespace dsalt {
 
-// Forward: one workgroup of 4 waves owns kFwdBM consecutive queries of one
-// (sequence, head); each wave owns 32 of them. Key tiles hold fwd_bn(D) = 32 keys (a
-// 4-stage ring of K and V tiles is 32 KB of LDS at D = 64, 64 KB at D = 128), and the
-// kernel runs fwd_waves_per_simd(D) waves per SIMD (3 at D = 64, 2 at D = 128). The
-// kernel also supports 64-key tiles. Landmark slots are padded to a multiple of
-// kFwdBN = 64, which every tile size divides.
-constexpr int kFwdBM = 128;
+// Forward: one workgroup of fwd_waves(D) waves owns fwd_bm(D) = 32 * fwd_waves(D)
+// consecutive queries of one (sequence, head); each wave owns 32 of them. Key tiles
+// hold fwd_bn(D) = 32 keys (a 4-stage ring of K and V tiles is 32 KB of LDS at D = 64,
+// 64 KB at D = 128), and the kernel runs fwd_waves_per_simd(D) waves per SIMD. The
+// kernel also supports 64-key tiles and 4-wave workgroups. Landmark slots are padded
+// to a multiple of kFwdBN = 64, which every tile size divides. kFwdBM is the smallest
+// block size (size checks).
 constexpr int kFwdBN = 64;
 constexpr int fwd_bn(int) { return 32; }
+constexpr int fwd_waves(int head_dim) { return head_dim == 64 ? 2 : 4; }
+constexpr int fwd_bm(int head_dim) { return 32 * fwd_waves(head_dim); }
+constexpr int kFwdBM = 64;
 constexpr int fwd_waves_per_simd(int head_dim) { return head_dim == 64 ? 3 : 2; }
+constexpr int fwd_stages(int head_dim) { return head_dim == 64 ? 3 : 4; }  // LDS ring depth
 
 hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream);
 hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream);

@@ -27,13 +27,13 @@ __device__ __forceinline__ int tile_swz(int row) {
     return SWZ == kSwzRow ? (row & 7) : ((row & 3) << 1);
 }
 
-template <int D, int ROWS = 64>
+template <int D, int ROWS = 64, int NW = 4>
 struct TileN {
-    static constexpr int CPR = D / 8;                        // 16-byte chunks per row
-    static constexpr int ROWB = D * 2;                       // bytes per row
-    static constexpr int BYTES = ROWS * ROWB;                // bytes per tile
-    static constexpr int LOADS_PER_WAVE = ROWS * CPR / 256;  // 64-lane load instructions per wave
-    static_assert(ROWS * CPR % 256 == 0, "4 waves x 64 lanes must cover the tile's 16-byte chunks");
+    static constexpr int CPR = D / 8;                              // 16-byte chunks per row
+    static constexpr int ROWB = D * 2;                             // bytes per row
+    static constexpr int BYTES = ROWS * ROWB;                      // bytes per tile
+    static constexpr int LOADS_PER_WAVE = ROWS * CPR / (64 * NW);  // load instructions per wave
+    static_assert(ROWS * CPR % (64 * NW) == 0, "NW waves x 64 lanes must cover the tile's 16-byte chunks");
 };
 template <int D>
 using Tile64 = TileN<D, 64>;
@@ -64,14 +64,14 @@ __device__ __forceinline__ void dma16(uint32_t voff, i32x4 rsrc, uint32_t lds) {
     asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
 }
 
-// This wave's share of the direct loads of one tile (4 waves cover the tile): LPW load
+// This wave's share of the direct loads of one tile (NW waves cover the tile): LPW load
 // instructions per tile, counted by vmcnt. Physical chunk slot g holds logical chunk
 // (g % CPR) ^ swz(row) of tile row g / CPR. The per-lane parts (tile row, byte offset of
 // the row and chunk for a given row stride) are computed once; a band tile then costs
 // one add per load, a gathered tile one multiply-add.
-template <int D, int SWZ, int ROWS = 64>
+template <int D, int SWZ, int ROWS = 64, int NW = 4>
 struct TileLanes {
-    static constexpr int CPR = D / 8, LPW = TileN<D, ROWS>::LOADS_PER_WAVE;
+    static constexpr int CPR = D / 8, LPW = TileN<D, ROWS, NW>::LOADS_PER_WAVE;
     int row[LPW];
     uint32_t chunk_off[LPW];  // byte offset of the lane's chunk inside its row
     uint32_t lane_off[LPW];   // row * stride + chunk_off
