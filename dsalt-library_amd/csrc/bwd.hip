@@ -39,8 +39,12 @@ namespace {
 
 constexpr int kPad8 = 8;  // row-major tile row padding (halves): conflict-free b128 reads
 constexpr int kPad4 = 4;  // transposed tile row padding (halves): conflict-free b64 reads
-constexpr int kBM = 128;  // queries (dq) / keys (kv) per workgroup
-constexpr int kTN = 64;   // keys per tile (dq) / queries per tile (kv, lmk_kv)
+constexpr int kBM = 128;    // keys per kv workgroup
+constexpr int kTN = 64;     // queries per tile (kv, lmk_kv)
+constexpr int kDqW = 2;     // waves per dq workgroup
+constexpr int kDqBM = 64;   // queries per dq workgroup (32 per wave)
+constexpr int kDqBN = 32;   // keys per dq tile
+constexpr int kDqStages = 3;  // dq LDS ring depth
 constexpr int kLC = 512;  // queries per lmk_kv chunk (chunks are numbered like query blocks)
 
 enum { kCoreTile = 0, kEdgeTile = 1, kLmkTile = 2 };  // tile kinds of the dq loop phases
@@ -71,14 +75,14 @@ struct BwdParams {
     void *dq, *dk, *dv;  // gradient outputs: fp32 if grad_f32, else the compute dtype
     float *d_bias, *d_w;
     float *ws_qrec;          // per-query records [H][kRecFields][T], written by bwd_dq_kernel
-    int *ws_minlo;           // [n_qblk]
+    int *ws_minlo;           // [n_dqblk]: smallest band start of each dq query block
     float *ws_dwh;           // [T*H] or null
     float *ws_ldk, *ws_ldv;  // landmark dK/dV partials [H][n_lchunk][k_pad][D] or null
     float *ws_ldb;           // landmark d_bias partials [H][n_lchunk][k_pad] or null
     int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, do_st, do_sh, lse_st, lse_sh, w_st;
     int64_t lp_sh, lp_ss, lp_sk, lb_sh, lb_ss, lb_sk;
     int64_t dq_st, dq_sh, dk_st, dk_sh, dv_st, dv_sh;
-    int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid_q, n_lgrp, n_lchunk, grad_f32, o_f32;
+    int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid_q, n_dqblk, grid_dq, n_lgrp, n_lchunk, grad_f32, o_f32;
     float scale, scale_log2, inv_tau, win_edge;
     float inv_c2;  // 1 / scale_log2: log2-unit bias -> raw q.k units
 };
@@ -127,22 +131,26 @@ __device__ __forceinline__ void pack_block(const f32x16 &x, uint32_t (&pk)[8]) {
 // ==================================================================================
 // dq: query-parallel dQ (band + landmarks) and per-head soft-edge d_w~
 // ==================================================================================
-// The forward's structure: one workgroup = 4 waves x 32 queries of one (sequence, head);
-// K and V tiles of 64 keys stream through a 4-stage LDS ring by direct global->LDS loads
-// (band tiles from the diagonal down, then the gathered landmark tiles). Per tile a wave
+// The forward's structure: one workgroup = kDqW waves x 32 queries of one (sequence,
+// head); K and V tiles of kDqBN keys stream through a kDqStages-deep LDS ring by direct
+// global->LDS loads (band tiles from the diagonal down, then the gathered landmark
+// tiles). Small workgroups and tiles keep the LDS ring (24 KB at D = 64) and the
+// registers small enough for 3 workgroups per SIMD set at D = 64. Per tile a wave
 // computes S^T = K.Q^T and dP^T = V.dO^T (lane = query column), P = 2^(S c + bias - lse2)
 // on admitted pairs, dS = P (dP - Delta), and dQ^T += K^T.dS^T with K read transposed.
 template <typename DT, int D, int MODE>
-__global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
+__global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(const BwdParams p) {
     typedef typename DT::vec8 vec8;
-    constexpr int BN = kTN;
+    constexpr int NW = kDqW, BM = kDqBM, NT = 64 * NW;
+    constexpr int BN = kDqBN, NRB = BN / 32;
     constexpr int KS = D / 16, ND = D / 32;
-    constexpr int TB = Tile64<D>::BYTES;
-    constexpr int NSTAGE = 4;
-    constexpr int LPT = 2 * Tile64<D>::LOADS_PER_WAVE;
+    typedef TileN<D, BN, NW> Tile;
+    constexpr int TB = Tile::BYTES;
+    constexpr int NSTAGE = kDqStages;
+    constexpr int LPT = 2 * Tile::LOADS_PER_WAVE;
 
     __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][K, V], both row-swizzled
-    __shared__ int s_red[4][2];
+    __shared__ int s_red[NW][2];
     __shared__ int s_ltmin[DSALT_MAX_K_LMK / BN];
     extern __shared__ int s_dyn[];
     int *s_lpos = s_dyn;                                          // INT_MAX: empty slot
@@ -151,29 +159,30 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
-    const int logical = xcd_remap(blockIdx.x, p.grid_q);
-    const int head = logical / p.n_qblk;
+    const int logical = xcd_remap(blockIdx.x, p.grid_dq);
+    const int head = logical / p.n_dqblk;
     if (head >= p.n_heads) return;
     int seq, blk, seq_start, seq_len;
-    const int target = p.n_qblk - 1 - (logical - head * p.n_qblk);
-    if (!find_block(p.cu, p.num_seqs, target, kBM, lane, seq, blk, seq_start, seq_len)) return;
-    const int wq0 = blk * kBM + wave * 32;
+    const int target = p.n_dqblk - 1 - (logical - head * p.n_dqblk);
+    if (!find_block(p.cu, p.num_seqs, target, BM, lane, seq, blk, seq_start, seq_len)) return;
+    const int wq0 = blk * BM + wave * 32;
     const int i = wq0 + ql;
     const bool qvalid = i < seq_len;
     const int64_t tok_i = (int64_t)seq_start + i;
-    const int ghi = min(blk * kBM + kBM - 1, seq_len - 1);
+    const int ghi = min(blk * BM + BM - 1, seq_len - 1);
 
     // ---- tile staging (band tiles from the diagonal down, then landmark tiles) ---------
     const uint32_t kst = (uint32_t)p.k_st * 2u, vst = (uint32_t)p.v_st * 2u;
     const i32x4 krs = buffer_rsrc(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh, (uint32_t)seq_len * kst);
     const i32x4 vrs = buffer_rsrc(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh, (uint32_t)seq_len * vst);
-    const TileLanes<D, kSwzRow> klanes(wave, lane, kst);
-    const TileLanes<D, kSwzRow> vlanes(wave, lane, vst);
+    const TileLanes<D, kSwzRow, BN, NW> klanes(wave, lane, kst);
+    const TileLanes<D, kSwzRow, BN, NW> vlanes(wave, lane, vst);
     const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
     auto band_key0 = [&](int t) { return ghi - (BN - 1) - t * BN; };
+    auto stage_of = [](int t) { return t % NSTAGE; };  // t >= 0, wave-uniform
     auto issue_band = [&](int t) {
         const int key0 = band_key0(t);
-        const uint32_t kl = tiles_lds + (t & (NSTAGE - 1)) * (2 * TB);
+        const uint32_t kl = tiles_lds + stage_of(t) * (2 * TB);
         klanes.load_band(kl, wave, krs, (uint32_t)key0 * kst);  // wraps when key0 < 0
         vlanes.load_band(kl + TB, wave, vrs, (uint32_t)key0 * vst);
     };
@@ -252,7 +261,7 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     const int whi = min(wq0 + 31, seq_len - 1);
     const int wchi = wq0;
 
-    for (int s = tid; s < p.k_pad; s += 256) {
+    for (int s = tid; s < p.k_pad; s += NT) {  // wave-uniform: k_pad is a multiple of 64
         int pos = INT_MAX;
         float b = 0.f;
         if (s < p.k_lmk) {
@@ -265,16 +274,30 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
         s_lpos[s] = pos;
         s_lbias[s] = b;
         s_lrow[s] = pos == INT_MAX ? 0 : pos;
-        const int tmin = wave_min_u(pos);
-        if (lane == 0) s_ltmin[s >> 6] = tmin;
+        // smallest position of each landmark tile (a wave holds 64 consecutive slots)
+        if (BN == 64) {
+            const int tmin = wave_min_u(pos);
+            if (lane == 0) s_ltmin[s >> 6] = tmin;
+        } else {
+            const int tlo = wave_min_u(hh == 0 ? pos : INT_MAX);
+            const int thi = wave_min_u(hh == 1 ? pos : INT_MAX);
+            if (lane == 0) {
+                s_ltmin[s >> 5] = tlo;
+                s_ltmin[(s >> 5) + 1] = thi;
+            }
+        }
     }
     if (lane == 0) {
         s_red[wave][0] = wlo;
         s_red[wave][1] = wpmax;
     }
     __syncthreads();
-    const int glo = min(min(s_red[0][0], s_red[1][0]), min(s_red[2][0], s_red[3][0]));
-    const int gpmax = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
+    int glo = s_red[0][0], gpmax = s_red[0][1];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+        glo = min(glo, s_red[w][0]);
+        gpmax = max(gpmax, s_red[w][1]);
+    }
     if (head == 0 && tid == 0) p.ws_minlo[target] = glo;  // bounds the query scan of the kv pass
     const int n_lt = p.k_pad / BN;
     const uint64_t lmask = __ballot(lane < n_lt && s_ltmin[lane < n_lt ? lane : 0] <= gpmax);
@@ -290,7 +313,7 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
             issue_band(t);
         } else {
             const int *lrow = s_lrow + lmk_tile(t) * BN;
-            const uint32_t kl = tiles_lds + (t & (NSTAGE - 1)) * (2 * TB);
+            const uint32_t kl = tiles_lds + stage_of(t) * (2 * TB);
             klanes.load_gather(kl, wave, krs, kst, lrow);
             vlanes.load_gather(kl + TB, wave, vrs, vst, lrow);
         }
@@ -306,10 +329,10 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
 
     // dS = P (dP - Delta) from shifted logits x (log2 units incl. biases, -inf where not
     // admitted), then dQ^T += K^T . dS^T with K of stage `stage` read transposed
-    auto dq_mfma = [&](const uint32_t (&pk)[2][8], int stage) {
+    auto dq_mfma = [&](const uint32_t (&pk)[NRB][8], int stage) {
         const char *ktile = s_tiles[stage][0];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
+        for (int kk = 0; kk < 2 * NRB; ++kk) {
             const int rb = kk >> 1, g = kk & 1;
             const vec8 b = bitcast<vec8>(
                 make_uint4(pk[rb][g * 4 + 0], pk[rb][g * 4 + 1], pk[rb][g * 4 + 2], pk[rb][g * 4 + 3]));
@@ -320,10 +343,10 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
             }
         }
     };
-    auto ds_dq = [&](f32x16 (&x)[2], const f32x16 (&pacc)[2], int stage) {
-        uint32_t pk[2][8];
+    auto ds_dq = [&](f32x16 (&x)[NRB], const f32x16 (&pacc)[NRB], int stage) {
+        uint32_t pk[NRB][8];
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
+        for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float p0 = fast_exp2(x[rb][2 * j] - lse2), p1 = fast_exp2(x[rb][2 * j + 1] - lse2);
@@ -341,17 +364,17 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
     auto tile = [&](int t, auto kind) {
         constexpr int KIND = decltype(kind)::value;
         if (t + NSTAGE - 1 < nt) issue_tile(t + NSTAGE - 1);
-        const int stage = t & (NSTAGE - 1);
+        const int stage = stage_of(t);
         const int tb = KIND != kLmkTile ? band_key0(t) : 0;
         const int lt = KIND == kLmkTile ? lmk_tile(t) : 0;
         const bool active = KIND != kLmkTile ? ((tb <= whi) && (tb + BN - 1 >= wlo)) : (s_ltmin[lt] <= wpmax);
         if (active) {
-            // S^T = K . Q^T and dP^T = V . dO^T (64 keys x 32 queries)
-            f32x16 sacc[2], pacc[2];
+            // S^T = K . Q^T and dP^T = V . dO^T (BN keys x 32 queries)
+            f32x16 sacc[NRB], pacc[NRB];
             const char *ktile = s_tiles[stage][0];
             const char *vtile = s_tiles[stage][1];
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
+            for (int rb = 0; rb < NRB; ++rb) {
                 f32x16 a0, a1;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) a0[r] = a1[r] = 0.f;
@@ -366,10 +389,10 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
                 pacc[rb] = a1;
             }
             // logits in log2 units with biases, -inf where not admitted
-            f32x16 x[2];
+            f32x16 x[NRB];
             if constexpr (KIND == kLmkTile) {
 #pragma unroll
-                for (int rb = 0; rb < 2; ++rb)
+                for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const int slot = lt * BN + rb * 32 + g * 8 + hh * 4;
@@ -392,9 +415,9 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
                     // edge keys; the edge terms are only formed where they are used
                     // (exp(-z) may overflow elsewhere)
                     const int Bc = corelo - tb - hh * 4;
-                    uint32_t pk[2][8];
+                    uint32_t pk[NRB][8];
 #pragma unroll
-                    for (int rb = 0; rb < 2; ++rb)
+                    for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
                         for (int j = 0; j < 8; ++j) {
                             float ds2[2];
@@ -420,13 +443,13 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
                 } else {
                     const uint32_t keep = rows_le(A) & ~rows_le(B - 1);
 #pragma unroll
-                    for (int rb = 0; rb < 2; ++rb)
+                    for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
                         for (int r = 0; r < 16; ++r) x[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r] * c);
                 }
             }
             if constexpr (KIND != kEdgeTile) ds_dq(x, pacc, stage);
-            if constexpr (KIND != kEdgeTile) {
+            if constexpr (KIND != kEdgeTile && NRB == 2) {
                 __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // K/V reads, lower half
                 __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // S^T/dP^T MFMAs, lower half
                 __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // K/V reads, upper half
@@ -447,11 +470,12 @@ __global__ void __launch_bounds__(256) bwd_dq_kernel(const BwdParams p) {
         if (t + NSTAGE - 1 < nt) tile_barrier<(NSTAGE - 2) * LPT>();
         else tile_barrier<0>();
     };
-    // band tiles inside every row's core: tile t holds keys ghi-63-64t .. ghi-64t, all
-    // >= wclo for t <= (ghi-63-wclo)/64
-    const int n_core = MODE == kSoft ? min(nb, (ghi - 63 - wclo >= 0) ? (ghi - 63 - wclo) / BN + 1 : 0) : nb;
+    // band tiles inside every row's core: tile t holds keys ghi-BN+1-BN*t .. ghi-BN*t,
+    // all >= wclo for t <= (ghi-BN+1-wclo)/BN
+    const int n_core =
+        MODE == kSoft ? min(nb, (ghi - (BN - 1) - wclo >= 0) ? (ghi - (BN - 1) - wclo) / BN + 1 : 0) : nb;
 
-    tile_barrier<LPT>();  // tiles 0 and 1 landed (tile 2 may be in flight)
+    tile_barrier<(NSTAGE - 2) * LPT>();  // tile 0 landed (later ones may be in flight)
     int t = 0;
     for (; t < n_core; ++t) tile(t, std::integral_constant<int, kCoreTile>());
     if constexpr (MODE == kSoft)
@@ -492,7 +516,7 @@ __global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
 
-    int head, seq, seq_start, seq_len, kblk = 0, gbase = 0, q_begin, q_end, slot = 0, sbw = 0, kw = 0, lcid = 0;
+    int head, seq, seq_start, seq_len, kblk = 0, q_begin, q_end, slot = 0, sbw = 0, kw = 0, lcid = 0;
     int key = INT_MAX;  // this lane's key position in the sequence (INT_MAX: none)
     float kbias2 = 0.f;
     if (!LMK) {
@@ -501,7 +525,6 @@ __global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
         if (head >= p.n_heads) return;
         const int target = p.n_qblk - 1 - (logical - head * p.n_qblk);
         if (!find_block(p.cu, p.num_seqs, target, kBM, lane, seq, kblk, seq_start, seq_len)) return;
-        gbase = target - kblk;
     } else {
         // workgroup = (head, 64-slot group, query chunk); chunk ids follow find_block
         const int per_head = p.n_lgrp * p.n_lchunk;
@@ -521,17 +544,20 @@ __global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
         const int kb = kblk * kBM;
         kw = kb + wave * 32;
         if (kw + ql < seq_len) key = kw + ql;
-        // last 128-query block whose smallest band start reaches this key block
-        const int nbs = (seq_len + kBM - 1) / kBM;
-        int last = kblk;
-        for (int b = kblk + 1 + tid; b < nbs; b += 256)
-            if (p.ws_minlo[gbase + b] <= kb + kBM - 1) last = max(last, b);
+        // last dq query block (kDqBM queries; block ids of the sequence start at
+        // seq_start / kDqBM + seq) whose smallest band start reaches this key block
+        const int dqbase = seq_start / kDqBM + seq;
+        const int nbs = (seq_len + kDqBM - 1) / kDqBM;
+        const int own = (kb + kBM - 1) / kDqBM;  // dq block of the key block's last key
+        int last = own;
+        for (int b = own + 1 + tid; b < nbs; b += 256)
+            if (p.ws_minlo[dqbase + b] <= kb + kBM - 1) last = max(last, b);
         last = wave_max_u(last);
         if (lane == 0) s_misc[wave] = last;
         __syncthreads();
         last = max(max(s_misc[0], s_misc[1]), max(s_misc[2], s_misc[3]));
         q_begin = kb;
-        q_end = min(seq_len, (last + 1) * kBM);
+        q_end = min(seq_len, (last + 1) * kDqBM);
     } else {
         if (slot < p.k_lmk) {
             const int64_t pp = p.lmk_pos[head * p.lp_sh + seq * p.lp_ss + slot * p.lp_sk];
@@ -973,7 +999,7 @@ WsLayout ws_layout(int T, int S, int H, int D, int k) {
     L.qrec = off;
     off += al((size_t)H * kRecFields * T * 4);
     L.minlo = off;
-    off += al((size_t)block_upper_bound(T, S, kBM) * 4);
+    off += al((size_t)block_upper_bound(T, S, kDqBM) * 4);
     L.dwh = off;
     off += al((size_t)T * H * 4);
     const size_t kp = (size_t)((k + 63) / 64 * 64);
@@ -992,7 +1018,7 @@ template <typename DT, int D, int MODE>
 hipError_t launch_typed(const BwdParams &p, hipStream_t stream) {
     // dq writes the per-query records that the key-parallel passes stream
     const size_t dyn = (size_t)p.k_pad * (2 * sizeof(int) + sizeof(float));
-    hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE>), dim3(p.grid_q), dim3(256), dyn, stream, p);
+    hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE>), dim3(p.grid_dq), dim3(64 * kDqW), dyn, stream, p);
     if (p.k_lmk > 0) {
         hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, true>), dim3(p.n_heads * p.n_lgrp * p.n_lchunk), dim3(256),
                            0, stream, p);
@@ -1069,6 +1095,8 @@ hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream) {
     p.n_lchunk = block_upper_bound(a.total_len, a.num_seqs, kLC);
     p.n_qblk = block_upper_bound(a.total_len, a.num_seqs, kBM);
     p.grid_q = (int)(((int64_t)p.n_qblk * a.n_heads + 7) / 8 * 8);
+    p.n_dqblk = block_upper_bound(a.total_len, a.num_seqs, kDqBM);
+    p.grid_dq = (int)(((int64_t)p.n_dqblk * a.n_heads + 7) / 8 * 8);
     p.scale = a.scale;
     p.scale_log2 = a.scale * kLog2e;
     p.inv_c2 = 1.f / p.scale_log2;
