@@ -39,8 +39,13 @@ namespace {
 
 constexpr int kPad8 = 8;  // row-major tile row padding (halves): conflict-free b128 reads
 constexpr int kPad4 = 4;  // transposed tile row padding (halves): conflict-free b64 reads
-constexpr int kBM = 128;    // keys per kv workgroup
-constexpr int kTN = 64;     // queries per tile (kv, lmk_kv)
+// band kv workgroups: waves (32 keys each), queries per tile and LDS ring depth; at
+// D = 128 one 32-query sub-block per tile would need more than 256 VGPRs
+constexpr int kv_waves(int d) { return d == 64 ? 2 : 4; }
+constexpr int kv_bm(int d) { return 32 * kv_waves(d); }  // keys per band kv workgroup
+constexpr int kv_qt(int d) { return d == 64 ? 32 : 64; }
+constexpr int kv_stages(int d) { return d == 64 ? 3 : 4; }
+constexpr int kTN = 64;     // queries per lmk_kv tile
 constexpr int kDqW = 2;     // waves per dq workgroup
 constexpr int kDqBM = 64;   // queries per dq workgroup (32 per wave)
 constexpr int kDqBN = 32;   // keys per dq tile
@@ -493,21 +498,30 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
 // kv (LMK = false): key-parallel band dK/dV;  lmk_kv (LMK = true): landmark dK/dV + d_bias
 // ==================================================================================
 // A wave owns 32 keys (band: consecutive keys; LMK: 32 landmark slots) held in registers
-// as B operands, and streams 64-query tiles of Q, dO and the per-query records through a
-// 4-stage LDS ring (direct global->LDS loads, one barrier per tile). Per 32-query
+// as B operands, and streams tiles of Q, dO and the per-query records through an LDS ring
+// (direct global->LDS loads, one barrier per tile): band workgroups are kv_waves(D)
+// waves with kv_qt(D)-query tiles on a kv_stages(D)-deep ring (2 waves, 32 queries, 3
+// stages = 27 KB at D = 64), lmk_kv workgroups 4 waves with 64-query tiles on a 4-stage
+// ring. Per 32-query
 // sub-block: S = Q.K^T and dP = dO.V^T (lane = key column, registers = query rows),
 // P = 2^(S c + bias - lse2) on admitted pairs, dS = P (dP - Delta), then dV^T += dO^T.P
 // and dK^T += Q^T.dS with Q and dO read transposed.
 template <typename DT, int D, int MODE, bool LMK>
-__global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
+__global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), 2) bwd_kv_kernel(const BwdParams p) {
     typedef typename DT::vec8 vec8;
-    constexpr int QT = kTN;  // queries per tile
+    constexpr int NW = LMK ? 4 : kv_waves(D), NT = 64 * NW;  // waves, threads
+    constexpr int kBM = kv_bm(D);                            // keys per band workgroup
+    constexpr int QT = LMK ? kTN : kv_qt(D);                 // queries per tile
+    constexpr int NSB = QT / 32;                       // 32-query sub-blocks per tile
     constexpr int KS = D / 16, ND = D / 32;
-    constexpr int TB = Tile64<D>::BYTES;
-    constexpr int NSTAGE = 4;
-    constexpr int RB = QT * 4;                                   // bytes of one record field per tile
-    constexpr int LPT = 2 * Tile64<D>::LOADS_PER_WAVE + 2;       // Q, dO, and 2 record fields per wave
-    static_assert(kRecFields == 8, "4 waves x 2 fields");
+    typedef TileN<D, QT, NW> Tile;
+    constexpr int TB = Tile::BYTES;
+    constexpr int NSTAGE = LMK ? 4 : kv_stages(D);
+    constexpr int RB = QT * 4;                         // bytes of one record field per tile
+    constexpr int FPI = 64 / QT;                       // record fields per 64-lane load
+    constexpr int RLW = kRecFields / (FPI * NW);       // record loads per wave per tile
+    constexpr int LPT = 2 * Tile::LOADS_PER_WAVE + RLW;  // Q, dO and record loads per wave
+    static_assert(kRecFields % (FPI * NW) == 0, "record fields split evenly over the waves");
 
     __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][Q, dO], row-swizzled
     __shared__ __align__(16) char s_rec[NSTAGE][kRecFields][RB];
@@ -550,12 +564,13 @@ __global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
         const int nbs = (seq_len + kDqBM - 1) / kDqBM;
         const int own = (kb + kBM - 1) / kDqBM;  // dq block of the key block's last key
         int last = own;
-        for (int b = own + 1 + tid; b < nbs; b += 256)
+        for (int b = own + 1 + tid; b < nbs; b += NT)
             if (p.ws_minlo[dqbase + b] <= kb + kBM - 1) last = max(last, b);
         last = wave_max_u(last);
         if (lane == 0) s_misc[wave] = last;
         __syncthreads();
-        last = max(max(s_misc[0], s_misc[1]), max(s_misc[2], s_misc[3]));
+#pragma unroll
+        for (int w = 0; w < NW; ++w) last = max(last, s_misc[w]);
         q_begin = kb;
         q_end = min(seq_len, (last + 1) * kDqBM);
     } else {
@@ -604,24 +619,28 @@ __global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
     // at or past seq_len get an out-of-range offset (zeros: admit nothing)
     const i32x4 rrs = buffer_rsrc(p.ws_qrec + (size_t)head * kRecFields * p.total_len,
                                   (uint32_t)(kRecFields * p.total_len * 4));
-    const TileLanes<D, kSwzRow> qlanes(wave, lane, qst);
-    const TileLanes<D, kSwzRow> dlanes(wave, lane, dst);
+    const TileLanes<D, kSwzRow, QT, NW> qlanes(wave, lane, qst);
+    const TileLanes<D, kSwzRow, QT, NW> dlanes(wave, lane, dst);
     const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
     const uint32_t rec_lds = lds_addr(&s_rec[0][0][0]);
     const int ntile = (q_end > q_begin) ? (q_end - q_begin + QT - 1) / QT : 0;
+    auto stage_of = [](int t) { return t % NSTAGE; };  // t >= 0, wave-uniform
     auto issue_tile = [&](int t) {
         const int q0 = q_begin + t * QT;
-        const int st = t & (NSTAGE - 1);
+        const int st = stage_of(t);
         const uint32_t tl = tiles_lds + st * (2 * TB);
         qlanes.load_band(tl, wave, qrs, (uint32_t)q0 * qst);
         dlanes.load_band(tl + TB, wave, drs, (uint32_t)q0 * dst);
-        const int q = q0 + lane;
+        // one load covers FPI consecutive fields (lane l: field f0 + l / QT, query l % QT),
+        // which are consecutive in LDS
+        const int q = q0 + lane % QT;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int f = wave * 2 + u;
+        for (int u = 0; u < RLW; ++u) {
+            const int f0 = (wave * RLW + u) * FPI;
+            const int f = f0 + lane / QT;
             const uint32_t off = (q < seq_len) ? (uint32_t)(((size_t)f * p.total_len + seq_start + q) * 4) : 0xFFFFFF00u;
             asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(off), "s"(rrs),
-                         "{m0}"(__builtin_amdgcn_readfirstlane(rec_lds + (st * kRecFields + f) * RB))
+                         "{m0}"(__builtin_amdgcn_readfirstlane(rec_lds + (st * kRecFields + f0) * RB))
                          : "memory");
         }
     };
@@ -679,26 +698,27 @@ __global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
         // are added in place by a wave-uniform branch.
         for (int t = 0; t < ntile; ++t) {
             if (t + NSTAGE - 1 < ntile) issue_tile(t + NSTAGE - 1);
-            const int st = t & (NSTAGE - 1);
+            const int st = stage_of(t);
             const char *qtile = s_tiles[st][0];
             const char *dtile = s_tiles[st][1];
             const int q0 = q_begin + t * QT;
-            bool live[2], edge[2];
+            bool live[NSB], edge[NSB], any = false;
 #pragma unroll
-            for (int sb = 0; sb < 2; ++sb) {
+            for (int sb = 0; sb < NSB; ++sb) {
                 const int qsb = q0 + sb * 32;
                 const int gmin_lo = INT_MAX - *rec_i(st, kRecGLo, sb * 32);
                 const int gmax_clo = INT_MAX - *rec_i(st, kRecGClo, sb * 32);
                 live[sb] = !((qsb >= q_end) || (qsb + 31 < kw) || (gmin_lo > wkmax));
                 edge[sb] = (MODE == kSoft) && live[sb] && (gmax_clo > wkmin);
+                any |= live[sb];
             }
-            if (live[0] | live[1]) {
-                f32x16 sacc[2], pacc[2];
-                sdp_mfma(qtile, dtile, 0, sacc[0], pacc[0]);
-                sdp_mfma(qtile, dtile, 1, sacc[1], pacc[1]);
+            if (any) {
+                f32x16 sacc[NSB], pacc[NSB];
+#pragma unroll
+                for (int sb = 0; sb < NSB; ++sb) sdp_mfma(qtile, dtile, sb, sacc[sb], pacc[sb]);
                 if (MODE == kSoft) {
 #pragma unroll
-                    for (int sb = 0; sb < 2; ++sb) {
+                    for (int sb = 0; sb < NSB; ++sb) {
                         if (!edge[sb]) continue;
                         const int qsb = q0 + sb * 32;
                         const int Cj = (kvalid ? key : INT_MAX / 2) - qsb - hh * 4;
@@ -720,9 +740,9 @@ __global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
                         }
                     }
                 }
-                uint32_t pkp[2][8], pks[2][8];
+                uint32_t pkp[NSB][8], pks[NSB][8];
 #pragma unroll
-                for (int sb = 0; sb < 2; ++sb) {
+                for (int sb = 0; sb < NSB; ++sb) {
                     const int qsb = q0 + sb * 32;
                     const int Cj = (kvalid ? key : INT_MAX / 2) - qsb - hh * 4;  // q >= key <=> cst >= Cj
                     const bool kv_ok = kvalid & live[sb];
@@ -755,8 +775,8 @@ __global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
                         pks[sb][g * 2 + 1] = DT::pack2(ds4[2], ds4[3]);
                     }
                 }
-                kv_mfma(qtile, dtile, 0, pkp[0], pks[0]);
-                kv_mfma(qtile, dtile, 1, pkp[1], pks[1]);
+#pragma unroll
+                for (int sb = 0; sb < NSB; ++sb) kv_mfma(qtile, dtile, sb, pkp[sb], pks[sb]);
             }
             // tile t+1 must have landed; tiles t+2 .. t+NSTAGE-1 may stay in flight
             if (t + NSTAGE - 1 < ntile) tile_barrier<(NSTAGE - 2) * LPT>();
@@ -765,7 +785,7 @@ __global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
     } else {
     for (int t = 0; t < ntile; ++t) {
             if (t + NSTAGE - 1 < ntile) issue_tile(t + NSTAGE - 1);
-            const int st = t & (NSTAGE - 1);
+            const int st = stage_of(t);
             const char *qtile = s_tiles[st][0];
             const char *dtile = s_tiles[st][1];
     #pragma unroll
@@ -933,7 +953,7 @@ __global__ void __launch_bounds__(256, 2) bwd_kv_kernel(const BwdParams p) {
         // order, through LDS (the tile ring is idle after the last barrier)
         float *red = reinterpret_cast<float *>(&s_tiles[0][0][0]);
         constexpr int PER_LANE = 2 * ND * 16 + 1;
-        static_assert(2 * 64 * PER_LANE * 4 <= sizeof(s_tiles), "reduction scratch");
+        static_assert(!LMK || 2 * 64 * PER_LANE * 4 <= sizeof(s_tiles), "reduction scratch");
         const int g = wave >> 1;
         float *mine = red + (size_t)(g * 64 + lane) * PER_LANE;
         if (sbw == 1) {
@@ -1025,7 +1045,7 @@ hipError_t launch_typed(const BwdParams &p, hipStream_t stream) {
         if (p.d_bias)
             hipLaunchKernelGGL(bwd_dbias_kernel, dim3(p.n_heads * p.num_seqs), dim3(64), 0, stream, p);
     }
-    hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false>), dim3(p.grid_q), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false>), dim3(p.grid_q), dim3(64 * kv_waves(D)), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -1093,7 +1113,7 @@ hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream) {
     p.k_pad = (a.k_lmk + 63) / 64 * 64;
     p.n_lgrp = p.k_pad / 64;
     p.n_lchunk = block_upper_bound(a.total_len, a.num_seqs, kLC);
-    p.n_qblk = block_upper_bound(a.total_len, a.num_seqs, kBM);
+    p.n_qblk = block_upper_bound(a.total_len, a.num_seqs, kv_bm(a.head_dim));
     p.grid_q = (int)(((int64_t)p.n_qblk * a.n_heads + 7) / 8 * 8);
     p.n_dqblk = block_upper_bound(a.total_len, a.num_seqs, kDqBM);
     p.grid_dq = (int)(((int64_t)p.n_dqblk * a.n_heads + 7) / 8 * 8);
