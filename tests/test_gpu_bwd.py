@@ -91,6 +91,15 @@ def test_bwd_16bit_gradient_outputs(mode):
              out_dtype=torch.bfloat16)
 
 
+@pytest.mark.parametrize("mode,D,k", [(hip.MODE_SOFT, 64, 1024), (hip.MODE_HARD, 128, 300)],
+                         ids=["soft-d64-k1024", "hard-d128-k300"])
+def test_bwd_many_landmarks(mode, D, k):
+    # landmark slots beyond 64 and up to DSALT_MAX_K_LMK: several slot groups of lmk_kv,
+    # k_pad not a multiple of 64 slots per tile pair, a sequence shorter than k
+    print(f"bwd many landmarks mode={mode} D={D} k={k}", flush=True)
+    run_case(mode, [900, 45, 500], 2, D, k, seed=33, n_min=4, n_max=160)
+
+
 def test_bwd_c3_packing():
     # 8 sequences, lengths numpy.random.seed(2); randint(256, 2049, 8)
     np.random.seed(2)

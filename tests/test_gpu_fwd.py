@@ -303,3 +303,19 @@ def test_fwd_extreme_logits(mode, case, dtype):
     assert torch.isfinite(out).all()
     close(out.cpu(), o_ref, f"extreme {case}")
     lse_close(lse.cpu(), l_ref, f"extreme {case} lse")
+
+
+@pytest.mark.parametrize("mode", [hip.MODE_HARD, hip.MODE_SOFT], ids=["hard", "soft"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("k", [300, 1024])
+def test_fwd_many_landmarks(mode, D, k):
+    """Up to DSALT_MAX_K_LMK landmark slots (k_pad 320: an odd number of 32-slot tiles;
+    1024: 32 landmark tiles), with a sequence shorter than k (slots past its length stay
+    empty)."""
+    lens, H = [1300, 45, 700], 2
+    print(f"fwd many landmarks mode={mode} D={D} k={k}", flush=True)
+    q, kk, v, w, pos, bias, cu = make_inputs(lens, H, D, k, mode, seed=31, n_min=4, n_max=200)
+    out, lse = run_hip(mode, q, kk, v, w, pos, bias, cu)
+    o_ref, l_ref = run_oracle(mode, q, kk, v, w, pos, bias, cu)
+    close(out, o_ref, f"many landmarks k={k}")
+    lse_close(lse, l_ref, f"many landmarks k={k} lse")
