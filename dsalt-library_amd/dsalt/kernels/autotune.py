@@ -9,15 +9,20 @@ from __future__ import annotations
 
 import torch
 
-# forward: 4 waves x 32 queries per workgroup, 64-key tiles, v_mfma_f32_32x32x16
-_GFX950_CONFIG = {"BLOCK_M": 128, "BLOCK_N": 64, "BLOCK_N_BWD": 64, "num_warps": 4, "num_stages": 2}
+# Forward workgroups (the constants of csrc/launch.h): BLOCK_M queries = num_warps waves
+# of 32, BLOCK_N keys per LDS tile, num_stages-deep LDS ring; BLOCK_N_BWD queries per tile
+# of the band dK/dV pass (csrc/bwd.hip). All products are v_mfma_f32_32x32x16.
+_GFX950_CONFIG = {
+    64: {"BLOCK_M": 64, "BLOCK_N": 32, "BLOCK_N_BWD": 32, "num_warps": 2, "num_stages": 3},
+    128: {"BLOCK_M": 128, "BLOCK_N": 32, "BLOCK_N_BWD": 64, "num_warps": 4, "num_stages": 4},
+}
 
 
 def get_tuned_config(head_dim: int, device: torch.device | None = None) -> dict:
     """The fixed gfx950 tile configuration for ``head_dim`` (64 or 128)."""
     if head_dim not in (64, 128):
         raise ValueError(f"head_dim must be 64 or 128, got {head_dim}")
-    return dict(_GFX950_CONFIG)
+    return dict(_GFX950_CONFIG[head_dim])
 
 
 def autotune_blocks(head_dim: int, device: torch.device | None = None, make_runner=None,

@@ -140,3 +140,26 @@ def test_cpu_tensors_raise():
     q = torch.zeros(8, 1, 64, dtype=torch.bfloat16)
     with pytest.raises(hip.DsaltError, match="ROCm GPU"):
         hip.fwd(0, q, q, q, torch.ones(8), None, None, torch.tensor([0, 8], dtype=torch.int32), 0.125)
+
+
+def test_tuned_config_matches_kernel_constants():
+    # the reported tiles are the ones csrc/launch.h and csrc/bwd.hip compile in
+    from dsalt.kernels import autotune_blocks, get_tuned_config
+    here = os.path.dirname(os.path.abspath(__file__))
+    launch = open(os.path.join(here, "..", "dsalt-library_amd", "csrc", "launch.h")).read()
+    bwd = open(os.path.join(here, "..", "dsalt-library_amd", "csrc", "bwd.hip")).read()
+
+    def const_fn(src, name):  # constexpr int name(int d) { return d == 64 ? A : B; }
+        m = re.search(r"constexpr int %s\(int[^)]*\) \{ return (?:\w+ == 64 \? (\d+) : (\d+)|(\d+)); \}" % name, src)
+        assert m, name
+        return (int(m.group(1)), int(m.group(2))) if m.group(1) else (int(m.group(3)),) * 2
+
+    waves, bn, stages, kv_qt = (const_fn(launch, "fwd_waves"), const_fn(launch, "fwd_bn"),
+                                const_fn(launch, "fwd_stages"), const_fn(bwd, "kv_qt"))
+    for i, d in enumerate((64, 128)):
+        cfg = get_tuned_config(d)
+        assert cfg == autotune_blocks(d)
+        assert cfg["num_warps"] == waves[i] and cfg["BLOCK_M"] == 32 * waves[i]
+        assert cfg["BLOCK_N"] == bn[i] and cfg["num_stages"] == stages[i] and cfg["BLOCK_N_BWD"] == kv_qt[i]
+    with pytest.raises(ValueError):
+        get_tuned_config(96)
