@@ -280,6 +280,19 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_
     float mu = 0.f;        // exponent offset: m2, or 0 while m2 is -inf
     float lsum0 = 0.f, lsum1 = 0.f;
     const float c = p.c;
+    // SOFT edge factors: for element slot j (tile row offset cst_j), exp(-z) of the edge
+    // logit z = (w~ - d) / tau splits as E * ec[j] with E = exp((A - w~ - mid) / tau) per
+    // lane and tile and ec[j] = exp((mid - cst_j) / tau) fixed. Every factor stays in the
+    // fp32 range while (win_edge + 1 + 16 NRB) / tau < 80 (edge keys have
+    // 0 <= z < (win_edge + 1) / tau); otherwise each element takes its own exp.
+    constexpr float kEdgeMid = 16.f * NRB - 2.5f;
+    const bool edge_fast = MODE == kSoft && (p.win_edge + 1.f + 16.f * NRB) * p.inv_tau < 80.f;
+    float ec[MODE == kSoft ? 16 * NRB : 1];
+    if constexpr (MODE == kSoft) {
+#pragma unroll
+        for (int j = 0; j < 16 * NRB; ++j)
+            ec[j] = fast_exp2((kEdgeMid - (float)((j >> 4) * 32 + acc_row_const(j & 15))) * p.inv_tau * kLog2e);
+    }
 
     // P = exp2(S * c - mu) of one tile: fp32 row sums (unrounded, as the LSE needs them)
     // and the 16-bit P^T operand. Masked scores are -inf and give 0.
@@ -335,15 +348,28 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_
             const int tb = band_key0(t);
             const int A = i - tb - hh * 4;
             const int Bc = corelo - tb - hh * 4;  // key >= corelo <=> cst >= Bc
+            if (edge_fast) {
+                // log2 sigmoid(z) = -log2(1 + E ec[j]): one v_log per element
+                const float E = fast_exp2(((float)A - wv - kEdgeMid) * p.inv_tau * kLog2e);
 #pragma unroll
-            for (int rb = 0; rb < NRB; ++rb)
+                for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int cst = rb * 32 + acc_row_const(r);
-                    float oms;
-                    const float edge = soft_edge_log2(wv, (float)(A - cst), p.inv_tau, oms);
-                    sacc[rb][r] += (cst < Bc) ? edge * p.inv_c : 0.f;
-                }
+                    for (int r = 0; r < 16; ++r) {
+                        const int cst = rb * 32 + acc_row_const(r);
+                        const float edge = -__builtin_amdgcn_logf(fmaf(E, ec[rb * 16 + r], 1.f));
+                        sacc[rb][r] += (cst < Bc) ? edge * p.inv_c : 0.f;
+                    }
+            } else {
+#pragma unroll
+                for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int cst = rb * 32 + acc_row_const(r);
+                        float oms;
+                        const float edge = soft_edge_log2(wv, (float)(A - cst), p.inv_tau, oms);
+                        sacc[rb][r] += (cst < Bc) ? edge * p.inv_c : 0.f;
+                    }
+            }
         }
     };
     // Band mask of tile t (keys outside [lo, i]; all kept for landmark tiles) applied in

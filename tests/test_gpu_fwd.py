@@ -319,3 +319,19 @@ def test_fwd_many_landmarks(mode, D, k):
     o_ref, l_ref = run_oracle(mode, q, kk, v, w, pos, bias, cu)
     close(out, o_ref, f"many landmarks k={k}")
     lse_close(lse, l_ref, f"many landmarks k={k} lse")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("tau,edge", [(1.0, 4.0), (0.5, 2.5), (0.15, 4.0), (3.0, 9.0)],
+                         ids=["t1-e4", "t0.5-e2.5", "t0.15-e4", "t3-e9"])
+def test_fwd_soft_edge_params(D, tau, edge):
+    """SOFT edge bias log sigmoid((w~ - d) / tau) over tau and win_edge: the factored
+    exp(-z) = E * ec[j] (one log per element) where (win_edge + 1 + 16 NRB) / tau < 80,
+    the per-element exp otherwise (tau = 0.15)."""
+    print(f"fwd soft edge D={D} tau={tau} edge={edge}", flush=True)
+    lens, H, k = [400, 130], 2, 12
+    q, kk, v, w, pos, bias, cu = make_inputs(lens, H, D, k, hip.MODE_SOFT, seed=41, n_min=2, n_max=120)
+    out, lse = run_hip(hip.MODE_SOFT, q, kk, v, w, pos, bias, cu, tau_win=tau, win_edge=edge)
+    o_ref, l_ref = run_oracle(hip.MODE_SOFT, q, kk, v, w, pos, bias, cu, tau_win=tau, win_edge=edge)
+    close(out, o_ref, f"soft edge tau={tau}")
+    lse_close(lse, l_ref, f"soft edge tau={tau} lse")
