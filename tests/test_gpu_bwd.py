@@ -100,6 +100,19 @@ def test_bwd_many_landmarks(mode, D, k):
     run_case(mode, [900, 45, 500], 2, D, k, seed=33, n_min=4, n_max=160)
 
 
+@pytest.mark.parametrize("mode,D", [(hip.MODE_HARD, 64), (hip.MODE_SOFT, 64), (hip.MODE_SOFT, 128)],
+                         ids=["hard-d64", "soft-d64", "soft-d128"])
+def test_bwd_many_sequences(mode, D):
+    # more than 64 sequences (block lookups scan cu_seqlens 64 entries at a time), empty
+    # ones, lengths that cross the 64-query dq blocks and 64 / 128-key kv blocks anywhere
+    rng = np.random.default_rng(17)
+    lens = [int(x) for x in rng.integers(0, 150, size=90)]
+    lens[5] = lens[70] = lens[89] = 0
+    lens[66] = 420
+    print(f"bwd many sequences mode={mode} D={D}", flush=True)
+    run_case(mode, lens, 2, D, 7, seed=17, n_min=2, n_max=60)
+
+
 def test_bwd_c3_packing():
     # 8 sequences, lengths numpy.random.seed(2); randint(256, 2049, 8)
     np.random.seed(2)
