@@ -12,8 +12,9 @@
 // element is produced by exactly one thread, in a fixed order.
 //
 // Kernels, launched in this order on one stream:
-//   dq      query-parallel, 4 waves x 32 queries per workgroup, the forward's tiling (band
-//           tiles, then gathered landmark tiles); S^T, dP^T and dQ^T on MFMA. Computes
+//   dq      query-parallel, kDqW waves x 32 queries per workgroup, the forward's tiling
+//           (band tiles of kDqBN keys, then gathered landmark tiles); S^T, dP^T and dQ^T
+//           on MFMA. Computes
 //           Delta = rowsum(O * dO) for its queries and writes dQ, the per-head soft-edge
 //           d_w~, the per-query records of the key-parallel passes and (head 0) the
 //           block's smallest band start, which bounds the query scan of `kv` (workspace).
@@ -21,8 +22,9 @@
 //           512 queries of one sequence); 4 waves = 2 slot groups x 2 query sub-blocks scan
 //           the chunk's queries in 64-query LDS tiles. Writes landmark dK/dV and d_bias
 //           partials per chunk (workspace).
-//   kv      key-parallel band dK/dV, 4 waves x 32 keys per workgroup, scanning 64-query LDS
-//           tiles from the key block to the last query block whose band reaches it; adds
+//   kv      key-parallel band dK/dV, kv_waves(D) waves x 32 keys per workgroup, scanning
+//           kv_qt(D)-query LDS tiles from the key block to the last dq query block whose
+//           band reaches it; adds
 //           the landmark partials (over the sequence's chunks) of keys that are landmark
 //           positions; its head-0 workgroups reduce d_w~ over heads.
 //   dbias   d_lmk_bias = sum of the lmk_kv chunk partials, one workgroup per (head, seq).
@@ -55,8 +57,8 @@ constexpr int kLC = 512;  // queries per lmk_kv chunk (chunks are numbered like 
 enum { kCoreTile = 0, kEdgeTile = 1, kLmkTile = 2 };  // tile kinds of the dq loop phases
 
 // Per-(head, query) record written by dq and streamed by kv next to the Q / dO tiles,
-// field-major ([H][field][T]) so that one 64-query tile of a field is one 256-byte
-// direct load. Integer fields are encoded so that an all-zero record (what an
+// field-major ([H][field][T]) so that one field of a 64-query tile is one 256-byte
+// direct load (two fields of a 32-query tile share one). Integer fields are encoded so that an all-zero record (what an
 // out-of-range load returns) admits no key: lo and corelo as INT_MAX - x, pmax as x + 1.
 enum {
     kRecLse2 = 0,    // LSE * log2(e), +inf for empty rows (float)
@@ -690,9 +692,9 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), 2) bwd_kv_kernel
     };
 
     if (!LMK) {
-        // Band: one basic block per 64-query tile. S/dP of both 32-query sub-blocks, the
-        // masks, P and dS of sub-block 0 (VALU) under the S/dP MFMAs of sub-block 1, and
-        // sub-block 1's VALU work under the dV/dK MFMAs of sub-block 0. The band masks
+        // Band: one basic block per tile of NSB 32-query sub-blocks (two at D = 128: the
+        // masks, P and dS of sub-block 0 (VALU) run under the S/dP MFMAs of sub-block 1,
+        // and sub-block 1's VALU work under the dV/dK MFMAs of sub-block 0). The band masks
         // (q >= key, lo(q) <= key) are branch-free; a sub-block without admitted pairs is
         // fully masked, a tile without any is skipped. SOFT edge biases (key < corelo(q))
         // are added in place by a wave-uniform branch.

@@ -9,8 +9,9 @@ namespace dsalt {
 
 // Forward: one workgroup of fwd_waves(D) waves owns fwd_bm(D) = 32 * fwd_waves(D)
 // consecutive queries of one (sequence, head); each wave owns 32 of them. Key tiles
-// hold fwd_bn(D) = 32 keys (a 4-stage ring of K and V tiles is 32 KB of LDS at D = 64,
-// 64 KB at D = 128), and the kernel runs fwd_waves_per_simd(D) waves per SIMD. The
+// hold fwd_bn(D) = 32 keys on an fwd_stages(D)-deep LDS ring of K and V tiles (3 stages
+// = 24 KB at D = 64, 4 stages = 64 KB at D = 128), and the kernel runs
+// fwd_waves_per_simd(D) waves per SIMD. The
 // kernel also supports 64-key tiles and 4-wave workgroups. Landmark slots are padded
 // to a multiple of kFwdBN = 64, which every tile size divides. kFwdBM is the smallest
 // block size (size checks).
