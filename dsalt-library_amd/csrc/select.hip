@@ -14,7 +14,8 @@
 //    (8-bit digits starting at the top bit of the candidates' key range, so that the
 //    first LDS histogram is not concentrated on a few exponent values; one wave scans
 //    the 256 bins) finds the exact k_eff-th key `thr` and how many keys equal to it are
-//    still needed.
+//    still needed. A pass whose boundary bin holds exactly the keys still needed ends the
+//    search: the selection is then every key at or above that bin's lower bound.
 //  * A final ordered pass emits the selected positions in ascending order: each thread
 //    owns a contiguous run of positions, and one workgroup scan of (finite keys > thr,
 //    keys == thr) gives every thread its first output slot. Keys == thr are taken by
@@ -99,7 +100,7 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
     __shared__ int s_hist[256];
     __shared__ int s_w[kSelWaves][2];
     __shared__ uint32_t s_mm[kSelWaves][2];
-    __shared__ int s_bc[2];
+    __shared__ int s_bc[3];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int head = blockIdx.x / p.num_seqs;
@@ -173,30 +174,46 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
                 const int incl = wave_incl_scan_dpp(sum4);
                 const int excl = incl - sum4;
                 if (excl < remaining && incl >= remaining) {
-                    int cum = excl, d;
+                    int cum = excl, d, cd;
                     if (cum + c0 >= remaining) {
                         d = 255 - 4 * lane;
+                        cd = c0;
                     } else if ((cum += c0) + c1 >= remaining) {
                         d = 254 - 4 * lane;
+                        cd = c1;
                     } else if ((cum += c1) + c2 >= remaining) {
                         d = 253 - 4 * lane;
+                        cd = c2;
                     } else {
                         cum += c2;
                         d = 252 - 4 * lane;
+                        cd = c3;
                     }
                     s_bc[0] = d;
                     s_bc[1] = cum;  // keys in the prefix with a larger digit
+                    s_bc[2] = cd;   // keys in the prefix with digit d
                 }
             }
             __syncthreads();
             prefix |= (uint32_t)s_bc[0] << shift;
             pmask |= 0xFFu << shift;
             remaining -= s_bc[1];
+            // every key of the chosen bin is needed: the selection is exactly the keys
+            // with rel >= prefix (the bin and everything above it), whatever the lower
+            // digits are - the passes for them are skipped
+            const bool whole_bin = s_bc[2] == remaining;
             __syncthreads();
-            if (shift == 0) break;
+            if (whole_bin) {
+                thr = kmin + prefix - 1u;  // kmin >= 1: thr >= 0 and key 0 is never taken
+                need_eq = 0;
+                break;
+            }
+            if (shift == 0) {
+                thr = kmin + prefix;
+                need_eq = remaining;
+                break;
+            }
         }
-        thr = kmin + prefix;
-        need_eq = remaining;
     }
 
     // ordered emission: emitted slots before this thread = finite keys > thr before it plus

@@ -239,6 +239,28 @@ def test_select_bit_exact(lens, H, k, tie):
     np.testing.assert_array_equal(got, orc.select_landmarks(scores, w, cu, k))
 
 
+@pytest.mark.parametrize("k", [64, 65, 63, 100])
+def test_select_clusters(k):
+    """Clusters of equal scores: the first radix pass can already hold exactly the keys
+    still needed (k = 64: the top cluster), or the boundary falls inside a cluster of
+    ties (k = 63, 65) or on a cluster edge deeper down (k = 100)."""
+    rng = np.random.default_rng(k)
+    lens, H = [700, 2048, 150], 3
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(cu[-1])
+    scores = np.ones((T, H), np.float32)
+    for s0, L in zip(cu[:-1], lens):
+        idx = rng.permutation(L)
+        scores[s0 + idx[:64]] = 5.0           # top cluster of 64 equal scores
+        scores[s0 + idx[64:100]] = 3.0        # next cluster of 36
+        scores[s0 + idx[100:130]] = rng.standard_normal((30, H)).astype(np.float32)
+    w = np.zeros(T, np.float32)               # nothing covered
+    dev = torch.device("cuda", 0)
+    got = hip.select_landmarks(torch.from_numpy(scores).to(dev), torch.from_numpy(w).to(dev),
+                               torch.from_numpy(cu).to(torch.int32).to(dev), k).cpu().numpy()
+    np.testing.assert_array_equal(got, orc.select_landmarks(scores, w, cu, k))
+
+
 def test_select_strided_scores():
     scores, w, cu = _select_case(5, [100, 60], 8)
     dev = torch.device("cuda", 0)
