@@ -97,8 +97,9 @@ __device__ __forceinline__ void block_excl_scan2(int a, int b, int lane, int wav
 // (C = ceil(L / 1024)), which keeps the output in position order with one workgroup scan.
 __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) {
     __shared__ uint32_t s_keys[kSelCache];
-    __shared__ int s_hist[256];
+    __shared__ int s_hist[2][256];  // double-buffered: pass n clears the buffer of pass n + 1
     __shared__ int s_w[kSelWaves][2];
+    __shared__ int s_cnt[kSelWaves];  // written once: its readers need no trailing barrier
     __shared__ uint32_t s_mm[kSelWaves][2];
     __shared__ int s_bc[3];
 
@@ -140,10 +141,16 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
         s_mm[wave][0] = kmin;
         s_mm[wave][1] = kmax;
     }
-    int e0, e1, ncand, unused;
-    block_excl_scan2(cnt, 0, lane, wave, s_w, e0, e1, ncand, unused);  // its barriers publish s_mm
+    // candidate count and key range: per-wave values, one barrier (which also publishes
+    // the cleared histogram of the first pass); s_cnt and s_mm are never rewritten
+    cnt = wave_sum_u(cnt);
+    if (lane == 0) s_cnt[wave] = cnt;
+    if (tid < 256) s_hist[0][tid] = 0;
+    __syncthreads();
+    int ncand = 0;
 #pragma unroll
     for (int w = 0; w < kSelWaves; ++w) {
+        ncand += s_cnt[w];
         kmin = min(kmin, s_mm[w][0]);
         kmax = max(kmax, s_mm[w][1]);
     }
@@ -156,20 +163,22 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
         const uint32_t range = kmax - kmin;
         const int nbits = range ? 32 - __clz((int)range) : 0;
         uint32_t prefix = 0u, pmask = 0u;
-        int remaining = k_eff;
+        int remaining = k_eff, buf = 0;
         for (int shift = max(nbits - 8, 0);; shift = max(shift - 8, 0)) {
-            if (tid < 256) s_hist[tid] = 0;
-            __syncthreads();
+            // s_hist[buf] is zero here (cleared before the previous barrier)
+            int *hist = s_hist[buf];
             for (int j = tid; j < L; j += kSelThreads) {
                 const uint32_t key = key_at(j);
                 const uint32_t rel = key - kmin;
-                if (key != 0u && (rel & pmask) == prefix) atomicAdd(&s_hist[(rel >> shift) & 255u], 1);
+                if (key != 0u && (rel & pmask) == prefix) atomicAdd(&hist[(rel >> shift) & 255u], 1);
             }
             __syncthreads();
+            if (wave == 1) s_hist[buf ^ 1][lane * 4 + 0] = s_hist[buf ^ 1][lane * 4 + 1] =
+                s_hist[buf ^ 1][lane * 4 + 2] = s_hist[buf ^ 1][lane * 4 + 3] = 0;  // next pass
             if (wave == 0) {
                 // lane covers digits 255-4*lane .. 252-4*lane (descending)
-                const int c0 = s_hist[255 - 4 * lane], c1 = s_hist[254 - 4 * lane];
-                const int c2 = s_hist[253 - 4 * lane], c3 = s_hist[252 - 4 * lane];
+                const int c0 = hist[255 - 4 * lane], c1 = hist[254 - 4 * lane];
+                const int c2 = hist[253 - 4 * lane], c3 = hist[252 - 4 * lane];
                 const int sum4 = c0 + c1 + c2 + c3;
                 const int incl = wave_incl_scan_dpp(sum4);
                 const int excl = incl - sum4;
@@ -202,7 +211,9 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
             // with rel >= prefix (the bin and everything above it), whatever the lower
             // digits are - the passes for them are skipped
             const bool whole_bin = s_bc[2] == remaining;
-            __syncthreads();
+            buf ^= 1;
+            // no barrier here: s_bc is rewritten only after the next pass's histogram
+            // barrier, which every thread reaches after this read
             if (whole_bin) {
                 thr = kmin + prefix - 1u;  // kmin >= 1: thr >= 0 and key 0 is never taken
                 need_eq = 0;
