@@ -64,7 +64,8 @@ __device__ __forceinline__ int wave_incl_scan_dpp(int x) {
     return x;
 }
 
-// Workgroup-wide exclusive prefix sums of two counters (thread order = tid order).
+// Workgroup-wide exclusive prefix sums of two counters (thread order = tid order). One
+// barrier: s_w must not be written again by the caller afterwards.
 __device__ __forceinline__ void block_excl_scan2(int a, int b, int lane, int wave, int (*s_w)[2], int &ea,
                                                  int &eb, int &ta, int &tb) {
     const int ia = wave_incl_scan_dpp(a), ib = wave_incl_scan_dpp(b);
@@ -88,7 +89,6 @@ __device__ __forceinline__ void block_excl_scan2(int a, int b, int lane, int wav
     }
     ea = oa + ia - a;
     eb = ob + ib - b;
-    __syncthreads();
 }
 
 // One workgroup of 1024 threads per (head, sequence). The key pass and the histogram
