@@ -46,7 +46,7 @@ constexpr int kPad4 = 4;  // transposed tile row padding (halves): conflict-free
 constexpr int kv_waves(int d) { return d == 64 ? 2 : 4; }
 constexpr int kv_bm(int d) { return 32 * kv_waves(d); }  // keys per band kv workgroup
 constexpr int kv_qt(int d) { return d == 64 ? 32 : 64; }
-constexpr int kv_stages(int d) { return d == 64 ? 3 : 4; }
+constexpr int kv_stages(int) { return 4; }
 constexpr int kTN = 64;     // queries per lmk_kv tile
 constexpr int kDqW = 2;     // waves per dq workgroup
 constexpr int kDqBM = 64;   // queries per dq workgroup (32 per wave)
@@ -502,9 +502,9 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
 // A wave owns 32 keys (band: consecutive keys; LMK: 32 landmark slots) held in registers
 // as B operands, and streams tiles of Q, dO and the per-query records through an LDS ring
 // (direct global->LDS loads, one barrier per tile): band workgroups are kv_waves(D)
-// waves with kv_qt(D)-query tiles on a kv_stages(D)-deep ring (2 waves, 32 queries, 3
-// stages = 27 KB at D = 64), lmk_kv workgroups 4 waves with 64-query tiles on a 4-stage
-// ring. Per 32-query
+// waves with kv_qt(D)-query tiles on a kv_stages(D)-deep ring (2 waves, 32 queries, 4
+// stages = 36 KB at D = 64: registers, not LDS, limit it to 4 workgroups per CU),
+// lmk_kv workgroups 4 waves with 64-query tiles on a 4-stage ring. Per 32-query
 // sub-block: S = Q.K^T and dP = dO.V^T (lane = key column, registers = query rows),
 // P = 2^(S c + bias - lse2) on admitted pairs, dS = P (dP - Delta), then dV^T += dO^T.P
 // and dK^T += Q^T.dS with Q and dO read transposed.
