@@ -11,10 +11,12 @@
 //    is an in-register max plus one v_permlane32_swap between the two lane halves, and
 //    P^T converts in place into the B operand of O^T += V^T . P^T (no data movement).
 //  * K and V tiles (BN = 32 keys: 4 KB each at D = 64, 8 KB at D = 128) go global ->
-//    LDS with direct loads (global_load_lds_dwordx4, no register staging) into a ring
-//    of NSTAGE buffers: loads run NSTAGE-1 tiles ahead of the MFMAs. The small tiles
-//    keep the LDS ring and the S / P registers small enough for 3 workgroups per CU at
-//    D = 64 and 2 at D = 128. K is read row-major, V with the transposing
+//    LDS with direct loads (buffer_load_dwordx4 ... lds, no register staging) into two
+//    rings of R slots, one for K and one for V: K runs R tiles ahead of the S = K Q^T
+//    MFMAs, V R-1 tiles ahead of the P V MFMAs. At D = 64 (R = 2: 16 KB of tiles, 128
+//    VGPRs) that fits 8 HARD workgroups per CU, i.e. a whole 2048-token x 16-head batch
+//    of 4 sequences in one dispatch round; 2 workgroups at D = 128. K is read
+//    row-major, V with the transposing
 //    ds_read_b64_tr_b16 (the PV operand needs keys along K); both tiles are XOR-swizzled
 //    so that either read pattern is bank-conflict free (tiles.h).
 //  * The workgroup streams the union of its waves' key ranges
@@ -61,7 +63,7 @@ struct FwdParams {
 };
 
 template <typename DT, int D, int MODE>
-__global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_kernel(const FwdParams p) {
+__global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE == kSoft)) fwd_kernel(const FwdParams p) {
     typedef typename DT::vec8 vec8;
     constexpr int NW = fwd_waves(D);        // waves per workgroup
     constexpr int BM = 32 * NW;             // queries per workgroup
@@ -72,10 +74,10 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_
     constexpr int ND = D / 32;              // 32-row blocks of O^T
     typedef TileN<D, BN, NW> Tile;
     constexpr int TB = Tile::BYTES;
-    constexpr int NSTAGE = fwd_stages(D);              // LDS ring depth (tiles)
+    constexpr int R = fwd_ring(D);                     // depth of the K ring and of the V ring
     constexpr int LPT = 2 * Tile::LOADS_PER_WAVE;      // load instructions per tile per wave
 
-    __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][K, V]
+    __shared__ __align__(1024) char s_tiles[2][R][TB];  // [K, V][slot]
     __shared__ int s_red[NW][2];
     __shared__ int s_ltmin[DSALT_MAX_K_LMK / BN];  // smallest position in each landmark tile
     extern __shared__ int s_dyn[];
@@ -116,13 +118,9 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_
     const TileLanes<D, kSwzTr, BN, NW> vlanes(wave, lane, vst);
     const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
     auto band_key0 = [&](int t) { return ghi - (BN - 1) - t * BN; };
-    auto stage_of = [](int t) { return t % NSTAGE; };  // t >= 0, wave-uniform
-    auto issue_band = [&](int t) {
-        const int key0 = band_key0(t);
-        const uint32_t kl = tiles_lds + stage_of(t) * (2 * TB);
-        klanes.load_band(kl, wave, krs, (uint32_t)key0 * kst);  // wraps when key0 < 0
-        vlanes.load_band(kl + TB, wave, vrs, (uint32_t)key0 * vst);
-    };
+    auto slot_of = [](int t) { return t % R; };  // ring slot of tile t >= 0, wave-uniform
+    auto k_lds = [&](int t) { return tiles_lds + slot_of(t) * TB; };
+    auto v_lds = [&](int t) { return tiles_lds + (R + slot_of(t)) * TB; };
     // ---- global loads of the setup, issued before the first tile loads: loads complete
     // in issue order, so waiting for these does not wait for the tiles ----------------
     // Invalid lanes load a clamped valid row (their results are never stored), so no
@@ -149,27 +147,32 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_
             if (p.lmk_bias) lbb[j] = p.lmk_bias[head * p.lb_sh + seq * p.lb_ss + s * p.lb_sk];
         }
     }
-    // the first NSTAGE-1 band tiles through the compiler builtin, so that the waits for
-    // the loads above count them (in-loop refills use inline asm, see tiles.h); rows
-    // below the sequence start are clamped to row 0
+    // the first band tiles (K of tiles 0 .. R-1, V of tiles 0 .. R-2, in tile order,
+    // K before V) through the compiler builtin, so that the waits for the loads above
+    // count them (in-loop refills use inline asm, see tiles.h)
     {
-        const char *kb = reinterpret_cast<const char *>(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh);
-        const char *vb = reinterpret_cast<const char *>(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh);
+        const __amdgpu_buffer_rsrc_t kbr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh), (short)0, (int)((uint32_t)seq_len * kst), 0x00020000);
+        const __amdgpu_buffer_rsrc_t vbr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh), (short)0, (int)((uint32_t)seq_len * vst), 0x00020000);
 #pragma unroll
-        for (int t = 0; t < NSTAGE - 1; ++t) {
-            const int key0 = band_key0(t);
-            char *kt = s_tiles[t][0];
-            char *vt = s_tiles[t][1];
+        for (int t = 0; t < R; ++t) {
+            const uint32_t key0 = (uint32_t)band_key0(t);  // wraps below the sequence start: reads zeros
 #pragma unroll
             for (int u = 0; u < Tile::LOADS_PER_WAVE; ++u) {
                 const int slot0 = (wave * Tile::LOADS_PER_WAVE + u) * 64;
-                const int64_t key = max(key0 + klanes.row[u], 0);
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void *)(kb + key * kst + klanes.chunk_off[u]),
-                    (__attribute__((address_space(3))) void *)(kt + slot0 * 16), 16, 0, 0);
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void *)(vb + key * vst + vlanes.chunk_off[u]),
-                    (__attribute__((address_space(3))) void *)(vt + slot0 * 16), 16, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    kbr, (__attribute__((address_space(3))) void *)(s_tiles[0][t] + slot0 * 16), 16,
+                    (int)(key0 * kst + klanes.lane_off[u]), 0, 0, 0);
+            }
+            if (t < R - 1) {
+#pragma unroll
+                for (int u = 0; u < Tile::LOADS_PER_WAVE; ++u) {
+                    const int slot0 = (wave * Tile::LOADS_PER_WAVE + u) * 64;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        vbr, (__attribute__((address_space(3))) void *)(s_tiles[1][t] + slot0 * 16), 16,
+                        (int)(key0 * vst + vlanes.lane_off[u]), 0, 0, 0);
+                }
             }
         }
     }
@@ -235,28 +238,27 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_
     // landmark tiles holding at least one position admissible for the workgroup
     const int n_lt = p.k_pad / BN;
     const uint64_t lmask = __ballot(lane < n_lt && s_ltmin[lane < n_lt ? lane : 0] <= gpmax);
-    // band tiles (at least the NSTAGE-1 issued above; extra ones are inactive)
-    const int nb = max((ghi - glo) / BN + 1, NSTAGE - 1);
+    // band tiles (at least the R issued above; extra ones are inactive)
+    const int nb = max((ghi - glo) / BN + 1, R);
     const int nt = nb + __popcll(lmask);
     auto lmk_tile = [&](int t) {  // landmark tile of iteration t >= nb: (t-nb)-th set bit
         uint64_t m = lmask;
         for (int j = nb; j < t; ++j) m &= m - 1;
         return (int)__builtin_ctzll(m);
     };
-    auto issue_tile = [&](int t) {
-        if (t < nb) {
-            issue_band(t);
-        } else {
-            const int *lrow = s_lrow + lmk_tile(t) * BN;
-            const uint32_t kl = tiles_lds + stage_of(t) * (2 * TB);
-            klanes.load_gather(kl, wave, krs, kst, lrow);
-            vlanes.load_gather(kl + TB, wave, vrs, vst, lrow);
-        }
+    // K or V rows of tile t into their ring slot
+    auto issue_k = [&](int t) {
+        if (t < nb) klanes.load_band(k_lds(t), wave, krs, (uint32_t)band_key0(t) * kst, kst);  // wraps when key0 < 0
+        else klanes.load_gather_lean(k_lds(t), wave, krs, kst, s_lrow + lmk_tile(t) * BN);
+    };
+    auto issue_v = [&](int t) {
+        if (t < nb) vlanes.load_band(v_lds(t), wave, vrs, (uint32_t)band_key0(t) * vst, vst);
+        else vlanes.load_gather_lean(v_lds(t), wave, vrs, vst, s_lrow + lmk_tile(t) * BN);
     };
 
-    // S^T (BN keys x 32 queries) = K . Q^T, raw q.k, from the K tile of stage `stage`
-    auto qk_tile = [&](int stage, f32x16 (&sacc)[NRB]) {
-        const char *ktile = s_tiles[stage][0];
+    // S^T (BN keys x 32 queries) = K . Q^T, raw q.k, from the K tile in ring slot `slot`
+    auto qk_tile = [&](int slot, f32x16 (&sacc)[NRB]) {
+        const char *ktile = s_tiles[0][slot];
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
             f32x16 acc;
@@ -309,8 +311,8 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_
             }
     };
     // O^T (D x 32 queries) += V^T . P^T ; k-step kk covers tile keys kk*16..+15
-    auto pv = [&](const uint32_t (&pk)[NRB][8], int stage) {
-        const char *vtile = s_tiles[stage][1];
+    auto pv = [&](const uint32_t (&pk)[NRB][8], int slot) {
+        const char *vtile = s_tiles[1][slot];
 #pragma unroll
         for (int kk = 0; kk < 2 * NRB; ++kk) {
             const int rb = kk >> 1, g = kk & 1;
@@ -422,17 +424,19 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_
     };
 
     // ---- software-pipelined tile loop ----------------------------------------------------
-    // Iteration t: refill the ring with tile t+3; part A: P of tile t (VALU) interleaved
-    // with S of tile t+1 (MFMA); part B: O += P V of tile t (MFMA) interleaved with the
-    // masks and row max of tile t+1 (VALU); then the max update and a wait until tile
-    // t+2 has landed. The ring holds tiles t (V in use), t+1 (K in use), t+2 (landing)
-    // and t+3 (in flight); tile t+3 reuses the stage of tile t-1, whose V every wave
-    // finished reading before the barrier that ended iteration t-1. Tiles outside a
-    // wave's key range are fully masked (P = 0) rather than skipped, which keeps the
-    // iteration branch-free. nt >= NSTAGE - 1, and tiles 0 .. NSTAGE-2 were issued during
-    // the setup. With NSTAGE = 3, tile t+2 is issued at the start of iteration t and must
-    // have landed at its end. The last iteration computes S of a tile that does not exist (stale LDS
-    // stage) and ignores it.
+    // Iteration t: issue K of tile t+R and V of tile t+R-1; part A: P of tile t (VALU)
+    // interleaved with S of tile t+1 (MFMA); part B: O += P V of tile t (MFMA)
+    // interleaved with the masks and row max of tile t+1 (VALU); then the max update and
+    // a wait until K of tile t+2 and V of tile t+1 have landed. K of tile t+R takes the
+    // slot of K of tile t, last read by iteration t-1; V of tile t+R-1 takes the slot of
+    // V of tile t-1, also last read by iteration t-1; every wave finished those reads
+    // before the barrier that ended iteration t-1. With R = 2 the loads issued in
+    // iteration t itself must land by its end (wait for all); with R = 3 the needed ones
+    // were issued an iteration earlier and the newest LPT loads may stay in flight.
+    // Tiles outside a wave's key range are fully
+    // masked (P = 0) rather than skipped, which keeps the iteration branch-free.
+    // nt >= R; the setup issued K of tiles 0 .. R-1 and V of tiles 0 .. R-2. The last
+    // iteration computes S of a tile that does not exist (stale LDS slot) and ignores it.
     // MFMAs and operand reads of the two parts of an iteration, and the VALU instructions
     // placed after each MFMA (part A: exp / sum / pack, ~56 per row block; part B: masks
     // and max, ~40 per row block)
@@ -440,9 +444,10 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_
     constexpr int VALU_A = (NRB * 56 - 16 + NQK - 1) / NQK + 2;
     constexpr int VALU_B = (NRB * 32 + NPV - 1) / NPV;
     auto step = [&](int t, f32x16 (&cur)[NRB], f32x16 (&nxt)[NRB]) {
-        if (t + NSTAGE - 1 < nt) issue_tile(t + NSTAGE - 1);
+        if (t + R < nt) issue_k(t + R);
+        if (t + R - 1 < nt) issue_v(t + R - 1);
         uint32_t pk[NRB][8];
-        qk_tile(stage_of(t + 1), nxt);
+        qk_tile(slot_of(t + 1), nxt);
         exp_pack(cur, pk);
         __builtin_amdgcn_sched_group_barrier(0x100, NQK, 0);  // K operand reads
         __builtin_amdgcn_sched_group_barrier(0x402, 16, 0);   // VALU / transcendental
@@ -459,7 +464,7 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_
         asm volatile("" : "+v"(lsum0), "+v"(lsum1));
         const bool more = t + 1 < nt;
         if (more) adjust(t + 1, nxt);
-        pv(pk, stage_of(t));
+        pv(pk, slot_of(t));
         const float tmax = mask_max(t + 1, nxt);
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * NPV, 1);  // V operand reads
         __builtin_amdgcn_sched_group_barrier(0x002, 12, 1);       // VALU
@@ -469,11 +474,11 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D)) fwd_
             __builtin_amdgcn_sched_group_barrier(0x002, VALU_B, 1);  // VALU
         }
         rescale(more ? tmax : -INFINITY);
-        if (t + NSTAGE - 1 < nt) tile_barrier<(NSTAGE - 3) * LPT>();
+        if (t + R < nt) tile_barrier<(R - 2) * LPT>();
         else tile_barrier<0>();
     };
     f32x16 sA[NRB], sB[NRB];
-    tile_barrier<(NSTAGE - 3) * LPT>();  // tiles 0 and 1 landed (tile 2 may be in flight)
+    tile_barrier<(R - 2) * LPT>();  // K of tiles 0, 1 and V of tile 0 landed
     qk_tile(0, sA);
     adjust(0, sA);
     rescale(mask_max(0, sA));

@@ -1,5 +1,5 @@
 // LDS tiles of ROWS (64 or 32) rows x D 16-bit elements (rows are tokens: keys or queries), filled
-// with direct global->LDS loads (global_load_lds_dwordx4, gfx950) and read back as
+// with direct global->LDS loads (buffer_load_dwordx4 ... lds) and read back as
 // v_mfma_f32_32x32x16 operands.
 //
 // The direct loads are issued through inline asm and completed with explicit
@@ -81,7 +81,9 @@ struct TileLanes {
             const int g = (wave * LPW + u) * 64 + lane;
             row[u] = g / CPR;
             chunk_off[u] = (uint32_t)(((g % CPR) ^ tile_swz<SWZ>(row[u])) << 4);
-            lane_off[u] = (uint32_t)row[u] * stride + chunk_off[u];
+            uint32_t m = (uint32_t)row[u] * stride;
+            asm volatile("" : "+v"(m));  // no v_mad_u64_u32 (it would hold chunk_off as a pair)
+            lane_off[u] = m + chunk_off[u];
         }
     }
     __device__ __forceinline__ static uint32_t lds_slot(uint32_t tile_lds, int wave, int u) {
@@ -93,12 +95,52 @@ struct TileLanes {
 #pragma unroll
         for (int u = 0; u < LPW; ++u) dma16(base_off + lane_off[u], rsrc, lds_slot(tile_lds, wave, u));
     }
+    // When the rows of consecutive loads of a lane are 8 apart (D = 64), every load has
+    // the swizzle of the first, so later offsets are lane_off[0] plus a uniform step:
+    // one register per tile side instead of LPW.
+    static constexpr int ROWSTEP = 64 / CPR;
+    __device__ __forceinline__ void load_band(uint32_t tile_lds, int wave, i32x4 rsrc, uint32_t base_off,
+                                              uint32_t stride) const {
+#pragma unroll
+        for (int u = 0; u < LPW; ++u) {
+            if constexpr (ROWSTEP % 8 == 0) {
+                // opaque uniform sum: otherwise lane_off[0] + step is hoisted out of the
+                // tile loop into a register of its own
+                uint32_t b = base_off + (uint32_t)(u * ROWSTEP) * stride;
+                asm volatile("" : "+s"(b));
+                dma16(b + lane_off[0], rsrc, lds_slot(tile_lds, wave, u));
+            }
+            else
+                dma16(base_off + lane_off[u], rsrc, lds_slot(tile_lds, wave, u));
+        }
+    }
+    // Tile row r from buffer row rows[r], with the lane's tile row and chunk recomputed
+    // from the lane id (mbcnt) instead of held in registers across a tile loop.
+    __device__ __forceinline__ static void load_gather_lean(uint32_t tile_lds, int wave, i32x4 rsrc, uint32_t stride,
+                                                            const int *rows) {
+        int lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+        asm volatile("" : "+v"(lane));  // opaque: nothing derived from it is hoisted out of the loop
+#pragma unroll
+        for (int u = 0; u < LPW; ++u) {
+            const int g = (wave * LPW + u) * 64 + lane;
+            const int r = g / CPR;
+            const uint32_t chunk = (uint32_t)(((g % CPR) ^ tile_swz<SWZ>(r)) << 4);
+            uint32_t off = (uint32_t)rows[r] * stride;
+            asm volatile("" : "+v"(off));
+            dma16(off + chunk, rsrc, lds_slot(tile_lds, wave, u));
+        }
+    }
     // Tile row r from buffer row rows[r].
     __device__ __forceinline__ void load_gather(uint32_t tile_lds, int wave, i32x4 rsrc, uint32_t stride,
                                                 const int *rows) const {
 #pragma unroll
-        for (int u = 0; u < LPW; ++u)
-            dma16((uint32_t)rows[row[u]] * stride + chunk_off[u], rsrc, lds_slot(tile_lds, wave, u));
+        for (int u = 0; u < LPW; ++u) {
+            // 32-bit multiply, then add: left to itself the compiler fuses these into
+            // v_mad_u64_u32, which holds chunk_off as a 64-bit register pair
+            uint32_t off = (uint32_t)rows[row[u]] * stride;
+            asm volatile("" : "+v"(off));
+            dma16(off + chunk_off[u], rsrc, lds_slot(tile_lds, wave, u));
+        }
     }
 };
 

@@ -10,11 +10,12 @@ from __future__ import annotations
 import torch
 
 # Forward workgroups (the constants of csrc/launch.h): BLOCK_M queries = num_warps waves
-# of 32, BLOCK_N keys per LDS tile, num_stages-deep LDS ring; BLOCK_N_BWD queries per tile
-# of the band dK/dV pass (csrc/bwd.hip). All products are v_mfma_f32_32x32x16.
+# of 32, BLOCK_N keys per LDS tile, num_stages-deep LDS rings of K and of V tiles;
+# BLOCK_N_BWD queries per tile of the band dK/dV pass (csrc/bwd.hip). All products are
+# v_mfma_f32_32x32x16.
 _GFX950_CONFIG = {
-    64: {"BLOCK_M": 64, "BLOCK_N": 32, "BLOCK_N_BWD": 32, "num_warps": 2, "num_stages": 3},
-    128: {"BLOCK_M": 128, "BLOCK_N": 32, "BLOCK_N_BWD": 64, "num_warps": 4, "num_stages": 4},
+    64: {"BLOCK_M": 64, "BLOCK_N": 32, "BLOCK_N_BWD": 32, "num_warps": 2, "num_stages": 2},
+    128: {"BLOCK_M": 128, "BLOCK_N": 32, "BLOCK_N_BWD": 64, "num_warps": 4, "num_stages": 3},
 }
 
 

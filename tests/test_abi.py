@@ -155,7 +155,7 @@ def test_tuned_config_matches_kernel_constants():
         return (int(m.group(1)), int(m.group(2))) if m.group(1) else (int(m.group(3)),) * 2
 
     waves, bn, stages, kv_qt = (const_fn(launch, "fwd_waves"), const_fn(launch, "fwd_bn"),
-                                const_fn(launch, "fwd_stages"), const_fn(bwd, "kv_qt"))
+                                const_fn(launch, "fwd_ring"), const_fn(bwd, "kv_qt"))
     for i, d in enumerate((64, 128)):
         cfg = get_tuned_config(d)
         assert cfg == autotune_blocks(d)
