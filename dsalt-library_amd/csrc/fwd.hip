@@ -482,6 +482,8 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     qk_tile(0, sA);
     adjust(0, sA);
     rescale(mask_max(0, sA));
+    // step 0 refills the slot of K of tile 0: every wave must have read it first
+    tile_barrier<(R - 2) * LPT>();
     for (int t = 0; t < nt; t += 2) {
         step(t, sA, sB);
         if (t + 1 < nt) step(t + 1, sB, sA);
