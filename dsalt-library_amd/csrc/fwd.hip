@@ -377,11 +377,25 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     // Band mask of tile t (keys outside [lo, i]; all kept for landmark tiles) applied in
     // place, branch-free; returns the tile's masked row max (raw units, -inf if empty).
     // Element (rb, r) is key tb + rb*32 + acc_row_const(r) + hh*4 =: tb + hh*4 + cst.
+    // With tb = ghi - BN + 1 - BN t, the bounds are cst <= A0 + BN t (key <= i) and
+    // cst >= B0 + BN t (key >= lo); nA0 / nB0 are the bit counts of rows_le at t = 0.
+    const int A0 = i - ghi + BN - 1 - hh * 4, B0 = lo - ghi + BN - 1 - hh * 4;
+    const int nA0 = 4 * (A0 >> 3) + min((A0 & 7) + 1, 4);
+    const int nB0 = 4 * ((B0 - 1) >> 3) + min(((B0 - 1) & 7) + 1, 4);
     auto mask_max = [&](int t, f32x16 (&sacc)[NRB]) -> float {
-        const int tb = band_key0(t);
-        const int A = i - tb - hh * 4;   // key <= i  <=> cst <= A
-        const int B = lo - tb - hh * 4;  // key >= lo <=> cst >= B
-        const uint32_t band = rows_le(A) & ~rows_le(B - 1);
+        uint32_t band;
+        if constexpr (NRB == 1) {
+            // rows_le(A0 + BN t) keeps the low clamp(nA0 + 16 t, 0, 16) bits (BN t is a
+            // multiple of 8), so the band is the bit field [nB, nA): med3, med3, bfm
+            const int nA = min(max(nA0 + 16 * t, 0), 16);
+            const int nB = min(max(nB0 + 16 * t, 0), 16);
+            band = ((1u << (nA - nB)) - 1u) << nB;
+        } else {
+            const int tb = band_key0(t);
+            const int A = i - tb - hh * 4;   // key <= i  <=> cst <= A
+            const int B = lo - tb - hh * 4;  // key >= lo <=> cst >= B
+            band = rows_le(A) & ~rows_le(B - 1);
+        }
         const uint32_t keep = (t < nb) ? band : 0xffffffffu;
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb)
@@ -493,8 +507,14 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     const float ltot = half_sum(lsum0 + lsum1);
     const bool nonempty = ltot > 1e-9f;
     const float inv = nonempty ? 1.f / ltot : 0.f;
-    if (qvalid) {
-        const int64_t ooff = tok_i * p.o_st + (int64_t)head * p.o_sh;
+    // the query of this lane again from the lane id (opaque, so that i and its token
+    // offset are not kept in registers across the tile loop)
+    int lq = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) & 31;
+    asm volatile("" : "+v"(lq));
+    const int ie = wq0 + lq;
+    const int64_t tok_e = (int64_t)seq_start + ie;
+    if (ie < seq_len) {
+        const int64_t ooff = tok_e * p.o_st + (int64_t)head * p.o_sh;
 #pragma unroll
         for (int d = 0; d < ND; ++d)
 #pragma unroll
@@ -512,7 +532,7 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
                 }
             }
         if (hh == 0)
-            p.lse[tok_i * p.lse_st + (int64_t)head * p.lse_sh] =
+            p.lse[tok_e * p.lse_st + (int64_t)head * p.lse_sh] =
                 nonempty ? (m2 + fast_log2(ltot)) * kLn2 : -INFINITY;
     }
 }
