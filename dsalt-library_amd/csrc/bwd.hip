@@ -362,6 +362,13 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
         dq_mfma(pk, stage);
     };
 
+    // Band tile t holds keys tb = ghi - BN + 1 - BN t ..: the bounds cst <= A and cst >= B of
+    // the tile below are A0 + BN t and B0 + BN t; nA0 / nB0 are the bit counts of rows_le
+    // at t = 0.
+    const int A0 = i - ghi + BN - 1 - hh * 4, B0 = lo - ghi + BN - 1 - hh * 4;
+    const int nA0 = 4 * (A0 >> 3) + min((A0 & 7) + 1, 4);
+    const int nB0 = 4 * ((B0 - 1) >> 3) + min(((B0 - 1) & 7) + 1, 4);
+
     // ---- tile loop, in phases of one tile kind: band tiles inside every row's core
     // (keep mask only), SOFT band tiles that reach below a row's core start (a suffix of
     // the band tiles; edge bias and d_w~), landmark tiles (bias, admission). A tile's
@@ -448,7 +455,16 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
                         }
                     dq_mfma(pk, stage);
                 } else {
-                    const uint32_t keep = rows_le(A) & ~rows_le(B - 1);
+                    uint32_t keep;
+                    if constexpr (NRB == 1) {
+                        // rows_le(A0 + BN t) keeps the low clamp(nA0 + 16 t, 0, 16) bits (BN t
+                        // is a multiple of 8): the band is the bit field [nB, nA)
+                        const int nA = min(max(nA0 + 16 * t, 0), 16);
+                        const int nB = min(max(nB0 + 16 * t, 0), 16);
+                        keep = ((1u << (nA - nB)) - 1u) << nB;
+                    } else {
+                        keep = rows_le(A) & ~rows_le(B - 1);
+                    }
 #pragma unroll
                     for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
