@@ -63,6 +63,7 @@ const char *dsalt_last_error(void) { return g_err; }
 size_t dsalt_fwd_args_size(void) { return sizeof(dsalt_fwd_args); }
 size_t dsalt_bwd_args_size(void) { return sizeof(dsalt_bwd_args); }
 size_t dsalt_select_args_size(void) { return sizeof(dsalt_select_args); }
+size_t dsalt_scores_args_size(void) { return sizeof(dsalt_scores_args); }
 
 int dsalt_fwd_check(const dsalt_fwd_args *a) {
     if (!a) return fail(DSALT_ERR_INVALID, "args is NULL");
@@ -120,6 +121,62 @@ int dsalt_select_landmarks(const dsalt_select_args *a, void *stream) {
     hipError_t e = dsalt::launch_select(*a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess)
         return fail(DSALT_ERR_LAUNCH, "dsalt_select_landmarks launch failed: %s", hipGetErrorString(e));
+    return DSALT_OK;
+}
+
+int64_t dsalt_scores_workspace_size(int32_t total_len, int32_t n_kv_heads) {
+    if (total_len < 0 || n_kv_heads < 1) return -1;
+    return dsalt::scores_workspace_bytes(total_len, n_kv_heads);
+}
+
+int dsalt_scores_check(const dsalt_scores_args *a) {
+    if (!a) return fail(DSALT_ERR_INVALID, "args is NULL");
+    if (a->total_len < 0) return fail(DSALT_ERR_INVALID, "total_len must be >= 0");
+    if (a->d_model < 1 || a->head_dim < 1 || a->n_heads < 1 || a->n_kv_heads < 1)
+        return fail(DSALT_ERR_INVALID, "d_model, head_dim, n_heads and n_kv_heads must be >= 1");
+    if (a->n_heads % a->n_kv_heads)
+        return fail(DSALT_ERR_INVALID, "n_kv_heads (%d) must divide n_heads (%d)", a->n_kv_heads, a->n_heads);
+    if (a->n_kv_heads > dsalt::scores_max_kv())
+        return fail(DSALT_ERR_UNSUPPORTED, "n_kv_heads must be <= %d (got %d)", dsalt::scores_max_kv(), a->n_kv_heads);
+    for (int dt : {a->x_dtype, a->v_dtype})
+        if (dt != DSALT_DTYPE_BF16 && dt != DSALT_DTYPE_F16 && dt != DSALT_DTYPE_F32)
+            return fail(DSALT_ERR_INVALID, "x_dtype and v_dtype must be DSALT_DTYPE_BF16, _F16 or _F32 (got %d, %d)",
+                        a->x_dtype, a->v_dtype);
+    const int ex = a->x_dtype == DSALT_DTYPE_F32 ? 4 : 8;  // elements per 16-byte load
+    const int ev = a->v_dtype == DSALT_DTYPE_F32 ? 4 : 8;
+    if (a->d_model % ex || a->head_dim % ev)
+        return fail(DSALT_ERR_UNSUPPORTED, "d_model (%d) and head_dim (%d) must be multiples of %d and %d",
+                    a->d_model, a->head_dim, ex, ev);
+    const int g = a->head_dim / ev;
+    if (g > 64 || (g & (g - 1)))
+        return fail(DSALT_ERR_UNSUPPORTED, "head_dim / %d must be a power of two <= 64 (head_dim %d)", ev, a->head_dim);
+    if (a->total_len == 0) return DSALT_OK;
+    if (!a->x || !a->v || !a->alpha || !a->scores)
+        return fail(DSALT_ERR_INVALID, "x, v, alpha and scores must be non-NULL");
+    if (!aligned(a->x, 16) || !aligned(a->v, 16)) return fail(DSALT_ERR_INVALID, "x and v must be 16-byte aligned");
+    if (a->x_stride_t < a->d_model || a->x_stride_t % ex)
+        return fail(DSALT_ERR_INVALID, "x row stride (%lld) must be >= d_model and a multiple of %d",
+                    (long long)a->x_stride_t, ex);
+    if (a->v_stride_t < 0 || a->v_stride_h < 0 || a->v_stride_t % ev || a->v_stride_h % ev)
+        return fail(DSALT_ERR_INVALID, "v strides (t=%lld, h=%lld) must be non-negative multiples of %d",
+                    (long long)a->v_stride_t, (long long)a->v_stride_h, ev);
+    if (a->scores_stride_t < 0 || a->scores_stride_h < 0 || (a->z_v && (a->z_v_stride_t < 0 || a->z_v_stride_h < 0)))
+        return fail(DSALT_ERR_INVALID, "output strides must be non-negative");
+    const int64_t need = dsalt::scores_workspace_bytes(a->total_len, a->n_kv_heads);
+    if (!a->workspace) return fail(DSALT_ERR_INVALID, "workspace is NULL (%lld bytes needed)", (long long)need);
+    if (a->workspace_bytes < need)
+        return fail(DSALT_ERR_INVALID, "workspace too small: %lld < %lld bytes", (long long)a->workspace_bytes,
+                    (long long)need);
+    if (!aligned(a->workspace, 256)) return fail(DSALT_ERR_INVALID, "workspace must be 256-byte aligned");
+    return DSALT_OK;
+}
+
+int dsalt_hybrid_scores(const dsalt_scores_args *a, void *stream) {
+    int rc = dsalt_scores_check(a);
+    if (rc) return rc;
+    hipError_t e = dsalt::launch_scores(*a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess)
+        return fail(DSALT_ERR_LAUNCH, "dsalt_hybrid_scores launch failed: %s", hipGetErrorString(e));
     return DSALT_OK;
 }
 

@@ -1,0 +1,249 @@
+// Hybrid landmark scores from the value projection (fused selector front-end).
+//
+// Reference: hybrid_scores_per_head (dsalt/kernels/landmark_tokens_ker.py:19-61):
+//   s[t, h] = alpha[h] * z(||x_t W_V,g(h)||) + (1 - alpha[h]) * z(||x_t||)
+// where z standardises over all T packed tokens (mean, unbiased std clamped at 1e-6) and
+// g(h) is the kv group of query head h. The reference forms x W_V^T with a GEMM; the
+// attention module has that product already (its pre-RoPE value projection v), so this
+// path takes v and reads each of x and v once.
+//
+// Two kernels, deterministic (no atomics, fixed reduction orders):
+//  1. norms_kernel: one workgroup per 32 tokens. ||x_t|| and ||v_t,g|| in fp32, each
+//     rounded to its input's dtype (what .norm() returns for a 16-bit tensor, before
+//     .float(); under autocast x is fp32 and v bf16),
+//     written to the workspace, plus the workgroup's fp64 partial sums of each quantity
+//     and of its square.
+//  2. standardize_kernel: every workgroup reduces the partials in the same order, takes
+//     the mean and the unbiased std in fp64 (rounded to fp32, std clamped at 1e-6 with
+//     NaN kept), and writes z_x, z_v and the scores with the reference's fp32 operation
+//     order (no FMA contraction).
+#include "common.h"
+#include "launch.h"
+
+namespace dsalt {
+namespace {
+
+constexpr int kNormTokens = 32;    // tokens per workgroup of norms_kernel
+constexpr int kStdTokens = 64;     // tokens per workgroup of standardize_kernel
+constexpr int kMaxKvScores = 128;  // largest n_kv_heads (LDS of norms_kernel)
+
+struct ScoreParams {
+    const void *x, *v;
+    const float *alpha;
+    float *scores, *z_x, *z_v;
+    float *xn, *vn;   // workspace: [T], [T, n_kv]
+    double *part;     // workspace: [nblk][1 + n_kv][2]
+    int64_t x_st, v_st, v_sh, s_st, s_sh, zv_st, zv_sh;
+    int T, d, n_kv, D, H, nblk;
+};
+
+// Element loads and the dtype rounding of a norm, per storage type.
+struct LdBF16 {
+    static constexpr int E = 8;  // elements per 16 bytes
+    static __device__ __forceinline__ float sumsq16(const void *p) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(p);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = __uint_as_float(w[i] << 16), b = __uint_as_float(w[i] & 0xffff0000u);
+            s += a * a;
+            s += b * b;
+        }
+        return s;
+    }
+    // round to nearest even bf16 (NaN kept)
+    static __device__ __forceinline__ float round(float x) {
+        uint32_t u = __float_as_uint(x);
+        if ((u & 0x7fffffffu) > 0x7f800000u) return x;
+        u += 0x7fffu + ((u >> 16) & 1u);
+        return __uint_as_float(u & 0xffff0000u);
+    }
+};
+struct LdF16 {
+    static constexpr int E = 8;
+    static __device__ __forceinline__ float sumsq16(const void *p) {
+        const uint4 u = *reinterpret_cast<const uint4 *>(p);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = F16::lo_f32(w[i]), b = F16::hi_f32(w[i]);
+            s += a * a;
+            s += b * b;
+        }
+        return s;
+    }
+    static __device__ __forceinline__ float round(float x) { return (float)(_Float16)x; }
+};
+struct LdF32 {
+    static constexpr int E = 4;
+    static __device__ __forceinline__ float sumsq16(const void *p) {
+        const float4 f = *reinterpret_cast<const float4 *>(p);
+        float s = f.x * f.x;
+        s += f.y * f.y;
+        s += f.z * f.z;
+        s += f.w * f.w;
+        return s;
+    }
+    static __device__ __forceinline__ float round(float x) { return x; }
+};
+
+// Sum over the `width` lanes of each aligned lane group (width a power of two <= 64);
+// every lane of the group receives it.
+__device__ __forceinline__ float group_sum(float x, int width) {
+    for (int o = 1; o < width; o <<= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+template <typename LX, typename LV>
+__global__ void __launch_bounds__(256) norms_kernel(const ScoreParams p) {
+    constexpr int EX = LX::E, EV = LV::E;
+    constexpr int BX = EX == 8 ? 2 : 4, BV = EV == 8 ? 2 : 4;  // bytes per element
+    __shared__ float s_n[kNormTokens][1 + kMaxKvScores];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t0 = blockIdx.x * kNormTokens;
+    const int G = p.D / EV;         // lanes per v row
+    const int rows_per = 64 / G;    // v rows per load instruction
+    for (int j = wave; j < kNormTokens; j += 4) {
+        const int t = t0 + j;
+        if (t >= p.T) break;  // wave-uniform
+        // ||x_t||: lanes stride the row in 16-byte chunks
+        const char *xr = static_cast<const char *>(p.x) + (int64_t)t * p.x_st * BX;
+        float sx = 0.f;
+        for (int c = lane * EX; c < p.d; c += 64 * EX) sx += LX::sumsq16(xr + (int64_t)c * BX);
+        sx = group_sum(sx, 64);
+        const float xn = LX::round(sqrtf(sx));
+        if (lane == 0) {
+            p.xn[t] = xn;
+            s_n[j][0] = xn;
+        }
+        // ||v_t,g||: G lanes per row, rows_per rows per step
+        const char *vr = static_cast<const char *>(p.v) + (int64_t)t * p.v_st * BV;
+        for (int g0 = 0; g0 < p.n_kv; g0 += rows_per) {
+            const int g = g0 + lane / G;
+            float sv = 0.f;
+            if (g < p.n_kv) sv = LV::sumsq16(vr + ((int64_t)g * p.v_sh + (lane % G) * EV) * BV);
+            sv = group_sum(sv, G);
+            const float vn = LV::round(sqrtf(sv));
+            if (g < p.n_kv && lane % G == 0) {
+                p.vn[(int64_t)t * p.n_kv + g] = vn;
+                s_n[j][1 + g] = vn;
+            }
+        }
+    }
+    __syncthreads();
+    // fp64 partial sums of this block's tokens, in token order
+    const int nt = min(kNormTokens, p.T - t0);
+    for (int q = threadIdx.x; q <= p.n_kv; q += blockDim.x) {
+        double s = 0.0, s2 = 0.0;
+        for (int j = 0; j < nt; ++j) {
+            const double a = s_n[j][q];
+            s += a;
+            s2 += a * a;
+        }
+        double *o = p.part + ((int64_t)blockIdx.x * (1 + p.n_kv) + q) * 2;
+        o[0] = s;
+        o[1] = s2;
+    }
+}
+
+__global__ void __launch_bounds__(256) standardize_kernel(const ScoreParams p) {
+#pragma clang fp contract(off)
+    __shared__ float s_mean[1 + kMaxKvScores], s_std[1 + kMaxKvScores];
+    for (int q = threadIdx.x; q <= p.n_kv; q += blockDim.x) {
+        double s = 0.0, s2 = 0.0;
+        for (int b = 0; b < p.nblk; ++b) {
+            const double *o = p.part + ((int64_t)b * (1 + p.n_kv) + q) * 2;
+            s += o[0];
+            s2 += o[1];
+        }
+        const double n = (double)p.T;
+        const double mean = s / n;
+        // unbiased variance; T = 1 gives 0/0 = NaN, as torch.std does
+        const double var = fmax(s2 - s * mean, 0.0) / (n - 1.0);
+        const float sd = (float)sqrt(var);
+        s_mean[q] = (float)mean;
+        s_std[q] = (sd != sd) ? sd : fmaxf(sd, 1e-6f);  // clamp(min=1e-6) keeps NaN
+    }
+    __syncthreads();
+    const int rep = p.H / p.n_kv;
+    const int t0 = blockIdx.x * kStdTokens;
+    const int nt = min(kStdTokens, p.T - t0);
+    for (int e = threadIdx.x; e < nt * p.H; e += blockDim.x) {
+        const int t = t0 + e / p.H, h = e % p.H, g = h / rep;
+        const float zx = (p.xn[t] - s_mean[0]) / s_std[0];
+        const float zv = (p.vn[(int64_t)t * p.n_kv + g] - s_mean[1 + g]) / s_std[1 + g];
+        const float a = p.alpha[h];
+        const float t1 = a * zv;
+        const float t2 = (1.0f - a) * zx;
+        p.scores[(int64_t)t * p.s_st + (int64_t)h * p.s_sh] = t1 + t2;
+        if (p.z_v) p.z_v[(int64_t)t * p.zv_st + (int64_t)h * p.zv_sh] = zv;
+        if (p.z_x && h == 0) p.z_x[t] = zx;
+    }
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+template <typename LX>
+void launch_norms_x(int v_dtype, const ScoreParams &p, hipStream_t stream) {
+    if (v_dtype == DSALT_DTYPE_BF16)
+        hipLaunchKernelGGL((norms_kernel<LX, LdBF16>), dim3(p.nblk), dim3(256), 0, stream, p);
+    else if (v_dtype == DSALT_DTYPE_F16)
+        hipLaunchKernelGGL((norms_kernel<LX, LdF16>), dim3(p.nblk), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((norms_kernel<LX, LdF32>), dim3(p.nblk), dim3(256), 0, stream, p);
+}
+
+void launch_norms(int x_dtype, int v_dtype, const ScoreParams &p, hipStream_t stream) {
+    if (x_dtype == DSALT_DTYPE_BF16) launch_norms_x<LdBF16>(v_dtype, p, stream);
+    else if (x_dtype == DSALT_DTYPE_F16) launch_norms_x<LdF16>(v_dtype, p, stream);
+    else launch_norms_x<LdF32>(v_dtype, p, stream);
+}
+
+}  // namespace
+
+int64_t scores_workspace_bytes(int total_len, int n_kv) {
+    const int nblk = (total_len + kNormTokens - 1) / kNormTokens;
+    return (int64_t)(align256((size_t)total_len * 4) + align256((size_t)total_len * n_kv * 4) +
+                     align256((size_t)nblk * (1 + n_kv) * 2 * 8));
+}
+
+int scores_max_kv() { return kMaxKvScores; }
+
+hipError_t launch_scores(const dsalt_scores_args &a, hipStream_t stream) {
+    if (a.total_len == 0) return hipSuccess;
+    ScoreParams p;
+    p.x = a.x;
+    p.v = a.v;
+    p.alpha = a.alpha;
+    p.scores = a.scores;
+    p.z_x = a.z_x;
+    p.z_v = a.z_v;
+    p.T = a.total_len;
+    p.d = a.d_model;
+    p.n_kv = a.n_kv_heads;
+    p.D = a.head_dim;
+    p.H = a.n_heads;
+    p.nblk = (a.total_len + kNormTokens - 1) / kNormTokens;
+    char *ws = static_cast<char *>(a.workspace);
+    p.xn = reinterpret_cast<float *>(ws);
+    ws += align256((size_t)p.T * 4);
+    p.vn = reinterpret_cast<float *>(ws);
+    ws += align256((size_t)p.T * p.n_kv * 4);
+    p.part = reinterpret_cast<double *>(ws);
+    p.x_st = a.x_stride_t;
+    p.v_st = a.v_stride_t;
+    p.v_sh = a.v_stride_h;
+    p.s_st = a.scores_stride_t;
+    p.s_sh = a.scores_stride_h;
+    p.zv_st = a.z_v_stride_t;
+    p.zv_sh = a.z_v_stride_h;
+    launch_norms(a.x_dtype, a.v_dtype, p, stream);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(standardize_kernel, dim3((p.T + kStdTokens - 1) / kStdTokens), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace dsalt

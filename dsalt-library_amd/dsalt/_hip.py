@@ -86,11 +86,26 @@ class SelectArgs(ctypes.Structure):
     ]
 
 
+class ScoresArgs(ctypes.Structure):
+    _fields_ = [
+        ("total_len", c_int32), ("d_model", c_int32), ("n_kv_heads", c_int32), ("head_dim", c_int32),
+        ("n_heads", c_int32), ("x_dtype", c_int32), ("v_dtype", c_int32), ("reserved0", c_int32),
+        ("x", c_void_p), ("x_stride_t", c_int64),
+        ("v", c_void_p), ("v_stride_t", c_int64), ("v_stride_h", c_int64),
+        ("alpha", c_void_p),
+        ("scores", c_void_p), ("scores_stride_t", c_int64), ("scores_stride_h", c_int64),
+        ("z_x", c_void_p),
+        ("z_v", c_void_p), ("z_v_stride_t", c_int64), ("z_v_stride_h", c_int64),
+        ("workspace", c_void_p), ("workspace_bytes", c_int64),
+    ]
+
+
 EXPORTED_SYMBOLS = (
     "dsalt_fwd", "dsalt_fwd_check", "dsalt_bwd", "dsalt_bwd_check", "dsalt_bwd_workspace_size",
     "dsalt_select_landmarks", "dsalt_select_check", "dsalt_quantize_windows",
     "dsalt_abi_version", "dsalt_last_error", "dsalt_fwd_args_size", "dsalt_bwd_args_size",
-    "dsalt_select_args_size",
+    "dsalt_select_args_size", "dsalt_hybrid_scores", "dsalt_scores_check", "dsalt_scores_workspace_size",
+    "dsalt_scores_args_size",
 )
 
 _lib = None
@@ -113,6 +128,8 @@ def lib() -> ctypes.CDLL:
         ("dsalt_bwd_check", [ctypes.POINTER(BwdArgs)]),
         ("dsalt_select_landmarks", [ctypes.POINTER(SelectArgs), c_void_p]),
         ("dsalt_select_check", [ctypes.POINTER(SelectArgs)]),
+        ("dsalt_hybrid_scores", [ctypes.POINTER(ScoresArgs), c_void_p]),
+        ("dsalt_scores_check", [ctypes.POINTER(ScoresArgs)]),
         ("dsalt_quantize_windows", [c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
     ):
         fn = getattr(h, name)
@@ -120,9 +137,11 @@ def lib() -> ctypes.CDLL:
         fn.restype = ctypes.c_int
     h.dsalt_bwd_workspace_size.argtypes = [c_int32] * 5
     h.dsalt_bwd_workspace_size.restype = c_int64
+    h.dsalt_scores_workspace_size.argtypes = [c_int32] * 2
+    h.dsalt_scores_workspace_size.restype = c_int64
     h.dsalt_abi_version.restype = ctypes.c_int
     h.dsalt_last_error.restype = ctypes.c_char_p
-    for n in ("dsalt_fwd_args_size", "dsalt_bwd_args_size", "dsalt_select_args_size"):
+    for n in ("dsalt_fwd_args_size", "dsalt_bwd_args_size", "dsalt_select_args_size", "dsalt_scores_args_size"):
         getattr(h, n).restype = c_size_t
     _lib = h
     check_abi()
@@ -134,7 +153,7 @@ def check_abi() -> None:
     if h.dsalt_abi_version() != ABI_VERSION:
         raise DsaltError(f"ABI version mismatch: library {h.dsalt_abi_version()} vs binding {ABI_VERSION}")
     for struct, fn in ((FwdArgs, h.dsalt_fwd_args_size), (BwdArgs, h.dsalt_bwd_args_size),
-                       (SelectArgs, h.dsalt_select_args_size)):
+                       (SelectArgs, h.dsalt_select_args_size), (ScoresArgs, h.dsalt_scores_args_size)):
         if ctypes.sizeof(struct) != fn():
             raise DsaltError(f"{struct.__name__} layout mismatch: {ctypes.sizeof(struct)} vs {fn()} bytes")
 
@@ -390,6 +409,63 @@ def select_landmarks(scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Te
     a.lmk_pos = out.data_ptr()
     _raise(lib().dsalt_select_landmarks(ctypes.byref(a), stream_handle(dev)), "dsalt_select_landmarks")
     return out
+
+
+_SCORE_DTYPES = {torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16, torch.float32: DTYPE_F32}
+
+
+def scores_args(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int,
+                scores: torch.Tensor, z_x: torch.Tensor | None, z_v: torch.Tensor | None,
+                ws: torch.Tensor | None) -> ScoresArgs:
+    """Argument block of dsalt_hybrid_scores (x [T, d], v [T, n_kv, D], alpha [H] fp32)."""
+    T, d = x.shape
+    _, n_kv, D = v.shape
+    a = ScoresArgs()
+    a.total_len, a.d_model, a.n_kv_heads, a.head_dim, a.n_heads = T, d, n_kv, D, n_heads
+    a.x_dtype = _SCORE_DTYPES.get(x.dtype, -1)
+    a.v_dtype = _SCORE_DTYPES.get(v.dtype, -1)
+    a.x, a.x_stride_t = x.data_ptr(), x.stride(0)
+    a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
+    a.alpha = alpha.data_ptr()
+    a.scores, a.scores_stride_t, a.scores_stride_h = scores.data_ptr(), scores.stride(0), scores.stride(1)
+    a.z_x = _ptr(z_x)
+    if z_v is not None:
+        a.z_v, a.z_v_stride_t, a.z_v_stride_h = z_v.data_ptr(), z_v.stride(0), z_v.stride(1)
+    if ws is not None:
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    return a
+
+
+def scores_workspace_size(T: int, n_kv: int) -> int:
+    n = lib().dsalt_scores_workspace_size(T, n_kv)
+    if n < 0:
+        raise DsaltError("invalid sizes for dsalt_scores_workspace_size")
+    return n
+
+
+def hybrid_scores(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int):
+    """``(scores [T, H], z_x [T], z_v [T, H])`` fp32 of the hybrid landmark score from the
+    hidden states x [T, d] and their value projection v = x W_V^T [T, n_kv, D]
+    (pre-RoPE), without the GEMM; no gradient (the selection is detached)."""
+    dev = require_gpu(x, v, alpha)
+    if x.dim() != 2 or v.dim() != 3 or v.shape[0] != x.shape[0]:
+        raise DsaltError(f"x must be [T, d] and v [T, n_kv, D] with the same T (got {tuple(x.shape)}, "
+                         f"{tuple(v.shape)})")
+    if x.dtype not in _SCORE_DTYPES or v.dtype not in _SCORE_DTYPES:
+        raise DsaltError(f"x and v must be bf16, fp16 or fp32 (got {x.dtype}, {v.dtype})")
+    x = x if x.stride(1) == 1 else x.contiguous()
+    v = v if v.stride(2) == 1 else v.contiguous()
+    alpha = alpha.detach().to(torch.float32).contiguous()
+    if alpha.shape != (n_heads,):
+        raise DsaltError(f"alpha must be [{n_heads}] (got {tuple(alpha.shape)})")
+    T = x.shape[0]
+    scores = torch.empty((T, n_heads), device=dev, dtype=torch.float32)
+    z_x = torch.empty((T,), device=dev, dtype=torch.float32)
+    z_v = torch.empty((T, n_heads), device=dev, dtype=torch.float32)
+    ws = torch.empty((scores_workspace_size(T, v.shape[1]),), device=dev, dtype=torch.uint8)
+    a = scores_args(x, v, alpha, n_heads, scores, z_x, z_v, ws)
+    _raise(lib().dsalt_hybrid_scores(ctypes.byref(a), stream_handle(dev)), "dsalt_hybrid_scores")
+    return scores, z_x, z_v
 
 
 class SelectLauncher:

@@ -50,3 +50,32 @@ def hybrid_scores_per_head(
 
     scores = alpha * z_v + (1.0 - alpha) * z_x.unsqueeze(1)
     return scores, z_x, z_v
+
+
+def hybrid_scores_from_v(
+    x: torch.Tensor,
+    v: torch.Tensor,
+    alpha: torch.Tensor,
+    n_heads: int,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The same score from the value projection ``v = x W_V^T`` ``[T, n_kv, dh]``
+    (pre-RoPE, as the attention module computes it), without a second GEMM.
+
+    Differentiable in x, v (hence W_V) and alpha; identical arithmetic to
+    :func:`hybrid_scores_per_head` once ``v`` equals its ``x @ W_V.T``. The no-gradient
+    selection path uses the HIP kernel ``dsalt_hybrid_scores`` instead
+    (:func:`dsalt._hip.hybrid_scores`).
+    """
+    x_norm = x.norm(dim=-1).float()
+    z_x = (x_norm - x_norm.mean()) / x_norm.std().clamp(min=1e-6)
+
+    n_kv = v.shape[1]
+    xwv = v.norm(dim=-1).float()
+    mu_v = xwv.mean(0, keepdim=True)
+    std_v = xwv.std(0, keepdim=True).clamp(min=1e-6)
+    z_v = (xwv - mu_v) / std_v
+    if n_kv != n_heads:
+        z_v = z_v.repeat_interleave(n_heads // n_kv, dim=1)
+
+    scores = alpha * z_v + (1.0 - alpha) * z_x.unsqueeze(1)
+    return scores, z_x, z_v

@@ -85,6 +85,7 @@ def _compute_landmark_indices(
     total_len: int,
     cu_list: list | None = None,
     head_dim: int | None = None,
+    v: torch.Tensor | None = None,
 ):
     """Top-``k_lmk`` landmark positions per (head, sequence), excluding covered tokens.
 
@@ -94,8 +95,17 @@ def _compute_landmark_indices(
     in ascending position order and padded with ``-1`` (the reference's
     ``topk(sorted=False)`` leaves slot order unspecified, so the set is what matches).
     ``n_min`` and ``total_len`` are accepted for signature compatibility.
+
+    ``v`` (optional, not in the reference's signature): the value projection
+    ``x @ W_V.T`` as ``[T, n_kv, dh]``, which the attention module already holds. With
+    it the scores come from the fused HIP kernel ``dsalt_hybrid_scores`` (norms and
+    standardisation in one pass over x and v) and the ``x @ W_V.T`` GEMM is skipped.
     """
     n_heads = alpha.shape[0]
+    if v is not None:
+        scores, z_x, z_v = _hip.hybrid_scores(x.detach(), v.detach(), alpha, n_heads)
+        lmk = _hip.select_landmarks(scores, w_sizes, cu_seqlens, int(k_lmk))
+        return lmk, z_x, z_v
     dh = head_dim if head_dim is not None else W_V.shape[0] // n_heads
     scores, z_x, z_v = _score_block(x, W_V, alpha, n_heads, dh)
     lmk = _hip.select_landmarks(scores.float(), w_sizes, cu_seqlens, int(k_lmk))

@@ -9,7 +9,8 @@ Packed input (``cu_seqlens`` given) runs the sparse path:
   * training: ``_train_selectors`` (continuous window, HIP landmark top-k, soft landmark
     weight log sigmoid(s/tau_lmk)) then the SOFT HIP kernels (forward + deterministic
     backward carrying d_w~ to win_gate and d_logw to alpha_w), dsalt_attention.py:440-487;
-  * inference: floor-quantised windows (HIP), HIP landmark top-k, the HARD HIP kernel,
+  * inference: floor-quantised windows (HIP), HIP hybrid scores from the value projection
+    and HIP landmark top-k, the HARD HIP kernel,
     dsalt_attention.py:610-625; then the ``_last_P`` diagnostic of sequence 0 unless
     ``_collect_last_P`` is set to False (dsalt_attention.py:636-702).
 The attention output stays in the compute dtype on the module path (the reference
@@ -28,7 +29,7 @@ import torch.nn as nn
 
 from .. import _hip
 from ..kernels._sparse import sparse_attention
-from ..kernels.landmark_tokens_ker import hybrid_scores_per_head
+from ..kernels.landmark_tokens_ker import hybrid_scores_from_v, hybrid_scores_per_head
 from ..kernels.selectors import _compute_landmark_indices
 from ..kernels.window_utils import apply_rotary_emb, build_rope_cache
 
@@ -45,7 +46,15 @@ class DSALTAttention(nn.Module):
     ``w~(i) = n_min + sigmoid(win_gate(x_i)) * (n_max - n_min)`` tokens and the
     landmarks left of the window, selected per (head, sequence) by the hybrid score
     with per-head balance ``alpha = sigmoid(alpha_w)``.
+
+    ``_fused_selector`` (default True): with ``qkv_bias=False`` the landmark scores are
+    formed from the module's own value projection ``v = x W_V^T`` (the fused HIP score
+    kernel for the detached selection, the same formula in torch for the
+    differentiable ``lmk_logw``) instead of a second ``x @ W_V.T`` GEMM. Set it to False
+    for the reference's GEMM path.
     """
+
+    _fused_selector = True
 
     def __init__(
         self,
@@ -156,19 +165,25 @@ class DSALTAttention(nn.Module):
             "the tokens to [T, d] and pass cu_seqlens (int32 [S + 1]) for sparse attention")
 
     @_dynamo_opaque
-    def _train_selectors(self, x, cu_seqlens, total_len, device, cu_list=None):
+    def _train_selectors(self, x, cu_seqlens, total_len, device, cu_list=None, v=None):
         """``(w_cont [T], lmk_pos [H,S,k], lmk_logw [H,S,k])`` (dsalt_attention.py:457-487):
-        the selection is detached; ``w_cont`` and ``lmk_logw`` carry the gradients."""
+        the selection is detached; ``w_cont`` and ``lmk_logw`` carry the gradients.
+        With ``v`` (the pre-RoPE value projection ``[T, n_kv, dh]``) the scores are
+        formed from it instead of a second ``x @ W_V.T`` GEMM."""
         w_cont = self._window_continuous(x)
         alpha = self._alpha()
+        fused = v is not None and self._fused_selector
         with torch.no_grad():
             w_disc = _hip.quantize_windows(w_cont.detach())
             lmk_pos, _, _ = _compute_landmark_indices(
                 x.detach(), self.v_proj.weight.detach(), alpha.detach().float(),
                 w_disc, cu_seqlens, self.k_lmk, self.n_min, total_len, cu_list,
-                head_dim=self.head_dim,
+                head_dim=self.head_dim, v=v.detach() if fused else None,
             )
-        scores, _, _ = hybrid_scores_per_head(x, self.v_proj.weight, alpha, self.n_heads, self.head_dim)
+        if fused:
+            scores, _, _ = hybrid_scores_from_v(x, v, alpha, self.n_heads)
+        else:
+            scores, _, _ = hybrid_scores_per_head(x, self.v_proj.weight, alpha, self.n_heads, self.head_dim)
         starts = cu_seqlens[:-1].to(device).long()
         safe_pos = lmk_pos.clamp(min=0)
         abs_pos = starts[None, :, None] + safe_pos
@@ -184,6 +199,9 @@ class DSALTAttention(nn.Module):
         q = self.q_proj(x).view(total_len, self.n_heads, self.head_dim)
         k = self.k_proj(x).view(total_len, self.n_kv_heads, self.head_dim)
         v = self.v_proj(x).view(total_len, self.n_kv_heads, self.head_dim)
+        # x W_V^T before RoPE and the kv repeat: the selector's value norms come from it
+        # (qkv_bias=False only; with a bias v is not x W_V^T)
+        v_sel = v if self.v_proj.bias is None else None
 
         if rope_cs is None:
             num_seqs = cu_seqlens.shape[0] - 1
@@ -206,7 +224,7 @@ class DSALTAttention(nn.Module):
 
         if self.training:
             self._last_P = None
-            w_cont, lmk_pos, lmk_logw = self._train_selectors(x, cu_seqlens, total_len, device, cu_list)
+            w_cont, lmk_pos, lmk_logw = self._train_selectors(x, cu_seqlens, total_len, device, cu_list, v_sel)
             out = sparse_attention(_hip.MODE_SOFT, q, k, v, lmk_pos, lmk_logw, w_cont, cu_seqlens,
                                    self.tau_win, float(self.win_edge))
             return self._apply_out_proj(out.reshape(total_len, self.d_model)), aux
@@ -216,6 +234,7 @@ class DSALTAttention(nn.Module):
         lmk_indices, _, _ = _compute_landmark_indices(
             x.detach(), self.v_proj.weight.detach(), alpha.detach().float(), w_sizes,
             cu_seqlens, self.k_lmk, self.n_min, total_len, cu_list, head_dim=self.head_dim,
+            v=v_sel.detach() if (self._fused_selector and v_sel is not None) else None,
         )
         # Hard A(i) = W(i) ∪ L(i): the score only selects (zero landmark bias).
         out = sparse_attention(_hip.MODE_HARD, q, k, v, lmk_indices, None, w_sizes, cu_seqlens)

@@ -181,6 +181,42 @@ int dsalt_select_landmarks(const dsalt_select_args *args, void *stream);
 int dsalt_select_check(const dsalt_select_args *args);
 
 /*
+ * Hybrid landmark scores from the value projection (fused selector front-end).
+ * Replaces hybrid_scores_per_head (dsalt/kernels/landmark_tokens_ker.py:19-61) without
+ * its x @ W_V^T GEMM: v is the pre-RoPE value projection x W_V^T [T, n_kv, D] that the
+ * attention module computes anyway. For token t and query head h (kv group
+ * g = h / (n_heads / n_kv_heads)):
+ *   scores[t, h] = alpha[h] * z_v[t, h] + (1 - alpha[h]) * z_x[t]
+ *   z_x[t] = (||x_t|| - mean) / max(std, 1e-6),  z_v[t, h] = the same over ||v_t,g||
+ * with mean and unbiased std over all T tokens (NaN std kept, as torch's clamp does).
+ * The norms are taken in fp32 and rounded to the input dtype, as x.norm() returns them
+ * for a 16-bit tensor. x, v: unit stride along d / D, 16-byte aligned rows; D / (16 bytes
+ * / v's element size) must be a power of two <= 64; n_kv_heads <= 128 and divides n_heads.
+ * The means and stds are reduced in fp64 in a fixed order: the result is deterministic.
+ */
+typedef struct dsalt_scores_args {
+    int32_t total_len, d_model, n_kv_heads, head_dim, n_heads;
+    int32_t x_dtype, v_dtype; /* each DSALT_DTYPE_BF16, _F16 or _F32 (autocast: fp32 x, bf16 v) */
+    int32_t reserved0;
+    const void *x; /* [T, d_model] */
+    int64_t x_stride_t;
+    const void *v; /* [T, n_kv_heads, head_dim] */
+    int64_t v_stride_t, v_stride_h;
+    const float *alpha; /* [n_heads] */
+    float *scores;      /* out: [T, n_heads] */
+    int64_t scores_stride_t, scores_stride_h;
+    float *z_x; /* out: [T] contiguous, may be NULL */
+    float *z_v; /* out: [T, n_heads], may be NULL */
+    int64_t z_v_stride_t, z_v_stride_h;
+    void *workspace; /* >= dsalt_scores_workspace_size(...) bytes, 256-byte aligned */
+    int64_t workspace_bytes;
+} dsalt_scores_args;
+
+int64_t dsalt_scores_workspace_size(int32_t total_len, int32_t n_kv_heads);
+int dsalt_hybrid_scores(const dsalt_scores_args *args, void *stream);
+int dsalt_scores_check(const dsalt_scores_args *args);
+
+/*
  * Window quantisation w = max(1, floor(w~)) (NaN stays NaN), the floor/clamp of
  * DSALTAttention._window_sizes(floor=True) and of _train_selectors
  * (dsalt/modules/dsalt_attention.py:277-284, :471). Either output may be NULL; the
@@ -195,6 +231,7 @@ const char *dsalt_last_error(void);
 size_t dsalt_fwd_args_size(void);
 size_t dsalt_bwd_args_size(void);
 size_t dsalt_select_args_size(void);
+size_t dsalt_scores_args_size(void);
 
 #ifdef __cplusplus
 }

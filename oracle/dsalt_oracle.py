@@ -54,6 +54,21 @@ def hybrid_scores(x: torch.Tensor, W_V: torch.Tensor, alpha: torch.Tensor, n_hea
     return scores, z_x, z_v
 
 
+def hybrid_scores_from_v(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int):
+    """(scores [T,H], z_x [T], z_v [T,H]) from the value projection v = x W_V^T
+    [T, n_kv, dh] instead of W_V: landmark_tokens_ker.py:45-61 with its GEMM's output
+    given (the module's pre-RoPE v). Norms in v's dtype, as the reference's."""
+    x_norm = x.norm(dim=-1).float()
+    z_x = (x_norm - x_norm.mean()) / x_norm.std().clamp(min=1e-6)
+    n_kv = v.shape[1]
+    xwv = v.norm(dim=-1).float()
+    z_v = (xwv - xwv.mean(0, keepdim=True)) / xwv.std(0, keepdim=True).clamp(min=1e-6)
+    if n_kv != n_heads:
+        z_v = z_v.repeat_interleave(n_heads // n_kv, dim=1)
+    scores = alpha * z_v + (1.0 - alpha) * z_x.unsqueeze(1)
+    return scores, z_x, z_v
+
+
 def window_continuous(win_logits: torch.Tensor, n_min: int, n_max: int) -> torch.Tensor:
     """w~ = n_min + sigmoid(logit) * (n_max - n_min); dsalt_attention.py:270-275."""
     return n_min + torch.sigmoid(win_logits) * (n_max - n_min)

@@ -38,6 +38,7 @@ def test_struct_sizes():
     assert ctypes.sizeof(hip.FwdArgs) == lib.dsalt_fwd_args_size()
     assert ctypes.sizeof(hip.BwdArgs) == lib.dsalt_bwd_args_size()
     assert ctypes.sizeof(hip.SelectArgs) == lib.dsalt_select_args_size()
+    assert ctypes.sizeof(hip.ScoresArgs) == lib.dsalt_scores_args_size()
 
 
 def _fake_fwd(**kw):
@@ -163,3 +164,59 @@ def test_tuned_config_matches_kernel_constants():
         assert cfg["BLOCK_N"] == bn[i] and cfg["num_stages"] == stages[i] and cfg["BLOCK_N_BWD"] == kv_qt[i]
     with pytest.raises(ValueError):
         get_tuned_config(96)
+
+
+def _scores_args(**kw):
+    a = hip.ScoresArgs()
+    a.total_len, a.d_model, a.n_kv_heads, a.head_dim, a.n_heads = 100, 512, 4, 64, 8
+    a.x_dtype = a.v_dtype = hip.DTYPE_BF16
+    a.x, a.x_stride_t = 0x10000, 512
+    a.v, a.v_stride_t, a.v_stride_h = 0x20000, 256, 64
+    a.alpha, a.scores, a.scores_stride_t, a.scores_stride_h = 0x30000, 0x40000, 8, 1
+    a.workspace = 0x50000
+    for k, v in kw.items():
+        setattr(a, k, v)
+    if "workspace_bytes" not in kw:
+        a.workspace_bytes = hip.lib().dsalt_scores_workspace_size(a.total_len, a.n_kv_heads)
+    return a
+
+
+def test_scores_workspace_size():
+    lib = hip.lib()
+    assert lib.dsalt_scores_workspace_size(-1, 4) == -1
+    assert lib.dsalt_scores_workspace_size(10, 0) == -1
+    small, big = lib.dsalt_scores_workspace_size(100, 4), lib.dsalt_scores_workspace_size(10000, 16)
+    assert 0 < small < big and small % 256 == 0
+
+
+@pytest.mark.parametrize("field,value,code,needle", [
+    ("n_kv_heads", 3, 1, "divide"),                 # 3 does not divide 8
+    ("x_dtype", 7, 1, "x_dtype"),
+    ("v_dtype", -1, 1, "v_dtype"),
+    ("head_dim", 96, 2, "power of two"),           # 96 / 8 = 12 chunks
+    ("d_model", 100, 2, "multiples"),
+    ("x", 0x10008, 1, "aligned"),
+    ("x_stride_t", 256, 1, "row stride"),           # < d_model
+    ("v_stride_h", 60, 1, "v strides"),
+    ("workspace", 0, 1, "workspace is NULL"),
+    ("workspace_bytes", 16, 1, "too small"),
+    ("workspace", 0x50010, 1, "256-byte"),
+    ("alpha", 0, 1, "non-NULL"),
+])
+def test_scores_check_rejects(field, value, code, needle):
+    lib = hip.lib()
+    assert lib.dsalt_scores_check(ctypes.byref(_scores_args())) == 0
+    assert lib.dsalt_scores_check(ctypes.byref(_scores_args(**{field: value}))) == code
+    assert needle in lib.dsalt_last_error().decode()
+
+
+def test_scores_check_fp32_and_gqa():
+    lib = hip.lib()
+    # fp32: 4 elements per 16-byte load, head_dim 64 -> 16 lanes per row
+    assert lib.dsalt_scores_check(ctypes.byref(_scores_args(x_dtype=hip.DTYPE_F32, v_dtype=hip.DTYPE_F32))) == 0
+    assert lib.dsalt_scores_check(ctypes.byref(_scores_args(v_dtype=hip.DTYPE_F32, head_dim=512))) == 2
+    # autocast: fp32 x with bf16 v
+    assert lib.dsalt_scores_check(ctypes.byref(_scores_args(x_dtype=hip.DTYPE_F32))) == 0
+    assert lib.dsalt_scores_check(ctypes.byref(_scores_args(n_kv_heads=8, v_stride_t=512))) == 0
+    assert lib.dsalt_scores_check(ctypes.byref(_scores_args(n_kv_heads=1, v_stride_t=64))) == 0
+    assert lib.dsalt_scores_check(ctypes.byref(_scores_args(n_kv_heads=256, n_heads=256))) == 2

@@ -1,0 +1,130 @@
+"""The fused selector front-end on the GPU: dsalt_hybrid_scores (the hybrid landmark
+score of landmark_tokens_ker.py:19-61 from the value projection v = x W_V^T) against the
+CPU oracle, and its use by the selector and the module.
+
+For fp32 inputs the scores match the float64-input oracle to fp32 rounding. For 16-bit
+inputs each norm is rounded to the input dtype, as x.norm() returns it; the kernel's
+fp32 sum of squares runs in another order than torch's, so a norm can land one unit in
+the last place of the 16-bit type away (about 1 norm in 10^4). The tests bound the
+fraction of such tokens instead of requiring equality."""
+import numpy as np
+import pytest
+import torch
+
+from dsalt import _hip
+from dsalt.kernels.landmark_tokens_ker import hybrid_scores_from_v
+from dsalt.kernels.selectors import _compute_landmark_indices
+from oracle import dsalt_oracle as orc
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def _inputs(T, d, n_kv, dh, H, seed, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, d, generator=g) * (1 + torch.rand(T, 1, generator=g))
+    W = torch.randn(n_kv * dh, d, generator=g) / d ** 0.5
+    alpha = torch.rand(H, generator=g)
+    v = (x @ W.T).view(T, n_kv, dh)
+    return x.to(dtype), v.to(dtype), alpha, W
+
+
+@pytest.mark.parametrize("n_kv", [16, 4], ids=["mha", "gqa"])
+def test_scores_fp32_match_oracle(n_kv):
+    print(f"scores fp32 n_kv={n_kv}", flush=True)
+    T, d, H, dh = 3000, 1024, 16, 64
+    x, v, alpha, _ = _inputs(T, d, n_kv, dh, H, 70)
+    s, zx, zv = _hip.hybrid_scores(x.to(DEV), v.to(DEV), alpha.to(DEV), H)
+    rs, rzx, rzv = orc.hybrid_scores_from_v(x.double(), v.double(), alpha.double(), H)
+    for got, ref, name in ((s, rs, "scores"), (zx, rzx, "z_x"), (zv, rzv, "z_v")):
+        err = (got.cpu().double() - ref).abs().max().item()
+        assert err < 2e-5, f"{name} max-abs error {err}"
+
+
+@pytest.mark.parametrize("xdt,vdt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                     (torch.float32, torch.bfloat16)], ids=["bf16", "fp16", "autocast"])
+def test_scores_16bit_match_oracle(xdt, vdt):
+    print(f"scores {xdt} {vdt}", flush=True)
+    T, d, H, dh, n_kv = 4096, 1024, 16, 64, 16
+    x, v, alpha, _ = _inputs(T, d, n_kv, dh, H, 71)
+    x, v = x.to(xdt), v.to(vdt)
+    s, zx, zv = _hip.hybrid_scores(x.to(DEV), v.to(DEV), alpha.to(DEV), H)
+    # the oracle takes the norms in the same 16-bit dtype (rounded there, then .float())
+    rs, rzx, rzv = orc.hybrid_scores_from_v(x, v, alpha, H)
+    for got, ref, name in ((s, rs, "scores"), (zx, rzx, "z_x"), (zv, rzv, "z_v")):
+        diff = (got.cpu() - ref).abs()
+        frac = (diff > 1e-4).float().mean().item()
+        assert frac < 2e-3, f"{name}: {frac:.2e} of the entries differ by more than 1e-4"
+        # one 16-bit ulp of a norm moves z by at most ulp(norm) / std
+        assert diff.max().item() < 0.5, f"{name} max-abs error {diff.max().item()}"
+
+
+def test_scores_deterministic_strided_and_tiny():
+    T, d, H, dh, n_kv = 1000, 256, 8, 128, 2
+    x, v, alpha, _ = _inputs(T, d, n_kv, dh, H, 72, torch.bfloat16)
+    wide = torch.zeros(T, d + 64, dtype=torch.bfloat16)
+    wide[:, 16:16 + d] = x  # row stride d + 64, 32-byte offset: still 16-byte aligned rows
+    xs = wide.to(DEV)[:, 16:16 + d]
+    a = _hip.hybrid_scores(xs, v.to(DEV), alpha.to(DEV), H)
+    b = _hip.hybrid_scores(x.to(DEV), v.to(DEV), alpha.to(DEV), H)
+    for p, q in zip(a, b):
+        assert torch.equal(p, q)  # same values, run to run and across strides
+    # one token: std = NaN (0/0), kept by the clamp, as torch.std gives
+    s1, zx1, _ = _hip.hybrid_scores(x[:1].to(DEV), v[:1].to(DEV), alpha.to(DEV), H)
+    assert torch.isnan(s1).all() and torch.isnan(zx1).all()
+    rs1, _, _ = orc.hybrid_scores_from_v(x[:1], v[:1], alpha, H)
+    assert torch.isnan(rs1).all()
+
+
+def test_selection_from_v_matches_gemm_path():
+    # the selector with v= (fused scores) against the oracle selection of the same
+    # scores (bit-exact), and against the GEMM path's selection (same sets up to ties)
+    g = torch.Generator().manual_seed(73)
+    lens = [700, 333, 1100]
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
+    T, d, H, dh, k = int(cu[-1]), 512, 8, 64, 32
+    x, v, alpha, W = _inputs(T, d, H, dh, H, 74)
+    w = (torch.rand(T, generator=g) * 200 + 1).floor()
+    lmk_v, _, _ = _compute_landmark_indices(x.to(DEV), W.to(DEV), alpha.to(DEV), w.to(DEV), cu.to(DEV), k, 1, T,
+                                            cu.tolist(), head_dim=dh, v=v.to(DEV))
+    s_v, _, _ = _hip.hybrid_scores(x.to(DEV), v.to(DEV), alpha.to(DEV), H)
+    np.testing.assert_array_equal(lmk_v.cpu().numpy(), orc.select_landmarks(s_v.cpu().numpy(), w.numpy(), cu.numpy(), k))
+    lmk_w, _, _ = _compute_landmark_indices(x.to(DEV), W.to(DEV), alpha.to(DEV), w.to(DEV), cu.to(DEV), k, 1, T,
+                                            cu.tolist(), head_dim=dh)
+    same = (lmk_v == lmk_w).float().mean().item()
+    assert same > 0.99, f"only {same:.4f} of the landmark slots agree with the GEMM path"
+
+
+def test_differentiable_scores_from_v_match_kernel_and_grad():
+    T, d, H, dh, n_kv = 500, 256, 4, 64, 2
+    x, v, alpha, W = _inputs(T, d, n_kv, dh, H, 75)
+    xd, Wd, ad = x.to(DEV).requires_grad_(), W.to(DEV).requires_grad_(), alpha.to(DEV).requires_grad_()
+    s_t, _, _ = hybrid_scores_from_v(xd, (xd @ Wd.T).view(T, n_kv, dh), ad, H)
+    s_k, _, _ = _hip.hybrid_scores(x.to(DEV), v.to(DEV), alpha.to(DEV), H)
+    assert (s_t.detach() - s_k).abs().max().item() < 1e-4
+    s_t.square().sum().backward()
+    xr, Wr, ar = x.double().requires_grad_(), W.double().requires_grad_(), alpha.double().requires_grad_()
+    s_r, _, _ = orc.hybrid_scores(xr, Wr, ar, H, dh)
+    s_r.square().sum().backward()
+    for got, ref in ((xd.grad, xr.grad), (Wd.grad, Wr.grad), (ad.grad, ar.grad)):
+        rel = (got.cpu().double() - ref).norm() / ref.norm()
+        assert rel < 1e-4, rel
+
+
+@pytest.mark.parametrize("training", [False, True], ids=["eval", "train"])
+def test_module_fused_selector(training):
+    from dsalt.modules import DSALTAttention
+    torch.manual_seed(5)
+    m = DSALTAttention(256, 4, 16, 128, 16, max_seq_len=1024).to(DEV)
+    m.train(training)
+    m._collect_last_P = False
+    lens = [600, 424]
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=DEV)
+    x = torch.randn(int(cu[-1]), 256, device=DEV)
+    outs = []
+    for fused in (True, False):
+        m._fused_selector = fused
+        out, _ = m(x, cu_seqlens=cu, cu_list=cu.tolist())
+        outs.append(out.detach())
+    err = (outs[0] - outs[1]).abs().max().item()
+    assert err < 2e-2, f"fused vs GEMM selector output differs by {err}"

@@ -189,6 +189,33 @@ def test_hybrid_scores_against_numpy():
     np.testing.assert_allclose(s.numpy(), alpha * zv_ref + (1 - alpha) * zx_ref[:, None], rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("n_kv", [4, 2, 1], ids=["mha", "gqa2", "mqa"])
+def test_hybrid_scores_from_v_is_the_gemm_path(n_kv):
+    # given v = x W_V^T, the from-v restatement is the same computation as hybrid_scores
+    # (landmark_tokens_ker.py:45-61), bit for bit in float64; GQA repeats z_v per group
+    rng = np.random.default_rng(4)
+    T, d, H, dh = 40, 32, 4, 8
+    x = torch.from_numpy(rng.standard_normal((T, d)))
+    W = torch.from_numpy(rng.standard_normal((n_kv * dh, d)))
+    alpha = torch.from_numpy(rng.random(H))
+    ref = orc.hybrid_scores(x, W, alpha, H, dh)
+    got = orc.hybrid_scores_from_v(x, (x @ W.T).view(T, n_kv, dh), alpha, H)
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+    # and against numpy, with the group repeat written out
+    vn = np.linalg.norm((x.numpy() @ W.numpy().T).reshape(T, n_kv, dh), axis=2)
+    zv = np.repeat((vn - vn.mean(0)) / vn.std(0, ddof=1), H // n_kv, axis=1)
+    np.testing.assert_allclose(got[2].numpy(), zv, rtol=1e-5, atol=1e-5)  # .float(): fp32 norms
+
+
+def test_hybrid_scores_single_token_is_nan():
+    # one token: the unbiased std is 0/0 = NaN, clamp(min=1e-6) keeps it (torch semantics)
+    x = torch.ones(1, 8, dtype=torch.float64)
+    s, zx, zv = orc.hybrid_scores_from_v(x, torch.ones(1, 2, 4, dtype=torch.float64),
+                                         torch.full((2,), 0.5, dtype=torch.float64), 2)
+    assert torch.isnan(s).all() and torch.isnan(zx).all()
+
+
 # ---------------------------------------------------------------- gradients
 
 def test_gradcheck_hard():
