@@ -225,6 +225,50 @@ def time_launches(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def measure_front_end(wl, w, cu, sel) -> dict:
+    """The inference selection path in bf16 at the workload's shape: hybrid scores + top-k,
+    by the reference's route (x @ W_V^T GEMM, norms and standardisation in torch,
+    landmark_tokens_ker.py:45-61) and by the fused one (dsalt_hybrid_scores on the
+    module's value projection). Both eager, launch costs included; the fused scores also
+    from a HIP graph (GPU time alone). HBM bytes of the fused score kernels: x and v read
+    once (bf16), norms and scores written and read back (fp32)."""
+    from dsalt import _hip
+    from dsalt.kernels.landmark_tokens_ker import hybrid_scores_per_head
+    mod, T, H, D = wl["mod"], wl["T"], wl["H"], wl["D"]
+    with torch.no_grad():
+        xb = wl["xp"].to(torch.bfloat16)
+        Wb = mod.v_proj.weight.to(torch.bfloat16)
+        vb = (xb @ Wb.T).view(T, H, D)
+        alpha = mod._alpha().float()
+    k = wl["k_lmk"]
+
+    def gemm_path():
+        s, _, _ = hybrid_scores_per_head(xb, Wb, alpha, H, D)
+        _hip.select_landmarks(s, w, cu, k)
+
+    scores = _hip.ScoresLauncher(xb, vb, alpha, H)
+    sel_f = _hip.SelectLauncher(scores.scores, w, cu, k)
+
+    def fused_path():
+        scores()
+        sel_f()
+
+    with torch.no_grad():
+        gemm_ms = time_launches(gemm_path, 50, 10)
+        fused_ms = time_launches(fused_path, 50, 10)
+        scores_graph_ms = time_graph(scores)
+    d = xb.shape[1]
+    bytes_scores = 2 * T * d + 2 * T * H * D + 4 * T * (1 + H) * 2 + 4 * T * H * 3
+    return {
+        "workload": "c2 inference selection (hybrid scores + top-k), bf16 x / W_V / v",
+        "gemm_path_us": gemm_ms * 1e3,
+        "fused_path_us": fused_ms * 1e3,
+        "fused_scores_graph_us": scores_graph_ms * 1e3,
+        "fused_scores_GB/s": bytes_scores / (scores_graph_ms * 1e-3) / 1e9,
+        "gemm_flops_saved": 2.0 * T * d * H * D,
+    }
+
+
 def cpu_baseline(wl, budget_s: float = 12.0):
     """The reference's CPU fallback cost (dense HARD mask + fp32 SDPA), restated in
     oracle/, timed on this host on one sequence of the workload (all heads)."""
@@ -308,6 +352,7 @@ def main():
     sel_ms = time_graph(sel)
     qz_ms = time_graph(_hip.QuantizeLauncher(w_cont))
     bytes_sel = 4 * T * H + 4 * T + 4 * (wl["B"] + 1) + 8 * H * wl["B"] * wl["k_lmk"]
+    front = measure_front_end(wl, w, cu, sel)
 
     # cold HBM: launches rotate over input sets whose total (> 512 MB) exceeds the
     # 256 MB last-level cache, so every launch reads Q, K and V from HBM
@@ -384,6 +429,7 @@ def main():
         "select": {"us": sel_ms * 1e3, "GB/s": bytes_sel / (sel_ms * 1e-3) / 1e9, "bytes": bytes_sel},
         "quantize_ms": qz_ms,
         "path_ms": ms + sel_ms + qz_ms,
+        "selector_front_end": front,
     }
     if not args.no_backward:
         res["backward"] = measure_backward(dev)

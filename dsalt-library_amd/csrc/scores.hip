@@ -7,23 +7,23 @@
 // attention module has that product already (its pre-RoPE value projection v), so this
 // path takes v and reads each of x and v once.
 //
-// Two kernels, deterministic (no atomics, fixed reduction orders):
-//  1. norms_kernel: one workgroup per 32 tokens. ||x_t|| and ||v_t,g|| in fp32, each
-//     rounded to its input's dtype (what .norm() returns for a 16-bit tensor, before
-//     .float(); under autocast x is fp32 and v bf16),
-//     written to the workspace, plus the workgroup's fp64 partial sums of each quantity
-//     and of its square.
-//  2. standardize_kernel: every workgroup reduces the partials in the same order, takes
-//     the mean and the unbiased std in fp64 (rounded to fp32, std clamped at 1e-6 with
-//     NaN kept), and writes z_x, z_v and the scores with the reference's fp32 operation
-//     order (no FMA contraction).
+// Three kernels, deterministic (no atomics, fixed reduction orders):
+//  1. norms_kernel: one wave per token, 16 tokens per workgroup. ||x_t|| and ||v_t,g||
+//     in fp32, each rounded to its input's dtype (what .norm() returns for a 16-bit
+//     tensor, before .float(); under autocast x is fp32 and v bf16), written to the
+//     workspace, plus the workgroup's fp64 partial sums of each quantity and its square.
+//  2. stats_kernel (one workgroup): the partials summed in a fixed order (lanes stride
+//     the blocks, then a fixed shuffle tree), the mean and the unbiased std in fp64,
+//     rounded to fp32, the std clamped at 1e-6 with NaN kept.
+//  3. standardize_kernel: z_x, z_v and the scores, elementwise, with the reference's
+//     fp32 operation order (no FMA contraction).
 #include "common.h"
 #include "launch.h"
 
 namespace dsalt {
 namespace {
 
-constexpr int kNormTokens = 32;    // tokens per workgroup of norms_kernel
+constexpr int kNormTokens = 16;    // tokens (= waves) per workgroup of norms_kernel
 constexpr int kStdTokens = 64;     // tokens per workgroup of standardize_kernel
 constexpr int kMaxKvScores = 128;  // largest n_kv_heads (LDS of norms_kernel)
 
@@ -33,6 +33,7 @@ struct ScoreParams {
     float *scores, *z_x, *z_v;
     float *xn, *vn;   // workspace: [T], [T, n_kv]
     double *part;     // workspace: [nblk][1 + n_kv][2]
+    float *stats;     // workspace: [1 + n_kv][2] (mean, std)
     int64_t x_st, v_st, v_sh, s_st, s_sh, zv_st, zv_sh;
     int T, d, n_kv, D, H, nblk;
 };
@@ -97,7 +98,7 @@ __device__ __forceinline__ float group_sum(float x, int width) {
 }
 
 template <typename LX, typename LV>
-__global__ void __launch_bounds__(256) norms_kernel(const ScoreParams p) {
+__global__ void __launch_bounds__(64 * kNormTokens) norms_kernel(const ScoreParams p) {
     constexpr int EX = LX::E, EV = LV::E;
     constexpr int BX = EX == 8 ? 2 : 4, BV = EV == 8 ? 2 : 4;  // bytes per element
     __shared__ float s_n[kNormTokens][1 + kMaxKvScores];
@@ -105,9 +106,8 @@ __global__ void __launch_bounds__(256) norms_kernel(const ScoreParams p) {
     const int t0 = blockIdx.x * kNormTokens;
     const int G = p.D / EV;         // lanes per v row
     const int rows_per = 64 / G;    // v rows per load instruction
-    for (int j = wave; j < kNormTokens; j += 4) {
-        const int t = t0 + j;
-        if (t >= p.T) break;  // wave-uniform
+    const int j = wave, t = t0 + wave;
+    if (t < p.T) {  // wave-uniform
         // ||x_t||: lanes stride the row in 16-byte chunks
         const char *xr = static_cast<const char *>(p.x) + (int64_t)t * p.x_st * BX;
         float sx = 0.f;
@@ -148,23 +148,37 @@ __global__ void __launch_bounds__(256) norms_kernel(const ScoreParams p) {
     }
 }
 
-__global__ void __launch_bounds__(256) standardize_kernel(const ScoreParams p) {
-#pragma clang fp contract(off)
-    __shared__ float s_mean[1 + kMaxKvScores], s_std[1 + kMaxKvScores];
-    for (int q = threadIdx.x; q <= p.n_kv; q += blockDim.x) {
+__global__ void __launch_bounds__(1024) stats_kernel(const ScoreParams p) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int q = wave; q <= p.n_kv; q += 16) {  // wave-uniform
         double s = 0.0, s2 = 0.0;
-        for (int b = 0; b < p.nblk; ++b) {
+        for (int b = lane; b < p.nblk; b += 64) {
             const double *o = p.part + ((int64_t)b * (1 + p.n_kv) + q) * 2;
             s += o[0];
             s2 += o[1];
         }
-        const double n = (double)p.T;
-        const double mean = s / n;
-        // unbiased variance; T = 1 gives 0/0 = NaN, as torch.std does
-        const double var = fmax(s2 - s * mean, 0.0) / (n - 1.0);
-        const float sd = (float)sqrt(var);
-        s_mean[q] = (float)mean;
-        s_std[q] = (sd != sd) ? sd : fmaxf(sd, 1e-6f);  // clamp(min=1e-6) keeps NaN
+        for (int off = 1; off < 64; off <<= 1) {
+            s += __shfl_xor(s, off);
+            s2 += __shfl_xor(s2, off);
+        }
+        if (lane == 0) {
+            const double n = (double)p.T;
+            const double mean = s / n;
+            // unbiased variance; T = 1 gives 0/0 = NaN, as torch.std does
+            const double var = fmax(s2 - s * mean, 0.0) / (n - 1.0);
+            const float sd = (float)sqrt(var);
+            p.stats[2 * q] = (float)mean;
+            p.stats[2 * q + 1] = (sd != sd) ? sd : fmaxf(sd, 1e-6f);  // clamp(min=1e-6) keeps NaN
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) standardize_kernel(const ScoreParams p) {
+#pragma clang fp contract(off)
+    __shared__ float s_mean[1 + kMaxKvScores], s_std[1 + kMaxKvScores];
+    for (int q = threadIdx.x; q <= p.n_kv; q += blockDim.x) {
+        s_mean[q] = p.stats[2 * q];
+        s_std[q] = p.stats[2 * q + 1];
     }
     __syncthreads();
     const int rep = p.H / p.n_kv;
@@ -188,11 +202,11 @@ size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 template <typename LX>
 void launch_norms_x(int v_dtype, const ScoreParams &p, hipStream_t stream) {
     if (v_dtype == DSALT_DTYPE_BF16)
-        hipLaunchKernelGGL((norms_kernel<LX, LdBF16>), dim3(p.nblk), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((norms_kernel<LX, LdBF16>), dim3(p.nblk), dim3(64 * kNormTokens), 0, stream, p);
     else if (v_dtype == DSALT_DTYPE_F16)
-        hipLaunchKernelGGL((norms_kernel<LX, LdF16>), dim3(p.nblk), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((norms_kernel<LX, LdF16>), dim3(p.nblk), dim3(64 * kNormTokens), 0, stream, p);
     else
-        hipLaunchKernelGGL((norms_kernel<LX, LdF32>), dim3(p.nblk), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((norms_kernel<LX, LdF32>), dim3(p.nblk), dim3(64 * kNormTokens), 0, stream, p);
 }
 
 void launch_norms(int x_dtype, int v_dtype, const ScoreParams &p, hipStream_t stream) {
@@ -206,7 +220,7 @@ void launch_norms(int x_dtype, int v_dtype, const ScoreParams &p, hipStream_t st
 int64_t scores_workspace_bytes(int total_len, int n_kv) {
     const int nblk = (total_len + kNormTokens - 1) / kNormTokens;
     return (int64_t)(align256((size_t)total_len * 4) + align256((size_t)total_len * n_kv * 4) +
-                     align256((size_t)nblk * (1 + n_kv) * 2 * 8));
+                     align256((size_t)nblk * (1 + n_kv) * 2 * 8) + align256((size_t)(1 + n_kv) * 2 * 4));
 }
 
 int scores_max_kv() { return kMaxKvScores; }
@@ -232,6 +246,8 @@ hipError_t launch_scores(const dsalt_scores_args &a, hipStream_t stream) {
     p.vn = reinterpret_cast<float *>(ws);
     ws += align256((size_t)p.T * p.n_kv * 4);
     p.part = reinterpret_cast<double *>(ws);
+    ws += align256((size_t)p.nblk * (1 + p.n_kv) * 2 * 8);
+    p.stats = reinterpret_cast<float *>(ws);
     p.x_st = a.x_stride_t;
     p.v_st = a.v_stride_t;
     p.v_sh = a.v_stride_h;
@@ -242,6 +258,8 @@ hipError_t launch_scores(const dsalt_scores_args &a, hipStream_t stream) {
     launch_norms(a.x_dtype, a.v_dtype, p, stream);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(stats_kernel, dim3(1), dim3(1024), 0, stream, p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(standardize_kernel, dim3((p.T + kStdTokens - 1) / kStdTokens), dim3(256), 0, stream, p);
     return hipGetLastError();
 }

@@ -468,6 +468,26 @@ def hybrid_scores(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads
     return scores, z_x, z_v
 
 
+class ScoresLauncher:
+    """hybrid_scores with its argument block, outputs and workspace built once: each call
+    launches the two score kernels on the current stream (for timing loops and graph
+    capture); `scores`, `z_x`, `z_v` hold the result."""
+
+    def __init__(self, x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int):
+        self.device = require_gpu(x, v, alpha)
+        self._keep = (x, v, alpha.detach().to(torch.float32).contiguous())
+        T = x.shape[0]
+        self.scores = torch.empty((T, n_heads), device=self.device, dtype=torch.float32)
+        self.z_x = torch.empty((T,), device=self.device, dtype=torch.float32)
+        self.z_v = torch.empty((T, n_heads), device=self.device, dtype=torch.float32)
+        self._ws = torch.empty((scores_workspace_size(T, v.shape[1]),), device=self.device, dtype=torch.uint8)
+        self._args = scores_args(x, v, self._keep[2], n_heads, self.scores, self.z_x, self.z_v, self._ws)
+        _raise(lib().dsalt_scores_check(ctypes.byref(self._args)), "dsalt_scores_check")
+
+    def __call__(self) -> None:
+        _raise(lib().dsalt_hybrid_scores(ctypes.byref(self._args), stream_handle(self.device)), "dsalt_hybrid_scores")
+
+
 class SelectLauncher:
     """select_landmarks with its argument block built once: each call launches the
     selection kernel on the current stream (for timing loops); `out` holds the result."""
