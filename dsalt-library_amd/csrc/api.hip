@@ -64,6 +64,7 @@ size_t dsalt_fwd_args_size(void) { return sizeof(dsalt_fwd_args); }
 size_t dsalt_bwd_args_size(void) { return sizeof(dsalt_bwd_args); }
 size_t dsalt_select_args_size(void) { return sizeof(dsalt_select_args); }
 size_t dsalt_scores_args_size(void) { return sizeof(dsalt_scores_args); }
+size_t dsalt_rope_args_size(void) { return sizeof(dsalt_rope_args); }
 
 int dsalt_fwd_check(const dsalt_fwd_args *a) {
     if (!a) return fail(DSALT_ERR_INVALID, "args is NULL");
@@ -177,6 +178,36 @@ int dsalt_hybrid_scores(const dsalt_scores_args *a, void *stream) {
     hipError_t e = dsalt::launch_scores(*a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess)
         return fail(DSALT_ERR_LAUNCH, "dsalt_hybrid_scores launch failed: %s", hipGetErrorString(e));
+    return DSALT_OK;
+}
+
+int dsalt_rope_check(const dsalt_rope_args *a) {
+    if (!a) return fail(DSALT_ERR_INVALID, "args is NULL");
+    if (a->total_len < 0 || a->n_q_heads < 0 || a->n_k_heads < 0)
+        return fail(DSALT_ERR_INVALID, "total_len and head counts must be >= 0");
+    if (a->head_dim < 2 || a->head_dim % 2) return fail(DSALT_ERR_INVALID, "head_dim must be even and >= 2");
+    if (a->dtype != DSALT_DTYPE_BF16 && a->dtype != DSALT_DTYPE_F16 && a->dtype != DSALT_DTYPE_F32)
+        return fail(DSALT_ERR_INVALID, "dtype must be DSALT_DTYPE_BF16, _F16 or _F32 (got %d)", a->dtype);
+    if (a->transpose != 0 && a->transpose != 1) return fail(DSALT_ERR_INVALID, "transpose must be 0 or 1");
+    if (a->total_len == 0) return DSALT_OK;
+    if ((a->n_q_heads && (!a->q || !a->q_out)) || (a->n_k_heads && (!a->k || !a->k_out)) || !a->cos || !a->sin)
+        return fail(DSALT_ERR_INVALID, "q, k, their outputs, cos and sin must be non-NULL");
+    if (a->cos_sin_stride < a->head_dim) return fail(DSALT_ERR_INVALID, "cos_sin_stride must be >= head_dim");
+    if (a->table_rows < 1) return fail(DSALT_ERR_INVALID, "table_rows must be >= 1");
+    if (!a->cu_seqlens && a->table_rows < a->total_len)
+        return fail(DSALT_ERR_INVALID, "per-token tables need total_len (%d) rows (got %d)", a->total_len, a->table_rows);
+    if (a->cu_seqlens && a->num_seqs < 1) return fail(DSALT_ERR_INVALID, "num_seqs must be >= 1 with cu_seqlens");
+    for (int64_t st : {a->q_stride_t, a->q_stride_h, a->k_stride_t, a->k_stride_h, a->q_out_stride_t,
+                       a->q_out_stride_h, a->k_out_stride_t, a->k_out_stride_h})
+        if (st < 0) return fail(DSALT_ERR_INVALID, "strides must be non-negative");
+    return DSALT_OK;
+}
+
+int dsalt_rope(const dsalt_rope_args *a, void *stream) {
+    int rc = dsalt_rope_check(a);
+    if (rc) return rc;
+    hipError_t e = dsalt::launch_rope(*a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(DSALT_ERR_LAUNCH, "dsalt_rope launch failed: %s", hipGetErrorString(e));
     return DSALT_OK;
 }
 

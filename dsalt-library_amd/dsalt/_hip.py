@@ -100,12 +100,25 @@ class ScoresArgs(ctypes.Structure):
     ]
 
 
+class RopeArgs(ctypes.Structure):
+    _fields_ = [
+        ("total_len", c_int32), ("num_seqs", c_int32), ("n_q_heads", c_int32), ("n_k_heads", c_int32),
+        ("head_dim", c_int32), ("dtype", c_int32), ("transpose", c_int32), ("table_rows", c_int32),
+        ("q", c_void_p), ("q_stride_t", c_int64), ("q_stride_h", c_int64),
+        ("k", c_void_p), ("k_stride_t", c_int64), ("k_stride_h", c_int64),
+        ("q_out", c_void_p), ("q_out_stride_t", c_int64), ("q_out_stride_h", c_int64),
+        ("k_out", c_void_p), ("k_out_stride_t", c_int64), ("k_out_stride_h", c_int64),
+        ("cos", c_void_p), ("sin", c_void_p), ("cos_sin_stride", c_int64),
+        ("cu_seqlens", c_void_p),
+    ]
+
+
 EXPORTED_SYMBOLS = (
     "dsalt_fwd", "dsalt_fwd_check", "dsalt_bwd", "dsalt_bwd_check", "dsalt_bwd_workspace_size",
     "dsalt_select_landmarks", "dsalt_select_check", "dsalt_quantize_windows",
     "dsalt_abi_version", "dsalt_last_error", "dsalt_fwd_args_size", "dsalt_bwd_args_size",
     "dsalt_select_args_size", "dsalt_hybrid_scores", "dsalt_scores_check", "dsalt_scores_workspace_size",
-    "dsalt_scores_args_size",
+    "dsalt_scores_args_size", "dsalt_rope", "dsalt_rope_check", "dsalt_rope_args_size",
 )
 
 _lib = None
@@ -130,6 +143,8 @@ def lib() -> ctypes.CDLL:
         ("dsalt_select_check", [ctypes.POINTER(SelectArgs)]),
         ("dsalt_hybrid_scores", [ctypes.POINTER(ScoresArgs), c_void_p]),
         ("dsalt_scores_check", [ctypes.POINTER(ScoresArgs)]),
+        ("dsalt_rope", [ctypes.POINTER(RopeArgs), c_void_p]),
+        ("dsalt_rope_check", [ctypes.POINTER(RopeArgs)]),
         ("dsalt_quantize_windows", [c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
     ):
         fn = getattr(h, name)
@@ -141,7 +156,8 @@ def lib() -> ctypes.CDLL:
     h.dsalt_scores_workspace_size.restype = c_int64
     h.dsalt_abi_version.restype = ctypes.c_int
     h.dsalt_last_error.restype = ctypes.c_char_p
-    for n in ("dsalt_fwd_args_size", "dsalt_bwd_args_size", "dsalt_select_args_size", "dsalt_scores_args_size"):
+    for n in ("dsalt_fwd_args_size", "dsalt_bwd_args_size", "dsalt_select_args_size", "dsalt_scores_args_size",
+              "dsalt_rope_args_size"):
         getattr(h, n).restype = c_size_t
     _lib = h
     check_abi()
@@ -153,7 +169,8 @@ def check_abi() -> None:
     if h.dsalt_abi_version() != ABI_VERSION:
         raise DsaltError(f"ABI version mismatch: library {h.dsalt_abi_version()} vs binding {ABI_VERSION}")
     for struct, fn in ((FwdArgs, h.dsalt_fwd_args_size), (BwdArgs, h.dsalt_bwd_args_size),
-                       (SelectArgs, h.dsalt_select_args_size), (ScoresArgs, h.dsalt_scores_args_size)):
+                       (SelectArgs, h.dsalt_select_args_size), (ScoresArgs, h.dsalt_scores_args_size),
+                       (RopeArgs, h.dsalt_rope_args_size)):
         if ctypes.sizeof(struct) != fn():
             raise DsaltError(f"{struct.__name__} layout mismatch: {ctypes.sizeof(struct)} vs {fn()} bytes")
 
@@ -466,6 +483,40 @@ def hybrid_scores(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads
     a = scores_args(x, v, alpha, n_heads, scores, z_x, z_v, ws)
     _raise(lib().dsalt_hybrid_scores(ctypes.byref(a), stream_handle(dev)), "dsalt_hybrid_scores")
     return scores, z_x, z_v
+
+
+def rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+         cu_seqlens: torch.Tensor | None = None, transpose: bool = False,
+         q_out: torch.Tensor | None = None, k_out: torch.Tensor | None = None):
+    """Rotary embedding of q [T, Hq, D] and k [T, Hk, D] (half-split) with fp32 tables
+    cos/sin [rows, D]: rows are positions inside the sequence when cu_seqlens is given,
+    tokens otherwise. ``transpose`` applies the backward rotation. Returns (q_out, k_out)."""
+    dev = require_gpu(q, k, cos, sin, cu_seqlens)
+    if q.dtype != k.dtype or q.dtype not in _SCORE_DTYPES:
+        raise DsaltError(f"q and k must share a dtype of bf16, fp16 or fp32 (got {q.dtype}, {k.dtype})")
+    if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise DsaltError(f"q and k must be [T, H, D] with the same T and D (got {tuple(q.shape)}, {tuple(k.shape)})")
+    q = q if q.stride(2) == 1 else q.contiguous()
+    k = k if k.stride(2) == 1 else k.contiguous()
+    cos = cos.to(torch.float32).contiguous()
+    sin = sin.to(torch.float32).contiguous()
+    if cos.dim() != 2 or cos.shape != sin.shape or cos.shape[1] != q.shape[2]:
+        raise DsaltError(f"cos and sin must be [rows, {q.shape[2]}] (got {tuple(cos.shape)}, {tuple(sin.shape)})")
+    q_out = torch.empty_like(q) if q_out is None else q_out
+    k_out = torch.empty_like(k) if k_out is None else k_out
+    cu = _cu_i32(cu_seqlens) if cu_seqlens is not None else None
+    a = RopeArgs()
+    a.total_len, a.n_q_heads, a.n_k_heads, a.head_dim = q.shape[0], q.shape[1], k.shape[1], q.shape[2]
+    a.num_seqs = cu.shape[0] - 1 if cu is not None else 1
+    a.dtype, a.transpose, a.table_rows = _SCORE_DTYPES[q.dtype], int(bool(transpose)), cos.shape[0]
+    a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+    a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
+    a.q_out, a.q_out_stride_t, a.q_out_stride_h = q_out.data_ptr(), q_out.stride(0), q_out.stride(1)
+    a.k_out, a.k_out_stride_t, a.k_out_stride_h = k_out.data_ptr(), k_out.stride(0), k_out.stride(1)
+    a.cos, a.sin, a.cos_sin_stride = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+    a.cu_seqlens = _ptr(cu)
+    _raise(lib().dsalt_rope(ctypes.byref(a), stream_handle(dev)), "dsalt_rope")
+    return q_out, k_out
 
 
 class ScoresLauncher:

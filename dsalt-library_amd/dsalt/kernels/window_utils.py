@@ -3,11 +3,43 @@
 ``build_rope_cache`` and ``apply_rotary_emb`` follow dsalt/kernels/window_utils.py:73-107
 (half-split rotation, positions divided by the YaRN scale). The reference wraps
 ``apply_rotary_emb`` in ``torch.compile``; here it runs eagerly, so no generated
-kernels enter the path.
+kernels enter the path. The module itself uses :func:`apply_rotary_emb_packed`, the
+HIP kernel ``dsalt_rope`` (one pass over q and k, positions from cu_seqlens in-kernel,
+the compiled function's fp32 arithmetic with one rounding), with its transposed
+rotation as the backward.
 """
 from __future__ import annotations
 
 import torch
+
+from .. import _hip
+
+
+class _RopeFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, cos, sin, cu_seqlens):
+        ctx.save_for_backward(cos, sin, cu_seqlens)
+        ctx.has_cu = cu_seqlens is not None
+        return _hip.rope(q, k, cos, sin, cu_seqlens)
+
+    @staticmethod
+    def backward(ctx, gq, gk):
+        cos, sin, cu = ctx.saved_tensors
+        q_shape, k_shape = gq.shape if gq is not None else None, gk.shape if gk is not None else None
+        gq = gq if gq is not None else torch.zeros(q_shape or gk.shape, device=gk.device, dtype=gk.dtype)
+        gk = gk if gk is not None else torch.zeros(k_shape or gq.shape, device=gq.device, dtype=gq.dtype)
+        dq, dk = _hip.rope(gq, gk, cos, sin, cu if ctx.has_cu else None, transpose=True)
+        return dq, dk, None, None, None
+
+
+def apply_rotary_emb_packed(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                            cu_seqlens: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """RoPE of packed ``q [T, Hq, D]``, ``k [T, Hk, D]`` on the GPU (differentiable in q and
+    k). ``cos``/``sin`` are fp32 tables ``[rows, D]``: with ``cu_seqlens`` row p is the
+    position p inside a sequence (the module's rope_cos / rope_sin,
+    dsalt_attention.py:570-585); without, row t is token t (the module's ``rope_cs``).
+    They are rounded to q's dtype, as the module's ``cos.to(q.dtype)`` does."""
+    return _RopeFunction.apply(q, k, cos, sin, cu_seqlens)
 
 
 def apply_rotary_emb(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor,

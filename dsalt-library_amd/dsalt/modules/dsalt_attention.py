@@ -31,7 +31,7 @@ from .. import _hip
 from ..kernels._sparse import sparse_attention
 from ..kernels.landmark_tokens_ker import hybrid_scores_from_v, hybrid_scores_per_head
 from ..kernels.selectors import _compute_landmark_indices
-from ..kernels.window_utils import apply_rotary_emb, build_rope_cache
+from ..kernels.window_utils import apply_rotary_emb_packed, build_rope_cache
 
 
 def _dynamo_opaque(fn):
@@ -203,20 +203,13 @@ class DSALTAttention(nn.Module):
         # (qkv_bias=False only; with a bias v is not x W_V^T)
         v_sel = v if self.v_proj.bias is None else None
 
+        # RoPE in one HIP pass (dsalt_attention.py:570-585): positions from cu_seqlens
+        # in-kernel, cos/sin rounded to q's dtype as the reference's cos.to(q.dtype)
         if rope_cs is None:
-            num_seqs = cu_seqlens.shape[0] - 1
-            cu_l = cu_seqlens.long()
-            lens = cu_l[1:] - cu_l[:-1]
-            seq_ids = torch.repeat_interleave(torch.arange(num_seqs, device=device), lens,
-                                              output_size=total_len)
-            pos_ids = torch.arange(total_len, device=device) - cu_l[:-1][seq_ids]
-            cos = self.rope_cos[pos_ids]
-            sin = self.rope_sin[pos_ids]
+            q, k = apply_rotary_emb_packed(q, k, self.rope_cos, self.rope_sin, cu_seqlens)
         else:
             cos, sin = rope_cs
-        cos = cos.to(q.dtype)
-        sin = sin.to(q.dtype)
-        q, k = apply_rotary_emb(q, k, cos.unsqueeze(1), sin.unsqueeze(1))
+            q, k = apply_rotary_emb_packed(q, k, cos.reshape(total_len, -1), sin.reshape(total_len, -1))
         k = self._repeat_kv(k)
         v = self._repeat_kv(v)
 

@@ -217,6 +217,41 @@ int dsalt_hybrid_scores(const dsalt_scores_args *args, void *stream);
 int dsalt_scores_check(const dsalt_scores_args *args);
 
 /*
+ * Rotary position embedding of q and k (half-split convention) in one pass.
+ * Replaces apply_rotary_emb (dsalt/kernels/window_utils.py:73-88) as called by
+ * DSALTAttention._packed (dsalt/modules/dsalt_attention.py:570-585): cos/sin rows are
+ * rounded to the tensor dtype (the module's cos.to(q.dtype)), products and sums are
+ * fp32 (no FMA contraction) and each result is rounded once, as the reference's
+ * compiled function computes it. transpose = 1 applies the transposed rotation (the
+ * backward: q = gradient of the output, q_out = gradient of the input).
+ * cos, sin: fp32 tables with rows of head_dim entries (row stride cos_sin_stride). With
+ * cu_seqlens, token t of sequence s reads row t - cu_seqlens[s] (the table must hold
+ * max_s L_s rows, where the reference's table lookup would fail, rows past table_rows give
+ * NaN outputs); with cu_seqlens = NULL, row t. q_out / k_out may alias q / k.
+ * head_dim must be even; unit stride along head_dim.
+ */
+typedef struct dsalt_rope_args {
+    int32_t total_len, num_seqs, n_q_heads, n_k_heads, head_dim;
+    int32_t dtype; /* of q, k and the outputs: BF16, F16 or F32 */
+    int32_t transpose;
+    int32_t table_rows; /* rows of cos / sin; a token whose row is past them gets NaN */
+    const void *q;
+    int64_t q_stride_t, q_stride_h;
+    const void *k;
+    int64_t k_stride_t, k_stride_h;
+    void *q_out;
+    int64_t q_out_stride_t, q_out_stride_h;
+    void *k_out;
+    int64_t k_out_stride_t, k_out_stride_h;
+    const float *cos, *sin;
+    int64_t cos_sin_stride;
+    const int32_t *cu_seqlens; /* may be NULL */
+} dsalt_rope_args;
+
+int dsalt_rope(const dsalt_rope_args *args, void *stream);
+int dsalt_rope_check(const dsalt_rope_args *args);
+
+/*
  * Window quantisation w = max(1, floor(w~)) (NaN stays NaN), the floor/clamp of
  * DSALTAttention._window_sizes(floor=True) and of _train_selectors
  * (dsalt/modules/dsalt_attention.py:277-284, :471). Either output may be NULL; the
@@ -232,6 +267,7 @@ size_t dsalt_fwd_args_size(void);
 size_t dsalt_bwd_args_size(void);
 size_t dsalt_select_args_size(void);
 size_t dsalt_scores_args_size(void);
+size_t dsalt_rope_args_size(void);
 
 #ifdef __cplusplus
 }

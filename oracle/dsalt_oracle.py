@@ -69,6 +69,29 @@ def hybrid_scores_from_v(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, 
     return scores, z_x, z_v
 
 
+def rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, pos: torch.Tensor,
+         dtype: torch.dtype | None = None):
+    """Rotary embedding of the module path (window_utils.py:73-88 as called by
+    dsalt_attention.py:570-585): rows cos/sin[pos[t]] rounded to `dtype` (the module's
+    cos.to(q.dtype)), the half-split rotation computed in float64, the result rounded
+    once to `dtype` (as the reference's compiled function rounds its fp32 result)."""
+    dtype = dtype or q.dtype
+    c = cos[pos].to(dtype).double().unsqueeze(1)
+    s = sin[pos].to(dtype).double().unsqueeze(1)
+
+    def rot(x):
+        h = x.shape[-1] // 2
+        return torch.cat([-x[..., h:], x[..., :h]], dim=-1)
+
+    qd, kd = q.double(), k.double()
+    return (qd * c + rot(qd) * s).to(dtype), (kd * c + rot(kd) * s).to(dtype)
+
+
+def seq_positions(cu: list[int]) -> torch.Tensor:
+    """Offset of every packed token inside its sequence."""
+    return torch.cat([torch.arange(cu[i + 1] - cu[i]) for i in range(len(cu) - 1)])
+
+
 def window_continuous(win_logits: torch.Tensor, n_min: int, n_max: int) -> torch.Tensor:
     """w~ = n_min + sigmoid(logit) * (n_max - n_min); dsalt_attention.py:270-275."""
     return n_min + torch.sigmoid(win_logits) * (n_max - n_min)

@@ -220,3 +220,26 @@ def test_scores_check_fp32_and_gqa():
     assert lib.dsalt_scores_check(ctypes.byref(_scores_args(n_kv_heads=8, v_stride_t=512))) == 0
     assert lib.dsalt_scores_check(ctypes.byref(_scores_args(n_kv_heads=1, v_stride_t=64))) == 0
     assert lib.dsalt_scores_check(ctypes.byref(_scores_args(n_kv_heads=256, n_heads=256))) == 2
+
+
+def test_rope_check():
+    lib = hip.lib()
+    a = hip.RopeArgs()
+    a.total_len, a.num_seqs, a.n_q_heads, a.n_k_heads, a.head_dim = 100, 2, 4, 2, 64
+    a.dtype, a.transpose, a.table_rows = hip.DTYPE_BF16, 0, 80
+    a.q = a.k = a.q_out = a.k_out = 0x10000
+    a.cos, a.sin, a.cos_sin_stride, a.cu_seqlens = 0x20000, 0x30000, 64, 0x40000
+    assert lib.dsalt_rope_check(ctypes.byref(a)) == 0
+    assert ctypes.sizeof(hip.RopeArgs) == lib.dsalt_rope_args_size()
+    for field, value, needle in (("head_dim", 63, "even"), ("dtype", 9, "dtype"), ("transpose", 2, "transpose"),
+                                 ("cos_sin_stride", 32, "cos_sin_stride"), ("table_rows", 0, "table_rows"),
+                                 ("cos", 0, "non-NULL")):
+        old = getattr(a, field)
+        setattr(a, field, value)
+        assert lib.dsalt_rope_check(ctypes.byref(a)) == 1
+        assert needle in lib.dsalt_last_error().decode()
+        setattr(a, field, old)
+    a.cu_seqlens = None  # per-token tables need total_len rows
+    assert lib.dsalt_rope_check(ctypes.byref(a)) == 1
+    a.table_rows = 100
+    assert lib.dsalt_rope_check(ctypes.byref(a)) == 0

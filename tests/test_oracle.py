@@ -216,6 +216,28 @@ def test_hybrid_scores_single_token_is_nan():
     assert torch.isnan(s).all() and torch.isnan(zx).all()
 
 
+def test_rope_oracle_pins():
+    # against the package's eager restatement of window_utils.py:73-88 (float64), the
+    # identity at cos = 1, sin = 0, and norm preservation of every rotated pair
+    import sys
+    sys.path.insert(0, "dsalt-library_amd")
+    from dsalt.kernels.window_utils import apply_rotary_emb, build_rope_cache
+    g = torch.Generator().manual_seed(9)
+    cu = [0, 5, 12]
+    T, H, D = 12, 3, 8
+    q, k = torch.randn(T, H, D, generator=g, dtype=torch.float64), torch.randn(T, 2, D, generator=g, dtype=torch.float64)
+    cos, sin = build_rope_cache(16, D, torch.device("cpu"), dtype=torch.float64)
+    pos = orc.seq_positions(cu)
+    assert pos.tolist() == [0, 1, 2, 3, 4, 0, 1, 2, 3, 4, 5, 6]
+    rq, rk = orc.rope(q, k, cos, sin, pos)
+    eq, ek = apply_rotary_emb(q, k, cos[pos].unsqueeze(1), sin[pos].unsqueeze(1))
+    assert torch.allclose(rq, eq, atol=1e-14) and torch.allclose(rk, ek, atol=1e-14)
+    iq, _ = orc.rope(q, k, torch.ones_like(cos), torch.zeros_like(sin), pos)
+    assert torch.equal(iq, q)
+    pair = lambda x: x[..., : D // 2] ** 2 + x[..., D // 2:] ** 2
+    assert torch.allclose(pair(rq), pair(q), atol=1e-12)
+
+
 # ---------------------------------------------------------------- gradients
 
 def test_gradcheck_hard():
