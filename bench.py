@@ -269,6 +269,36 @@ def measure_front_end(wl, w, cu, sel) -> dict:
     }
 
 
+def measure_rope(wl, cu) -> dict:
+    """The module's RoPE at the workload's shape in bf16: the reference's route written
+    eagerly (position gather, cos/sin cast, rotation in torch ops; the reference compiles
+    it with Inductor, which is not used here) against dsalt_rope (one pass, from a HIP
+    graph). Bytes of dsalt_rope: q and k read and written once (bf16); the tables are a
+    few hundred KB and stay in cache."""
+    from dsalt import _hip
+    from dsalt.kernels.window_utils import apply_rotary_emb
+    mod, T, H, D = wl["mod"], wl["T"], wl["H"], wl["D"]
+    g = torch.Generator(device=cu.device).manual_seed(5)
+    q = torch.randn(T, H, D, device=cu.device, generator=g).to(torch.bfloat16)
+    k = torch.randn(T, H, D, device=cu.device, generator=g).to(torch.bfloat16)
+    cos_t, sin_t = mod.rope_cos.float().contiguous(), mod.rope_sin.float().contiguous()
+    pos_ids = torch.arange(T, device=cu.device) % wl["L"]
+
+    def eager():
+        cos = cos_t[pos_ids].to(q.dtype)
+        sin = sin_t[pos_ids].to(q.dtype)
+        apply_rotary_emb(q, k, cos.unsqueeze(1), sin.unsqueeze(1))
+
+    qo, ko = torch.empty_like(q), torch.empty_like(k)
+    hip = lambda: _hip.rope(q, k, cos_t, sin_t, cu, q_out=qo, k_out=ko)
+    with torch.no_grad():
+        eager_ms = time_launches(eager, 50, 10)
+        hip_ms = time_graph(hip)
+    nbytes = 2 * (q.numel() + k.numel()) * 2
+    return {"workload": "c2 RoPE of q and k, bf16", "eager_torch_us": eager_ms * 1e3, "hip_us": hip_ms * 1e3,
+            "hip_GB/s": nbytes / (hip_ms * 1e-3) / 1e9}
+
+
 def cpu_baseline(wl, budget_s: float = 12.0):
     """The reference's CPU fallback cost (dense HARD mask + fp32 SDPA), restated in
     oracle/, timed on this host on one sequence of the workload (all heads)."""
@@ -430,6 +460,7 @@ def main():
         "quantize_ms": qz_ms,
         "path_ms": ms + sel_ms + qz_ms,
         "selector_front_end": front,
+        "rope": measure_rope(wl, cu),
     }
     if not args.no_backward:
         res["backward"] = measure_backward(dev)

@@ -46,6 +46,34 @@ struct Elem<BF16> {
     static __device__ __forceinline__ void st(void *p, int64_t i, float x) {
         static_cast<uint16_t *>(p)[i] = (uint16_t)(__float_as_uint(round(x)) >> 16);
     }
+    template <int VW>
+    static __device__ __forceinline__ void ldv(const void *p, int64_t i, float *x) {
+        if constexpr (VW == 8) {
+            const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i);
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[2 * e] = __uint_as_float(w[e] << 16);
+                x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < VW; ++e) x[e] = ld(p, i + e);
+        }
+    }
+    template <int VW>
+    static __device__ __forceinline__ void stv(void *p, int64_t i, const float *x) {
+        if constexpr (VW == 8) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                w[e] = (__float_as_uint(round(x[2 * e])) >> 16) | (__float_as_uint(round(x[2 * e + 1])) & 0xffff0000u);
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(p) + i) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < VW; ++e) st(p, i + e, x[e]);
+        }
+    }
 };
 template <>
 struct Elem<F16> {
@@ -54,6 +82,16 @@ struct Elem<F16> {
     }
     static __device__ __forceinline__ float round(float x) { return (float)(_Float16)x; }
     static __device__ __forceinline__ void st(void *p, int64_t i, float x) { static_cast<_Float16 *>(p)[i] = (_Float16)x; }
+    template <int VW>
+    static __device__ __forceinline__ void ldv(const void *p, int64_t i, float *x) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) x[e] = ld(p, i + e);
+    }
+    template <int VW>
+    static __device__ __forceinline__ void stv(void *p, int64_t i, const float *x) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) st(p, i + e, x[e]);
+    }
 };
 struct F32 {};
 template <>
@@ -61,24 +99,42 @@ struct Elem<F32> {
     static __device__ __forceinline__ float ld(const void *p, int64_t i) { return static_cast<const float *>(p)[i]; }
     static __device__ __forceinline__ float round(float x) { return x; }
     static __device__ __forceinline__ void st(void *p, int64_t i, float x) { static_cast<float *>(p)[i] = x; }
+    template <int VW>
+    static __device__ __forceinline__ void ldv(const void *p, int64_t i, float *x) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) x[e] = ld(p, i + e);
+    }
+    template <int VW>
+    static __device__ __forceinline__ void stv(void *p, int64_t i, const float *x) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) st(p, i + e, x[e]);
+    }
 };
 
-// One thread per (token, head, j < D/2) of q then k: both elements of the rotated pair.
-// Reads and writes of a pair happen in the same thread, so out may alias in.
-template <typename DT>
+template <int VW>
+__device__ __forceinline__ void ldv_f32(const float *p, float *x) {
+#pragma unroll
+    for (int e = 0; e < VW; ++e) x[e] = p[e];
+}
+
+// One thread per (token, head, VW consecutive j < D/2) of q then k: both elements of
+// each rotated pair. Reads and writes of a pair happen in the same thread, so out may
+// alias in. VW = 8 moves 16-byte (16-bit types) or 32-byte (fp32) vectors per half.
+template <typename DT, int VW>
 __global__ void __launch_bounds__(256) rope_kernel(const RopeParams p) {
 #pragma clang fp contract(off)
     typedef Elem<DT> E;
     const int half = p.D >> 1;
-    const int64_t per_tok = (int64_t)(p.heads[0] + p.heads[1]) * half;
+    const int nj = half / VW;  // vectors per half-row
+    const int64_t per_tok = (int64_t)(p.heads[0] + p.heads[1]) * nj;
     const int64_t n = (int64_t)p.T * per_tok;
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
          idx += (int64_t)gridDim.x * blockDim.x) {
         const int t = (int)(idx / per_tok);
         int r = (int)(idx - (int64_t)t * per_tok);
-        const int which = r >= p.heads[0] * half;  // 0: q, 1: k
-        if (which) r -= p.heads[0] * half;
-        const int h = r / half, j = r - h * half;
+        const int which = r >= p.heads[0] * nj;  // 0: q, 1: k
+        if (which) r -= p.heads[0] * nj;
+        const int h = r / nj, j0 = (r - h * nj) * VW;
         int pos = t;
         if (p.cu) {  // offset inside the sequence: binary search over cu_seqlens
             int lo = 0, hi = p.S;  // cu[lo] <= t < cu[hi]
@@ -89,27 +145,32 @@ __global__ void __launch_bounds__(256) rope_kernel(const RopeParams p) {
             }
             pos = t - p.cu[lo];
         }
-        float c0 = NAN, c1 = NAN, s0 = NAN, s1 = NAN;  // a row past the table: NaN outputs
-        if (pos < p.rows) {
-            const float *cr = p.cos + (int64_t)pos * p.cs_st, *sr = p.sin + (int64_t)pos * p.cs_st;
-            c0 = E::round(cr[j]);
-            c1 = E::round(cr[j + half]);
-            s0 = E::round(sr[j]);
-            s1 = E::round(sr[j + half]);
-        }
+        const bool in_table = pos < p.rows;  // a row past the table: NaN outputs
+        const float *cr = p.cos + (int64_t)(in_table ? pos : 0) * p.cs_st;
+        const float *sr = p.sin + (int64_t)(in_table ? pos : 0) * p.cs_st;
         const int64_t ib = (int64_t)t * p.in_st[which] + (int64_t)h * p.in_sh[which];
-        const float a = E::ld(p.in[which], ib + j), b = E::ld(p.in[which], ib + j + half);
-        float o0, o1;
-        if (!p.transpose) {
-            o0 = a * c0 - b * s0;
-            o1 = b * c1 + a * s1;
-        } else {
-            o0 = a * c0 + b * s1;
-            o1 = b * c1 - a * s0;
-        }
         const int64_t ob = (int64_t)t * p.out_st[which] + (int64_t)h * p.out_sh[which];
-        E::st(p.out[which], ob + j, o0);
-        E::st(p.out[which], ob + j + half, o1);
+        float a[VW], b[VW], c0[VW], c1[VW], s0[VW], s1[VW], o0[VW], o1[VW];
+        E::template ldv<VW>(p.in[which], ib + j0, a);
+        E::template ldv<VW>(p.in[which], ib + j0 + half, b);
+        ldv_f32<VW>(cr + j0, c0);
+        ldv_f32<VW>(cr + j0 + half, c1);
+        ldv_f32<VW>(sr + j0, s0);
+        ldv_f32<VW>(sr + j0 + half, s1);
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+            const float cc0 = in_table ? E::round(c0[e]) : NAN, cc1 = in_table ? E::round(c1[e]) : NAN;
+            const float ss0 = in_table ? E::round(s0[e]) : NAN, ss1 = in_table ? E::round(s1[e]) : NAN;
+            if (!p.transpose) {
+                o0[e] = a[e] * cc0 - b[e] * ss0;
+                o1[e] = b[e] * cc1 + a[e] * ss1;
+            } else {
+                o0[e] = a[e] * cc0 + b[e] * ss1;
+                o1[e] = b[e] * cc1 - a[e] * ss0;
+            }
+        }
+        E::template stv<VW>(p.out[which], ob + j0, o0);
+        E::template stv<VW>(p.out[which], ob + j0 + half, o1);
     }
 }
 
@@ -141,11 +202,19 @@ hipError_t launch_rope(const dsalt_rope_args &a, hipStream_t stream) {
     p.S = a.num_seqs;
     p.transpose = a.transpose;
     p.rows = a.table_rows;
-    const int64_t n = (int64_t)a.total_len * (a.n_q_heads + a.n_k_heads) * (a.head_dim / 2);
+    // 8 pairs per thread when every half-row vector is 16-byte aligned (16-bit types)
+    const int half = a.head_dim / 2;
+    auto al16 = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+    const bool vec = a.dtype == DSALT_DTYPE_BF16 && half % 8 == 0 && al16(a.q) && al16(a.k) && al16(a.q_out) &&
+                     al16(a.k_out) && a.q_stride_t % 8 == 0 && a.q_stride_h % 8 == 0 && a.k_stride_t % 8 == 0 &&
+                     a.k_stride_h % 8 == 0 && a.q_out_stride_t % 8 == 0 && a.q_out_stride_h % 8 == 0 &&
+                     a.k_out_stride_t % 8 == 0 && a.k_out_stride_h % 8 == 0;
+    const int64_t n = (int64_t)a.total_len * (a.n_q_heads + a.n_k_heads) * (vec ? half / 8 : half);
     const int grid = (int)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536);
-    if (a.dtype == DSALT_DTYPE_BF16) hipLaunchKernelGGL(rope_kernel<BF16>, dim3(grid), dim3(256), 0, stream, p);
-    else if (a.dtype == DSALT_DTYPE_F16) hipLaunchKernelGGL(rope_kernel<F16>, dim3(grid), dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL(rope_kernel<F32>, dim3(grid), dim3(256), 0, stream, p);
+    if (vec) hipLaunchKernelGGL((rope_kernel<BF16, 8>), dim3(grid), dim3(256), 0, stream, p);
+    else if (a.dtype == DSALT_DTYPE_BF16) hipLaunchKernelGGL((rope_kernel<BF16, 1>), dim3(grid), dim3(256), 0, stream, p);
+    else if (a.dtype == DSALT_DTYPE_F16) hipLaunchKernelGGL((rope_kernel<F16, 1>), dim3(grid), dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((rope_kernel<F32, 1>), dim3(grid), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
