@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import argparse
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -25,7 +26,42 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-ffp-contract=fast", "-Wall", "-Wno-unused-result",
     "-mllvm", "-amdgpu-mfma-vgpr-form",  # MFMA C/D in VGPRs: no accvgpr copies for softmax
+    "-Rpass-analysis=kernel-resource-usage",  # per-kernel register / scratch report (checked below)
 ]
+
+_REMARK = re.compile(r"remark:\s+(Function Name|TotalSGPRs|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|"
+                     r"Dynamic Stack|Occupancy \[waves/SIMD\]|SGPRs Spill|VGPRs Spill|"
+                     r"LDS Size \[bytes/block\]): (\S+)")
+
+
+def resource_report(stderr: str) -> list[dict]:
+    """Per-kernel resource figures from the compiler's kernel-resource-usage remarks."""
+    kernels: list[dict] = []
+    for line in stderr.splitlines():
+        m = _REMARK.search(line)
+        if not m:
+            continue
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            kernels.append({"name": val})
+        elif kernels:
+            kernels[-1][key] = val
+    return kernels
+
+
+def spill_violations(kernels: list[dict]) -> list[str]:
+    """Kernels that spill registers or use scratch memory. The tile rings wait on
+    hand-counted vector-memory counters (s_waitcnt vmcnt(N)); a compiler-inserted
+    scratch access would be counted too and silently break them, so none is allowed."""
+    bad = []
+    for k in kernels:
+        why = [f"{f}={k[f]}" for f in ("SGPRs Spill", "VGPRs Spill", "ScratchSize [bytes/lane]")
+               if k.get(f, "0") != "0"]
+        if k.get("Dynamic Stack", "False") != "False":
+            why.append("dynamic stack")
+        if why:
+            bad.append(f"{k['name']}: {', '.join(why)}")
+    return bad
 
 
 def hipcc() -> str:
@@ -45,7 +81,17 @@ def compile_one(src: str) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stdout}\n{res.stderr}")
-    warn = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l and l.strip())
+    kernels = resource_report(res.stderr)
+    bad = spill_violations(kernels)
+    if bad:
+        raise RuntimeError(f"{os.path.basename(src)}: register spills / scratch use are not allowed:\n  "
+                           + "\n  ".join(bad))
+    with open(obj + ".resources.txt", "w") as f:
+        for k in kernels:
+            f.write(" ".join(f"{a}={b}" for a, b in k.items()) + "\n")
+    warn = "\n".join(l for l in res.stderr.splitlines()
+                     if "packed-fp32-ops" not in l and "kernel-resource-usage" not in l and l.strip()
+                     and not re.match(r"^\s*\d*\s*\|", l) and "remark" not in l)
     if warn:
         print(warn, file=sys.stderr)
     return obj

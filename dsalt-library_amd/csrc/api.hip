@@ -4,6 +4,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <initializer_list>
+
 #include "launch.h"
 
 namespace {
@@ -54,6 +56,19 @@ int check_common(int mode, int dtype, int T, int S, int H, int D, int k, const i
     return DSALT_OK;
 }
 
+// Rows of one sequence are addressed through buffer resources with 32-bit byte
+// offsets (row index x row stride): every such operand must span < 4 GiB over total_len
+// rows. `row_bytes` lists each operand's row stride in bytes.
+int check_span32(int total_len, std::initializer_list<int64_t> row_bytes) {
+    int64_t widest = 0;
+    for (int64_t b : row_bytes) widest = b > widest ? b : widest;
+    if ((int64_t)total_len * widest >= ((int64_t)1 << 32))
+        return fail(DSALT_ERR_UNSUPPORTED,
+                    "a sequence's rows must span < 4 GiB (total_len %d x row stride %lld B)", total_len,
+                    (long long)widest);
+    return DSALT_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -86,12 +101,7 @@ int dsalt_fwd_check(const dsalt_fwd_args *a) {
     if (!(a->scale == a->scale)) return fail(DSALT_ERR_INVALID, "scale is NaN");
     if (a->scale == 0.f || !(fabsf(a->scale) < INFINITY))
         return fail(DSALT_ERR_UNSUPPORTED, "scale must be finite and non-zero (got %g)", (double)a->scale);
-    // K/V rows of one sequence are addressed with 32-bit byte offsets
-    const int64_t row_bytes = 2 * (a->k_stride_t > a->v_stride_t ? a->k_stride_t : a->v_stride_t);
-    if ((int64_t)a->total_len * row_bytes >= ((int64_t)1 << 32))
-        return fail(DSALT_ERR_UNSUPPORTED, "a sequence's K/V rows must span < 4 GiB (total_len %d x row stride %lld B)",
-                    a->total_len, (long long)row_bytes);
-    return DSALT_OK;
+    return check_span32(a->total_len, {2 * a->q_stride_t, 2 * a->k_stride_t, 2 * a->v_stride_t});
 }
 
 int dsalt_fwd(const dsalt_fwd_args *a, void *stream) {
@@ -265,7 +275,9 @@ int dsalt_bwd_check(const dsalt_bwd_args *a) {
                         (long long)a->workspace_bytes, (long long)need);
         if (!aligned(a->workspace, 256)) return fail(DSALT_ERR_INVALID, "workspace must be 256-byte aligned");
     }
-    return DSALT_OK;
+    const int64_t ob = a->out_dtype == DSALT_DTYPE_F32 ? 4 : 2;
+    return check_span32(a->total_len, {2 * a->q_stride_t, 2 * a->k_stride_t, 2 * a->v_stride_t,
+                                       2 * a->dout_stride_t, ob * a->out_stride_t});
 }
 
 int dsalt_bwd(const dsalt_bwd_args *a, void *stream) {

@@ -39,8 +39,6 @@
 namespace dsalt {
 namespace {
 
-constexpr int kPad8 = 8;  // row-major tile row padding (halves): conflict-free b128 reads
-constexpr int kPad4 = 4;  // transposed tile row padding (halves): conflict-free b64 reads
 // band kv workgroups: waves (32 keys each), queries per tile and LDS ring depth; at
 // D = 128 one 32-query sub-block per tile would need more than 256 VGPRs
 constexpr int kv_waves(int d) { return d == 64 ? 2 : 4; }

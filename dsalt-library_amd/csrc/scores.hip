@@ -10,7 +10,8 @@
 // Three kernels, deterministic (no atomics, fixed reduction orders):
 //  1. norms_kernel: one wave per token, 16 tokens per workgroup. ||x_t|| and ||v_t,g||
 //     in fp32, each rounded to its input's dtype (what .norm() returns for a 16-bit
-//     tensor, before .float(); under autocast x is fp32 and v bf16), written to the
+//     tensor, before .float()) unless norms_f32 is set (autocast runs .norm() in fp32
+//     and returns it unrounded), written to the
 //     workspace, plus the workgroup's fp64 partial sums of each quantity and its square.
 //  2. stats_kernel (one workgroup): the partials summed in a fixed order (lanes stride
 //     the blocks, then a fixed shuffle tree), the mean and the unbiased std in fp64,
@@ -35,7 +36,7 @@ struct ScoreParams {
     double *part;     // workspace: [nblk][1 + n_kv][2]
     float *stats;     // workspace: [1 + n_kv][2] (mean, std)
     int64_t x_st, v_st, v_sh, s_st, s_sh, zv_st, zv_sh;
-    int T, d, n_kv, D, H, nblk;
+    int T, d, n_kv, D, H, nblk, norms_f32;
 };
 
 // Element loads and the dtype rounding of a norm, per storage type.
@@ -113,7 +114,7 @@ __global__ void __launch_bounds__(64 * kNormTokens) norms_kernel(const ScorePara
         float sx = 0.f;
         for (int c = lane * EX; c < p.d; c += 64 * EX) sx += LX::sumsq16(xr + (int64_t)c * BX);
         sx = group_sum(sx, 64);
-        const float xn = LX::round(sqrtf(sx));
+        const float xn = p.norms_f32 ? sqrtf(sx) : LX::round(sqrtf(sx));
         if (lane == 0) {
             p.xn[t] = xn;
             s_n[j][0] = xn;
@@ -125,7 +126,7 @@ __global__ void __launch_bounds__(64 * kNormTokens) norms_kernel(const ScorePara
             float sv = 0.f;
             if (g < p.n_kv) sv = LV::sumsq16(vr + ((int64_t)g * p.v_sh + (lane % G) * EV) * BV);
             sv = group_sum(sv, G);
-            const float vn = LV::round(sqrtf(sv));
+            const float vn = p.norms_f32 ? sqrtf(sv) : LV::round(sqrtf(sv));
             if (g < p.n_kv && lane % G == 0) {
                 p.vn[(int64_t)t * p.n_kv + g] = vn;
                 s_n[j][1 + g] = vn;
@@ -240,6 +241,7 @@ hipError_t launch_scores(const dsalt_scores_args &a, hipStream_t stream) {
     p.D = a.head_dim;
     p.H = a.n_heads;
     p.nblk = (a.total_len + kNormTokens - 1) / kNormTokens;
+    p.norms_f32 = a.norms_f32 != 0;
     char *ws = static_cast<char *>(a.workspace);
     p.xn = reinterpret_cast<float *>(ws);
     ws += align256((size_t)p.T * 4);

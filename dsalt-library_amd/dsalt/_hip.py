@@ -13,7 +13,9 @@ from ctypes import c_float, c_int32, c_int64, c_size_t, c_void_p
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libdsalt_hip.so")
+# the in-tree build; DSALT_HIP_LIB names another copy of the library
+LIB_PATH = os.environ.get("DSALT_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                           "libdsalt_hip.so")
 
 DSALT_OK = 0
 MODE_HARD = 0
@@ -89,7 +91,7 @@ class SelectArgs(ctypes.Structure):
 class ScoresArgs(ctypes.Structure):
     _fields_ = [
         ("total_len", c_int32), ("d_model", c_int32), ("n_kv_heads", c_int32), ("head_dim", c_int32),
-        ("n_heads", c_int32), ("x_dtype", c_int32), ("v_dtype", c_int32), ("reserved0", c_int32),
+        ("n_heads", c_int32), ("x_dtype", c_int32), ("v_dtype", c_int32), ("norms_f32", c_int32),
         ("x", c_void_p), ("x_stride_t", c_int64),
         ("v", c_void_p), ("v_stride_t", c_int64), ("v_stride_h", c_int64),
         ("alpha", c_void_p),
@@ -353,15 +355,31 @@ class BwdLauncher:
 def _bwd_args(mode, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, scale, tau_win, win_edge,
               need_dw, grad_dtype):
     dev = require_gpu(q, k, v, out, lse, dout, w, cu_seqlens)
+    if q.dim() != 3:
+        raise DsaltError(f"q must be [T, H, D], got {tuple(q.shape)}")
     T, H, D = q.shape
+    for name, t in (("k", k), ("v", v), ("out", out), ("dout", dout)):
+        if tuple(t.shape) != (T, H, D):
+            raise DsaltError(f"{name} shape {tuple(t.shape)} != q shape {(T, H, D)}")
+    if k.dtype != q.dtype or v.dtype != q.dtype or q.dtype not in _DTYPES:
+        raise DsaltError(f"q/k/v must share a bf16/fp16 dtype, got {q.dtype} {k.dtype} {v.dtype}")
+    if tuple(lse.shape) != (T, H) or lse.dtype != torch.float32:
+        raise DsaltError(f"lse must be float32 [T={T}, H={H}], got {lse.dtype} {tuple(lse.shape)}")
     cu = _cu_i32(cu_seqlens)
     S = cu.shape[0] - 1
     w = _f32_vec(w)
+    if w.dim() != 1 or w.shape[0] != T:
+        raise DsaltError(f"w must be [T={T}], got {tuple(w.shape)}")
     dout = as_kernel_operand(dout, q.dtype)
-    kl = 0 if lmk_pos is None else lmk_pos.shape[2]
-    if lmk_pos is not None and lmk_pos.dtype != torch.int64:
-        lmk_pos = lmk_pos.long()
+    kl = 0 if lmk_pos is None else lmk_pos.shape[-1]
+    if lmk_pos is not None:
+        if lmk_pos.dim() != 3 or lmk_pos.shape[0] != H or lmk_pos.shape[1] != S:
+            raise DsaltError(f"landmark positions must be [H={H}, S={S}, k], got {tuple(lmk_pos.shape)}")
+        if lmk_pos.dtype != torch.int64:
+            lmk_pos = lmk_pos.long()
     if lmk_bias is not None:
+        if lmk_pos is None or lmk_bias.shape != lmk_pos.shape:
+            raise DsaltError(f"landmark bias shape {tuple(lmk_bias.shape)} does not match the positions")
         lmk_bias = _f32_vec(lmk_bias)
     gdt = q.dtype if grad_dtype is None else grad_dtype
     if gdt not in (q.dtype, torch.float32):
@@ -431,14 +449,24 @@ def select_landmarks(scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Te
 _SCORE_DTYPES = {torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16, torch.float32: DTYPE_F32}
 
 
+def autocast_norms() -> bool:
+    """True when torch's GPU autocast is on: .norm() then runs in fp32 and returns its
+    result unrounded, whatever the 16-bit input dtype."""
+    try:
+        return bool(torch.is_autocast_enabled("cuda"))
+    except TypeError:  # torch < 2.4 takes no device type
+        return bool(torch.is_autocast_enabled())
+
+
 def scores_args(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int,
                 scores: torch.Tensor, z_x: torch.Tensor | None, z_v: torch.Tensor | None,
-                ws: torch.Tensor | None) -> ScoresArgs:
+                ws: torch.Tensor | None, norms_f32: bool = False) -> ScoresArgs:
     """Argument block of dsalt_hybrid_scores (x [T, d], v [T, n_kv, D], alpha [H] fp32)."""
     T, d = x.shape
     _, n_kv, D = v.shape
     a = ScoresArgs()
     a.total_len, a.d_model, a.n_kv_heads, a.head_dim, a.n_heads = T, d, n_kv, D, n_heads
+    a.norms_f32 = int(bool(norms_f32))
     a.x_dtype = _SCORE_DTYPES.get(x.dtype, -1)
     a.v_dtype = _SCORE_DTYPES.get(v.dtype, -1)
     a.x, a.x_stride_t = x.data_ptr(), x.stride(0)
@@ -460,10 +488,15 @@ def scores_workspace_size(T: int, n_kv: int) -> int:
     return n
 
 
-def hybrid_scores(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int):
+def hybrid_scores(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int,
+                  norms_f32: bool | None = None):
     """``(scores [T, H], z_x [T], z_v [T, H])`` fp32 of the hybrid landmark score from the
     hidden states x [T, d] and their value projection v = x W_V^T [T, n_kv, D]
-    (pre-RoPE), without the GEMM; no gradient (the selection is detached)."""
+    (pre-RoPE), without the GEMM; no gradient (the selection is detached).
+    ``norms_f32`` (default: whether autocast is on) keeps the norms of 16-bit inputs in
+    fp32 instead of rounding them to the input dtype."""
+    if norms_f32 is None:
+        norms_f32 = autocast_norms()
     dev = require_gpu(x, v, alpha)
     if x.dim() != 2 or v.dim() != 3 or v.shape[0] != x.shape[0]:
         raise DsaltError(f"x must be [T, d] and v [T, n_kv, D] with the same T (got {tuple(x.shape)}, "
@@ -480,7 +513,7 @@ def hybrid_scores(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads
     z_x = torch.empty((T,), device=dev, dtype=torch.float32)
     z_v = torch.empty((T, n_heads), device=dev, dtype=torch.float32)
     ws = torch.empty((scores_workspace_size(T, v.shape[1]),), device=dev, dtype=torch.uint8)
-    a = scores_args(x, v, alpha, n_heads, scores, z_x, z_v, ws)
+    a = scores_args(x, v, alpha, n_heads, scores, z_x, z_v, ws, norms_f32)
     _raise(lib().dsalt_hybrid_scores(ctypes.byref(a), stream_handle(dev)), "dsalt_hybrid_scores")
     return scores, z_x, z_v
 
@@ -524,7 +557,8 @@ class ScoresLauncher:
     launches the two score kernels on the current stream (for timing loops and graph
     capture); `scores`, `z_x`, `z_v` hold the result."""
 
-    def __init__(self, x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int):
+    def __init__(self, x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int,
+                 norms_f32: bool = False):
         self.device = require_gpu(x, v, alpha)
         self._keep = (x, v, alpha.detach().to(torch.float32).contiguous())
         T = x.shape[0]
@@ -532,7 +566,7 @@ class ScoresLauncher:
         self.z_x = torch.empty((T,), device=self.device, dtype=torch.float32)
         self.z_v = torch.empty((T, n_heads), device=self.device, dtype=torch.float32)
         self._ws = torch.empty((scores_workspace_size(T, v.shape[1]),), device=self.device, dtype=torch.uint8)
-        self._args = scores_args(x, v, self._keep[2], n_heads, self.scores, self.z_x, self.z_v, self._ws)
+        self._args = scores_args(x, v, self._keep[2], n_heads, self.scores, self.z_x, self.z_v, self._ws, norms_f32)
         _raise(lib().dsalt_scores_check(ctypes.byref(self._args)), "dsalt_scores_check")
 
     def __call__(self) -> None:

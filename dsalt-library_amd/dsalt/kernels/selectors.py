@@ -1,77 +1,99 @@
 """Selector helpers: packed metadata, landmark top-k and the landmark K/V gather.
 
-Same names and signatures as dsalt/kernels/selectors.py. The landmark top-k runs in the
-HIP selection kernel (bit-exact on the fp32 scores, positions returned in ascending
-order with -1 in the unused slots). The HIP attention kernels derive the packed block
-layout from cu_seqlens and gather landmark rows themselves; ``_seq_meta``,
-``_build_seq_block_map`` and ``_build_landmark_kv`` remain for callers of the
-reference's helper API. Their caches are keyed by the packing itself (the reference
-keys them by (total_len, num_seqs[, block]) only, which goes stale across packings of
-equal total length).
+Same names, signatures and results as dsalt/kernels/selectors.py. The landmark top-k
+runs in the HIP selection kernel (bit-exact on the fp32 scores, positions returned in
+ascending order with -1 in the unused slots). The HIP attention kernels derive the
+packed block layout from cu_seqlens and gather landmark rows themselves, so
+``_seq_meta``, ``_build_seq_block_map`` and ``_build_landmark_kv`` only serve callers
+of the reference's helper API. Their caches are keyed by the packing itself (the
+reference keys them by (total_len, num_seqs[, block]) only, which goes stale across
+packings of equal total length).
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from .. import _hip
-from .landmark_tokens_ker import hybrid_scores_per_head
+from .landmark_tokens_ker import hybrid_scores_from_v, hybrid_scores_per_head
 
-_SEQ_BLOCK_MAP_CACHE: dict = {}
-_SEQ_META_CACHE: dict = {}
-_CACHE_LIMIT = 64
-
-
-def _cu_key(cu_seqlens: torch.Tensor, cu_list: list | None) -> tuple:
-    if cu_list is not None:
-        return tuple(int(c) for c in cu_list)
-    return tuple(int(c) for c in cu_seqlens.detach().to("cpu").tolist())
+_CACHE: dict = {}
+_CACHE_LIMIT = 128
 
 
-def _cache_put(cache: dict, key, val) -> None:
-    if len(cache) >= _CACHE_LIMIT:
-        cache.pop(next(iter(cache)))
-    cache[key] = val
+def _boundaries(cu_seqlens: torch.Tensor, cu_list: list | None) -> tuple:
+    """The packing as a tuple of ints (the host hint when given, else one device read)."""
+    src = cu_list if cu_list is not None else cu_seqlens.detach().cpu().tolist()
+    return tuple(int(c) for c in src)
+
+
+def _memo(key, make):
+    hit = _CACHE.get(key)
+    if hit is None:
+        if len(_CACHE) >= _CACHE_LIMIT:
+            _CACHE.clear()
+        hit = _CACHE[key] = make()
+    return hit
 
 
 def _seq_meta(cu_seqlens: torch.Tensor, total: int, device: torch.device, cu_list: list | None = None):
     """``(num_seqs, lens, starts, seq_ids, seq_off, max_len)`` of a packing
-    (selectors.py:15-34)."""
-    key = (_cu_key(cu_seqlens, cu_list), str(device))
-    if key in _SEQ_META_CACHE:
-        return _SEQ_META_CACHE[key]
-    cu = torch.tensor(key[0], dtype=torch.long, device=device)
-    num_seqs = cu.shape[0] - 1
-    lens = cu[1:] - cu[:-1]
-    starts = cu[:-1]
-    seq_ids = torch.repeat_interleave(torch.arange(num_seqs, device=device), lens)
-    seq_off = torch.arange(total, device=device) - starts[seq_ids]
-    max_len = max((key[0][b + 1] - key[0][b] for b in range(num_seqs)), default=0)
-    val = (num_seqs, lens, starts, seq_ids, seq_off, max_len)
-    _cache_put(_SEQ_META_CACHE, key, val)
-    return val
+    (selectors.py:15-34): per-token sequence id and offset inside the sequence."""
+    bounds = _boundaries(cu_seqlens, cu_list)
+
+    def make():
+        cu = torch.tensor(bounds, dtype=torch.long, device=device)
+        tok = torch.arange(total, dtype=torch.long, device=device)
+        # sequence of token t: the number of sequence ends <= t
+        seq_ids = torch.searchsorted(cu[1:], tok, right=True)
+        seq_off = tok - cu[seq_ids]
+        lens = cu[1:] - cu[:-1]
+        spans = np.diff(np.asarray(bounds, dtype=np.int64))
+        return (len(bounds) - 1, lens, cu[:-1], seq_ids, seq_off, int(spans.max()) if spans.size else 0)
+
+    return _memo(("meta", bounds, int(total), str(device)), make)
 
 
 def _build_seq_block_map(cu_seqlens: torch.Tensor, block_m: int, device: torch.device,
                          cu_list: list | None = None) -> tuple[torch.Tensor, int]:
-    """``(seq_block_map [total_blocks, 2] int32, total_blocks)``: each ``block_m`` block of
-    queries mapped to ``(sequence, block-in-sequence)`` (selectors.py:37-67)."""
-    cu = _cu_key(cu_seqlens, cu_list)
-    key = (cu, int(block_m), str(device))
-    if key in _SEQ_BLOCK_MAP_CACHE:
-        return _SEQ_BLOCK_MAP_CACHE[key]
-    lens = torch.tensor([cu[b + 1] - cu[b] for b in range(len(cu) - 1)], dtype=torch.long)
-    blocks_per = (lens + block_m - 1) // block_m
-    total_blks = int(blocks_per.sum())
-    seq_col = torch.repeat_interleave(torch.arange(lens.shape[0], dtype=torch.int32), blocks_per)
-    blk_col = (torch.arange(total_blks, dtype=torch.int32)
-               - torch.repeat_interleave(blocks_per.cumsum(0) - blocks_per, blocks_per).int())
-    result = torch.stack([seq_col, blk_col], dim=1).contiguous().to(device)
-    _cache_put(_SEQ_BLOCK_MAP_CACHE, key, (result, total_blks))
-    return result, total_blks
+    """``(seq_block_map [total_blocks, 2] int32, total_blocks)``: block b of ``block_m``
+    queries, counted over the sequences in order, is (sequence, block inside it)
+    (selectors.py:37-67)."""
+    bounds = _boundaries(cu_seqlens, cu_list)
+
+    def make():
+        spans = np.diff(np.asarray(bounds, dtype=np.int64))
+        nblk = -(-spans // int(block_m))            # ceil(L_s / block_m)
+        first = np.concatenate(([0], np.cumsum(nblk)))
+        b = np.arange(first[-1], dtype=np.int64)
+        seq = np.searchsorted(first[1:], b, side="right")
+        table = np.stack((seq, b - first[seq]), axis=1).astype(np.int32)
+        return torch.from_numpy(table).to(device), int(first[-1])
+
+    return _memo(("blocks", bounds, int(block_m), str(device)), make)
 
 
 def _score_block(x: torch.Tensor, W_V: torch.Tensor, alpha: torch.Tensor, n_heads: int, dh: int):
     return hybrid_scores_per_head(x, W_V, alpha, n_heads, dh)
+
+
+def selection_scores(x: torch.Tensor, W_V: torch.Tensor, alpha: torch.Tensor, n_heads: int, dh: int,
+                     v: torch.Tensor | None = None, hip_scores: bool = False):
+    """``(scores [T, H] fp32, z_x, z_v)`` for the landmark selection.
+
+    * ``v is None``: the reference's route, ``x @ W_V.T`` then the torch norms.
+    * ``v`` given (the module's pre-RoPE value projection ``x W_V^T`` as ``[T, n_kv, dh]``):
+      the same torch norms on ``v`` (torch forms ``v_proj(x)`` with the same matmul, so
+      the scores are bit-identical and the second GEMM is saved).
+    * ``hip_scores``: the one-pass HIP kernel over x and v (deterministic; its fp32 norm
+      sums run in another order than torch's, so a 16-bit norm can land one ulp away and
+      move a near-tie landmark).
+    """
+    if v is None:
+        return _score_block(x, W_V, alpha, n_heads, dh)
+    if hip_scores:
+        return _hip.hybrid_scores(x.detach(), v.detach(), alpha, n_heads)
+    return hybrid_scores_from_v(x, v, alpha, n_heads)
 
 
 def _compute_landmark_indices(
@@ -86,6 +108,7 @@ def _compute_landmark_indices(
     cu_list: list | None = None,
     head_dim: int | None = None,
     v: torch.Tensor | None = None,
+    hip_scores: bool = False,
 ):
     """Top-``k_lmk`` landmark positions per (head, sequence), excluding covered tokens.
 
@@ -96,33 +119,33 @@ def _compute_landmark_indices(
     ``topk(sorted=False)`` leaves slot order unspecified, so the set is what matches).
     ``n_min`` and ``total_len`` are accepted for signature compatibility.
 
-    ``v`` (optional, not in the reference's signature): the value projection
-    ``x @ W_V.T`` as ``[T, n_kv, dh]``, which the attention module already holds. With
-    it the scores come from the fused HIP kernel ``dsalt_hybrid_scores`` (norms and
-    standardisation in one pass over x and v) and the ``x @ W_V.T`` GEMM is skipped.
+    ``v`` and ``hip_scores`` (not in the reference's signature) pick the score route of
+    :func:`selection_scores`.
     """
     n_heads = alpha.shape[0]
-    if v is not None:
-        scores, z_x, z_v = _hip.hybrid_scores(x.detach(), v.detach(), alpha, n_heads)
-        lmk = _hip.select_landmarks(scores, w_sizes, cu_seqlens, int(k_lmk))
-        return lmk, z_x, z_v
     dh = head_dim if head_dim is not None else W_V.shape[0] // n_heads
-    scores, z_x, z_v = _score_block(x, W_V, alpha, n_heads, dh)
-    lmk = _hip.select_landmarks(scores.float(), w_sizes, cu_seqlens, int(k_lmk))
+    with torch.no_grad():
+        scores, z_x, z_v = selection_scores(x, W_V, alpha, n_heads, dh, v, hip_scores)
+        lmk = _hip.select_landmarks(scores.float(), w_sizes, cu_seqlens, int(k_lmk))
     return lmk, z_x, z_v
 
 
 def _build_landmark_kv(K: torch.Tensor, V: torch.Tensor, lmk_indices: torch.Tensor,
                        cu_seqlens: torch.Tensor, k_lmk: int, n_heads: int,
                        head_dim: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """Gather landmark keys/values into ``[H, S, k, D]``; empty slots are zero
-    (selectors.py:137-159). The HIP kernels do this gather in-kernel; this helper only
-    serves callers of the reference's API."""
-    starts = cu_seqlens[:-1].to(K.device).long()
-    safe_idx = lmk_indices.clamp(min=0)
-    abs_idx = starts[None, :, None] + safe_idx
-    h_idx = torch.arange(n_heads, device=K.device)[:, None, None]
-    invalid = (lmk_indices < 0).unsqueeze(-1)
-    lmk_K = K[abs_idx, h_idx, :].masked_fill(invalid, 0.0)
-    lmk_V = V[abs_idx, h_idx, :].masked_fill(invalid, 0.0)
-    return lmk_K.contiguous(), lmk_V.contiguous()
+    """Landmark keys/values ``[H, S, k, D]`` (selectors.py:137-159); empty slots are zero.
+    The HIP kernels do this gather in-kernel; this helper only serves callers of the
+    reference's API."""
+    H, S, k = lmk_indices.shape
+    T = K.shape[0]
+    first = cu_seqlens[:-1].to(device=K.device, dtype=torch.long)
+    empty = lmk_indices < 0
+    # flat row of (token first[s] + pos, head h) in a [T * H, D] view
+    token = first.view(1, S, 1) + lmk_indices.clamp_min(0)
+    flat = (token * H + torch.arange(H, device=K.device).view(H, 1, 1)).reshape(-1)
+
+    def take(src: torch.Tensor) -> torch.Tensor:
+        rows = src.reshape(T * H, src.shape[-1]).index_select(0, flat).view(H, S, k, src.shape[-1])
+        return torch.where(empty.unsqueeze(-1), torch.zeros((), dtype=rows.dtype, device=rows.device), rows)
+
+    return take(K).contiguous(), take(V).contiguous()

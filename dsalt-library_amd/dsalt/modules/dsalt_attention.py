@@ -9,10 +9,10 @@ Packed input (``cu_seqlens`` given) runs the sparse path:
   * training: ``_train_selectors`` (continuous window, HIP landmark top-k, soft landmark
     weight log sigmoid(s/tau_lmk)) then the SOFT HIP kernels (forward + deterministic
     backward carrying d_w~ to win_gate and d_logw to alpha_w), dsalt_attention.py:440-487;
-  * inference: floor-quantised windows (HIP), HIP hybrid scores from the value projection
-    and HIP landmark top-k, the HARD HIP kernel,
-    dsalt_attention.py:610-625; then the ``_last_P`` diagnostic of sequence 0 unless
-    ``_collect_last_P`` is set to False (dsalt_attention.py:636-702).
+  * inference: floor-quantised windows (HIP), hybrid scores from the value projection
+    and HIP landmark top-k, the HARD HIP kernel, dsalt_attention.py:610-625; then the
+    ``_last_P`` diagnostic of sequence 0 unless ``_collect_last_P`` is set to False
+    (dsalt_attention.py:636-702).
 The attention output stays in the compute dtype on the module path (the reference
 round-trips it through fp32, which only the ``dsalt.kernels`` entry points keep).
 
@@ -47,14 +47,18 @@ class DSALTAttention(nn.Module):
     landmarks left of the window, selected per (head, sequence) by the hybrid score
     with per-head balance ``alpha = sigmoid(alpha_w)``.
 
-    ``_fused_selector`` (default True): with ``qkv_bias=False`` the landmark scores are
-    formed from the module's own value projection ``v = x W_V^T`` (the fused HIP score
-    kernel for the detached selection, the same formula in torch for the
-    differentiable ``lmk_logw``) instead of a second ``x @ W_V.T`` GEMM. Set it to False
-    for the reference's GEMM path.
+    ``_fused_selector`` (default True): without a projection bias the landmark scores are
+    formed from the module's own value projection ``v = x W_V^T`` instead of a second
+    ``x @ W_V.T`` GEMM, with the reference's torch norm and standardisation ops, so the
+    fp32 scores (and therefore the selected landmarks) are bit-identical to the
+    reference's route. ``_hip_scores`` (default False) computes them instead with the
+    one-pass HIP score kernel, which saves the torch passes but rounds its fp32 norm sums
+    in another order (a 16-bit norm can land one ulp away and move a near-tie landmark).
+    ``_last_selection`` holds the ``(windows, landmark positions)`` of the last forward.
     """
 
     _fused_selector = True
+    _hip_scores = False
 
     def __init__(
         self,
@@ -101,24 +105,27 @@ class DSALTAttention(nn.Module):
         self.win_edge = 4
 
         self._last_P: torch.Tensor | None = None
+        self._last_selection: tuple | None = None
 
         cos, sin = build_rope_cache(max_seq_len, self.head_dim, torch.device("cpu"),
                                     base=rope_base, scale=yarn_scale)
         self.register_buffer("rope_cos", cos, persistent=False)
         self.register_buffer("rope_sin", sin, persistent=False)
 
-    # ---- small pieces (dsalt_attention.py:243-284, :331-342) ---------------------------
+    # ---- small pieces (dsalt_attention.py:243-284) ---------------------------------------
     def _alpha(self) -> torch.Tensor:
         return torch.sigmoid(self.alpha_w)
 
     def _apply_out_proj(self, out: torch.Tensor) -> torch.Tensor:
-        return self.out_proj(out.to(self.out_proj.weight.dtype))
+        """out_proj in its weight's dtype (the attention output may be fp32 or 16-bit)."""
+        wdt = self.out_proj.weight.dtype
+        return self.out_proj(out if out.dtype == wdt else out.to(wdt))
 
     def _repeat_kv(self, t: torch.Tensor) -> torch.Tensor:
+        """[T, n_kv, D] -> [T, H, D]: kv head g serves query heads g*n_rep .. g*n_rep+n_rep-1."""
         if self.n_rep == 1:
             return t
-        T, _, D = t.shape
-        return t.unsqueeze(2).expand(T, self.n_kv_heads, self.n_rep, D).reshape(T, self.n_heads, D)
+        return t.repeat_interleave(self.n_rep, dim=1)
 
     def _window_continuous(self, x: torch.Tensor) -> torch.Tensor:
         """``w~ = n_min + sigmoid(win_gate(x)) * (n_max - n_min)``, differentiable, ``[T]``."""
@@ -134,25 +141,18 @@ class DSALTAttention(nn.Module):
         return w_cont.round().clamp(min=1)
 
     @torch.no_grad()
-    def _rope(self, n: int, device: torch.device):
-        max_n = self.rope_cos.shape[0]
-        if n <= max_n:
-            return self.rope_cos[:n].to(device), self.rope_sin[:n].to(device)
-        return self.rope_cos.to(device), self.rope_sin.to(device)
-
-    def _aux_zero(self, device: torch.device, dtype: torch.dtype) -> torch.Tensor:
-        return torch.zeros((), device=device, dtype=dtype)
-
-    @torch.no_grad()
     def warmup(self, device: torch.device) -> None:
-        was_training = self.training
-        self.eval()
-        dummy_T = max(self.n_min * 2, 16)
-        x_w = torch.randn(dummy_T, self.d_model, device=device)
-        cu_w = torch.tensor([0, dummy_T], dtype=torch.int32, device=device)
-        self._packed(x_w, cu_w, dummy_T, device)
-        torch.cuda.synchronize(device)
-        self.train(was_training)
+        """One small inference forward on ``device``: loads the HIP library and makes the
+        first launches outside any timed region. The training flag is restored."""
+        mode = self.training
+        try:
+            self.train(False)
+            n = max(16, 2 * self.n_min)
+            x = torch.randn(n, self.d_model, device=device, dtype=self.q_proj.weight.dtype)
+            self._packed(x, torch.tensor([0, n], dtype=torch.int32, device=device), n, device)
+            torch.cuda.synchronize(device)
+        finally:
+            self.train(mode)
 
     # ---- forward -----------------------------------------------------------------------
     def forward(self, x: torch.Tensor, cu_seqlens: torch.Tensor | None = None,
@@ -168,29 +168,32 @@ class DSALTAttention(nn.Module):
     def _train_selectors(self, x, cu_seqlens, total_len, device, cu_list=None, v=None):
         """``(w_cont [T], lmk_pos [H,S,k], lmk_logw [H,S,k])`` (dsalt_attention.py:457-487):
         the selection is detached; ``w_cont`` and ``lmk_logw`` carry the gradients.
-        With ``v`` (the pre-RoPE value projection ``[T, n_kv, dh]``) the scores are
-        formed from it instead of a second ``x @ W_V.T`` GEMM."""
+        With ``v`` (the pre-RoPE value projection ``[T, n_kv, dh]``, equal to ``x @ W_V.T``
+        when the projection has no bias) the scores are formed from it instead of a second
+        GEMM; the selection sees bit-identical scores either way."""
         w_cont = self._window_continuous(x)
         alpha = self._alpha()
-        fused = v is not None and self._fused_selector
+        route_v = v if self._fused_selector else None
         with torch.no_grad():
             w_disc = _hip.quantize_windows(w_cont.detach())
             lmk_pos, _, _ = _compute_landmark_indices(
                 x.detach(), self.v_proj.weight.detach(), alpha.detach().float(),
                 w_disc, cu_seqlens, self.k_lmk, self.n_min, total_len, cu_list,
-                head_dim=self.head_dim, v=v.detach() if fused else None,
-            )
-        if fused:
-            scores, _, _ = hybrid_scores_from_v(x, v, alpha, self.n_heads)
+                head_dim=self.head_dim, v=None if route_v is None else route_v.detach(),
+                hip_scores=self._hip_scores)
+        # the differentiable scores (the selection above ran on a detached copy of them)
+        if route_v is not None:
+            scores, _, _ = hybrid_scores_from_v(x, route_v, alpha, self.n_heads)
         else:
             scores, _, _ = hybrid_scores_per_head(x, self.v_proj.weight, alpha, self.n_heads, self.head_dim)
-        starts = cu_seqlens[:-1].to(device).long()
-        safe_pos = lmk_pos.clamp(min=0)
-        abs_pos = starts[None, :, None] + safe_pos
-        head_ix = torch.arange(self.n_heads, device=device)[:, None, None]
-        s_sel = scores[abs_pos, head_ix]
-        lmk_logw = torch.log(torch.sigmoid(s_sel / self.tau_lmk).clamp(min=1e-20))
-        lmk_logw = torch.where(lmk_pos >= 0, lmk_logw, torch.full_like(lmk_logw, float("-inf")))
+        H, S, k = lmk_pos.shape
+        # score of each selected landmark: column h of scores at token cu[s] + pos
+        first = cu_seqlens[:-1].to(device=device, dtype=torch.long)
+        tok = (first.view(1, S, 1) + lmk_pos.clamp_min(0)).reshape(H, S * k)
+        s_sel = scores.t().gather(1, tok).view(H, S, k)
+        lmk_logw = torch.sigmoid(s_sel / self.tau_lmk).clamp(min=1e-20).log()
+        lmk_logw = lmk_logw.masked_fill(lmk_pos < 0, float("-inf"))
+        self._last_selection = (w_disc, lmk_pos)
         return w_cont, lmk_pos, lmk_logw
 
     def _packed(self, x: torch.Tensor, cu_seqlens: torch.Tensor, total_len: int, device: torch.device,
@@ -200,7 +203,7 @@ class DSALTAttention(nn.Module):
         k = self.k_proj(x).view(total_len, self.n_kv_heads, self.head_dim)
         v = self.v_proj(x).view(total_len, self.n_kv_heads, self.head_dim)
         # x W_V^T before RoPE and the kv repeat: the selector's value norms come from it
-        # (qkv_bias=False only; with a bias v is not x W_V^T)
+        # (only without a projection bias, where v is exactly x W_V^T)
         v_sel = v if self.v_proj.bias is None else None
 
         # RoPE in one HIP pass (dsalt_attention.py:570-585): positions from cu_seqlens
@@ -213,7 +216,7 @@ class DSALTAttention(nn.Module):
         k = self._repeat_kv(k)
         v = self._repeat_kv(v)
 
-        aux = self._aux_zero(x.device, x.dtype)
+        aux = x.new_zeros(())
 
         if self.training:
             self._last_P = None
@@ -224,46 +227,44 @@ class DSALTAttention(nn.Module):
 
         w_sizes = self._window_sizes(x, floor=True)
         alpha = self._alpha()
+        route_v = v_sel if self._fused_selector else None
         lmk_indices, _, _ = _compute_landmark_indices(
             x.detach(), self.v_proj.weight.detach(), alpha.detach().float(), w_sizes,
             cu_seqlens, self.k_lmk, self.n_min, total_len, cu_list, head_dim=self.head_dim,
-            v=v_sel.detach() if (self._fused_selector and v_sel is not None) else None,
-        )
+            v=None if route_v is None else route_v.detach(), hip_scores=self._hip_scores)
+        self._last_selection = (w_sizes, lmk_indices)
         # Hard A(i) = W(i) ∪ L(i): the score only selects (zero landmark bias).
         out = sparse_attention(_hip.MODE_HARD, q, k, v, lmk_indices, None, w_sizes, cu_seqlens)
 
-        if not getattr(self, "_collect_last_P", True):
-            self._last_P = None
+        if getattr(self, "_collect_last_P", True):
+            self._last_P = self._first_sequence_probs(x, q, k, w_sizes, alpha, cu_seqlens, cu_list)
         else:
-            self._last_P = self._first_sequence_probs(x, q, k, w_sizes, alpha, cu_seqlens, cu_list, device)
+            self._last_P = None
         return self._apply_out_proj(out.reshape(total_len, self.d_model)), aux
 
     @torch.no_grad()
-    def _first_sequence_probs(self, x, q, k, w_sizes, alpha, cu_seqlens, cu_list, device):
-        """Dense ``[H, T0, T0]`` attention probabilities of sequence 0 under the HARD set,
-        the metrics diagnostic of dsalt_attention.py:643-702 (landmarks re-selected on
-        sequence 0 alone, in fp32). O(T0^2); disabled by ``_collect_last_P = False``."""
-        if cu_list is not None:
-            s0, e0 = int(cu_list[0]), int(cu_list[1])
-        else:
-            s0, e0 = (int(c) for c in cu_seqlens[:2].tolist())
-        T0 = e0 - s0
-        q0 = q[s0:e0].transpose(0, 1)
-        k0 = k[s0:e0].transpose(0, 1)
-        scale = 1.0 / math.sqrt(self.head_dim)
-        cu0 = torch.tensor([0, T0], dtype=torch.int32, device=device)
-        w0 = w_sizes[s0:e0]
-        lmk_idx, _, _ = _compute_landmark_indices(
-            x[s0:e0].float().detach(), self.v_proj.weight.float().detach(), alpha.detach().float(),
-            w0.float(), cu0, self.k_lmk, self.n_min, T0, [0, T0], head_dim=self.head_dim)
-        rows = torch.arange(T0, device=device)
-        w0l = w0.long()
-        in_win = (rows[None, :] >= rows[:, None] - w0l[:, None] + 1) & (rows[None, :] <= rows[:, None])
-        lmk0 = lmk_idx[:, 0, :]
-        col_is_lmk = torch.zeros(self.n_heads, T0 + 1, dtype=torch.bool, device=device)
-        col_is_lmk.scatter_(1, torch.where(lmk0 >= 0, lmk0, T0), True)
-        in_lmk = col_is_lmk[:, None, :T0] & (rows[None, None, :] <= rows[None, :, None])
-        full_mask = in_win.unsqueeze(0) | in_lmk
-        sc = torch.matmul(q0, k0.transpose(-2, -1).contiguous()) * scale
-        additive = sc.new_full((self.n_heads, T0, T0), float("-inf")).masked_fill_(full_mask, 0.0)
-        return torch.softmax(sc + additive, dim=-1).detach()
+    def _first_sequence_probs(self, x, q, k, w_sizes, alpha, cu_seqlens, cu_list):
+        """Dense ``[H, L0, L0]`` attention probabilities of the first packed sequence under
+        the HARD set (the metrics diagnostic of dsalt_attention.py:636-702): the landmarks
+        are selected again on that sequence alone from fp32 scores, the logits are formed
+        in q's dtype, and keys outside ``(i - w_i, i] ∪ {landmarks <= i}`` get probability
+        0. O(L0^2); ``_collect_last_P = False`` turns it off."""
+        bounds = cu_list if cu_list is not None else cu_seqlens[:2].tolist()
+        a, b = int(bounds[0]), int(bounds[1])
+        n = b - a
+        dev = q.device
+        seg = slice(a, b)
+        w0 = w_sizes[seg]
+        lmk, _, _ = _compute_landmark_indices(
+            x[seg].detach().float(), self.v_proj.weight.detach().float(), alpha.detach().float(), w0.float(),
+            torch.tensor([0, n], dtype=torch.int32, device=dev), self.k_lmk, self.n_min, n, [0, n],
+            head_dim=self.head_dim)
+        pos = torch.arange(n, device=dev)
+        back = pos.view(n, 1) - pos.view(1, n)                      # i - j
+        in_band = (back >= 0) & (back < w0.long().view(n, 1))       # i - w_i < j <= i
+        is_lmk = torch.zeros(self.n_heads, n + 1, dtype=torch.bool, device=dev)
+        is_lmk.scatter_(1, torch.where(lmk[:, 0] >= 0, lmk[:, 0], n), True)
+        keep = in_band.unsqueeze(0) | (is_lmk[:, None, :n] & (back >= 0).unsqueeze(0))
+        logits = torch.matmul(q[seg].transpose(0, 1), k[seg].transpose(0, 1).transpose(1, 2).contiguous())
+        logits = logits * (1.0 / math.sqrt(self.head_dim))
+        return logits.masked_fill(~keep, float("-inf")).softmax(dim=-1)

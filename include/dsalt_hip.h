@@ -190,14 +190,15 @@ int dsalt_select_check(const dsalt_select_args *args);
  *   z_x[t] = (||x_t|| - mean) / max(std, 1e-6),  z_v[t, h] = the same over ||v_t,g||
  * with mean and unbiased std over all T tokens (NaN std kept, as torch's clamp does).
  * The norms are taken in fp32 and rounded to the input dtype, as x.norm() returns them
- * for a 16-bit tensor. x, v: unit stride along d / D, 16-byte aligned rows; D / (16 bytes
+ * for a 16-bit tensor, unless norms_f32 is nonzero: torch's autocast computes .norm() in
+ * fp32 and returns it unrounded. x, v: unit stride along d / D, 16-byte aligned rows; D / (16 bytes
  * / v's element size) must be a power of two <= 64; n_kv_heads <= 128 and divides n_heads.
  * The means and stds are reduced in fp64 in a fixed order: the result is deterministic.
  */
 typedef struct dsalt_scores_args {
     int32_t total_len, d_model, n_kv_heads, head_dim, n_heads;
     int32_t x_dtype, v_dtype; /* each DSALT_DTYPE_BF16, _F16 or _F32 (autocast: fp32 x, bf16 v) */
-    int32_t reserved0;
+    int32_t norms_f32;        /* nonzero: keep the norms in fp32 (.norm() under autocast) */
     const void *x; /* [T, d_model] */
     int64_t x_stride_t;
     const void *v; /* [T, n_kv_heads, head_dim] */

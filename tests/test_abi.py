@@ -243,3 +243,21 @@ def test_rope_check():
     assert lib.dsalt_rope_check(ctypes.byref(a)) == 1
     a.table_rows = 100
     assert lib.dsalt_rope_check(ctypes.byref(a)) == 0
+
+
+def test_exports_are_none_without_the_library():
+    # the reference leaves its kernel entry points None when its kernels cannot load
+    # (dsalt/kernels/__init__.py:23-35); the same holds here when libdsalt_hip.so is absent
+    import subprocess
+    import sys
+
+    code = ("import dsalt, dsalt.kernels as k\n"
+            "assert not k._HIP_OK\n"
+            "assert k.dsalt_triton_attention is None and k.dsalt_triton_backward is None\n"
+            "assert k.autotune_blocks is None and k.get_tuned_config is None\n"
+            "assert dsalt.dsalt_triton_attention is None\n"
+            "print('ok')\n")
+    pkg = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "dsalt-library_amd")
+    env = dict(os.environ, PYTHONPATH=pkg, DSALT_HIP_LIB="/nonexistent/libdsalt_hip.so")
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
+    assert res.returncode == 0 and res.stdout.strip() == "ok", res.stderr

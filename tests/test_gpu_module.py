@@ -53,6 +53,12 @@ def test_module_train_matches_reference_golden(path):
         for s in range(lmk_pos.shape[1]):
             assert sorted(lmk_pos[h, s].tolist()) == sorted(d["lmk_pos"][h, s].tolist())
     out, aux = mod(x, cu_seqlens=cu)
+    # the selection the forward itself used (the module's default route) is the
+    # reference's, set for set
+    used = mod._last_selection[1].cpu()
+    for h in range(used.shape[0]):
+        for s in range(used.shape[1]):
+            assert sorted(used[h, s].tolist()) == sorted(d["lmk_pos"][h, s].tolist())
     assert float(aux) == 0.0
     check(out.detach(), d["out"], "out")
     out.backward(torch.from_numpy(d["dout"]).to(DEV))

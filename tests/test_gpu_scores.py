@@ -6,7 +6,13 @@ For fp32 inputs the scores match the float64-input oracle to fp32 rounding. For 
 inputs each norm is rounded to the input dtype, as x.norm() returns it; the kernel's
 fp32 sum of squares runs in another order than torch's, so a norm can land one unit in
 the last place of the 16-bit type away (about 1 norm in 10^4). The tests bound the
-fraction of such tokens instead of requiring equality."""
+fraction of such tokens instead of requiring equality. Under autocast torch keeps the
+norms in fp32 (``norms_f32``), and the kernel matches the float64 oracle to fp32
+rounding again.
+
+The module's default selection route does not use this kernel: it applies torch's own
+norm ops to v, which is bit-identical to the reference's x @ W_V.T route
+(tests/test_gpu_headline.py)."""
 import numpy as np
 import pytest
 import torch
@@ -41,14 +47,29 @@ def test_scores_fp32_match_oracle(n_kv):
         assert err < 2e-5, f"{name} max-abs error {err}"
 
 
+def test_scores_autocast_norms_f32():
+    # under autocast .norm() of a bf16 tensor runs in fp32 and is not rounded back
+    T, d, H, dh, n_kv = 4096, 1024, 16, 64, 16
+    x, v, alpha, _ = _inputs(T, d, n_kv, dh, H, 76)
+    x, v = x.to(torch.bfloat16), v.to(torch.bfloat16)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        s, zx, zv = _hip.hybrid_scores(x.to(DEV), v.to(DEV), alpha.to(DEV), H)
+        # torch's own autocast route on the same operands, for the record
+        ts, _, _ = hybrid_scores_from_v(x.to(DEV), v.to(DEV), alpha.to(DEV), H)
+    rs, rzx, rzv = orc.hybrid_scores_from_v(x.double(), v.double(), alpha.double(), H)
+    for got, ref, name in ((s, rs, "scores"), (zx, rzx, "z_x"), (zv, rzv, "z_v"), (ts, rs, "torch scores")):
+        err = (got.cpu().double() - ref).abs().max().item()
+        assert err < 5e-5, f"{name} max-abs error {err}"
+
+
 @pytest.mark.parametrize("xdt,vdt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
-                                     (torch.float32, torch.bfloat16)], ids=["bf16", "fp16", "autocast"])
+                                     (torch.float32, torch.bfloat16)], ids=["bf16", "fp16", "mixed"])
 def test_scores_16bit_match_oracle(xdt, vdt):
     print(f"scores {xdt} {vdt}", flush=True)
     T, d, H, dh, n_kv = 4096, 1024, 16, 64, 16
     x, v, alpha, _ = _inputs(T, d, n_kv, dh, H, 71)
     x, v = x.to(xdt), v.to(vdt)
-    s, zx, zv = _hip.hybrid_scores(x.to(DEV), v.to(DEV), alpha.to(DEV), H)
+    s, zx, zv = _hip.hybrid_scores(x.to(DEV), v.to(DEV), alpha.to(DEV), H, norms_f32=False)
     # the oracle takes the norms in the same 16-bit dtype (rounded there, then .float())
     rs, rzx, rzv = orc.hybrid_scores_from_v(x, v, alpha, H)
     for got, ref, name in ((s, rs, "scores"), (zx, rzx, "z_x"), (zv, rzv, "z_v")):
@@ -76,22 +97,27 @@ def test_scores_deterministic_strided_and_tiny():
     assert torch.isnan(rs1).all()
 
 
-def test_selection_from_v_matches_gemm_path():
-    # the selector with v= (fused scores) against the oracle selection of the same
-    # scores (bit-exact), and against the GEMM path's selection (same sets up to ties)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_selection_from_v_matches_gemm_path(dtype):
+    # v = x @ W.T formed on the GPU (as the module's v_proj does): the default v route
+    # selects exactly the GEMM route's sets; the HIP score kernel's selection is bit-exact
+    # on its own scores and agrees with the GEMM route up to near-ties
     g = torch.Generator().manual_seed(73)
     lens = [700, 333, 1100]
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
     T, d, H, dh, k = int(cu[-1]), 512, 8, 64, 32
-    x, v, alpha, W = _inputs(T, d, H, dh, H, 74)
+    x, _, alpha, W = _inputs(T, d, H, dh, H, 74)
+    xd, Wd = x.to(DEV, dtype), W.to(DEV, dtype)
+    vd = (xd @ Wd.T).view(T, H, dh)
     w = (torch.rand(T, generator=g) * 200 + 1).floor()
-    lmk_v, _, _ = _compute_landmark_indices(x.to(DEV), W.to(DEV), alpha.to(DEV), w.to(DEV), cu.to(DEV), k, 1, T,
-                                            cu.tolist(), head_dim=dh, v=v.to(DEV))
-    s_v, _, _ = _hip.hybrid_scores(x.to(DEV), v.to(DEV), alpha.to(DEV), H)
-    np.testing.assert_array_equal(lmk_v.cpu().numpy(), orc.select_landmarks(s_v.cpu().numpy(), w.numpy(), cu.numpy(), k))
-    lmk_w, _, _ = _compute_landmark_indices(x.to(DEV), W.to(DEV), alpha.to(DEV), w.to(DEV), cu.to(DEV), k, 1, T,
-                                            cu.tolist(), head_dim=dh)
-    same = (lmk_v == lmk_w).float().mean().item()
+    args = (xd, Wd, alpha.to(DEV), w.to(DEV), cu.to(DEV), k, 1, T, cu.tolist())
+    lmk_w, _, _ = _compute_landmark_indices(*args, head_dim=dh)
+    lmk_v, _, _ = _compute_landmark_indices(*args, head_dim=dh, v=vd)
+    assert torch.equal(lmk_v, lmk_w)
+    lmk_h, _, _ = _compute_landmark_indices(*args, head_dim=dh, v=vd, hip_scores=True)
+    s_v, _, _ = _hip.hybrid_scores(xd, vd, alpha.to(DEV), H)
+    np.testing.assert_array_equal(lmk_h.cpu().numpy(), orc.select_landmarks(s_v.cpu().numpy(), w.numpy(), cu.numpy(), k))
+    same = (lmk_h == lmk_w).float().mean().item()
     assert same > 0.99, f"only {same:.4f} of the landmark slots agree with the GEMM path"
 
 
@@ -121,10 +147,14 @@ def test_module_fused_selector(training):
     lens = [600, 424]
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=DEV)
     x = torch.randn(int(cu[-1]), 256, device=DEV)
-    outs = []
-    for fused in (True, False):
-        m._fused_selector = fused
+    outs, sels = [], []
+    for fused, hip_scores in ((True, False), (False, False), (True, True)):
+        m._fused_selector, m._hip_scores = fused, hip_scores
         out, _ = m(x, cu_seqlens=cu, cu_list=cu.tolist())
         outs.append(out.detach())
-    err = (outs[0] - outs[1]).abs().max().item()
-    assert err < 2e-2, f"fused vs GEMM selector output differs by {err}"
+        sels.append(m._last_selection[1].clone())
+    m._fused_selector, m._hip_scores = True, False
+    # the default route is the GEMM route's selection, hence the same output bit for bit
+    assert torch.equal(sels[0], sels[1]) and torch.equal(outs[0], outs[1])
+    err = (outs[2] - outs[1]).abs().max().item()
+    assert err < 2e-2, f"HIP-score selector output differs by {err}"
