@@ -5,6 +5,7 @@
 #include <string.h>
 
 #include <initializer_list>
+#include <mutex>
 
 #include "launch.h"
 
@@ -66,6 +67,35 @@ int check_span32(int total_len, std::initializer_list<int64_t> row_bytes) {
         return fail(DSALT_ERR_UNSUPPORTED,
                     "a sequence's rows must span < 4 GiB (total_len %d x row stride %lld B)", total_len,
                     (long long)widest);
+    return DSALT_OK;
+}
+
+// Scratch of dsalt_bwd_noalloc: one static array per GPU (each device holds its own copy
+// at its own address from the moment the library's code is loaded on it). In host code
+// `scratch` names a host-side stand-in, not device memory: its device address is looked
+// up once per device with hipGetSymbolAddress (that device current) and only that
+// address is ever handed to kernels.
+__device__ __align__(256) char scratch[DSALT_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 256;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device id, null until looked up
+
+int scratch_address(void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(DSALT_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(DSALT_ERR_UNSUPPORTED, "device id %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(DSALT_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
     return DSALT_OK;
 }
 
@@ -285,6 +315,28 @@ int dsalt_bwd(const dsalt_bwd_args *a, void *stream) {
     if (rc) return rc;
     hipError_t e = dsalt::launch_bwd(*a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(DSALT_ERR_LAUNCH, "dsalt_bwd launch failed: %s", hipGetErrorString(e));
+    return DSALT_OK;
+}
+
+int dsalt_bwd_noalloc(const dsalt_bwd_args *a, void *stream) {
+    if (!a) return fail(DSALT_ERR_INVALID, "args is NULL");
+    const int64_t need = dsalt_bwd_workspace_size(a->total_len, a->num_seqs, a->n_heads, a->head_dim, a->k_lmk);
+    if (need < 0) return fail(DSALT_ERR_INVALID, "invalid sizes (total_len, num_seqs, n_heads, k_lmk)");
+    if (need > DSALT_NOALLOC_SCRATCH_BYTES)
+        return fail(DSALT_ERR_UNSUPPORTED,
+                    "dsalt_bwd_noalloc: this call needs %lld bytes of scratch, above the static %lld "
+                    "(use dsalt_bwd with a caller workspace)",
+                    (long long)need, (long long)DSALT_NOALLOC_SCRATCH_BYTES);
+    void *scratch_ptr = nullptr;
+    int rc = scratch_address(&scratch_ptr);
+    if (rc) return rc;
+    dsalt_bwd_args b = *a;
+    b.workspace = scratch_ptr;
+    b.workspace_bytes = DSALT_NOALLOC_SCRATCH_BYTES;
+    if ((rc = dsalt_bwd_check(&b))) return rc;
+    hipError_t e = dsalt::launch_bwd(b, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess)
+        return fail(DSALT_ERR_LAUNCH, "dsalt_bwd_noalloc launch failed: %s", hipGetErrorString(e));
     return DSALT_OK;
 }
 

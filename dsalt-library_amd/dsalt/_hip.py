@@ -121,7 +121,9 @@ EXPORTED_SYMBOLS = (
     "dsalt_abi_version", "dsalt_last_error", "dsalt_fwd_args_size", "dsalt_bwd_args_size",
     "dsalt_select_args_size", "dsalt_hybrid_scores", "dsalt_scores_check", "dsalt_scores_workspace_size",
     "dsalt_scores_args_size", "dsalt_rope", "dsalt_rope_check", "dsalt_rope_args_size",
+    "dsalt_bwd_noalloc",
 )
+NOALLOC_SCRATCH_BYTES = 128 << 20  # DSALT_NOALLOC_SCRATCH_BYTES
 
 _lib = None
 
@@ -141,6 +143,7 @@ def lib() -> ctypes.CDLL:
         ("dsalt_fwd_check", [ctypes.POINTER(FwdArgs)]),
         ("dsalt_bwd", [ctypes.POINTER(BwdArgs), c_void_p]),
         ("dsalt_bwd_check", [ctypes.POINTER(BwdArgs)]),
+        ("dsalt_bwd_noalloc", [ctypes.POINTER(BwdArgs), c_void_p]),
         ("dsalt_select_landmarks", [ctypes.POINTER(SelectArgs), c_void_p]),
         ("dsalt_select_check", [ctypes.POINTER(SelectArgs)]),
         ("dsalt_hybrid_scores", [ctypes.POINTER(ScoresArgs), c_void_p]),

@@ -158,6 +158,23 @@ int dsalt_bwd(const dsalt_bwd_args *args, void *stream);
 int dsalt_bwd_check(const dsalt_bwd_args *args);
 
 /*
+ * dsalt_bwd without a caller workspace and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The backward's scratch (per-query records, block band starts, per-head window
+ * partials, landmark partials) lives in a static device array of
+ * DSALT_NOALLOC_SCRATCH_BYTES bytes that the library holds on every GPU it runs on until
+ * the process ends; args->workspace and args->workspace_bytes are ignored. A call whose
+ * dsalt_bwd_workspace_size(...) exceeds that size returns DSALT_ERR_UNSUPPORTED without
+ * launching. Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other threads) race and must be serialised by the caller. The array
+ * keeps the last call's contents; the kernels write every scratch entry they read.
+ * The first call on a device looks the array's address up (with that device current).
+ */
+#define DSALT_NOALLOC_SCRATCH_BYTES ((int64_t)128 << 20)
+int dsalt_bwd_noalloc(const dsalt_bwd_args *args, void *stream);
+
+/*
  * Landmark top-k selection.
  * Replaces the covered mask, the per-(head, sequence) torch.topk and the -1 fill of
  * _compute_landmark_indices (dsalt/kernels/selectors.py:105-134).
