@@ -42,6 +42,11 @@ struct BF16 {
     // the low / high element of a packed pair
     static __device__ __forceinline__ float lo_f32(uint32_t x) { return __uint_as_float(x << 16); }
     static __device__ __forceinline__ float hi_f32(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+    // acc + lo + hi of a packed pair, in fp32 (v_dot2c_f32_bf16 against (1, 1))
+    static __device__ __forceinline__ float add_pair(uint32_t x, float acc) {
+        const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+        return __builtin_amdgcn_fdot2_f32_bf16(bitcast<bf16x2>(x), one, acc, false);
+    }
 };
 
 struct F16 {
@@ -58,6 +63,11 @@ struct F16 {
     }
     static __device__ __forceinline__ float lo_f32(uint32_t x) { return to_f32((uint16_t)x); }
     static __device__ __forceinline__ float hi_f32(uint32_t x) { return to_f32((uint16_t)(x >> 16)); }
+    // acc + lo + hi of a packed pair, in fp32 (v_dot2c_f32_f16 against (1, 1))
+    static __device__ __forceinline__ float add_pair(uint32_t x, float acc) {
+        const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+        return __builtin_amdgcn_fdot2(bitcast<f16x2>(x), one, acc, false);
+    }
 };
 
 // Row index (within a 32-row MFMA block) of accumulator register r of a lane in half
@@ -105,6 +115,13 @@ __device__ __forceinline__ float half_max(float x) {
 __device__ __forceinline__ float half_sum(float x) {
     auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// max(a, b, c) as one v_maximum3_f32 (gfx950). IEEE maximum propagates NaN and needs
+// no quieted inputs; through fmaxf (maxNum) the compiler quiets MFMA results with an
+// extra v_max_f32 x, x per operand before combining them.
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

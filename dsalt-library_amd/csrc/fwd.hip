@@ -44,6 +44,10 @@ namespace dsalt {
 namespace {
 
 constexpr float kStaleMax = 8.0f;  // allowed growth of the row max before a rescale (log2)
+// Band mask table: acc_row_const(r) <= 27 for the 16 accumulator elements of a lane, so
+// rows d = 0 (nothing masked) .. 28 (everything masked) cover every clamped bound.
+constexpr int kMaskRows = 29;
+constexpr int kMaskStride = 20;
 
 struct FwdParams {
     const uint16_t *q, *k, *v;
@@ -80,6 +84,10 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     __shared__ __align__(1024) char s_tiles[2][R][TB];  // [K, V][slot]
     __shared__ int s_red[NW][2];
     __shared__ int s_ltmin[DSALT_MAX_K_LMK / BN];  // smallest position in each landmark tile
+    // Band mask rows: row d holds, per accumulator element r of a 32-key row block, -inf
+    // when the element's row offset acc_row_const(r) is below d, else 0 (rows padded to
+    // 80 bytes so that lanes reading different rows spread over the banks).
+    __shared__ __align__(16) float s_mtab[kMaskRows][kMaskStride];
     extern __shared__ int s_dyn[];
     int *s_lpos = s_dyn;                                          // INT_MAX: empty slot
     float *s_lbias = reinterpret_cast<float *>(s_dyn + p.k_pad);  // raw-unit bias
@@ -194,7 +202,6 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     const int wlo = wave_min_u(qvalid ? lo : INT_MAX);
     const int wclo = wave_max_u(qvalid ? corelo : INT_MIN);
     const int wpmax = wave_max_u(qvalid ? pmax : -1);
-    const int wchi = wq0;                        // first query of the wave
 
     // ---- landmark slots -> LDS (invalid / out-of-sequence slots become INT_MAX) --------
     // k_pad is a multiple of 64: slot block j of wave w (64 slots from s = 64 (NW j + w))
@@ -227,6 +234,10 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
         s_red[wave][0] = wlo;
         s_red[wave][1] = wpmax;
     }
+    for (int e = tid; e < kMaskRows * 16; e += NT) {
+        const int d = e >> 4, r = e & 15;
+        s_mtab[d][r] = acc_row_const(r) < d ? -INFINITY : 0.f;
+    }
     // LDS writes visible to the workgroup; the tile loads stay in flight
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     int glo = s_red[0][0], gpmax = s_red[0][1];
@@ -256,14 +267,28 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
         else vlanes.load_gather_lean(v_lds(t), wave, vrs, vst, s_lrow + lmk_tile(t) * BN);
     };
 
-    // S^T (BN keys x 32 queries) = K . Q^T, raw q.k, from the K tile in ring slot `slot`
-    auto qk_tile = [&](int slot, f32x16 (&sacc)[NRB]) {
+    // S^T (BN keys x 32 queries) = K . Q^T, raw q.k, of tile t from the K tile in ring
+    // slot `slot`. The accumulator starts from the band mask's lower edge: element (rb, r)
+    // is key tb + 32 rb + acc_row_const(r) + 4 hh, below lo exactly when
+    // acc_row_const(r) < lo - tb - 32 rb - 4 hh = mb + BN t - 32 rb, so its initial value
+    // is mask row clamp(mb + BN t - 32 rb, 0, 28): -inf there (the MFMA keeps it -inf), 0
+    // elsewhere. No VALU touches the elements; landmark tiles start from row 0 (zeros).
+    const int mb = lo - ghi + BN - 1 - hh * 4;
+    auto qk_tile = [&](int t, int slot, f32x16 (&sacc)[NRB]) {
         const char *ktile = s_tiles[0][slot];
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
+            const int d = (t < nb) ? min(max(mb + BN * t - 32 * rb, 0), kMaskRows - 1) : 0;
+            const float4 *mrow = reinterpret_cast<const float4 *>(&s_mtab[d][0]);
             f32x16 acc;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+            for (int g = 0; g < 4; ++g) {
+                const float4 m4 = mrow[g];
+                acc[4 * g + 0] = m4.x;
+                acc[4 * g + 1] = m4.y;
+                acc[4 * g + 2] = m4.z;
+                acc[4 * g + 3] = m4.w;
+            }
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
                 const vec8 a = bitcast<vec8>(tile_read_row16<D>(ktile, rb * 32 + ql, 2 * s + hh));
@@ -296,8 +321,9 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
             ec[j] = fast_exp2((kEdgeMid - (float)((j >> 4) * 32 + acc_row_const(j & 15))) * p.inv_tau * kLog2e);
     }
 
-    // P = exp2(S * c - mu) of one tile: fp32 row sums (unrounded, as the LSE needs them)
-    // and the 16-bit P^T operand. Masked scores are -inf and give 0.
+    // P = exp2(S * c - mu) of one tile: the 16-bit P^T operand, and the row sums of the
+    // same rounded P in fp32 (one v_dot2 per pair), so that O is normalised by exactly
+    // the weights its P V products used. Masked scores are -inf and give 0.
     auto exp_pack = [&](const f32x16 (&sacc)[NRB], uint32_t (&pk)[NRB][8]) {
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb)
@@ -305,9 +331,9 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
             for (int j = 0; j < 8; ++j) {
                 const float e0 = fast_exp2(fmaf(sacc[rb][2 * j], c, -mu));
                 const float e1 = fast_exp2(fmaf(sacc[rb][2 * j + 1], c, -mu));
-                if (j & 1) lsum1 += e0 + e1;
-                else lsum0 += e0 + e1;
                 pk[rb][j] = DT::pack2(e0, e1);
+                if (j & 1) lsum1 = DT::add_pair(pk[rb][j], lsum1);
+                else lsum0 = DT::add_pair(pk[rb][j], lsum0);
             }
     };
     // O^T (D x 32 queries) += V^T . P^T ; k-step kk covers tile keys kk*16..+15
@@ -374,57 +400,57 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
             }
         }
     };
-    // Band mask of tile t (keys outside [lo, i]; all kept for landmark tiles) applied in
-    // place, branch-free; returns the tile's masked row max (raw units, -inf if empty).
-    // Element (rb, r) is key tb + rb*32 + acc_row_const(r) + hh*4 =: tb + hh*4 + cst.
-    // With tb = ghi - BN + 1 - BN t, the bounds are cst <= A0 + BN t (key <= i) and
-    // cst >= B0 + BN t (key >= lo); nA0 / nB0 are the bit counts of rows_le at t = 0.
-    const int A0 = i - ghi + BN - 1 - hh * 4, B0 = lo - ghi + BN - 1 - hh * 4;
+    // Causal edge of tile t (keys after the lane's query), applied in place by VALU. Only
+    // tiles t < NC = BM / BN reach past a wave's first query (tile t ends at key ghi - BN t
+    // and every wave starts at ghi - BM + 1 or later); the lower edge came with the
+    // accumulator's initial value. Element (rb, r) is key tb + hh*4 + cst with cst = rb*32 + acc_row_const(r),
+    // kept iff cst <= A0 + BN t; nA0 is the bit count of rows_le at t = 0.
+    const int A0 = i - ghi + BN - 1 - hh * 4;
     const int nA0 = 4 * (A0 >> 3) + min((A0 & 7) + 1, 4);
-    const int nB0 = 4 * ((B0 - 1) >> 3) + min(((B0 - 1) & 7) + 1, 4);
-    auto mask_max = [&](int t, f32x16 (&sacc)[NRB]) -> float {
-        uint32_t band;
-        if constexpr (NRB == 1) {
-            // rows_le(A0 + BN t) keeps the low clamp(nA0 + 16 t, 0, 16) bits (BN t is a
-            // multiple of 8), so the band is the bit field [nB, nA): med3, med3, bfm
-            const int nA = min(max(nA0 + 16 * t, 0), 16);
-            const int nB = min(max(nB0 + 16 * t, 0), 16);
-            band = ((1u << (nA - nB)) - 1u) << nB;
-        } else {
-            const int tb = band_key0(t);
-            const int A = i - tb - hh * 4;   // key <= i  <=> cst <= A
-            const int B = lo - tb - hh * 4;  // key >= lo <=> cst >= B
-            band = rows_le(A) & ~rows_le(B - 1);
+    // Returns the tile's row max (raw units, -inf if empty), after the causal edge when
+    // `causal` (tiles t < NC).
+    auto mask_max = [&](auto causal, int t, f32x16 (&sacc)[NRB]) -> float {
+        if constexpr (decltype(causal)::value) {
+            uint32_t keep;
+            if constexpr (NRB == 1) {
+                // rows_le(A0 + BN t) keeps the low clamp(nA0 + 16 t, 0, 16) bits
+                const int nA = min(max(nA0 + 16 * t, 0), 16);
+                keep = (uint32_t)((1ull << nA) - 1ull);
+            } else {
+                keep = rows_le(A0 + BN * t);
+            }
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r]);
         }
-        const uint32_t keep = (t < nb) ? band : 0xffffffffu;
-#pragma unroll
-        for (int rb = 0; rb < NRB; ++rb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r]);
         // v_max3 trees, two chains per row block
         float tm[2 * NRB];
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
-            tm[2 * rb] = fmaxf(fmaxf(sacc[rb][0], sacc[rb][1]), sacc[rb][2]);
-            tm[2 * rb + 1] = fmaxf(fmaxf(sacc[rb][3], sacc[rb][4]), sacc[rb][5]);
+            tm[2 * rb] = max3f(sacc[rb][0], sacc[rb][1], sacc[rb][2]);
+            tm[2 * rb + 1] = max3f(sacc[rb][3], sacc[rb][4], sacc[rb][5]);
         }
 #pragma unroll
         for (int r = 6; r < 16; r += 2)
 #pragma unroll
             for (int rb = 0; rb < NRB; ++rb) {
                 float &x = tm[2 * rb + (NRB == 1 ? ((r >> 1) & 1) : 0)];
-                x = fmaxf(fmaxf(x, sacc[rb][r]), sacc[rb][r + 1]);
+                x = max3f(x, sacc[rb][r], sacc[rb][r + 1]);
             }
-        float mx = fmaxf(tm[0], tm[1]);
-        if constexpr (NRB == 2) mx = fmaxf(mx, fmaxf(tm[2], tm[3]));
-        return half_max(mx);
+        float mx = max3f(tm[0], tm[1], tm[1]);
+        if constexpr (NRB == 2) mx = max3f(mx, tm[2], tm[3]);
+        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+        return max3f(__uint_as_float(sw[0]), __uint_as_float(sw[1]), __uint_as_float(sw[1]));
     };
     // Raise the running max when the tile max exceeds it by more than kStaleMax
     // (wave-uniform branch, rare after the first tile): O and l are rescaled to it.
-    auto rescale = [&](float tmax) {
-        const float tm2 = tmax * c;
-        const bool raise = tm2 > m2 + kStaleMax;
-        if (__builtin_amdgcn_ballot_w64(raise)) {
+    // `thr` is m2 + kStaleMax in raw score units, so the test is one compare.
+    float thr = -INFINITY;
+    auto rescale = [&](bool more, float tmax) {
+        const bool raise = tmax > thr;
+        if (__builtin_amdgcn_ballot_w64(raise) && more) {
+            const float tm2 = tmax * c;
             const float alpha = raise ? fast_exp2(m2 - tm2) : 1.f;
             lsum0 *= alpha;
             lsum1 *= alpha;
@@ -434,6 +460,7 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
                 for (int r = 0; r < 16; ++r) oacc[d][r] *= alpha;
             m2 = raise ? tm2 : m2;
             mu = (m2 == -INFINITY) ? 0.f : m2;
+            thr = raise ? tmax + kStaleMax * p.inv_c : thr;
         }
     };
 
@@ -452,18 +479,18 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     // nt >= R; the setup issued K of tiles 0 .. R-1 and V of tiles 0 .. R-2. The last
     // iteration computes S of a tile that does not exist (stale LDS slot) and ignores it.
     // MFMAs and operand reads of the two parts of an iteration, and the VALU instructions
-    // placed after each MFMA (part A: exp / sum / pack, ~56 per row block; part B: masks
-    // and max, ~40 per row block)
+    // placed after each MFMA (part A: exp / pack / sum, ~48 per row block; part B: the
+    // max tree, 8 v_maximum3 per row block, two after each P V MFMA)
     constexpr int NQK = KS * NRB, NPV = 2 * ND * NRB;
     constexpr int VALU_A = (NRB * 56 - 16 + NQK - 1) / NQK + 2;
-    constexpr int VALU_B = (NRB * 32 + NPV - 1) / NPV;
-    auto step = [&](int t, f32x16 (&cur)[NRB], f32x16 (&nxt)[NRB]) {
+    constexpr int VALU_B = 2;
+    auto step = [&](auto causal, int t, f32x16 (&cur)[NRB], f32x16 (&nxt)[NRB]) {
         if (t + R < nt) issue_k(t + R);
         if (t + R - 1 < nt) issue_v(t + R - 1);
         uint32_t pk[NRB][8];
-        qk_tile(slot_of(t + 1), nxt);
+        qk_tile(t + 1, slot_of(t + 1), nxt);
         exp_pack(cur, pk);
-        __builtin_amdgcn_sched_group_barrier(0x100, NQK, 0);  // K operand reads
+        __builtin_amdgcn_sched_group_barrier(0x100, NQK + 4 * NRB, 0);  // mask rows, K operand reads
         __builtin_amdgcn_sched_group_barrier(0x402, 16, 0);   // VALU / transcendental
 #pragma unroll
         for (int m = 0; m < NQK; ++m) {
@@ -479,28 +506,47 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
         const bool more = t + 1 < nt;
         if (more) adjust(t + 1, nxt);
         pv(pk, slot_of(t));
-        const float tmax = mask_max(t + 1, nxt);
+        const float tmax = mask_max(causal, t + 1, nxt);
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * NPV, 1);  // V operand reads
-        __builtin_amdgcn_sched_group_barrier(0x002, 12, 1);       // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);        // VALU
 #pragma unroll
         for (int m = 0; m < NPV; ++m) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);       // MFMA
             __builtin_amdgcn_sched_group_barrier(0x002, VALU_B, 1);  // VALU
         }
-        rescale(more ? tmax : -INFINITY);
+        rescale(more, tmax);
         if (t + R < nt) tile_barrier<(R - 2) * LPT>();
         else tile_barrier<0>();
     };
     f32x16 sA[NRB], sB[NRB];
     tile_barrier<(R - 2) * LPT>();  // K of tiles 0, 1 and V of tile 0 landed
-    qk_tile(0, sA);
+    using causal_edge = std::true_type;
+    using no_causal_edge = std::false_type;
+    qk_tile(0, slot_of(0), sA);
     adjust(0, sA);
-    rescale(mask_max(0, sA));
+    rescale(true, mask_max(causal_edge(), 0, sA));
     // step 0 refills the slot of K of tile 0: every wave must have read it first
     tile_barrier<(R - 2) * LPT>();
-    for (int t = 0; t < nt; t += 2) {
-        step(t, sA, sB);
-        if (t + 1 < nt) step(t + 1, sB, sA);
+    // steps 0 .. NC-2 mask the causal edge of tiles 1 .. NC-1; later tiles lie below every
+    // query of the workgroup (nt >= R >= 2, so step 0 always runs)
+    constexpr int NC = BM / BN;
+    static_assert(NC >= 1 && NC <= 4, "causal peel covers at most four tiles");
+    if constexpr (NC > 1) step(causal_edge(), 0, sA, sB);
+    if constexpr (NC > 2) {
+        if (1 < nt) step(causal_edge(), 1, sB, sA);
+    }
+    if constexpr (NC > 3) {
+        if (2 < nt) step(causal_edge(), 2, sA, sB);
+    }
+    constexpr int T0 = NC - 1;  // first step without a causal edge
+    for (int t = T0; t < nt; t += 2) {
+        if constexpr (T0 % 2 == 0) {
+            step(no_causal_edge(), t, sA, sB);
+            if (t + 1 < nt) step(no_causal_edge(), t + 1, sB, sA);
+        } else {
+            step(no_causal_edge(), t, sB, sA);
+            if (t + 1 < nt) step(no_causal_edge(), t + 1, sA, sB);
+        }
     }
 
     // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln 2 --------------------------------
