@@ -15,6 +15,11 @@ path. It restates, on the CPU, the reference algorithm of LeonardoCofone/dsalt-l
                          the dense reference dsalt_attention.py:520-563
   gradients              torch autograd through attention_hard / attention_soft in fp64
                          (the formulas of dsalt_triton_train.py:302-383, :439-476)
+  attention_dense        the dense batched variant of _batched / _diff_logbias
+                         (dsalt/modules/dsalt_attention.py:286-329, :371-438): soft window
+                         tail on every causal key, landmarks admitted at d >= max(1, floor(w~)),
+                         union = elementwise max of the two log-biases
+  module_batched_forward dsalt_attention.py:371-401 (B = 1) from the module parameters
   cpu_baseline_hard      the reference's CPU fallback cost model: dense per-sequence mask +
                          F.scaled_dot_product_attention in fp32 (dsalt_attention.py:95-144,
                          dsalt/kernels/sparse_attn.py:29-57), with the HARD kernel's mask
@@ -503,3 +508,111 @@ def module_eval_forward(params: dict, cfg: dict, x: torch.Tensor, cu):
     lmk_pos = torch.from_numpy(select_landmarks(s32.numpy(), w_sizes, np.array(cu), cfg["k_lmk"]))
     o, _ = attention_hard(q, k, v, w_sizes, lmk_pos, None, cu)
     return o.reshape(T, d_model) @ params["out_proj.weight"].T, (w_sizes, lmk_pos)
+
+
+# ---------------------------------------------------------------------------------------
+# dense batched variant: dsalt/modules/dsalt_attention.py:286-329 (log-biases), :371-401
+# (_batched), :403-438 (_diff_logbias)
+# ---------------------------------------------------------------------------------------
+
+
+def dense_logbias(w_cont: torch.Tensor, lmk_bias_dense: torch.Tensor, T: int, tau_win: float = 1.0,
+                  win_edge: float = 4.0) -> torch.Tensor:
+    """The union log-bias [H, T, T] of the dense variant (natural-log units).
+
+    Window (dsalt_attention.py:286-312): d = i - j; 0 in the core d <= w~_i - win_edge
+    (fp32 compare), log(max(sigmoid((w~_i - d) / tau), 1e-20)) elsewhere for d >= 0, -inf
+    for d < 0. Landmarks (:314-329, validity :420-433): lmk_bias_dense[h, j] (-inf for
+    keys that are not landmarks of head h) where d >= 0 and d >= max(1, floor(w~_i)).
+    Union (:389): the elementwise maximum (torch.maximum: ties split the gradient).
+    Differentiable in w_cont (through the soft tail) and lmk_bias_dense."""
+    idx = torch.arange(T)
+    d = (idx.unsqueeze(1) - idx.unsqueeze(0)).to(torch.float32)            # [T, T] = i - j
+    w32 = w_cont.detach().to(torch.float32).unsqueeze(1)
+    core = d <= (w32 - torch.tensor(win_edge, dtype=torch.float32))
+    w_i = w_cont.unsqueeze(1)
+    g = torch.sigmoid((w_i - d.to(w_cont.dtype)) / tau_win)
+    logb = torch.log(g.clamp(min=1e-20))
+    logb = torch.where(core, torch.zeros_like(logb), logb)
+    logb = logb.masked_fill(d < 0, float("-inf"))
+    w_disc = torch.floor(w32).clamp(min=1)
+    valid = (d >= 0) & (d >= w_disc)                                         # [T, T]
+    lmk = lmk_bias_dense.unsqueeze(1).expand(-1, T, T)                       # [H, T(i), T(j)]
+    lmk = torch.where(valid.unsqueeze(0), lmk, torch.full_like(lmk, float("-inf")))
+    return torch.maximum(logb.unsqueeze(0), lmk)
+
+
+def attention_dense(q, k, v, w_cont, lmk_bias_dense, tau_win=1.0, win_edge=4.0, scale=None):
+    """Dense batched DSALT attention of one sequence (dsalt_attention.py:371-401):
+    softmax over every causal key of q.k * scale + the union log-bias. q/k/v [T, H, D],
+    w_cont [T], lmk_bias_dense [H, T]. Returns (O [T, H, D], LSE [T, H])."""
+    T, H, D = q.shape
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    bias = dense_logbias(w_cont, lmk_bias_dense, T, tau_win, win_edge).to(q.dtype)
+    logits = torch.matmul(q.transpose(0, 1), k.transpose(0, 1).transpose(-1, -2)) * scale + bias
+    lse = torch.logsumexp(logits, dim=-1)                                      # [H, T]
+    p = torch.exp(logits - lse.unsqueeze(-1))
+    o = torch.matmul(p, v.transpose(0, 1))                                     # [H, T, D]
+    return o.transpose(0, 1), lse.transpose(0, 1)
+
+
+def dense_landmark_bias(scores: torch.Tensor, k_lmk: int, tau_lmk: float = 2.0) -> torch.Tensor:
+    """lmk_bias_dense [H, T]: log(clamp(sigmoid(s / tau_lmk), 1e-20)) at the top-min(k, T)
+    keys of each head over all T tokens (no covered exclusion; the selection is made on
+    the detached fp32 scores), -inf elsewhere (dsalt_attention.py:318-329, :421-431)."""
+    T, H = scores.shape
+    sel = torch.zeros(H, T, dtype=torch.bool)
+    k_act = min(k_lmk, T)
+    if k_act > 0:
+        s32 = scores.detach().to(torch.float32).numpy()
+        w0 = np.zeros(T, dtype=np.float32)                                     # nothing covered
+        pos = select_landmarks(s32, w0, np.array([0, T]), k_act)              # [H, 1, k]
+        for h in range(H):
+            p = pos[h, 0]
+            sel[h, p[p >= 0]] = True
+    w_lmk = torch.log(torch.sigmoid(scores / tau_lmk).clamp(min=1e-20)).transpose(0, 1)
+    return torch.where(sel, w_lmk, torch.full_like(w_lmk, float("-inf")))
+
+
+def module_batched_forward(params: dict, cfg: dict, x: torch.Tensor, tau_win=1.0, tau_lmk=2.0,
+                           win_edge=4.0):
+    """DSALTAttention.forward(x) without cu_seqlens for x [1, T, d_model]
+    (dsalt_attention.py:371-401): q/k/v projections, RoPE at positions 0..T-1, GQA
+    repeat, continuous windows, hybrid scores on x (GEMM route), the dense union
+    log-bias, softmax, out_proj. Differentiable in x and the parameters. Returns
+    (out [1, T, d_model], (w_cont, lmk_bias_dense))."""
+    xs = x[0]
+    T, d_model = xs.shape
+    H = cfg["n_heads"]
+    D = d_model // H
+    n_kv = cfg.get("n_kv_heads") or H
+
+    def lin(name, inp):
+        y = inp @ params[name + ".weight"].T
+        b = params.get(name + ".bias")
+        return y if b is None else y + b
+
+    q = lin("q_proj", xs).view(T, H, D)
+    k = lin("k_proj", xs).view(T, n_kv, D)
+    v = lin("v_proj", xs).view(T, n_kv, D)
+    cos, sin = rope_cache(cfg["max_seq_len"], D, cfg.get("rope_base", 10000.0), cfg.get("yarn_scale", 1.0),
+                          dtype=xs.dtype)
+    c, s_ = cos[:T].unsqueeze(1), sin[:T].unsqueeze(1)
+    q, k = rotate(q, c, s_), rotate(k, c, s_)
+    if n_kv != H:
+        rep = H // n_kv
+        k = k.unsqueeze(2).expand(T, n_kv, rep, D).reshape(T, H, D)
+        v = v.unsqueeze(2).expand(T, n_kv, rep, D).reshape(T, H, D)
+    w_cont = cfg["n_min"] + torch.sigmoid(lin("win_gate", xs).squeeze(-1)) * (cfg["n_max"] - cfg["n_min"])
+    alpha = torch.sigmoid(params["alpha_w"])
+    scores, _, _ = hybrid_scores(xs, params["v_proj.weight"], alpha, H, D)
+    with torch.no_grad():
+        s_sel, _, _ = hybrid_scores(xs.detach().float(), params["v_proj.weight"].detach().float(),
+                                    alpha.detach().float(), H, D)
+    lb = dense_landmark_bias(scores, cfg["k_lmk"], tau_lmk)
+    # the selection itself is made on the detached fp32 scores
+    sel = dense_landmark_bias(s_sel, cfg["k_lmk"], tau_lmk) > float("-inf")
+    lb = torch.where(sel, lb, torch.full_like(lb, float("-inf")))
+    o, _ = attention_dense(q, k, v, w_cont, lb, tau_win, win_edge)
+    out = o.reshape(T, d_model) @ params["out_proj.weight"].T
+    return out.unsqueeze(0), (w_cont, lb)

@@ -8,7 +8,10 @@ What it pins: the part no closed form covers - the module composition of
 dsalt/modules/dsalt_attention.py in training mode on packed uniform-length input
 (q/k/v projections -> RoPE -> _train_selectors (continuous window, landmark top-k,
 soft landmark weight) -> the dense SOFT attention of _packed_train ->
-out_proj), and the gradients of the output with respect to x and every parameter.
+out_proj), and the gradients of the output with respect to x and every parameter;
+and the dense batched variant forward(x) for x [1, T, d_model] (_batched /
+_diff_logbias, :366-438) in training mode (output and every gradient) and in eval mode
+(output and the dense _last_P), with the landmark keys each head selected.
 On a CPU the reference takes its dense path (_packed_train, :489-563), which is the
 reference's own definition of the training kernel's math. TORCHDYNAMO_DISABLE=1 runs
 its torch.compile'd RoPE eagerly.
@@ -36,10 +39,61 @@ CASES = {
 }
 
 
+# the dense batched variant: DSALTAttention.forward(x) with x [1, T, d_model] and no
+# cu_seqlens (dsalt/modules/dsalt_attention.py:366-438)
+BATCHED_CASES = {
+    "module_batched_mha": dict(d_model=128, n_heads=2, n_min=4, n_max=40, k_lmk=8, max_seq_len=256,
+                               n_kv_heads=None, qkv_bias=False, yarn_scale=1.0, rope_base=10000.0,
+                               T=96, seed=3),
+    "module_batched_gqa": dict(d_model=128, n_heads=2, n_min=2, n_max=24, k_lmk=5, max_seq_len=128,
+                               n_kv_heads=1, qkv_bias=True, yarn_scale=2.0, rope_base=500.0,
+                               T=80, seed=4),
+}
+
+
+def write_batched(DSALTAttention, hybrid_scores_per_head) -> None:
+    import torch
+
+    for name, cfg in BATCHED_CASES.items():
+        torch.manual_seed(cfg["seed"])
+        mod = DSALTAttention(cfg["d_model"], cfg["n_heads"], cfg["n_min"], cfg["n_max"], cfg["k_lmk"],
+                             cfg["max_seq_len"], yarn_scale=cfg["yarn_scale"], n_kv_heads=cfg["n_kv_heads"],
+                             qkv_bias=cfg["qkv_bias"], rope_base=cfg["rope_base"])
+        T = cfg["T"]
+        x = torch.randn(1, T, cfg["d_model"])
+        # the landmark keys of each head, selected over all T tokens (dsalt_attention.py:421-428)
+        with torch.no_grad():
+            scores, _, _ = hybrid_scores_per_head(x[0], mod.v_proj.weight, torch.sigmoid(mod.alpha_w),
+                                                  cfg["n_heads"], cfg["d_model"] // cfg["n_heads"])
+            _, top = torch.topk(scores, min(cfg["k_lmk"], T), dim=0, sorted=False)
+            sel = torch.zeros(cfg["n_heads"], T, dtype=torch.bool)
+            sel.scatter_(1, top.transpose(0, 1), True)
+            w_cont = mod._window_continuous(x[0])
+        mod.train()
+        xg = x.clone().requires_grad_()
+        out, _ = mod(xg)
+        dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(200 + cfg["seed"]))
+        out.backward(dout)
+        mod.eval()
+        with torch.no_grad():
+            out_eval, _ = mod(x)
+        arrays = {"config": np.array(json.dumps(cfg)), "x": x.numpy(), "out": out.detach().numpy(),
+                  "dout": dout.numpy(), "grad.x": xg.grad.numpy(), "w_cont": w_cont.numpy(),
+                  "lmk_sel": sel.numpy().astype(np.uint8), "out_eval": out_eval.numpy(),
+                  "last_P": mod._last_P.numpy()}
+        for pname, prm in mod.named_parameters():
+            arrays["p." + pname] = prm.detach().numpy()
+            arrays["grad." + pname] = prm.grad.numpy()
+        path = os.path.join(HERE, name + ".npz")
+        np.savez_compressed(path, **arrays)
+        print(f"wrote {path} ({os.path.getsize(path)} bytes)")
+
+
 def main(ref_root: str) -> None:
     os.environ.setdefault("TORCHDYNAMO_DISABLE", "1")
     sys.path.insert(0, ref_root)
     import torch
+    from dsalt.kernels.landmark_tokens_ker import hybrid_scores_per_head
     from dsalt.modules.dsalt_attention import DSALTAttention
 
     for name, cfg in CASES.items():
@@ -69,6 +123,7 @@ def main(ref_root: str) -> None:
         path = os.path.join(HERE, name + ".npz")
         np.savez_compressed(path, **arrays)
         print(f"wrote {path} ({os.path.getsize(path)} bytes)")
+    write_batched(DSALTAttention, hybrid_scores_per_head)
 
 
 if __name__ == "__main__":
