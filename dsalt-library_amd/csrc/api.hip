@@ -37,8 +37,9 @@ int check_tensor(const char *name, const void *p, int64_t st, int64_t sh, int ve
 
 int check_common(int mode, int dtype, int T, int S, int H, int D, int k, const int32_t *cu,
                  const float *w, const int64_t *lmk_pos) {
-    if (mode != DSALT_MODE_HARD && mode != DSALT_MODE_SOFT)
-        return fail(DSALT_ERR_INVALID, "mode must be DSALT_MODE_HARD or DSALT_MODE_SOFT (got %d)", mode);
+    if (mode != DSALT_MODE_HARD && mode != DSALT_MODE_SOFT && mode != DSALT_MODE_DENSE)
+        return fail(DSALT_ERR_INVALID, "mode must be DSALT_MODE_HARD, DSALT_MODE_SOFT or DSALT_MODE_DENSE (got %d)",
+                    mode);
     if (dtype != DSALT_DTYPE_BF16 && dtype != DSALT_DTYPE_F16)
         return fail(DSALT_ERR_INVALID, "dtype must be DSALT_DTYPE_BF16 or DSALT_DTYPE_F16 (got %d)", dtype);
     if (T < 0) return fail(DSALT_ERR_INVALID, "total_len must be >= 0 (got %d)", T);
@@ -48,7 +49,13 @@ int check_common(int mode, int dtype, int T, int S, int H, int D, int k, const i
         return fail(DSALT_ERR_UNSUPPORTED, "head_dim must be 64 or 128 (got %d)", D);
     if (k < 0 || k > DSALT_MAX_K_LMK)
         return fail(DSALT_ERR_UNSUPPORTED, "k_lmk must be in [0, %d] (got %d)", DSALT_MAX_K_LMK, k);
-    if (!cu) return fail(DSALT_ERR_INVALID, "cu_seqlens is NULL");
+    if (mode == DSALT_MODE_DENSE) {
+        if (S != 1) return fail(DSALT_ERR_INVALID, "DSALT_MODE_DENSE takes one sequence (num_seqs = %d)", S);
+        if (k != 0)
+            return fail(DSALT_ERR_INVALID, "DSALT_MODE_DENSE takes its landmarks as an [H, T] bias table (k_lmk = %d)", k);
+    } else if (!cu) {
+        return fail(DSALT_ERR_INVALID, "cu_seqlens is NULL");
+    }
     if (!w) return fail(DSALT_ERR_INVALID, "w (window sizes) is NULL");
     if (k > 0 && !lmk_pos) return fail(DSALT_ERR_INVALID, "lmk_pos is NULL while k_lmk = %d", k);
     const int64_t blocks = (int64_t)dsalt::block_upper_bound(T, S, dsalt::kFwdBM) * H;
@@ -57,13 +64,29 @@ int check_common(int mode, int dtype, int T, int S, int H, int D, int k, const i
     return DSALT_OK;
 }
 
+int check_mode_scalars(int mode, float scale, float tau_win, float win_edge) {
+    if (mode != DSALT_MODE_HARD && !(tau_win > 0.f))
+        return fail(DSALT_ERR_INVALID, "tau_win must be > 0 (got %g)", (double)tau_win);
+    if (mode == DSALT_MODE_DENSE && !(fabsf(win_edge) < INFINITY))
+        return fail(DSALT_ERR_INVALID, "win_edge must be finite (got %g)", (double)win_edge);
+    if (!(scale == scale)) return fail(DSALT_ERR_INVALID, "scale is NaN");
+    if (scale == 0.f || !(fabsf(scale) < INFINITY))
+        return fail(DSALT_ERR_UNSUPPORTED, "scale must be finite and non-zero (got %g)", (double)scale);
+    if (mode == DSALT_MODE_DENSE && !(scale > 0.f))
+        return fail(DSALT_ERR_UNSUPPORTED, "DSALT_MODE_DENSE needs scale > 0 (got %g)", (double)scale);
+    return DSALT_OK;
+}
+
 // Rows of one sequence are addressed through buffer resources with 32-bit byte
 // offsets (row index x row stride): every such operand must span < 4 GiB over total_len
-// rows. `row_bytes` lists each operand's row stride in bytes.
+// rows plus kSpanMargin, so that the rows of a tile that starts up to kSpanMargin rows
+// below the buffer (their offsets wrap to above 4 GiB - kSpanMargin x stride) fall out
+// of range and read zeros. `row_bytes` lists each operand's row stride in bytes.
+constexpr int64_t kSpanMargin = 64;
 int check_span32(int total_len, std::initializer_list<int64_t> row_bytes) {
     int64_t widest = 0;
     for (int64_t b : row_bytes) widest = b > widest ? b : widest;
-    if ((int64_t)total_len * widest >= ((int64_t)1 << 32))
+    if (((int64_t)total_len + kSpanMargin) * widest >= ((int64_t)1 << 32))
         return fail(DSALT_ERR_UNSUPPORTED,
                     "a sequence's rows must span < 4 GiB (total_len %d x row stride %lld B)", total_len,
                     (long long)widest);
@@ -126,11 +149,7 @@ int dsalt_fwd_check(const dsalt_fwd_args *a) {
         if ((rc = check_tensor("out", a->out, a->out_stride_t * m, a->out_stride_h * m, (int)(4 * m)))) return rc;
     }
     if (!a->lse) return fail(DSALT_ERR_INVALID, "lse is NULL");
-    if (a->mode == DSALT_MODE_SOFT && !(a->tau_win > 0.f))
-        return fail(DSALT_ERR_INVALID, "tau_win must be > 0 (got %g)", (double)a->tau_win);
-    if (!(a->scale == a->scale)) return fail(DSALT_ERR_INVALID, "scale is NaN");
-    if (a->scale == 0.f || !(fabsf(a->scale) < INFINITY))
-        return fail(DSALT_ERR_UNSUPPORTED, "scale must be finite and non-zero (got %g)", (double)a->scale);
+    if ((rc = check_mode_scalars(a->mode, a->scale, a->tau_win, a->win_edge))) return rc;
     return check_span32(a->total_len, {2 * a->q_stride_t, 2 * a->k_stride_t, 2 * a->v_stride_t});
 }
 
@@ -291,13 +310,11 @@ int dsalt_bwd_check(const dsalt_bwd_args *a) {
     if ((rc = check_tensor("dk", a->dk, a->dk_stride_t * gm, a->dk_stride_h * gm, gv))) return rc;
     if ((rc = check_tensor("dv", a->dv, a->dv_stride_t * gm, a->dv_stride_h * gm, gv))) return rc;
     if (!a->lse) return fail(DSALT_ERR_INVALID, "lse is NULL");
-    if (a->mode == DSALT_MODE_SOFT && !(a->tau_win > 0.f))
-        return fail(DSALT_ERR_INVALID, "tau_win must be > 0 (got %g)", (double)a->tau_win);
-    if (!(a->scale == a->scale)) return fail(DSALT_ERR_INVALID, "scale is NaN");
-    if (a->scale == 0.f || !(fabsf(a->scale) < INFINITY))
-        return fail(DSALT_ERR_UNSUPPORTED, "scale must be finite and non-zero (got %g)", (double)a->scale);
-    const int64_t need = dsalt::bwd_workspace_bytes(a->total_len, a->num_seqs, a->n_heads, a->head_dim,
-                                                    a->k_lmk);
+    if ((rc = check_mode_scalars(a->mode, a->scale, a->tau_win, a->win_edge))) return rc;
+    const int64_t need = a->mode == DSALT_MODE_DENSE
+                             ? dsalt::dense_bwd_workspace_bytes(a->total_len, a->n_heads)
+                             : dsalt::bwd_workspace_bytes(a->total_len, a->num_seqs, a->n_heads, a->head_dim,
+                                                          a->k_lmk);
     if (need > 0) {
         if (!a->workspace) return fail(DSALT_ERR_INVALID, "workspace is NULL (%lld bytes needed)", (long long)need);
         if (a->workspace_bytes < need)

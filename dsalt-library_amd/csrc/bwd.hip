@@ -34,6 +34,7 @@
 #include "launch.h"
 #include "tiles.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace dsalt {
@@ -1077,10 +1078,14 @@ hipError_t launch_dt(const BwdParams &p, int head_dim, int mode, hipStream_t str
 }  // namespace
 
 int64_t bwd_workspace_bytes(int total_len, int num_seqs, int n_heads, int head_dim, int k_lmk) {
-    return (int64_t)ws_layout(total_len, num_seqs, n_heads, head_dim, k_lmk).total;
+    const int64_t sparse = (int64_t)ws_layout(total_len, num_seqs, n_heads, head_dim, k_lmk).total;
+    // one sequence without landmark slots may also be a dense-mode call
+    if (num_seqs == 1 && k_lmk == 0) return std::max(sparse, dense_bwd_workspace_bytes(total_len, n_heads));
+    return sparse;
 }
 
 hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream) {
+    if (a.mode == DSALT_MODE_DENSE) return launch_dense_bwd(a, stream);
     if (a.total_len == 0) {
         return hipSuccess;
     }

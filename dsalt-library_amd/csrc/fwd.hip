@@ -601,6 +601,7 @@ hipError_t launch_dt(const FwdParams &p, int head_dim, int mode, size_t dyn, hip
 }  // namespace
 
 hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream) {
+    if (a.mode == DSALT_MODE_DENSE) return launch_dense_fwd(a, stream);
     if (a.total_len == 0) return hipSuccess;
     FwdParams p;
     p.q = static_cast<const uint16_t *>(a.q);

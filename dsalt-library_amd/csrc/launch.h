@@ -42,4 +42,10 @@ inline int block_upper_bound(int total_len, int num_seqs, int bm) {
 
 int64_t bwd_workspace_bytes(int total_len, int num_seqs, int n_heads, int head_dim, int k_lmk);
 
+// Dense batched mode (dense.hip): one sequence, every causal key, the [H, T] landmark
+// bias table.
+hipError_t launch_dense_fwd(const dsalt_fwd_args &a, hipStream_t stream);
+hipError_t launch_dense_bwd(const dsalt_bwd_args &a, hipStream_t stream);
+int64_t dense_bwd_workspace_bytes(int total_len, int n_heads);
+
 }  // namespace dsalt

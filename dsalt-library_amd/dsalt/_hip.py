@@ -20,6 +20,7 @@ LIB_PATH = os.environ.get("DSALT_HIP_LIB") or os.path.join(os.path.dirname(os.pa
 DSALT_OK = 0
 MODE_HARD = 0
 MODE_SOFT = 1
+MODE_DENSE = 2
 DTYPE_BF16 = 0
 DTYPE_F16 = 1
 DTYPE_F32 = 2
@@ -424,6 +425,138 @@ def _bwd_args(mode, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, s
     a.scale, a.tau_win, a.win_edge = float(scale), float(tau_win), float(win_edge)
     keep = (q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu, ws)  # must outlive the args
     return a, keep, (dq, dk, dv, d_bias, d_w), dev
+
+
+def _dense_common(q, k, v, w_cont, lmk_bias):
+    """Shape and dtype checks shared by the dense-mode forward and backward."""
+    if q.dim() != 3:
+        raise DsaltError(f"q must be [T, H, D], got {tuple(q.shape)}")
+    T, H, D = q.shape
+    for name, t in (("k", k), ("v", v)):
+        if tuple(t.shape) != (T, H, D):
+            raise DsaltError(f"{name} shape {tuple(t.shape)} != q shape {(T, H, D)}")
+    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise DsaltError(f"q/k/v must share a bf16/fp16 dtype, got {q.dtype} {k.dtype} {v.dtype}")
+    w = _f32_vec(w_cont)
+    if w.dim() != 1 or w.shape[0] != T:
+        raise DsaltError(f"w_cont must be [T={T}], got {tuple(w.shape)}")
+    if lmk_bias is not None:
+        if tuple(lmk_bias.shape) != (H, T):
+            raise DsaltError(f"dense landmark bias must be [H={H}, T={T}], got {tuple(lmk_bias.shape)}")
+        lmk_bias = _f32_vec(lmk_bias)
+    return T, H, D, w, lmk_bias
+
+
+def dense_fwd(q, k, v, w_cont, lmk_bias, scale: float, tau_win: float = 1.0, win_edge: float = 4.0,
+              out_dtype: torch.dtype | None = None):
+    """Dense batched forward of one sequence (DSALT_MODE_DENSE): q/k/v [T, H, D] kernel
+    operands, w_cont [T], lmk_bias [H, T] fp32 (-inf off the landmarks) or None. Returns
+    (out [T, H, D] in ``out_dtype`` (default q.dtype), lse [T, H] fp32)."""
+    launcher = DenseFwdLauncher(q, k, v, w_cont, lmk_bias, scale, tau_win, win_edge, out_dtype)
+    launcher()
+    return launcher.out, launcher.lse
+
+
+class DenseFwdLauncher:
+    """A dense-mode forward with its argument block built once (re-launchable)."""
+
+    def __init__(self, q, k, v, w_cont, lmk_bias, scale: float, tau_win: float = 1.0, win_edge: float = 4.0,
+                 out_dtype: torch.dtype | None = None):
+        self.device = require_gpu(q, k, v, w_cont, lmk_bias)
+        T, H, D, w, lb = _dense_common(q, k, v, w_cont, lmk_bias)
+        odt = q.dtype if out_dtype is None else out_dtype
+        if odt not in (q.dtype, torch.float32):
+            raise DsaltError(f"out dtype must be {q.dtype} or torch.float32, got {odt}")
+        self.out = torch.empty((T, H, D), device=self.device, dtype=odt)
+        self.lse = torch.empty((H, T), device=self.device, dtype=torch.float32).t()
+        a = FwdArgs()
+        a.mode, a.dtype, a.total_len, a.num_seqs = MODE_DENSE, _DTYPES[q.dtype], T, 1
+        a.n_heads, a.head_dim, a.k_lmk = H, D, 0
+        a.out_dtype = DTYPE_F32 if odt == torch.float32 else _DTYPES[q.dtype]
+        a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+        a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
+        a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
+        a.out, a.out_stride_t, a.out_stride_h = self.out.data_ptr(), self.out.stride(0), self.out.stride(1)
+        a.lse, a.lse_stride_t, a.lse_stride_h = self.lse.data_ptr(), self.lse.stride(0), self.lse.stride(1)
+        a.w, a.w_stride = w.data_ptr(), w.stride(0)
+        if lb is not None:
+            a.lmk_bias = lb.data_ptr()
+            a.lmk_bias_stride_h, a.lmk_bias_stride_k = lb.stride(0), lb.stride(1)
+        a.scale, a.tau_win, a.win_edge = float(scale), float(tau_win), float(win_edge)
+        self.args = a
+        self._keep = (q, k, v, w, lb)
+        self._fn = lib().dsalt_fwd
+        self._ref = ctypes.byref(self.args)
+
+    def __call__(self) -> None:
+        _raise(self._fn(self._ref, stream_handle(self.device)), "dsalt_fwd (dense)")
+
+
+def dense_bwd(q, k, v, out, lse, dout, w_cont, lmk_bias, scale: float, tau_win: float = 1.0,
+              win_edge: float = 4.0, need_dw: bool = True, grad_dtype: torch.dtype | None = None):
+    """Dense-mode backward. Returns (dq, dk, dv in ``grad_dtype`` (default q.dtype),
+    d_lmk_bias [H, T] fp32 or None (when lmk_bias is None), d_w [T] fp32 or None)."""
+    launcher = DenseBwdLauncher(q, k, v, out, lse, dout, w_cont, lmk_bias, scale, tau_win, win_edge,
+                                need_dw, grad_dtype)
+    launcher()
+    return launcher.results
+
+
+class DenseBwdLauncher:
+    """A dense-mode backward with its argument block, outputs and workspace built once."""
+
+    def __init__(self, q, k, v, out, lse, dout, w_cont, lmk_bias, scale: float, tau_win: float = 1.0,
+                 win_edge: float = 4.0, need_dw: bool = True, grad_dtype: torch.dtype | None = None):
+        self.device = require_gpu(q, k, v, out, lse, dout, w_cont, lmk_bias)
+        T, H, D, w, lb = _dense_common(q, k, v, w_cont, lmk_bias)
+        if tuple(out.shape) != (T, H, D) or tuple(dout.shape) != (T, H, D):
+            raise DsaltError(f"out/dout must be [{T}, {H}, {D}], got {tuple(out.shape)} {tuple(dout.shape)}")
+        if out.dtype not in (q.dtype, torch.float32):
+            raise DsaltError(f"saved output must be {q.dtype} or torch.float32, got {out.dtype}")
+        if tuple(lse.shape) != (T, H) or lse.dtype != torch.float32:
+            raise DsaltError(f"lse must be float32 [T={T}, H={H}], got {lse.dtype} {tuple(lse.shape)}")
+        dout = as_kernel_operand(dout, q.dtype)
+        gdt = q.dtype if grad_dtype is None else grad_dtype
+        if gdt not in (q.dtype, torch.float32):
+            raise DsaltError(f"grad_dtype must be {q.dtype} or torch.float32, got {gdt}")
+        dev = self.device
+        dq = torch.empty(q.shape, device=dev, dtype=gdt)
+        dk = torch.empty(q.shape, device=dev, dtype=gdt)
+        dv = torch.empty(q.shape, device=dev, dtype=gdt)
+        d_lb = torch.empty((H, T), device=dev, dtype=torch.float32) if lb is not None else None
+        d_w = torch.empty((T,), device=dev, dtype=torch.float32) if need_dw else None
+        ws_bytes = bwd_workspace_size(T, 1, H, D, 0)
+        ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+        a = BwdArgs()
+        a.mode, a.dtype, a.total_len, a.num_seqs = MODE_DENSE, _DTYPES[q.dtype], T, 1
+        a.n_heads, a.head_dim, a.k_lmk = H, D, 0
+        a.grad_dtype = DTYPE_F32 if gdt == torch.float32 else _DTYPES[q.dtype]
+        a.out_dtype = DTYPE_F32 if out.dtype == torch.float32 else _DTYPES[q.dtype]
+        a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
+        a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
+        a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
+        a.out, a.out_stride_t, a.out_stride_h = out.data_ptr(), out.stride(0), out.stride(1)
+        a.lse, a.lse_stride_t, a.lse_stride_h = lse.data_ptr(), lse.stride(0), lse.stride(1)
+        a.dout, a.dout_stride_t, a.dout_stride_h = dout.data_ptr(), dout.stride(0), dout.stride(1)
+        a.w, a.w_stride = w.data_ptr(), w.stride(0)
+        if lb is not None:
+            a.lmk_bias = lb.data_ptr()
+            a.lmk_bias_stride_h, a.lmk_bias_stride_k = lb.stride(0), lb.stride(1)
+            a.d_lmk_bias = d_lb.data_ptr()
+        a.dq, a.dq_stride_t, a.dq_stride_h = dq.data_ptr(), dq.stride(0), dq.stride(1)
+        a.dk, a.dk_stride_t, a.dk_stride_h = dk.data_ptr(), dk.stride(0), dk.stride(1)
+        a.dv, a.dv_stride_t, a.dv_stride_h = dv.data_ptr(), dv.stride(0), dv.stride(1)
+        a.d_w = _ptr(d_w)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
+        a.scale, a.tau_win, a.win_edge = float(scale), float(tau_win), float(win_edge)
+        self.args = a
+        self._keep = (q, k, v, out, lse, dout, w, lb, ws)
+        self.results = (dq, dk, dv, d_lb, d_w)
+        self._fn = lib().dsalt_bwd
+        self._ref = ctypes.byref(self.args)
+
+    def __call__(self) -> None:
+        _raise(self._fn(self._ref, stream_handle(self.device)), "dsalt_bwd (dense)")
 
 
 def select_landmarks(scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Tensor,

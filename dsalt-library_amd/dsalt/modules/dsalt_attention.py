@@ -16,9 +16,16 @@ Packed input (``cu_seqlens`` given) runs the sparse path:
 The attention output stays in the compute dtype on the module path (the reference
 round-trips it through fp32, which only the ``dsalt.kernels`` entry points keep).
 
-There is no non-GPU fallback: CPU tensors raise. The reference's batched ``[B, T, d]``
-path (a dense O(T^2) soft-tail variant) is not provided; pass packed tokens with
-``cu_seqlens``.
+Unpacked input ``[1, T, d]`` (no ``cu_seqlens``) runs the dense batched variant of
+dsalt_attention.py:371-438 on the DSALT_MODE_DENSE HIP kernels: every causal key with
+the soft window tail, landmark weights log sigmoid(s/tau_lmk) at the top-k keys of each
+head (selected by the HIP top-k over the whole sequence) left of floor(w~), union by
+maximum; differentiable in w~ and the landmark weights in training and eval alike. In
+eval ``_last_P`` holds the dense [H, T, T] probabilities unless ``_collect_last_P`` is
+False. B > 1 raises (the reference's view of the [1, T, d] result fails there too), and
+so does attention dropout in training.
+
+There is no non-GPU fallback: CPU tensors raise.
 """
 from __future__ import annotations
 
@@ -28,6 +35,7 @@ import torch
 import torch.nn as nn
 
 from .. import _hip
+from ..kernels._dense import dense_attention, dense_probabilities
 from ..kernels._sparse import sparse_attention
 from ..kernels.landmark_tokens_ker import hybrid_scores_from_v, hybrid_scores_per_head
 from ..kernels.selectors import _compute_landmark_indices
@@ -160,9 +168,61 @@ class DSALTAttention(nn.Module):
                 cu_list: list | None = None) -> tuple[torch.Tensor, torch.Tensor]:
         if cu_seqlens is not None:
             return self._packed(x, cu_seqlens, x.shape[0], x.device, rope_cs, cu_list)
-        raise NotImplementedError(
-            "the dense batched [B, T, d] DSALT variant is not provided by the HIP path; pack "
-            "the tokens to [T, d] and pass cu_seqlens (int32 [S + 1]) for sparse attention")
+        B, T, _ = x.shape
+        return self._batched(x, B, T, x.device)
+
+    def _batched(self, x: torch.Tensor, B: int, T: int, device: torch.device):
+        """Dense batched forward of ``x [1, T, d]`` (dsalt_attention.py:371-438)."""
+        _hip.require_gpu(x)
+        if B != 1:
+            raise ValueError(f"the dense batched path takes one sequence [1, T, d] (got B = {B}); pack "
+                             "several sequences to [T, d] and pass cu_seqlens")
+        if self.training and self.dropout > 0:
+            raise NotImplementedError("attention dropout is not supported by the dense HIP path")
+        xs = x[0]
+        q = self.q_proj(xs).view(T, self.n_heads, self.head_dim)
+        k = self.k_proj(xs).view(T, self.n_kv_heads, self.head_dim)
+        v = self.v_proj(xs).view(T, self.n_kv_heads, self.head_dim)
+        v_sel = v if (self.v_proj.bias is None and self._fused_selector) else None
+        cu = torch.tensor([0, T], dtype=torch.int32, device=device)
+        q, k = apply_rotary_emb_packed(q, k, self.rope_cos, self.rope_sin, cu)
+        k = self._repeat_kv(k)
+        v = self._repeat_kv(v)
+
+        w_cont, lmk_bias, lmk_pos = self._dense_selectors(xs, T, device, v_sel)
+        out = dense_attention(q, k, v, w_cont, lmk_bias, self.tau_win, float(self.win_edge))
+        if not self.training and getattr(self, "_collect_last_P", True):
+            self._last_P = dense_probabilities(q, k, w_cont, lmk_bias, self.tau_win, float(self.win_edge))
+        else:
+            self._last_P = None
+        self._last_selection = (w_cont.detach(), lmk_pos)
+        aux = x.new_zeros(())
+        return self._apply_out_proj(out.reshape(1, T, self.d_model)), aux
+
+    @_dynamo_opaque
+    def _dense_selectors(self, x, T, device, v=None):
+        """``(w_cont [T], lmk_bias [H, T], lmk_pos [H, 1, k])`` of the dense variant
+        (dsalt_attention.py:403-438): the top-min(k, T) keys of each head over the whole
+        sequence by the detached fp32 hybrid score (nothing excluded: the window exclusion
+        is per query, in the kernel), weight log(max(sigmoid(s / tau_lmk), 1e-20)) there
+        and -inf elsewhere. ``w_cont`` and the weights carry the gradients."""
+        w_cont = self._window_continuous(x)
+        alpha = self._alpha()
+        if v is not None:
+            scores, _, _ = hybrid_scores_from_v(x, v, alpha, self.n_heads)
+        else:
+            scores, _, _ = hybrid_scores_per_head(x, self.v_proj.weight, alpha, self.n_heads, self.head_dim)
+        k_act = min(self.k_lmk, T)
+        with torch.no_grad():
+            cu = torch.tensor([0, T], dtype=torch.int32, device=device)
+            lmk_pos = _hip.select_landmarks(scores.detach().float().contiguous(),
+                                            torch.zeros(T, device=device), cu, k_act)
+            sel = torch.zeros(self.n_heads, T + 1, dtype=torch.bool, device=device)
+            sel.scatter_(1, torch.where(lmk_pos[:, 0] >= 0, lmk_pos[:, 0], T), True)
+            sel = sel[:, :T]
+        w_lmk = torch.log(torch.sigmoid(scores.float() / self.tau_lmk).clamp(min=1e-20)).t()   # [H, T]
+        lmk_bias = torch.where(sel, w_lmk, torch.full_like(w_lmk, float("-inf")))
+        return w_cont, lmk_bias, lmk_pos
 
     @_dynamo_opaque
     def _train_selectors(self, x, cu_seqlens, total_len, device, cu_list=None, v=None):

@@ -11,6 +11,12 @@
  *                      core d <= w~ - win_edge, log sigmoid((w~ - d) / tau_win) on the edge;
  *                      landmark p admitted iff p <= i and (float)p < (float)i - w~(i);
  *                      logit bias lmk_logw[slot]
+ *   DENSE (batched):   one unpacked sequence [1, T, d]; every causal key j <= i of query i:
+ *                      window bias 0 in the core d = i - j <= w~(i) - win_edge (fp32
+ *                      compare), else log(max(sigmoid((w~(i) - d) / tau_win), 1e-20));
+ *                      landmark bias lmk_bias[h, j] (an [H, T] table, -inf off the head's
+ *                      landmarks) where d >= max(1, floor(w~(i))); the logit bias is the
+ *                      larger of the two (equal biases share the gradient in halves)
  *
  * Logits are q.k * scale (+ bias); softmax is computed online in fp32; O is stored in
  * the input dtype and LSE = max + log(sum) in fp32 (natural log; -inf for empty rows,
@@ -50,7 +56,7 @@ enum {
 };
 
 enum { DSALT_DTYPE_BF16 = 0, DSALT_DTYPE_F16 = 1, DSALT_DTYPE_F32 = 2 /* outputs and gradients only */ };
-enum { DSALT_MODE_HARD = 0, DSALT_MODE_SOFT = 1 };
+enum { DSALT_MODE_HARD = 0, DSALT_MODE_SOFT = 1, DSALT_MODE_DENSE = 2 };
 
 /* Largest k_lmk the kernels accept (landmark slots per head and sequence). */
 #define DSALT_MAX_K_LMK 1024
@@ -65,11 +71,17 @@ enum { DSALT_MODE_HARD = 0, DSALT_MODE_SOFT = 1 };
  * kernel; `out` is written (no prior memset) in the input dtype, or in fp32 when
  * out_dtype = DSALT_DTYPE_F32 (the reference's entry points return O as fp32).
  * Limits: `scale` finite and non-zero (a negative scale is applied by negating Q);
- * total_len x max(k, v row stride) x 2 bytes < 4 GiB (K/V rows of a sequence are
+ * (total_len + 64) x max(k, v row stride) x 2 bytes < 4 GiB (K/V rows of a sequence are
  * addressed with 32-bit offsets). Both are checked and return DSALT_ERR_UNSUPPORTED.
+ *
+ * DSALT_MODE_DENSE replaces the dense softmax of DSALTAttention._batched
+ * (dsalt/modules/dsalt_attention.py:371-401, biases :286-329): num_seqs = 1, k_lmk = 0,
+ * lmk_pos NULL, cu_seqlens may be NULL; lmk_bias is the [H, T] table lmk_bias[h, j] at
+ * lmk_bias + h * lmk_bias_stride_h + j * lmk_bias_stride_k (NULL: no landmarks;
+ * lmk_bias_stride_s is ignored); w holds w~; scale must be > 0.
  */
 typedef struct dsalt_fwd_args {
-    int32_t mode;      /* DSALT_MODE_HARD or DSALT_MODE_SOFT */
+    int32_t mode;      /* DSALT_MODE_HARD, DSALT_MODE_SOFT or DSALT_MODE_DENSE */
     int32_t dtype;     /* DSALT_DTYPE_* of q, k, v and out */
     int32_t total_len; /* T */
     int32_t num_seqs;  /* S >= 1 */
@@ -114,6 +126,10 @@ int dsalt_fwd_check(const dsalt_fwd_args *args);
  *   dsalt_triton_backward (dsalt/kernels/dsalt_triton_bwd.py:219-324) with its kernels
  *       _dsalt_bwd_preprocess / _dsalt_bwd_kernel (:17-216).
  * Deterministic: no atomics; every output element is written by exactly one thread.
+ * DSALT_MODE_DENSE (the autograd backward of the dense softmax of DSALTAttention._batched,
+ * dsalt/modules/dsalt_attention.py:371-401): the forward's conventions; d_lmk_bias is
+ * [H, T] contiguous (the gradient of every lmk_bias[h, j], 0 where it is -inf) and d_w is
+ * [T]. dsalt_bwd_workspace_size(T, 1, H, D, 0) covers its workspace.
  */
 typedef struct dsalt_bwd_args {
     int32_t mode, dtype, total_len, num_seqs, n_heads, head_dim, k_lmk;

@@ -17,7 +17,7 @@ from oracle import dsalt_oracle as orc
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
-GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "module_*.npz")))
+GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "module_train_*.npz")))
 
 
 def check(got, ref, what):
@@ -101,13 +101,19 @@ def mod_lmk0(mod, x, cfg, L0):
     return lmk[:, 0].cpu().numpy()
 
 
-def test_module_rejects_cpu_and_batched_input():
+def test_module_rejects_cpu_and_unsupported_batched_input():
     mod = DSALTAttention(128, 2, 4, 40, 8, 256)
     x = torch.randn(64, 128)
     with pytest.raises(Exception, match="ROCm GPU"):
         mod(x, cu_seqlens=torch.tensor([0, 64], dtype=torch.int32))
-    with pytest.raises(NotImplementedError):
-        mod.to(DEV)(torch.randn(1, 64, 128, device=DEV))
+    with pytest.raises(Exception, match="ROCm GPU"):
+        mod(torch.randn(1, 64, 128))
+    mod = mod.to(DEV)
+    with pytest.raises(ValueError, match="one sequence"):
+        mod(torch.randn(2, 64, 128, device=DEV))
+    drop = DSALTAttention(128, 2, 4, 40, 8, 256, dropout=0.1).to(DEV).train()
+    with pytest.raises(NotImplementedError, match="dropout"):
+        drop(torch.randn(1, 64, 128, device=DEV))
 
 
 def test_module_bf16_autocast_train_step():
