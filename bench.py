@@ -191,6 +191,113 @@ def measure_backward(device: torch.device, steps: int = 50, warmup: int = 20) ->
     }
 
 
+def measure_dense(device: torch.device, steps: int = 50, warmup: int = 20) -> dict:
+    """The dense batched variant (DSALT_MODE_DENSE) at config 1's shape on the GPU: module
+    seed 0, x ~ N(0, 1) [1, 1024, 512], 8 heads x 64, bf16; q/k/v, w~ and the landmark
+    table from the module's own projections and selector. Forward and backward launch
+    times; FLOPs are the causal pairs' 4 D (forward) and 10 D (backward: S, dP, dV, dK,
+    dQ) per pair."""
+    from dsalt import _hip
+    from dsalt.modules import DSALTAttention
+    from dsalt.kernels.window_utils import apply_rotary_emb_packed
+
+    B, L, d_model, H, n_min, n_max, k_lmk, seed = CONFIGS["c1"]
+    torch.manual_seed(seed)
+    mod = DSALTAttention(d_model, H, n_min, n_max, k_lmk, max_seq_len=L)
+    x = torch.randn(B, L, d_model)
+    mod = mod.to(device).to(torch.bfloat16)
+    xs = x[0].to(device, torch.bfloat16)
+    D = d_model // H
+    with torch.no_grad():
+        q = mod.q_proj(xs).view(L, H, D)
+        k = mod.k_proj(xs).view(L, H, D)
+        v = mod.v_proj(xs).view(L, H, D).contiguous()
+        cu = torch.tensor([0, L], dtype=torch.int32, device=device)
+        q, k = apply_rotary_emb_packed(q, k, mod.rope_cos, mod.rope_sin, cu)
+        w_cont, lb, _ = mod._dense_selectors(xs, L, device, mod.v_proj(xs).view(L, H, D))
+        w_cont, lb = w_cont.float(), lb.float().contiguous()
+    scale = 1.0 / math.sqrt(D)
+    fwd = _hip.DenseFwdLauncher(q.contiguous(), k.contiguous(), v, w_cont, lb, scale)
+    fwd_ms = time_launches(fwd, steps, warmup)
+    dout = torch.randn_like(q)
+    bwd = _hip.DenseBwdLauncher(q.contiguous(), k.contiguous(), v, fwd.out, fwd.lse, dout, w_cont, lb, scale)
+    bwd_ms = time_launches(bwd, steps, warmup)
+    pairs = H * L * (L + 1) // 2
+    bytes_fwd = 2 * L * H * D * 4 + 4 * L * H + 4 * L + 4 * H * L
+    return {
+        "workload": f"dense batched [1, {L}, {d_model}], {H} heads x {D}, module seed {seed}, bf16",
+        "pairs": pairs,
+        "fwd_us": fwd_ms * 1e3,
+        "bwd_us": bwd_ms * 1e3,
+        "fwd_mfma_frac": 4.0 * D * pairs / (fwd_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "bwd_mfma_frac": 10.0 * D * pairs / (bwd_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "fwd_hbm_frac": bytes_fwd / (fwd_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "tokens_per_s_fwd": L / (fwd_ms * 1e-3),
+    }
+
+
+def measure_lm(device: torch.device, steps: int = 5, warmup: int = 2) -> dict:
+    """Config 5: DSALTLMHeadModel(32000, 1024, 24, 16, 32, 512, 64, 2048) inference forward
+    in bf16 at random init (seed 4) on input_ids [8, 2048] packed to [16384] with
+    cu_seqlens, _last_P off. End-to-end time per forward (logits included) and the share
+    spent inside the attention modules (q/k/v projections, RoPE, selection, the HIP
+    attention kernel, out_proj), from CUDA events around each attention call."""
+    from dsalt.model import DSALTLMHeadModel
+
+    torch.manual_seed(4)
+    with torch.device(device):  # parameters initialised on the GPU (the RoPE tables are built on the CPU)
+        model = DSALTLMHeadModel(32000, 1024, 24, 16, 32, 512, 64, 2048)
+    model = model.to(device, torch.bfloat16).eval()
+    model.set_collect_last_P(False)
+    ids = torch.randint(0, 32000, (8 * 2048,), device=device)
+    cu = torch.arange(0, 8 * 2048 + 1, 2048, dtype=torch.int32, device=device)
+    marks = []
+    on = [False]
+
+    def pre(_m, _a):
+        if on[0]:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            marks.append([e, None])
+
+    def post(_m, _a, _o):
+        if on[0]:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            marks[-1][1] = e
+
+    hooks = []
+    for layer in model.layers:
+        hooks.append(layer.attn.register_forward_pre_hook(pre))
+        hooks.append(layer.attn.register_forward_hook(post))
+    with torch.no_grad():
+        for _ in range(warmup):
+            model(ids, cu_seqlens=cu)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        on[0] = True
+        start.record()
+        for _ in range(steps):
+            model(ids, cu_seqlens=cu)
+        end.record()
+        torch.cuda.synchronize()
+        on[0] = False
+    for h in hooks:
+        h.remove()
+    ms = start.elapsed_time(end) / steps
+    attn_ms = sum(a.elapsed_time(b) for a, b in marks) / steps
+    T = ids.numel()
+    return {
+        "workload": "c5: DSALTLMHeadModel(32000, 1024, 24 layers, 16 heads, n_min 32, n_max 512, k_lmk 64) "
+                    "inference forward, bf16, 8 x 2048 packed tokens, random init seed 4",
+        "ms_per_forward": ms,
+        "tokens_per_s": T / (ms * 1e-3),
+        "attn_module_ms": attn_ms,
+        "attn_share": attn_ms / ms,
+        "steps": steps,
+    }
+
+
 def time_graph(fn, per_graph: int = 50, replays: int = 10) -> float:
     """Per-launch time of `fn` from a HIP graph of `per_graph` captured launches, replayed
     `replays` times: kernels shorter than the host's launch cost are timed on the GPU
@@ -212,10 +319,20 @@ def time_graph(fn, per_graph: int = 50, replays: int = 10) -> float:
     return start.elapsed_time(end) / (replays * per_graph)
 
 
+WARMUP_MIN_S = 0.25  # the GPU clock ramps over ~10 ms of back-to-back launches
+
+
 def time_launches(fn, steps: int, warmup: int) -> float:
+    """Mean time per launch of `steps` launches, after `warmup` launches and then at least
+    WARMUP_MIN_S seconds more of them (so the clock state does not depend on the flag)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < WARMUP_MIN_S:
+        for _ in range(50):  # back to back: the clock ramps under sustained load
+            fn()
+        torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
@@ -312,25 +429,57 @@ def cpu_baseline(wl, budget_s: float = 12.0):
     pos = wl["lmk"][:, :1].cpu().numpy()
     cu = [0, L]
     orc.cpu_baseline_hard(q32, k32, v32, w, pos, cu)  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while True:
+    times = []
+    t_all = time.perf_counter()
+    while len(times) < 5:
+        t0 = time.perf_counter()
         orc.cpu_baseline_hard(q32, k32, v32, w, pos, cu)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 20:
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all >= budget_s and len(times) >= 3:
             break
-    return {"value": reps * L / el, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} x 1 sequence of {L} tokens, {wl['H']} heads (dense mask + fp32 SDPA)"}
+    med = float(np.median(times))
+    return {"value": L / med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu": cpu_model(), "torch": torch.__version__,
+            "sample": f"median of {len(times)} runs of 1 sequence of {L} tokens, {wl['H']} heads "
+                      f"(dense mask + fp32 SDPA)",
+            "runs_s": times}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+FWD_SOURCES = ("dsalt-library_amd/csrc/fwd.hip", "dsalt-library_amd/csrc/common.h",
+               "dsalt-library_amd/csrc/tiles.h")
+
+
+def source_hash(paths=FWD_SOURCES) -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for p in paths:
+        with open(os.path.join(ROOT, p), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
 
 
 def load_traffic(cfg: str):
-    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE, if recorded."""
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE, if recorded for
+    the forward sources as they are now (None when the record is missing or stale)."""
     path = os.path.join(ROOT, "profiles", f"fwd_{cfg}_traffic.json")
     if not os.path.exists(path):
-        return None
+        return None, None
     with open(path) as f:
         rec = json.load(f)
-    return rec.get("hbm_bytes_per_launch")
+    if rec.get("source_sha16") != source_hash():
+        return None, rec.get("source_sha16")
+    return rec.get("hbm_bytes_per_launch"), rec.get("source_sha16")
 
 
 def main():
@@ -343,6 +492,8 @@ def main():
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-backward", action="store_true", help="skip the config-3 backward measurement")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the dense-variant and config-5 LM measurements")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -407,7 +558,7 @@ def main():
     bytes_alg = 2 * T * H * D * 4 + 4 * T * H + 4 * T + 8 * H * wl["B"] * wl["k_lmk"]
     t_s = ms * 1e-3
     tflops = flops / t_s / 1e12
-    traffic = load_traffic(args.config)
+    traffic, traffic_sha = load_traffic(args.config)
 
     res = {
         "metric": "DSALT attn fwd tokens/s & % bf16 MFMA peak (16h×64d, seq 2048)",
@@ -438,6 +589,8 @@ def main():
             "unit": "GB/s",
             "frac": bytes_alg / t_s / 1e9 / HBM_PEAK_GBS,
             "traffic": traffic,
+            "traffic_source_sha16": traffic_sha,
+            "source_sha16": source_hash(),
         },
         "mfma": {
             "achieved": tflops,
@@ -464,6 +617,9 @@ def main():
     }
     if not args.no_backward:
         res["backward"] = measure_backward(dev)
+    if not args.no_extras:
+        res["dense"] = measure_dense(dev)
+        res["lm_c5"] = measure_lm(dev)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(wl)
     print(json.dumps(res))

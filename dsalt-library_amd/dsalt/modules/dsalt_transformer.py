@@ -1,0 +1,69 @@
+"""Pre-norm transformer block around DSALTAttention (dsalt/modules/dsalt_transformer.py).
+
+The LM consumer of the attention path: x + attn(norm(x)), then x + ffn(norm(x)), with a
+SwiGLU feed-forward. Parameter names and creation order follow the reference
+(attn_norm, ffn_norm, attn, ffn; gate_proj, up_proj, down_proj) so state dicts load and
+seeded initialisations agree. Only the attention runs on the HIP kernels; the norms,
+projections and FFN are torch (hipBLASLt GEMMs).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+import torch.utils.checkpoint
+
+from ..kernels.RMSENorm import RMSENorm
+from .dsalt_attention import DSALTAttention
+
+
+class SwiGLUFFN(nn.Module):
+    """``down_proj(silu(gate_proj(x)) * up_proj(x))`` (dsalt_transformer.py:10-21)."""
+
+    def __init__(self, d_model: int, d_ff: int, dropout: float = 0.0):
+        super().__init__()
+        self.gate_proj = nn.Linear(d_model, d_ff, bias=False)
+        self.up_proj = nn.Linear(d_model, d_ff, bias=False)
+        self.down_proj = nn.Linear(d_ff, d_model, bias=False)
+        self.drop = nn.Dropout(dropout)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        h = F.silu(self.gate_proj(x))
+        h = h * self.up_proj(x)
+        return self.drop(self.down_proj(h))
+
+
+class DSALTTransformerBlock(nn.Module):
+    """RMSNorm -> DSALTAttention -> residual, RMSNorm -> SwiGLU -> residual
+    (dsalt_transformer.py:24-88); ``gradient_checkpointing`` recomputes the attention and
+    the FFN in the backward when training."""
+
+    def __init__(self, d_model: int, n_heads: int, n_min: int, n_max: int, k_lmk: int, max_seq_len: int,
+                 d_ff: int, dropout: float = 0.0, yarn_scale: float = 1.0, layer_idx: int = 0,
+                 n_kv_heads: int | None = None, qkv_bias: bool = False, rope_base: float = 10000.0):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.attn_norm = RMSENorm(d_model)
+        self.ffn_norm = RMSENorm(d_model)
+        self.attn = DSALTAttention(d_model=d_model, n_heads=n_heads, n_min=n_min, n_max=n_max, k_lmk=k_lmk,
+                                   max_seq_len=max_seq_len, dropout=dropout, yarn_scale=yarn_scale,
+                                   layer_idx=layer_idx, n_kv_heads=n_kv_heads, qkv_bias=qkv_bias,
+                                   rope_base=rope_base)
+        self.ffn = SwiGLUFFN(d_model=d_model, d_ff=d_ff, dropout=dropout)
+
+    def forward(self, x: torch.Tensor, cu_seqlens: torch.Tensor | None = None, max_seqlen: int | None = None,
+                gradient_checkpointing: bool = False, rope_cs: tuple | None = None,
+                cu_list: list | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        aux_box = []
+
+        def attend(h):
+            o, a = self.attn(h, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen, rope_cs=rope_cs, cu_list=cu_list)
+            aux_box.append(a)
+            return o
+
+        recompute = gradient_checkpointing and self.training
+        h = self.attn_norm(x)
+        x = x + (torch.utils.checkpoint.checkpoint(attend, h, use_reentrant=False) if recompute else attend(h))
+        h = self.ffn_norm(x)
+        x = x + (torch.utils.checkpoint.checkpoint(self.ffn, h, use_reentrant=False) if recompute else self.ffn(h))
+        return x, aux_box[0]

@@ -20,6 +20,9 @@ path. It restates, on the CPU, the reference algorithm of LeonardoCofone/dsalt-l
                          tail on every causal key, landmarks admitted at d >= max(1, floor(w~)),
                          union = elementwise max of the two log-biases
   module_batched_forward dsalt_attention.py:371-401 (B = 1) from the module parameters
+  lm_forward             DSALTLMHeadModel eval logits (dsalt/model/dsalt_lm.py:237-280):
+                         embedding, pre-norm blocks (RMSNorm, attention, SwiGLU), final
+                         RMSNorm, tied head; lm_train_loss the packed training loss
   cpu_baseline_hard      the reference's CPU fallback cost model: dense per-sequence mask +
                          F.scaled_dot_product_attention in fp32 (dsalt_attention.py:95-144,
                          dsalt/kernels/sparse_attn.py:29-57), with the HARD kernel's mask
@@ -616,3 +619,49 @@ def module_batched_forward(params: dict, cfg: dict, x: torch.Tensor, tau_win=1.0
     o, _ = attention_dense(q, k, v, w_cont, lb, tau_win, win_edge)
     out = o.reshape(T, d_model) @ params["out_proj.weight"].T
     return out.unsqueeze(0), (w_cont, lb)
+
+
+# ---------------------------------------------------------------------------------------
+# the LM consumer: dsalt/model/dsalt_lm.py:237-280, dsalt/modules/dsalt_transformer.py:
+# 76-86, dsalt/kernels/RMSENorm.py:20-22
+# ---------------------------------------------------------------------------------------
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """x / sqrt(mean(x^2) + eps) * weight over the last dimension (F.rms_norm)."""
+    return x * torch.rsqrt(x.square().mean(-1, keepdim=True) + eps) * weight
+
+
+def _lm_trunk(params: dict, cfg: dict, input_ids: torch.Tensor, attend) -> torch.Tensor:
+    """Embedding, the pre-norm blocks (attend(sub_params, h) is the attention module's
+    output) and the final RMSNorm (dsalt_lm.py:254-272, dsalt_transformer.py:80-85)."""
+    x = params["embed_tokens.weight"][input_ids]
+    for li in range(cfg["n_layers"]):
+        pre = f"layers.{li}."
+        sub = {k[len(pre) + 5:]: v for k, v in params.items() if k.startswith(pre + "attn.")}
+        x = x + attend(sub, rms_norm(x, params[pre + "attn_norm.weight"]))
+        h = rms_norm(x, params[pre + "ffn_norm.weight"])
+        g = h @ params[pre + "ffn.gate_proj.weight"].T
+        u = h @ params[pre + "ffn.up_proj.weight"].T
+        x = x + (F.silu(g) * u) @ params[pre + "ffn.down_proj.weight"].T
+    return rms_norm(x, params["final_norm.weight"])
+
+
+def lm_forward(params: dict, cfg: dict, input_ids: torch.Tensor, cu=None) -> torch.Tensor:
+    """Logits of DSALTLMHeadModel in eval mode (tied head): packed ``input_ids [T]`` with
+    ``cu`` (each attention is module_eval_forward: HARD set, zero landmark bias), or
+    ``[1, T]`` without (each attention is module_batched_forward: the dense variant).
+    ``params`` holds the model's state dict in the working dtype."""
+    if cu is not None:
+        x = _lm_trunk(params, cfg, input_ids, lambda sub, h: module_eval_forward(sub, cfg, h, cu)[0])
+    else:
+        x = _lm_trunk(params, cfg, input_ids, lambda sub, h: module_batched_forward(sub, cfg, h)[0])
+    return x @ params["embed_tokens.weight"].T
+
+
+def lm_train_loss(params: dict, cfg: dict, input_ids: torch.Tensor, cu, labels: torch.Tensor) -> torch.Tensor:
+    """Training loss of DSALTLMHeadModel on packed input (tied head): each attention is
+    module_train_forward (SOFT), then the mean token cross-entropy over labels other
+    than -100 (dsalt_lm.py:19-39, :187-197). Differentiable in the parameters."""
+    x = _lm_trunk(params, cfg, input_ids, lambda sub, h: module_train_forward(sub, cfg, h, cu)[0])
+    logits = x @ params["embed_tokens.weight"].T
+    return F.cross_entropy(logits, labels.long(), ignore_index=-100, reduction="sum") / (labels != -100).sum()

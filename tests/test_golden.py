@@ -3,7 +3,9 @@ reference's own DSALTAttention (tests/golden/make_golden.py): the packed trainin
 forward (oracle.module_train_forward: output, selectors, gradients with respect to x
 and every parameter) and the dense batched variant for x [1, T, d_model]
 (oracle.module_batched_forward: training output and every gradient, the selected
-landmark keys, the eval output and the dense _last_P probabilities). CPU only."""
+landmark keys, the eval output and the dense _last_P probabilities); and the LM
+consumer (oracle.lm_forward on [1, T] input, oracle.lm_train_loss on packed input with
+its gradients) against the reference's DSALTLMHeadModel. CPU only."""
 import glob
 import json
 import math
@@ -17,6 +19,7 @@ from oracle import dsalt_oracle as orc
 
 GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "module_train_*.npz")))
 BATCHED = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "module_batched_*.npz")))
+LM = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "lm_*.npz")))
 
 
 def load(path):
@@ -115,3 +118,24 @@ def test_dense_bias_special_cases():
     assert b[8, 3] == 0.0
     assert abs(b[12, 3].item() - torch.nn.functional.logsigmoid(torch.tensor(1.5, dtype=torch.float64)).item()) < 1e-12
     assert b[13, 3] == -0.25
+
+
+@pytest.mark.parametrize("path", LM, ids=[os.path.basename(p) for p in LM])
+def test_oracle_lm_matches_reference_golden(path):
+    d, cfg, params = load(path)
+    p64 = {k: v.double() for k, v in params.items()}
+    ids_b = torch.from_numpy(d["ids_batched"]).long()
+    with torch.no_grad():
+        logits_b = orc.lm_forward(p64, cfg, ids_b)
+    assert rel_l2(logits_b, d["logits_batched"]) < 1e-5
+    # the training loss on packed input and its gradients (tied head: one leaf)
+    leaves = {k: v.clone().requires_grad_() for k, v in p64.items() if k != "lm_head.weight"}
+    loss = orc.lm_train_loss(leaves, cfg, torch.from_numpy(d["ids"]).long(), d["cu"],
+                             torch.from_numpy(d["labels"]))
+    assert abs(loss.item() - float(d["loss"])) < 1e-5
+    loss.backward()
+    # the reference ran in fp32 through two blocks: its gradients carry ~3e-4 relative
+    # rounding on the smallest ones (alpha_w ~ 4e-5)
+    for k in d.files:
+        if k.startswith("grad."):
+            assert rel_l2(leaves[k[5:]].grad, d[k]) < 1e-3, k
