@@ -494,6 +494,8 @@ def main():
     ap.add_argument("--no-backward", action="store_true", help="skip the config-3 backward measurement")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the dense-variant and config-5 LM measurements")
+    ap.add_argument("--only", choices=("lm", "dense", "backward"), default=None,
+                    help="run only that measurement and print its JSON (for profiling)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -505,6 +507,10 @@ def main():
     from dsalt import _hip
 
     dev = torch.device("cuda", 0)
+    if args.only is not None:
+        fn = {"lm": measure_lm, "dense": measure_dense, "backward": measure_backward}[args.only]
+        print(json.dumps(fn(dev)))
+        return
     if args.copy_calib_mib > 0:
         n = args.copy_calib_mib * (1 << 20) // 4
         src = torch.randn(n, device=dev)
