@@ -106,3 +106,30 @@ def test_headline_forward_on_module_selectors(cfg, rows, mode):
     print(f"  out max-abs {ma:.2e} rel-L2 {rl:.2e}; lse max-abs {lerr:.2e}", flush=True)
     assert ma <= MAX_ABS and rl <= REL_L2, f"{cfg} {mode}: max-abs {ma:.3e}, rel-L2 {rl:.3e}"
     assert lerr <= 2e-2
+
+
+def test_c3_backward_on_module_selectors():
+    """Config 3 backward (SOFT) on the windows, landmarks and landmark weights the module
+    produces (bench.make_train_workload: seed 2, the c3 packing), every gradient against
+    fp64 autograd through the oracle. dQ/dK/dV and the window and landmark-weight
+    gradients (d_w~ [T], d_logw [H, S, k]) are held to the north-star bar itself:
+    max-abs 2e-2 (absolute) and relative L2 1e-2."""
+    print("c3 backward on module selectors", flush=True)
+    wl = bench.make_train_workload(DEV)
+    q, k, v, w, lmk, logw, cu = wl["q"], wl["k"], wl["v"], wl["w"], wl["lmk"], wl["logw"], wl["cu"]
+    scale = 1.0 / math.sqrt(wl["D"])
+    out, lse = hip.fwd(hip.MODE_SOFT, q, k, v, w, lmk, logw, cu, scale, 1.0, 4.0, out_dtype=torch.float32)
+    dq, dk, dv, dlw, dw = hip.bwd(hip.MODE_SOFT, q, k, v, out, lse, wl["dout"], w, lmk, logw, cu, scale, 1.0, 4.0,
+                                  need_dw=True, grad_dtype=torch.float32)
+    torch.cuda.synchronize()
+    q64, k64, v64 = (t.cpu().double().requires_grad_() for t in (q, k, v))
+    w64 = w.cpu().double().requires_grad_()
+    lw64 = logw.cpu().double().requires_grad_()
+    o, _ = orc.attention_soft(q64, k64, v64, w64, lmk.cpu(), lw64, wl["cu_list"], tau_win=1.0, win_edge=4.0)
+    (o * wl["dout"].cpu().double()).sum().backward()
+    ref_lw = torch.where(torch.isfinite(logw.cpu().double()), lw64.grad, torch.zeros_like(lw64.grad))
+    for name, got, ref in (("dq", dq, q64.grad), ("dk", dk, k64.grad), ("dv", dv, v64.grad),
+                           ("d_w", dw, w64.grad), ("d_logw", dlw, ref_lw)):
+        ma, rl = _errs(got, ref)
+        print(f"  {name}: max-abs {ma:.3e} rel-L2 {rl:.3e} (max |ref| {ref.abs().max().item():.3e})", flush=True)
+        assert ma <= MAX_ABS and rl <= REL_L2, f"c3 {name}: max-abs {ma:.3e}, rel-L2 {rl:.3e}"
