@@ -64,6 +64,12 @@ int check_common(int mode, int dtype, int T, int S, int H, int D, int k, const i
     return DSALT_OK;
 }
 
+int check_kv_heads(int n_heads, int n_kv) {
+    if (n_kv < 0 || (n_kv > 0 && n_heads % n_kv != 0))
+        return fail(DSALT_ERR_INVALID, "n_kv_heads must be 0 or divide n_heads = %d (got %d)", n_heads, n_kv);
+    return DSALT_OK;
+}
+
 int check_mode_scalars(int mode, float scale, float tau_win, float win_edge) {
     if (mode != DSALT_MODE_HARD && !(tau_win > 0.f))
         return fail(DSALT_ERR_INVALID, "tau_win must be > 0 (got %g)", (double)tau_win);
@@ -150,6 +156,7 @@ int dsalt_fwd_check(const dsalt_fwd_args *a) {
     }
     if (!a->lse) return fail(DSALT_ERR_INVALID, "lse is NULL");
     if ((rc = check_mode_scalars(a->mode, a->scale, a->tau_win, a->win_edge))) return rc;
+    if ((rc = check_kv_heads(a->n_heads, a->n_kv_heads))) return rc;
     return check_span32(a->total_len, {2 * a->q_stride_t, 2 * a->k_stride_t, 2 * a->v_stride_t});
 }
 
@@ -311,6 +318,7 @@ int dsalt_bwd_check(const dsalt_bwd_args *a) {
     if ((rc = check_tensor("dv", a->dv, a->dv_stride_t * gm, a->dv_stride_h * gm, gv))) return rc;
     if (!a->lse) return fail(DSALT_ERR_INVALID, "lse is NULL");
     if ((rc = check_mode_scalars(a->mode, a->scale, a->tau_win, a->win_edge))) return rc;
+    if ((rc = check_kv_heads(a->n_heads, a->n_kv_heads))) return rc;
     const int64_t need = a->mode == DSALT_MODE_DENSE
                              ? dsalt::dense_bwd_workspace_bytes(a->total_len, a->n_heads)
                              : dsalt::bwd_workspace_bytes(a->total_len, a->num_seqs, a->n_heads, a->head_dim,

@@ -89,6 +89,7 @@ struct BwdParams {
     int64_t lp_sh, lp_ss, lp_sk, lb_sh, lb_ss, lb_sk;
     int64_t dq_st, dq_sh, dk_st, dk_sh, dv_st, dv_sh;
     int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid_q, n_dqblk, grid_dq, n_lgrp, n_lchunk, grad_f32, o_f32;
+    int kv_rep;  // query heads per K/V head
     float scale, scale_log2, inv_tau, win_edge;
     float inv_c2;  // 1 / scale_log2: log2-unit bias -> raw q.k units
 };
@@ -179,8 +180,8 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
 
     // ---- tile staging (band tiles from the diagonal down, then landmark tiles) ---------
     const uint32_t kst = (uint32_t)p.k_st * 2u, vst = (uint32_t)p.v_st * 2u;
-    const i32x4 krs = buffer_rsrc(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh, (uint32_t)seq_len * kst);
-    const i32x4 vrs = buffer_rsrc(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh, (uint32_t)seq_len * vst);
+    const i32x4 krs = buffer_rsrc(p.k + (int64_t)seq_start * p.k_st + (int64_t)kv_head(head, p.kv_rep) * p.k_sh, (uint32_t)seq_len * kst);
+    const i32x4 vrs = buffer_rsrc(p.v + (int64_t)seq_start * p.v_st + (int64_t)kv_head(head, p.kv_rep) * p.v_sh, (uint32_t)seq_len * vst);
     const TileLanes<D, kSwzRow, BN, NW> klanes(wave, lane, kst);
     const TileLanes<D, kSwzRow, BN, NW> vlanes(wave, lane, vst);
     const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
@@ -619,8 +620,8 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), 2) bwd_kv_kernel
         for (int s = 0; s < KS; ++s) {
             uint4 a = make_uint4(0, 0, 0, 0), b = a;
             if (kvalid) {
-                a = ld16(p.k + tok * p.k_st + (int64_t)head * p.k_sh + s * 16 + hh * 8);
-                b = ld16(p.v + tok * p.v_st + (int64_t)head * p.v_sh + s * 16 + hh * 8);
+                a = ld16(p.k + tok * p.k_st + (int64_t)kv_head(head, p.kv_rep) * p.k_sh + s * 16 + hh * 8);
+                b = ld16(p.v + tok * p.v_st + (int64_t)kv_head(head, p.kv_rep) * p.v_sh + s * 16 + hh * 8);
             }
             kreg[s] = bitcast<vec8>(a);
             vreg[s] = bitcast<vec8>(b);
@@ -1130,6 +1131,7 @@ hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream) {
     p.total_len = a.total_len;
     p.num_seqs = a.num_seqs;
     p.n_heads = a.n_heads;
+    p.kv_rep = a.n_kv_heads > 0 ? a.n_heads / a.n_kv_heads : 1;
     p.k_lmk = a.k_lmk;
     p.k_pad = (a.k_lmk + 63) / 64 * 64;
     p.n_lgrp = p.k_pad / 64;

@@ -250,6 +250,10 @@ __device__ __forceinline__ int xcd_remap(int bid, int grid) {
 // [x * n_heads / 8, (x + 1) * n_heads / 8) (their K/V rows stay in one L2) and receives
 // its items rank-major, the heads interleaved: rank 0 of every head first. Otherwise XCD
 // x owns a contiguous range of head-major items. `head` may be >= n_heads for padding.
+// K/V head of query head `head` when `rep` consecutive query heads share one K/V head
+// (grouped-query attention); a uniform branch, no division without grouping.
+__device__ __forceinline__ int kv_head(int head, int rep) { return rep == 1 ? head : head / rep; }
+
 __device__ __forceinline__ void head_rank(int bid, int grid, int n_heads, int n_rank, int &head, int &rank) {
     if ((n_heads & 7) == 0) {
         const int hpx = n_heads >> 3, j = bid >> 3;

@@ -62,6 +62,7 @@ struct DenseParams {
     int64_t lb_sh, lb_st;
     int64_t dq_st, dq_sh, dk_st, dk_sh, dv_st, dv_sh;
     int T, H, n_blk, grid, out_f32, o_f32, grad_f32;
+    int kv_rep;      // query heads per K/V head
     float c;         // scale * log2(e): raw q.k -> log2-unit logit
     float inv_c;     // 1 / c
     float scale;
@@ -121,8 +122,8 @@ __global__ void __launch_bounds__(64 * kDW, 2) dense_fwd_kernel(const DenseParam
     const int nt = ghi / BN + 1;  // tiles reaching key 0
 
     const uint32_t kst = (uint32_t)p.k_st * 2u, vst = (uint32_t)p.v_st * 2u;
-    const i32x4 krs = buffer_rsrc(p.k + (int64_t)head * p.k_sh, (uint32_t)p.T * kst);
-    const i32x4 vrs = buffer_rsrc(p.v + (int64_t)head * p.v_sh, (uint32_t)p.T * vst);
+    const i32x4 krs = buffer_rsrc(p.k + (int64_t)kv_head(head, p.kv_rep) * p.k_sh, (uint32_t)p.T * kst);
+    const i32x4 vrs = buffer_rsrc(p.v + (int64_t)kv_head(head, p.kv_rep) * p.v_sh, (uint32_t)p.T * vst);
     const TileLanes<D, kSwzRow, BN, NW> klanes(wave, lane, kst);
     const TileLanes<D, kSwzTr, BN, NW> vlanes(wave, lane, vst);
     const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
@@ -350,8 +351,8 @@ __global__ void __launch_bounds__(64 * kDW, 2) dense_dq_kernel(const DenseParams
     const int nt = ghi / BN + 1;
 
     const uint32_t kst = (uint32_t)p.k_st * 2u, vst = (uint32_t)p.v_st * 2u;
-    const i32x4 krs = buffer_rsrc(p.k + (int64_t)head * p.k_sh, (uint32_t)p.T * kst);
-    const i32x4 vrs = buffer_rsrc(p.v + (int64_t)head * p.v_sh, (uint32_t)p.T * vst);
+    const i32x4 krs = buffer_rsrc(p.k + (int64_t)kv_head(head, p.kv_rep) * p.k_sh, (uint32_t)p.T * kst);
+    const i32x4 vrs = buffer_rsrc(p.v + (int64_t)kv_head(head, p.kv_rep) * p.v_sh, (uint32_t)p.T * vst);
     const TileLanes<D, kSwzRow, BN, NW> klanes(wave, lane, kst);
     const TileLanes<D, kSwzRow, BN, NW> vlanes(wave, lane, vst);
     const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
@@ -537,8 +538,8 @@ __global__ void __launch_bounds__(64 * kDW, D == 64 ? 2 : 1) dense_kv_kernel(con
     const int tj = kvalid ? j : p.T - 1;
     vec8 kv[KS], vv[KS];
     {
-        const uint16_t *kp = p.k + (int64_t)tj * p.k_st + (int64_t)head * p.k_sh + hh * 8;
-        const uint16_t *vp = p.v + (int64_t)tj * p.v_st + (int64_t)head * p.v_sh + hh * 8;
+        const uint16_t *kp = p.k + (int64_t)tj * p.k_st + (int64_t)kv_head(head, p.kv_rep) * p.k_sh + hh * 8;
+        const uint16_t *vp = p.v + (int64_t)tj * p.v_st + (int64_t)kv_head(head, p.kv_rep) * p.v_sh + hh * 8;
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
             kv[s] = bitcast<vec8>(*reinterpret_cast<const uint4 *>(kp + s * 16));
@@ -717,6 +718,7 @@ hipError_t dense_bwd_dt(const DenseParams &p, int D, hipStream_t stream) {
 hipError_t launch_dense_fwd(const dsalt_fwd_args &a, hipStream_t stream) {
     if (a.total_len == 0) return hipSuccess;
     DenseParams p = dense_params(a.total_len, a.n_heads, a.head_dim);
+    p.kv_rep = a.n_kv_heads > 0 ? a.n_heads / a.n_kv_heads : 1;
     p.q = static_cast<const uint16_t *>(a.q);
     p.k = static_cast<const uint16_t *>(a.k);
     p.v = static_cast<const uint16_t *>(a.v);
@@ -746,6 +748,7 @@ int64_t dense_bwd_workspace_bytes(int total_len, int n_heads) {
 hipError_t launch_dense_bwd(const dsalt_bwd_args &a, hipStream_t stream) {
     if (a.total_len == 0) return hipSuccess;
     DenseParams p = dense_params(a.total_len, a.n_heads, a.head_dim);
+    p.kv_rep = a.n_kv_heads > 0 ? a.n_heads / a.n_kv_heads : 1;
     p.q = static_cast<const uint16_t *>(a.q);
     p.k = static_cast<const uint16_t *>(a.k);
     p.v = static_cast<const uint16_t *>(a.v);

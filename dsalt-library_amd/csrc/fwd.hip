@@ -60,6 +60,7 @@ struct FwdParams {
     int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lse_st, lse_sh, w_st;
     int64_t lp_sh, lp_ss, lp_sk, lb_sh, lb_ss, lb_sk;
     int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid, out_f32;
+    int kv_rep;       // query heads per K/V head
     uint32_t q_sign;  // 0x80008000 when scale < 0 (Q is negated on load and |scale| used)
     float c;          // |scale| * log2(e): raw q.k -> log2-unit logit
     float inv_c;      // 1 / c: log2-unit (or natural, times log2 e) bias -> raw units
@@ -120,8 +121,8 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     // (wrapped offsets) read as zeros, empty landmark slots load row 0; the masks give
     // all of them probability 0.
     const uint32_t kst = (uint32_t)p.k_st * 2u, vst = (uint32_t)p.v_st * 2u;  // row strides (bytes)
-    const i32x4 krs = buffer_rsrc(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh, (uint32_t)seq_len * kst);
-    const i32x4 vrs = buffer_rsrc(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh, (uint32_t)seq_len * vst);
+    const i32x4 krs = buffer_rsrc(p.k + (int64_t)seq_start * p.k_st + (int64_t)kv_head(head, p.kv_rep) * p.k_sh, (uint32_t)seq_len * kst);
+    const i32x4 vrs = buffer_rsrc(p.v + (int64_t)seq_start * p.v_st + (int64_t)kv_head(head, p.kv_rep) * p.v_sh, (uint32_t)seq_len * vst);
     const TileLanes<D, kSwzRow, BN, NW> klanes(wave, lane, kst);
     const TileLanes<D, kSwzTr, BN, NW> vlanes(wave, lane, vst);
     const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
@@ -160,9 +161,9 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     // count them (in-loop refills use inline asm, see tiles.h)
     {
         const __amdgpu_buffer_rsrc_t kbr = __builtin_amdgcn_make_buffer_rsrc(
-            (void *)(p.k + (int64_t)seq_start * p.k_st + (int64_t)head * p.k_sh), (short)0, (int)((uint32_t)seq_len * kst), 0x00020000);
+            (void *)(p.k + (int64_t)seq_start * p.k_st + (int64_t)kv_head(head, p.kv_rep) * p.k_sh), (short)0, (int)((uint32_t)seq_len * kst), 0x00020000);
         const __amdgpu_buffer_rsrc_t vbr = __builtin_amdgcn_make_buffer_rsrc(
-            (void *)(p.v + (int64_t)seq_start * p.v_st + (int64_t)head * p.v_sh), (short)0, (int)((uint32_t)seq_len * vst), 0x00020000);
+            (void *)(p.v + (int64_t)seq_start * p.v_st + (int64_t)kv_head(head, p.kv_rep) * p.v_sh), (short)0, (int)((uint32_t)seq_len * vst), 0x00020000);
 #pragma unroll
         for (int t = 0; t < R; ++t) {
             const uint32_t key0 = (uint32_t)band_key0(t);  // wraps below the sequence start: reads zeros
@@ -625,6 +626,7 @@ hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream) {
     p.total_len = a.total_len;
     p.num_seqs = a.num_seqs;
     p.n_heads = a.n_heads;
+    p.kv_rep = a.n_kv_heads > 0 ? a.n_heads / a.n_kv_heads : 1;
     p.k_lmk = a.k_lmk;
     p.k_pad = (a.k_lmk + kFwdBN - 1) / kFwdBN * kFwdBN;
     p.n_qblk = block_upper_bound(a.total_len, a.num_seqs, fwd_bm(a.head_dim));

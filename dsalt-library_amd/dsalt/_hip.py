@@ -49,7 +49,7 @@ class FwdArgs(ctypes.Structure):
         ("lmk_bias", c_void_p), ("lmk_bias_stride_h", c_int64), ("lmk_bias_stride_s", c_int64),
         ("lmk_bias_stride_k", c_int64),
         ("cu_seqlens", c_void_p),
-        ("scale", c_float), ("tau_win", c_float), ("win_edge", c_float), ("reserved1", c_float),
+        ("scale", c_float), ("tau_win", c_float), ("win_edge", c_float), ("n_kv_heads", c_int32),
     ]
 
 
@@ -57,7 +57,7 @@ class BwdArgs(ctypes.Structure):
     _fields_ = [
         ("mode", c_int32), ("dtype", c_int32), ("total_len", c_int32), ("num_seqs", c_int32),
         ("n_heads", c_int32), ("head_dim", c_int32), ("k_lmk", c_int32), ("grad_dtype", c_int32),
-        ("out_dtype", c_int32), ("reserved0", c_int32),
+        ("out_dtype", c_int32), ("n_kv_heads", c_int32),
         ("q", c_void_p), ("q_stride_t", c_int64), ("q_stride_h", c_int64),
         ("k", c_void_p), ("k_stride_t", c_int64), ("k_stride_h", c_int64),
         ("v", c_void_p), ("v_stride_t", c_int64), ("v_stride_h", c_int64),
@@ -227,6 +227,28 @@ def as_kernel_operand(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
+def kv_heads(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> int:
+    """Number of K/V heads of q [T, H, D], k / v [T, n_kv, D] (n_kv divides H: query head h
+    reads K/V head h // (H // n_kv)); validates the shapes and dtypes."""
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise DsaltError(f"q/k/v must be [T, H, D], got {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    T, H, D = q.shape
+    n_kv = k.shape[1]
+    if k.shape != v.shape or k.shape[0] != T or k.shape[2] != D or n_kv < 1 or H % n_kv:
+        raise DsaltError(f"k/v must be [T, n_kv, D] with n_kv dividing H = {H}: q {tuple(q.shape)}, "
+                         f"k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise DsaltError(f"q/k/v must share a bf16/fp16 dtype, got {q.dtype} {k.dtype} {v.dtype}")
+    return n_kv
+
+
+def group_sum(g: torch.Tensor, n_kv: int) -> torch.Tensor:
+    """Per-query-head gradients [T, H, D] summed over each group of H // n_kv heads ->
+    [T, n_kv, D] (the gradient of a K/V head that several query heads share)."""
+    T, H, D = g.shape
+    return g if n_kv == H else g.view(T, n_kv, H // n_kv, D).sum(2)
+
+
 def _f32_vec(t: torch.Tensor) -> torch.Tensor:
     return t if t.dtype == torch.float32 else t.float()
 
@@ -269,8 +291,7 @@ class FwdLauncher:
 def _fwd_args(mode, q, k, v, w, lmk_pos, lmk_bias, cu_seqlens, scale, tau_win, win_edge, out, lse, out_dtype):
     dev = require_gpu(q, k, v, w, cu_seqlens)
     T, H, D = q.shape
-    if k.shape != q.shape or v.shape != q.shape:
-        raise DsaltError(f"q/k/v shapes differ: {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    n_kv = kv_heads(q, k, v)
     if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
         raise DsaltError(f"q/k/v must share a bf16/fp16 dtype, got {q.dtype} {k.dtype} {v.dtype}")
     cu = _cu_i32(cu_seqlens)
@@ -300,7 +321,7 @@ def _fwd_args(mode, q, k, v, w, lmk_pos, lmk_bias, cu_seqlens, scale, tau_win, w
         lse = torch.empty((H, T), device=dev, dtype=torch.float32).t()
     a = FwdArgs()
     a.mode, a.dtype, a.total_len, a.num_seqs = mode, _DTYPES[q.dtype], T, S
-    a.n_heads, a.head_dim, a.k_lmk = H, D, kl
+    a.n_heads, a.head_dim, a.k_lmk, a.n_kv_heads = H, D, kl, n_kv
     a.out_dtype = DTYPE_F32 if odt == torch.float32 else _DTYPES[q.dtype]
     a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
     a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
@@ -331,8 +352,9 @@ def bwd(mode: int, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, sc
         tau_win: float = 1.0, win_edge: float = 4.0, need_dw: bool = False,
         grad_dtype: torch.dtype | None = None):
     """Sparse-attention backward. Returns (dq, dk, dv, d_lmk_bias [H,S,k] fp32 or None,
-    d_w [T] fp32 or None); dq/dk/dv are in ``grad_dtype`` (q.dtype or torch.float32,
-    default q.dtype)."""
+    d_w [T] fp32 or None); dq/dk/dv are [T, H, D] per query head in ``grad_dtype`` (q.dtype
+    or torch.float32, default q.dtype): with grouped K/V heads ``group_sum`` gives the K/V
+    gradients."""
     launcher = BwdLauncher(mode, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, scale,
                            tau_win, win_edge, need_dw, grad_dtype)
     launcher()
@@ -362,7 +384,8 @@ def _bwd_args(mode, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, s
     if q.dim() != 3:
         raise DsaltError(f"q must be [T, H, D], got {tuple(q.shape)}")
     T, H, D = q.shape
-    for name, t in (("k", k), ("v", v), ("out", out), ("dout", dout)):
+    n_kv = kv_heads(q, k, v)
+    for name, t in (("out", out), ("dout", dout)):
         if tuple(t.shape) != (T, H, D):
             raise DsaltError(f"{name} shape {tuple(t.shape)} != q shape {(T, H, D)}")
     if k.dtype != q.dtype or v.dtype != q.dtype or q.dtype not in _DTYPES:
@@ -397,7 +420,7 @@ def _bwd_args(mode, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, s
     ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
     a = BwdArgs()
     a.mode, a.dtype, a.total_len, a.num_seqs = mode, _DTYPES[q.dtype], T, S
-    a.n_heads, a.head_dim, a.k_lmk = H, D, kl
+    a.n_heads, a.head_dim, a.k_lmk, a.n_kv_heads = H, D, kl, n_kv
     a.grad_dtype = DTYPE_F32 if gdt == torch.float32 else _DTYPES[q.dtype]
     if out.dtype not in (q.dtype, torch.float32):
         raise DsaltError(f"saved output must be {q.dtype} or torch.float32, got {out.dtype}")
@@ -429,14 +452,8 @@ def _bwd_args(mode, q, k, v, out, lse, dout, w, lmk_pos, lmk_bias, cu_seqlens, s
 
 def _dense_common(q, k, v, w_cont, lmk_bias):
     """Shape and dtype checks shared by the dense-mode forward and backward."""
-    if q.dim() != 3:
-        raise DsaltError(f"q must be [T, H, D], got {tuple(q.shape)}")
-    T, H, D = q.shape
-    for name, t in (("k", k), ("v", v)):
-        if tuple(t.shape) != (T, H, D):
-            raise DsaltError(f"{name} shape {tuple(t.shape)} != q shape {(T, H, D)}")
-    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise DsaltError(f"q/k/v must share a bf16/fp16 dtype, got {q.dtype} {k.dtype} {v.dtype}")
+    T, H, D = q.shape if q.dim() == 3 else (0, 0, 0)
+    n_kv = kv_heads(q, k, v)
     w = _f32_vec(w_cont)
     if w.dim() != 1 or w.shape[0] != T:
         raise DsaltError(f"w_cont must be [T={T}], got {tuple(w.shape)}")
@@ -444,7 +461,7 @@ def _dense_common(q, k, v, w_cont, lmk_bias):
         if tuple(lmk_bias.shape) != (H, T):
             raise DsaltError(f"dense landmark bias must be [H={H}, T={T}], got {tuple(lmk_bias.shape)}")
         lmk_bias = _f32_vec(lmk_bias)
-    return T, H, D, w, lmk_bias
+    return T, H, D, n_kv, w, lmk_bias
 
 
 def dense_fwd(q, k, v, w_cont, lmk_bias, scale: float, tau_win: float = 1.0, win_edge: float = 4.0,
@@ -463,7 +480,7 @@ class DenseFwdLauncher:
     def __init__(self, q, k, v, w_cont, lmk_bias, scale: float, tau_win: float = 1.0, win_edge: float = 4.0,
                  out_dtype: torch.dtype | None = None):
         self.device = require_gpu(q, k, v, w_cont, lmk_bias)
-        T, H, D, w, lb = _dense_common(q, k, v, w_cont, lmk_bias)
+        T, H, D, n_kv, w, lb = _dense_common(q, k, v, w_cont, lmk_bias)
         odt = q.dtype if out_dtype is None else out_dtype
         if odt not in (q.dtype, torch.float32):
             raise DsaltError(f"out dtype must be {q.dtype} or torch.float32, got {odt}")
@@ -471,7 +488,7 @@ class DenseFwdLauncher:
         self.lse = torch.empty((H, T), device=self.device, dtype=torch.float32).t()
         a = FwdArgs()
         a.mode, a.dtype, a.total_len, a.num_seqs = MODE_DENSE, _DTYPES[q.dtype], T, 1
-        a.n_heads, a.head_dim, a.k_lmk = H, D, 0
+        a.n_heads, a.head_dim, a.k_lmk, a.n_kv_heads = H, D, 0, n_kv
         a.out_dtype = DTYPE_F32 if odt == torch.float32 else _DTYPES[q.dtype]
         a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
         a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
@@ -508,7 +525,7 @@ class DenseBwdLauncher:
     def __init__(self, q, k, v, out, lse, dout, w_cont, lmk_bias, scale: float, tau_win: float = 1.0,
                  win_edge: float = 4.0, need_dw: bool = True, grad_dtype: torch.dtype | None = None):
         self.device = require_gpu(q, k, v, out, lse, dout, w_cont, lmk_bias)
-        T, H, D, w, lb = _dense_common(q, k, v, w_cont, lmk_bias)
+        T, H, D, n_kv, w, lb = _dense_common(q, k, v, w_cont, lmk_bias)
         if tuple(out.shape) != (T, H, D) or tuple(dout.shape) != (T, H, D):
             raise DsaltError(f"out/dout must be [{T}, {H}, {D}], got {tuple(out.shape)} {tuple(dout.shape)}")
         if out.dtype not in (q.dtype, torch.float32):
@@ -529,7 +546,7 @@ class DenseBwdLauncher:
         ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
         a = BwdArgs()
         a.mode, a.dtype, a.total_len, a.num_seqs = MODE_DENSE, _DTYPES[q.dtype], T, 1
-        a.n_heads, a.head_dim, a.k_lmk = H, D, 0
+        a.n_heads, a.head_dim, a.k_lmk, a.n_kv_heads = H, D, 0, n_kv
         a.grad_dtype = DTYPE_F32 if gdt == torch.float32 else _DTYPES[q.dtype]
         a.out_dtype = DTYPE_F32 if out.dtype == torch.float32 else _DTYPES[q.dtype]
         a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)

@@ -43,10 +43,12 @@ class _DenseAttention(torch.autograd.Function):
     def backward(ctx, grad_out):
         q_c, k_c, v_c, out, lse, w_f, lb = ctx.saved_tensors
         od = ctx.dsalt_q_dtype
-        gdt = torch.float32 if od == torch.float32 else q_c.dtype
+        n_kv = k_c.shape[1]
+        gdt = torch.float32 if (od == torch.float32 or n_kv != q_c.shape[1]) else q_c.dtype
         need_dw = ctx.needs_input_grad[3]
         dq, dk, dv, d_lb, d_w = _hip.dense_bwd(q_c, k_c, v_c, out, lse, grad_out, w_f, lb, ctx.dsalt_scale,
                                                ctx.dsalt_tau, ctx.dsalt_edge, need_dw=need_dw, grad_dtype=gdt)
+        dk, dv = _hip.group_sum(dk, n_kv), _hip.group_sum(dv, n_kv)
         if not ctx.needs_input_grad[4]:
             d_lb = None
         return (dq.to(od), dk.to(od), dv.to(od),
@@ -55,7 +57,8 @@ class _DenseAttention(torch.autograd.Function):
 
 
 def dense_attention(q, k, v, w_cont, lmk_bias, tau_win: float = 1.0, win_edge: float = 4.0) -> torch.Tensor:
-    """Differentiable dense DSALT attention of one sequence: q/k/v [T, H, D], w_cont [T],
+    """Differentiable dense DSALT attention of one sequence: q [T, H, D], k/v [T, n_kv, D]
+    (n_kv divides H; grouped heads share K/V without a copy), w_cont [T],
     lmk_bias [H, T] (natural log, -inf off the landmarks) or None. Returns O [T, H, D] in
     the compute dtype."""
     return _DenseAttention.apply(q, k, v, w_cont, lmk_bias, tau_win, win_edge)

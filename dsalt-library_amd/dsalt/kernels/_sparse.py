@@ -47,11 +47,14 @@ def _backward(ctx, grad_out, need_dw: bool):
     q_c, k_c, v_c, out, lse, lp, lb, w_f, cu = ctx.saved_tensors
     od = ctx.dsalt_q_dtype
     # gradients come back in q's dtype; fp32 inputs (computed in fp16) get fp32 gradients
-    # written directly by the kernels
-    gdt = torch.float32 if od == torch.float32 else q_c.dtype
+    # written directly by the kernels, and so do grouped K/V heads (per-query-head dK/dV
+    # are summed over each group in fp32)
+    n_kv = k_c.shape[1]
+    gdt = torch.float32 if (od == torch.float32 or n_kv != q_c.shape[1]) else q_c.dtype
     dq, dk, dv, d_bias, d_w = _hip.bwd(
         ctx.dsalt_mode, q_c, k_c, v_c, out, lse, grad_out, w_f, lp, lb, cu,
         ctx.dsalt_scale, ctx.dsalt_tau, ctx.dsalt_edge, need_dw=need_dw, grad_dtype=gdt)
+    dk, dv = _hip.group_sum(dk, n_kv), _hip.group_sum(dv, n_kv)
     return (dq.to(od), dk.to(od), dv.to(od),
             None if d_bias is None else d_bias.to(od),
             None if d_w is None else d_w.to(od))

@@ -186,13 +186,14 @@ class DSALTAttention(nn.Module):
         v_sel = v if (self.v_proj.bias is None and self._fused_selector) else None
         cu = torch.tensor([0, T], dtype=torch.int32, device=device)
         q, k = apply_rotary_emb_packed(q, k, self.rope_cos, self.rope_sin, cu)
-        k = self._repeat_kv(k)
-        v = self._repeat_kv(v)
 
+        # grouped K/V heads go to the kernels as they are (query head h reads K/V head
+        # h // n_rep); no repeated copy
         w_cont, lmk_bias, lmk_pos = self._dense_selectors(xs, T, device, v_sel)
         out = dense_attention(q, k, v, w_cont, lmk_bias, self.tau_win, float(self.win_edge))
         if not self.training and getattr(self, "_collect_last_P", True):
-            self._last_P = dense_probabilities(q, k, w_cont, lmk_bias, self.tau_win, float(self.win_edge))
+            self._last_P = dense_probabilities(q, self._repeat_kv(k), w_cont, lmk_bias, self.tau_win,
+                                               float(self.win_edge))
         else:
             self._last_P = None
         self._last_selection = (w_cont.detach(), lmk_pos)
@@ -273,8 +274,8 @@ class DSALTAttention(nn.Module):
         else:
             cos, sin = rope_cs
             q, k = apply_rotary_emb_packed(q, k, cos.reshape(total_len, -1), sin.reshape(total_len, -1))
-        k = self._repeat_kv(k)
-        v = self._repeat_kv(v)
+        # grouped K/V heads go to the kernels as they are (query head h reads K/V head
+        # h // n_rep); no repeated copy
 
         aux = x.new_zeros(())
 
@@ -325,6 +326,7 @@ class DSALTAttention(nn.Module):
         is_lmk = torch.zeros(self.n_heads, n + 1, dtype=torch.bool, device=dev)
         is_lmk.scatter_(1, torch.where(lmk[:, 0] >= 0, lmk[:, 0], n), True)
         keep = in_band.unsqueeze(0) | (is_lmk[:, None, :n] & (back >= 0).unsqueeze(0))
-        logits = torch.matmul(q[seg].transpose(0, 1), k[seg].transpose(0, 1).transpose(1, 2).contiguous())
+        k0 = self._repeat_kv(k[seg])
+        logits = torch.matmul(q[seg].transpose(0, 1), k0.transpose(0, 1).transpose(1, 2).contiguous())
         logits = logits * (1.0 / math.sqrt(self.head_dim))
         return logits.masked_fill(~keep, float("-inf")).softmax(dim=-1)

@@ -109,7 +109,9 @@ typedef struct dsalt_fwd_args {
     float scale;               /* logit scale, normally 1/sqrt(D) */
     float tau_win;             /* SOFT only */
     float win_edge;            /* SOFT only */
-    float reserved1;
+    int32_t n_kv_heads;        /* K/V heads, 0 = n_heads; must divide n_heads: query head h
+                                  reads K/V head h / (n_heads / n_kv_heads) (grouped-query
+                                  attention without a repeated K/V copy) */
 } dsalt_fwd_args;
 
 int dsalt_fwd(const dsalt_fwd_args *args, void *stream);
@@ -135,7 +137,8 @@ typedef struct dsalt_bwd_args {
     int32_t mode, dtype, total_len, num_seqs, n_heads, head_dim, k_lmk;
     int32_t grad_dtype; /* dq/dk/dv element type: `dtype` or DSALT_DTYPE_F32 */
     int32_t out_dtype;  /* element type of the saved forward output: `dtype` or DSALT_DTYPE_F32 */
-    int32_t reserved0;
+    int32_t n_kv_heads; /* as in dsalt_fwd_args; dk/dv are still per query head [T, H, D]
+                           (the caller sums each group of n_heads / n_kv_heads heads) */
     const void *q;
     int64_t q_stride_t, q_stride_h;
     const void *k;

@@ -81,6 +81,8 @@ def test_fwd_check_accepts_valid_args():
     ("scale", 0.0, 2, "scale"),
     ("scale", float("inf"), 2, "scale"),
     ("k_stride_t", 1 << 30, 2, "4 GiB"),
+    ("n_kv_heads", 3, 1, "n_kv_heads"),
+    ("n_kv_heads", -1, 1, "n_kv_heads"),
 ])
 def test_fwd_check_rejects(field, value, code, needle):
     kw = {field: value}
@@ -261,3 +263,15 @@ def test_exports_are_none_without_the_library():
     env = dict(os.environ, PYTHONPATH=pkg, DSALT_HIP_LIB="/nonexistent/libdsalt_hip.so")
     res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=300)
     assert res.returncode == 0 and res.stdout.strip() == "ok", res.stderr
+
+
+def test_dense_mode_checks():
+    # DSALT_MODE_DENSE: one sequence, landmarks as a table (k_lmk = 0), positive scale;
+    # cu_seqlens may be NULL; grouped K/V heads accepted when they divide n_heads
+    ok = _fake_fwd(mode=hip.MODE_DENSE, num_seqs=1, k_lmk=0, lmk_pos=None, cu_seqlens=None)
+    assert _check(ok)[0] == 0, _check(ok)
+    assert _check(_fake_fwd(mode=hip.MODE_DENSE, num_seqs=1, k_lmk=0, lmk_pos=None, n_kv_heads=2))[0] == 0
+    for kw, needle in ((dict(num_seqs=2), "one sequence"), (dict(num_seqs=1, k_lmk=4), "table"),
+                       (dict(num_seqs=1, k_lmk=0, lmk_pos=None, scale=-0.125), "scale > 0")):
+        rc, msg = _check(_fake_fwd(mode=hip.MODE_DENSE, **kw))
+        assert rc != 0 and needle in msg, (kw, rc, msg)
