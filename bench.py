@@ -386,11 +386,13 @@ def measure_front_end(wl, w, cu, sel) -> dict:
     }
 
 
-def measure_rope(wl, cu) -> dict:
+def measure_rope(wl, cu, fwd_ms: float) -> dict:
     """The module's RoPE at the workload's shape in bf16: the reference's route written
     eagerly (position gather, cos/sin cast, rotation in torch ops; the reference compiles
-    it with Inductor, which is not used here) against dsalt_rope (one pass, from a HIP
-    graph). Bytes of dsalt_rope: q and k read and written once (bf16); the tables are a
+    it with Inductor, which is not used here) against dsalt_rope of q and k (one pass,
+    from a HIP graph), and the inference path the module takes: dsalt_rope of k alone
+    plus the HARD forward rotating q as it loads it (its time against the plain forward's
+    `fwd_ms`). Bytes of dsalt_rope: q and k read and written once (bf16); the tables are a
     few hundred KB and stay in cache."""
     from dsalt import _hip
     from dsalt.kernels.window_utils import apply_rotary_emb
@@ -408,12 +410,23 @@ def measure_rope(wl, cu) -> dict:
 
     qo, ko = torch.empty_like(q), torch.empty_like(k)
     hip = lambda: _hip.rope(q, k, cos_t, sin_t, cu, q_out=qo, k_out=ko)
+    hip_k = lambda: _hip.rope(None, k, cos_t, sin_t, cu, k_out=ko)
+    # the HARD forward on the workload with q rotated on load (q of the workload serves as
+    # the un-rotated input: the cost does not depend on the values)
+    fused = _hip.FwdLauncher(_hip.MODE_HARD, wl["q"], wl["k"], wl["v"], wl["w"], wl["lmk"], None, cu,
+                             1.0 / math.sqrt(D), rope=(cos_t, sin_t))
     with torch.no_grad():
         eager_ms = time_launches(eager, 50, 10)
         hip_ms = time_graph(hip)
+        hip_k_ms = time_graph(hip_k)
+        fused_ms = time_launches(fused, 200, 100)
     nbytes = 2 * (q.numel() + k.numel()) * 2
     return {"workload": "c2 RoPE of q and k, bf16", "eager_torch_us": eager_ms * 1e3, "hip_us": hip_ms * 1e3,
-            "hip_GB/s": nbytes / (hip_ms * 1e-3) / 1e9}
+            "hip_GB/s": nbytes / (hip_ms * 1e-3) / 1e9,
+            "module_path": {"rope_k_us": hip_k_ms * 1e3, "fwd_rotating_q_us": fused_ms * 1e3,
+                            "fwd_plain_us": fwd_ms * 1e3,
+                            "rope_plus_fwd_us": hip_k_ms * 1e3 + fused_ms * 1e3,
+                            "unfused_rope_plus_fwd_us": hip_ms * 1e3 + fwd_ms * 1e3}}
 
 
 def cpu_baseline(wl, budget_s: float = 12.0):
@@ -619,7 +632,7 @@ def main():
         "quantize_ms": qz_ms,
         "path_ms": ms + sel_ms + qz_ms,
         "selector_front_end": front,
-        "rope": measure_rope(wl, cu),
+        "rope": measure_rope(wl, cu, ms),
     }
     if not args.no_backward:
         res["backward"] = measure_backward(dev)

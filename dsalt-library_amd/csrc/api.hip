@@ -157,6 +157,16 @@ int dsalt_fwd_check(const dsalt_fwd_args *a) {
     if (!a->lse) return fail(DSALT_ERR_INVALID, "lse is NULL");
     if ((rc = check_mode_scalars(a->mode, a->scale, a->tau_win, a->win_edge))) return rc;
     if ((rc = check_kv_heads(a->n_heads, a->n_kv_heads))) return rc;
+    if (a->rope_cos || a->rope_sin) {
+        if (!a->rope_cos || !a->rope_sin) return fail(DSALT_ERR_INVALID, "rope_cos and rope_sin must both be set");
+        if (a->mode == DSALT_MODE_DENSE)
+            return fail(DSALT_ERR_UNSUPPORTED, "the RoPE of Q on load is not available in DSALT_MODE_DENSE");
+        if (a->rope_rows < 1 || a->rope_stride < a->head_dim || !aligned(a->rope_cos, 16) || !aligned(a->rope_sin, 16) ||
+            a->rope_stride % 4)
+            return fail(DSALT_ERR_INVALID,
+                        "RoPE tables need rope_rows >= 1, rope_stride >= head_dim and a multiple of 4, 16-byte "
+                        "alignment (rows %d, stride %lld)", a->rope_rows, (long long)a->rope_stride);
+    }
     return check_span32(a->total_len, {2 * a->q_stride_t, 2 * a->k_stride_t, 2 * a->v_stride_t});
 }
 

@@ -42,6 +42,8 @@ struct BF16 {
     // the low / high element of a packed pair
     static __device__ __forceinline__ float lo_f32(uint32_t x) { return __uint_as_float(x << 16); }
     static __device__ __forceinline__ float hi_f32(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+    // x rounded to the nearest bf16 (ties to even), returned as fp32
+    static __device__ __forceinline__ float round(float x) { return (float)(__bf16)x; }
     // acc + lo + hi of a packed pair, in fp32 (v_dot2c_f32_bf16 against (1, 1))
     static __device__ __forceinline__ float add_pair(uint32_t x, float acc) {
         const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
@@ -63,6 +65,8 @@ struct F16 {
     }
     static __device__ __forceinline__ float lo_f32(uint32_t x) { return to_f32((uint16_t)x); }
     static __device__ __forceinline__ float hi_f32(uint32_t x) { return to_f32((uint16_t)(x >> 16)); }
+    // x rounded to the nearest fp16 (ties to even), returned as fp32
+    static __device__ __forceinline__ float round(float x) { return (float)(_Float16)x; }
     // acc + lo + hi of a packed pair, in fp32 (v_dot2c_f32_f16 against (1, 1))
     static __device__ __forceinline__ float add_pair(uint32_t x, float acc) {
         const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};

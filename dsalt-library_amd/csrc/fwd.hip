@@ -61,6 +61,10 @@ struct FwdParams {
     int64_t lp_sh, lp_ss, lp_sk, lb_sh, lb_ss, lb_sk;
     int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid, out_f32;
     int kv_rep;       // query heads per K/V head
+    const float *rope_cos, *rope_sin;  // non-null: rotate Q on load (RoPE tables [rope_rows][D])
+    int64_t rope_st;
+    int rope_rows;
+    int rope_half;    // the tables' second half equals the first: read D/2 columns
     uint32_t q_sign;  // 0x80008000 when scale < 0 (Q is negated on load and |scale| used)
     float c;          // |scale| * log2(e): raw q.k -> log2-unit logit
     float inv_c;      // 1 / c: log2-unit (or natural, times log2 e) bias -> raw units
@@ -187,6 +191,59 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     }
 
     // ---- Q (B operand: query column ql, head-dim chunk hh*8 of every 16) ---------------
+    // With RoPE tables, Q is rotated here exactly as dsalt_rope does it: the lane holds
+    // both halves of every rotated pair (chunk s and s + KS/2 are head dims c and c + D/2),
+    // cos/sin of the query's position are rounded to the element type, products and
+    // difference / sum in fp32 without contraction, one rounding of the result.
+    if (p.rope_cos) {
+        const int pos = qvalid ? i : seq_len - 1;
+        const bool in_table = pos < p.rope_rows;
+        const float *cr = p.rope_cos + (int64_t)(in_table ? pos : 0) * p.rope_st + hh * 8;
+        const float *sr = p.rope_sin + (int64_t)(in_table ? pos : 0) * p.rope_st + hh * 8;
+        // the lane's 8 columns of each half as two 16-byte loads per table and half
+        auto ld8 = [&](const float *t, float (&x)[8]) {
+            const float4 u = *reinterpret_cast<const float4 *>(t), v4 = *reinterpret_cast<const float4 *>(t + 4);
+            x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w; x[4] = v4.x; x[5] = v4.y; x[6] = v4.z; x[7] = v4.w;
+        };
+#pragma unroll
+        for (int s = 0; s < KS / 2; ++s) {
+            const int s2 = s + KS / 2;
+            float c0[8], c1[8], s0[8], s1[8];
+            ld8(cr + s * 16, c0);
+            ld8(sr + s * 16, s0);
+            if (p.rope_half) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    c1[e] = c0[e];
+                    s1[e] = s0[e];
+                }
+            } else {
+                ld8(cr + s * 16 + D / 2, c1);
+                ld8(sr + s * 16 + D / 2, s1);
+            }
+            uint4 ra = bitcast<uint4>(qv[s]), rb = bitcast<uint4>(qv[s2]);
+            const uint32_t wa[4] = {ra.x, ra.y, ra.z, ra.w}, wb[4] = {rb.x, rb.y, rb.z, rb.w};
+            uint32_t oa[4], ob[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float lo[2], hi[2];
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2) {
+                    const int c = 2 * e + h2;
+                    const float a = h2 ? DT::hi_f32(wa[e]) : DT::lo_f32(wa[e]);
+                    const float b = h2 ? DT::hi_f32(wb[e]) : DT::lo_f32(wb[e]);
+                    const float cc0 = in_table ? DT::round(c0[c]) : NAN, cc1 = in_table ? DT::round(c1[c]) : NAN;
+                    const float ss0 = in_table ? DT::round(s0[c]) : NAN, ss1 = in_table ? DT::round(s1[c]) : NAN;
+                    lo[h2] = __fsub_rn(__fmul_rn(a, cc0), __fmul_rn(b, ss0));
+                    hi[h2] = __fadd_rn(__fmul_rn(b, cc1), __fmul_rn(a, ss1));
+                }
+                oa[e] = DT::pack2(lo[0], lo[1]);
+                ob[e] = DT::pack2(hi[0], hi[1]);
+            }
+            qv[s] = bitcast<vec8>(make_uint4(oa[0], oa[1], oa[2], oa[3]));
+            qv[s2] = bitcast<vec8>(make_uint4(ob[0], ob[1], ob[2], ob[3]));
+        }
+    }
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
         uint4 raw = bitcast<uint4>(qv[s]);
@@ -627,6 +684,11 @@ hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream) {
     p.num_seqs = a.num_seqs;
     p.n_heads = a.n_heads;
     p.kv_rep = a.n_kv_heads > 0 ? a.n_heads / a.n_kv_heads : 1;
+    p.rope_cos = a.rope_cos;
+    p.rope_sin = a.rope_sin;
+    p.rope_st = a.rope_stride;
+    p.rope_rows = a.rope_rows;
+    p.rope_half = a.rope_half;
     p.k_lmk = a.k_lmk;
     p.k_pad = (a.k_lmk + kFwdBN - 1) / kFwdBN * kFwdBN;
     p.n_qblk = block_upper_bound(a.total_len, a.num_seqs, fwd_bm(a.head_dim));

@@ -50,6 +50,8 @@ class FwdArgs(ctypes.Structure):
         ("lmk_bias_stride_k", c_int64),
         ("cu_seqlens", c_void_p),
         ("scale", c_float), ("tau_win", c_float), ("win_edge", c_float), ("n_kv_heads", c_int32),
+        ("rope_cos", c_void_p), ("rope_sin", c_void_p), ("rope_stride", c_int64), ("rope_rows", c_int32),
+        ("rope_half", c_int32),
     ]
 
 
@@ -227,6 +229,26 @@ def as_kernel_operand(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
+_ROPE_TABLES = {}
+
+
+def rope_tables(cos: torch.Tensor, sin: torch.Tensor):
+    """(cos, sin) as contiguous fp32 tables and whether every row repeats its first half in
+    its second (tables built as cat(freqs, freqs): the kernel then reads half of each row).
+    Cached per source storage and version, so a module's tables are converted and checked
+    once, not on every forward (the check synchronises)."""
+    key = (cos.data_ptr(), sin.data_ptr(), tuple(cos.shape), cos.dtype, cos._version, sin._version)
+    hit = _ROPE_TABLES.get(key)
+    if hit is None:
+        c32, s32 = cos.to(torch.float32).contiguous(), sin.to(torch.float32).contiguous()
+        h = c32.shape[-1] // 2
+        half = c32.dim() == 2 and bool(torch.equal(c32[:, :h], c32[:, h:])) and bool(torch.equal(s32[:, :h], s32[:, h:]))
+        if len(_ROPE_TABLES) > 64:
+            _ROPE_TABLES.clear()
+        hit = _ROPE_TABLES[key] = (c32, s32, half, (cos, sin))  # the sources stay alive with the key
+    return hit[0], hit[1], hit[2]
+
+
 def kv_heads(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> int:
     """Number of K/V heads of q [T, H, D], k / v [T, n_kv, D] (n_kv divides H: query head h
     reads K/V head h // (H // n_kv)); validates the shapes and dtypes."""
@@ -263,12 +285,14 @@ def fwd(mode: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, w: torch.T
         lmk_pos: torch.Tensor | None, lmk_bias: torch.Tensor | None, cu_seqlens: torch.Tensor,
         scale: float, tau_win: float = 1.0, win_edge: float = 4.0,
         out: torch.Tensor | None = None, lse: torch.Tensor | None = None,
-        out_dtype: torch.dtype | None = None):
+        out_dtype: torch.dtype | None = None, rope: tuple | None = None):
     """Sparse-attention forward. q/k/v must already be kernel operands (see
-    ``as_kernel_operand``). Returns (out [T,H,D] in ``out_dtype`` (q.dtype or float32,
-    default q.dtype, or the dtype of a given ``out``), lse [T,H] fp32)."""
+    ``as_kernel_operand``). ``rope = (cos, sin)`` (fp32 tables [rows, D], rows = positions
+    inside a sequence) rotates the un-rotated q on load; k must be rotated already.
+    Returns (out [T,H,D] in ``out_dtype`` (q.dtype or float32, default q.dtype, or the
+    dtype of a given ``out``), lse [T,H] fp32)."""
     launcher = FwdLauncher(mode, q, k, v, w, lmk_pos, lmk_bias, cu_seqlens, scale, tau_win, win_edge,
-                           out, lse, out_dtype)
+                           out, lse, out_dtype, rope)
     launcher()
     return launcher.out, launcher.lse
 
@@ -278,9 +302,9 @@ class FwdLauncher:
     the current stream with the same buffers (used for repeated timing and replay)."""
 
     def __init__(self, mode: int, q, k, v, w, lmk_pos, lmk_bias, cu_seqlens, scale: float,
-                 tau_win: float = 1.0, win_edge: float = 4.0, out=None, lse=None, out_dtype=None):
+                 tau_win: float = 1.0, win_edge: float = 4.0, out=None, lse=None, out_dtype=None, rope=None):
         self.args, self._keep, self.out, self.lse, self.device = _fwd_args(
-            mode, q, k, v, w, lmk_pos, lmk_bias, cu_seqlens, scale, tau_win, win_edge, out, lse, out_dtype)
+            mode, q, k, v, w, lmk_pos, lmk_bias, cu_seqlens, scale, tau_win, win_edge, out, lse, out_dtype, rope)
         self._fn = lib().dsalt_fwd
         self._ref = ctypes.byref(self.args)
 
@@ -288,7 +312,8 @@ class FwdLauncher:
         _raise(self._fn(self._ref, stream_handle(self.device)), "dsalt_fwd")
 
 
-def _fwd_args(mode, q, k, v, w, lmk_pos, lmk_bias, cu_seqlens, scale, tau_win, win_edge, out, lse, out_dtype):
+def _fwd_args(mode, q, k, v, w, lmk_pos, lmk_bias, cu_seqlens, scale, tau_win, win_edge, out, lse, out_dtype,
+              rope=None):
     dev = require_gpu(q, k, v, w, cu_seqlens)
     T, H, D = q.shape
     n_kv = kv_heads(q, k, v)
@@ -337,7 +362,15 @@ def _fwd_args(mode, q, k, v, w, lmk_pos, lmk_bias, cu_seqlens, scale, tau_win, w
             a.lmk_bias_stride_h, a.lmk_bias_stride_s, a.lmk_bias_stride_k = lmk_bias.stride()
     a.cu_seqlens = cu.data_ptr()
     a.scale, a.tau_win, a.win_edge = float(scale), float(tau_win), float(win_edge)
-    keep = (q, k, v, w, lmk_pos, lmk_bias, cu, out, lse)  # converted tensors must outlive the args
+    cos = sin = None
+    if rope is not None:
+        require_gpu(*rope)
+        cos, sin, half = rope_tables(*rope)
+        if cos.dim() != 2 or cos.shape != sin.shape or cos.shape[1] != D:
+            raise DsaltError(f"RoPE tables must be [rows, {D}] (got {tuple(cos.shape)}, {tuple(sin.shape)})")
+        a.rope_cos, a.rope_sin, a.rope_stride, a.rope_rows = cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0]
+        a.rope_half = int(half)
+    keep = (q, k, v, w, lmk_pos, lmk_bias, cu, out, lse, cos, sin)  # converted tensors must outlive the args
     return a, keep, out, lse, dev
 
 
@@ -676,8 +709,15 @@ def rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
          q_out: torch.Tensor | None = None, k_out: torch.Tensor | None = None):
     """Rotary embedding of q [T, Hq, D] and k [T, Hk, D] (half-split) with fp32 tables
     cos/sin [rows, D]: rows are positions inside the sequence when cu_seqlens is given,
-    tokens otherwise. ``transpose`` applies the backward rotation. Returns (q_out, k_out)."""
-    dev = require_gpu(q, k, cos, sin, cu_seqlens)
+    tokens otherwise. ``transpose`` applies the backward rotation. Either of q and k may be
+    None (only the other is rotated). Returns (q_out, k_out)."""
+    if q is None and k is None:
+        raise DsaltError("rope needs q or k")
+    ref = q if q is not None else k
+    dev = require_gpu(ref, k, cos, sin, cu_seqlens)
+    q_only, k_only = k is None, q is None
+    q = ref if q is None else q
+    k = ref if k is None else k
     if q.dtype != k.dtype or q.dtype not in _SCORE_DTYPES:
         raise DsaltError(f"q and k must share a dtype of bf16, fp16 or fp32 (got {q.dtype}, {k.dtype})")
     if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
@@ -688,11 +728,13 @@ def rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     sin = sin.to(torch.float32).contiguous()
     if cos.dim() != 2 or cos.shape != sin.shape or cos.shape[1] != q.shape[2]:
         raise DsaltError(f"cos and sin must be [rows, {q.shape[2]}] (got {tuple(cos.shape)}, {tuple(sin.shape)})")
-    q_out = torch.empty_like(q) if q_out is None else q_out
-    k_out = torch.empty_like(k) if k_out is None else k_out
+    q_out = (torch.empty_like(q) if q_out is None else q_out) if not k_only else q
+    k_out = (torch.empty_like(k) if k_out is None else k_out) if not q_only else k
     cu = _cu_i32(cu_seqlens) if cu_seqlens is not None else None
     a = RopeArgs()
-    a.total_len, a.n_q_heads, a.n_k_heads, a.head_dim = q.shape[0], q.shape[1], k.shape[1], q.shape[2]
+    a.total_len, a.head_dim = q.shape[0], q.shape[2]
+    a.n_q_heads = 0 if k_only else q.shape[1]
+    a.n_k_heads = 0 if q_only else k.shape[1]
     a.num_seqs = cu.shape[0] - 1 if cu is not None else 1
     a.dtype, a.transpose, a.table_rows = _SCORE_DTYPES[q.dtype], int(bool(transpose)), cos.shape[0]
     a.q, a.q_stride_t, a.q_stride_h = q.data_ptr(), q.stride(0), q.stride(1)
@@ -702,7 +744,7 @@ def rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     a.cos, a.sin, a.cos_sin_stride = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
     a.cu_seqlens = _ptr(cu)
     _raise(lib().dsalt_rope(ctypes.byref(a), stream_handle(dev)), "dsalt_rope")
-    return q_out, k_out
+    return (None if k_only else q_out), (None if q_only else k_out)
 
 
 class ScoresLauncher:

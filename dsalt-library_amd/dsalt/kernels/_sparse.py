@@ -17,8 +17,10 @@ from .. import _hip
 
 
 def _forward(ctx, mode: int, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens, tau_win, win_edge,
-             out_f32: bool = False):
+             out_f32: bool = False, rope=None):
     _hip.require_gpu(q, k, v, w, cu_seqlens)
+    if rope is not None and torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        raise _hip.DsaltError("the RoPE of q on load is forward-only; rotate q beforehand when gradients are needed")
     if q.dim() != 3:
         raise _hip.DsaltError(f"q must be packed [T, H, D], got {tuple(q.shape)}")
     scale = 1.0 / math.sqrt(q.shape[-1])
@@ -32,7 +34,7 @@ def _forward(ctx, mode: int, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens, tau_win,
         lp = lmk_pos.detach()
     lb = None if (lmk_bias is None or lp is None) else lmk_bias.detach().float()
     out, lse = _hip.fwd(mode, q_c, k_c, v_c, w_f, lp, lb, cu_seqlens, scale, tau_win, win_edge,
-                        out_dtype=torch.float32 if out_f32 else None)
+                        out_dtype=torch.float32 if out_f32 else None, rope=rope)
     ctx.save_for_backward(q_c, k_c, v_c, out, lse, lp, lb, w_f, cu_seqlens)
     ctx.dsalt_mode = mode
     ctx.dsalt_scale = scale
@@ -64,8 +66,8 @@ class _SparseAttention(torch.autograd.Function):
     """Module-path variant: returns O in the compute dtype (no fp32 round trip)."""
 
     @staticmethod
-    def forward(ctx, mode, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens, tau_win, win_edge):
-        return _forward(ctx, mode, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens, tau_win, win_edge)
+    def forward(ctx, mode, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens, tau_win, win_edge, rope):
+        return _forward(ctx, mode, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens, tau_win, win_edge, rope=rope)
 
     @staticmethod
     def backward(ctx, grad_out):
@@ -73,10 +75,12 @@ class _SparseAttention(torch.autograd.Function):
         dq, dk, dv, d_bias, d_w = _backward(ctx, grad_out, need_dw)
         if not ctx.needs_input_grad[5]:
             d_bias = None
-        return None, dq, dk, dv, None, d_bias, d_w, None, None, None
+        return None, dq, dk, dv, None, d_bias, d_w, None, None, None, None
 
 
 def sparse_attention(mode: int, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens,
-                     tau_win: float = 1.0, win_edge: float = 4.0) -> torch.Tensor:
-    """Differentiable DSALT attention returning O [T, H, D] in the compute dtype."""
-    return _SparseAttention.apply(mode, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens, tau_win, win_edge)
+                     tau_win: float = 1.0, win_edge: float = 4.0, rope=None) -> torch.Tensor:
+    """Differentiable DSALT attention returning O [T, H, D] in the compute dtype. With
+    ``rope = (cos, sin)`` q is the un-rotated query and the kernel rotates it on load
+    (forward only; k must be rotated already)."""
+    return _SparseAttention.apply(mode, q, k, v, lmk_pos, lmk_bias, w, cu_seqlens, tau_win, win_edge, rope)

@@ -32,6 +32,14 @@ class _RopeFunction(torch.autograd.Function):
         return dq, dk, None, None, None
 
 
+def rotate_packed(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                  cu_seqlens: torch.Tensor | None = None) -> torch.Tensor:
+    """RoPE of one packed tensor ``[T, H, D]`` with the HIP kernel (no autograd): for the
+    inference path, where only k is rotated ahead of the attention kernel (which rotates q
+    itself) and for the first-sequence diagnostic."""
+    return _hip.rope(None, x, cos, sin, cu_seqlens)[1]
+
+
 def apply_rotary_emb_packed(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                             cu_seqlens: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """RoPE of packed ``q [T, Hq, D]``, ``k [T, Hk, D]`` on the GPU (differentiable in q and

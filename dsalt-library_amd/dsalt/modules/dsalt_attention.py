@@ -39,7 +39,7 @@ from ..kernels._dense import dense_attention, dense_probabilities
 from ..kernels._sparse import sparse_attention
 from ..kernels.landmark_tokens_ker import hybrid_scores_from_v, hybrid_scores_per_head
 from ..kernels.selectors import _compute_landmark_indices
-from ..kernels.window_utils import apply_rotary_emb_packed, build_rope_cache
+from ..kernels.window_utils import apply_rotary_emb_packed, build_rope_cache, rotate_packed
 
 
 def _dynamo_opaque(fn):
@@ -268,8 +268,13 @@ class DSALTAttention(nn.Module):
         v_sel = v if self.v_proj.bias is None else None
 
         # RoPE in one HIP pass (dsalt_attention.py:570-585): positions from cu_seqlens
-        # in-kernel, cos/sin rounded to q's dtype as the reference's cos.to(q.dtype)
-        if rope_cs is None:
+        # in-kernel, cos/sin rounded to q's dtype as the reference's cos.to(q.dtype). At
+        # inference without autograd only k is rotated here: the attention kernel rotates
+        # q as it loads it (the same arithmetic), so q is never written back rotated.
+        fuse_q = not self.training and rope_cs is None and not torch.is_grad_enabled()
+        if fuse_q:
+            k = rotate_packed(k, self.rope_cos, self.rope_sin, cu_seqlens)
+        elif rope_cs is None:
             q, k = apply_rotary_emb_packed(q, k, self.rope_cos, self.rope_sin, cu_seqlens)
         else:
             cos, sin = rope_cs
@@ -295,9 +300,13 @@ class DSALTAttention(nn.Module):
             v=None if route_v is None else route_v.detach(), hip_scores=self._hip_scores)
         self._last_selection = (w_sizes, lmk_indices)
         # Hard A(i) = W(i) ∪ L(i): the score only selects (zero landmark bias).
-        out = sparse_attention(_hip.MODE_HARD, q, k, v, lmk_indices, None, w_sizes, cu_seqlens)
+        out = sparse_attention(_hip.MODE_HARD, q, k, v, lmk_indices, None, w_sizes, cu_seqlens,
+                               rope=(self.rope_cos, self.rope_sin) if fuse_q else None)
 
         if getattr(self, "_collect_last_P", True):
+            if fuse_q:  # the diagnostic needs the rotated q of the first sequence
+                n0 = int(cu_list[1]) if cu_list is not None else int(cu_seqlens[1])
+                q = rotate_packed(q[:n0].contiguous(), self.rope_cos, self.rope_sin, cu_seqlens[:2])
             self._last_P = self._first_sequence_probs(x, q, k, w_sizes, alpha, cu_seqlens, cu_list)
         else:
             self._last_P = None

@@ -112,6 +112,16 @@ typedef struct dsalt_fwd_args {
     int32_t n_kv_heads;        /* K/V heads, 0 = n_heads; must divide n_heads: query head h
                                   reads K/V head h / (n_heads / n_kv_heads) (grouped-query
                                   attention without a repeated K/V copy) */
+    /* Optional RoPE of Q on load (HARD / SOFT): when rope_cos is not NULL, q holds the
+     * un-rotated queries and the kernel rotates them as dsalt_rope would (half-split
+     * pairs, the row of the query's position inside its sequence from rope_cos /
+     * rope_sin [rope_rows, >= head_dim] fp32, rounded to the element type; NaN for a
+     * position past the table). K must already be rotated. */
+    const float *rope_cos, *rope_sin;
+    int64_t rope_stride; /* row stride of the tables (elements) */
+    int32_t rope_rows;
+    int32_t rope_half;   /* 1: every row's columns D/2.. equal its columns ..D/2 (tables built
+                            as cat(freqs, freqs)); the kernel then reads half of each row */
 } dsalt_fwd_args;
 
 int dsalt_fwd(const dsalt_fwd_args *args, void *stream);

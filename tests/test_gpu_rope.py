@@ -4,6 +4,8 @@ per-token tables, in-place use, rows past the table, and the backward against fp
 autograd of the formula. The kernel computes in fp32 and rounds once; the oracle in
 float64 and rounds once, so 16-bit results agree bit for bit except where the fp32
 result sits on a rounding boundary (one ulp of the 16-bit type)."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -85,3 +87,43 @@ def test_rope_backward_matches_autograd(dtype):
     for got, ref in ((qd.grad, q64.grad), (kd.grad, k64.grad)):
         err = (got.cpu().double() - ref).abs().max().item()
         assert err < tol * max(1.0, ref.abs().max().item()), err
+
+
+@pytest.mark.parametrize("mode,D,dtype", [(0, 64, torch.bfloat16), (1, 64, torch.float16), (0, 128, torch.bfloat16),
+                                          (1, 128, torch.bfloat16)],
+                         ids=["hard-d64-bf16", "soft-d64-f16", "hard-d128-bf16", "soft-d128-bf16"])
+@pytest.mark.parametrize("tables", ["rope_cache", "arbitrary"])
+def test_forward_rotates_q_on_load_bit_identical(mode, D, dtype, tables):
+    # the forward's RoPE of q on load equals dsalt_rope followed by the plain forward, bit
+    # for bit (same arithmetic: tables rounded to the element type, fp32 products, no
+    # contraction, one rounding), for packed sequences whose positions restart at 0
+    from dsalt.kernels.window_utils import build_rope_cache
+    from test_gpu_fwd import make_inputs
+    print(f"rope on load mode={mode} D={D} {dtype}", flush=True)
+    q, k, v, w, pos, bias, cu = make_inputs([300, 77, 512], 4, D, 12, mode, seed=90 + D, dtype=dtype,
+                                            n_min=4, n_max=120)
+    if tables == "rope_cache":  # halves repeat: the kernel reads half of each row
+        cos, sin = build_rope_cache(600, D, torch.device("cpu"), base=10000.0)
+    else:  # halves differ: every column read
+        g = torch.Generator().manual_seed(D)
+        cos, sin = torch.randn(600, D, generator=g), torch.randn(600, D, generator=g)
+    qd, kd, vd, cud = (t.to(DEV) for t in (q, k, v, cu))
+    cosd, sind = cos.to(DEV), sin.to(DEV)
+    q_rot, k_rot = _hip.rope(qd, kd, cosd, sind, cud)
+    args = (w.to(DEV), pos.to(DEV), bias.to(DEV), cud, 1.0 / math.sqrt(D))
+    o_ref, l_ref = _hip.fwd(mode, q_rot, k_rot, vd, *args, out_dtype=torch.float32)
+    o_fus, l_fus = _hip.fwd(mode, qd, k_rot, vd, *args, out_dtype=torch.float32, rope=(cosd, sind))
+    torch.cuda.synchronize()
+    assert torch.equal(o_ref, o_fus)
+    assert torch.equal(torch.nan_to_num(l_ref), torch.nan_to_num(l_fus))
+
+
+def test_rope_k_only_matches_pair():
+    from dsalt.kernels.window_utils import build_rope_cache, rotate_packed
+    q = torch.randn(200, 4, 64, device=DEV, dtype=torch.bfloat16)
+    k = torch.randn(200, 2, 64, device=DEV, dtype=torch.bfloat16)
+    cos, sin = build_rope_cache(256, 64, DEV)
+    cu = torch.tensor([0, 120, 200], dtype=torch.int32, device=DEV)
+    q2, k2 = _hip.rope(q, k, cos, sin, cu)
+    assert torch.equal(rotate_packed(k, cos, sin, cu), k2)
+    assert torch.equal(_hip.rope(q, None, cos, sin, cu)[0], q2)
