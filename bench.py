@@ -520,10 +520,6 @@ def main():
     from dsalt import _hip
 
     dev = torch.device("cuda", 0)
-    if args.only is not None:
-        fn = {"lm": measure_lm, "dense": measure_dense, "backward": measure_backward}[args.only]
-        print(json.dumps(fn(dev)))
-        return
     if args.copy_calib_mib > 0:
         n = args.copy_calib_mib * (1 << 20) // 4
         src = torch.randn(n, device=dev)
@@ -532,6 +528,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.only is not None:
+        fn = {"lm": measure_lm, "dense": measure_dense, "backward": measure_backward}[args.only]
+        print(json.dumps(fn(dev)))
+        return
     wl = make_workload(args.config, dev)
     q, k, v, w, lmk, cu = wl["q"], wl["k"], wl["v"], wl["w"], wl["lmk"], wl["cu"]
     T, H, D = wl["T"], wl["H"], wl["D"]
