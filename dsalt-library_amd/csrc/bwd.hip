@@ -266,7 +266,6 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
     }
     const int wpmax = wave_max_u(qvalid ? pmax : -1);
     const int whi = min(wq0 + 31, seq_len - 1);
-    const int wchi = wq0;
 
     for (int s = tid; s < p.k_pad; s += NT) {  // wave-uniform: k_pad is a multiple of 64
         int pos = INT_MAX;
@@ -525,7 +524,7 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
 // P = 2^(S c + bias - lse2) on admitted pairs, dS = P (dP - Delta), then dV^T += dO^T.P
 // and dK^T += Q^T.dS with Q and dO read transposed.
 template <typename DT, int D, int MODE, bool LMK>
-__global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), 2) bwd_kv_kernel(const BwdParams p) {
+__global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1) bwd_kv_kernel(const BwdParams p) {
     typedef typename DT::vec8 vec8;
     constexpr int NW = LMK ? 4 : kv_waves(D), NT = 64 * NW;  // waves, threads
     constexpr int kBM = kv_bm(D);                            // keys per band workgroup

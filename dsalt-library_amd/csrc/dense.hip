@@ -15,16 +15,21 @@
 // larger one, and equal biases share dS in halves (torch.maximum's gradient).
 //
 // Kernels (one launch each, in this order for the backward):
-//   dense_fwd_kernel   query-parallel, 2 waves x 32 queries per workgroup, 32-key tiles
-//                      from the diagonal down to key 0 on a double-buffered direct-load
-//                      LDS ring; S^T = K.Q^T and O^T += V^T.P^T on MFMA, online softmax.
+//   dense_fwd_kernel   query-parallel, 64 queries per workgroup, 32-key tiles from the
+//                      diagonal down to key 0, split over wave groups (4 at D = 64, 2 at
+//                      D = 128; a group is 2 waves x 32 queries walking every NG-th tile
+//                      on its own double-buffered direct-load LDS ring); S^T = K.Q^T and
+//                      O^T += V^T.P^T on MFMA, online softmax per group, the groups'
+//                      (max, sum, O) merged through LDS at the end.
 //   dense_prep_kernel  Delta = rowsum(O dO) per (head, query) and the per-query window
 //                      record (w~, first core key, last landmark key).
 //   dense_dq_kernel    query-parallel: P, dP^T = V.dO^T, dS, dQ^T += K^T.dS^T and the
-//                      per-head window gradient of each query.
-//   dense_kv_kernel    key-parallel, 2 waves x 32 keys: S = Q.K^T, dP = dO.V^T, dS,
+//                      per-head window gradient of each query (the forward's group split,
+//                      partial sums merged in group order).
+//   dense_kv_kernel    key-parallel, 64 keys per workgroup: S = Q.K^T, dP = dO.V^T, dS,
 //                      dV^T += dO^T.P, dK^T += Q^T.dS and the landmark-bias gradient of
-//                      each key, over the query tiles at or after the key block.
+//                      each key, over the query tiles at or after the key block, the tiles
+//                      split over wave groups as above.
 //   dense_dw_kernel    d_w~[i] = sum over heads of the window gradients.
 // Every output element is written by one thread: the results are deterministic.
 #include "common.h"
@@ -36,7 +41,6 @@
 namespace dsalt {
 namespace {
 
-constexpr int kDW = 2;         // waves per workgroup (32 queries or keys each)
 constexpr int kDB = 64;        // queries (or keys) per workgroup
 constexpr int kDN = 32;        // keys (or queries) per tile
 constexpr float kLog2Clamp = -66.43856189774724f;  // log2(1e-20): the reference's sigmoid clamp
@@ -98,45 +102,59 @@ __device__ __forceinline__ float window_bias2(float e, bool core, float &oms, bo
 // ==================================================================================
 // forward
 // ==================================================================================
-template <typename DT, int D>
-__global__ void __launch_bounds__(64 * kDW, 2) dense_fwd_kernel(const DenseParams p) {
-    typedef typename DT::vec8 vec8;
-    constexpr int NW = kDW, BM = kDB, BN = kDN;
-    constexpr int KS = D / 16, ND = D / 32;
-    typedef TileN<D, BN, NW> Tile;
-    constexpr int TB = Tile::BYTES;
+// Key tiles of a workgroup are split over kFwdGroups(D) wave groups: group g (waves 2g,
+// 2g+1, the workgroup's 64 queries) walks tiles t = g, g + NG, ... on its own double-
+// buffered ring, keeping its own running max, sum and O; the groups step together (one
+// workgroup barrier per step) and their states are merged through LDS at the end, in
+// group order. A workgroup's serial tile chain is NG times shorter.
+constexpr int dense_fwd_groups(int D) { return D == 64 ? 4 : 2; }
 
-    __shared__ __align__(1024) char s_tiles[2][2][TB];  // [slot][K, V]
-    __shared__ __align__(16) float s_lb[2][BN];          // landmark bias of the slot's keys (log2 units)
+template <typename DT, int D>
+__global__ void __launch_bounds__(128 * dense_fwd_groups(D), 1) dense_fwd_kernel(const DenseParams p) {
+    typedef typename DT::vec8 vec8;
+    constexpr int NG = dense_fwd_groups(D);
+    constexpr int BM = kDB, BN = kDN;
+    constexpr int KS = D / 16, ND = D / 32;
+    typedef TileN<D, BN, 2> Tile;
+    constexpr int TB = Tile::BYTES;
+    constexpr int MERGE = ND * 16 + 2;  // floats per lane of a group state: O, max, sum
+    static_assert((NG - 1) * 2 * 64 * MERGE * 4 <= NG * 2 * 2 * TB, "merge buffer fits in the tile rings");
+
+    __shared__ __align__(1024) char s_tiles[NG][2][2][TB];  // [group][slot][K, V]
+    __shared__ __align__(16) float s_lb[NG][2][BN];          // landmark bias of the slot's keys (log2 units)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 1, wi = wave & 1;
     const int ql = lane & 31, hh = lane >> 5;
     int head, rank;
     head_rank(blockIdx.x, p.grid, p.H, p.n_blk, head, rank);
     if (head >= p.H) return;
     const int blk = p.n_blk - 1 - rank;  // long blocks first
-    const int wq0 = blk * BM + wave * 32;
+    const int wq0 = blk * BM + wi * 32;
     const int i = wq0 + ql;
     const bool qvalid = i < p.T;
     const int ghi = min(blk * BM + BM - 1, p.T - 1);
-    const int nt = ghi / BN + 1;  // tiles reaching key 0
+    const int nt = ghi / BN + 1;             // tiles reaching key 0
+    const int nit = (nt + NG - 1) / NG;      // steps of the workgroup
 
     const uint32_t kst = (uint32_t)p.k_st * 2u, vst = (uint32_t)p.v_st * 2u;
-    const i32x4 krs = buffer_rsrc(p.k + (int64_t)kv_head(head, p.kv_rep) * p.k_sh, (uint32_t)p.T * kst);
-    const i32x4 vrs = buffer_rsrc(p.v + (int64_t)kv_head(head, p.kv_rep) * p.v_sh, (uint32_t)p.T * vst);
-    const TileLanes<D, kSwzRow, BN, NW> klanes(wave, lane, kst);
-    const TileLanes<D, kSwzTr, BN, NW> vlanes(wave, lane, vst);
-    const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
+    const int kvh = kv_head(head, p.kv_rep);
+    const i32x4 krs = buffer_rsrc(p.k + (int64_t)kvh * p.k_sh, (uint32_t)p.T * kst);
+    const i32x4 vrs = buffer_rsrc(p.v + (int64_t)kvh * p.v_sh, (uint32_t)p.T * vst);
+    const TileLanes<D, kSwzRow, BN, 2> klanes(wi, lane, kst);
+    const TileLanes<D, kSwzTr, BN, 2> vlanes(wi, lane, vst);
+    const uint32_t tiles_lds = lds_addr(&s_tiles[grp][0][0][0]);
     auto key0 = [&](int t) { return ghi - (BN - 1) - t * BN; };
-    auto issue = [&](int t) {  // K and V of tile t into slot t % 2 (keys below 0 read zeros)
-        const uint32_t base = tiles_lds + (t & 1) * (2 * TB);
-        klanes.load_band(base, wave, krs, (uint32_t)key0(t) * kst);
-        vlanes.load_band(base + TB, wave, vrs, (uint32_t)key0(t) * vst);
+    auto issue = [&](int it) {  // the group's tile of step it into slot it % 2 (keys below 0 read zeros)
+        const int t = grp + NG * it;
+        const uint32_t base = tiles_lds + (it & 1) * (2 * TB);
+        klanes.load_band(base, wi, krs, (uint32_t)key0(t) * kst);
+        vlanes.load_band(base + TB, wi, vrs, (uint32_t)key0(t) * vst);
     };
-    // landmark bias of tile t's keys, staged through registers by wave 0 (lanes 0..31)
+    // landmark bias of tile t's keys, staged through registers by the group's first wave
     auto lb_load = [&](int t) -> float {
         const int j = key0(t) + ql;
-        if (!p.lb || wave != 0 || hh != 0 || j < 0 || j >= p.T) return -INFINITY;
+        if (!p.lb || wi != 0 || hh != 0 || j < 0 || j >= p.T) return -INFINITY;
         return p.lb[(int64_t)head * p.lb_sh + (int64_t)j * p.lb_st] * kLog2e;
     };
 
@@ -156,8 +174,9 @@ __global__ void __launch_bounds__(64 * kDW, 2) dense_fwd_kernel(const DenseParam
 #pragma unroll
     for (int r = 0; r < 16; ++r) ec[r] = fast_exp2((kEdgeMidD - (float)acc_row_const(r)) * p.inv_tau * kLog2e);
 
-    issue(0);
-    float lbr = lb_load(0);
+    const bool act0 = grp < nt;
+    if (act0) issue(0);
+    float lbr = act0 ? lb_load(grp) : -INFINITY;
 
     f32x16 oacc[ND];
 #pragma unroll
@@ -167,16 +186,19 @@ __global__ void __launch_bounds__(64 * kDW, 2) dense_fwd_kernel(const DenseParam
     float m2 = -INFINITY, mu = 0.f, thr = -INFINITY;
     float lsum0 = 0.f, lsum1 = 0.f;
 
-    for (int t = 0; t < nt; ++t) {
-        const int slot = t & 1;
-        if (wave == 0 && hh == 0) s_lb[slot][ql] = lbr;
-        tile_barrier<0>();  // tile t landed for every wave; everyone left tile t-1
-        if (t + 1 < nt) {
-            issue(t + 1);
-            lbr = lb_load(t + 1);
+    for (int it = 0; it < nit; ++it) {
+        const int t = grp + NG * it;
+        const bool act = t < nt;               // group-uniform
+        const int slot = it & 1;
+        if (wi == 0 && hh == 0) s_lb[grp][slot][ql] = lbr;
+        tile_barrier<0>();  // the step's tiles landed for every group; everyone left step it-1
+        if (t + NG < nt) {
+            issue(it + 1);
+            lbr = lb_load(t + NG);
         }
-        const char *ktile = s_tiles[slot][0];
-        const char *vtile = s_tiles[slot][1];
+        if (!act) continue;
+        const char *ktile = s_tiles[grp][slot][0];
+        const char *vtile = s_tiles[grp][slot][1];
         f32x16 s;
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[r] = 0.f;
@@ -194,7 +216,7 @@ __global__ void __launch_bounds__(64 * kDW, 2) dense_fwd_kernel(const DenseParam
         float lbv[16];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const float4 l4 = *reinterpret_cast<const float4 *>(&s_lb[slot][g * 8 + hh * 4]);
+            const float4 l4 = *reinterpret_cast<const float4 *>(&s_lb[grp][slot][g * 8 + hh * 4]);
             lbv[4 * g] = l4.x; lbv[4 * g + 1] = l4.y; lbv[4 * g + 2] = l4.z; lbv[4 * g + 3] = l4.w;
         }
         float tmax = -INFINITY;
@@ -226,12 +248,15 @@ __global__ void __launch_bounds__(64 * kDW, 2) dense_fwd_kernel(const DenseParam
             mu = (m2 == -INFINITY) ? 0.f : m2;
             thr = raise ? tmax + 8.f * p.inv_c : thr;
         }
+        // the row sums take the fp32 P (the LSE then matches the fp32 softmax the
+        // backward recomputes); O accumulates the 16-bit P the MFMA consumes
         uint32_t pk[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            pk[j] = DT::pack2(fast_exp2(fmaf(s[2 * j], c, -mu)), fast_exp2(fmaf(s[2 * j + 1], c, -mu)));
-            if (j & 1) lsum1 = DT::add_pair(pk[j], lsum1);
-            else lsum0 = DT::add_pair(pk[j], lsum0);
+            const float e0 = fast_exp2(fmaf(s[2 * j], c, -mu)), e1 = fast_exp2(fmaf(s[2 * j + 1], c, -mu));
+            pk[j] = DT::pack2(e0, e1);
+            if (j & 1) lsum1 += e0 + e1;
+            else lsum0 += e0 + e1;
         }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
@@ -241,9 +266,38 @@ __global__ void __launch_bounds__(64 * kDW, 2) dense_fwd_kernel(const DenseParam
                 oacc[d] = DT::mfma(bitcast<vec8>(tile_read_tr<D>(vtile, kk * 16, d * 32, lane)), b, oacc[d]);
         }
     }
-    tile_barrier<0>();
+    tile_barrier<0>();  // every group is done with its ring: the rings become the merge buffer
 
-    const float ltot = half_sum(lsum0 + lsum1);
+    // merge: groups 1..NG-1 publish (O, max, sum) per lane, group 0 folds them in group
+    // order (the max of the maxima, each state rescaled to it)
+    float *mbuf = reinterpret_cast<float *>(&s_tiles[0][0][0][0]);
+    auto mslot = [&](int g, int e) { return mbuf + ((((g - 1) * 2 + wi) * MERGE + e) * 64 + lane); };
+    float lsum = lsum0 + lsum1;
+    if (grp > 0) {
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) *mslot(grp, d * 16 + r) = oacc[d][r];
+        *mslot(grp, ND * 16) = m2;
+        *mslot(grp, ND * 16 + 1) = lsum;
+    }
+    __syncthreads();
+    if (grp > 0) return;
+#pragma unroll
+    for (int g = 1; g < NG; ++g) {
+        const float mg = *mslot(g, ND * 16), lg = *mslot(g, ND * 16 + 1);
+        const float mn = fmaxf(m2, mg);
+        const float a0 = (m2 == -INFINITY) ? 0.f : fast_exp2(m2 - mn);
+        const float ag = (mg == -INFINITY) ? 0.f : fast_exp2(mg - mn);
+        lsum = lsum * a0 + lg * ag;
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[d][r] = oacc[d][r] * a0 + *mslot(g, d * 16 + r) * ag;
+        m2 = mn;
+    }
+
+    const float ltot = half_sum(lsum);
     const bool nonempty = ltot > 1e-9f;
     const float inv = nonempty ? 1.f / ltot : 0.f;
     if (qvalid) {
@@ -326,45 +380,55 @@ __device__ __forceinline__ void bias_shares(float bw, float bl, float &sw, float
     sl = bl > bw ? 1.f : (bw == bl ? 0.5f : 0.f);
 }
 
-// Query-parallel dQ and the per-head window gradient, the forward's tiling.
-template <typename DT, int D>
-__global__ void __launch_bounds__(64 * kDW, 2) dense_dq_kernel(const DenseParams p) {
-    typedef typename DT::vec8 vec8;
-    constexpr int NW = kDW, BM = kDB, BN = kDN;
-    constexpr int KS = D / 16, ND = D / 32;
-    typedef TileN<D, BN, NW> Tile;
-    constexpr int TB = Tile::BYTES;
+// Query-parallel dQ and the per-head window gradient, the forward's tiling and its
+// key-tile split over dense_bwd_groups(D) wave groups (partial dQ and window gradients
+// summed through LDS in group order at the end).
+constexpr int dense_bwd_groups(int D) { return D == 64 ? 4 : 2; }
 
-    __shared__ __align__(1024) char s_tiles[2][2][TB];  // [slot][K, V], both row-swizzled
-    __shared__ __align__(16) float s_lb[2][BN];
+template <typename DT, int D>
+__global__ void __launch_bounds__(128 * dense_bwd_groups(D), 1) dense_dq_kernel(const DenseParams p) {
+    typedef typename DT::vec8 vec8;
+    constexpr int NG = dense_bwd_groups(D);
+    constexpr int BM = kDB, BN = kDN;
+    constexpr int KS = D / 16, ND = D / 32;
+    typedef TileN<D, BN, 2> Tile;
+    constexpr int TB = Tile::BYTES;
+    constexpr int MERGE = ND * 16 + 1;  // floats per lane of a group's partial: dQ, window gradient
+    static_assert((NG - 1) * 2 * 64 * MERGE * 4 <= NG * 2 * 2 * TB, "merge buffer fits in the tile rings");
+
+    __shared__ __align__(1024) char s_tiles[NG][2][2][TB];  // [group][slot][K, V], both row-swizzled
+    __shared__ __align__(16) float s_lb[NG][2][BN];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 1, wi = wave & 1;
     const int ql = lane & 31, hh = lane >> 5;
     int head, rank;
     head_rank(blockIdx.x, p.grid, p.H, p.n_blk, head, rank);
     if (head >= p.H) return;
     const int blk = p.n_blk - 1 - rank;
-    const int wq0 = blk * BM + wave * 32;
+    const int wq0 = blk * BM + wi * 32;
     const int i = wq0 + ql;
     const bool qvalid = i < p.T;
     const int ghi = min(blk * BM + BM - 1, p.T - 1);
     const int nt = ghi / BN + 1;
+    const int nit = (nt + NG - 1) / NG;
 
     const uint32_t kst = (uint32_t)p.k_st * 2u, vst = (uint32_t)p.v_st * 2u;
     const i32x4 krs = buffer_rsrc(p.k + (int64_t)kv_head(head, p.kv_rep) * p.k_sh, (uint32_t)p.T * kst);
     const i32x4 vrs = buffer_rsrc(p.v + (int64_t)kv_head(head, p.kv_rep) * p.v_sh, (uint32_t)p.T * vst);
-    const TileLanes<D, kSwzRow, BN, NW> klanes(wave, lane, kst);
-    const TileLanes<D, kSwzRow, BN, NW> vlanes(wave, lane, vst);
-    const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
+    const TileLanes<D, kSwzRow, BN, 2> klanes(wi, lane, kst);
+    const TileLanes<D, kSwzRow, BN, 2> vlanes(wi, lane, vst);
+    const uint32_t tiles_lds = lds_addr(&s_tiles[grp][0][0][0]);
     auto key0 = [&](int t) { return ghi - (BN - 1) - t * BN; };
-    auto issue = [&](int t) {
-        const uint32_t base = tiles_lds + (t & 1) * (2 * TB);
-        klanes.load_band(base, wave, krs, (uint32_t)key0(t) * kst);
-        vlanes.load_band(base + TB, wave, vrs, (uint32_t)key0(t) * vst);
+    auto issue = [&](int it) {  // the group's tile of step it into slot it % 2
+        const int t = grp + NG * it;
+        const uint32_t base = tiles_lds + (it & 1) * (2 * TB);
+        klanes.load_band(base, wi, krs, (uint32_t)key0(t) * kst);
+        vlanes.load_band(base + TB, wi, vrs, (uint32_t)key0(t) * vst);
     };
     auto lb_load = [&](int t) -> float {
         const int j = key0(t) + ql;
-        if (!p.lb || wave != 0 || hh != 0 || j < 0 || j >= p.T) return -INFINITY;
+        if (!p.lb || wi != 0 || hh != 0 || j < 0 || j >= p.T) return -INFINITY;
         return p.lb[(int64_t)head * p.lb_sh + (int64_t)j * p.lb_st] * kLog2e;
     };
 
@@ -390,8 +454,8 @@ __global__ void __launch_bounds__(64 * kDW, 2) dense_dq_kernel(const DenseParams
     for (int r = 0; r < 16; ++r) ec[r] = fast_exp2((kEdgeMidD - (float)acc_row_const(r)) * p.inv_tau * kLog2e);
     const bool live = qvalid && lse2 < INFINITY && lse2 > -INFINITY;
 
-    issue(0);
-    float lbr = lb_load(0);
+    if (grp < nt) issue(0);
+    float lbr = grp < nt ? lb_load(grp) : -INFINITY;
     f32x16 dq[ND];
 #pragma unroll
     for (int d = 0; d < ND; ++d)
@@ -399,16 +463,18 @@ __global__ void __launch_bounds__(64 * kDW, 2) dense_dq_kernel(const DenseParams
         for (int r = 0; r < 16; ++r) dq[d][r] = 0.f;
     float dwl = 0.f;
 
-    for (int t = 0; t < nt; ++t) {
-        const int slot = t & 1;
-        if (wave == 0 && hh == 0) s_lb[slot][ql] = lbr;
-        tile_barrier<0>();
-        if (t + 1 < nt) {
-            issue(t + 1);
-            lbr = lb_load(t + 1);
+    for (int it = 0; it < nit; ++it) {
+        const int t = grp + NG * it;
+        const int slot = it & 1;
+        if (wi == 0 && hh == 0) s_lb[grp][slot][ql] = lbr;
+        tile_barrier<0>();  // the step's tiles landed for every group; everyone left step it-1
+        if (t + NG < nt) {
+            issue(it + 1);
+            lbr = lb_load(t + NG);
         }
-        const char *ktile = s_tiles[slot][0];
-        const char *vtile = s_tiles[slot][1];
+        if (t >= nt) continue;  // group-uniform
+        const char *ktile = s_tiles[grp][slot][0];
+        const char *vtile = s_tiles[grp][slot][1];
         f32x16 s, dp;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -429,7 +495,7 @@ __global__ void __launch_bounds__(64 * kDW, 2) dense_dq_kernel(const DenseParams
         float lbv[16];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const float4 l4 = *reinterpret_cast<const float4 *>(&s_lb[slot][g * 8 + hh * 4]);
+            const float4 l4 = *reinterpret_cast<const float4 *>(&s_lb[grp][slot][g * 8 + hh * 4]);
             lbv[4 * g] = l4.x; lbv[4 * g + 1] = l4.y; lbv[4 * g + 2] = l4.z; lbv[4 * g + 3] = l4.w;
         }
         uint32_t pk[8];
@@ -463,7 +529,28 @@ __global__ void __launch_bounds__(64 * kDW, 2) dense_dq_kernel(const DenseParams
                 dq[d] = DT::mfma(bitcast<vec8>(tile_read_tr<D, kSwzRow>(ktile, kk * 16, d * 32, lane)), b, dq[d]);
         }
     }
-    tile_barrier<0>();
+    tile_barrier<0>();  // every group is done with its ring: the rings become the merge buffer
+    {
+        float *mbuf = reinterpret_cast<float *>(&s_tiles[0][0][0][0]);
+        auto mslot = [&](int g, int e) { return mbuf + ((((g - 1) * 2 + wi) * MERGE + e) * 64 + lane); };
+        if (grp > 0) {
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) *mslot(grp, d * 16 + r) = dq[d][r];
+            *mslot(grp, ND * 16) = dwl;
+        }
+        __syncthreads();
+        if (grp > 0) return;
+#pragma unroll
+        for (int g = 1; g < NG; ++g) {
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) dq[d][r] += *mslot(g, d * 16 + r);
+            dwl += *mslot(g, ND * 16);
+        }
+    }
     const float dw = half_sum(dwl) * p.inv_tau;
     if (qvalid) {
         const int64_t off = (int64_t)i * p.dq_st + (int64_t)head * p.dq_sh;
@@ -488,45 +575,53 @@ __global__ void __launch_bounds__(64 * kDW, 2) dense_dq_kernel(const DenseParams
 }
 
 // Key-parallel dK, dV and the landmark-bias gradient: a wave owns 32 keys (lane = key
-// column of S = Q.K^T), and scans the 32-query tiles at or after its workgroup's keys.
+// column of S = Q.K^T), and scans the 32-query tiles at or after its workgroup's keys,
+// split over dense_bwd_groups(D) wave groups as in dense_dq_kernel (partial dK, dV and
+// bias gradients summed through LDS in group order).
 template <typename DT, int D>
-__global__ void __launch_bounds__(64 * kDW, D == 64 ? 2 : 1) dense_kv_kernel(const DenseParams p) {
+__global__ void __launch_bounds__(128 * dense_bwd_groups(D), 1) dense_kv_kernel(const DenseParams p) {
     typedef typename DT::vec8 vec8;
-    constexpr int NW = kDW, BK = kDB, QN = kDN;
+    constexpr int NG = dense_bwd_groups(D);
+    constexpr int BK = kDB, QN = kDN;
     constexpr int KS = D / 16, ND = D / 32;
-    typedef TileN<D, QN, NW> Tile;
+    typedef TileN<D, QN, 2> Tile;
     constexpr int TB = Tile::BYTES;
+    constexpr int MERGE = ND * 16 + 1;  // floats per lane and merge round: dK (+ bias gradient), then dV
+    static_assert((NG - 1) * 2 * 64 * MERGE * 4 <= NG * 2 * 2 * TB, "merge buffer fits in the tile rings");
 
-    __shared__ __align__(1024) char s_tiles[2][2][TB];   // [slot][Q, dO], both row-swizzled
-    __shared__ __align__(16) float s_qf[2][5][QN];        // per-query lse2, delta, w~, core, pmax
+    __shared__ __align__(1024) char s_tiles[NG][2][2][TB];   // [group][slot][Q, dO], both row-swizzled
+    __shared__ __align__(16) float s_qf[NG][2][5][QN];        // per-query lse2, delta, w~, core, pmax
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 1, wi = wave & 1;
     const int kl = lane & 31, hh = lane >> 5;
     int head, rank;
     head_rank(blockIdx.x, p.grid, p.H, p.n_blk, head, rank);
     if (head >= p.H) return;
     const int kblk = rank;                 // early keys see the most queries: launched first
     const int k0 = kblk * BK;
-    const int j = k0 + wave * 32 + kl;     // this lane's key
+    const int j = k0 + wi * 32 + kl;       // this lane's key
     const bool kvalid = j < p.T;
     const int nu = (p.T - k0 + QN - 1) / QN;  // query tiles from k0 to T - 1
+    const int nit = (nu + NG - 1) / NG;
 
     const uint32_t qst = (uint32_t)p.q_st * 2u, dst = (uint32_t)p.do_st * 2u;
     const i32x4 qrs = buffer_rsrc(p.q + (int64_t)head * p.q_sh, (uint32_t)p.T * qst);
     const i32x4 drs = buffer_rsrc(p.dout + (int64_t)head * p.do_sh, (uint32_t)p.T * dst);
-    const TileLanes<D, kSwzRow, QN, NW> qlanes(wave, lane, qst);
-    const TileLanes<D, kSwzRow, QN, NW> dlanes(wave, lane, dst);
-    const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
+    const TileLanes<D, kSwzRow, QN, 2> qlanes(wi, lane, qst);
+    const TileLanes<D, kSwzRow, QN, 2> dlanes(wi, lane, dst);
+    const uint32_t tiles_lds = lds_addr(&s_tiles[grp][0][0][0]);
     auto qtile0 = [&](int u) { return k0 + u * QN; };
-    auto issue = [&](int u) {
-        const uint32_t base = tiles_lds + (u & 1) * (2 * TB);
-        qlanes.load_band(base, wave, qrs, (uint32_t)qtile0(u) * qst);  // rows past T read zeros
-        dlanes.load_band(base + TB, wave, drs, (uint32_t)qtile0(u) * dst);
+    auto issue = [&](int it) {  // the group's query tile of step it into slot it % 2
+        const int u = grp + NG * it;
+        const uint32_t base = tiles_lds + (it & 1) * (2 * TB);
+        qlanes.load_band(base, wi, qrs, (uint32_t)qtile0(u) * qst);  // rows past T read zeros
+        dlanes.load_band(base + TB, wi, drs, (uint32_t)qtile0(u) * dst);
     };
-    // per-query fields of tile u (wave 0, lanes 0..31), staged through registers
+    // per-query fields of tile u (the group's first wave, lanes 0..31), staged through registers
     auto qf_load = [&](int u, float (&f)[5]) {
         const int iq = qtile0(u) + kl;
-        const bool ok = wave == 0 && hh == 0 && iq < p.T;
+        const bool ok = wi == 0 && hh == 0 && iq < p.T;
         const int ii = ok ? iq : 0;
         f[0] = ok ? p.lse[(int64_t)ii * p.lse_st + (int64_t)head * p.lse_sh] * kLog2e : INFINITY;
         f[1] = ok ? p.ws_delta[(int64_t)head * p.T + ii] : 0.f;
@@ -549,9 +644,9 @@ __global__ void __launch_bounds__(64 * kDW, D == 64 ? 2 : 1) dense_kv_kernel(con
     const float lbj = (p.lb && kvalid) ? p.lb[(int64_t)head * p.lb_sh + (int64_t)j * p.lb_st] * kLog2e : -INFINITY;
     const float c = p.c;
 
-    issue(0);
+    if (grp < nu) issue(0);
     float qf[5];
-    qf_load(0, qf);
+    qf_load(grp, qf);  // fields of a tile past the sequence read as "no query"
     f32x16 dk[ND], dv[ND];
 #pragma unroll
     for (int d = 0; d < ND; ++d)
@@ -562,19 +657,21 @@ __global__ void __launch_bounds__(64 * kDW, D == 64 ? 2 : 1) dense_kv_kernel(con
         }
     float dlb = 0.f;
 
-    for (int u = 0; u < nu; ++u) {
-        const int slot = u & 1;
-        if (wave == 0 && hh == 0) {
+    for (int it = 0; it < nit; ++it) {
+        const int u = grp + NG * it;
+        const int slot = it & 1;
+        if (wi == 0 && hh == 0) {
 #pragma unroll
-            for (int f = 0; f < 5; ++f) s_qf[slot][f][kl] = qf[f];
+            for (int f = 0; f < 5; ++f) s_qf[grp][slot][f][kl] = qf[f];
         }
-        tile_barrier<0>();
-        if (u + 1 < nu) {
-            issue(u + 1);
-            qf_load(u + 1, qf);
+        tile_barrier<0>();  // the step's tiles landed for every group; everyone left step it-1
+        if (u + NG < nu) {
+            issue(it + 1);
+            qf_load(u + NG, qf);
         }
-        const char *qtile = s_tiles[slot][0];
-        const char *dtile = s_tiles[slot][1];
+        if (u >= nu) continue;  // group-uniform
+        const char *qtile = s_tiles[grp][slot][0];
+        const char *dtile = s_tiles[grp][slot][1];
         f32x16 s, dp;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -594,7 +691,7 @@ __global__ void __launch_bounds__(64 * kDW, D == 64 ? 2 : 1) dense_kv_kernel(con
             float fv[5][4];
 #pragma unroll
             for (int f = 0; f < 5; ++f) {
-                const float4 v4 = *reinterpret_cast<const float4 *>(&s_qf[slot][f][g * 8 + hh * 4]);
+                const float4 v4 = *reinterpret_cast<const float4 *>(&s_qf[grp][slot][f][g * 8 + hh * 4]);
                 fv[f][0] = v4.x; fv[f][1] = v4.y; fv[f][2] = v4.z; fv[f][3] = v4.w;
             }
             float pr[4], dsv[4];
@@ -633,7 +730,46 @@ __global__ void __launch_bounds__(64 * kDW, D == 64 ? 2 : 1) dense_kv_kernel(con
             }
         }
     }
-    tile_barrier<0>();
+    tile_barrier<0>();  // every group is done with its ring: the rings become the merge buffer
+    {
+        float *mbuf = reinterpret_cast<float *>(&s_tiles[0][0][0][0]);
+        auto mslot = [&](int g, int e) { return mbuf + ((((g - 1) * 2 + wi) * MERGE + e) * 64 + lane); };
+        // round 1: dK and the bias gradient
+        if (grp > 0) {
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) *mslot(grp, d * 16 + r) = dk[d][r];
+            *mslot(grp, ND * 16) = dlb;
+        }
+        __syncthreads();
+        if (grp == 0) {
+#pragma unroll
+            for (int g = 1; g < NG; ++g) {
+#pragma unroll
+                for (int d = 0; d < ND; ++d)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) dk[d][r] += *mslot(g, d * 16 + r);
+                dlb += *mslot(g, ND * 16);
+            }
+        }
+        __syncthreads();
+        // round 2: dV
+        if (grp > 0) {
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) *mslot(grp, d * 16 + r) = dv[d][r];
+        }
+        __syncthreads();
+        if (grp > 0) return;
+#pragma unroll
+        for (int g = 1; g < NG; ++g)
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) dv[d][r] += *mslot(g, d * 16 + r);
+    }
     const float dl = half_sum(dlb);  // dS is the gradient of a natural-log logit, hence of its bias
     if (kvalid) {
         const int64_t ok = (int64_t)j * p.dk_st + (int64_t)head * p.dk_sh;
@@ -693,8 +829,8 @@ void set_common(DenseParams &p, float scale, float tau_win, float win_edge) {
 
 template <typename DT>
 hipError_t dense_fwd_dt(const DenseParams &p, int D, hipStream_t stream) {
-    if (D == 64) hipLaunchKernelGGL((dense_fwd_kernel<DT, 64>), dim3(p.grid), dim3(64 * kDW), 0, stream, p);
-    else hipLaunchKernelGGL((dense_fwd_kernel<DT, 128>), dim3(p.grid), dim3(64 * kDW), 0, stream, p);
+    if (D == 64) hipLaunchKernelGGL((dense_fwd_kernel<DT, 64>), dim3(p.grid), dim3(128 * dense_fwd_groups(64)), 0, stream, p);
+    else hipLaunchKernelGGL((dense_fwd_kernel<DT, 128>), dim3(p.grid), dim3(128 * dense_fwd_groups(128)), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -703,11 +839,11 @@ hipError_t dense_bwd_dt(const DenseParams &p, int D, hipStream_t stream) {
     const int64_t n = (int64_t)p.T * p.H;
     hipLaunchKernelGGL((dense_prep_kernel<DT>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p, D);
     if (D == 64) {
-        hipLaunchKernelGGL((dense_dq_kernel<DT, 64>), dim3(p.grid), dim3(64 * kDW), 0, stream, p);
-        hipLaunchKernelGGL((dense_kv_kernel<DT, 64>), dim3(p.grid), dim3(64 * kDW), 0, stream, p);
+        hipLaunchKernelGGL((dense_dq_kernel<DT, 64>), dim3(p.grid), dim3(128 * dense_bwd_groups(64)), 0, stream, p);
+        hipLaunchKernelGGL((dense_kv_kernel<DT, 64>), dim3(p.grid), dim3(128 * dense_bwd_groups(64)), 0, stream, p);
     } else {
-        hipLaunchKernelGGL((dense_dq_kernel<DT, 128>), dim3(p.grid), dim3(64 * kDW), 0, stream, p);
-        hipLaunchKernelGGL((dense_kv_kernel<DT, 128>), dim3(p.grid), dim3(64 * kDW), 0, stream, p);
+        hipLaunchKernelGGL((dense_dq_kernel<DT, 128>), dim3(p.grid), dim3(128 * dense_bwd_groups(128)), 0, stream, p);
+        hipLaunchKernelGGL((dense_kv_kernel<DT, 128>), dim3(p.grid), dim3(128 * dense_bwd_groups(128)), 0, stream, p);
     }
     if (p.d_w) hipLaunchKernelGGL(dense_dw_kernel, dim3((p.T + 255) / 256), dim3(256), 0, stream, p);
     return hipGetLastError();
