@@ -361,10 +361,10 @@ def measure_front_end(wl, w, cu, sel) -> dict:
 
     def gemm_path():
         s, _, _ = hybrid_scores_per_head(xb, Wb, alpha, H, D)
-        _hip.select_landmarks(s, w, cu, k)
+        _hip.select_landmarks(s, w, cu, k, max_seqlen=wl["L"])
 
     scores = _hip.ScoresLauncher(xb, vb, alpha, H)
-    sel_f = _hip.SelectLauncher(scores.scores, w, cu, k)
+    sel_f = _hip.SelectLauncher(scores.scores, w, cu, k, max_seqlen=wl["L"])
 
     def fused_path():
         scores()
@@ -548,7 +548,7 @@ def main():
         mod = wl["mod"]
         scores, _, _ = hybrid_scores_per_head(wl["xp"], mod.v_proj.weight, mod._alpha().float(), H, D)
         w_cont = mod._window_continuous(wl["xp"]).float()
-    sel = _hip.SelectLauncher(scores, w, cu, wl["k_lmk"])
+    sel = _hip.SelectLauncher(scores, w, cu, wl["k_lmk"], max_seqlen=wl["L"])
     sel_ms = time_graph(sel)
     qz_ms = time_graph(_hip.QuantizeLauncher(w_cont))
     bytes_sel = 4 * T * H + 4 * T + 4 * (wl["B"] + 1) + 8 * H * wl["B"] * wl["k_lmk"]

@@ -189,7 +189,19 @@ int dsalt_select_check(const dsalt_select_args *a) {
         return fail(DSALT_ERR_INVALID, "scores, w, cu_seqlens and lmk_pos must be non-NULL");
     if ((int64_t)a->num_seqs * a->n_heads > (int64_t)INT32_MAX)
         return fail(DSALT_ERR_UNSUPPORTED, "too many (head, sequence) pairs");
+    if (a->max_seqlen < 0) return fail(DSALT_ERR_INVALID, "max_seqlen must be >= 0 (0: unknown)");
+    if (a->workspace) {
+        const int64_t need = dsalt::select_workspace_bytes(a->total_len, a->num_seqs, a->n_heads, a->k_lmk);
+        if (a->workspace_bytes < need || !aligned(a->workspace, 16))
+            return fail(DSALT_ERR_INVALID, "select workspace needs %lld bytes, 16-byte aligned (got %lld)",
+                        (long long)need, (long long)a->workspace_bytes);
+    }
     return DSALT_OK;
+}
+
+int64_t dsalt_select_workspace_size(int32_t total_len, int32_t num_seqs, int32_t n_heads, int32_t k_lmk) {
+    if (total_len < 0 || num_seqs < 1 || n_heads < 1 || k_lmk < 0 || k_lmk > DSALT_MAX_K_LMK) return -1;
+    return dsalt::select_workspace_bytes(total_len, num_seqs, n_heads, k_lmk);
 }
 
 int dsalt_select_landmarks(const dsalt_select_args *a, void *stream) {

@@ -27,6 +27,7 @@ constexpr int fwd_ring(int head_dim) { return head_dim == 64 ? 2 : 3; }  // K / 
 hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream);
 hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream);
 hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream);
+int64_t select_workspace_bytes(int total_len, int num_seqs, int n_heads, int k);
 hipError_t launch_rope(const dsalt_rope_args &a, hipStream_t stream);
 hipError_t launch_scores(const dsalt_scores_args &a, hipStream_t stream);
 int64_t scores_workspace_bytes(int total_len, int n_kv);

@@ -6,21 +6,29 @@
 // quantisation is DSALTAttention._window_sizes(floor=True) / the floor+clamp of
 // _train_selectors (dsalt/modules/dsalt_attention.py:277-284, :471).
 //
-// Design: one 1024-thread workgroup per (head, sequence).
+// Design: a 1024-thread workgroup selects the top k_eff of n items (select_block):
 //  * Each score becomes a 32-bit key whose unsigned order is the score order
 //    (NaN > +inf > finite > ..., -0 folded onto +0); covered tokens and -inf get key 0,
-//    which marks "not a candidate". Keys are cached in LDS for L <= 16384.
+//    which marks "not a candidate". Keys are cached in LDS for n <= 16384.
 //  * If more than k_eff candidates exist, an MSB-first radix select over key - min_key
 //    (8-bit digits starting at the top bit of the candidates' key range, so that the
 //    first LDS histogram is not concentrated on a few exponent values; one wave scans
 //    the 256 bins) finds the exact k_eff-th key `thr` and how many keys equal to it are
 //    still needed. A pass whose boundary bin holds exactly the keys still needed ends the
 //    search: the selection is then every key at or above that bin's lower bound.
-//  * A final ordered pass emits the selected positions in ascending order: each thread
-//    owns a contiguous run of positions, and one workgroup scan of (finite keys > thr,
-//    keys == thr) gives every thread its first output slot. Keys == thr are taken by
-//    position (ties: lower position wins). NaN/+inf picks occupy their slot but are not
-//    emitted; every slot after the last emitted one is -1.
+//  * A final ordered pass emits the selected items in ascending order: each thread owns
+//    a contiguous run of items, and one workgroup scan of (keys > thr, keys == thr) gives
+//    every thread its first output slot. Keys == thr are taken in item order (ties: lower
+//    item wins). Final selections skip NaN/+inf picks (they occupy their slot but are not
+//    emitted; every slot after the last emitted one is -1).
+// The selection is the top k_eff under the total order (key descending, position
+// ascending). Short sequences (L <= kSplitMin) take one workgroup per (head, sequence)
+// over the scores. Longer ones, when the caller passes a workspace, first take one
+// workgroup per 2048-position chunk (select_chunk_kernel: the chunk's own top k_eff,
+// non-finite picks included, written as (key, position) candidates in position order):
+// the global top k_eff is contained in the union of the chunks' (an item ranked above
+// another globally is ranked above it in its chunk too). select_kernel then selects
+// from the candidates, concatenated in chunk order (hence in position order).
 // Fully deterministic; integer-exact with respect to the fp32 scores.
 #include "common.h"
 #include "launch.h"
@@ -32,6 +40,18 @@ constexpr int kSelThreads = 1024;
 constexpr int kSelWaves = kSelThreads / 64;
 constexpr int kSelCache = 16384;               // keys cached in LDS (64 KB)
 constexpr uint32_t kKeyPosInf = 0xFF800000u;   // key of +inf; finite keys are below it
+constexpr int kSelChunk = 2048;                // positions per chunk of a long sequence
+constexpr int kSplitMin = 4096;                // longer sequences are selected chunk-wise
+constexpr int kMergeCap = 8192;                // candidates a final selection may gather
+constexpr int kMaxChunks = 512;                // chunks of one chunk-wise selected sequence
+static_assert(2 * kMergeCap <= kSelCache, "candidate keys and positions share the key cache");
+
+// Whether a sequence of length L is selected chunk-wise (when a workspace is given): its
+// chunks' candidates must fit the final workgroup's LDS.
+__host__ __device__ inline bool split_sequence(int L, int k) {
+    const int nch = (L + kSelChunk - 1) / kSelChunk;
+    return L > kSplitMin && nch <= kMaxChunks && (int64_t)nch * k <= kMergeCap;
+}
 
 struct SelParams {
     const float *scores;
@@ -41,6 +61,11 @@ struct SelParams {
     const int32_t *cu;
     int64_t *out;
     int num_seqs, n_heads, k;
+    // chunked selection of long sequences (null ws_key: one workgroup per (head, sequence))
+    uint32_t *ws_key;  // [H][n_chunk_ub][k] candidate keys
+    int32_t *ws_pos;   // [H][n_chunk_ub][k] candidate positions (relative to the sequence)
+    int32_t *ws_cnt;   // [H][n_chunk_ub] candidates per chunk
+    int n_chunk_ub;
 };
 
 // Order-preserving 32-bit key of an fp32 score (unsigned order = score order).
@@ -91,44 +116,36 @@ __device__ __forceinline__ void block_excl_scan2(int a, int b, int lane, int wav
     eb = ob + ib - b;
 }
 
-// One workgroup of 1024 threads per (head, sequence). The key pass and the histogram
-// passes stride over positions (j = tid + 1024 i: coalesced loads, conflict-free LDS);
-// for the emission thread t owns the contiguous positions [t*C, t*C + C)
-// (C = ceil(L / 1024)), which keeps the output in position order with one workgroup scan.
-__global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) {
-    __shared__ uint32_t s_keys[kSelCache];
-    __shared__ int s_hist[2][256];  // double-buffered: pass n clears the buffer of pass n + 1
-    __shared__ int s_w[kSelWaves][2];
-    __shared__ int s_cnt[kSelWaves];  // written once: its readers need no trailing barrier
-    __shared__ uint32_t s_mm[kSelWaves][2];
-    __shared__ int s_bc[3];
+struct SelShared {
+    uint32_t keys[kSelCache];
+    int hist[2][256];  // double-buffered: pass n clears the buffer of pass n + 1
+    int w[kSelWaves][2];
+    int cnt[kSelWaves];  // written once: its readers need no trailing barrier
+    uint32_t mm[kSelWaves][2];
+    int bc[3];
+};
 
+// The top k_eff of items 0 .. n-1 of key key_of(j) (0: not a candidate), emitted as
+// emit(slot, j, key) in ascending item order. The key pass and the histogram passes stride
+// over items (j = tid + 1024 i: coalesced loads, conflict-free LDS); for the emission
+// thread t owns the contiguous items [t*C, t*C + C) (C = ceil(n / 1024)), which keeps
+// the output in item order with one workgroup scan. `all` emits NaN/+inf picks too (for
+// candidates); otherwise they only count towards k_eff. Returns the number of slots
+// emitted. Every thread of the workgroup calls it; `sh` is the workgroup's LDS.
+template <class KeyFn, class EmitFn>
+__device__ __forceinline__ int select_block(SelShared &sh, int n, int k_eff, bool all, KeyFn key_of, EmitFn emit) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int head = blockIdx.x / p.num_seqs;
-    const int seq = blockIdx.x - head * p.num_seqs;
-    const int start = p.cu[seq];
-    const int L = p.cu[seq + 1] - start;
-    int64_t *out = p.out + ((int64_t)head * p.num_seqs + seq) * p.k;
-    const int k_eff = min(p.k, max(L, 0));
-    const bool cached = L <= kSelCache;
-    const int C = (max(L, 0) + kSelThreads - 1) / kSelThreads;
-    const int j0 = tid * C, j1 = min(j0 + C, max(L, 0));
-
-    auto make_key = [&](int j) -> uint32_t {
-        const int64_t tok = (int64_t)start + j;
-        const float wj = p.w[tok * p.w_st];
-        // covered <=> j < trunc(w_j) <=> j + 1 <= w_j   (j >= 0 integer)
-        if ((float)(j + 1) <= wj) return 0u;
-        return order_key(p.scores[tok * p.sc_st + (int64_t)head * p.sc_sh]);
-    };
-    auto key_at = [&](int j) -> uint32_t { return cached ? s_keys[j] : make_key(j); };
+    const bool cached = n <= kSelCache;
+    const int C = (max(n, 0) + kSelThreads - 1) / kSelThreads;
+    const int j0 = tid * C, j1 = min(j0 + C, max(n, 0));
+    auto key_at = [&](int j) -> uint32_t { return cached ? sh.keys[j] : key_of(j); };
 
     // pass 0: keys, candidate count and the candidates' key range
     int cnt = 0;
     uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
-    for (int j = tid; j < L; j += kSelThreads) {
-        const uint32_t key = make_key(j);
-        if (cached) s_keys[j] = key;
+    for (int j = tid; j < n; j += kSelThreads) {
+        const uint32_t key = key_of(j);
+        if (cached) sh.keys[j] = key;
         if (key != 0u) {
             ++cnt;
             kmin = min(kmin, key);
@@ -138,21 +155,21 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
     kmin = (uint32_t)wave_min_u((int)(kmin ^ 0x80000000u)) ^ 0x80000000u;  // unsigned via sign flip
     kmax = (uint32_t)wave_max_u((int)(kmax ^ 0x80000000u)) ^ 0x80000000u;
     if (lane == 0) {
-        s_mm[wave][0] = kmin;
-        s_mm[wave][1] = kmax;
+        sh.mm[wave][0] = kmin;
+        sh.mm[wave][1] = kmax;
     }
     // candidate count and key range: per-wave values, one barrier (which also publishes
-    // the cleared histogram of the first pass); s_cnt and s_mm are never rewritten
+    // the cleared histogram of the first pass); cnt and mm are never rewritten
     cnt = wave_sum_u(cnt);
-    if (lane == 0) s_cnt[wave] = cnt;
-    if (tid < 256) s_hist[0][tid] = 0;
+    if (lane == 0) sh.cnt[wave] = cnt;
+    if (tid < 256) sh.hist[0][tid] = 0;
     __syncthreads();
     int ncand = 0;
 #pragma unroll
     for (int w = 0; w < kSelWaves; ++w) {
-        ncand += s_cnt[w];
-        kmin = min(kmin, s_mm[w][0]);
-        kmax = max(kmax, s_mm[w][1]);
+        ncand += sh.cnt[w];
+        kmin = min(kmin, sh.mm[w][0]);
+        kmax = max(kmax, sh.mm[w][1]);
     }
 
     uint32_t thr = 0u;  // select key > thr, plus the first need_eq keys == thr
@@ -165,16 +182,16 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
         uint32_t prefix = 0u, pmask = 0u;
         int remaining = k_eff, buf = 0;
         for (int shift = max(nbits - 8, 0);; shift = max(shift - 8, 0)) {
-            // s_hist[buf] is zero here (cleared before the previous barrier)
-            int *hist = s_hist[buf];
-            for (int j = tid; j < L; j += kSelThreads) {
+            // hist[buf] is zero here (cleared before the previous barrier)
+            int *hist = sh.hist[buf];
+            for (int j = tid; j < n; j += kSelThreads) {
                 const uint32_t key = key_at(j);
                 const uint32_t rel = key - kmin;
                 if (key != 0u && (rel & pmask) == prefix) atomicAdd(&hist[(rel >> shift) & 255u], 1);
             }
             __syncthreads();
-            if (wave == 1) s_hist[buf ^ 1][lane * 4 + 0] = s_hist[buf ^ 1][lane * 4 + 1] =
-                s_hist[buf ^ 1][lane * 4 + 2] = s_hist[buf ^ 1][lane * 4 + 3] = 0;  // next pass
+            if (wave == 1) sh.hist[buf ^ 1][lane * 4 + 0] = sh.hist[buf ^ 1][lane * 4 + 1] =
+                sh.hist[buf ^ 1][lane * 4 + 2] = sh.hist[buf ^ 1][lane * 4 + 3] = 0;  // next pass
             if (wave == 0) {
                 // lane covers digits 255-4*lane .. 252-4*lane (descending)
                 const int c0 = hist[255 - 4 * lane], c1 = hist[254 - 4 * lane];
@@ -198,21 +215,21 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
                         d = 252 - 4 * lane;
                         cd = c3;
                     }
-                    s_bc[0] = d;
-                    s_bc[1] = cum;  // keys in the prefix with a larger digit
-                    s_bc[2] = cd;   // keys in the prefix with digit d
+                    sh.bc[0] = d;
+                    sh.bc[1] = cum;  // keys in the prefix with a larger digit
+                    sh.bc[2] = cd;   // keys in the prefix with digit d
                 }
             }
             __syncthreads();
-            prefix |= (uint32_t)s_bc[0] << shift;
+            prefix |= (uint32_t)sh.bc[0] << shift;
             pmask |= 0xFFu << shift;
-            remaining -= s_bc[1];
+            remaining -= sh.bc[1];
             // every key of the chosen bin is needed: the selection is exactly the keys
             // with rel >= prefix (the bin and everything above it), whatever the lower
             // digits are - the passes for them are skipped
-            const bool whole_bin = s_bc[2] == remaining;
+            const bool whole_bin = sh.bc[2] == remaining;
             buf ^= 1;
-            // no barrier here: s_bc is rewritten only after the next pass's histogram
+            // no barrier here: bc is rewritten only after the next pass's histogram
             // barrier, which every thread reaches after this read
             if (whole_bin) {
                 thr = kmin + prefix - 1u;  // kmin >= 1: thr >= 0 and key 0 is never taken
@@ -227,37 +244,128 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
         }
     }
 
-    // ordered emission: emitted slots before this thread = finite keys > thr before it plus
-    // the equal keys selected before it (equal keys are selected in position order)
-    if (k_eff > 0) {
-        int n_gt = 0, n_eq = 0;
-        for (int j = j0; j < j1; ++j) {
-            const uint32_t key = key_at(j);
-            n_gt += (key > thr) && (key < kKeyPosInf);
-            n_eq += (need_eq > 0) && (key == thr);
-        }
-        int gt_before, eq_before, gt_tot, eq_tot;
-        block_excl_scan2(n_gt, n_eq, lane, wave, s_w, gt_before, eq_before, gt_tot, eq_tot);
-        const bool thr_finite = thr < kKeyPosInf;
-        int slot = gt_before + (thr_finite ? min(eq_before, need_eq) : 0);
-        int eq_rank = eq_before;
-        for (int j = j0; j < j1; ++j) {
-            const uint32_t key = key_at(j);
-            bool emit = (key > thr) && (key < kKeyPosInf);
-            if ((need_eq > 0) && (key == thr)) {
-                emit = thr_finite && eq_rank < need_eq;
-                ++eq_rank;
-            }
-            if (emit) {
-                if (slot < p.k) out[slot] = j;
-                ++slot;
-            }
-        }
-        const int total = gt_tot + (thr_finite ? min(eq_tot, need_eq) : 0);
-        for (int s2 = total + tid; s2 < p.k; s2 += kSelThreads) out[s2] = -1;
-    } else {
-        for (int s2 = tid; s2 < p.k; s2 += kSelThreads) out[s2] = -1;
+    // ordered emission: emitted slots before this thread = emitted keys > thr before it
+    // plus the equal keys selected before it (equal keys are selected in item order)
+    if (k_eff <= 0) return 0;
+    const bool eq_ok = all || thr < kKeyPosInf;  // equal keys emitted (not NaN / +inf finals)
+    auto is_gt = [&](uint32_t key) { return key > thr && (all || key < kKeyPosInf); };
+    int n_gt = 0, n_eq = 0;
+    for (int j = j0; j < j1; ++j) {
+        const uint32_t key = key_at(j);
+        n_gt += is_gt(key);
+        n_eq += (need_eq > 0) && (key == thr);
     }
+    int gt_before, eq_before, gt_tot, eq_tot;
+    block_excl_scan2(n_gt, n_eq, lane, wave, sh.w, gt_before, eq_before, gt_tot, eq_tot);
+    int slot = gt_before + (eq_ok ? min(eq_before, need_eq) : 0);
+    int eq_rank = eq_before;
+    for (int j = j0; j < j1; ++j) {
+        const uint32_t key = key_at(j);
+        bool take = is_gt(key);
+        if ((need_eq > 0) && (key == thr)) {
+            take = eq_ok && eq_rank < need_eq;
+            ++eq_rank;
+        }
+        if (take) {
+            emit(slot, j, key);
+            ++slot;
+        }
+    }
+    return gt_tot + (eq_ok ? min(eq_tot, need_eq) : 0);
+}
+
+// Chunks of long sequences (L > kSplitMin): one workgroup per (head, chunk id of
+// find_block over kSelChunk-position chunks); candidates of the chunk to the workspace.
+__global__ void __launch_bounds__(kSelThreads) select_chunk_kernel(const SelParams p) {
+    __shared__ SelShared sh;
+    const int lane = threadIdx.x & 63;
+    const int head = blockIdx.x / p.n_chunk_ub;
+    const int cid = blockIdx.x - head * p.n_chunk_ub;
+    int seq, chunk, start, L;
+    if (!find_block(p.cu, p.num_seqs, cid, kSelChunk, lane, seq, chunk, start, L)) return;
+    if (!split_sequence(L, p.k)) return;  // selected from the scores by select_kernel
+    const int c0 = chunk * kSelChunk;
+    const int n = min(kSelChunk, L - c0);
+    const int k_eff = min(p.k, L);
+    uint32_t *ck = p.ws_key + ((int64_t)head * p.n_chunk_ub + cid) * p.k;
+    int32_t *cp = p.ws_pos + ((int64_t)head * p.n_chunk_ub + cid) * p.k;
+    auto key_of = [&](int j) -> uint32_t {
+        const int pos = c0 + j;
+        const int64_t tok = (int64_t)start + pos;
+        // covered <=> pos < trunc(w_pos) <=> pos + 1 <= w_pos   (pos >= 0 integer)
+        if ((float)(pos + 1) <= p.w[tok * p.w_st]) return 0u;
+        return order_key(p.scores[tok * p.sc_st + (int64_t)head * p.sc_sh]);
+    };
+    auto emit = [&](int slot, int j, uint32_t key) {
+        if (slot < p.k) {
+            ck[slot] = key;
+            cp[slot] = c0 + j;
+        }
+    };
+    const int total = select_block(sh, n, min(k_eff, n), true, key_of, emit);
+    if (threadIdx.x == 0) p.ws_cnt[(int64_t)head * p.n_chunk_ub + cid] = min(total, p.k);
+}
+
+// One workgroup per (head, sequence): the final selection, from the scores or (long
+// sequences with a workspace) from the chunks' candidates.
+__global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) {
+    __shared__ SelShared sh;
+    __shared__ int s_off[kMaxChunks + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int head = blockIdx.x / p.num_seqs;
+    const int seq = blockIdx.x - head * p.num_seqs;
+    const int start = p.cu[seq];
+    const int L = max(p.cu[seq + 1] - start, 0);
+    int64_t *out = p.out + ((int64_t)head * p.num_seqs + seq) * p.k;
+    const int k_eff = min(p.k, L);
+    int total;
+    if (p.ws_key && split_sequence(L, p.k)) {
+        // the chunks' candidates in chunk order: keys into sh.keys[0, n), positions into
+        // s_pos = sh.keys[kMergeCap, 2 kMergeCap) (select_block caches only keys[0, n))
+        int32_t *s_pos = reinterpret_cast<int32_t *>(sh.keys + kMergeCap);
+        const int cid0 = start / kSelChunk + seq, nch = (L + kSelChunk - 1) / kSelChunk;
+        const int64_t cbase = (int64_t)head * p.n_chunk_ub + cid0;
+        if (wave == 0) {  // offsets of the chunks' runs (nch <= kMaxChunks)
+            int run = 0;
+            for (int c0 = 0; c0 < nch; c0 += 64) {
+                const int c = c0 + lane;
+                const int v = c < nch ? p.ws_cnt[cbase + c] : 0;
+                const int incl = wave_incl_scan_dpp(v);
+                if (c < nch) s_off[c] = run + incl - v;
+                run += __builtin_amdgcn_readlane(incl, 63);
+            }
+            if (lane == 0) s_off[nch] = run;
+        }
+        __syncthreads();
+        const int n = s_off[nch];
+        for (int c = wave; c < nch; c += kSelWaves) {
+            const int off = s_off[c], cnt = s_off[c + 1] - off;
+            for (int e = lane; e < cnt; e += 64) {
+                sh.keys[off + e] = p.ws_key[(cbase + c) * p.k + e];
+                s_pos[off + e] = p.ws_pos[(cbase + c) * p.k + e];
+            }
+        }
+        __syncthreads();
+        // keys are read back from sh.keys (n <= kMergeCap <= kSelCache: the pass-0 copy
+        // onto itself is harmless)
+        auto key_of = [&](int j) -> uint32_t { return sh.keys[j]; };
+        auto emit = [&](int slot, int j, uint32_t) {
+            if (slot < p.k) out[slot] = s_pos[j];
+        };
+        total = select_block(sh, n, k_eff, false, key_of, emit);
+    } else {
+        auto key_of = [&](int j) -> uint32_t {
+            const int64_t tok = (int64_t)start + j;
+            // covered <=> j < trunc(w_j) <=> j + 1 <= w_j   (j >= 0 integer)
+            if ((float)(j + 1) <= p.w[tok * p.w_st]) return 0u;
+            return order_key(p.scores[tok * p.sc_st + (int64_t)head * p.sc_sh]);
+        };
+        auto emit = [&](int slot, int j, uint32_t) {
+            if (slot < p.k) out[slot] = j;
+        };
+        total = select_block(sh, L, k_eff, false, key_of, emit);
+    }
+    for (int s2 = total + tid; s2 < p.k; s2 += kSelThreads) out[s2] = -1;
 }
 
 __global__ void quantize_kernel(const float *__restrict__ w, int64_t n, float *__restrict__ wq,
@@ -272,6 +380,15 @@ __global__ void quantize_kernel(const float *__restrict__ w, int64_t n, float *_
 
 }  // namespace
 
+// Workspace of the chunk-wise selection: per (head, chunk id) k candidate keys, k
+// positions and a count.
+int64_t select_workspace_bytes(int total_len, int num_seqs, int n_heads, int k) {
+    if (total_len <= kSplitMin || k == 0) return 0;
+    auto al = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
+    const int64_t n = (int64_t)n_heads * block_upper_bound(total_len, num_seqs, kSelChunk);
+    return 2 * al(n * k * 4) + al(n * 4);
+}
+
 hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream) {
     if (a.k_lmk == 0) return hipSuccess;
     SelParams p;
@@ -285,6 +402,20 @@ hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream) {
     p.num_seqs = a.num_seqs;
     p.n_heads = a.n_heads;
     p.k = a.k_lmk;
+    p.ws_key = nullptr;
+    p.ws_pos = nullptr;
+    p.ws_cnt = nullptr;
+    p.n_chunk_ub = block_upper_bound(a.total_len, a.num_seqs, kSelChunk);
+    const int64_t need = select_workspace_bytes(a.total_len, a.num_seqs, a.n_heads, a.k_lmk);
+    if (a.workspace && need > 0 && (a.max_seqlen <= 0 || a.max_seqlen > kSplitMin)) {
+        const int64_t n = (int64_t)a.n_heads * p.n_chunk_ub;
+        const int64_t part = (n * a.k_lmk * 4 + 255) & ~(int64_t)255;
+        char *ws = static_cast<char *>(a.workspace);
+        p.ws_key = reinterpret_cast<uint32_t *>(ws);
+        p.ws_pos = reinterpret_cast<int32_t *>(ws + part);
+        p.ws_cnt = reinterpret_cast<int32_t *>(ws + 2 * part);
+        hipLaunchKernelGGL(select_chunk_kernel, dim3((unsigned)n), dim3(kSelThreads), 0, stream, p);
+    }
     hipLaunchKernelGGL(select_kernel, dim3(a.num_seqs * a.n_heads), dim3(kSelThreads), 0, stream, p);
     return hipGetLastError();
 }

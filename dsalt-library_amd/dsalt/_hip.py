@@ -88,6 +88,8 @@ class SelectArgs(ctypes.Structure):
         ("w", c_void_p), ("w_stride", c_int64),
         ("cu_seqlens", c_void_p),
         ("lmk_pos", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_int64),
+        ("max_seqlen", c_int32),
     ]
 
 
@@ -124,9 +126,10 @@ EXPORTED_SYMBOLS = (
     "dsalt_abi_version", "dsalt_last_error", "dsalt_fwd_args_size", "dsalt_bwd_args_size",
     "dsalt_select_args_size", "dsalt_hybrid_scores", "dsalt_scores_check", "dsalt_scores_workspace_size",
     "dsalt_scores_args_size", "dsalt_rope", "dsalt_rope_check", "dsalt_rope_args_size",
-    "dsalt_bwd_noalloc",
+    "dsalt_bwd_noalloc", "dsalt_select_workspace_size",
 )
 NOALLOC_SCRATCH_BYTES = 128 << 20  # DSALT_NOALLOC_SCRATCH_BYTES
+SELECT_SPLIT_MIN = 4096  # longer sequences can be selected chunk-wise
 
 _lib = None
 
@@ -162,6 +165,8 @@ def lib() -> ctypes.CDLL:
     h.dsalt_bwd_workspace_size.restype = c_int64
     h.dsalt_scores_workspace_size.argtypes = [c_int32] * 2
     h.dsalt_scores_workspace_size.restype = c_int64
+    h.dsalt_select_workspace_size.argtypes = [c_int32] * 4
+    h.dsalt_select_workspace_size.restype = c_int64
     h.dsalt_abi_version.restype = ctypes.c_int
     h.dsalt_last_error.restype = ctypes.c_char_p
     for n in ("dsalt_fwd_args_size", "dsalt_bwd_args_size", "dsalt_select_args_size", "dsalt_scores_args_size",
@@ -609,25 +614,45 @@ class DenseBwdLauncher:
         _raise(self._fn(self._ref, stream_handle(self.device)), "dsalt_bwd (dense)")
 
 
-def select_landmarks(scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Tensor,
-                     k_lmk: int) -> torch.Tensor:
-    """Top-k landmark positions [H, S, k] int64 (ascending, -1 padded) from fp32 scores [T, H]."""
-    dev = require_gpu(scores, w, cu_seqlens)
+def _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen=None):
+    """The argument block of one selection and the tensors it points into. chunked:
+    pass the workspace, so that long sequences are selected chunk-wise; max_seqlen (a
+    bound on the sequence lengths, None: unknown) lets the library skip the chunk stage
+    when no sequence is long."""
     if scores.dtype != torch.float32:
         raise DsaltError(f"scores must be float32, got {scores.dtype}")
     T, H = scores.shape
-    cu = _cu_i32(cu_seqlens)
     S = cu.shape[0] - 1
-    w = _f32_vec(w)
-    out = torch.empty((H, S, k_lmk), device=dev, dtype=torch.int64)
-    if k_lmk == 0:
-        return out
     a = SelectArgs()
     a.total_len, a.num_seqs, a.n_heads, a.k_lmk = T, S, H, k_lmk
     a.scores, a.scores_stride_t, a.scores_stride_h = scores.data_ptr(), scores.stride(0), scores.stride(1)
     a.w, a.w_stride = w.data_ptr(), w.stride(0)
     a.cu_seqlens = cu.data_ptr()
     a.lmk_pos = out.data_ptr()
+    a.max_seqlen = 0 if max_seqlen is None else min(int(max_seqlen), 2**31 - 1)
+    ws = None
+    if chunked and (max_seqlen is None or max_seqlen > SELECT_SPLIT_MIN):
+        ws_bytes = lib().dsalt_select_workspace_size(T, S, H, k_lmk)
+        if ws_bytes < 0:
+            raise DsaltError(f"dsalt_select_workspace_size: invalid shape (T={T}, S={S}, H={H}, k={k_lmk})")
+        if ws_bytes > 0:
+            ws = torch.empty(ws_bytes, device=scores.device, dtype=torch.uint8)
+            a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
+    return a, (scores, w, cu, out, ws)
+
+
+def select_landmarks(scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Tensor,
+                     k_lmk: int, chunked: bool = True, max_seqlen: int | None = None) -> torch.Tensor:
+    """Top-k landmark positions [H, S, k] int64 (ascending, -1 padded) from fp32 scores [T, H].
+    chunked=False selects every sequence with one workgroup per (head, sequence);
+    max_seqlen: a bound on the sequence lengths when the caller knows one (None: unknown)."""
+    dev = require_gpu(scores, w, cu_seqlens)
+    cu = _cu_i32(cu_seqlens)
+    w = _f32_vec(w)
+    out = torch.empty((scores.shape[1], cu.shape[0] - 1, k_lmk), device=dev, dtype=torch.int64)
+    if k_lmk == 0:
+        return out
+    a, _keep = _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen)
     _raise(lib().dsalt_select_landmarks(ctypes.byref(a), stream_handle(dev)), "dsalt_select_landmarks")
     return out
 
@@ -772,24 +797,13 @@ class SelectLauncher:
     """select_landmarks with its argument block built once: each call launches the
     selection kernel on the current stream (for timing loops); `out` holds the result."""
 
-    def __init__(self, scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Tensor, k_lmk: int):
+    def __init__(self, scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Tensor, k_lmk: int,
+                 chunked: bool = True, max_seqlen: int | None = None):
         self.device = require_gpu(scores, w, cu_seqlens)
-        if scores.dtype != torch.float32:
-            raise DsaltError(f"scores must be float32, got {scores.dtype}")
-        T, H = scores.shape
-        self._cu = _cu_i32(cu_seqlens)
-        self._w = _f32_vec(w)
-        self._scores = scores
-        S = self._cu.shape[0] - 1
-        self.out = torch.empty((H, S, k_lmk), device=self.device, dtype=torch.int64)
-        a = SelectArgs()
-        a.total_len, a.num_seqs, a.n_heads, a.k_lmk = T, S, H, k_lmk
-        a.scores, a.scores_stride_t, a.scores_stride_h = scores.data_ptr(), scores.stride(0), scores.stride(1)
-        a.w, a.w_stride = self._w.data_ptr(), self._w.stride(0)
-        a.cu_seqlens = self._cu.data_ptr()
-        a.lmk_pos = self.out.data_ptr()
-        self._args = a
-        self._ref = ctypes.byref(a)
+        cu = _cu_i32(cu_seqlens)
+        self.out = torch.empty((scores.shape[1], cu.shape[0] - 1, k_lmk), device=self.device, dtype=torch.int64)
+        self._args, self._keep = _select_args(scores, _f32_vec(w), cu, k_lmk, self.out, chunked, max_seqlen)
+        self._ref = ctypes.byref(self._args)
         self._fn = lib().dsalt_select_landmarks
 
     def __call__(self) -> None:

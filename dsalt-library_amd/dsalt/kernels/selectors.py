@@ -126,7 +126,8 @@ def _compute_landmark_indices(
     dh = head_dim if head_dim is not None else W_V.shape[0] // n_heads
     with torch.no_grad():
         scores, z_x, z_v = selection_scores(x, W_V, alpha, n_heads, dh, v, hip_scores)
-        lmk = _hip.select_landmarks(scores.float(), w_sizes, cu_seqlens, int(k_lmk))
+        max_len = None if cu_list is None else max((b - a for a, b in zip(cu_list[:-1], cu_list[1:])), default=0)
+        lmk = _hip.select_landmarks(scores.float(), w_sizes, cu_seqlens, int(k_lmk), max_seqlen=max_len)
     return lmk, z_x, z_v
 
 

@@ -217,7 +217,7 @@ class DSALTAttention(nn.Module):
         with torch.no_grad():
             cu = torch.tensor([0, T], dtype=torch.int32, device=device)
             lmk_pos = _hip.select_landmarks(scores.detach().float().contiguous(),
-                                            torch.zeros(T, device=device), cu, k_act)
+                                            torch.zeros(T, device=device), cu, k_act, max_seqlen=T)
             sel = torch.zeros(self.n_heads, T + 1, dtype=torch.bool, device=device)
             sel.scatter_(1, torch.where(lmk_pos[:, 0] >= 0, lmk_pos[:, 0], T), True)
             sel = sel[:, :T]

@@ -212,6 +212,14 @@ int dsalt_bwd_noalloc(const dsalt_bwd_args *args, void *stream);
  * ranks above every finite score; equal scores: the lower position wins). Selected
  * finite-score positions are written in ascending order, followed by -1 in every
  * remaining slot (the reference's -inf/NaN/+inf slots also become -1).
+ * workspace (optional, NULL allowed): with at least dsalt_select_workspace_size(...)
+ * bytes, sequences longer than 4096 tokens (with ceil(L / 2048) * k <= 8192) are
+ * selected in two stages - the top k of every 2048-position chunk by one workgroup each,
+ * then the top k of the chunks' candidates - instead of by one workgroup per (head,
+ * sequence). The result is identical; the workspace only adds parallelism. A size of 0
+ * means no sequence can use it. max_seqlen: 0, or a bound on every sequence's length
+ * (the chunk stage is skipped when it is <= 4096, saving its launch when no sequence is
+ * long; a bound that is too small only means the one-workgroup route for everything).
  */
 typedef struct dsalt_select_args {
     int32_t total_len, num_seqs, n_heads, k_lmk;
@@ -221,8 +229,12 @@ typedef struct dsalt_select_args {
     int64_t w_stride;
     const int32_t *cu_seqlens;
     int64_t *lmk_pos; /* out: [H, S, k] contiguous int64 */
+    void *workspace;  /* NULL, or >= dsalt_select_workspace_size(...) bytes, 16-byte aligned */
+    int64_t workspace_bytes;
+    int32_t max_seqlen; /* 0 (unknown) or an upper bound on the sequence lengths */
 } dsalt_select_args;
 
+int64_t dsalt_select_workspace_size(int32_t total_len, int32_t num_seqs, int32_t n_heads, int32_t k_lmk);
 int dsalt_select_landmarks(const dsalt_select_args *args, void *stream);
 int dsalt_select_check(const dsalt_select_args *args);
 

@@ -270,6 +270,58 @@ def test_select_strided_scores():
     np.testing.assert_array_equal(got.cpu().numpy(), orc.select_landmarks(scores, w, cu, 9))
 
 
+def _select_gpu(scores, w, cu, k, chunked=True):
+    dev = torch.device("cuda", 0)
+    return hip.select_landmarks(torch.from_numpy(scores).to(dev), torch.from_numpy(w).to(dev),
+                                torch.from_numpy(cu).to(torch.int32).to(dev), k, chunked=chunked).cpu().numpy()
+
+
+@pytest.mark.parametrize("lens,H,k", [
+    ([4097, 6000, 50, 16384], 2, 64),      # just past the chunk-wise threshold, ragged last chunks
+    ([8193, 4096, 12000], 3, 1),
+    ([6000, 16384], 2, 1024),              # 8 chunks x 1024 candidates: the gather's capacity
+    ([20000, 5000], 2, 1024),              # 10 x 1024 > capacity: one workgroup per sequence
+    ([300, 4500, 7, 9000], 2, 128),
+])
+@pytest.mark.parametrize("tie", [True, False], ids=["ties", "distinct"])
+def test_select_chunked_bit_exact(lens, H, k, tie):
+    """Sequences longer than 4096 tokens go through the per-chunk top-k and the top-k of
+    the chunks' candidates; same bar as the single-workgroup path: the oracle exactly."""
+    print(f"select chunked lens={lens} H={H} k={k} tie={tie}", flush=True)
+    scores, w, cu = _select_case(sum(lens) % 997 + k, lens, H, tie)
+    np.testing.assert_array_equal(_select_gpu(scores, w, cu, k), orc.select_landmarks(scores, w, cu, k))
+
+
+def test_select_chunked_concentrated_and_tied():
+    """The top k all in one chunk (ascending scores: the last chunk supplies every pick,
+    the others candidates that lose), one cluster of equal scores spanning every chunk
+    (ties across chunk boundaries go to the lower position), and windows that cover
+    most of a chunk (chunks with fewer than k candidates)."""
+    lens, H, k = [10000, 9000, 6000], 3, 128
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    T = int(cu[-1])
+    scores = np.zeros((T, H), np.float32)
+    w = np.zeros(T, np.float32)
+    for s, (s0, L) in enumerate(zip(cu[:-1], lens)):
+        off = np.arange(L, dtype=np.float32)
+        scores[s0:s0 + L, 0] = off                       # ascending
+        scores[s0:s0 + L, 1] = 2.0                       # one cluster of ties
+        scores[s0:s0 + L, 2] = -off                      # descending (first chunk wins)
+        if s == 2:
+            w[s0:s0 + L] = np.where(off < 4000, off + 1.0, 0.0)  # first 4000 tokens: every key covered
+    np.testing.assert_array_equal(_select_gpu(scores, w, cu, k), orc.select_landmarks(scores, w, cu, k))
+
+
+def test_select_chunked_equals_single_workgroup_c4():
+    """Config 4's selection shape (one 16384-token sequence, 16 heads, k = 128): the
+    chunk-wise and the single-workgroup selections agree bit for bit, and with the oracle."""
+    print("select c4 chunked vs single", flush=True)
+    scores, w, cu = _select_case(44, [16384], 16, tie=False)
+    got = _select_gpu(scores, w, cu, 128)
+    np.testing.assert_array_equal(got, _select_gpu(scores, w, cu, 128, chunked=False))
+    np.testing.assert_array_equal(got, orc.select_landmarks(scores, w, cu, 128))
+
+
 def test_quantize_bit_exact():
     rng = np.random.default_rng(1)
     w = np.concatenate([rng.random(10000).astype(np.float32) * 600 - 50,
