@@ -145,7 +145,7 @@ __device__ __forceinline__ void pack_block(const f32x16 &x, uint32_t (&pk)[8]) {
 // registers small enough for 3 workgroups per SIMD set at D = 64. Per tile a wave
 // computes S^T = K.Q^T and dP^T = V.dO^T (lane = query column), P = 2^(S c + bias - lse2)
 // on admitted pairs, dS = P (dP - Delta), and dQ^T += K^T.dS^T with K read transposed.
-template <typename DT, int D, int MODE>
+template <typename DT, int D, int MODE, bool EFAST>
 __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(const BwdParams p) {
     typedef typename DT::vec8 vec8;
     constexpr int NW = kDqW, BM = kDqBM, NT = 64 * NW;
@@ -159,10 +159,17 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
     __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][K, V], both row-swizzled
     __shared__ int s_red[NW][2];
     __shared__ int s_ltmin[DSALT_MAX_K_LMK / BN];
+    // SOFT edge factors ec[j] = exp((kEdgeMid - cst_j) / tau) of the element slots j
+    __shared__ __align__(16) float s_ec[16 * NRB];
     extern __shared__ int s_dyn[];
     int *s_lpos = s_dyn;                                          // INT_MAX: empty slot
     float *s_lbias = reinterpret_cast<float *>(s_dyn + p.k_pad);  // log2 units
     int *s_lrow = s_dyn + 2 * p.k_pad;
+    // SOFT edge tiles (EFAST, chosen by dq_edge_fast on the host): exp(-z) of an edge key
+    // factors as E ec[j], both factors in the fp32 range while (win_edge + 1 + 16 NRB) / tau
+    // < 80 (edge keys have 0 <= z < (win_edge + 1) / tau); otherwise each element takes
+    // its own exp. One path per instantiation keeps the kernel within its scalar registers.
+    constexpr float kEdgeMid = 16.f * NRB - 2.5f;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
@@ -297,6 +304,8 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
         s_red[wave][0] = wlo;
         s_red[wave][1] = wpmax;
     }
+    if (MODE == kSoft && EFAST && tid < 16 * NRB)
+        s_ec[tid] = fast_exp2((kEdgeMid - (float)((tid >> 4) * 32 + acc_row_const(tid & 15))) * p.inv_tau * kLog2e);
     __syncthreads();
     int glo = s_red[0][0], gpmax = s_red[0][1];
 #pragma unroll
@@ -425,33 +434,70 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
                 const int B = lo - tb - hh * 4;  // key >= lo <=> cst >= B
                 if constexpr (MODE == kSoft && KIND == kEdgeTile) {
                     // edge bias, P, dS and the d_w~ term fused per element: dS (1 - sigma) on
-                    // edge keys; the edge terms are only formed where they are used
-                    // (exp(-z) may overflow elsewhere)
+                    // edge keys (cst < Bc; such keys also satisfy cst <= A)
                     const int Bc = corelo - tb - hh * 4;
                     uint32_t pk[NRB][8];
+                    if constexpr (EFAST) {
+                        // sigma(z) = 1 / (1 + u), u = exp(-z) = E ec[j] (E per lane and tile,
+                        // ec[j] per element slot, both in range on edge keys); the edge bias
+                        // enters P as the factor sigma (P = 2^(S c - lse2) sigma), and
+                        // 1 - sigma = 0 exactly where u = 0 (core keys, masked elements)
+                        const float E = fast_exp2(((float)A - wc - kEdgeMid) * p.inv_tau * kLog2e);
 #pragma unroll
-                    for (int rb = 0; rb < NRB; ++rb)
+                        for (int rb = 0; rb < NRB; ++rb) {
+                            float ec[16];
 #pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            float ds2[2];
-#pragma unroll
-                            for (int h2 = 0; h2 < 2; ++h2) {
-                                const int r = 2 * j + h2;
-                                const int cst = rb * 32 + acc_row_const(r);
-                                const bool ok = (cst <= A) & (cst >= B);
-                                const bool is_edge = (cst < Bc) & ok;
-                                const float z = ((float)wc - (float)(A - cst)) * p.inv_tau;
-                                const float e = fast_exp2(is_edge ? -z * kLog2e : 0.f);  // exp(-z)
-                                const float onep = 1.f + e;
-                                const float edge = is_edge ? -fast_log2(onep) : 0.f;  // log2 sigmoid(z)
-                                const float y = fmaf(sacc[rb][r], c, edge);
-                                const float pr = ok ? fast_exp2(y - lse2) : 0.f;
-                                const float dsv = pr * (pacc[rb][r] - delta);
-                                dw += is_edge ? dsv * (e * __builtin_amdgcn_rcpf(onep)) : 0.f;
-                                ds2[h2] = dsv;
+                            for (int g = 0; g < 4; ++g) {
+                                const float4 e4 = *reinterpret_cast<const float4 *>(&s_ec[rb * 16 + g * 4]);
+                                ec[4 * g] = e4.x;
+                                ec[4 * g + 1] = e4.y;
+                                ec[4 * g + 2] = e4.z;
+                                ec[4 * g + 3] = e4.w;
                             }
-                            pk[rb][j] = DT::pack2(ds2[0], ds2[1]);
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                float ds2[2];
+#pragma unroll
+                                for (int h2 = 0; h2 < 2; ++h2) {
+                                    const int r = 2 * j + h2;
+                                    const int cst = rb * 32 + acc_row_const(r);
+                                    const bool ok = (cst <= A) & (cst >= B);
+                                    const float u = ((cst < Bc) & (cst >= B)) ? E * ec[r] : 0.f;
+                                    const float sig = __builtin_amdgcn_rcpf(1.f + u);
+                                    const float pr = fast_exp2(ok ? fmaf(sacc[rb][r], c, -lse2) : -INFINITY) * sig;
+                                    const float dsv = pr * (pacc[rb][r] - delta);
+                                    dw = fmaf(dsv, 1.f - sig, dw);
+                                    ds2[h2] = dsv;
+                                }
+                                pk[rb][j] = DT::pack2(ds2[0], ds2[1]);
+                            }
                         }
+                    } else {
+                        // every factor formed per element (exp(-z) may overflow off the edge)
+#pragma unroll
+                        for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                float ds2[2];
+#pragma unroll
+                                for (int h2 = 0; h2 < 2; ++h2) {
+                                    const int r = 2 * j + h2;
+                                    const int cst = rb * 32 + acc_row_const(r);
+                                    const bool ok = (cst <= A) & (cst >= B);
+                                    const bool is_edge = (cst < Bc) & ok;
+                                    const float z = ((float)wc - (float)(A - cst)) * p.inv_tau;
+                                    const float e = fast_exp2(is_edge ? -z * kLog2e : 0.f);  // exp(-z)
+                                    const float onep = 1.f + e;
+                                    const float edge = is_edge ? -fast_log2(onep) : 0.f;  // log2 sigmoid(z)
+                                    const float y = fmaf(sacc[rb][r], c, edge);
+                                    const float pr = ok ? fast_exp2(y - lse2) : 0.f;
+                                    const float dsv = pr * (pacc[rb][r] - delta);
+                                    dw += is_edge ? dsv * (e * __builtin_amdgcn_rcpf(onep)) : 0.f;
+                                    ds2[h2] = dsv;
+                                }
+                                pk[rb][j] = DT::pack2(ds2[0], ds2[1]);
+                            }
+                    }
                     dq_mfma(pk, stage);
                 } else {
                     uint32_t keep;
@@ -1051,11 +1097,19 @@ WsLayout ws_layout(int T, int S, int H, int D, int k) {
     return L;
 }
 
+// Whether the SOFT dq kernel takes the factored edge path (see bwd_dq_kernel).
+inline bool dq_edge_fast(const BwdParams &p) { return (p.win_edge + 1.f + 16.f * (kDqBN / 32)) * p.inv_tau < 80.f; }
+
 template <typename DT, int D, int MODE>
 hipError_t launch_typed(const BwdParams &p, hipStream_t stream) {
     // dq writes the per-query records that the key-parallel passes stream
     const size_t dyn = (size_t)p.k_pad * (2 * sizeof(int) + sizeof(float));
-    hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE>), dim3(p.grid_dq), dim3(64 * kDqW), dyn, stream, p);
+    bool efast = false;
+    if constexpr (MODE == kSoft) efast = dq_edge_fast(p);
+    if (efast)  // instantiated for SOFT only
+        hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE, MODE == kSoft>), dim3(p.grid_dq), dim3(64 * kDqW), dyn, stream, p);
+    else
+        hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE, false>), dim3(p.grid_dq), dim3(64 * kDqW), dyn, stream, p);
     if (p.k_lmk > 0) {
         hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, true>), dim3(p.n_heads * p.n_lgrp * p.n_lchunk), dim3(256),
                            0, stream, p);

@@ -84,6 +84,15 @@ def test_bwd_f16_soft_edge_params():
              edge=3.0)
 
 
+@pytest.mark.parametrize("tau,edge,D", [(0.2, 4.0, 64), (0.25, 6.0, 128), (3.0, 1.0, 64)],
+                         ids=["tau0.2-d64", "tau0.25-edge6-d128", "tau3-edge1-d64"])
+def test_bwd_soft_edge_factor_paths(tau, edge, D):
+    # the dq pass factors the edge's exp(-z) per lane and slot while (edge + 17) / tau < 80
+    # and takes a per-element exp otherwise (tau 0.2 and 0.25 with edge 6)
+    print(f"bwd soft tau={tau} edge={edge} D={D}", flush=True)
+    run_case(hip.MODE_SOFT, [400, 130], 2, D, 8, seed=44, n_min=3, n_max=120, tau=tau, edge=edge)
+
+
 @pytest.mark.parametrize("mode", [hip.MODE_HARD, hip.MODE_SOFT], ids=["hard", "soft"])
 def test_bwd_16bit_gradient_outputs(mode):
     print(f"bwd bf16 outputs mode={mode}", flush=True)
