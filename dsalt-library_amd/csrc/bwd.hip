@@ -569,7 +569,7 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
 // sub-block: S = Q.K^T and dP = dO.V^T (lane = key column, registers = query rows),
 // P = 2^(S c + bias - lse2) on admitted pairs, dS = P (dP - Delta), then dV^T += dO^T.P
 // and dK^T += Q^T.dS with Q and dO read transposed.
-template <typename DT, int D, int MODE, bool LMK>
+template <typename DT, int D, int MODE, bool LMK, bool EFAST>
 __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1) bwd_kv_kernel(const BwdParams p) {
     typedef typename DT::vec8 vec8;
     constexpr int NW = LMK ? 4 : kv_waves(D), NT = 64 * NW;  // waves, threads
@@ -589,6 +589,8 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][Q, dO], row-swizzled
     __shared__ __align__(16) char s_rec[NSTAGE][kRecFields][RB];
     __shared__ int s_misc[8];
+    // SOFT edge (EFAST): per wave, the query factors R_q of the current sub-block
+    __shared__ __align__(16) float s_rq[EFAST ? NW : 1][EFAST ? 32 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
@@ -656,6 +658,11 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     const bool kvalid = key != INT_MAX;
     const int wkmin = LMK ? wave_min_u(key) : kw;
     const int wkmax = LMK ? wave_max_u(kvalid ? key : -1) : min(kw + 31, seq_len - 1);
+    // SOFT edge factors (EFAST): exp(-z) = exp((q - key - w~_q) / tau) splits as R_q L_key
+    // with L_key = exp((wkmin - key) / tau); on an edge pair of this wave both factors stay
+    // in the fp32 range while (win_edge + 33) / tau < 80 (kv_edge_fast)
+    const float kit = p.inv_tau * kLog2e;
+    const float lkey = EFAST ? fast_exp2((float)(wkmin - (kvalid ? key : wkmin + 31)) * kit) : 0.f;
 
     // this lane's key row as the B operand of S = Q K^T and dP = dO V^T
     vec8 kreg[KS], vreg[KS];
@@ -758,8 +765,10 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
         // and sub-block 1's VALU work under the dV/dK MFMAs of sub-block 0). The band masks
         // (q >= key, lo(q) <= key) are branch-free; a sub-block without admitted pairs is
         // fully masked, a tile without any is skipped. SOFT edge biases (key < corelo(q))
-        // are added in place by a wave-uniform branch.
-        for (int t = 0; t < ntile; ++t) {
+        // are added in place by a wave-uniform branch, or (EFAST) enter P as a factor in the
+        // tiles from the first one with an edge pair on (a second copy of the tile loop).
+        auto band_tile = [&](int t, auto edge_phase) {
+            constexpr bool EP = decltype(edge_phase)::value;
             if (t + NSTAGE - 1 < ntile) issue_tile(t + NSTAGE - 1);
             const int st = stage_of(t);
             const char *qtile = s_tiles[st][0];
@@ -779,7 +788,7 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
                 f32x16 sacc[NSB], pacc[NSB];
 #pragma unroll
                 for (int sb = 0; sb < NSB; ++sb) sdp_mfma(qtile, dtile, sb, sacc[sb], pacc[sb]);
-                if (MODE == kSoft) {
+                if (MODE == kSoft && !EFAST) {
 #pragma unroll
                     for (int sb = 0; sb < NSB; ++sb) {
                         if (!edge[sb]) continue;
@@ -804,11 +813,23 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
                     }
                 }
                 uint32_t pkp[NSB][8], pks[NSB][8];
-#pragma unroll
-                for (int sb = 0; sb < NSB; ++sb) {
+                // P and dS of sub-block sb; with_edge (EFAST): the SOFT edge enters P as the
+                // factor sigma(z) = 1 / (1 + u), u = exp(-z) = R_q L_key, on edge pairs
+                // (key < corelo(q)); u = 0 elsewhere, so that sigma = 1 exactly
+                auto p_ds = [&](int sb, auto with_edge) {
+                    constexpr bool WE = decltype(with_edge)::value;
                     const int qsb = q0 + sb * 32;
                     const int Cj = (kvalid ? key : INT_MAX / 2) - qsb - hh * 4;  // q >= key <=> cst >= Cj
                     const bool kv_ok = kvalid & live[sb];
+                    if constexpr (WE) {
+                        // R_q = exp((q - w~_q - wkmin) / tau) of the sub-block's 32 queries, one per
+                        // lane, through this wave's LDS row (LDS operations of a wave run in order)
+                        const float wq = *rec_f(st, kRecWc, sb * 32 + ql);
+                        const float rq = fast_exp2(((float)(qsb + ql - wkmin) - wq) * kit);
+                        // a NaN window (no band, no edge pair) gets 0: u is never NaN
+                        if (hh == 0) s_rq[wave][ql] = (rq == rq) ? rq : 0.f;
+                        __builtin_amdgcn_wave_barrier();
+                    }
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const int qi = sb * 32 + g * 8 + hh * 4;
@@ -822,13 +843,27 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
                         const float la[4] = {l4.x, l4.y, l4.z, l4.w};
                         const float da[4] = {d4.x, d4.y, d4.z, d4.w};
                         const int oa[4] = {o4.x, o4.y, o4.z, o4.w};
+                        int ca[4] = {0, 0, 0, 0};
+                        float ra[4] = {0.f, 0.f, 0.f, 0.f};
+                        if constexpr (WE) {
+                            const int4 c4 = *reinterpret_cast<const int4 *>(rec_i(st, kRecClo, qi));
+                            const float4 r4 = *reinterpret_cast<const float4 *>(&s_rq[wave][g * 8 + hh * 4]);
+                            ca[0] = c4.x; ca[1] = c4.y; ca[2] = c4.z; ca[3] = c4.w;
+                            ra[0] = r4.x; ra[1] = r4.y; ra[2] = r4.z; ra[3] = r4.w;
+                        }
                         float pr4[4], ds4[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int r = g * 4 + e;
                             const bool ok = (acc_row_const(r) >= Cj) & (oa[e] >= nkey) & kv_ok;
                             // masked before the exp (exp2(-inf) = 0): a select, never a branch
-                            const float pr = fast_exp2(ok ? fmaf(sacc[sb][r], c, -la[e]) : -INFINITY);
+                            float pr = fast_exp2(ok ? fmaf(sacc[sb][r], c, -la[e]) : -INFINITY);
+                            if constexpr (WE) {
+                                // u in [0, inf] (R_q >= 0, L_key > 0): sigma = 0 where it
+                                // overflows, which only masked pairs (P = 0) reach
+                                const float u = (nkey > ca[e]) ? ra[e] * lkey : 0.f;
+                                pr *= __builtin_amdgcn_rcpf(1.f + u);
+                            }
                             pr4[e] = pr;
                             ds4[e] = pr * (pacc[sb][r] - da[e]);
                         }
@@ -837,13 +872,36 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
                         pks[sb][g * 2] = DT::pack2(ds4[0], ds4[1]);
                         pks[sb][g * 2 + 1] = DT::pack2(ds4[2], ds4[3]);
                     }
-                }
+                    if constexpr (WE) __builtin_amdgcn_wave_barrier();  // R row read before the next write
+                };
+#pragma unroll
+                for (int sb = 0; sb < NSB; ++sb) p_ds(sb, std::integral_constant<bool, EP>());
 #pragma unroll
                 for (int sb = 0; sb < NSB; ++sb) kv_mfma(qtile, dtile, sb, pkp[sb], pks[sb]);
             }
             // tile t+1 must have landed; tiles t+2 .. t+NSTAGE-1 may stay in flight
             if (t + NSTAGE - 1 < ntile) tile_barrier<(NSTAGE - 2) * LPT>();
             else tile_barrier<0>();
+        };
+        int t = 0;
+        if constexpr (MODE == kSoft && EFAST) {
+            // tile t has landed here: its sub-block summaries say whether it holds an edge pair
+            auto has_edge = [&](int tt) {
+                const int st = stage_of(tt);
+                bool e = false;
+#pragma unroll
+                for (int sb = 0; sb < NSB; ++sb) {
+                    const int qsb = q_begin + tt * QT + sb * 32;
+                    const int gmin_lo = INT_MAX - *rec_i(st, kRecGLo, sb * 32);
+                    const int gmax_clo = INT_MAX - *rec_i(st, kRecGClo, sb * 32);
+                    e |= !((qsb >= q_end) || (qsb + 31 < kw) || (gmin_lo > wkmax)) && (gmax_clo > wkmin);
+                }
+                return e;
+            };
+            for (; t < ntile && !has_edge(t); ++t) band_tile(t, std::false_type());
+            for (; t < ntile; ++t) band_tile(t, std::true_type());
+        } else {
+            for (; t < ntile; ++t) band_tile(t, std::false_type());
         }
     } else {
     for (int t = 0; t < ntile; ++t) {
@@ -1097,8 +1155,9 @@ WsLayout ws_layout(int T, int S, int H, int D, int k) {
     return L;
 }
 
-// Whether the SOFT dq kernel takes the factored edge path (see bwd_dq_kernel).
+// Whether the SOFT dq / band dK-dV kernels take their factored edge paths (see the kernels).
 inline bool dq_edge_fast(const BwdParams &p) { return (p.win_edge + 1.f + 16.f * (kDqBN / 32)) * p.inv_tau < 80.f; }
+inline bool kv_edge_fast(const BwdParams &p) { return (p.win_edge + 33.f) * p.inv_tau < 80.f; }
 
 template <typename DT, int D, int MODE>
 hipError_t launch_typed(const BwdParams &p, hipStream_t stream) {
@@ -1111,12 +1170,22 @@ hipError_t launch_typed(const BwdParams &p, hipStream_t stream) {
     else
         hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE, false>), dim3(p.grid_dq), dim3(64 * kDqW), dyn, stream, p);
     if (p.k_lmk > 0) {
-        hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, true>), dim3(p.n_heads * p.n_lgrp * p.n_lchunk), dim3(256),
+        hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, true, false>), dim3(p.n_heads * p.n_lgrp * p.n_lchunk), dim3(256),
                            0, stream, p);
         if (p.d_bias)
             hipLaunchKernelGGL(bwd_dbias_kernel, dim3(p.n_heads * p.num_seqs), dim3(64), 0, stream, p);
     }
-    hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false>), dim3(p.grid_q), dim3(64 * kv_waves(D)), 0, stream, p);
+    // the factored edge path of the band dK/dV kernel exists at D = 64 only (at D = 128 its
+    // second tile loop does not fit the scalar registers)
+    constexpr bool kKvFast = MODE == kSoft && D == 64;
+    bool kv_fast = false;
+    if constexpr (kKvFast) kv_fast = kv_edge_fast(p);
+    if (kv_fast)
+        hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false, kKvFast>), dim3(p.grid_q), dim3(64 * kv_waves(D)), 0,
+                           stream, p);
+    else
+        hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false, false>), dim3(p.grid_q), dim3(64 * kv_waves(D)), 0,
+                           stream, p);
     return hipGetLastError();
 }
 
