@@ -22,12 +22,12 @@
 //           512 queries of one sequence); 4 waves = 2 slot groups x 2 query sub-blocks scan
 //           the chunk's queries in 64-query LDS tiles. Writes landmark dK/dV and d_bias
 //           partials per chunk (workspace).
+//   lmk_combine  sums the lmk_kv chunk partials of each (head, sequence) in a fixed
+//           order: d_lmk_bias, and each slot's landmark dK/dV (into the first chunk row).
 //   kv      key-parallel band dK/dV, kv_waves(D) waves x 32 keys per workgroup, scanning
 //           kv_qt(D)-query LDS tiles from the key block to the last dq query block whose
-//           band reaches it; adds
-//           the landmark partials (over the sequence's chunks) of keys that are landmark
-//           positions; its head-0 workgroups reduce d_w~ over heads.
-//   dbias   d_lmk_bias = sum of the lmk_kv chunk partials, one workgroup per (head, seq).
+//           band reaches it; keys that are landmark positions start from their combined
+//           landmark dK/dV; its head-0 workgroups reduce d_w~ over heads.
 // Every MFMA is v_mfma_f32_32x32x16 with operands in the layouts of the forward kernel:
 // a lane owns one column (query or key) of each 32x32 block and 16 rows of it.
 #include "common.h"
@@ -722,6 +722,43 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     for (int d = 0; d < ND; ++d)
 #pragma unroll
         for (int r = 0; r < 16; ++r) dk[d][r] = dv[d][r] = 0.f;
+    if (!LMK && p.ws_ldk) {
+        // keys that are landmark positions start from their landmark dK/dV: the slot sums
+        // over the sequence's query chunks, which bwd_lmk_combine_kernel left in the first
+        // chunk's row (fixed order). These loads go out before the tile ring's, so that the
+        // ring's counted waits still cover exactly its own loads.
+        const int c_first = seq_start / kLC + seq;
+        for (int s0 = 0; s0 < p.k_lmk; s0 += 64) {
+            int pos = -1;
+            if (s0 + lane < p.k_lmk) {
+                const int64_t pp = p.lmk_pos[head * p.lp_sh + seq * p.lp_ss + (s0 + lane) * p.lp_sk];
+                if (pp >= kw && pp < min(kw + 32, seq_len)) pos = (int)pp;
+            }
+            unsigned long long m = __ballot(pos >= 0);
+            while (m) {
+                const int b = __ffsll((long long)m) - 1;
+                m &= m - 1;
+                const int pb = __shfl(pos, b);
+                if (key == pb) {
+                    const size_t row = ((size_t)head * p.n_lchunk + c_first) * p.k_pad + s0 + b;
+                    const float *gk = p.ws_ldk + row * D;
+                    const float *gv = p.ws_ldv + row * D;
+#pragma unroll
+                    for (int d = 0; d < ND; ++d)
+#pragma unroll
+                        for (int g = 0; g < 4; ++g) {
+                            const int dd = d * 32 + g * 8 + hh * 4;
+                            const float4 a = *reinterpret_cast<const float4 *>(gk + dd);
+                            const float4 b4 = *reinterpret_cast<const float4 *>(gv + dd);
+                            dk[d][g * 4 + 0] += a.x; dk[d][g * 4 + 1] += a.y;
+                            dk[d][g * 4 + 2] += a.z; dk[d][g * 4 + 3] += a.w;
+                            dv[d][g * 4 + 0] += b4.x; dv[d][g * 4 + 1] += b4.y;
+                            dv[d][g * 4 + 2] += b4.z; dv[d][g * 4 + 3] += b4.w;
+                        }
+                }
+            }
+        }
+    }
     float dbias = 0.f;
     const float c = p.scale_log2;
     const int nkey = INT_MAX - (kvalid ? key : INT_MAX / 2);  // lo(q) <= key <=> rec lo >= nkey
@@ -1018,43 +1055,6 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     }
 
     if (!LMK) {
-        // landmark contributions of keys that are landmark positions (computed by lmk_kv
-        // per query chunk; summed here over the sequence's chunks in a fixed order)
-        if (p.ws_ldk) {
-            const int c_first = seq_start / kLC + seq, n_ch = (seq_len + kLC - 1) / kLC;
-            for (int s0 = 0; s0 < p.k_lmk; s0 += 64) {
-                int pos = -1;
-                if (s0 + lane < p.k_lmk) {
-                    const int64_t pp = p.lmk_pos[head * p.lp_sh + seq * p.lp_ss + (s0 + lane) * p.lp_sk];
-                    if (pp >= kw && pp < min(kw + 32, seq_len)) pos = (int)pp;
-                }
-                unsigned long long m = __ballot(pos >= 0);
-                while (m) {
-                    const int b = __ffsll((long long)m) - 1;
-                    m &= m - 1;
-                    const int pb = __shfl(pos, b);
-                    if (key == pb) {
-                        for (int ch = 0; ch < n_ch; ++ch) {
-                            const size_t row = ((size_t)head * p.n_lchunk + c_first + ch) * p.k_pad + s0 + b;
-                            const float *gk = p.ws_ldk + row * D;
-                            const float *gv = p.ws_ldv + row * D;
-#pragma unroll
-                            for (int d = 0; d < ND; ++d)
-#pragma unroll
-                                for (int g = 0; g < 4; ++g) {
-                                    const int dd = d * 32 + g * 8 + hh * 4;
-                                    const float4 a = *reinterpret_cast<const float4 *>(gk + dd);
-                                    const float4 b4 = *reinterpret_cast<const float4 *>(gv + dd);
-                                    dk[d][g * 4 + 0] += a.x; dk[d][g * 4 + 1] += a.y;
-                                    dk[d][g * 4 + 2] += a.z; dk[d][g * 4 + 3] += a.w;
-                                    dv[d][g * 4 + 0] += b4.x; dv[d][g * 4 + 1] += b4.y;
-                                    dv[d][g * 4 + 2] += b4.z; dv[d][g * 4 + 3] += b4.w;
-                                }
-                        }
-                    }
-                }
-            }
-        }
         if (kvalid) {
             const int64_t tok = (int64_t)seq_start + key;
             store_row<DT, ND>(p.dk, tok * p.dk_st + (int64_t)head * p.dk_sh, p.grad_f32, dk, p.scale, hh);
@@ -1116,17 +1116,42 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     }
 }
 
-// d_bias[h, s, slot] = sum over the query chunks of sequence s of the lmk_kv partials
-// (fixed order; zero for empty sequences). One workgroup of 64 threads per (head, sequence).
-__global__ void __launch_bounds__(64) bwd_dbias_kernel(const BwdParams p) {
+// Landmark partials of lmk_kv summed over the query chunks of each sequence, in a fixed
+// order: d_bias[h, s, slot] (zero for empty sequences), and the dK/dV rows of every slot,
+// written into the sequence's first chunk row (read there by the band dK/dV pass). Grid
+// (head x sequence, column blocks): a thread sums one float4 column of dK and of dV, its
+// chunk loads issued four at a time.
+constexpr int kCombineThreads = 256;
+template <int D>
+__global__ void __launch_bounds__(kCombineThreads) bwd_lmk_combine_kernel(const BwdParams p) {
     const int head = blockIdx.x / p.num_seqs, seq = blockIdx.x - head * p.num_seqs;
     const int seq_start = p.cu[seq], seq_len = p.cu[seq + 1] - seq_start;
     const int c_first = seq_start / kLC + seq, n_ch = (seq_len + kLC - 1) / kLC;
-    for (int sl = threadIdx.x; sl < p.k_lmk; sl += 64) {
-        float acc = 0.f;
-        for (int ch = 0; ch < n_ch; ++ch) acc += p.ws_ldb[((size_t)head * p.n_lchunk + c_first + ch) * p.k_pad + sl];
-        p.d_bias[((size_t)head * p.num_seqs + seq) * p.k_lmk + sl] = acc;
+    const size_t base = (size_t)head * p.n_lchunk + c_first;  // first chunk row of the sequence
+    if (p.d_bias && blockIdx.y == 0) {
+        for (int sl = threadIdx.x; sl < p.k_lmk; sl += kCombineThreads) {
+            float acc = 0.f;
+            for (int ch = 0; ch < n_ch; ++ch) acc += p.ws_ldb[(base + ch) * p.k_pad + sl];
+            p.d_bias[((size_t)head * p.num_seqs + seq) * p.k_lmk + sl] = acc;
+        }
     }
+    constexpr int C4 = D / 4;  // float4 columns per row
+    const int e = blockIdx.y * kCombineThreads + threadIdx.x;
+    if (n_ch <= 1 || e >= p.k_lmk * C4) return;
+    const int sl = e / C4, c4 = e - sl * C4;
+    const size_t cs = (size_t)p.k_pad * D;  // floats between the same slot of consecutive chunks
+    const size_t off = (base * p.k_pad + sl) * D + 4 * c4;
+    float4 ak = *reinterpret_cast<const float4 *>(p.ws_ldk + off);
+    float4 av = *reinterpret_cast<const float4 *>(p.ws_ldv + off);
+#pragma unroll 4
+    for (int ch = 1; ch < n_ch; ++ch) {
+        const float4 bk = *reinterpret_cast<const float4 *>(p.ws_ldk + off + ch * cs);
+        const float4 bv = *reinterpret_cast<const float4 *>(p.ws_ldv + off + ch * cs);
+        ak.x += bk.x; ak.y += bk.y; ak.z += bk.z; ak.w += bk.w;
+        av.x += bv.x; av.y += bv.y; av.z += bv.z; av.w += bv.w;
+    }
+    *reinterpret_cast<float4 *>(p.ws_ldk + off) = ak;
+    *reinterpret_cast<float4 *>(p.ws_ldv + off) = av;
 }
 
 struct WsLayout {
@@ -1172,8 +1197,9 @@ hipError_t launch_typed(const BwdParams &p, hipStream_t stream) {
     if (p.k_lmk > 0) {
         hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, true, false>), dim3(p.n_heads * p.n_lgrp * p.n_lchunk), dim3(256),
                            0, stream, p);
-        if (p.d_bias)
-            hipLaunchKernelGGL(bwd_dbias_kernel, dim3(p.n_heads * p.num_seqs), dim3(64), 0, stream, p);
+        const int col_blocks = (p.k_lmk * (D / 4) + kCombineThreads - 1) / kCombineThreads;
+        hipLaunchKernelGGL(bwd_lmk_combine_kernel<D>, dim3(p.n_heads * p.num_seqs, col_blocks), dim3(kCombineThreads), 0,
+                           stream, p);
     }
     // the factored edge path of the band dK/dV kernel exists at D = 64 only (at D = 128 its
     // second tile loop does not fit the scalar registers)
