@@ -342,8 +342,9 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
     float dw = 0.f;
     const float c = p.scale_log2;
 
-    // dS = P (dP - Delta) from shifted logits x (log2 units incl. biases, -inf where not
-    // admitted), then dQ^T += K^T . dS^T with K of stage `stage` read transposed
+    // dS = P (dP - Delta) from shifted logits x = logit - lse2 (log2 units incl. biases,
+    // -inf where not admitted), then dQ^T += K^T . dS^T with K of stage `stage` read
+    // transposed
     auto dq_mfma = [&](const uint32_t (&pk)[NRB][8], int stage) {
         const char *ktile = s_tiles[stage][0];
 #pragma unroll
@@ -364,7 +365,7 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
         for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float p0 = fast_exp2(x[rb][2 * j] - lse2), p1 = fast_exp2(x[rb][2 * j + 1] - lse2);
+                const float p0 = fast_exp2(x[rb][2 * j]), p1 = fast_exp2(x[rb][2 * j + 1]);
                 pk[rb][j] = DT::pack2(p0 * (pacc[rb][2 * j] - delta), p1 * (pacc[rb][2 * j + 1] - delta));
             }
         dq_mfma(pk, stage);
@@ -410,7 +411,7 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
                 sacc[rb] = a0;
                 pacc[rb] = a1;
             }
-            // logits in log2 units with biases, -inf where not admitted
+            // logits minus lse2 in log2 units with biases, -inf where not admitted
             f32x16 x[NRB];
             if constexpr (KIND == kLmkTile) {
 #pragma unroll
@@ -425,7 +426,7 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const int r = g * 4 + e;
-                            x[rb][r] = (pp[e] <= pmax) ? fmaf(sacc[rb][r], c, bb[e]) : -INFINITY;
+                            x[rb][r] = (pp[e] <= pmax) ? fmaf(sacc[rb][r], c, bb[e] - lse2) : -INFINITY;
                         }
                     }
             } else {
@@ -513,7 +514,7 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
 #pragma unroll
                     for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) x[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r] * c);
+                        for (int r = 0; r < 16; ++r) x[rb][r] = keep_if(keep, rb * 16 + r, fmaf(sacc[rb][r], c, -lse2));
                 }
             }
             if constexpr (KIND != kEdgeTile) ds_dq(x, pacc, stage);
