@@ -42,15 +42,18 @@ constexpr int kSelCache = 16384;               // keys cached in LDS (64 KB)
 constexpr uint32_t kKeyPosInf = 0xFF800000u;   // key of +inf; finite keys are below it
 constexpr int kSelChunk = 2048;                // positions per chunk of a long sequence
 constexpr int kSplitMin = 4096;                // longer sequences are selected chunk-wise
-constexpr int kMergeCap = 8192;                // candidates a final selection may gather
-constexpr int kMaxChunks = 512;                // chunks of one chunk-wise selected sequence
+constexpr int kMergeCap = 8192;                // candidate slots a final selection may gather
 static_assert(2 * kMergeCap <= kSelCache, "candidate keys and positions share the key cache");
 
+// Candidate slots per chunk: the chunk's top k, or a superset of at most k + min(k, 128)
+// items when the first radix pass already bounds one (see select_block's `cap`).
+__host__ __device__ inline int chunk_slots(int k) { return k + (k < 128 ? k : 128); }
+
 // Whether a sequence of length L is selected chunk-wise (when a workspace is given): its
-// chunks' candidates must fit the final workgroup's LDS.
+// chunks' candidate slots must fit the final workgroup's LDS.
 __host__ __device__ inline bool split_sequence(int L, int k) {
     const int nch = (L + kSelChunk - 1) / kSelChunk;
-    return L > kSplitMin && nch <= kMaxChunks && (int64_t)nch * k <= kMergeCap;
+    return L > kSplitMin && (int64_t)nch * chunk_slots(k) <= kMergeCap;
 }
 
 struct SelParams {
@@ -62,9 +65,8 @@ struct SelParams {
     int64_t *out;
     int num_seqs, n_heads, k;
     // chunked selection of long sequences (null ws_key: one workgroup per (head, sequence))
-    uint32_t *ws_key;  // [H][n_chunk_ub][k] candidate keys
-    int32_t *ws_pos;   // [H][n_chunk_ub][k] candidate positions (relative to the sequence)
-    int32_t *ws_cnt;   // [H][n_chunk_ub] candidates per chunk
+    uint32_t *ws_key;  // [H][n_chunk_ub][chunk_slots(k)] candidate keys, 0 in unused slots
+    int32_t *ws_pos;   // [H][n_chunk_ub][chunk_slots(k)] candidate positions in the sequence
     int n_chunk_ub;
 };
 
@@ -130,10 +132,14 @@ struct SelShared {
 // over items (j = tid + 1024 i: coalesced loads, conflict-free LDS); for the emission
 // thread t owns the contiguous items [t*C, t*C + C) (C = ceil(n / 1024)), which keeps
 // the output in item order with one workgroup scan. `all` emits NaN/+inf picks too (for
-// candidates); otherwise they only count towards k_eff. Returns the number of slots
-// emitted. Every thread of the workgroup calls it; `sh` is the workgroup's LDS.
+// candidates); otherwise they only count towards k_eff. cap >= k_eff: a set of at most
+// cap items that contains the top k_eff may be emitted instead (every candidate when there
+// are at most cap, else the keys at or above a radix bin that already bounds such a set);
+// cap = k_eff gives exactly the top k_eff. Returns the number of slots emitted. Every
+// thread of the workgroup calls it; `sh` is the workgroup's LDS.
 template <class KeyFn, class EmitFn>
-__device__ __forceinline__ int select_block(SelShared &sh, int n, int k_eff, bool all, KeyFn key_of, EmitFn emit) {
+__device__ __forceinline__ int select_block(SelShared &sh, int n, int k_eff, int cap, bool all, KeyFn key_of,
+                                            EmitFn emit) {
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool cached = n <= kSelCache;
     const int C = (max(n, 0) + kSelThreads - 1) / kSelThreads;
@@ -174,7 +180,7 @@ __device__ __forceinline__ int select_block(SelShared &sh, int n, int k_eff, boo
 
     uint32_t thr = 0u;  // select key > thr, plus the first need_eq keys == thr
     int need_eq = 0;
-    if (k_eff > 0 && ncand > k_eff) {
+    if (k_eff > 0 && ncand > cap) {
         // MSB-first radix select on rel = key - kmin, 8-bit digits from the top set bit of
         // the candidates' range (the first digit is spread over the whole histogram)
         const uint32_t range = kmax - kmin;
@@ -224,10 +230,11 @@ __device__ __forceinline__ int select_block(SelShared &sh, int n, int k_eff, boo
             prefix |= (uint32_t)sh.bc[0] << shift;
             pmask |= 0xFFu << shift;
             remaining -= sh.bc[1];
-            // every key of the chosen bin is needed: the selection is exactly the keys
-            // with rel >= prefix (the bin and everything above it), whatever the lower
-            // digits are - the passes for them are skipped
-            const bool whole_bin = sh.bc[2] == remaining;
+            // the keys with rel >= prefix (the bin and everything above it) number at most
+            // `cap`: they are the selection (cap = k_eff: every key of the bin is needed)
+            // or a superset of it (cap > k_eff, for candidates), whatever the lower digits
+            // are - the passes for them are skipped
+            const bool whole_bin = k_eff - remaining + sh.bc[2] <= cap;
             buf ^= 1;
             // no barrier here: bc is rewritten only after the next pass's histogram
             // barrier, which every thread reaches after this read
@@ -275,7 +282,9 @@ __device__ __forceinline__ int select_block(SelShared &sh, int n, int k_eff, boo
 }
 
 // Chunks of long sequences (L > kSplitMin): one workgroup per (head, chunk id of
-// find_block over kSelChunk-position chunks); candidates of the chunk to the workspace.
+// find_block over kSelChunk-position chunks); a superset of the chunk's top k (at most
+// chunk_slots(k) items, NaN/+inf picks included) to the workspace as (key, position)
+// candidates in position order, the remaining slots with key 0.
 __global__ void __launch_bounds__(kSelThreads) select_chunk_kernel(const SelParams p) {
     __shared__ SelShared sh;
     const int lane = threadIdx.x & 63;
@@ -286,9 +295,10 @@ __global__ void __launch_bounds__(kSelThreads) select_chunk_kernel(const SelPara
     if (!split_sequence(L, p.k)) return;  // selected from the scores by select_kernel
     const int c0 = chunk * kSelChunk;
     const int n = min(kSelChunk, L - c0);
-    const int k_eff = min(p.k, L);
-    uint32_t *ck = p.ws_key + ((int64_t)head * p.n_chunk_ub + cid) * p.k;
-    int32_t *cp = p.ws_pos + ((int64_t)head * p.n_chunk_ub + cid) * p.k;
+    const int k_eff = min(min(p.k, L), n);
+    const int cs = chunk_slots(p.k);
+    uint32_t *ck = p.ws_key + ((int64_t)head * p.n_chunk_ub + cid) * cs;
+    int32_t *cp = p.ws_pos + ((int64_t)head * p.n_chunk_ub + cid) * cs;
     auto key_of = [&](int j) -> uint32_t {
         const int pos = c0 + j;
         const int64_t tok = (int64_t)start + pos;
@@ -297,21 +307,20 @@ __global__ void __launch_bounds__(kSelThreads) select_chunk_kernel(const SelPara
         return order_key(p.scores[tok * p.sc_st + (int64_t)head * p.sc_sh]);
     };
     auto emit = [&](int slot, int j, uint32_t key) {
-        if (slot < p.k) {
+        if (slot < cs) {
             ck[slot] = key;
             cp[slot] = c0 + j;
         }
     };
-    const int total = select_block(sh, n, min(k_eff, n), true, key_of, emit);
-    if (threadIdx.x == 0) p.ws_cnt[(int64_t)head * p.n_chunk_ub + cid] = min(total, p.k);
+    const int total = min(select_block(sh, n, k_eff, max(k_eff, cs), true, key_of, emit), cs);
+    for (int sl = total + (int)threadIdx.x; sl < cs; sl += kSelThreads) ck[sl] = 0u;
 }
 
 // One workgroup per (head, sequence): the final selection, from the scores or (long
 // sequences with a workspace) from the chunks' candidates.
 __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) {
     __shared__ SelShared sh;
-    __shared__ int s_off[kMaxChunks + 1];
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tid = threadIdx.x;
     const int head = blockIdx.x / p.num_seqs;
     const int seq = blockIdx.x - head * p.num_seqs;
     const int start = p.cu[seq];
@@ -320,39 +329,22 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
     const int k_eff = min(p.k, L);
     int total;
     if (p.ws_key && split_sequence(L, p.k)) {
-        // the chunks' candidates in chunk order: keys into sh.keys[0, n), positions into
-        // s_pos = sh.keys[kMergeCap, 2 kMergeCap) (select_block caches only keys[0, n))
+        // the chunks' candidate slots, concatenated in chunk order (the candidates in
+        // position order, unused slots key 0): keys cached by select_block in
+        // sh.keys[0, n), positions in s_pos = sh.keys[kMergeCap, 2 kMergeCap)
+        const int cs = chunk_slots(p.k);
+        const int n = (L + kSelChunk - 1) / kSelChunk * cs;
+        const uint32_t *gk = p.ws_key + ((int64_t)head * p.n_chunk_ub + start / kSelChunk + seq) * cs;
+        const int32_t *gp = p.ws_pos + ((int64_t)head * p.n_chunk_ub + start / kSelChunk + seq) * cs;
         int32_t *s_pos = reinterpret_cast<int32_t *>(sh.keys + kMergeCap);
-        const int cid0 = start / kSelChunk + seq, nch = (L + kSelChunk - 1) / kSelChunk;
-        const int64_t cbase = (int64_t)head * p.n_chunk_ub + cid0;
-        if (wave == 0) {  // offsets of the chunks' runs (nch <= kMaxChunks)
-            int run = 0;
-            for (int c0 = 0; c0 < nch; c0 += 64) {
-                const int c = c0 + lane;
-                const int v = c < nch ? p.ws_cnt[cbase + c] : 0;
-                const int incl = wave_incl_scan_dpp(v);
-                if (c < nch) s_off[c] = run + incl - v;
-                run += __builtin_amdgcn_readlane(incl, 63);
-            }
-            if (lane == 0) s_off[nch] = run;
-        }
-        __syncthreads();
-        const int n = s_off[nch];
-        for (int c = wave; c < nch; c += kSelWaves) {
-            const int off = s_off[c], cnt = s_off[c + 1] - off;
-            for (int e = lane; e < cnt; e += 64) {
-                sh.keys[off + e] = p.ws_key[(cbase + c) * p.k + e];
-                s_pos[off + e] = p.ws_pos[(cbase + c) * p.k + e];
-            }
-        }
-        __syncthreads();
-        // keys are read back from sh.keys (n <= kMergeCap <= kSelCache: the pass-0 copy
-        // onto itself is harmless)
-        auto key_of = [&](int j) -> uint32_t { return sh.keys[j]; };
+        auto key_of = [&](int j) -> uint32_t {  // pass 0 only (n <= kMergeCap: cached)
+            s_pos[j] = gp[j];
+            return gk[j];
+        };
         auto emit = [&](int slot, int j, uint32_t) {
             if (slot < p.k) out[slot] = s_pos[j];
         };
-        total = select_block(sh, n, k_eff, false, key_of, emit);
+        total = select_block(sh, n, k_eff, k_eff, false, key_of, emit);
     } else {
         auto key_of = [&](int j) -> uint32_t {
             const int64_t tok = (int64_t)start + j;
@@ -363,7 +355,7 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
         auto emit = [&](int slot, int j, uint32_t) {
             if (slot < p.k) out[slot] = j;
         };
-        total = select_block(sh, L, k_eff, false, key_of, emit);
+        total = select_block(sh, L, k_eff, k_eff, false, key_of, emit);
     }
     for (int s2 = total + tid; s2 < p.k; s2 += kSelThreads) out[s2] = -1;
 }
@@ -380,13 +372,13 @@ __global__ void quantize_kernel(const float *__restrict__ w, int64_t n, float *_
 
 }  // namespace
 
-// Workspace of the chunk-wise selection: per (head, chunk id) k candidate keys, k
-// positions and a count.
+// Workspace of the chunk-wise selection: per (head, chunk id) chunk_slots(k) candidate
+// keys and as many positions.
 int64_t select_workspace_bytes(int total_len, int num_seqs, int n_heads, int k) {
     if (total_len <= kSplitMin || k == 0) return 0;
     auto al = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
     const int64_t n = (int64_t)n_heads * block_upper_bound(total_len, num_seqs, kSelChunk);
-    return 2 * al(n * k * 4) + al(n * 4);
+    return 2 * al(n * chunk_slots(k) * 4);
 }
 
 hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream) {
@@ -404,16 +396,13 @@ hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream) {
     p.k = a.k_lmk;
     p.ws_key = nullptr;
     p.ws_pos = nullptr;
-    p.ws_cnt = nullptr;
     p.n_chunk_ub = block_upper_bound(a.total_len, a.num_seqs, kSelChunk);
     const int64_t need = select_workspace_bytes(a.total_len, a.num_seqs, a.n_heads, a.k_lmk);
     if (a.workspace && need > 0 && (a.max_seqlen <= 0 || a.max_seqlen > kSplitMin)) {
         const int64_t n = (int64_t)a.n_heads * p.n_chunk_ub;
-        const int64_t part = (n * a.k_lmk * 4 + 255) & ~(int64_t)255;
         char *ws = static_cast<char *>(a.workspace);
         p.ws_key = reinterpret_cast<uint32_t *>(ws);
-        p.ws_pos = reinterpret_cast<int32_t *>(ws + part);
-        p.ws_cnt = reinterpret_cast<int32_t *>(ws + 2 * part);
+        p.ws_pos = reinterpret_cast<int32_t *>(ws + need / 2);
         hipLaunchKernelGGL(select_chunk_kernel, dim3((unsigned)n), dim3(kSelThreads), 0, stream, p);
     }
     hipLaunchKernelGGL(select_kernel, dim3(a.num_seqs * a.n_heads), dim3(kSelThreads), 0, stream, p);

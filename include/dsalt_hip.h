@@ -213,10 +213,10 @@ int dsalt_bwd_noalloc(const dsalt_bwd_args *args, void *stream);
  * finite-score positions are written in ascending order, followed by -1 in every
  * remaining slot (the reference's -inf/NaN/+inf slots also become -1).
  * workspace (optional, NULL allowed): with at least dsalt_select_workspace_size(...)
- * bytes, sequences longer than 4096 tokens (with ceil(L / 2048) * k <= 8192) are
- * selected in two stages - the top k of every 2048-position chunk by one workgroup each,
- * then the top k of the chunks' candidates - instead of by one workgroup per (head,
- * sequence). The result is identical; the workspace only adds parallelism. A size of 0
+ * bytes, sequences longer than 4096 tokens (with ceil(L / 2048) * (k + min(k, 128)) <=
+ * 8192) are selected in two stages - a superset of the top k of every 2048-position chunk
+ * (at most k + min(k, 128) candidates) by one workgroup each, then the top k of the chunks'
+ * candidates - instead of by one workgroup per (head, sequence). The result is identical; the workspace only adds parallelism. A size of 0
  * means no sequence can use it. max_seqlen: 0, or a bound on every sequence's length
  * (the chunk stage is skipped when it is <= 4096, saving its launch when no sequence is
  * long; a bound that is too small only means the one-workgroup route for everything).

@@ -140,8 +140,8 @@ def test_select_check():
 
 def test_select_workspace_size_and_check():
     """The chunk-wise selection's workspace: none below 4097 tokens; with one, the size
-    per (head, chunk id) is k keys + k positions + a count; too small or misaligned
-    workspaces are rejected."""
+    per (head, chunk id) is k + min(k, 128) candidate keys and as many positions; too
+    small or misaligned workspaces are rejected."""
     lib = hip.lib()
     assert lib.dsalt_select_workspace_size(4096, 1, 16, 128) == 0
     assert lib.dsalt_select_workspace_size(16384, 1, 16, 0) == 0
@@ -149,7 +149,7 @@ def test_select_workspace_size_and_check():
     need = lib.dsalt_select_workspace_size(16384, 1, 16, 128)
     n = 16 * (16384 // 2048 + 1)  # heads x chunk ids (ceil(T / 2048) + S)
     al = lambda b: -(-b // 256) * 256
-    assert need == 2 * al(n * 128 * 4) + al(n * 4)
+    assert need == 2 * al(n * (128 + 128) * 4)
     a = hip.SelectArgs()
     a.total_len, a.num_seqs, a.n_heads, a.k_lmk = 16384, 1, 16, 128
     a.scores, a.w, a.cu_seqlens, a.lmk_pos = 0x1000, 0x2000, 0x3000, 0x4000

@@ -279,14 +279,16 @@ def _select_gpu(scores, w, cu, k, chunked=True):
 @pytest.mark.parametrize("lens,H,k", [
     ([4097, 6000, 50, 16384], 2, 64),      # just past the chunk-wise threshold, ragged last chunks
     ([8193, 4096, 12000], 3, 1),
-    ([6000, 16384], 2, 1024),              # 8 chunks x 1024 candidates: the gather's capacity
-    ([20000, 5000], 2, 1024),              # 10 x 1024 > capacity: one workgroup per sequence
+    ([6000, 16384], 2, 896),               # 8 chunks x (896 + 128) slots: the gather's capacity
+    ([20000, 5000], 2, 1024),              # 10 x 1152 slots > capacity: one workgroup per sequence
     ([300, 4500, 7, 9000], 2, 128),
 ])
 @pytest.mark.parametrize("tie", [True, False], ids=["ties", "distinct"])
 def test_select_chunked_bit_exact(lens, H, k, tie):
-    """Sequences longer than 4096 tokens go through the per-chunk top-k and the top-k of
-    the chunks' candidates; same bar as the single-workgroup path: the oracle exactly."""
+    """Sequences longer than 4096 tokens go through the per-chunk candidates (the chunk's
+    top k, or a superset of at most k + min(k, 128) when the first radix pass bounds one)
+    and the top-k of the chunks' candidates; same bar as the single-workgroup path: the
+    oracle exactly."""
     print(f"select chunked lens={lens} H={H} k={k} tie={tie}", flush=True)
     scores, w, cu = _select_case(sum(lens) % 997 + k, lens, H, tie)
     np.testing.assert_array_equal(_select_gpu(scores, w, cu, k), orc.select_landmarks(scores, w, cu, k))
