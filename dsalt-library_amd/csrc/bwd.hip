@@ -173,12 +173,15 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
-    const int logical = xcd_remap(blockIdx.x, p.grid_dq);
-    const int head = logical / p.n_dqblk;
+    // the forward's dispatch order: XCDs own whole heads, and blocks arrive rank-major over
+    // the heads in decreasing block index (the long late blocks of every sequence first,
+    // the short first blocks last, in the last dispatch round)
+    int head, rank;
+    head_rank(blockIdx.x, p.grid_dq, p.n_heads, p.n_dqblk, head, rank);
     if (head >= p.n_heads) return;
     int seq, blk, seq_start, seq_len;
-    const int target = p.n_dqblk - 1 - (logical - head * p.n_dqblk);
-    if (!find_block(p.cu, p.num_seqs, target, BM, lane, seq, blk, seq_start, seq_len)) return;
+    if (!find_block_desc(p.cu, p.num_seqs, rank, p.n_dqblk, BM, lane, seq, blk, seq_start, seq_len)) return;
+    const int target = seq_start / BM + seq + blk;  // the block's find_block id (ws_minlo index)
     const int wq0 = blk * BM + wave * 32;
     const int i = wq0 + ql;
     const bool qvalid = i < seq_len;
@@ -600,11 +603,14 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     int key = INT_MAX;  // this lane's key position in the sequence (INT_MAX: none)
     float kbias2 = 0.f;
     if (!LMK) {
-        const int logical = xcd_remap(blockIdx.x, p.grid_q);
-        head = logical / p.n_qblk;
+        // XCDs own whole heads; key blocks arrive rank-major over the heads, farthest from
+        // the sequence end first (they are attended by the most queries): the short last
+        // blocks of every sequence fill the last dispatch round
+        int rank, bdesc;
+        head_rank(blockIdx.x, p.grid_q, p.n_heads, p.n_qblk, head, rank);
         if (head >= p.n_heads) return;
-        const int target = p.n_qblk - 1 - (logical - head * p.n_qblk);
-        if (!find_block(p.cu, p.num_seqs, target, kBM, lane, seq, kblk, seq_start, seq_len)) return;
+        if (!find_block_desc(p.cu, p.num_seqs, rank, p.n_qblk, kBM, lane, seq, bdesc, seq_start, seq_len)) return;
+        kblk = (seq_len + kBM - 1) / kBM - 1 - bdesc;
     } else {
         // workgroup = (head, 64-slot group, query chunk); chunk ids follow find_block
         const int per_head = p.n_lgrp * p.n_lchunk;
