@@ -729,11 +729,20 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     for (int d = 0; d < ND; ++d)
 #pragma unroll
         for (int r = 0; r < 16; ++r) dk[d][r] = dv[d][r] = 0.f;
+    float dbias = 0.f;
+    const float c = p.scale_log2;
+    const int nkey = INT_MAX - (kvalid ? key : INT_MAX / 2);  // lo(q) <= key <=> rec lo >= nkey
+
+#pragma unroll
+    for (int t = 0; t < NSTAGE - 1; ++t)
+        if (t < ntile) issue_tile(t);
     if (!LMK && p.ws_ldk) {
         // keys that are landmark positions start from their landmark dK/dV: the slot sums
         // over the sequence's query chunks, which bwd_lmk_combine_kernel left in the first
-        // chunk's row (fixed order). These loads go out before the tile ring's, so that the
-        // ring's counted waits still cover exactly its own loads.
+        // chunk's row (fixed order). These loads go out after the ring's first tiles, so
+        // that their latency overlaps the tiles'; they are consumed here, before the first
+        // counted wait, and the compiler's wait for them (for every load before them, the
+        // ring's included) leaves nothing of them in flight at that wait.
         const int c_first = seq_start / kLC + seq;
         for (int s0 = 0; s0 < p.k_lmk; s0 += 64) {
             int pos = -1;
@@ -766,13 +775,6 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
             }
         }
     }
-    float dbias = 0.f;
-    const float c = p.scale_log2;
-    const int nkey = INT_MAX - (kvalid ? key : INT_MAX / 2);  // lo(q) <= key <=> rec lo >= nkey
-
-#pragma unroll
-    for (int t = 0; t < NSTAGE - 1; ++t)
-        if (t < ntile) issue_tile(t);
     if (ntile >= NSTAGE - 1) tile_barrier<(NSTAGE - 2) * LPT>();
     else tile_barrier<0>();
 
