@@ -60,8 +60,9 @@ enum { kCoreTile = 0, kEdgeTile = 1, kLmkTile = 2 };  // tile kinds of the dq lo
 // direct load (two fields of a 32-query tile share one). Integer fields are encoded so that an all-zero record (what an
 // out-of-range load returns) admits no key: lo and corelo as INT_MAX - x, pmax as x + 1.
 enum {
-    kRecLse2 = 0,    // LSE * log2(e), +inf for empty rows (float)
-    kRecDelta = 1,   // rowsum(O * dO) (float)
+    kRecLse2 = 0,    // -LSE / scale: minus the LSE in raw q.k units (float; -inf * sign(scale)
+                     // for empty rows), the initial value of an S accumulator
+    kRecDelta = 1,   // -rowsum(O * dO) (float), the initial value of a dP accumulator
     kRecLo = 2,      // INT_MAX - first band key
     kRecClo = 3,     // INT_MAX - first zero-bias band key (SOFT core start)
     kRecPmax = 4,    // largest admissible landmark position + 1
@@ -265,8 +266,8 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
     if (qvalid && hh == 0) {
         float *rec = p.ws_qrec + (size_t)head * kRecFields * p.total_len + tok_i;
         const size_t T = (size_t)p.total_len;
-        rec[kRecLse2 * T] = lse2;
-        rec[kRecDelta * T] = delta;
+        rec[kRecLse2 * T] = -lse2 * p.inv_c2;  // (S + this) * scale_log2 = S scale_log2 - lse2
+        rec[kRecDelta * T] = -delta;
         reinterpret_cast<int *>(rec)[kRecLo * T] = INT_MAX - lo;
         reinterpret_cast<int *>(rec)[kRecClo * T] = INT_MAX - corelo;
         reinterpret_cast<int *>(rec)[kRecPmax * T] = pmax + 1;
@@ -594,7 +595,8 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     __shared__ __align__(16) char s_rec[NSTAGE][kRecFields][RB];
     __shared__ int s_misc[8];
     // SOFT edge (EFAST): per wave, the query factors R_q of the current sub-block
-    __shared__ __align__(16) float s_rq[EFAST ? NW : 1][EFAST ? 32 : 1];
+    // (the D = 64 band loop double-buffers it: row t & 1 holds tile t's factors)
+    __shared__ __align__(16) float s_rq[EFAST ? NW : 1][EFAST ? 2 : 1][EFAST ? 32 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
@@ -643,6 +645,7 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
         __syncthreads();
 #pragma unroll
         for (int w = 0; w < NW; ++w) last = max(last, s_misc[w]);
+        last = __builtin_amdgcn_readfirstlane(last);  // wave-uniform: it bounds the tile loops
         q_begin = kb;
         q_end = min(seq_len, (last + 1) * kDqBM);
     } else {
@@ -658,7 +661,7 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
         const int mn = wave_min_u(key);
         if (lane == 0) s_misc[wave] = mn;
         __syncthreads();
-        const int gmin = min(min(s_misc[0], s_misc[1]), min(s_misc[2], s_misc[3]));
+        const int gmin = __builtin_amdgcn_readfirstlane(min(min(s_misc[0], s_misc[1]), min(s_misc[2], s_misc[3])));
         if (gmin == INT_MAX || gmin >= q_end) q_begin = q_end;
         else if (gmin > q_begin) q_begin += (gmin - q_begin) / QT * QT;
     }
@@ -706,8 +709,8 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
         const int q0 = q_begin + t * QT;
         const int st = stage_of(t);
         const uint32_t tl = tiles_lds + st * (2 * TB);
-        qlanes.load_band(tl, wave, qrs, (uint32_t)q0 * qst);
-        dlanes.load_band(tl + TB, wave, drs, (uint32_t)q0 * dst);
+        qlanes.load_band(tl, wave, uniform_rsrc(qrs), (uint32_t)q0 * qst);
+        dlanes.load_band(tl + TB, wave, uniform_rsrc(drs), (uint32_t)q0 * dst);
         // one load covers FPI consecutive fields (lane l: field f0 + l / QT, query l % QT),
         // which are consecutive in LDS
         const int q = q0 + lane % QT;
@@ -716,7 +719,7 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
             const int f0 = (wave * RLW + u) * FPI;
             const int f = f0 + lane / QT;
             const uint32_t off = (q < seq_len) ? (uint32_t)(((size_t)f * p.total_len + seq_start + q) * 4) : 0xFFFFFF00u;
-            asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(off), "s"(rrs),
+            asm volatile("buffer_load_dword %0, %1, 0 offen lds" ::"v"(off), "s"(uniform_rsrc(rrs)),
                          "{m0}"(__builtin_amdgcn_readfirstlane(rec_lds + (st * kRecFields + f0) * RB))
                          : "memory");
         }
@@ -805,7 +808,209 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
         }
     };
 
-    if (!LMK) {
+    if constexpr (!LMK && NSB == 1) {
+        // Band, one 32-query sub-block per tile (D = 64), software-pipelined: step t runs the
+        // S/dP MFMAs of tile t+1 under the masks, P and dS (VALU) of tile t, then dV/dK +=
+        // of tile t. Every tile of the scan is computed: a tile without admitted pairs gives
+        // P = dS = 0. The band masks (q >= key, lo(q) <= key) are branch-free. SOFT edge
+        // biases (key < corelo(q)) are added in place per element, or (EFAST) enter P as a
+        // factor in the steps from the first tile with an edge pair on; the query factors
+        // R_q of tile t+1 go to this wave's LDS row (t+1) & 1 during step t.
+        static_assert(NSTAGE >= 3, "the pipelined band loop keeps two tiles ahead of the MFMAs");
+        // (summary fields read as wave-uniform values: they steer the loops)
+        auto tile_live = [&](int st, int qsb) {
+            const int gmin_lo = INT_MAX - __builtin_amdgcn_readfirstlane(*rec_i(st, kRecGLo, 0));
+            return !((qsb >= q_end) || (qsb + 31 < kw) || (gmin_lo > wkmax));
+        };
+        // EFAST: R_q = exp((q - w~_q - wkmin) / tau) of tile tt's queries, one per lane, into
+        // row tt & 1 (a NaN window - no band, no edge pair - gets 0, so u is never NaN)
+        auto put_rq = [&](int tt) {
+            if constexpr (MODE == kSoft && EFAST) {
+                const float wq = *rec_f(stage_of(tt), kRecWc, ql);
+                const float rq = fast_exp2(((float)(q_begin + tt * QT + ql - wkmin) - wq) * kit);
+                if (hh == 0) s_rq[wave][tt & 1][ql] = (rq == rq) ? rq : 0.f;
+            }
+        };
+        // P and dS of the tile in stage st (first query qsb) from its accumulators: sc = S - L
+        // (raw units, L the query's LSE / scale) and pc = dP - Delta, both started from the
+        // records. DIAG: the tile may hold pairs with q < key (the causal test is needed).
+        auto p_ds1 = [&](int st, int qsb, bool live, f32x16 &sc, const f32x16 &pc, int row, auto with_edge,
+                         auto diag, uint32_t (&pkp)[8], uint32_t (&pks)[8]) {
+            constexpr bool WE = decltype(with_edge)::value;
+            constexpr bool DIAG = decltype(diag)::value;
+            const int Cj = (kvalid ? key : INT_MAX / 2) - qsb - hh * 4;  // q >= key <=> cst >= Cj
+            // lo(q) <= key <=> rec lo >= nkey; records hold INT_MAX - lo >= 0 (0 when out of
+            // range), so one unsigned compare against ~0 admits nothing
+            const uint32_t nk = (kvalid & live) ? (uint32_t)nkey : 0xFFFFFFFFu;
+            if constexpr (MODE == kSoft && !EFAST) {
+                const int gmax_clo = INT_MAX - *rec_i(st, kRecGClo, 0);
+                if (live && gmax_clo > wkmin) {
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int qi = g * 8 + hh * 4;
+                        const int4 c4 = *reinterpret_cast<const int4 *>(rec_i(st, kRecClo, qi));
+                        const float4 w4 = *reinterpret_cast<const float4 *>(rec_f(st, kRecWc, qi));
+                        const int ca[4] = {c4.x, c4.y, c4.z, c4.w};
+                        const float wa[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int r = g * 4 + e;
+                            float oms;
+                            const float eb = soft_edge_log2(wa[e], (float)(acc_row_const(r) - Cj), p.inv_tau, oms);
+                            sc[r] += (nkey > ca[e]) ? eb * p.inv_c2 : 0.f;  // key < corelo(q), raw-score units
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int qi = g * 8 + hh * 4;
+                const int4 o4 = *reinterpret_cast<const int4 *>(rec_i(st, kRecLo, qi));
+                const uint32_t oa[4] = {(uint32_t)o4.x, (uint32_t)o4.y, (uint32_t)o4.z, (uint32_t)o4.w};
+                int ca[4] = {0, 0, 0, 0};
+                float ra[4] = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (WE) {
+                    const int4 c4 = *reinterpret_cast<const int4 *>(rec_i(st, kRecClo, qi));
+                    const float4 r4 = *reinterpret_cast<const float4 *>(&s_rq[wave][row][qi]);
+                    ca[0] = c4.x; ca[1] = c4.y; ca[2] = c4.z; ca[3] = c4.w;
+                    ra[0] = r4.x; ra[1] = r4.y; ra[2] = r4.z; ra[3] = r4.w;
+                }
+                float pr4[4], ds4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = g * 4 + e;
+                    bool ok = oa[e] >= nk;
+                    if constexpr (DIAG) ok = ok & (acc_row_const(r) >= Cj);
+                    // masked before the exp (exp2(-inf) = 0): a select, never a branch
+                    float pr = fast_exp2(ok ? sc[r] * c : -INFINITY);
+                    if constexpr (WE) {
+                        // u in [0, inf] (R_q >= 0, L_key > 0): sigma = 0 where it overflows,
+                        // which only masked pairs (P = 0) reach
+                        const float u = (nkey > ca[e]) ? ra[e] * lkey : 0.f;
+                        pr *= __builtin_amdgcn_rcpf(1.f + u);
+                    }
+                    pr4[e] = pr;
+                    ds4[e] = pr * pc[r];
+                }
+                pkp[g * 2] = DT::pack2(pr4[0], pr4[1]);
+                pkp[g * 2 + 1] = DT::pack2(pr4[2], pr4[3]);
+                pks[g * 2] = DT::pack2(ds4[0], ds4[1]);
+                pks[g * 2 + 1] = DT::pack2(ds4[2], ds4[3]);
+            }
+        };
+        // 32 x 32 accumulators of the tile in stage st started from record field f of its
+        // queries, plus the products of tile half `half` (0: Q, 1: dO) with the lane's key
+        // row `kr` (kreg or vreg): lane = key column, registers = query rows
+        auto rec_mfma = [&](int st, int f, int half, const vec8 (&kr)[KS], f32x16 &acc) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const float4 v = *reinterpret_cast<const float4 *>(rec_f(st, f, g * 8 + hh * 4));
+                acc[4 * g] = v.x;
+                acc[4 * g + 1] = v.y;
+                acc[4 * g + 2] = v.z;
+                acc[4 * g + 3] = v.w;
+            }
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+                acc = DT::mfma(bitcast<vec8>(tile_read_row16<D>(s_tiles[st][half], ql, 2 * s + hh)), kr[s], acc);
+        };
+        // step t: dP - Delta of tile t and S - L of tile t+1 (MFMA) under P and dS of tile t
+        // (VALU), then dV/dK += of tile t
+        auto pstep = [&](int t, auto we, auto diag, f32x16 &sc, f32x16 &sn) {
+            constexpr bool WE = decltype(we)::value;
+            if (t + NSTAGE - 1 < ntile) issue_tile(t + NSTAGE - 1);
+            const int st = stage_of(t);
+            const int qsb = q_begin + t * QT;
+            const bool live = tile_live(st, qsb);
+            uint32_t pkp[8], pks[8];
+            f32x16 pc;
+            rec_mfma(st, kRecDelta, 1, vreg, pc);
+            // S of tile t+1 (landed; past the last tile a stale stage, ignored)
+            rec_mfma(stage_of(t + 1), kRecLse2, 0, kreg, sn);
+            p_ds1(st, qsb, live, sc, pc, t & 1, we, diag, pkp, pks);
+            if constexpr (!(MODE == kSoft && !EFAST)) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // dP initial values, dO operands
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // dP MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // S initial values, Q operands
+                    __builtin_amdgcn_sched_group_barrier(0x402, WE ? 10 : 6, 0);  // VALU (P)
+                }
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // S MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x402, WE ? 20 : 12, 0);  // VALU
+                }
+            }
+            put_rq(t + 1);
+            kv_mfma(s_tiles[st][0], s_tiles[st][1], 0, pkp, pks);
+            // tile t+2 must have landed (the next step's S); tiles t+3 .. t+NSTAGE-1 may
+            // stay in flight
+            if (t + NSTAGE - 1 < ntile) tile_barrier<(NSTAGE - 3) * LPT>();
+            else tile_barrier<0>();
+        };
+        // tiles 0 and 1 landed (tile 2 may be in flight)
+        if (ntile >= NSTAGE - 1) tile_barrier<(NSTAGE - 3) * LPT>();
+        else tile_barrier<0>();
+        f32x16 sA, sB;
+        rec_mfma(0, kRecLse2, 0, kreg, sA);
+        put_rq(0);
+        using yes = std::true_type;
+        using no = std::false_type;
+        // Steps 0 and 1 are the only ones with pairs q < key (tile t holds queries
+        // kb + 32 t .., wave w keys kb + 32 w ..); after them the next tile's S is in sA
+        // again. Then steps two at a time with the two S accumulators swapping roles; a loop
+        // that ends after an odd step leaves the next tile's S in sB and moves it to sA.
+        int t = 0;
+        if constexpr (MODE == kSoft && EFAST) {
+            // tile t has landed at the start of step t: its summary says whether it holds an
+            // edge pair; the edge phase starts at the first such tile
+            auto has_edge = [&](int tt) {
+                const int st = stage_of(tt);
+                const int gmax_clo = INT_MAX - __builtin_amdgcn_readfirstlane(*rec_i(st, kRecGClo, 0));
+                return tile_live(st, q_begin + tt * QT) && (gmax_clo > wkmin);
+            };
+            bool edge_on = false;
+            if (t < ntile) {
+                edge_on = has_edge(t);
+                if (edge_on) pstep(t, yes(), yes(), sA, sB);
+                else pstep(t, no(), yes(), sA, sB);
+                ++t;
+            }
+            if (t < ntile) {
+                edge_on = edge_on || has_edge(t);
+                if (edge_on) pstep(t, yes(), yes(), sB, sA);
+                else pstep(t, no(), yes(), sB, sA);
+                ++t;
+            }
+            if (!edge_on) {
+                while (t < ntile && !has_edge(t)) {
+                    pstep(t, no(), no(), sA, sB);
+                    if (++t >= ntile || has_edge(t)) {
+                        sA = sB;
+                        break;
+                    }
+                    pstep(t, no(), no(), sB, sA);
+                    ++t;
+                }
+            }
+            while (t < ntile) {
+                pstep(t, yes(), no(), sA, sB);
+                if (++t >= ntile) break;
+                pstep(t, yes(), no(), sB, sA);
+                ++t;
+            }
+        } else {
+            if (t < ntile) pstep(t++, no(), yes(), sA, sB);
+            if (t < ntile) pstep(t++, no(), yes(), sB, sA);
+            while (t < ntile) {
+                pstep(t, no(), no(), sA, sB);
+                if (++t >= ntile) break;
+                pstep(t, no(), no(), sB, sA);
+                ++t;
+            }
+        }
+    } else if (!LMK) {
         // Band: one basic block per tile of NSB 32-query sub-blocks (two at D = 128: the
         // masks, P and dS of sub-block 0 (VALU) run under the S/dP MFMAs of sub-block 1,
         // and sub-block 1's VALU work under the dV/dK MFMAs of sub-block 0). The band masks
@@ -873,7 +1078,7 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
                         const float wq = *rec_f(st, kRecWc, sb * 32 + ql);
                         const float rq = fast_exp2(((float)(qsb + ql - wkmin) - wq) * kit);
                         // a NaN window (no band, no edge pair) gets 0: u is never NaN
-                        if (hh == 0) s_rq[wave][ql] = (rq == rq) ? rq : 0.f;
+                        if (hh == 0) s_rq[wave][0][ql] = (rq == rq) ? rq : 0.f;
                         __builtin_amdgcn_wave_barrier();
                     }
 #pragma unroll
@@ -893,7 +1098,7 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
                         float ra[4] = {0.f, 0.f, 0.f, 0.f};
                         if constexpr (WE) {
                             const int4 c4 = *reinterpret_cast<const int4 *>(rec_i(st, kRecClo, qi));
-                            const float4 r4 = *reinterpret_cast<const float4 *>(&s_rq[wave][g * 8 + hh * 4]);
+                            const float4 r4 = *reinterpret_cast<const float4 *>(&s_rq[wave][0][g * 8 + hh * 4]);
                             ca[0] = c4.x; ca[1] = c4.y; ca[2] = c4.z; ca[3] = c4.w;
                             ra[0] = r4.x; ra[1] = r4.y; ra[2] = r4.z; ra[3] = r4.w;
                         }
@@ -903,7 +1108,7 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
                             const int r = g * 4 + e;
                             const bool ok = (acc_row_const(r) >= Cj) & (oa[e] >= nkey) & kv_ok;
                             // masked before the exp (exp2(-inf) = 0): a select, never a branch
-                            float pr = fast_exp2(ok ? fmaf(sacc[sb][r], c, -la[e]) : -INFINITY);
+                            float pr = fast_exp2(ok ? (sacc[sb][r] + la[e]) * c : -INFINITY);
                             if constexpr (WE) {
                                 // u in [0, inf] (R_q >= 0, L_key > 0): sigma = 0 where it
                                 // overflows, which only masked pairs (P = 0) reach
@@ -911,7 +1116,7 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
                                 pr *= __builtin_amdgcn_rcpf(1.f + u);
                             }
                             pr4[e] = pr;
-                            ds4[e] = pr * (pacc[sb][r] - da[e]);
+                            ds4[e] = pr * (pacc[sb][r] + da[e]);
                         }
                         pkp[sb][g * 2] = DT::pack2(pr4[0], pr4[1]);
                         pkp[sb][g * 2 + 1] = DT::pack2(pr4[2], pr4[3]);
@@ -1009,10 +1214,10 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
                         float pr;
                         if (LMK) {
                             // landmark admitted: key <= pmax(q) <=> key < rec pmax (key = INT_MAX when empty)
-                            pr = (key < oa[e]) ? fast_exp2(fmaf(sacc[r], c, kbias2 - la[e])) : 0.f;
+                            pr = (key < oa[e]) ? fast_exp2(fmaf(sacc[r] + la[e], c, kbias2)) : 0.f;
                         } else {
                             const bool ok = (!need_hi | (cst >= Cj)) & (!need_lo | (oa[e] >= nkey)) & kvalid;
-                            float x = fmaf(sacc[r], c, -la[e]);
+                            float x = (sacc[r] + la[e]) * c;
                             if (MODE == kSoft && need_edge) {
                                 float oms;
                                 const float edge = soft_edge_log2(wa[e], (float)(cst - Cj), p.inv_tau, oms);
@@ -1020,7 +1225,7 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
                             }
                             pr = ok ? fast_exp2(x) : 0.f;
                         }
-                        const float ds = pr * (pacc[r] - da[e]);
+                        const float ds = pr * (pacc[r] + da[e]);
                         if (LMK) dbias += ds;
                         pr4[e] = pr;
                         ds4[e] = ds;

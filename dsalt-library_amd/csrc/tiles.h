@@ -58,6 +58,17 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void *base, uint32_t bytes) {
     return r;
 }
 
+// A descriptor re-read as wave-uniform, for callers whose loops the compiler cannot
+// prove uniform: it may otherwise hold the descriptor in vector registers, which the "s"
+// operand of the direct loads below does not accept.
+__device__ __forceinline__ i32x4 uniform_rsrc(i32x4 r) {
+    r.x = __builtin_amdgcn_readfirstlane(r.x);
+    r.y = __builtin_amdgcn_readfirstlane(r.y);
+    r.z = __builtin_amdgcn_readfirstlane(r.z);
+    r.w = __builtin_amdgcn_readfirstlane(r.w);
+    return r;
+}
+
 // buffer_load_dwordx4 ... lds: lane i's 16 bytes at byte offset voff of the buffer land
 // at LDS byte m0 + 16 * i. `lds` must be wave-uniform (it is moved into m0).
 __device__ __forceinline__ void dma16(uint32_t voff, i32x4 rsrc, uint32_t lds) {
