@@ -10,19 +10,22 @@ namespace dsalt {
 // Forward: one workgroup of fwd_waves(D) waves owns fwd_bm(D) = 32 * fwd_waves(D)
 // consecutive queries of one (sequence, head); each wave owns 32 of them. Key tiles
 // hold fwd_bn(D) = 32 keys; K and V tiles each sit on an fwd_ring(D)-deep LDS ring
-// (2 + 2 tiles = 16 KB at D = 64, 3 + 3 = 48 KB at D = 128). The HARD kernel runs
+// (2 + 2 tiles = 16 KB at D = 64, 32 KB at D = 128). The HARD kernel runs
 // fwd_waves_per_simd(D, false) waves per SIMD: at D = 64 that is 4 (128 VGPRs, 8
 // workgroups per CU); the SOFT kernel keeps 3 (its edge factors need more registers).
-// The kernel also supports 64-key tiles and 4-wave workgroups. Landmark slots are
-// padded to a multiple of kFwdBN = 64, which every tile size divides. kFwdBM is the
+// At D = 128 both run 2 (about 210-230 VGPRs, 4 workgroups per CU, which the 35 KB of
+// LDS per workgroup also allows; 4-wave workgroups with a 3-deep ring ran the same
+// residency with twice the queries per key union: c4 167.7 against 158.4 us). The
+// kernel also supports 64-key tiles, 4-wave workgroups and 3-deep rings. Landmark slots
+// are padded to a multiple of kFwdBN = 64, which every tile size divides. kFwdBM is the
 // smallest block size (size checks).
 constexpr int kFwdBN = 64;
 constexpr int fwd_bn(int) { return 32; }
-constexpr int fwd_waves(int head_dim) { return head_dim == 64 ? 2 : 4; }
+constexpr int fwd_waves(int) { return 2; }
 constexpr int fwd_bm(int head_dim) { return 32 * fwd_waves(head_dim); }
 constexpr int kFwdBM = 64;
 constexpr int fwd_waves_per_simd(int head_dim, bool soft) { return head_dim == 64 ? (soft ? 3 : 4) : 2; }
-constexpr int fwd_ring(int head_dim) { return head_dim == 64 ? 2 : 3; }  // K / V ring depth
+constexpr int fwd_ring(int) { return 2; }  // K / V ring depth
 
 hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream);
 hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream);

@@ -15,7 +15,7 @@ import torch
 # v_mfma_f32_32x32x16.
 _GFX950_CONFIG = {
     64: {"BLOCK_M": 64, "BLOCK_N": 32, "BLOCK_N_BWD": 32, "num_warps": 2, "num_stages": 2},
-    128: {"BLOCK_M": 128, "BLOCK_N": 32, "BLOCK_N_BWD": 64, "num_warps": 4, "num_stages": 3},
+    128: {"BLOCK_M": 64, "BLOCK_N": 32, "BLOCK_N_BWD": 64, "num_warps": 2, "num_stages": 2},
 }
 
 
