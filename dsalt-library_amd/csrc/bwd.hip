@@ -22,12 +22,12 @@
 //           512 queries of one sequence); 4 waves = 2 slot groups x 2 query sub-blocks scan
 //           the chunk's queries in 64-query LDS tiles. Writes landmark dK/dV and d_bias
 //           partials per chunk (workspace).
-//   lmk_combine  sums the lmk_kv chunk partials of each (head, sequence) in a fixed
-//           order: d_lmk_bias, and each slot's landmark dK/dV (into the first chunk row).
 //   kv      key-parallel band dK/dV, kv_waves(D) waves x 32 keys per workgroup, scanning
 //           kv_qt(D)-query LDS tiles from the key block to the last dq query block whose
-//           band reaches it; keys that are landmark positions start from their combined
-//           landmark dK/dV; its head-0 workgroups reduce d_w~ over heads.
+//           band reaches it; keys that are landmark positions start from their landmark
+//           dK/dV (the lmk_kv chunk partials summed in chunk order in the prologue); its
+//           head-0 workgroups reduce d_w~ over heads, and H x S workgroups appended to its
+//           grid sum the d_bias partials of each (head, sequence).
 // Every MFMA is v_mfma_f32_32x32x16 with operands in the layouts of the forward kernel:
 // a lane owns one column (query or key) of each 32x32 block and 16 rows of it.
 #include "common.h"
@@ -594,6 +594,9 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     __shared__ __align__(1024) char s_tiles[NSTAGE][2][TB];  // [stage][Q, dO], row-swizzled
     __shared__ __align__(16) char s_rec[NSTAGE][kRecFields][RB];
     __shared__ int s_misc[8];
+    // band pass: one landmark slot's summed dK and dV rows, handed from the whole wave to
+    // the key's two lanes
+    __shared__ __align__(16) float s_lx[LMK ? 1 : NW][LMK ? 4 : 2 * D];
     // SOFT edge (EFAST): per wave, the query factors R_q of the current sub-block
     // (the D = 64 band loop double-buffers it: row t & 1 holds tile t's factors)
     __shared__ __align__(16) float s_rq[EFAST ? NW : 1][EFAST ? 2 : 1][EFAST ? 32 : 1];
@@ -601,6 +604,21 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ql = lane & 31, hh = lane >> 5;
 
+    if (!LMK && (int)blockIdx.x >= p.grid_q) {
+        // the landmark-bias gradient of (head, sequence) blockIdx.x - grid_q: the lmk_kv
+        // chunk partials summed in chunk order (zero for an empty sequence)
+        const int id = blockIdx.x - p.grid_q;
+        const int h = id / p.num_seqs, sq = id - h * p.num_seqs;
+        const int st0 = p.cu[sq], len = p.cu[sq + 1] - st0;
+        const int n_ch = (len + kLC - 1) / kLC;
+        const size_t base = (size_t)h * p.n_lchunk + st0 / kLC + sq;  // the sequence's first chunk row
+        for (int sl = threadIdx.x; sl < p.k_lmk; sl += NT) {
+            float acc = 0.f;
+            for (int ch = 0; ch < n_ch; ++ch) acc += p.ws_ldb[(base + ch) * p.k_pad + sl];
+            p.d_bias[((size_t)h * p.num_seqs + sq) * p.k_lmk + sl] = acc;
+        }
+        return;
+    }
     int head, seq, seq_start, seq_len, kblk = 0, q_begin, q_end, slot = 0, sbw = 0, kw = 0, lcid = 0;
     int key = INT_MAX;  // this lane's key position in the sequence (INT_MAX: none)
     float kbias2 = 0.f;
@@ -740,13 +758,21 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     for (int t = 0; t < NSTAGE - 1; ++t)
         if (t < ntile) issue_tile(t);
     if (!LMK && p.ws_ldk) {
-        // keys that are landmark positions start from their landmark dK/dV: the slot sums
-        // over the sequence's query chunks, which bwd_lmk_combine_kernel left in the first
-        // chunk's row (fixed order). These loads go out after the ring's first tiles, so
-        // that their latency overlaps the tiles'; they are consumed here, before the first
-        // counted wait, and the compiler's wait for them (for every load before them, the
-        // ring's included) leaves nothing of them in flight at that wait.
+        // Keys that are landmark positions start from their landmark dK/dV: the slot's
+        // lmk_kv partials summed over the sequence's query chunks in chunk order. The whole
+        // wave sums each such slot (lane j: DV consecutive floats of the dK row for j < 32,
+        // of the dV row for j >= 32; one load per chunk, all chunks in flight together) and
+        // hands the sums to the key's two lanes through LDS. These loads go out after the
+        // ring's first tiles, so that their latency overlaps the tiles'; they are consumed
+        // here, before the first counted wait, and the compiler's wait for them (for every
+        // load before them, the ring's included) leaves nothing of them in flight at that
+        // wait.
+        constexpr int DV = D / 32;  // floats per lane of one slot's dK + dV rows
+        typedef float fvec __attribute__((ext_vector_type(DV)));
         const int c_first = seq_start / kLC + seq;
+        const int n_ch = (seq_len + kLC - 1) / kLC;
+        const float *src0 = (lane < 32 ? p.ws_ldk : p.ws_ldv) + (lane & 31) * DV;
+        float *xch = s_lx[wave];
         for (int s0 = 0; s0 < p.k_lmk; s0 += 64) {
             int pos = -1;
             if (s0 + lane < p.k_lmk) {
@@ -758,23 +784,36 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
                 const int b = __ffsll((long long)m) - 1;
                 m &= m - 1;
                 const int pb = __shfl(pos, b);
+                const size_t row0 = ((size_t)head * p.n_lchunk + c_first) * p.k_pad + s0 + b;
+                const size_t cstride = (size_t)p.k_pad * D;  // floats between chunk rows of a slot
+                fvec acc = *reinterpret_cast<const fvec *>(src0 + row0 * D);
+                int ch = 1;
+                for (; ch + 4 <= n_ch; ch += 4) {
+                    fvec x[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        x[u] = *reinterpret_cast<const fvec *>(src0 + row0 * D + (size_t)(ch + u) * cstride);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) acc += x[u];
+                }
+                for (; ch < n_ch; ++ch) acc += *reinterpret_cast<const fvec *>(src0 + row0 * D + (size_t)ch * cstride);
+                *reinterpret_cast<fvec *>(xch + (lane < 32 ? 0 : D) + (lane & 31) * DV) = acc;
+                __builtin_amdgcn_wave_barrier();  // a wave's LDS operations run in order
                 if (key == pb) {
-                    const size_t row = ((size_t)head * p.n_lchunk + c_first) * p.k_pad + s0 + b;
-                    const float *gk = p.ws_ldk + row * D;
-                    const float *gv = p.ws_ldv + row * D;
 #pragma unroll
                     for (int d = 0; d < ND; ++d)
 #pragma unroll
                         for (int g = 0; g < 4; ++g) {
                             const int dd = d * 32 + g * 8 + hh * 4;
-                            const float4 a = *reinterpret_cast<const float4 *>(gk + dd);
-                            const float4 b4 = *reinterpret_cast<const float4 *>(gv + dd);
+                            const float4 a = *reinterpret_cast<const float4 *>(xch + dd);
+                            const float4 b4 = *reinterpret_cast<const float4 *>(xch + D + dd);
                             dk[d][g * 4 + 0] += a.x; dk[d][g * 4 + 1] += a.y;
                             dk[d][g * 4 + 2] += a.z; dk[d][g * 4 + 3] += a.w;
                             dv[d][g * 4 + 0] += b4.x; dv[d][g * 4 + 1] += b4.y;
                             dv[d][g * 4 + 2] += b4.z; dv[d][g * 4 + 3] += b4.w;
                         }
                 }
+                __builtin_amdgcn_wave_barrier();  // read before the next slot's write
             }
         }
     }
@@ -1330,44 +1369,6 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     }
 }
 
-// Landmark partials of lmk_kv summed over the query chunks of each sequence, in a fixed
-// order: d_bias[h, s, slot] (zero for empty sequences), and the dK/dV rows of every slot,
-// written into the sequence's first chunk row (read there by the band dK/dV pass). Grid
-// (head x sequence, column blocks): a thread sums one float4 column of dK and of dV, its
-// chunk loads issued four at a time.
-constexpr int kCombineThreads = 256;
-template <int D>
-__global__ void __launch_bounds__(kCombineThreads) bwd_lmk_combine_kernel(const BwdParams p) {
-    const int head = blockIdx.x / p.num_seqs, seq = blockIdx.x - head * p.num_seqs;
-    const int seq_start = p.cu[seq], seq_len = p.cu[seq + 1] - seq_start;
-    const int c_first = seq_start / kLC + seq, n_ch = (seq_len + kLC - 1) / kLC;
-    const size_t base = (size_t)head * p.n_lchunk + c_first;  // first chunk row of the sequence
-    if (p.d_bias && blockIdx.y == 0) {
-        for (int sl = threadIdx.x; sl < p.k_lmk; sl += kCombineThreads) {
-            float acc = 0.f;
-            for (int ch = 0; ch < n_ch; ++ch) acc += p.ws_ldb[(base + ch) * p.k_pad + sl];
-            p.d_bias[((size_t)head * p.num_seqs + seq) * p.k_lmk + sl] = acc;
-        }
-    }
-    constexpr int C4 = D / 4;  // float4 columns per row
-    const int e = blockIdx.y * kCombineThreads + threadIdx.x;
-    if (n_ch <= 1 || e >= p.k_lmk * C4) return;
-    const int sl = e / C4, c4 = e - sl * C4;
-    const size_t cs = (size_t)p.k_pad * D;  // floats between the same slot of consecutive chunks
-    const size_t off = (base * p.k_pad + sl) * D + 4 * c4;
-    float4 ak = *reinterpret_cast<const float4 *>(p.ws_ldk + off);
-    float4 av = *reinterpret_cast<const float4 *>(p.ws_ldv + off);
-#pragma unroll 4
-    for (int ch = 1; ch < n_ch; ++ch) {
-        const float4 bk = *reinterpret_cast<const float4 *>(p.ws_ldk + off + ch * cs);
-        const float4 bv = *reinterpret_cast<const float4 *>(p.ws_ldv + off + ch * cs);
-        ak.x += bk.x; ak.y += bk.y; ak.z += bk.z; ak.w += bk.w;
-        av.x += bv.x; av.y += bv.y; av.z += bv.z; av.w += bv.w;
-    }
-    *reinterpret_cast<float4 *>(p.ws_ldk + off) = ak;
-    *reinterpret_cast<float4 *>(p.ws_ldv + off) = av;
-}
-
 struct WsLayout {
     size_t qrec, minlo, dwh, ldk, ldv, ldb, total;
 };
@@ -1408,23 +1409,22 @@ hipError_t launch_typed(const BwdParams &p, hipStream_t stream) {
         hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE, MODE == kSoft>), dim3(p.grid_dq), dim3(64 * kDqW), dyn, stream, p);
     else
         hipLaunchKernelGGL((bwd_dq_kernel<DT, D, MODE, false>), dim3(p.grid_dq), dim3(64 * kDqW), dyn, stream, p);
-    if (p.k_lmk > 0) {
+    if (p.k_lmk > 0)
         hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, true, false>), dim3(p.n_heads * p.n_lgrp * p.n_lchunk), dim3(256),
                            0, stream, p);
-        const int col_blocks = (p.k_lmk * (D / 4) + kCombineThreads - 1) / kCombineThreads;
-        hipLaunchKernelGGL(bwd_lmk_combine_kernel<D>, dim3(p.n_heads * p.num_seqs, col_blocks), dim3(kCombineThreads), 0,
-                           stream, p);
-    }
+    // the band pass also sums the landmark partials: each landmark key's dK/dV in its
+    // prologue, d_bias in H x S workgroups appended to its grid
+    const int grid_kv = p.grid_q + ((p.k_lmk > 0 && p.d_bias) ? p.n_heads * p.num_seqs : 0);
     // the factored edge path of the band dK/dV kernel exists at D = 64 only (at D = 128 its
     // second tile loop does not fit the scalar registers)
     constexpr bool kKvFast = MODE == kSoft && D == 64;
     bool kv_fast = false;
     if constexpr (kKvFast) kv_fast = kv_edge_fast(p);
     if (kv_fast)
-        hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false, kKvFast>), dim3(p.grid_q), dim3(64 * kv_waves(D)), 0,
+        hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false, kKvFast>), dim3(grid_kv), dim3(64 * kv_waves(D)), 0,
                            stream, p);
     else
-        hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false, false>), dim3(p.grid_q), dim3(64 * kv_waves(D)), 0,
+        hipLaunchKernelGGL((bwd_kv_kernel<DT, D, MODE, false, false>), dim3(grid_kv), dim3(64 * kv_waves(D)), 0,
                            stream, p);
     return hipGetLastError();
 }
