@@ -570,7 +570,8 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
 // (direct global->LDS loads, one barrier per tile): band workgroups are kv_waves(D)
 // waves with kv_qt(D)-query tiles on a kv_stages(D)-deep ring (2 waves, 32 queries, 4
 // stages = 36 KB at D = 64: registers, not LDS, limit it to 4 workgroups per CU),
-// lmk_kv workgroups 4 waves with 64-query tiles on a 4-stage ring. Per 32-query
+// lmk_kv workgroups 4 waves with 64-query tiles on a 2-stage ring (37 KB; 4 stages, 74 KB,
+// halved the workgroups per CU and measured 1.5 us slower at c3). Per 32-query
 // sub-block: S = Q.K^T and dP = dO.V^T (lane = key column, registers = query rows),
 // P = 2^(S c + bias - lse2) on admitted pairs, dS = P (dP - Delta), then dV^T += dO^T.P
 // and dK^T += Q^T.dS with Q and dO read transposed.
@@ -584,7 +585,7 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
     constexpr int KS = D / 16, ND = D / 32;
     typedef TileN<D, QT, NW> Tile;
     constexpr int TB = Tile::BYTES;
-    constexpr int NSTAGE = LMK ? 4 : kv_stages(D);
+    constexpr int NSTAGE = LMK ? 2 : kv_stages(D);
     constexpr int RB = QT * 4;                         // bytes of one record field per tile
     constexpr int FPI = 64 / QT;                       // record fields per 64-lane load
     constexpr int RLW = kRecFields / (FPI * NW);       // record loads per wave per tile
@@ -1326,30 +1327,31 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
         // combine the two query sub-blocks of each slot group (waves 2g+1 into 2g), fixed
         // order, through LDS (the tile ring is idle after the last barrier)
         float *red = reinterpret_cast<float *>(&s_tiles[0][0][0]);
-        constexpr int PER_LANE = 2 * ND * 16 + 1;
+        constexpr int PER_LANE = ND * 16 + 1;  // dK (then dV) of a lane, and its d_bias term
         static_assert(!LMK || 2 * 64 * PER_LANE * 4 <= sizeof(s_tiles), "reduction scratch");
         const int g = wave >> 1;
         float *mine = red + (size_t)(g * 64 + lane) * PER_LANE;
-        if (sbw == 1) {
 #pragma unroll
-            for (int d = 0; d < ND; ++d)
+        for (int half = 0; half < 2; ++half) {
+            f32x16 (&acc)[ND] = half ? dv : dk;
+            if (sbw == 1) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    mine[d * 16 + r] = dk[d][r];
-                    mine[ND * 16 + d * 16 + r] = dv[d][r];
-                }
-            mine[2 * ND * 16] = dbias;
+                for (int d = 0; d < ND; ++d)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) mine[d * 16 + r] = acc[d][r];
+                if (half == 0) mine[ND * 16] = dbias;
+            }
+            __syncthreads();
+            if (sbw == 0) {
+#pragma unroll
+                for (int d = 0; d < ND; ++d)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[d][r] += mine[d * 16 + r];
+                if (half == 0) dbias += mine[ND * 16];
+            }
+            __syncthreads();
         }
-        __syncthreads();
         if (sbw == 0) {
-#pragma unroll
-            for (int d = 0; d < ND; ++d)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    dk[d][r] += mine[d * 16 + r];
-                    dv[d][r] += mine[ND * 16 + d * 16 + r];
-                }
-            dbias += mine[2 * ND * 16];
             const float db = half_sum(dbias);
             const size_t row = ((size_t)head * p.n_lchunk + lcid) * p.k_pad + slot;
             float *gk = p.ws_ldk + row * D;
