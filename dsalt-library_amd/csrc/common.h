@@ -197,7 +197,12 @@ struct MaxOp {
 __device__ __forceinline__ int wave_min_u(int x) { return wave_reduce_dpp(x, MinOp()); }
 __device__ __forceinline__ int wave_max_u(int x) { return wave_reduce_dpp(x, MaxOp()); }
 
-enum { kHard = 0, kSoft = 1 };
+// Window modes of the kernels. kSoft and kSoftWide have the same SOFT semantics and
+// differ only in how the forward applies the window edge: kSoft starts the scores of
+// each query from a short row of edge biases (at most ceil(win_edge) = 4 edge keys);
+// kSoftWide computes the bias on every band element below the core (wider edges). The
+// backward instantiates kHard and kSoft only.
+enum { kHard = 0, kSoft = 1, kSoftWide = 2 };
 
 // Key ranges of query offset i (all inclusive, relative to its sequence) given its
 // window value wv:

@@ -44,6 +44,16 @@ namespace dsalt {
 namespace {
 
 constexpr float kStaleMax = 8.0f;  // allowed growth of the row max before a rescale (log2)
+// SOFT: win_edge <= kEdgeTab runs kSoft, whose score accumulators start from a per-query
+// row of kEtabLen initial values. The row holds ceil(win_edge) <= kEdgeTab edge keys,
+// which is every edge while w~ - win_edge is exact in fp32 (w~ < 2^25). Wider edges run
+// kSoftWide (edge bias computed on every band element below the core).
+constexpr int kEdgeTab = 4;
+constexpr int kEtabLen = kEdgeTab + 8;  // entries per query row: keys lo - 4 .. lo + kEdgeTab + 3
+// row of query q (of the workgroup) at q * kEtabLen + q / 8: with kEtabLen = 12 the 32
+// rows of a wave then start in 32 different banks
+__host__ __device__ constexpr int etab_row(int q) { return q * kEtabLen + (q >> 3); }
+static_assert(kEdgeTab == 4, "edge table rows are laid out for 4 edge keys");
 // Band mask table: acc_row_const(r) <= 27 for the 16 accumulator elements of a lane, so
 // rows d = 0 (nothing masked) .. 28 (everything masked) cover every clamped bound.
 constexpr int kMaskRows = 29;
@@ -72,7 +82,7 @@ struct FwdParams {
 };
 
 template <typename DT, int D, int MODE>
-__global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE == kSoft)) fwd_kernel(const FwdParams p) {
+__global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE == kSoftWide)) fwd_kernel(const FwdParams p) {
     typedef typename DT::vec8 vec8;
     constexpr int NW = fwd_waves(D);        // waves per workgroup
     constexpr int BM = 32 * NW;             // queries per workgroup
@@ -92,7 +102,10 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     // Band mask rows: row d holds, per accumulator element r of a 32-key row block, -inf
     // when the element's row offset acc_row_const(r) is below d, else 0 (rows padded to
     // 80 bytes so that lanes reading different rows spread over the banks).
-    __shared__ __align__(16) float s_mtab[kMaskRows][kMaskStride];
+    __shared__ __align__(16) float s_mtab[MODE == kSoft ? 1 : kMaskRows][kMaskStride];
+    // kSoft: per query, the initial scores of keys lo - 4 .. lo + kEdgeTab + 3 (-inf below
+    // the band, the edge biases, 0 in the core)
+    __shared__ float s_etab[MODE == kSoft ? etab_row(BM) : 1];
     extern __shared__ int s_dyn[];
     int *s_lpos = s_dyn;                                          // INT_MAX: empty slot
     float *s_lbias = reinterpret_cast<float *>(s_dyn + p.k_pad);  // raw-unit bias
@@ -258,7 +271,7 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     int lo, corelo, pmax;
     query_ranges<MODE>(i, wv, p.win_edge, lo, corelo, pmax);
     const int wlo = wave_min_u(qvalid ? lo : INT_MAX);
-    const int wclo = wave_max_u(qvalid ? corelo : INT_MIN);
+    const int wclo = MODE == kSoftWide ? wave_max_u(qvalid ? corelo : INT_MIN) : INT_MIN;
     const int wpmax = wave_max_u(qvalid ? pmax : -1);
 
     // ---- landmark slots -> LDS (invalid / out-of-sequence slots become INT_MAX) --------
@@ -292,9 +305,26 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
         s_red[wave][0] = wlo;
         s_red[wave][1] = wpmax;
     }
-    for (int e = tid; e < kMaskRows * 16; e += NT) {
-        const int d = e >> 4, r = e & 15;
-        s_mtab[d][r] = acc_row_const(r) < d ? -INFINITY : 0.f;
+    if constexpr (MODE != kSoft) {
+        for (int e = tid; e < kMaskRows * 16; e += NT) {
+            const int d = e >> 4, r = e & 15;
+            s_mtab[d][r] = acc_row_const(r) < d ? -INFINITY : 0.f;
+        }
+    } else {
+        // the query's row: entry x + 4 holds the initial score of key lo + x, x = -4 ..
+        // kEdgeTab + 3: -inf below the band, the edge bias log sigmoid((w~ - d) / tau) in
+        // raw units for lo <= key < corelo (dsalt_triton_train.py:151-155), 0 in the core.
+        // The lane pair splits the row.
+        constexpr int EH = kEtabLen / 2;
+        float *erow = s_etab + etab_row(wave * 32 + ql);
+        const int ne = corelo - lo;
+#pragma unroll
+        for (int e = 0; e < EH; ++e) {
+            const int x = hh * EH + e - 4;
+            float oms;
+            const float edge = soft_edge_log2(wv, (float)(i - lo - x), p.inv_tau, oms) * p.inv_c;
+            erow[hh * EH + e] = x < 0 ? -INFINITY : (x < ne ? edge : 0.f);
+        }
     }
     // LDS writes visible to the workgroup; the tile loads stay in flight
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -331,21 +361,46 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     // acc_row_const(r) < lo - tb - 32 rb - 4 hh = mb + BN t - 32 rb, so its initial value
     // is mask row clamp(mb + BN t - 32 rb, 0, 28): -inf there (the MFMA keeps it -inf), 0
     // elsewhere. No VALU touches the elements; landmark tiles start from row 0 (zeros).
+    // kSoft instead reads the initial values from the query's edge row, four consecutive
+    // keys (elements 4g .. 4g + 3) at a time: the entries of keys x .. x + 3 relative to
+    // lo with x clamped to [-4, kEdgeTab] (one v_med3 and two ds_read2 per group; all four
+    // entries are -inf below the clamp and 0 above it; landmark tiles clamp to the top,
+    // 0): the band's lower edge and the SOFT edge bias together.
     const int mb = lo - ghi + BN - 1 - hh * 4;
     auto qk_tile = [&](int t, int slot, f32x16 (&sacc)[NRB]) {
         const char *ktile = s_tiles[0][slot];
+        // kSoft: the edge row from the lane id, per tile (opaque: not held across the loop)
+        int el = 0;
+        if constexpr (MODE == kSoft) {
+            el = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+            asm volatile("" : "+v"(el));
+        }
+        const float *erow = s_etab + etab_row(wave * 32 + (el & 31)) + 4;
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb) {
-            const int d = (t < nb) ? min(max(mb + BN * t - 32 * rb, 0), kMaskRows - 1) : 0;
-            const float4 *mrow = reinterpret_cast<const float4 *>(&s_mtab[d][0]);
             f32x16 acc;
+            if constexpr (MODE == kSoft) {
+                const int x0 = (t < nb) ? -(mb + BN * t - 32 * rb) : (1 << 20);  // key - lo of row offset 0
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const float4 m4 = mrow[g];
-                acc[4 * g + 0] = m4.x;
-                acc[4 * g + 1] = m4.y;
-                acc[4 * g + 2] = m4.z;
-                acc[4 * g + 3] = m4.w;
+                for (int g = 0; g < 4; ++g) {
+                    const int y = min(max(x0, -4 - 8 * g), kEdgeTab - 8 * g);
+                    const float *e4 = erow + 8 * g + y;
+                    acc[4 * g + 0] = e4[0];
+                    acc[4 * g + 1] = e4[1];
+                    acc[4 * g + 2] = e4[2];
+                    acc[4 * g + 3] = e4[3];
+                }
+            } else {
+                const int d = (t < nb) ? min(max(mb + BN * t - 32 * rb, 0), kMaskRows - 1) : 0;
+                const float4 *mrow = reinterpret_cast<const float4 *>(&s_mtab[d][0]);
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 m4 = mrow[g];
+                    acc[4 * g + 0] = m4.x;
+                    acc[4 * g + 1] = m4.y;
+                    acc[4 * g + 2] = m4.z;
+                    acc[4 * g + 3] = m4.w;
+                }
             }
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
@@ -365,15 +420,15 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     float mu = 0.f;        // exponent offset: m2, or 0 while m2 is -inf
     float lsum0 = 0.f, lsum1 = 0.f;
     const float c = p.c;
-    // SOFT edge factors: for element slot j (tile row offset cst_j), exp(-z) of the edge
+    // kSoftWide edge factors: for element slot j (tile row offset cst_j), exp(-z) of the edge
     // logit z = (w~ - d) / tau splits as E * ec[j] with E = exp((A - w~ - mid) / tau) per
     // lane and tile and ec[j] = exp((mid - cst_j) / tau) fixed. Every factor stays in the
     // fp32 range while (win_edge + 1 + 16 NRB) / tau < 80 (edge keys have
     // 0 <= z < (win_edge + 1) / tau); otherwise each element takes its own exp.
     constexpr float kEdgeMid = 16.f * NRB - 2.5f;
-    const bool edge_fast = MODE == kSoft && (p.win_edge + 1.f + 16.f * NRB) * p.inv_tau < 80.f;
-    float ec[MODE == kSoft ? 16 * NRB : 1];
-    if constexpr (MODE == kSoft) {
+    const bool edge_fast = MODE == kSoftWide && (p.win_edge + 1.f + 16.f * NRB) * p.inv_tau < 80.f;
+    float ec[MODE == kSoftWide ? 16 * NRB : 1];
+    if constexpr (MODE == kSoftWide) {
 #pragma unroll
         for (int j = 0; j < 16 * NRB; ++j)
             ec[j] = fast_exp2((kEdgeMid - (float)((j >> 4) * 32 + acc_row_const(j & 15))) * p.inv_tau * kLog2e);
@@ -410,8 +465,8 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
         }
     };
     // Per-element adjustments that only some tiles need, applied in place to the raw
-    // scores of tile t (t < nt): landmark admission (p <= p_max(i)) and bias, and the
-    // SOFT edge bias of band tiles that reach below a row's core.
+    // scores of tile t (t < nt): landmark admission (p <= p_max(i)) and bias, and (kSoftWide)
+    // the SOFT edge bias of band tiles that reach below a row's core.
     auto adjust = [&](int t, f32x16 (&sacc)[NRB]) {
         if (t >= nb) {
             const int lt = lmk_tile(t);
@@ -430,7 +485,7 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
                         sacc[rb][r] = (pp[e] <= pmax) ? sacc[rb][r] + bb[e] : -INFINITY;
                     }
                 }
-        } else if (MODE == kSoft && band_key0(t) < wclo) {
+        } else if (MODE == kSoftWide && band_key0(t) < wclo) {
             const int tb = band_key0(t);
             const int A = i - tb - hh * 4;
             const int Bc = corelo - tb - hh * 4;  // key >= corelo <=> cst >= Bc
@@ -649,11 +704,14 @@ hipError_t launch_typed(const FwdParams &p, size_t dyn, hipStream_t stream) {
 
 template <typename DT>
 hipError_t launch_dt(const FwdParams &p, int head_dim, int mode, size_t dyn, hipStream_t stream) {
-    if (head_dim == 64)
-        return mode == DSALT_MODE_HARD ? launch_typed<DT, 64, kHard>(p, dyn, stream)
-                                       : launch_typed<DT, 64, kSoft>(p, dyn, stream);
-    return mode == DSALT_MODE_HARD ? launch_typed<DT, 128, kHard>(p, dyn, stream)
-                                   : launch_typed<DT, 128, kSoft>(p, dyn, stream);
+    // SOFT edges of at most kEdgeTab keys per query start the scores from the edge rows
+    const bool wide = mode == DSALT_MODE_SOFT && !(p.win_edge <= (float)kEdgeTab);
+    if (head_dim == 64) {
+        if (mode == DSALT_MODE_HARD) return launch_typed<DT, 64, kHard>(p, dyn, stream);
+        return wide ? launch_typed<DT, 64, kSoftWide>(p, dyn, stream) : launch_typed<DT, 64, kSoft>(p, dyn, stream);
+    }
+    if (mode == DSALT_MODE_HARD) return launch_typed<DT, 128, kHard>(p, dyn, stream);
+    return wide ? launch_typed<DT, 128, kSoftWide>(p, dyn, stream) : launch_typed<DT, 128, kSoft>(p, dyn, stream);
 }
 
 }  // namespace

@@ -12,8 +12,9 @@ namespace dsalt {
 // hold fwd_bn(D) = 32 keys; K and V tiles each sit on an fwd_ring(D)-deep LDS ring
 // (2 + 2 tiles = 16 KB at D = 64, 32 KB at D = 128). The HARD kernel runs
 // fwd_waves_per_simd(D, false) waves per SIMD: at D = 64 that is 4 (128 VGPRs, 8
-// workgroups per CU); the SOFT kernel keeps 3 (its edge factors need more registers).
-// At D = 128 both run 2 (about 210-230 VGPRs, 4 workgroups per CU, which the 35 KB of
+// workgroups per CU), and so does the SOFT kernel whose scores start from per-query edge
+// rows; the wide-edge SOFT kernel (win_edge > 4, edge bias computed per element) keeps 3
+// (its edge factors need more registers). At D = 128 all run 2 (about 210-230 VGPRs, 4 workgroups per CU, which the 35 KB of
 // LDS per workgroup also allows; 4-wave workgroups with a 3-deep ring ran the same
 // residency with twice the queries per key union: c4 167.7 against 158.4 us). The
 // kernel also supports 64-key tiles, 4-wave workgroups and 3-deep rings. Landmark slots
@@ -24,7 +25,7 @@ constexpr int fwd_bn(int) { return 32; }
 constexpr int fwd_waves(int) { return 2; }
 constexpr int fwd_bm(int head_dim) { return 32 * fwd_waves(head_dim); }
 constexpr int kFwdBM = 64;
-constexpr int fwd_waves_per_simd(int head_dim, bool soft) { return head_dim == 64 ? (soft ? 3 : 4) : 2; }
+constexpr int fwd_waves_per_simd(int head_dim, bool wide_edge) { return head_dim == 64 ? (wide_edge ? 3 : 4) : 2; }
 constexpr int fwd_ring(int) { return 2; }  // K / V ring depth
 
 hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream);

@@ -398,12 +398,14 @@ def test_fwd_many_landmarks(mode, D, k):
 
 
 @pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("tau,edge", [(1.0, 4.0), (0.5, 2.5), (0.15, 4.0), (3.0, 9.0)],
-                         ids=["t1-e4", "t0.5-e2.5", "t0.15-e4", "t3-e9"])
+@pytest.mark.parametrize("tau,edge", [(1.0, 4.0), (0.5, 2.5), (0.15, 4.0), (1.0, 8.0), (3.0, 9.0), (0.15, 12.0)],
+                         ids=["t1-e4", "t0.5-e2.5", "t0.15-e4", "t1-e8", "t3-e9", "t0.15-e12"])
 def test_fwd_soft_edge_params(D, tau, edge):
-    """SOFT edge bias log sigmoid((w~ - d) / tau) over tau and win_edge: the factored
-    exp(-z) = E * ec[j] (one log per element) where (win_edge + 1 + 16 NRB) / tau < 80,
-    the per-element exp otherwise (tau = 0.15)."""
+    """SOFT edge bias log sigmoid((w~ - d) / tau) over tau and win_edge. win_edge <= 4
+    starts the scores from per-query rows of edge biases (the first three cases); wider
+    edges bias every band element in the loop, with the factored exp(-z) = E * ec[j] (one
+    log per element) where (win_edge + 1 + 16 NRB) / tau < 80 (win_edge 8 and 9) and the
+    per-element exp otherwise (tau = 0.15, win_edge 12)."""
     print(f"fwd soft edge D={D} tau={tau} edge={edge}", flush=True)
     lens, H, k = [400, 130], 2, 12
     q, kk, v, w, pos, bias, cu = make_inputs(lens, H, D, k, hip.MODE_SOFT, seed=41, n_min=2, n_max=120)
