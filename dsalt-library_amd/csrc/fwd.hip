@@ -637,7 +637,14 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     using no_causal_edge = std::false_type;
     qk_tile(0, slot_of(0), sA);
     adjust(0, sA);
-    rescale(true, mask_max(causal_edge(), 0, sA));
+    {
+        // the first tile's max: O and l are still zero, so nothing is rescaled
+        const float tmax = mask_max(causal_edge(), 0, sA);
+        const bool raise = tmax > thr;
+        m2 = raise ? tmax * c : m2;
+        mu = (m2 == -INFINITY) ? 0.f : m2;
+        thr = raise ? tmax + kStaleMax * p.inv_c : thr;
+    }
     // step 0 refills the slot of K of tile 0: every wave must have read it first
     tile_barrier<(R - 2) * LPT>();
     // steps 0 .. NC-2 mask the causal edge of tiles 1 .. NC-1; later tiles lie below every
