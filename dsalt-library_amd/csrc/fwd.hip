@@ -70,6 +70,7 @@ struct FwdParams {
     int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, o_st, o_sh, lse_st, lse_sh, w_st;
     int64_t lp_sh, lp_ss, lp_sk, lb_sh, lb_ss, lb_sk;
     int total_len, num_seqs, n_heads, k_lmk, k_pad, n_qblk, grid, out_f32;
+    int prio_span;    // > 0: wave priority by dispatch order over the first prio_span workgroups
     int kv_rep;       // query heads per K/V head
     const float *rope_cos, *rope_sin;  // non-null: rotate Q on load (RoPE tables [rope_rows][D])
     int64_t rope_st;
@@ -631,6 +632,18 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
         if (t + R < nt) tile_barrier<(R - 2) * LPT>();
         else tile_barrier<0>();
     };
+    // Wave priority by dispatch order (grids of at most two dispatch rounds): the
+    // workgroups of a round start together, but the later-dispatched ones get their
+    // set-up loads served last and start their tile loops up to ~5 us later (c2), so the
+    // loop issues the later quarters of the round first (s_setprio 1 .. 3; workgroups of a
+    // second round 3).
+    if (p.prio_span > 0) {
+        const int pq = __builtin_amdgcn_readfirstlane(
+            (int)blockIdx.x < p.prio_span ? (int)(((int64_t)blockIdx.x * 4) / p.prio_span) : 3);
+        if (pq == 1) __builtin_amdgcn_s_setprio(1);
+        else if (pq == 2) __builtin_amdgcn_s_setprio(2);
+        else if (pq >= 3) __builtin_amdgcn_s_setprio(3);
+    }
     f32x16 sA[NRB], sB[NRB];
     tile_barrier<(R - 2) * LPT>();  // K of tiles 0, 1 and V of tile 0 landed
     using causal_edge = std::true_type;
@@ -704,7 +717,16 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
 }
 
 template <typename DT, int D, int MODE>
-hipError_t launch_typed(const FwdParams &p, size_t dyn, hipStream_t stream) {
+hipError_t launch_typed(FwdParams p, size_t dyn, hipStream_t stream) {
+    // workgroups resident at once (one dispatch round): the wave-priority span
+    int dev = 0, n_cu = 0, per_cu = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fwd_kernel<DT, D, MODE>, 64 * fwd_waves(D), dyn) ==
+            hipSuccess) {
+        const int64_t round = (int64_t)n_cu * per_cu;
+        p.prio_span = (round > 0 && p.grid <= 2 * round) ? (int)(p.grid < round ? p.grid : round) : 0;
+    }
     hipLaunchKernelGGL((fwd_kernel<DT, D, MODE>), dim3(p.grid), dim3(64 * fwd_waves(D)), dyn, stream, p);
     return hipGetLastError();
 }
@@ -759,6 +781,7 @@ hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream) {
     p.n_qblk = block_upper_bound(a.total_len, a.num_seqs, fwd_bm(a.head_dim));
     const int64_t blocks = (int64_t)p.n_qblk * a.n_heads;
     p.grid = (int)((blocks + 7) / 8 * 8);
+    p.prio_span = 0;  // set per kernel in launch_typed
     p.q_sign = a.scale < 0.f ? 0x80008000u : 0u;
     p.c = fabsf(a.scale) * kLog2e;
     p.inv_c = 1.f / p.c;
