@@ -38,6 +38,7 @@
 #include "launch.h"
 #include "tiles.h"
 
+#include <atomic>
 #include <type_traits>
 
 namespace dsalt {
@@ -96,6 +97,15 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     constexpr int TB = Tile::BYTES;
     constexpr int R = fwd_ring(D);                     // depth of the K ring and of the V ring
     constexpr int LPT = 2 * Tile::LOADS_PER_WAVE;      // load instructions per tile per wave
+    constexpr int NC = BM / BN;                        // band tiles reaching past a wave's first query
+    static_assert(NC >= 1 && NC <= 4, "causal peel covers at most four tiles");
+    static_assert(R <= NC, "the tiles issued before the set-up are peel band tiles");
+    // The first attempt keeps the exponent offset mu where the diagonal tiles (which hold
+    // every query's own key) put it and takes no row max after them: P = 2^(S c - mu) may
+    // then exceed the usual 2^8, which needs the 16-bit type to have the exponent range of
+    // fp32: bf16. (The wide-edge SOFT kernel, whose edge factors fill the registers, keeps
+    // the single attempt.)
+    constexpr bool kTryFast = std::is_same<DT, BF16>::value && MODE != kSoftWide;
 
     __shared__ __align__(1024) char s_tiles[2][R][TB];  // [K, V][slot]
     __shared__ int s_red[NW][2];
@@ -132,19 +142,21 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     const int ghi = min(blk * BM + BM - 1, seq_len - 1);  // last query of the workgroup
 
     // ---- tile staging: direct global -> LDS loads ----------------------------------------
-    // Band tiles run from the diagonal down: tile t holds keys ghi-BN+1-BN*t .. ghi-BN*t, so
-    // the first tiles are known before the windows are read and their loads overlap the
-    // setup. Landmark tiles follow the band tiles. K/V rows are read through buffer
-    // resources whose range is this (sequence, head): rows below the sequence start
-    // (wrapped offsets) read as zeros, empty landmark slots load row 0; the masks give
-    // all of them probability 0.
+    // Tile order: the NC band tiles of the diagonal (t < NC; band tile b holds keys
+    // ghi-BN+1-BN*b .. ghi-BN*b, so they are known before the windows are read and their
+    // loads overlap the setup), then the landmark tiles, then the remaining band tiles
+    // from the diagonal down. A wave whose own band ends before the workgroup's has its
+    // idle tiles last and only takes part in the loads and barriers for them. K/V rows are
+    // read through buffer resources whose range is this (sequence, head): rows below the
+    // sequence start (wrapped offsets) read as zeros, empty landmark slots load row 0; the
+    // masks give all of them probability 0.
     const uint32_t kst = (uint32_t)p.k_st * 2u, vst = (uint32_t)p.v_st * 2u;  // row strides (bytes)
     const i32x4 krs = buffer_rsrc(p.k + (int64_t)seq_start * p.k_st + (int64_t)kv_head(head, p.kv_rep) * p.k_sh, (uint32_t)seq_len * kst);
     const i32x4 vrs = buffer_rsrc(p.v + (int64_t)seq_start * p.v_st + (int64_t)kv_head(head, p.kv_rep) * p.v_sh, (uint32_t)seq_len * vst);
     const TileLanes<D, kSwzRow, BN, NW> klanes(wave, lane, kst);
     const TileLanes<D, kSwzTr, BN, NW> vlanes(wave, lane, vst);
     const uint32_t tiles_lds = lds_addr(&s_tiles[0][0][0]);
-    auto band_key0 = [&](int t) { return ghi - (BN - 1) - t * BN; };
+    auto band_key0 = [&](int b) { return ghi - (BN - 1) - b * BN; };
     auto slot_of = [](int t) { return t % R; };  // ring slot of tile t >= 0, wave-uniform
     auto k_lds = [&](int t) { return tiles_lds + slot_of(t) * TB; };
     auto v_lds = [&](int t) { return tiles_lds + (R + slot_of(t)) * TB; };
@@ -313,9 +325,9 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
         }
     } else {
         // the query's row: entry x + 4 holds the initial score of key lo + x, x = -4 ..
-        // kEdgeTab + 3: -inf below the band, the edge bias log sigmoid((w~ - d) / tau) in
-        // raw units for lo <= key < corelo (dsalt_triton_train.py:151-155), 0 in the core.
-        // The lane pair splits the row.
+        // kEdgeTab + 3: -inf below the band, the edge bias log2 sigmoid((w~ - d) / tau)
+        // for lo <= key < corelo (dsalt_triton_train.py:151-155), 0 in the core. The lane
+        // pair splits the row.
         constexpr int EH = kEtabLen / 2;
         float *erow = s_etab + etab_row(wave * 32 + ql);
         const int ne = corelo - lo;
@@ -338,38 +350,50 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     // landmark tiles holding at least one position admissible for the workgroup
     const int n_lt = p.k_pad / BN;
     const uint64_t lmask = __ballot(lane < n_lt && s_ltmin[lane < n_lt ? lane : 0] <= gpmax);
-    // band tiles (at least the R issued above; extra ones are inactive)
-    const int nb = max((ghi - glo) / BN + 1, R);
-    const int nt = nb + __popcll(lmask);
-    auto lmk_tile = [&](int t) {  // landmark tile of iteration t >= nb: (t-nb)-th set bit
+    const int nl = __popcll(lmask);
+    // band tiles of the workgroup (at least the NC of the peel; extra ones are inactive)
+    const int nb = max((ghi - glo) / BN + 1, NC);
+    const int nt = nb + nl;
+    // tile t: band tile t for t < NC, landmark tile for NC <= t < NC + nl, band tile t - nl after
+    auto is_lmk = [&](int t) { return t >= NC && t < NC + nl; };
+    auto band_of = [&](int t) { return t < NC ? t : t - nl; };
+    auto lmk_tile = [&](int t) {  // landmark tile of iteration t: the (t-NC)-th set bit
         uint64_t m = lmask;
-        for (int j = nb; j < t; ++j) m &= m - 1;
+        for (int j = NC; j < t; ++j) m &= m - 1;
         return (int)__builtin_ctzll(m);
     };
+    // the band tiles with work for this wave: 0 .. nbw-1; its steps: t < t_end
+    const int nbw = wlo <= ghi ? (ghi - wlo) / BN + 1 : 0;
+    const int t_end = NC + nl + max(nbw - NC, 0);
+    // band tile 0 (keys from ghi - BN + 1) reaches this wave's last query
+    const bool live0 = ghi - (BN - 1) <= min(wq0 + 31, seq_len - 1);
     // K or V rows of tile t into their ring slot
     auto issue_k = [&](int t) {
-        if (t < nb) klanes.load_band(k_lds(t), wave, krs, (uint32_t)band_key0(t) * kst, kst);  // wraps when key0 < 0
-        else klanes.load_gather_lean(k_lds(t), wave, krs, kst, s_lrow + lmk_tile(t) * BN);
+        if (is_lmk(t)) klanes.load_gather_lean(k_lds(t), wave, krs, kst, s_lrow + lmk_tile(t) * BN);
+        else klanes.load_band(k_lds(t), wave, krs, (uint32_t)band_key0(band_of(t)) * kst, kst);  // wraps when key0 < 0
     };
     auto issue_v = [&](int t) {
-        if (t < nb) vlanes.load_band(v_lds(t), wave, vrs, (uint32_t)band_key0(t) * vst, vst);
-        else vlanes.load_gather_lean(v_lds(t), wave, vrs, vst, s_lrow + lmk_tile(t) * BN);
+        if (is_lmk(t)) vlanes.load_gather_lean(v_lds(t), wave, vrs, vst, s_lrow + lmk_tile(t) * BN);
+        else vlanes.load_band(v_lds(t), wave, vrs, (uint32_t)band_key0(band_of(t)) * vst, vst);
     };
 
     // S^T (BN keys x 32 queries) = K . Q^T, raw q.k, of tile t from the K tile in ring
     // slot `slot`. The accumulator starts from the band mask's lower edge: element (rb, r)
     // is key tb + 32 rb + acc_row_const(r) + 4 hh, below lo exactly when
-    // acc_row_const(r) < lo - tb - 32 rb - 4 hh = mb + BN t - 32 rb, so its initial value
-    // is mask row clamp(mb + BN t - 32 rb, 0, 28): -inf there (the MFMA keeps it -inf), 0
-    // elsewhere. No VALU touches the elements; landmark tiles start from row 0 (zeros).
-    // kSoft instead reads the initial values from the query's edge row, four consecutive
-    // keys (elements 4g .. 4g + 3) at a time: the entries of keys x .. x + 3 relative to
-    // lo with x clamped to [-4, kEdgeTab] (one v_med3 and two ds_read2 per group; all four
-    // entries are -inf below the clamp and 0 above it; landmark tiles clamp to the top,
-    // 0): the band's lower edge and the SOFT edge bias together.
-    const int mb = lo - ghi + BN - 1 - hh * 4;
+    // acc_row_const(r) < lo - tb - 32 rb - 4 hh = mb + BN b - 32 rb (b the band index), so
+    // its initial value is mask row clamp(mb + BN b - 32 rb, 0, 28): -inf there (the MFMA
+    // keeps it -inf), 0 elsewhere. No VALU touches the elements; landmark tiles start from
+    // row 0 (zeros). kSoft instead reads the initial values from the query's edge row,
+    // four consecutive keys (elements 4g .. 4g + 3) at a time: the entries of keys
+    // x .. x + 3 relative to lo with x clamped to [-4, kEdgeTab] (one v_med3 and two
+    // ds_read2 per group; all four entries are -inf below the clamp and 0 above it;
+    // landmark tiles clamp to the top, 0): the band's lower edge and the SOFT edge bias
+    // together.
+    int mb = lo - ghi + BN - 1 - hh * 4;
     auto qk_tile = [&](int t, int slot, f32x16 (&sacc)[NRB]) {
         const char *ktile = s_tiles[0][slot];
+        const bool band = !is_lmk(t);
+        const int b = band_of(t);
         // kSoft: the edge row from the lane id, per tile (opaque: not held across the loop)
         int el = 0;
         if constexpr (MODE == kSoft) {
@@ -381,7 +405,7 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
         for (int rb = 0; rb < NRB; ++rb) {
             f32x16 acc;
             if constexpr (MODE == kSoft) {
-                const int x0 = (t < nb) ? -(mb + BN * t - 32 * rb) : (1 << 20);  // key - lo of row offset 0
+                const int x0 = band ? -(mb + BN * b - 32 * rb) : (1 << 20);  // key - lo of row offset 0
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int y = min(max(x0, -4 - 8 * g), kEdgeTab - 8 * g);
@@ -392,7 +416,7 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
                     acc[4 * g + 3] = e4[3];
                 }
             } else {
-                const int d = (t < nb) ? min(max(mb + BN * t - 32 * rb, 0), kMaskRows - 1) : 0;
+                const int d = band ? min(max(mb + BN * b - 32 * rb, 0), kMaskRows - 1) : 0;
                 const float4 *mrow = reinterpret_cast<const float4 *>(&s_mtab[d][0]);
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
@@ -412,15 +436,10 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
         }
     };
 
-    f32x16 oacc[ND];
-#pragma unroll
-    for (int d = 0; d < ND; ++d)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[d][r] = 0.f;
-    float m2 = -INFINITY;  // running max (log2 units), stale by at most kStaleMax
-    float mu = 0.f;        // exponent offset: m2, or 0 while m2 is -inf
-    float lsum0 = 0.f, lsum1 = 0.f;
     const float c = p.c;
+    f32x16 oacc[ND];
+    float m2, mu, thr;     // running max (log2 units, stale by at most kStaleMax), exponent offset, raise threshold (raw)
+    float lsum0, lsum1;    // row sums of the rounded P
     // kSoftWide edge factors: for element slot j (tile row offset cst_j), exp(-z) of the edge
     // logit z = (w~ - d) / tau splits as E * ec[j] with E = exp((A - w~ - mid) / tau) per
     // lane and tile and ec[j] = exp((mid - cst_j) / tau) fixed. Every factor stays in the
@@ -435,9 +454,10 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
             ec[j] = fast_exp2((kEdgeMid - (float)((j >> 4) * 32 + acc_row_const(j & 15))) * p.inv_tau * kLog2e);
     }
 
-    // P = exp2(S * c - mu) of one tile: the 16-bit P^T operand, and the row sums of the
-    // same rounded P in fp32 (one v_dot2 per pair), so that O is normalised by exactly
-    // the weights its P V products used. Masked scores are -inf and give 0.
+    // P = 2^(S c - mu) of one tile: the 16-bit P^T operand, and
+    // the row sums of the same rounded P in fp32 (one v_dot2 per pair), so that O is
+    // normalised by exactly the weights its P V products used. Masked scores are -inf
+    // and give 0.
     auto exp_pack = [&](const f32x16 (&sacc)[NRB], uint32_t (&pk)[NRB][8]) {
 #pragma unroll
         for (int rb = 0; rb < NRB; ++rb)
@@ -465,11 +485,11 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
             }
         }
     };
-    // Per-element adjustments that only some tiles need, applied in place to the raw
-    // scores of tile t (t < nt): landmark admission (p <= p_max(i)) and bias, and (kSoftWide)
-    // the SOFT edge bias of band tiles that reach below a row's core.
+    // Per-element adjustments that only some tiles need, applied in place to the scores
+    // of tile t: landmark admission (p <= p_max(i)) and bias, and (kSoftWide) the SOFT
+    // edge bias of band tiles that reach below a row's core.
     auto adjust = [&](int t, f32x16 (&sacc)[NRB]) {
-        if (t >= nb) {
+        if (is_lmk(t)) {
             const int lt = lmk_tile(t);
 #pragma unroll
             for (int rb = 0; rb < NRB; ++rb)
@@ -486,8 +506,8 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
                         sacc[rb][r] = (pp[e] <= pmax) ? sacc[rb][r] + bb[e] : -INFINITY;
                     }
                 }
-        } else if (MODE == kSoftWide && band_key0(t) < wclo) {
-            const int tb = band_key0(t);
+        } else if (MODE == kSoftWide && band_key0(band_of(t)) < wclo) {
+            const int tb = band_key0(band_of(t));
             const int A = i - tb - hh * 4;
             const int Bc = corelo - tb - hh * 4;  // key >= corelo <=> cst >= Bc
             if (edge_fast) {
@@ -514,30 +534,31 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
             }
         }
     };
-    // Causal edge of tile t (keys after the lane's query), applied in place by VALU. Only
-    // tiles t < NC = BM / BN reach past a wave's first query (tile t ends at key ghi - BN t
-    // and every wave starts at ghi - BM + 1 or later); the lower edge came with the
-    // accumulator's initial value. Element (rb, r) is key tb + hh*4 + cst with cst = rb*32 + acc_row_const(r),
-    // kept iff cst <= A0 + BN t; nA0 is the bit count of rows_le at t = 0.
-    const int A0 = i - ghi + BN - 1 - hh * 4;
-    const int nA0 = 4 * (A0 >> 3) + min((A0 & 7) + 1, 4);
-    // Returns the tile's row max (raw units, -inf if empty), after the causal edge when
-    // `causal` (tiles t < NC).
-    auto mask_max = [&](auto causal, int t, f32x16 (&sacc)[NRB]) -> float {
-        if constexpr (decltype(causal)::value) {
-            uint32_t keep;
-            if constexpr (NRB == 1) {
-                // rows_le(A0 + BN t) keeps the low clamp(nA0 + 16 t, 0, 16) bits
-                const int nA = min(max(nA0 + 16 * t, 0), 16);
-                keep = (uint32_t)((1ull << nA) - 1ull);
-            } else {
-                keep = rows_le(A0 + BN * t);
-            }
-#pragma unroll
-            for (int rb = 0; rb < NRB; ++rb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r]);
+    // Causal edge of band tile t < NC (keys after the lane's query), applied in place by
+    // VALU; later band tiles lie below every query of the workgroup. Element (rb, r) is key
+    // tb + hh*4 + cst with cst = rb*32 + acc_row_const(r), kept iff cst <= A0 + BN t; nA0 is
+    // the bit count of rows_le at t = 0.
+    int A0 = i - ghi + BN - 1 - hh * 4;
+    int nA0 = 4 * (A0 >> 3) + min((A0 & 7) + 1, 4);
+    auto causal_keep = [&](int t, f32x16 (&sacc)[NRB]) {
+        uint32_t keep;
+        if constexpr (NRB == 1) {
+            // rows_le(A0 + BN t) keeps the low clamp(nA0 + 16 t, 0, 16) bits
+            const int nA = min(max(nA0 + 16 * t, 0), 16);
+            keep = (uint32_t)((1ull << nA) - 1ull);
+        } else {
+            keep = rows_le(A0 + BN * t);
         }
+        // opaque: the per-element masks are formed here, at each use (the two attempts
+        // would otherwise share them and hold them across the first attempt's loop)
+        asm volatile("" : "+v"(keep));
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[rb][r] = keep_if(keep, rb * 16 + r, sacc[rb][r]);
+    };
+    // The tile's row max (raw units, -inf if empty), used by the second attempt only.
+    auto tile_max = [&](const f32x16 (&sacc)[NRB]) -> float {
         // v_max3 trees, two chains per row block
         float tm[2 * NRB];
 #pragma unroll
@@ -557,10 +578,8 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
         auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
         return max3f(__uint_as_float(sw[0]), __uint_as_float(sw[1]), __uint_as_float(sw[1]));
     };
-    // Raise the running max when the tile max exceeds it by more than kStaleMax
-    // (wave-uniform branch, rare after the first tile): O and l are rescaled to it.
-    // `thr` is m2 + kStaleMax in raw score units, so the test is one compare.
-    float thr = -INFINITY;
+    // Second attempt: raise the running max when the tile max exceeds it by more than
+    // kStaleMax (wave-uniform branch, rare after the first tile): O and l are rescaled to it.
     auto rescale = [&](bool more, float tmax) {
         const bool raise = tmax > thr;
         if (__builtin_amdgcn_ballot_w64(raise) && more) {
@@ -579,59 +598,117 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     };
 
     // ---- software-pipelined tile loop ----------------------------------------------------
-    // Iteration t: issue K of tile t+R and V of tile t+R-1; part A: P of tile t (VALU)
-    // interleaved with S of tile t+1 (MFMA); part B: O += P V of tile t (MFMA)
-    // interleaved with the masks and row max of tile t+1 (VALU); then the max update and
-    // a wait until K of tile t+2 and V of tile t+1 have landed. K of tile t+R takes the
-    // slot of K of tile t, last read by iteration t-1; V of tile t+R-1 takes the slot of
-    // V of tile t-1, also last read by iteration t-1; every wave finished those reads
-    // before the barrier that ended iteration t-1. With R = 2 the loads issued in
-    // iteration t itself must land by its end (wait for all); with R = 3 the needed ones
-    // were issued an iteration earlier and the newest LPT loads may stay in flight.
-    // Tiles outside a wave's key range are fully
-    // masked (P = 0) rather than skipped, which keeps the iteration branch-free.
-    // nt >= R; the setup issued K of tiles 0 .. R-1 and V of tiles 0 .. R-2. The last
-    // iteration computes S of a tile that does not exist (stale LDS slot) and ignores it.
-    // MFMAs and operand reads of the two parts of an iteration, and the VALU instructions
-    // placed after each MFMA (part A: exp / pack / sum, ~48 per row block; part B: the
-    // max tree, 8 v_maximum3 per row block, two after each P V MFMA)
+    // Step t: issue K of tile t+R and V of tile t+R-1; part A: P of tile t (VALU)
+    // interleaved with S of tile t+1 (MFMA); part B: O += P V of tile t (MFMA) interleaved
+    // with the adjustments (and, in the second attempt, the row max) of tile t+1; then a
+    // wait until K of tile t+2 and V of tile t+1 have landed. K of tile t+R takes the slot
+    // of K of tile t, last read by step t-1; V of tile t+R-1 takes the slot of V of tile
+    // t-1, also last read by step t-1; every wave finished those reads before the barrier
+    // that ended step t-1. With R = 2 the loads issued in step t itself must land by its
+    // end (wait for all); with R = 3 the needed ones were issued a step earlier and the
+    // newest LPT loads may stay in flight. A wave computes steps t < t_end (its last one
+    // computes S of a tile it does not use) and then only issues its share of the
+    // remaining tiles' loads and waits at their barriers (drain).
     constexpr int NQK = KS * NRB, NPV = 2 * ND * NRB;
     constexpr int VALU_A = (NRB * 56 - 16 + NQK - 1) / NQK + 2;
     constexpr int VALU_B = 2;
-    auto step = [&](auto causal, int t, f32x16 (&cur)[NRB], f32x16 (&nxt)[NRB]) {
+    using causal_edge = std::true_type;
+    using no_causal_edge = std::false_type;
+    // `causal`: tile t+1 has a causal edge (t + 1 < NC); `live`: tile t has work for the wave
+    auto step = [&](auto fast, auto causal, int t, bool live, f32x16 (&cur)[NRB], f32x16 (&nxt)[NRB]) {
         if (t + R < nt) issue_k(t + R);
         if (t + R - 1 < nt) issue_v(t + R - 1);
         uint32_t pk[NRB][8];
         qk_tile(t + 1, slot_of(t + 1), nxt);
-        exp_pack(cur, pk);
-        __builtin_amdgcn_sched_group_barrier(0x100, NQK + 4 * NRB, 0);  // mask rows, K operand reads
-        __builtin_amdgcn_sched_group_barrier(0x402, 16, 0);   // VALU / transcendental
+        if (live) {
+            exp_pack(cur, pk);
+            __builtin_amdgcn_sched_group_barrier(0x100, NQK + 4 * NRB, 0);  // mask rows, K operand reads
+            __builtin_amdgcn_sched_group_barrier(0x402, 16, 0);   // VALU / transcendental
 #pragma unroll
-        for (int m = 0; m < NQK; ++m) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x402, VALU_A, 0);  // VALU / transcendental
+            for (int m = 0; m < NQK; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x402, VALU_A, 0);  // VALU / transcendental
+            }
+            // keep P and the row sums in part A (otherwise they sink past the branch below)
+#pragma unroll
+            for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(pk[rb][j]));
+            asm volatile("" : "+v"(lsum0), "+v"(lsum1));
         }
-        // keep P and the row sums in part A (otherwise they sink past the branch below)
-#pragma unroll
-        for (int rb = 0; rb < NRB; ++rb)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(pk[rb][j]));
-        asm volatile("" : "+v"(lsum0), "+v"(lsum1));
-        const bool more = t + 1 < nt;
+        const bool more = t + 1 < t_end;
         if (more) adjust(t + 1, nxt);
-        pv(pk, slot_of(t));
-        const float tmax = mask_max(causal, t + 1, nxt);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * NPV, 1);  // V operand reads
-        __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);        // VALU
+        if (live) pv(pk, slot_of(t));
+        if constexpr (decltype(fast)::value && !decltype(causal)::value) {
+            // first attempt after the peel: the offset stays where the peel left it
+        } else {
+            if constexpr (decltype(causal)::value) causal_keep(t + 1, nxt);
+            const float tmax = tile_max(nxt);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * NPV, 1);  // V operand reads
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 1);        // VALU
 #pragma unroll
-        for (int m = 0; m < NPV; ++m) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);       // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, VALU_B, 1);  // VALU
+            for (int m = 0; m < NPV; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);       // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, VALU_B, 1);  // VALU
+            }
+            rescale(more, tmax);
         }
-        rescale(more, tmax);
         if (t + R < nt) tile_barrier<(R - 2) * LPT>();
         else tile_barrier<0>();
     };
+    // One pass over the tiles: the peel (tiles 0 .. NC-1 with their causal edge), the
+    // pipelined loop over the wave's steps, the drain. oacc / l / m2 start at zero / -inf.
+    auto attempt = [&](auto fast) {
+        // opaque per attempt: values derived from these for the peel tiles are recomputed
+        // in each attempt instead of being held across the first one
+        asm volatile("" : "+v"(mb), "+v"(A0), "+v"(nA0));
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[d][r] = 0.f;
+        m2 = -INFINITY;
+        mu = 0.f;
+        thr = -INFINITY;
+        lsum0 = 0.f;
+        lsum1 = 0.f;
+        f32x16 sA[NRB], sB[NRB];
+        tile_barrier<(R - 2) * LPT>();  // K of tiles 0, 1 and V of tile 0 landed
+        if (live0) {
+            qk_tile(0, slot_of(0), sA);
+            adjust(0, sA);
+            causal_keep(0, sA);
+            // the first tile's max: O and l are still zero, so nothing is rescaled
+            const float tmax = tile_max(sA);
+            const bool raise = tmax > thr;
+            m2 = raise ? tmax * c : m2;
+            mu = (m2 == -INFINITY) ? 0.f : m2;
+            thr = raise ? tmax + kStaleMax * p.inv_c : thr;
+        }
+        // step 0 refills the slot of K of tile 0: every wave must have read it first
+        tile_barrier<(R - 2) * LPT>();
+        // steps 0 .. NC-2 mask the causal edge of tiles 1 .. NC-1 (nt >= NC >= R)
+        if constexpr (NC > 1) step(fast, causal_edge(), 0, live0, sA, sB);
+        if constexpr (NC > 2) step(fast, causal_edge(), 1, true, sB, sA);
+        if constexpr (NC > 3) step(fast, causal_edge(), 2, true, sA, sB);
+        constexpr int T0 = NC - 1;  // first step without a causal edge
+        int t = T0;
+        for (; t < t_end; t += 2) {
+            if constexpr (T0 % 2 == 0) {
+                step(fast, no_causal_edge(), t, true, sA, sB);
+                if (t + 1 < t_end) step(fast, no_causal_edge(), t + 1, true, sB, sA);
+            } else {
+                step(fast, no_causal_edge(), t, true, sB, sA);
+                if (t + 1 < t_end) step(fast, no_causal_edge(), t + 1, true, sA, sB);
+            }
+        }
+        for (t = max(t_end, T0); t < nt; ++t) {
+            if (t + R < nt) issue_k(t + R);
+            if (t + R - 1 < nt) issue_v(t + R - 1);
+            if (t + R < nt) tile_barrier<(R - 2) * LPT>();
+            else tile_barrier<0>();
+        }
+    };
+
     // Wave priority by dispatch order (grids of at most two dispatch rounds): the
     // workgroups of a round start together, but the later-dispatched ones get their
     // set-up loads served last and start their tile loops up to ~5 us later (c2), so the
@@ -644,47 +721,39 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
         else if (pq == 2) __builtin_amdgcn_s_setprio(2);
         else if (pq >= 3) __builtin_amdgcn_s_setprio(3);
     }
-    f32x16 sA[NRB], sB[NRB];
-    tile_barrier<(R - 2) * LPT>();  // K of tiles 0, 1 and V of tile 0 landed
-    using causal_edge = std::true_type;
-    using no_causal_edge = std::false_type;
-    qk_tile(0, slot_of(0), sA);
-    adjust(0, sA);
-    {
-        // the first tile's max: O and l are still zero, so nothing is rescaled
-        const float tmax = mask_max(causal_edge(), 0, sA);
-        const bool raise = tmax > thr;
-        m2 = raise ? tmax * c : m2;
-        mu = (m2 == -INFINITY) ? 0.f : m2;
-        thr = raise ? tmax + kStaleMax * p.inv_c : thr;
-    }
-    // step 0 refills the slot of K of tile 0: every wave must have read it first
-    tile_barrier<(R - 2) * LPT>();
-    // steps 0 .. NC-2 mask the causal edge of tiles 1 .. NC-1; later tiles lie below every
-    // query of the workgroup (nt >= R >= 2, so step 0 always runs)
-    constexpr int NC = BM / BN;
-    static_assert(NC >= 1 && NC <= 4, "causal peel covers at most four tiles");
-    if constexpr (NC > 1) step(causal_edge(), 0, sA, sB);
-    if constexpr (NC > 2) {
-        if (1 < nt) step(causal_edge(), 1, sB, sA);
-    }
-    if constexpr (NC > 3) {
-        if (2 < nt) step(causal_edge(), 2, sA, sB);
-    }
-    constexpr int T0 = NC - 1;  // first step without a causal edge
-    for (int t = T0; t < nt; t += 2) {
-        if constexpr (T0 % 2 == 0) {
-            step(no_causal_edge(), t, sA, sB);
-            if (t + 1 < nt) step(no_causal_edge(), t + 1, sB, sA);
-        } else {
-            step(no_causal_edge(), t, sB, sA);
-            if (t + 1 < nt) step(no_causal_edge(), t + 1, sA, sB);
+    // First attempt with the offset fixed after the diagonal tiles (bf16). It stands when
+    // every valid row total lies in [2^-60, 2^60]: then no P exceeded 2^60 (nothing
+    // overflowed) and every P that underflowed weighs less than 2^-66 of its row. Otherwise
+    // (logits far above the diagonal tiles' maximum, rows without keys there, NaN) the
+    // workgroup runs the tiles again with the running max.
+    bool redo = true;
+    if constexpr (kTryFast) {
+        attempt(std::true_type());
+        const float lt = half_sum(lsum0 + lsum1);
+        const bool bad = qvalid && !(lt >= 0x1p-60f && lt <= 0x1p60f);
+        const int wave_bad = __builtin_amdgcn_ballot_w64(bad) != 0;  // every lane votes
+        if (lane == 0) s_red[wave][0] = wave_bad;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        int any = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) any |= s_red[w][0];
+        redo = __builtin_amdgcn_readfirstlane(any) != 0;
+        if (redo) {
+            // the ring is idle (every wave passed the last tile barrier): reload its first tiles
+#pragma unroll
+            for (int tt = 0; tt < R; ++tt) {
+                klanes.load_band(k_lds(tt), wave, krs, (uint32_t)band_key0(tt) * kst, kst);
+                if (tt < R - 1) vlanes.load_band(v_lds(tt), wave, vrs, (uint32_t)band_key0(tt) * vst, vst);
+            }
         }
     }
+#ifndef DSALT_NO_SLOW
+    if (redo) attempt(std::false_type());
+#endif
 
-    // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln 2 --------------------------------
+    // ---- epilogue: O = acc / l, LSE = (mu + log2 l) * ln 2 --------------------------------
     const float ltot = half_sum(lsum0 + lsum1);
-    const bool nonempty = ltot > 1e-9f;
+    const bool nonempty = ltot > 0x1p-100f;
     const float inv = nonempty ? 1.f / ltot : 0.f;
     // the query of this lane again from the lane id (opaque, so that i and its token
     // offset are not kept in registers across the tile loop)
@@ -712,21 +781,43 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
             }
         if (hh == 0)
             p.lse[tok_e * p.lse_st + (int64_t)head * p.lse_sh] =
-                nonempty ? (m2 + fast_log2(ltot)) * kLn2 : -INFINITY;
+                nonempty ? (mu + fast_log2(ltot)) * kLn2 : -INFINITY;
     }
+}
+
+// Workgroups of fwd_kernel<DT, D, MODE> resident on the whole device at once (one dispatch
+// round) for `dyn` bytes of dynamic LDS, or 0 when HIP cannot say. Queried once per
+// (device, landmark padding) and cached: a forward launch then makes no HIP queries
+// besides hipGetDevice. Concurrent first calls store the same value.
+template <typename DT, int D, int MODE>
+int64_t dispatch_round(int dev, size_t dyn) {
+    constexpr int kDevs = 64, kPads = DSALT_MAX_K_LMK / kFwdBN + 1;
+    static std::atomic<int64_t> cache[kDevs][kPads];  // 0: not queried yet; -1: unknown
+    const int pad = (int)(dyn / (kFwdBN * (2 * sizeof(int) + sizeof(float))));
+    if (dev < 0 || dev >= kDevs || pad >= kPads) return 0;
+    int64_t r = cache[dev][pad].load(std::memory_order_relaxed);
+    if (r == 0) {
+        int n_cu = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fwd_kernel<DT, D, MODE>, 64 * fwd_waves(D), dyn) ==
+                hipSuccess &&
+            n_cu > 0 && per_cu > 0)
+            r = (int64_t)n_cu * per_cu;
+        else
+            r = -1;
+        (void)hipGetLastError();  // a failed query must not be reported as a launch error
+        cache[dev][pad].store(r, std::memory_order_relaxed);
+    }
+    return r > 0 ? r : 0;
 }
 
 template <typename DT, int D, int MODE>
 hipError_t launch_typed(FwdParams p, size_t dyn, hipStream_t stream) {
-    // workgroups resident at once (one dispatch round): the wave-priority span
-    int dev = 0, n_cu = 0, per_cu = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fwd_kernel<DT, D, MODE>, 64 * fwd_waves(D), dyn) ==
-            hipSuccess) {
-        const int64_t round = (int64_t)n_cu * per_cu;
-        p.prio_span = (round > 0 && p.grid <= 2 * round) ? (int)(p.grid < round ? p.grid : round) : 0;
-    }
+    // the wave-priority span: the first dispatch round, for grids of at most two rounds
+    int dev = -1;
+    const int64_t round = hipGetDevice(&dev) == hipSuccess ? dispatch_round<DT, D, MODE>(dev, dyn) : 0;
+    (void)hipGetLastError();
+    p.prio_span = (round > 0 && p.grid <= 2 * round) ? (int)(p.grid < round ? p.grid : round) : 0;
     hipLaunchKernelGGL((fwd_kernel<DT, D, MODE>), dim3(p.grid), dim3(64 * fwd_waves(D)), dyn, stream, p);
     return hipGetLastError();
 }
