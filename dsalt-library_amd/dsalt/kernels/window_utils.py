@@ -50,6 +50,44 @@ def apply_rotary_emb_packed(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor,
     return _RopeFunction.apply(q, k, cos, sin, cu_seqlens)
 
 
+def compute_window_sizes(x_prev: torch.Tensor, n_min: int, n_max: int) -> torch.Tensor:
+    """A fixed window ``(n_min + n_max) // 2`` for each of the ``x_prev.shape[0]`` tokens,
+    fp32 on ``x_prev``'s device (window_utils.py:4-16 of the reference; the module predicts
+    its windows with ``win_gate`` instead)."""
+    return torch.full((x_prev.shape[0],), float((n_min + n_max) // 2), dtype=torch.float32, device=x_prev.device)
+
+
+def _band(rows: torch.Tensor, starts: torch.Tensor, w: torch.Tensor, n_cols: int) -> torch.Tensor:
+    """Boolean ``[len(rows), n_cols]``: row r admits columns ``max(starts[r], rows[r] - w[r] + 1)
+    .. rows[r]`` (absolute indices)."""
+    lo = torch.maximum(rows - w + 1, starts)
+    cols = torch.arange(n_cols, device=rows.device)
+    return (cols[None, :] >= lo[:, None]) & (cols[None, :] <= rows[:, None])
+
+
+def build_local_window_mask(seq_len: int, window_sizes: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """Causal local-window mask ``[T, T]`` of one sequence, True = attend: row i admits
+    keys ``max(0, i - w_i + 1) .. i`` with ``w_i`` clamped to ``[1, T]`` and truncated
+    to an integer (window_utils.py:19-38 of the reference)."""
+    rows = torch.arange(seq_len, device=device)
+    w = window_sizes.to(device).clamp(min=1, max=seq_len).long()
+    return _band(rows, torch.zeros_like(rows), w, seq_len)
+
+
+def build_local_window_mask_packed(cu_seqlens: torch.Tensor, window_sizes: torch.Tensor, total_len: int,
+                                   device: torch.device) -> torch.Tensor:
+    """Local-window mask ``[T, T]`` over packed sequences, True = attend: token t of a
+    sequence starting at s admits ``max(s, t - w_t + 1) .. t`` (``w_t`` clamped below at 1,
+    truncated), so never a key of another sequence (window_utils.py:41-70 of the
+    reference)."""
+    cu = cu_seqlens.to(device=device, dtype=torch.long)
+    lens = cu[1:] - cu[:-1]
+    starts = torch.repeat_interleave(cu[:-1], lens, output_size=total_len)
+    rows = torch.arange(total_len, device=device)
+    w = window_sizes.to(device).clamp(min=1).long()
+    return _band(rows, starts, w, total_len)
+
+
 def apply_rotary_emb(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor,
                      sin: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Rotate ``q`` and ``k`` with the precomputed ``(cos, sin)`` (half-split convention)."""
