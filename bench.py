@@ -366,23 +366,121 @@ def measure_front_end(wl, w, cu, sel) -> dict:
     scores = _hip.ScoresLauncher(xb, vb, alpha, H)
     sel_f = _hip.SelectLauncher(scores.scores, w, cu, k, max_seqlen=wl["L"])
 
-    def fused_path():
+    def hip_scores_path():
         scores()
         sel_f()
 
+    from dsalt.kernels.landmark_tokens_ker import hybrid_scores_from_v
+
+    def v_route_path():
+        s, _, _ = hybrid_scores_from_v(xb, vb, alpha, H)
+        _hip.select_landmarks(s, w, cu, k, max_seqlen=wl["L"])
+
     with torch.no_grad():
         gemm_ms = time_launches(gemm_path, 50, 10)
-        fused_ms = time_launches(fused_path, 50, 10)
+        v_route_ms = time_launches(v_route_path, 50, 10)
+        hip_ms = time_launches(hip_scores_path, 50, 10)
         scores_graph_ms = time_graph(scores)
     d = xb.shape[1]
     bytes_scores = 2 * T * d + 2 * T * H * D + 4 * T * (1 + H) * 2 + 4 * T * H * 3
     return {
         "workload": "c2 inference selection (hybrid scores + top-k), bf16 x / W_V / v",
         "gemm_path_us": gemm_ms * 1e3,
-        "fused_path_us": fused_ms * 1e3,
-        "fused_scores_graph_us": scores_graph_ms * 1e3,
-        "fused_scores_GB/s": bytes_scores / (scores_graph_ms * 1e-3) / 1e9,
+        "default_v_route_us": v_route_ms * 1e3,
+        "hip_scores_path_us": hip_ms * 1e3,
+        "hip_scores_graph_us": scores_graph_ms * 1e3,
+        "hip_scores_GB/s": bytes_scores / (scores_graph_ms * 1e-3) / 1e9,
         "gemm_flops_saved": 2.0 * T * d * H * D,
+        "note": "gemm_path: the reference's x @ W_V^T route; default_v_route: the module's default "
+                "(the same torch norms on its own value projection, no second GEMM); hip_scores_path: "
+                "the opt-in one-pass HIP score kernel (DSALTAttention._hip_scores)",
+    }
+
+
+def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
+    """The c2 inference forward as DSALTAttention runs it by default, in bf16 (module cast to
+    bf16, _collect_last_P off, packed with cu_seqlens and its host copy): the whole
+    module call, and each of its stages eager, launch costs included: q/k/v projections,
+    RoPE of k (q is rotated inside the attention kernel), the window gate and its
+    quantisation, the landmark scores (torch norms on the module's value projection),
+    the top-k selection, the HARD attention forward rotating q on load, out_proj."""
+    import copy
+    from dsalt import _hip
+    from dsalt.kernels._sparse import sparse_attention
+    from dsalt.kernels.selectors import selection_scores
+    from dsalt.kernels.window_utils import rotate_packed
+
+    mod = copy.deepcopy(wl["mod"]).to(torch.bfloat16).eval()
+    mod._collect_last_P = False
+    T, H, D, L, kl = wl["T"], wl["H"], wl["D"], wl["L"], wl["k_lmk"]
+    x = wl["xp"].to(torch.bfloat16)
+    cu = wl["cu"]
+    cu_list = cu.tolist()
+    cos, sin = mod.rope_cos, mod.rope_sin
+    with torch.no_grad():
+        q = mod.q_proj(x).view(T, H, D)
+        k = mod.k_proj(x).view(T, H, D)
+        v = mod.v_proj(x).view(T, H, D)
+        kr = rotate_packed(k, cos, sin, cu)
+        w = mod._window_sizes(x, floor=True)
+        alpha = mod._alpha().detach().float()
+        sc, _, _ = selection_scores(x, mod.v_proj.weight, alpha, H, D, v=v)
+        sc = sc.float()
+        lmk = _hip.select_landmarks(sc, w, cu, kl, max_seqlen=L)
+        out = sparse_attention(_hip.MODE_HARD, q, kr, v, lmk, None, w, cu, rope=(cos, sin))
+    stages = {
+        "qkv_proj": lambda: (mod.q_proj(x), mod.k_proj(x), mod.v_proj(x)),
+        "rope_k": lambda: rotate_packed(k, cos, sin, cu),
+        "window_gate_and_quantize": lambda: mod._window_sizes(x, floor=True),
+        "landmark_scores": lambda: selection_scores(x, mod.v_proj.weight, alpha, H, D, v=v),
+        "select_topk": lambda: _hip.select_landmarks(sc, w, cu, kl, max_seqlen=L),
+        "attention_fwd_rotating_q": lambda: sparse_attention(_hip.MODE_HARD, q, kr, v, lmk, None, w, cu,
+                                                             rope=(cos, sin)),
+        "out_proj": lambda: mod._apply_out_proj(out.reshape(T, H * D)),
+    }
+    res = {"workload": "c2 DSALTAttention(1024, 16, 32, 512, 64) inference forward, bf16, packed 4 x 2048, "
+                       "default routes (v-route scores, k RoPE pass, q rotated in the attention kernel)"}
+    with torch.no_grad():
+        res["module_forward_us"] = time_launches(lambda: mod(x, cu_seqlens=cu, cu_list=cu_list), steps,
+                                                 warmup) * 1e3
+        for name, fn in stages.items():
+            res[name + "_us"] = time_launches(fn, steps, warmup) * 1e3
+    res["stages_sum_us"] = sum(v for kk, v in res.items() if kk.endswith("_us") and kk != "module_forward_us")
+    return res
+
+
+def measure_c4(device: torch.device, steps: int = 100, warmup: int = 100) -> dict:
+    """the HARD forward on the seed-3 module's own windows and landmarks
+    (DSALTAttention(2048, 16, 64, 1024, 128, 16384), x ~ N(0, 1) [1, 16384, 2048], bf16
+    q/k/v), timed like the headline: MFMA fraction on the exact pair count, HBM fraction on
+    the algorithmic bytes."""
+    from dsalt import _hip
+
+    wl = make_workload("c4", device)
+    q, k, v, w, lmk, cu = wl["q"], wl["k"], wl["v"], wl["w"], wl["lmk"], wl["cu"]
+    T, H, D = wl["T"], wl["H"], wl["D"]
+    f = _hip.FwdLauncher(_hip.MODE_HARD, q, k, v, w, lmk, None, cu, 1.0 / math.sqrt(D))
+    ms = time_launches(f, steps, warmup)
+    P = effective_pairs_hard(w.float().cpu().numpy(), lmk.cpu().numpy(), cu.cpu().tolist())
+    t = ms * 1e-3
+    bytes_alg = 2 * T * H * D * 4 + 4 * T * H + 4 * T + 8 * H * wl["B"] * wl["k_lmk"]
+    traffic, traffic_sha = load_traffic("c4")
+    del wl, f
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"c4: HARD DSALT attention forward, 1 x 16384 tokens, {H} heads x {D} head_dim, n_min 64, "
+                    "n_max 1024, k_lmk 128, module seed 3, bf16",
+        "us_per_launch": ms * 1e3,
+        "tokens_per_s": T / t,
+        "pairs": P,
+        "keys_per_query": P / (T * H),
+        "mfma_tflops": 4.0 * D * P / t / 1e12,
+        "mfma_frac": 4.0 * D * P / t / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "hbm_GBs": bytes_alg / t / 1e9,
+        "hbm_frac": bytes_alg / t / 1e9 / HBM_PEAK_GBS,
+        "bytes_per_launch": bytes_alg,
+        "traffic": traffic,
+        "traffic_source_sha16": traffic_sha,
     }
 
 
@@ -507,8 +605,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-backward", action="store_true", help="skip the config-3 backward measurement")
     ap.add_argument("--no-extras", action="store_true",
-                    help="skip the dense-variant and config-5 LM measurements")
-    ap.add_argument("--only", choices=("lm", "dense", "backward"), default=None,
+                    help="skip the config-4, dense-variant and config-5 LM measurements")
+    ap.add_argument("--only", choices=("lm", "dense", "backward", "c4"), default=None,
                     help="run only that measurement and print its JSON (for profiling)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (counter calibration)")
@@ -530,7 +628,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if args.only is not None:
-        fn = {"lm": measure_lm, "dense": measure_dense, "backward": measure_backward}[args.only]
+        fn = {"lm": measure_lm, "dense": measure_dense, "backward": measure_backward, "c4": measure_c4}[args.only]
         print(json.dumps(fn(dev)))
         return
     wl = make_workload(args.config, dev)
@@ -634,7 +732,10 @@ def main():
         "path_ms": ms + sel_ms + qz_ms,
         "selector_front_end": front,
         "rope": measure_rope(wl, cu, ms),
+        "module_path_c2": measure_module_path(wl),
     }
+    if not args.no_extras and args.config == "c2":
+        res["c4"] = measure_c4(dev)
     if not args.no_backward:
         res["backward"] = measure_backward(dev)
     if not args.no_extras:
