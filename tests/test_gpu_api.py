@@ -13,14 +13,17 @@ from dsalt.kernels import dsalt_triton_attention, dsalt_triton_backward
 from dsalt.kernels.dsalt_triton_train import dsalt_triton_train_attention
 from dsalt.kernels.selectors import _build_landmark_kv, _build_seq_block_map, _compute_landmark_indices
 from oracle import dsalt_oracle as orc
-from test_gpu_fwd import close, make_inputs
+from test_gpu_fwd import close, make_inputs, summed_grad_bar
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
 
 
+SUMMED = ("d_bias", "d_logw", "d_w")  # sums over the queries of a landmark slot / heads and edge keys
+
+
 def _grad_bar(ref):
-    return 2e-2 * max(ref.abs().max().item(), 1.0)
+    return 2e-2 * min(1.0, max(ref.abs().max().item(), 1e-3))
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32-as-fp16"])
@@ -46,7 +49,7 @@ def test_dsalt_triton_attention_autograd(dtype):
     close(out.detach().cpu(), o.detach(), "out")
     for name, got, ref in (("dq", qd.grad, q64.grad), ("dk", kd.grad, k64.grad), ("dv", vd.grad, v64.grad),
                            ("d_bias", bd.grad, b64.grad)):
-        close(got.float().cpu(), ref, name, max_abs=_grad_bar(ref))
+        close(got.float().cpu(), ref, name, max_abs=summed_grad_bar(ref) if name in SUMMED else _grad_bar(ref))
 
 
 def test_dsalt_triton_train_attention_autograd():
@@ -72,7 +75,7 @@ def test_dsalt_triton_train_attention_autograd():
     l_ref = torch.where(torch.isfinite(logw.double()), l64.grad, torch.zeros_like(l64.grad))
     for name, got, ref in (("dq", qd.grad, q64.grad), ("dk", kd.grad, k64.grad), ("dv", vd.grad, v64.grad),
                            ("d_logw", lw.grad, l_ref), ("d_w", wd.grad, w64.grad)):
-        close(got.float().cpu(), ref, name, max_abs=_grad_bar(ref))
+        close(got.float().cpu(), ref, name, max_abs=summed_grad_bar(ref) if name in SUMMED else _grad_bar(ref))
 
 
 def test_dsalt_triton_backward_signature():
@@ -94,7 +97,7 @@ def test_dsalt_triton_backward_signature():
     o, _ = orc.attention_hard(q64, k64, v64, w, pos, b64, cu.tolist())
     (o * dout.to(torch.bfloat16).double()).sum().backward()
     for name, got, ref in (("dq", dq, q64.grad), ("dk", dk, k64.grad), ("dv", dv, v64.grad), ("d_bias", db, b64.grad)):
-        close(got.cpu(), ref, name, max_abs=_grad_bar(ref))
+        close(got.cpu(), ref, name, max_abs=summed_grad_bar(ref) if name in SUMMED else _grad_bar(ref))
 
 
 def test_selector_helpers_match_reference_semantics():

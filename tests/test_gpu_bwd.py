@@ -11,7 +11,7 @@ import torch
 
 import dsalt._hip as hip
 from oracle import dsalt_oracle as orc
-from test_gpu_fwd import close, make_inputs
+from test_gpu_fwd import close, make_inputs, summed_grad_bar
 
 pytestmark = pytest.mark.gpu
 
@@ -47,17 +47,15 @@ def run_case(mode, lens, H, D, k, seed, n_min, n_max, kind="random", dtype=torch
     for name, got, ref in (("dq", dq, q64.grad), ("dk", dk, k64.grad), ("dv", dv, v64.grad)):
         if grad_dtype == torch.float32:
             close(got.float().cpu(), ref, name)
-        else:  # 16-bit O and gradients: the bar is relative to the largest gradient (rounding)
-            close(got.float().cpu(), ref, name, max_abs=2e-2 * max(ref.abs().max().item(), 1.0))
+        else:  # 16-bit O and gradients: never looser than the absolute bar
+            close(got.float().cpu(), ref, name, max_abs=2e-2 * min(1.0, max(ref.abs().max().item(), 1e-3)))
     if k > 0:
         ref = b64.grad.clone()
         if mode == hip.MODE_SOFT:  # slots with lmk_logw = -inf carry no gradient
             ref = torch.where(torch.isfinite(bias.double()), ref, torch.zeros_like(ref))
-        scale_b = max(ref.abs().max().item(), 1.0)
-        close(dbias.cpu(), ref, "d_lmk_bias", max_abs=2e-2 * scale_b)
+        close(dbias.cpu(), ref, "d_lmk_bias", max_abs=summed_grad_bar(ref))
     if mode == hip.MODE_SOFT:
-        scale_w = max(w64.grad.abs().max().item(), 1.0)
-        close(dw.cpu(), w64.grad, "d_w", max_abs=2e-2 * scale_w)
+        close(dw.cpu(), w64.grad, "d_w", max_abs=summed_grad_bar(w64.grad))
 
 
 CASES = [

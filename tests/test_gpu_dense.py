@@ -37,7 +37,7 @@ def check(got, ref, what, rel=1e-2, frac=2e-2):
     diff = got - ref
     rl = (diff.norm() / ref.norm().clamp_min(1e-30)).item()
     ma = diff.abs().max().item() if diff.numel() else 0.0
-    bar = frac * max(ref.abs().max().item() if ref.numel() else 0.0, 1e-3)
+    bar = frac * min(1.0, max(ref.abs().max().item() if ref.numel() else 0.0, 1e-3))
     print(f"  {what}: rel-L2 {rl:.2e} max-abs {ma:.2e} (bar {bar:.2e})", flush=True)
     assert rl <= rel and ma <= bar, f"{what}: rel-L2 {rl:.3e}, max-abs {ma:.3e} (bar {bar:.3e})"
 

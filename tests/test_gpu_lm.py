@@ -30,7 +30,7 @@ def check(got, ref, what):
     diff = got - ref
     rl = (diff.norm() / ref.norm().clamp_min(1e-30)).item()
     ma = diff.abs().max().item()
-    bar = 2e-2 * max(ref.abs().max().item(), 1e-3)
+    bar = 2e-2 * min(1.0, max(ref.abs().max().item(), 1e-3))
     print(f"  {what}: rel-L2 {rl:.2e} max-abs {ma:.2e} (bar {bar:.2e})", flush=True)
     assert rl <= 1e-2 and ma <= bar, f"{what}: rel-L2 {rl:.3e}, max-abs {ma:.3e} (bar {bar:.3e})"
 
