@@ -345,8 +345,9 @@ def time_launches(fn, steps: int, warmup: int) -> float:
 def measure_front_end(wl, w, cu, sel) -> dict:
     """The inference selection path in bf16 at the workload's shape: hybrid scores + top-k,
     by the reference's route (x @ W_V^T GEMM, norms and standardisation in torch,
-    landmark_tokens_ker.py:45-61) and by the fused one (dsalt_hybrid_scores on the
-    module's value projection). Both eager, launch costs included; the fused scores also
+    landmark_tokens_ker.py:45-61), by the torch ops on the module's value projection, and
+    by the module's default (dsalt_hybrid_scores on the module's value projection). All
+    eager, launch costs included; the HIP scores also
     from a HIP graph (GPU time alone). HBM bytes of the fused score kernels: x and v read
     once (bf16), norms and scores written and read back (fp32)."""
     from dsalt import _hip
@@ -386,14 +387,14 @@ def measure_front_end(wl, w, cu, sel) -> dict:
     return {
         "workload": "c2 inference selection (hybrid scores + top-k), bf16 x / W_V / v",
         "gemm_path_us": gemm_ms * 1e3,
-        "default_v_route_us": v_route_ms * 1e3,
+        "torch_v_route_us": v_route_ms * 1e3,
         "hip_scores_path_us": hip_ms * 1e3,
         "hip_scores_graph_us": scores_graph_ms * 1e3,
         "hip_scores_GB/s": bytes_scores / (scores_graph_ms * 1e-3) / 1e9,
         "gemm_flops_saved": 2.0 * T * d * H * D,
-        "note": "gemm_path: the reference's x @ W_V^T route; default_v_route: the module's default "
-                "(the same torch norms on its own value projection, no second GEMM); hip_scores_path: "
-                "the opt-in one-pass HIP score kernel (DSALTAttention._hip_scores)",
+        "note": "gemm_path: the reference's x @ W_V^T route; torch_v_route: the same torch norms on the "
+                "module's own value projection (no second GEMM, DSALTAttention._hip_scores = False); "
+                "hip_scores_path: the module's default, the one-pass HIP score kernel on x and v",
     }
 
 
@@ -401,9 +402,10 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
     """The c2 inference forward as DSALTAttention runs it by default, in bf16 (module cast to
     bf16, _collect_last_P off, packed with cu_seqlens and its host copy): the whole
     module call, and each of its stages eager, launch costs included: q/k/v projections,
-    RoPE of k (q is rotated inside the attention kernel), the window gate and its
-    quantisation, the landmark scores (torch norms on the module's value projection),
-    the top-k selection, the HARD attention forward rotating q on load, out_proj."""
+    RoPE of k (q is rotated inside the attention kernel), the window gate, the landmark
+    scores (HIP score kernel on x and the module's value projection; the torch route's
+    cost beside it, not in the sum), the top-k selection with the
+    window quantisation fused in, the HARD attention forward rotating q on load, out_proj."""
     import copy
     from dsalt import _hip
     from dsalt.kernels._sparse import sparse_attention
@@ -423,29 +425,33 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
         v = mod.v_proj(x).view(T, H, D)
         kr = rotate_packed(k, cos, sin, cu)
         w = mod._window_sizes(x, floor=True)
+        wc = mod._window_continuous(x)
         alpha = mod._alpha().detach().float()
-        sc, _, _ = selection_scores(x, mod.v_proj.weight, alpha, H, D, v=v)
+        sc, _, _ = selection_scores(x, mod.v_proj.weight, alpha, H, D, v=v, hip_scores=True)
         sc = sc.float()
         lmk = _hip.select_landmarks(sc, w, cu, kl, max_seqlen=L)
         out = sparse_attention(_hip.MODE_HARD, q, kr, v, lmk, None, w, cu, rope=(cos, sin))
     stages = {
         "qkv_proj": lambda: (mod.q_proj(x), mod.k_proj(x), mod.v_proj(x)),
         "rope_k": lambda: rotate_packed(k, cos, sin, cu),
-        "window_gate_and_quantize": lambda: mod._window_sizes(x, floor=True),
-        "landmark_scores": lambda: selection_scores(x, mod.v_proj.weight, alpha, H, D, v=v),
-        "select_topk": lambda: _hip.select_landmarks(sc, w, cu, kl, max_seqlen=L),
+        "window_gate": lambda: mod._window_continuous(x),
+        "landmark_scores": lambda: selection_scores(x, mod.v_proj.weight, alpha, H, D, v=v, hip_scores=True),
+        "landmark_scores_torch_route": lambda: selection_scores(x, mod.v_proj.weight, alpha, H, D, v=v),
+        "select_topk_and_quantize": lambda: _hip.select_landmarks_quantize(sc, wc, cu, kl, max_seqlen=L),
         "attention_fwd_rotating_q": lambda: sparse_attention(_hip.MODE_HARD, q, kr, v, lmk, None, w, cu,
                                                              rope=(cos, sin)),
         "out_proj": lambda: mod._apply_out_proj(out.reshape(T, H * D)),
     }
     res = {"workload": "c2 DSALTAttention(1024, 16, 32, 512, 64) inference forward, bf16, packed 4 x 2048, "
-                       "default routes (v-route scores, k RoPE pass, q rotated in the attention kernel)"}
+                       "default routes (HIP scores on x and v, k RoPE pass, windows quantised in the selection, "
+                       "q rotated in the attention kernel)"}
     with torch.no_grad():
         res["module_forward_us"] = time_launches(lambda: mod(x, cu_seqlens=cu, cu_list=cu_list), steps,
                                                  warmup) * 1e3
         for name, fn in stages.items():
             res[name + "_us"] = time_launches(fn, steps, warmup) * 1e3
-    res["stages_sum_us"] = sum(v for kk, v in res.items() if kk.endswith("_us") and kk != "module_forward_us")
+    res["stages_sum_us"] = sum(v for kk, v in res.items()
+                               if kk.endswith("_us") and kk not in ("module_forward_us", "landmark_scores_torch_route_us"))
     return res
 
 
@@ -650,6 +656,11 @@ def main():
     sel = _hip.SelectLauncher(scores, w, cu, wl["k_lmk"], max_seqlen=wl["L"])
     sel_ms = time_graph(sel)
     qz_ms = time_graph(_hip.QuantizeLauncher(w_cont))
+    # the module's inference path: the windows quantised by the selection launch itself
+    selq = _hip.SelectLauncher(scores, w_cont, cu, wl["k_lmk"], max_seqlen=wl["L"], quantize=True)
+    selq_ms = time_graph(selq)
+    if not (torch.equal(selq.out, sel.out) and torch.equal(selq.w_out, w.float())):
+        raise RuntimeError("fused selection + quantisation differs from the separate launches")
     bytes_sel = 4 * T * H + 4 * T + 4 * (wl["B"] + 1) + 8 * H * wl["B"] * wl["k_lmk"]
     front = measure_front_end(wl, w, cu, sel)
 
@@ -729,7 +740,8 @@ def main():
         "select_ms": sel_ms,
         "select": {"us": sel_ms * 1e3, "GB/s": bytes_sel / (sel_ms * 1e-3) / 1e9, "bytes": bytes_sel},
         "quantize_ms": qz_ms,
-        "path_ms": ms + sel_ms + qz_ms,
+        "select_quantize_us": selq_ms * 1e3,  # one launch: selection with the quantisation fused in
+        "path_ms": ms + selq_ms,
         "selector_front_end": front,
         "rope": measure_rope(wl, cu, ms),
         "module_path_c2": measure_module_path(wl),

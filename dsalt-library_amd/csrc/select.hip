@@ -12,10 +12,14 @@
 //    which marks "not a candidate". Keys are cached in LDS for n <= 16384.
 //  * If more than k_eff candidates exist, an MSB-first radix select over key - min_key
 //    (8-bit digits starting at the top bit of the candidates' key range, so that the
-//    first LDS histogram is not concentrated on a few exponent values; one wave scans
-//    the 256 bins) finds the exact k_eff-th key `thr` and how many keys equal to it are
-//    still needed. A pass whose boundary bin holds exactly the keys still needed ends the
-//    search: the selection is then every key at or above that bin's lower bound.
+//    first LDS histogram is not concentrated on a few exponent values) finds the exact
+//    k_eff-th key `thr` and how many keys equal to it are still needed. Each pass is one
+//    barrier: the histograms rotate over three LDS buffers (a pass counts into one and
+//    clears the next pass's, which the waves finished reading two barriers earlier) and
+//    every wave scans the 256 bins itself (one ds_read_b128 and a DPP scan), so no
+//    second barrier broadcasts the boundary bin. A pass whose boundary bin holds exactly
+//    the keys still needed ends the search: the selection is then every key at or above
+//    that bin's lower bound.
 //  * A final ordered pass emits the selected items in ascending order: each thread owns
 //    a contiguous run of items, and one workgroup scan of (keys > thr, keys == thr) gives
 //    every thread its first output slot. Keys == thr are taken in item order (ties: lower
@@ -30,6 +34,12 @@
 // another globally is ranked above it in its chunk too). select_kernel then selects
 // from the candidates, concatenated in chunk order (hence in position order).
 // Fully deterministic; integer-exact with respect to the fp32 scores.
+//
+// Window quantisation can ride along (w_out): the windows are then the continuous w~,
+// a token is covered when its offset o satisfies o + 1 <= q(w~) with q(w) = max(1,
+// floor(w)) (NaN kept, so never covered) - exactly the test on the quantised windows,
+// since q is idempotent - and the workgroups of head 0 write q(w~) for the tokens they
+// read, which saves the quantisation its own launch.
 #include "common.h"
 #include "launch.h"
 
@@ -63,6 +73,7 @@ struct SelParams {
     int64_t w_st;
     const int32_t *cu;
     int64_t *out;
+    float *w_out;  // non-null: w holds w~; q(w~) is written here and used for the covered test
     int num_seqs, n_heads, k;
     // chunked selection of long sequences (null ws_key: one workgroup per (head, sequence))
     uint32_t *ws_key;  // [H][n_chunk_ub][chunk_slots(k)] candidate keys, 0 in unused slots
@@ -118,17 +129,20 @@ __device__ __forceinline__ void block_excl_scan2(int a, int b, int lane, int wav
     eb = ob + ib - b;
 }
 
+// max(1, floor(w)), NaN kept: DSALTAttention._window_sizes(floor=True)
+__device__ __forceinline__ float quantize_window(float x) { return (x != x) ? x : fmaxf(floorf(x), 1.f); }
+
 struct SelShared {
     uint32_t keys[kSelCache];
-    int hist[2][256];  // double-buffered: pass n clears the buffer of pass n + 1
+    __align__(16) int hist[3][256];  // radix pass p counts into hist[p % 3], clears hist[(p + 1) % 3]
     int w[kSelWaves][2];
     int cnt[kSelWaves];  // written once: its readers need no trailing barrier
     uint32_t mm[kSelWaves][2];
-    int bc[3];
 };
 
-// The top k_eff of items 0 .. n-1 of key key_of(j) (0: not a candidate), emitted as
-// emit(slot, j, key) in ascending item order. The key pass and the histogram passes stride
+// The top k_eff of items 0 .. n-1 of key key_of(j, first) (0: not a candidate; `first`
+// is true on the first of possibly several calls per item), emitted as emit(slot, j, key)
+// in ascending item order. The key pass and the histogram passes stride
 // over items (j = tid + 1024 i: coalesced loads, conflict-free LDS); for the emission
 // thread t owns the contiguous items [t*C, t*C + C) (C = ceil(n / 1024)), which keeps
 // the output in item order with one workgroup scan. `all` emits NaN/+inf picks too (for
@@ -144,13 +158,13 @@ __device__ __forceinline__ int select_block(SelShared &sh, int n, int k_eff, int
     const bool cached = n <= kSelCache;
     const int C = (max(n, 0) + kSelThreads - 1) / kSelThreads;
     const int j0 = tid * C, j1 = min(j0 + C, max(n, 0));
-    auto key_at = [&](int j) -> uint32_t { return cached ? sh.keys[j] : key_of(j); };
+    auto key_at = [&](int j) -> uint32_t { return cached ? sh.keys[j] : key_of(j, false); };
 
     // pass 0: keys, candidate count and the candidates' key range
     int cnt = 0;
     uint32_t kmin = 0xFFFFFFFFu, kmax = 0u;
     for (int j = tid; j < n; j += kSelThreads) {
-        const uint32_t key = key_of(j);
+        const uint32_t key = key_of(j, true);
         if (cached) sh.keys[j] = key;
         if (key != 0u) {
             ++cnt;
@@ -182,63 +196,56 @@ __device__ __forceinline__ int select_block(SelShared &sh, int n, int k_eff, int
     int need_eq = 0;
     if (k_eff > 0 && ncand > cap) {
         // MSB-first radix select on rel = key - kmin, 8-bit digits from the top set bit of
-        // the candidates' range (the first digit is spread over the whole histogram)
+        // the candidates' range (the first digit is spread over the whole histogram).
+        // hist[0] was cleared before the barrier above; pass p clears hist[(p + 1) % 3] for
+        // the next pass: that buffer was counted in pass p - 2 and read by every wave
+        // before it counted pass p - 1, i.e. before the barrier that ended pass p - 1.
         const uint32_t range = kmax - kmin;
         const int nbits = range ? 32 - __clz((int)range) : 0;
         uint32_t prefix = 0u, pmask = 0u;
-        int remaining = k_eff, buf = 0;
-        for (int shift = max(nbits - 8, 0);; shift = max(shift - 8, 0)) {
-            // hist[buf] is zero here (cleared before the previous barrier)
-            int *hist = sh.hist[buf];
+        int remaining = k_eff;
+        for (int pass = 0, shift = max(nbits - 8, 0);; ++pass, shift = max(shift - 8, 0)) {
+            int *hist = sh.hist[pass % 3];
+            if (tid < 256) sh.hist[(pass + 1) % 3][tid] = 0;
             for (int j = tid; j < n; j += kSelThreads) {
                 const uint32_t key = key_at(j);
                 const uint32_t rel = key - kmin;
                 if (key != 0u && (rel & pmask) == prefix) atomicAdd(&hist[(rel >> shift) & 255u], 1);
             }
             __syncthreads();
-            if (wave == 1) sh.hist[buf ^ 1][lane * 4 + 0] = sh.hist[buf ^ 1][lane * 4 + 1] =
-                sh.hist[buf ^ 1][lane * 4 + 2] = sh.hist[buf ^ 1][lane * 4 + 3] = 0;  // next pass
-            if (wave == 0) {
-                // lane covers digits 255-4*lane .. 252-4*lane (descending)
-                const int c0 = hist[255 - 4 * lane], c1 = hist[254 - 4 * lane];
-                const int c2 = hist[253 - 4 * lane], c3 = hist[252 - 4 * lane];
-                const int sum4 = c0 + c1 + c2 + c3;
-                const int incl = wave_incl_scan_dpp(sum4);
-                const int excl = incl - sum4;
-                if (excl < remaining && incl >= remaining) {
-                    int cum = excl, d, cd;
-                    if (cum + c0 >= remaining) {
-                        d = 255 - 4 * lane;
-                        cd = c0;
-                    } else if ((cum += c0) + c1 >= remaining) {
-                        d = 254 - 4 * lane;
-                        cd = c1;
-                    } else if ((cum += c1) + c2 >= remaining) {
-                        d = 253 - 4 * lane;
-                        cd = c2;
-                    } else {
-                        cum += c2;
-                        d = 252 - 4 * lane;
-                        cd = c3;
-                    }
-                    sh.bc[0] = d;
-                    sh.bc[1] = cum;  // keys in the prefix with a larger digit
-                    sh.bc[2] = cd;   // keys in the prefix with digit d
-                }
+            // every wave finds the boundary digit: lane l holds digits 255-4l .. 252-4l
+            // (descending); exactly one lane's range reaches the remaining count
+            const int4 h4 = *reinterpret_cast<const int4 *>(&hist[252 - 4 * lane]);
+            const int c0 = h4.w, c1 = h4.z, c2 = h4.y, c3 = h4.x;
+            const int sum4 = c0 + c1 + c2 + c3;
+            const int incl = wave_incl_scan_dpp(sum4);
+            int cum = incl - sum4, d, cd;
+            if (cum + c0 >= remaining) {
+                d = 255 - 4 * lane;
+                cd = c0;
+            } else if ((cum += c0) + c1 >= remaining) {
+                d = 254 - 4 * lane;
+                cd = c1;
+            } else if ((cum += c1) + c2 >= remaining) {
+                d = 253 - 4 * lane;
+                cd = c2;
+            } else {
+                cum += c2;
+                d = 252 - 4 * lane;
+                cd = c3;
             }
-            __syncthreads();
-            prefix |= (uint32_t)sh.bc[0] << shift;
+            const int src = __builtin_ctzll(__ballot(incl - sum4 < remaining && incl >= remaining));
+            d = __builtin_amdgcn_readlane(d, src);
+            cum = __builtin_amdgcn_readlane(cum, src);  // keys in the prefix with a larger digit
+            cd = __builtin_amdgcn_readlane(cd, src);    // keys in the prefix with digit d
+            prefix |= (uint32_t)d << shift;
             pmask |= 0xFFu << shift;
-            remaining -= sh.bc[1];
+            remaining -= cum;
             // the keys with rel >= prefix (the bin and everything above it) number at most
             // `cap`: they are the selection (cap = k_eff: every key of the bin is needed)
             // or a superset of it (cap > k_eff, for candidates), whatever the lower digits
             // are - the passes for them are skipped
-            const bool whole_bin = k_eff - remaining + sh.bc[2] <= cap;
-            buf ^= 1;
-            // no barrier here: bc is rewritten only after the next pass's histogram
-            // barrier, which every thread reaches after this read
-            if (whole_bin) {
+            if (k_eff - remaining + cd <= cap) {
                 thr = kmin + prefix - 1u;  // kmin >= 1: thr >= 0 and key 0 is never taken
                 need_eq = 0;
                 break;
@@ -281,6 +288,19 @@ __device__ __forceinline__ int select_block(SelShared &sh, int n, int k_eff, int
     return gt_tot + (eq_ok ? min(eq_tot, need_eq) : 0);
 }
 
+// Key of token `tok` at offset `pos` of its sequence for `head`: 0 when covered
+// (pos < trunc(w), i.e. pos + 1 <= w for the integer pos + 1; with w_out the test is on
+// q(w~) and, on the first visit by a head-0 workgroup, q(w~) is stored).
+__device__ __forceinline__ uint32_t cand_key(const SelParams &p, int head, int pos, int64_t tok, bool first) {
+    float wv = p.w[tok * p.w_st];
+    const uint32_t key = order_key(p.scores[tok * p.sc_st + (int64_t)head * p.sc_sh]);
+    if (p.w_out) {
+        wv = quantize_window(wv);
+        if (first && head == 0) p.w_out[tok] = wv;
+    }
+    return ((float)(pos + 1) <= wv) ? 0u : key;
+}
+
 // Chunks of long sequences (L > kSplitMin): one workgroup per (head, chunk id of
 // find_block over kSelChunk-position chunks); a superset of the chunk's top k (at most
 // chunk_slots(k) items, NaN/+inf picks included) to the workspace as (key, position)
@@ -299,12 +319,10 @@ __global__ void __launch_bounds__(kSelThreads) select_chunk_kernel(const SelPara
     const int cs = chunk_slots(p.k);
     uint32_t *ck = p.ws_key + ((int64_t)head * p.n_chunk_ub + cid) * cs;
     int32_t *cp = p.ws_pos + ((int64_t)head * p.n_chunk_ub + cid) * cs;
-    auto key_of = [&](int j) -> uint32_t {
+    auto key_of = [&](int j, bool first) -> uint32_t {
         const int pos = c0 + j;
         const int64_t tok = (int64_t)start + pos;
-        // covered <=> pos < trunc(w_pos) <=> pos + 1 <= w_pos   (pos >= 0 integer)
-        if ((float)(pos + 1) <= p.w[tok * p.w_st]) return 0u;
-        return order_key(p.scores[tok * p.sc_st + (int64_t)head * p.sc_sh]);
+        return cand_key(p, head, pos, tok, first);
     };
     auto emit = [&](int slot, int j, uint32_t key) {
         if (slot < cs) {
@@ -337,7 +355,7 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
         const uint32_t *gk = p.ws_key + ((int64_t)head * p.n_chunk_ub + start / kSelChunk + seq) * cs;
         const int32_t *gp = p.ws_pos + ((int64_t)head * p.n_chunk_ub + start / kSelChunk + seq) * cs;
         int32_t *s_pos = reinterpret_cast<int32_t *>(sh.keys + kMergeCap);
-        auto key_of = [&](int j) -> uint32_t {  // pass 0 only (n <= kMergeCap: cached)
+        auto key_of = [&](int j, bool) -> uint32_t {  // pass 0 only (n <= kMergeCap: cached)
             s_pos[j] = gp[j];
             return gk[j];
         };
@@ -346,11 +364,8 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
         };
         total = select_block(sh, n, k_eff, k_eff, false, key_of, emit);
     } else {
-        auto key_of = [&](int j) -> uint32_t {
-            const int64_t tok = (int64_t)start + j;
-            // covered <=> j < trunc(w_j) <=> j + 1 <= w_j   (j >= 0 integer)
-            if ((float)(j + 1) <= p.w[tok * p.w_st]) return 0u;
-            return order_key(p.scores[tok * p.sc_st + (int64_t)head * p.sc_sh]);
+        auto key_of = [&](int j, bool first) -> uint32_t {
+            return cand_key(p, head, j, (int64_t)start + j, first);
         };
         auto emit = [&](int slot, int j, uint32_t) {
             if (slot < p.k) out[slot] = j;
@@ -360,13 +375,13 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
     for (int s2 = total + tid; s2 < p.k; s2 += kSelThreads) out[s2] = -1;
 }
 
-__global__ void quantize_kernel(const float *__restrict__ w, int64_t n, float *__restrict__ wq,
+__global__ void quantize_kernel(const float *__restrict__ w, int64_t w_st, int64_t n, float *__restrict__ wq,
                                 int32_t *__restrict__ wi) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= n) return;
-    const float x = w[idx];
+    const float x = w[idx * w_st];
     const float f = floorf(x);
-    if (wq) wq[idx] = (x != x) ? x : fmaxf(f, 1.f);
+    if (wq) wq[idx] = quantize_window(x);
     if (wi) wi[idx] = (x >= 1.f) ? (int32_t)fminf(f, 1073741824.f) : 1;
 }
 
@@ -382,7 +397,13 @@ int64_t select_workspace_bytes(int total_len, int num_seqs, int n_heads, int k) 
 }
 
 hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream) {
-    if (a.k_lmk == 0) return hipSuccess;
+    if (a.k_lmk == 0) {  // nothing to select; the windows are still quantised
+        if (!a.w_out || a.total_len == 0) return hipSuccess;
+        const int64_t blocks = ((int64_t)a.total_len + 255) / 256;
+        hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a.w, a.w_stride,
+                           (int64_t)a.total_len, a.w_out, (int32_t *)nullptr);
+        return hipGetLastError();
+    }
     SelParams p;
     p.scores = a.scores;
     p.sc_st = a.scores_stride_t;
@@ -391,6 +412,7 @@ hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream) {
     p.w_st = a.w_stride;
     p.cu = a.cu_seqlens;
     p.out = a.lmk_pos;
+    p.w_out = a.w_out;
     p.num_seqs = a.num_seqs;
     p.n_heads = a.n_heads;
     p.k = a.k_lmk;
@@ -414,8 +436,8 @@ hipError_t launch_quantize(const float *w_cont, int64_t n, float *w_out, int32_t
     if (n == 0 || (!w_out && !w_int)) return hipSuccess;
     const int threads = 256;
     const int64_t blocks = (n + threads - 1) / threads;
-    hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)blocks), dim3(threads), 0, stream, w_cont, n, w_out,
-                       w_int);
+    hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)blocks), dim3(threads), 0, stream, w_cont, (int64_t)1, n,
+                       w_out, w_int);
     return hipGetLastError();
 }
 

@@ -25,7 +25,7 @@ DTYPE_BF16 = 0
 DTYPE_F16 = 1
 DTYPE_F32 = 2
 MAX_K_LMK = 1024
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _DTYPES = {torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
 
@@ -90,6 +90,7 @@ class SelectArgs(ctypes.Structure):
         ("lmk_pos", c_void_p),
         ("workspace", c_void_p), ("workspace_bytes", c_int64),
         ("max_seqlen", c_int32),
+        ("w_out", c_void_p),
     ]
 
 
@@ -614,11 +615,12 @@ class DenseBwdLauncher:
         _raise(self._fn(self._ref, stream_handle(self.device)), "dsalt_bwd (dense)")
 
 
-def _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen=None):
+def _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen=None, w_out=None):
     """The argument block of one selection and the tensors it points into. chunked:
     pass the workspace, so that long sequences are selected chunk-wise; max_seqlen (a
     bound on the sequence lengths, None: unknown) lets the library skip the chunk stage
-    when no sequence is long."""
+    when no sequence is long; w_out (fp32 [T], contiguous): w is the continuous w~ and
+    the kernel also writes the quantised windows there."""
     if scores.dtype != torch.float32:
         raise DsaltError(f"scores must be float32, got {scores.dtype}")
     T, H = scores.shape
@@ -630,6 +632,10 @@ def _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen=None):
     a.cu_seqlens = cu.data_ptr()
     a.lmk_pos = out.data_ptr()
     a.max_seqlen = 0 if max_seqlen is None else min(int(max_seqlen), 2**31 - 1)
+    if w_out is not None:
+        if w_out.dtype != torch.float32 or w_out.numel() != T or (T > 1 and w_out.stride(0) != 1):
+            raise DsaltError("w_out must be a contiguous float32 tensor of total_len entries")
+        a.w_out = w_out.data_ptr()
     ws = None
     if chunked and (max_seqlen is None or max_seqlen > SELECT_SPLIT_MIN):
         ws_bytes = lib().dsalt_select_workspace_size(T, S, H, k_lmk)
@@ -638,7 +644,7 @@ def _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen=None):
         if ws_bytes > 0:
             ws = torch.empty(ws_bytes, device=scores.device, dtype=torch.uint8)
             a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
-    return a, (scores, w, cu, out, ws)
+    return a, (scores, w, cu, out, ws, w_out)
 
 
 def select_landmarks(scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Tensor,
@@ -655,6 +661,21 @@ def select_landmarks(scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Te
     a, _keep = _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen)
     _raise(lib().dsalt_select_landmarks(ctypes.byref(a), stream_handle(dev)), "dsalt_select_landmarks")
     return out
+
+
+def select_landmarks_quantize(scores: torch.Tensor, w_cont: torch.Tensor, cu_seqlens: torch.Tensor,
+                              k_lmk: int, chunked: bool = True, max_seqlen: int | None = None):
+    """The window quantisation and the landmark selection in one launch: returns (w [T]
+    fp32 = max(1, floor(w~)), NaN kept; landmark positions [H, S, k] as select_landmarks
+    returns them for that w)."""
+    dev = require_gpu(scores, w_cont, cu_seqlens)
+    cu = _cu_i32(cu_seqlens)
+    w_cont = _f32_vec(w_cont)
+    out = torch.empty((scores.shape[1], cu.shape[0] - 1, k_lmk), device=dev, dtype=torch.int64)
+    w_out = torch.empty(w_cont.shape[0], device=dev, dtype=torch.float32)
+    a, _keep = _select_args(scores, w_cont, cu, k_lmk, out, chunked, max_seqlen, w_out)
+    _raise(lib().dsalt_select_landmarks(ctypes.byref(a), stream_handle(dev)), "dsalt_select_landmarks")
+    return w_out, out
 
 
 _SCORE_DTYPES = {torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16, torch.float32: DTYPE_F32}
@@ -697,6 +718,28 @@ def scores_workspace_size(T: int, n_kv: int) -> int:
     if n < 0:
         raise DsaltError("invalid sizes for dsalt_scores_workspace_size")
     return n
+
+
+SCORES_MAX_KV = 128  # largest n_kv_heads of dsalt_hybrid_scores
+
+
+def scores_supported(x: torch.Tensor, v: torch.Tensor) -> bool:
+    """Whether dsalt_hybrid_scores takes x [T, d] and v [T, n_kv, D] (dtype and shape rules
+    of dsalt_scores_check): bf16 / fp16 / fp32, d and D multiples of one 16-byte load,
+    D / (elements per load) a power of two <= 64, n_kv <= 128."""
+    if x.dtype not in _SCORE_DTYPES or v.dtype not in _SCORE_DTYPES or x.dim() != 2 or v.dim() != 3:
+        return False
+    ex = 4 if x.dtype == torch.float32 else 8
+    ev = 4 if v.dtype == torch.float32 else 8
+    d, n_kv, D = x.shape[1], v.shape[1], v.shape[2]
+    g = D // ev
+    if not (d % ex == 0 and D % ev == 0 and 0 < g <= 64 and (g & (g - 1)) == 0 and 1 <= n_kv <= SCORES_MAX_KV):
+        return False
+    # operands as hybrid_scores passes them (a strided last dim is made contiguous there)
+    xs = x.stride(0) if x.stride(1) == 1 else d
+    vt, vh = (v.stride(0), v.stride(1)) if v.stride(2) == 1 else (n_kv * D, D)
+    aligned = (x.stride(1) != 1 or x.data_ptr() % 16 == 0) and (v.stride(2) != 1 or v.data_ptr() % 16 == 0)
+    return aligned and xs >= d and xs % ex == 0 and vt >= 0 and vh >= 0 and vt % ev == 0 and vh % ev == 0
 
 
 def hybrid_scores(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int,
@@ -798,11 +841,14 @@ class SelectLauncher:
     selection kernel on the current stream (for timing loops); `out` holds the result."""
 
     def __init__(self, scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Tensor, k_lmk: int,
-                 chunked: bool = True, max_seqlen: int | None = None):
+                 chunked: bool = True, max_seqlen: int | None = None, quantize: bool = False):
         self.device = require_gpu(scores, w, cu_seqlens)
         cu = _cu_i32(cu_seqlens)
         self.out = torch.empty((scores.shape[1], cu.shape[0] - 1, k_lmk), device=self.device, dtype=torch.int64)
-        self._args, self._keep = _select_args(scores, _f32_vec(w), cu, k_lmk, self.out, chunked, max_seqlen)
+        w = _f32_vec(w)
+        # quantize: w is w~ and the launch also writes the quantised windows to self.w_out
+        self.w_out = torch.empty(w.shape[0], device=self.device, dtype=torch.float32) if quantize else None
+        self._args, self._keep = _select_args(scores, w, cu, k_lmk, self.out, chunked, max_seqlen, self.w_out)
         self._ref = ctypes.byref(self._args)
         self._fn = lib().dsalt_select_landmarks
 

@@ -86,12 +86,14 @@ def selection_scores(x: torch.Tensor, W_V: torch.Tensor, alpha: torch.Tensor, n_
       the same torch norms on ``v`` (torch forms ``v_proj(x)`` with the same matmul, so
       the scores are bit-identical and the second GEMM is saved).
     * ``hip_scores``: the one-pass HIP kernel over x and v (deterministic; its fp32 norm
-      sums run in another order than torch's, so a 16-bit norm can land one ulp away and
-      move a near-tie landmark).
+      sums run in another order than torch's, so a score can differ from the torch
+      route's in its last bits - a near-tie landmark could move; the landmark sets of
+      configs 2 and 4 are those of the torch route, set for set). Shapes the kernel does
+      not take (``_hip.scores_supported``) use the torch norms on ``v``.
     """
     if v is None:
         return _score_block(x, W_V, alpha, n_heads, dh)
-    if hip_scores:
+    if hip_scores and _hip.scores_supported(x, v):
         return _hip.hybrid_scores(x.detach(), v.detach(), alpha, n_heads)
     return hybrid_scores_from_v(x, v, alpha, n_heads)
 
@@ -129,6 +131,24 @@ def _compute_landmark_indices(
         max_len = None if cu_list is None else max((b - a for a, b in zip(cu_list[:-1], cu_list[1:])), default=0)
         lmk = _hip.select_landmarks(scores.float(), w_sizes, cu_seqlens, int(k_lmk), max_seqlen=max_len)
     return lmk, z_x, z_v
+
+
+def _landmarks_and_windows(x: torch.Tensor, W_V: torch.Tensor, alpha: torch.Tensor, w_cont: torch.Tensor,
+                           cu_seqlens: torch.Tensor, k_lmk: int, cu_list: list | None = None,
+                           head_dim: int | None = None, v: torch.Tensor | None = None,
+                           hip_scores: bool = False):
+    """``(w_sizes [T] fp32, lmk [H, S, k_lmk] int64)``: the window quantisation of
+    ``DSALTAttention._window_sizes(floor=True)`` (dsalt_attention.py:277-284 of the
+    reference) and :func:`_compute_landmark_indices` on those windows, with the
+    quantisation done by the selection launch itself (``w_cont`` is the continuous
+    ``w~``). Same results as the two steps apart."""
+    n_heads = alpha.shape[0]
+    dh = head_dim if head_dim is not None else W_V.shape[0] // n_heads
+    with torch.no_grad():
+        scores, _, _ = selection_scores(x, W_V, alpha, n_heads, dh, v, hip_scores)
+        max_len = None if cu_list is None else max((b - a for a, b in zip(cu_list[:-1], cu_list[1:])), default=0)
+        return _hip.select_landmarks_quantize(scores.float(), w_cont.detach(), cu_seqlens, int(k_lmk),
+                                              max_seqlen=max_len)
 
 
 def _build_landmark_kv(K: torch.Tensor, V: torch.Tensor, lmk_indices: torch.Tensor,

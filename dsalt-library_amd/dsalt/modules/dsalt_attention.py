@@ -38,7 +38,7 @@ from .. import _hip
 from ..kernels._dense import dense_attention, dense_probabilities
 from ..kernels._sparse import sparse_attention
 from ..kernels.landmark_tokens_ker import hybrid_scores_from_v, hybrid_scores_per_head
-from ..kernels.selectors import _compute_landmark_indices
+from ..kernels.selectors import _compute_landmark_indices, _landmarks_and_windows
 from ..kernels.window_utils import apply_rotary_emb_packed, build_rope_cache, rotate_packed
 
 
@@ -57,16 +57,19 @@ class DSALTAttention(nn.Module):
 
     ``_fused_selector`` (default True): without a projection bias the landmark scores are
     formed from the module's own value projection ``v = x W_V^T`` instead of a second
-    ``x @ W_V.T`` GEMM, with the reference's torch norm and standardisation ops, so the
-    fp32 scores (and therefore the selected landmarks) are bit-identical to the
-    reference's route. ``_hip_scores`` (default False) computes them instead with the
-    one-pass HIP score kernel, which saves the torch passes but rounds its fp32 norm sums
-    in another order (a 16-bit norm can land one ulp away and move a near-tie landmark).
+    ``x @ W_V.T`` GEMM. ``_hip_scores`` (default True) forms the selection's scores with
+    the one-pass HIP score kernel over x and v (norms, standardisation and the hybrid
+    combination in two launches, no torch passes); it rounds its fp32 norm sums in another
+    order than torch, so a score can differ in its last bits from the reference's route -
+    the landmark sets of configs 2 and 4 (fp32, bf16, autocast) are the reference route's,
+    set for set, but a near-tie could move. ``_hip_scores = False`` keeps torch's own norm
+    and standardisation ops on v, whose fp32 scores are bit-identical to the reference's
+    route. The differentiable landmark weights of training always use the torch ops.
     ``_last_selection`` holds the ``(windows, landmark positions)`` of the last forward.
     """
 
     _fused_selector = True
-    _hip_scores = False
+    _hip_scores = True
 
     def __init__(
         self,
@@ -235,13 +238,11 @@ class DSALTAttention(nn.Module):
         w_cont = self._window_continuous(x)
         alpha = self._alpha()
         route_v = v if self._fused_selector else None
-        with torch.no_grad():
-            w_disc = _hip.quantize_windows(w_cont.detach())
-            lmk_pos, _, _ = _compute_landmark_indices(
-                x.detach(), self.v_proj.weight.detach(), alpha.detach().float(),
-                w_disc, cu_seqlens, self.k_lmk, self.n_min, total_len, cu_list,
-                head_dim=self.head_dim, v=None if route_v is None else route_v.detach(),
-                hip_scores=self._hip_scores)
+        with torch.no_grad():  # windows quantised by the selection launch
+            w_disc, lmk_pos = _landmarks_and_windows(
+                x.detach(), self.v_proj.weight.detach(), alpha.detach().float(), w_cont.detach(),
+                cu_seqlens, self.k_lmk, cu_list, head_dim=self.head_dim,
+                v=None if route_v is None else route_v.detach(), hip_scores=self._hip_scores)
         # the differentiable scores (the selection above ran on a detached copy of them)
         if route_v is not None:
             scores, _, _ = hybrid_scores_from_v(x, route_v, alpha, self.n_heads)
@@ -291,13 +292,15 @@ class DSALTAttention(nn.Module):
                                    self.tau_win, float(self.win_edge))
             return self._apply_out_proj(out.reshape(total_len, self.d_model)), aux
 
-        w_sizes = self._window_sizes(x, floor=True)
         alpha = self._alpha()
         route_v = v_sel if self._fused_selector else None
-        lmk_indices, _, _ = _compute_landmark_indices(
-            x.detach(), self.v_proj.weight.detach(), alpha.detach().float(), w_sizes,
-            cu_seqlens, self.k_lmk, self.n_min, total_len, cu_list, head_dim=self.head_dim,
-            v=None if route_v is None else route_v.detach(), hip_scores=self._hip_scores)
+        # the windows are quantised by the selection launch itself (same values as
+        # _window_sizes(floor=True) followed by _compute_landmark_indices)
+        with torch.no_grad():
+            w_sizes, lmk_indices = _landmarks_and_windows(
+                x.detach(), self.v_proj.weight.detach(), alpha.detach().float(), self._window_continuous(x),
+                cu_seqlens, self.k_lmk, cu_list, head_dim=self.head_dim,
+                v=None if route_v is None else route_v.detach(), hip_scores=self._hip_scores)
         self._last_selection = (w_sizes, lmk_indices)
         # Hard A(i) = W(i) ∪ L(i): the score only selects (zero landmark bias).
         out = sparse_attention(_hip.MODE_HARD, q, k, v, lmk_indices, None, w_sizes, cu_seqlens,

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define DSALT_ABI_VERSION 1
+#define DSALT_ABI_VERSION 2
 
 enum {
     DSALT_OK = 0,
@@ -220,6 +220,13 @@ int dsalt_bwd_noalloc(const dsalt_bwd_args *args, void *stream);
  * means no sequence can use it. max_seqlen: 0, or a bound on every sequence's length
  * (the chunk stage is skipped when it is <= 4096, saving its launch when no sequence is
  * long; a bound that is too small only means the one-workgroup route for everything).
+ * w_out (optional, NULL allowed): fuses the window quantisation of
+ * DSALTAttention._window_sizes(floor=True) (dsalt/modules/dsalt_attention.py:277-284)
+ * into the selection. w then holds the continuous windows w~; w_out [T] (contiguous)
+ * receives q(w~) = max(1, floor(w~)) (NaN stays NaN) for every token of
+ * [cu_seqlens[0], cu_seqlens[S]), and a token is covered iff o + 1 <= q(w~) - the
+ * selection is that of dsalt_quantize_windows followed by this call without w_out.
+ * w_out may equal w (in place).
  */
 typedef struct dsalt_select_args {
     int32_t total_len, num_seqs, n_heads, k_lmk;
@@ -232,6 +239,7 @@ typedef struct dsalt_select_args {
     void *workspace;  /* NULL, or >= dsalt_select_workspace_size(...) bytes, 16-byte aligned */
     int64_t workspace_bytes;
     int32_t max_seqlen; /* 0 (unknown) or an upper bound on the sequence lengths */
+    float *w_out;       /* NULL, or [T] fp32: quantised windows (w is then w~) */
 } dsalt_select_args;
 
 int64_t dsalt_select_workspace_size(int32_t total_len, int32_t num_seqs, int32_t n_heads, int32_t k_lmk);

@@ -335,6 +335,42 @@ def test_select_chunked_equals_single_workgroup_c4():
     np.testing.assert_array_equal(got, orc.select_landmarks(scores, w, cu, 128))
 
 
+@pytest.mark.parametrize("lens,H,k", [
+    ([50, 0, 7, 300], 4, 16),
+    ([2048] * 4, 16, 64),                  # config 2's shape
+    ([4097, 6000, 50, 16384], 2, 64),      # chunk-wise sequences write their windows from the chunks
+    ([20000, 33], 2, 128),                 # longer than the LDS key cache (keys re-read)
+    ([30, 70], 3, 0),                      # nothing to select: only the quantisation
+])
+def test_select_with_quantize_bit_exact(lens, H, k):
+    """Selection with the window quantisation fused in (w_out): the quantised windows are
+    the oracle's max(1, floor(w~)) (NaN kept) bit for bit, and the selection is the
+    oracle's on those windows - including continuous windows below 1 (a token at offset
+    0 is then covered) and NaN windows (never covered). In place (w_out = w) gives the
+    same."""
+    print(f"select+quantize lens={lens[:3]} H={H} k={k}", flush=True)
+    scores, _, cu = _select_case(len(lens) * 7 + k, lens, H, tie=True)
+    rng = np.random.default_rng(k + 3)
+    T = scores.shape[0]
+    w = (rng.random(T) * 80 - 10).astype(np.float32)   # includes w~ < 1 and negative
+    w[rng.random(T) < 0.02] = np.nan
+    w[rng.random(T) < 0.01] = np.inf
+    dev = torch.device("cuda", 0)
+    st = torch.from_numpy(scores).to(dev)
+    cut = torch.from_numpy(cu).to(torch.int32).to(dev)
+    wq, got = hip.select_landmarks_quantize(st, torch.from_numpy(w).to(dev), cut, k)
+    wq_ref = orc.quantize_windows(w)
+    np.testing.assert_array_equal(wq.cpu().numpy(), wq_ref)
+    np.testing.assert_array_equal(got.cpu().numpy(), orc.select_landmarks(scores, wq_ref, cu, k))
+    # in place: the windows buffer receives the quantised values
+    wbuf = torch.from_numpy(w).to(dev)
+    out = torch.empty((H, len(lens), k), device=dev, dtype=torch.int64)
+    a, _keep = hip._select_args(st, wbuf, cut, k, out, True, None, wbuf)
+    assert hip.lib().dsalt_select_landmarks(hip.ctypes.byref(a), hip.stream_handle(dev)) == 0
+    np.testing.assert_array_equal(wbuf.cpu().numpy(), wq_ref)
+    np.testing.assert_array_equal(out.cpu().numpy(), got.cpu().numpy())
+
+
 def test_quantize_bit_exact():
     rng = np.random.default_rng(1)
     w = np.concatenate([rng.random(10000).astype(np.float32) * 600 - 50,

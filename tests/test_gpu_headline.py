@@ -1,11 +1,11 @@
 """Headline configurations on the selectors the module actually produces.
 
-* Selection route parity at config 2 (seed 1): the module's default route (the hybrid
-  scores from its own value projection v = x W_V^T, torch norms) must pick exactly the
-  landmark sets of the reference's route (x @ W_V.T, then the norms), per (head,
-  sequence), for an fp32 module, a bf16 module and an fp32 module under bf16 autocast.
-  The opt-in HIP score kernel's agreement is reported (it rounds its norm sums in another
-  order).
+* Selection route parity at configs 2 (seed 1) and 4 (seed 3): the module's default
+  route (the HIP score kernel over x and its own value projection v = x W_V^T) and the
+  torch route on v must both pick exactly the landmark sets of the reference's route
+  (x @ W_V.T, then torch's norms), per (head, sequence), for an fp32 module, a bf16
+  module and an fp32 module under bf16 autocast; the torch route on v also gives the
+  same fp32 scores bit for bit.
 * Forward parity at configs 2 and 4, HARD and SOFT, on the windows and landmarks the
   module produces (built as bench.py builds them: seed 1 / seed 3, x ~ N(0, 1)), against
   the fp64 oracle on a window of query rows of every sequence. Bar (north star):
@@ -30,9 +30,9 @@ def _errs(got, ref):
     return diff.abs().max().item(), (diff.norm() / ref.double().norm().clamp_min(1e-30)).item()
 
 
-def _c2_module(dtype_mode):
+def _c2_module(dtype_mode, cfg="c2"):
     from dsalt.modules import DSALTAttention
-    B, L, d_model, H, n_min, n_max, k_lmk, seed = bench.CONFIGS["c2"]
+    B, L, d_model, H, n_min, n_max, k_lmk, seed = bench.CONFIGS[cfg]
     torch.manual_seed(seed)
     mod = DSALTAttention(d_model, H, n_min, n_max, k_lmk, max_seq_len=L)
     x = torch.randn(B * L, d_model)
@@ -54,25 +54,22 @@ def _run_route(mod, x, cu, fused, hip_scores, autocast):
     return w.clone(), lmk.clone()
 
 
-@pytest.mark.parametrize("dtype_mode", ["fp32", "bf16", "autocast"])
-def test_c2_default_selection_equals_gemm_route(dtype_mode):
-    print(f"c2 selection routes {dtype_mode}", flush=True)
-    mod, x, cu = _c2_module(dtype_mode)
+@pytest.mark.parametrize("cfg,dtype_mode", [("c2", "fp32"), ("c2", "bf16"), ("c2", "autocast"),
+                                            ("c4", "bf16"), ("c4", "autocast")])
+def test_default_selection_equals_gemm_route(cfg, dtype_mode):
+    print(f"{cfg} selection routes {dtype_mode}", flush=True)
+    mod, x, cu = _c2_module(dtype_mode, cfg)
     ac = dtype_mode == "autocast"
     w_g, lmk_g = _run_route(mod, x, cu, fused=False, hip_scores=False, autocast=ac)
-    w_f, lmk_f = _run_route(mod, x, cu, fused=True, hip_scores=False, autocast=ac)
-    assert torch.equal(w_g, w_f)
+    w_t, lmk_t = _run_route(mod, x, cu, fused=True, hip_scores=False, autocast=ac)
+    w_h, lmk_h = _run_route(mod, x, cu, fused=True, hip_scores=True, autocast=ac)
+    mod._fused_selector, mod._hip_scores = True, True
+    assert torch.equal(w_g, w_t) and torch.equal(w_g, w_h)
     # slots are emitted in ascending position order, so equal sets are equal rows
-    same = (lmk_g == lmk_f).all(-1)
-    print(f"  default route: {int(same.sum())}/{same.numel()} (head, sequence) sets equal", flush=True)
-    assert bool(same.all()), f"{int((~same).sum())} landmark sets differ from the x @ W_V.T route"
-    # the opt-in HIP score kernel: reported, near-ties may move
-    _, lmk_h = _run_route(mod, x, cu, fused=True, hip_scores=True, autocast=ac)
-    slots = (lmk_h == lmk_g).float().mean().item()
-    sets = (lmk_h == lmk_g).all(-1).float().mean().item()
-    print(f"  HIP score kernel: {slots:.4%} of the slots, {sets:.2%} of the sets equal", flush=True)
-    assert slots > 0.99
-    mod._fused_selector, mod._hip_scores = True, False
+    for name, lmk in (("torch route on v", lmk_t), ("HIP score kernel (default)", lmk_h)):
+        same = (lmk_g == lmk).all(-1)
+        print(f"  {name}: {int(same.sum())}/{same.numel()} (head, sequence) sets equal", flush=True)
+        assert bool(same.all()), f"{name}: {int((~same).sum())} landmark sets differ from the x @ W_V.T route"
 
 
 @pytest.mark.parametrize("cfg,windows", [("c2", [(0, 256), (1024, 1280), (1536, 1792)]),

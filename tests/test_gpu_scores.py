@@ -153,8 +153,10 @@ def test_module_fused_selector(training):
         out, _ = m(x, cu_seqlens=cu, cu_list=cu.tolist())
         outs.append(out.detach())
         sels.append(m._last_selection[1].clone())
-    m._fused_selector, m._hip_scores = True, False
-    # the default route is the GEMM route's selection, hence the same output bit for bit
+    m._fused_selector, m._hip_scores = True, True
+    # the torch route on v is the GEMM route's selection, hence the same output bit for
+    # bit; the default HIP score route selects the same sets here
     assert torch.equal(sels[0], sels[1]) and torch.equal(outs[0], outs[1])
+    assert torch.equal(sels[2], sels[1])
     err = (outs[2] - outs[1]).abs().max().item()
     assert err < 2e-2, f"HIP-score selector output differs by {err}"
