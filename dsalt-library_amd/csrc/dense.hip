@@ -71,7 +71,7 @@ struct DenseParams {
     float inv_c;     // 1 / c
     float scale;
     float inv_tau, win_edge;
-    int edge_fast;   // the window tail from per-tile factors (16 / tau < 80)
+    int edge_fast;   // the window tail from per-tile factors (13.5 / tau < 40)
 };
 
 // First key of the zero-bias core (d <= w~ - win_edge, i.e. j >= i - floor(w~ - win_edge))
@@ -824,7 +824,11 @@ void set_common(DenseParams &p, float scale, float tau_win, float win_edge) {
     p.inv_c = 1.f / p.c;
     p.inv_tau = 1.f / tau_win;
     p.win_edge = win_edge;
-    p.edge_fast = 16.f * p.inv_tau < 80.f;
+    // The factored tail e = E * ec[r] needs E = exp((A - w~ - 13.5) / tau) finite wherever
+    // the true e = exp((d - w~) / tau) is below the clamp (e <= e^46; beyond it the bias is
+    // log 1e-20 either way): E <= e^46 / min ec = e^(46 + 13.5 / tau) < e^88 needs
+    // 13.5 / tau < 42; with a margin, tau > 0.3375. Smaller tau takes one exp per element.
+    p.edge_fast = kEdgeMidD * p.inv_tau < 40.f;
 }
 
 template <typename DT>

@@ -199,8 +199,12 @@ int dsalt_bwd_check(const dsalt_bwd_args *args);
  * (other streams, other threads) race and must be serialised by the caller. The array
  * keeps the last call's contents; the kernels write every scratch entry they read.
  * The first call on a device looks the array's address up (with that device current).
+ * The size covers the backward of every benchmark configuration of the reference (the
+ * largest, 16 heads x 128 dims over one 16384-token sequence with k = 128, needs 75.3 MiB);
+ * since the array sits in the library's code object, every process that loads the
+ * library holds it on each GPU it launches on, whether or not it calls this entry point.
  */
-#define DSALT_NOALLOC_SCRATCH_BYTES ((int64_t)128 << 20)
+#define DSALT_NOALLOC_SCRATCH_BYTES ((int64_t)76 << 20)
 int dsalt_bwd_noalloc(const dsalt_bwd_args *args, void *stream);
 
 /*

@@ -121,6 +121,36 @@ def test_dense_kernels_match_oracle(case):
     check(d_w, dw_r, "d_w")
 
 
+@pytest.mark.parametrize("tau", [0.15, 0.25, 3.0])
+@pytest.mark.parametrize("edge", [2.0, 8.0])
+@pytest.mark.parametrize("case", [CASES[1], CASES[3], CASES[5]], ids=["T33-D64", "T257-D64", "T200-D128"])
+def test_dense_edge_params(case, tau, edge):
+    """Other window-edge temperatures and widths than the module default (tau = 1,
+    win_edge = 4): tau = 0.15 takes one exp per tail element, tau = 0.25 also (its
+    factored tail would overflow where the true bias is still above the clamp), tau = 3
+    the factored tail; every output and gradient against the fp64 oracle."""
+    T, H, D, dtype, seed, w_kind, lmk = case
+    print(f"dense edge params T={T} D={D} tau={tau} edge={edge}", flush=True)
+    q, k, v, w, lb = make_case(T, H, D, dtype, seed, w_kind, lmk)
+    scale = 1.0 / math.sqrt(D)
+    qg, kg, vg, wg = (t.to(DEV) for t in (q, k, v, w))
+    lbg = None if lb is None else lb.to(DEV)
+    out, lse = hip.dense_fwd(qg, kg, vg, wg, lbg, scale, tau, edge, out_dtype=torch.float32)
+    dout = torch.randn(T, H, D, generator=torch.Generator().manual_seed(seed + 200)).to(dtype)
+    dq, dk, dv, d_lb, d_w = hip.dense_bwd(qg, kg, vg, out, lse, dout.to(DEV), wg, lbg, scale, tau, edge,
+                                          need_dw=True, grad_dtype=torch.float32)
+    torch.cuda.synchronize()
+    o_r, l_r, dq_r, dk_r, dv_r, dlb_r, dw_r = oracle_grads(q, k, v, w, lb, dout, tau, edge)
+    check(out, o_r, "O")
+    assert (lse.cpu().double() - l_r).abs().max().item() <= 2e-2
+    check(dq, dq_r, "dQ")
+    check(dk, dk_r, "dK")
+    check(dv, dv_r, "dV")
+    if lb is not None:
+        check(d_lb, dlb_r, "d_lmk_bias")
+    check(d_w, dw_r, "d_w")
+
+
 def test_dense_output_dtypes_and_relaunch():
     # 16-bit outputs and gradients equal the fp32 ones rounded; a second launch of the
     # same launcher reproduces the first bit for bit (deterministic, no stale state)
