@@ -612,6 +612,8 @@ def main():
     ap.add_argument("--no-backward", action="store_true", help="skip the config-3 backward measurement")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the config-4, dense-variant and config-5 LM measurements")
+    ap.add_argument("--only-fwd", action="store_true",
+                    help="time only the headline forward of --config and exit (for profiling)")
     ap.add_argument("--only", choices=("lm", "dense", "backward", "c4"), default=None,
                     help="run only that measurement and print its JSON (for profiling)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
@@ -646,6 +648,9 @@ def main():
 
     step = _hip.FwdLauncher(_hip.MODE_HARD, q, k, v, w, lmk, None, cu, scale, out=out, lse=lse)
     ms = time_launches(step, args.steps, args.warmup)
+    if args.only_fwd:  # the headline forward alone (for counter profiles of that kernel)
+        print(json.dumps({"workload": args.config, "ms_per_step": ms, "steps": args.steps}))
+        return
 
     # selection + quantisation (the rest of the inference hot path), reported alongside
     from dsalt.kernels.landmark_tokens_ker import hybrid_scores_per_head
