@@ -398,6 +398,34 @@ def measure_front_end(wl, w, cu, sel) -> dict:
     }
 
 
+def measure_host_launch(device: torch.device, calls: int = 4000) -> dict:
+    """Host cost of one forward launch through the C ABI (argument block prebuilt, as the
+    module's launcher reuses it): wall time of `calls` back-to-back launches of a forward
+    so small (64 tokens, 16 heads) that the GPU finishes each before the host issues the
+    next, so the wall time is the host's. The same for the HIP runtime alone (an empty
+    torch fill launch) for reference."""
+    from dsalt import _hip
+    g = torch.Generator(device="cpu").manual_seed(0)
+    T, H, D = 64, 16, 64
+    q, k, v = (torch.randn(T, H, D, generator=g).to(device, torch.bfloat16) for _ in range(3))
+    w = torch.full((T,), 16.0, device=device)
+    cu = torch.tensor([0, T], dtype=torch.int32, device=device)
+    lmk = torch.full((H, 1, 8), -1, dtype=torch.int64, device=device)
+    f = _hip.FwdLauncher(_hip.MODE_HARD, q, k, v, w, lmk, None, cu, 0.125)
+    buf = torch.empty(1, device=device)
+    res = {}
+    for name, fn in (("dsalt_fwd_us", f), ("torch_fill_us", lambda: buf.fill_(1.0))):
+        for _ in range(200):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        torch.cuda.synchronize()
+        res[name] = (time.perf_counter() - t0) / calls * 1e6
+    return res
+
+
 def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
     """The c2 inference forward as DSALTAttention runs it by default, in bf16 (module cast to
     bf16, _collect_last_P off, packed with cu_seqlens and its host copy): the whole
@@ -750,6 +778,7 @@ def main():
         "selector_front_end": front,
         "rope": measure_rope(wl, cu, ms),
         "module_path_c2": measure_module_path(wl),
+        "host_launch": measure_host_launch(dev),
     }
     if not args.no_extras and args.config == "c2":
         res["c4"] = measure_c4(dev)
