@@ -430,10 +430,11 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
     """The c2 inference forward as DSALTAttention runs it by default, in bf16 (module cast to
     bf16, _collect_last_P off, packed with cu_seqlens and its host copy): the whole
     module call, and each of its stages eager, launch costs included: q/k/v projections,
-    RoPE of k (q is rotated inside the attention kernel), the window gate, the landmark
-    scores (HIP score kernel on x and the module's value projection; the torch route's
-    cost beside it, not in the sum), the top-k selection with the
-    window quantisation fused in, the HARD attention forward rotating q on load, out_proj."""
+    RoPE of k (q is rotated inside the attention kernel), the window gate's GEMV, the
+    landmark scores (HIP score kernel on x and the module's value projection; the torch
+    route's cost beside it, not in the sum), the top-k selection with the windows formed
+    from the gate logits and quantised in the same launch, the HARD attention forward
+    rotating q on load, out_proj."""
     import copy
     from dsalt import _hip
     from dsalt.kernels._sparse import sparse_attention
@@ -453,7 +454,7 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
         v = mod.v_proj(x).view(T, H, D)
         kr = rotate_packed(k, cos, sin, cu)
         w = mod._window_sizes(x, floor=True)
-        wc = mod._window_continuous(x)
+        gl = mod.win_gate(x).squeeze(-1)
         alpha = mod._alpha().detach().float()
         sc, _, _ = selection_scores(x, mod.v_proj.weight, alpha, H, D, v=v, hip_scores=True)
         sc = sc.float()
@@ -462,16 +463,17 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
     stages = {
         "qkv_proj": lambda: (mod.q_proj(x), mod.k_proj(x), mod.v_proj(x)),
         "rope_k": lambda: rotate_packed(k, cos, sin, cu),
-        "window_gate": lambda: mod._window_continuous(x),
+        "window_gate_gemv": lambda: mod.win_gate(x),
         "landmark_scores": lambda: selection_scores(x, mod.v_proj.weight, alpha, H, D, v=v, hip_scores=True),
         "landmark_scores_torch_route": lambda: selection_scores(x, mod.v_proj.weight, alpha, H, D, v=v),
-        "select_topk_and_quantize": lambda: _hip.select_landmarks_quantize(sc, wc, cu, kl, max_seqlen=L),
+        "select_topk_and_windows": lambda: _hip.select_landmarks_quantize(sc, None, cu, kl, max_seqlen=L,
+                                                                          gate=(gl, mod.n_min, mod.n_max)),
         "attention_fwd_rotating_q": lambda: sparse_attention(_hip.MODE_HARD, q, kr, v, lmk, None, w, cu,
                                                              rope=(cos, sin)),
         "out_proj": lambda: mod._apply_out_proj(out.reshape(T, H * D)),
     }
     res = {"workload": "c2 DSALTAttention(1024, 16, 32, 512, 64) inference forward, bf16, packed 4 x 2048, "
-                       "default routes (HIP scores on x and v, k RoPE pass, windows quantised in the selection, "
+                       "default routes (HIP scores on x and v, k RoPE pass, windows from the gate logits in the selection, "
                        "q rotated in the attention kernel)"}
     with torch.no_grad():
         res["module_forward_us"] = time_launches(lambda: mod(x, cu_seqlens=cu, cu_list=cu_list), steps,

@@ -185,8 +185,16 @@ int dsalt_select_check(const dsalt_select_args *a) {
     if (a->n_heads < 1) return fail(DSALT_ERR_INVALID, "n_heads must be >= 1");
     if (a->k_lmk < 0 || a->k_lmk > DSALT_MAX_K_LMK)
         return fail(DSALT_ERR_UNSUPPORTED, "k_lmk must be in [0, %d] (got %d)", DSALT_MAX_K_LMK, a->k_lmk);
-    if (!a->scores || !a->w || !a->cu_seqlens || (!a->lmk_pos && a->k_lmk > 0))
-        return fail(DSALT_ERR_INVALID, "scores, w, cu_seqlens and lmk_pos must be non-NULL");
+    if (!a->scores || (!a->w && !a->w_logit) || !a->cu_seqlens || (!a->lmk_pos && a->k_lmk > 0))
+        return fail(DSALT_ERR_INVALID, "scores, w (or w_logit), cu_seqlens and lmk_pos must be non-NULL");
+    if (a->w_logit) {
+        if (!a->w_out) return fail(DSALT_ERR_INVALID, "w_logit needs w_out (the quantised windows are returned there)");
+        if (a->w_logit_dtype != DSALT_DTYPE_BF16 && a->w_logit_dtype != DSALT_DTYPE_F16)
+            return fail(DSALT_ERR_UNSUPPORTED, "w_logit_dtype must be DSALT_DTYPE_BF16 or _F16 (got %d)",
+                        a->w_logit_dtype);
+        if (!(a->n_min == a->n_min) || !(a->n_max == a->n_max))
+            return fail(DSALT_ERR_INVALID, "n_min and n_max must not be NaN");
+    }
     if ((int64_t)a->num_seqs * a->n_heads > (int64_t)INT32_MAX)
         return fail(DSALT_ERR_UNSUPPORTED, "too many (head, sequence) pairs");
     if (a->max_seqlen < 0) return fail(DSALT_ERR_INVALID, "max_seqlen must be >= 0 (0: unknown)");

@@ -74,6 +74,10 @@ struct SelParams {
     const int32_t *cu;
     int64_t *out;
     float *w_out;  // non-null: w holds w~; q(w~) is written here and used for the covered test
+    const void *w_logit;  // non-null: w~ is formed from these window-gate logits instead of read
+    int64_t w_logit_st;
+    int w_logit_dt;
+    float n_min, span;    // w~ = n_min + sigmoid(logit) * span
     int num_seqs, n_heads, k;
     // chunked selection of long sequences (null ws_key: one workgroup per (head, sequence))
     uint32_t *ws_key;  // [H][n_chunk_ub][chunk_slots(k)] candidate keys, 0 in unused slots
@@ -131,6 +135,27 @@ __device__ __forceinline__ void block_excl_scan2(int a, int b, int lane, int wav
 
 // max(1, floor(w)), NaN kept: DSALTAttention._window_sizes(floor=True)
 __device__ __forceinline__ float quantize_window(float x) { return (x != x) ? x : fmaxf(floorf(x), 1.f); }
+
+// The module's continuous window of token `tok` from its 16-bit gate logit, in torch's
+// operation order and roundings: sigmoid(x) = 1 / (1 + exp(-x)) in fp32 (expf, IEEE
+// division), rounded to the logit's dtype; times span, rounded; plus n_min, rounded
+// (dsalt_attention.py:270-276 of the reference: n_min + sigmoid(win_gate(x)) * (n_max - n_min)).
+template <typename R>
+__device__ __forceinline__ float gate_window(float x, float n_min, float span, R rnd) {
+    const float sg = rnd(1.f / (1.f + expf(-x)));
+    const float t = rnd(__fmul_rn(sg, span));
+    return rnd(__fadd_rn(n_min, t));
+}
+__device__ __forceinline__ float window_of(const float *w, int64_t w_st, const void *logit, int64_t l_st, int l_dt,
+                                           float n_min, float span, int64_t tok) {
+    if (!logit) return w[tok * w_st];
+    if (l_dt == DSALT_DTYPE_BF16) {
+        const float x = BF16::to_f32(static_cast<const uint16_t *>(logit)[tok * l_st]);
+        return gate_window(x, n_min, span, [](float v) { return BF16::round(v); });
+    }
+    const float x = F16::to_f32(static_cast<const uint16_t *>(logit)[tok * l_st]);
+    return gate_window(x, n_min, span, [](float v) { return F16::round(v); });
+}
 
 struct SelShared {
     uint32_t keys[kSelCache];
@@ -292,7 +317,7 @@ __device__ __forceinline__ int select_block(SelShared &sh, int n, int k_eff, int
 // (pos < trunc(w), i.e. pos + 1 <= w for the integer pos + 1; with w_out the test is on
 // q(w~) and, on the first visit by a head-0 workgroup, q(w~) is stored).
 __device__ __forceinline__ uint32_t cand_key(const SelParams &p, int head, int pos, int64_t tok, bool first) {
-    float wv = p.w[tok * p.w_st];
+    float wv = window_of(p.w, p.w_st, p.w_logit, p.w_logit_st, p.w_logit_dt, p.n_min, p.span, tok);
     const uint32_t key = order_key(p.scores[tok * p.sc_st + (int64_t)head * p.sc_sh]);
     if (p.w_out) {
         wv = quantize_window(wv);
@@ -376,10 +401,11 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
 }
 
 __global__ void quantize_kernel(const float *__restrict__ w, int64_t w_st, int64_t n, float *__restrict__ wq,
-                                int32_t *__restrict__ wi) {
+                                int32_t *__restrict__ wi, const void *logit, int64_t l_st, int l_dt, float n_min,
+                                float span) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= n) return;
-    const float x = w[idx * w_st];
+    const float x = window_of(w, w_st, logit, l_st, l_dt, n_min, span, idx);
     const float f = floorf(x);
     if (wq) wq[idx] = quantize_window(x);
     if (wi) wi[idx] = (x >= 1.f) ? (int32_t)fminf(f, 1073741824.f) : 1;
@@ -401,7 +427,8 @@ hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream) {
         if (!a.w_out || a.total_len == 0) return hipSuccess;
         const int64_t blocks = ((int64_t)a.total_len + 255) / 256;
         hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a.w, a.w_stride,
-                           (int64_t)a.total_len, a.w_out, (int32_t *)nullptr);
+                           (int64_t)a.total_len, a.w_out, (int32_t *)nullptr, a.w_logit, a.w_logit_stride,
+                           (int)a.w_logit_dtype, a.n_min, a.n_max - a.n_min);
         return hipGetLastError();
     }
     SelParams p;
@@ -413,6 +440,11 @@ hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream) {
     p.cu = a.cu_seqlens;
     p.out = a.lmk_pos;
     p.w_out = a.w_out;
+    p.w_logit = a.w_logit;
+    p.w_logit_st = a.w_logit_stride;
+    p.w_logit_dt = a.w_logit_dtype;
+    p.n_min = a.n_min;
+    p.span = a.n_max - a.n_min;
     p.num_seqs = a.num_seqs;
     p.n_heads = a.n_heads;
     p.k = a.k_lmk;
@@ -437,7 +469,7 @@ hipError_t launch_quantize(const float *w_cont, int64_t n, float *w_out, int32_t
     const int threads = 256;
     const int64_t blocks = (n + threads - 1) / threads;
     hipLaunchKernelGGL(quantize_kernel, dim3((unsigned)blocks), dim3(threads), 0, stream, w_cont, (int64_t)1, n,
-                       w_out, w_int);
+                       w_out, w_int, (const void *)nullptr, (int64_t)0, 0, 0.f, 0.f);
     return hipGetLastError();
 }
 

@@ -91,6 +91,8 @@ class SelectArgs(ctypes.Structure):
         ("workspace", c_void_p), ("workspace_bytes", c_int64),
         ("max_seqlen", c_int32),
         ("w_out", c_void_p),
+        ("w_logit", c_void_p), ("w_logit_stride", c_int64), ("w_logit_dtype", c_int32),
+        ("n_min", c_float), ("n_max", c_float),
     ]
 
 
@@ -615,12 +617,13 @@ class DenseBwdLauncher:
         _raise(self._fn(self._ref, stream_handle(self.device)), "dsalt_bwd (dense)")
 
 
-def _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen=None, w_out=None):
+def _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen=None, w_out=None, gate=None):
     """The argument block of one selection and the tensors it points into. chunked:
     pass the workspace, so that long sequences are selected chunk-wise; max_seqlen (a
     bound on the sequence lengths, None: unknown) lets the library skip the chunk stage
     when no sequence is long; w_out (fp32 [T], contiguous): w is the continuous w~ and
-    the kernel also writes the quantised windows there."""
+    the kernel also writes the quantised windows there; gate = (logits [T], n_min, n_max):
+    the windows are formed from the window gate's logits in the launch (w unused)."""
     if scores.dtype != torch.float32:
         raise DsaltError(f"scores must be float32, got {scores.dtype}")
     T, H = scores.shape
@@ -628,7 +631,15 @@ def _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen=None, w_out=None
     a = SelectArgs()
     a.total_len, a.num_seqs, a.n_heads, a.k_lmk = T, S, H, k_lmk
     a.scores, a.scores_stride_t, a.scores_stride_h = scores.data_ptr(), scores.stride(0), scores.stride(1)
-    a.w, a.w_stride = w.data_ptr(), w.stride(0)
+    if w is not None:
+        a.w, a.w_stride = w.data_ptr(), w.stride(0)
+    if gate is not None:
+        logit, n_min, n_max = gate
+        if logit.dtype not in (torch.bfloat16, torch.float16) or logit.dim() != 1 or logit.shape[0] != T:
+            raise DsaltError(f"window-gate logits must be a [T] bf16 or fp16 vector (got {logit.dtype}, "
+                             f"{tuple(logit.shape)})")
+        a.w_logit, a.w_logit_stride, a.w_logit_dtype = logit.data_ptr(), logit.stride(0), _SCORE_DTYPES[logit.dtype]
+        a.n_min, a.n_max = float(n_min), float(n_max)
     a.cu_seqlens = cu.data_ptr()
     a.lmk_pos = out.data_ptr()
     a.max_seqlen = 0 if max_seqlen is None else min(int(max_seqlen), 2**31 - 1)
@@ -644,7 +655,7 @@ def _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen=None, w_out=None
         if ws_bytes > 0:
             ws = torch.empty(ws_bytes, device=scores.device, dtype=torch.uint8)
             a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
-    return a, (scores, w, cu, out, ws, w_out)
+    return a, (scores, w, cu, out, ws, w_out, gate)
 
 
 def select_landmarks(scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Tensor,
@@ -663,17 +674,27 @@ def select_landmarks(scores: torch.Tensor, w: torch.Tensor, cu_seqlens: torch.Te
     return out
 
 
-def select_landmarks_quantize(scores: torch.Tensor, w_cont: torch.Tensor, cu_seqlens: torch.Tensor,
-                              k_lmk: int, chunked: bool = True, max_seqlen: int | None = None):
+def select_landmarks_quantize(scores: torch.Tensor, w_cont: torch.Tensor | None, cu_seqlens: torch.Tensor,
+                              k_lmk: int, chunked: bool = True, max_seqlen: int | None = None, gate=None):
     """The window quantisation and the landmark selection in one launch: returns (w [T]
     fp32 = max(1, floor(w~)), NaN kept; landmark positions [H, S, k] as select_landmarks
-    returns them for that w)."""
-    dev = require_gpu(scores, w_cont, cu_seqlens)
+    returns them for that w). ``gate = (logits [T], n_min, n_max)`` forms w~ = n_min +
+    sigmoid(logits) * (n_max - n_min) in the launch, with torch's roundings in the logits'
+    16-bit dtype (``w_cont`` is then unused and may be None)."""
+    dev = require_gpu(scores, cu_seqlens, w_cont if gate is None else gate[0])
     cu = _cu_i32(cu_seqlens)
-    w_cont = _f32_vec(w_cont)
+    T = scores.shape[0]
+    if gate is None:
+        w_cont = _f32_vec(w_cont)
+    else:
+        w_cont = None
+        logit = gate[0]
+        if logit.dim() == 2 and logit.shape[1] == 1:
+            logit = logit[:, 0]
+        gate = (logit, gate[1], gate[2])
     out = torch.empty((scores.shape[1], cu.shape[0] - 1, k_lmk), device=dev, dtype=torch.int64)
-    w_out = torch.empty(w_cont.shape[0], device=dev, dtype=torch.float32)
-    a, _keep = _select_args(scores, w_cont, cu, k_lmk, out, chunked, max_seqlen, w_out)
+    w_out = torch.empty(T, device=dev, dtype=torch.float32)
+    a, _keep = _select_args(scores, w_cont, cu, k_lmk, out, chunked, max_seqlen, w_out, gate)
     _raise(lib().dsalt_select_landmarks(ctypes.byref(a), stream_handle(dev)), "dsalt_select_landmarks")
     return w_out, out
 

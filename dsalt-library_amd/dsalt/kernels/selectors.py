@@ -133,22 +133,23 @@ def _compute_landmark_indices(
     return lmk, z_x, z_v
 
 
-def _landmarks_and_windows(x: torch.Tensor, W_V: torch.Tensor, alpha: torch.Tensor, w_cont: torch.Tensor,
+def _landmarks_and_windows(x: torch.Tensor, W_V: torch.Tensor, alpha: torch.Tensor, w_cont: torch.Tensor | None,
                            cu_seqlens: torch.Tensor, k_lmk: int, cu_list: list | None = None,
                            head_dim: int | None = None, v: torch.Tensor | None = None,
-                           hip_scores: bool = False):
+                           hip_scores: bool = False, gate=None):
     """``(w_sizes [T] fp32, lmk [H, S, k_lmk] int64)``: the window quantisation of
     ``DSALTAttention._window_sizes(floor=True)`` (dsalt_attention.py:277-284 of the
     reference) and :func:`_compute_landmark_indices` on those windows, with the
     quantisation done by the selection launch itself (``w_cont`` is the continuous
-    ``w~``). Same results as the two steps apart."""
+    ``w~``; or ``gate = (window-gate logits [T], n_min, n_max)``, from which the launch
+    also forms ``w~`` with torch's roundings). Same results as the steps apart."""
     n_heads = alpha.shape[0]
     dh = head_dim if head_dim is not None else W_V.shape[0] // n_heads
     with torch.no_grad():
         scores, _, _ = selection_scores(x, W_V, alpha, n_heads, dh, v, hip_scores)
         max_len = None if cu_list is None else max((b - a for a, b in zip(cu_list[:-1], cu_list[1:])), default=0)
-        return _hip.select_landmarks_quantize(scores.float(), w_cont.detach(), cu_seqlens, int(k_lmk),
-                                              max_seqlen=max_len)
+        return _hip.select_landmarks_quantize(scores.float(), None if w_cont is None else w_cont.detach(),
+                                              cu_seqlens, int(k_lmk), max_seqlen=max_len, gate=gate)
 
 
 def _build_landmark_kv(K: torch.Tensor, V: torch.Tensor, lmk_indices: torch.Tensor,

@@ -294,13 +294,19 @@ class DSALTAttention(nn.Module):
 
         alpha = self._alpha()
         route_v = v_sel if self._fused_selector else None
-        # the windows are quantised by the selection launch itself (same values as
-        # _window_sizes(floor=True) followed by _compute_landmark_indices)
+        # the windows are formed from the gate's logits and quantised by the selection
+        # launch itself (same values as _window_sizes(floor=True) followed by
+        # _compute_landmark_indices)
         with torch.no_grad():
+            logit = self.win_gate(x).squeeze(-1)
+            # 16-bit logits: the launch forms the windows (torch's fp32 sigmoid is not
+            # reproduced bit for bit, so fp32 logits take torch's window ops)
+            gate = (logit, self.n_min, self.n_max) if logit.dtype in (torch.bfloat16, torch.float16) else None
+            w_cont = None if gate is not None else self.n_min + torch.sigmoid(logit) * (self.n_max - self.n_min)
             w_sizes, lmk_indices = _landmarks_and_windows(
-                x.detach(), self.v_proj.weight.detach(), alpha.detach().float(), self._window_continuous(x),
+                x.detach(), self.v_proj.weight.detach(), alpha.detach().float(), w_cont,
                 cu_seqlens, self.k_lmk, cu_list, head_dim=self.head_dim,
-                v=None if route_v is None else route_v.detach(), hip_scores=self._hip_scores)
+                v=None if route_v is None else route_v.detach(), hip_scores=self._hip_scores, gate=gate)
         self._last_selection = (w_sizes, lmk_indices)
         # Hard A(i) = W(i) ∪ L(i): the score only selects (zero landmark bias).
         out = sparse_attention(_hip.MODE_HARD, q, k, v, lmk_indices, None, w_sizes, cu_seqlens,

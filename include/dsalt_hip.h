@@ -231,6 +231,15 @@ int dsalt_bwd_noalloc(const dsalt_bwd_args *args, void *stream);
  * [cu_seqlens[0], cu_seqlens[S]), and a token is covered iff o + 1 <= q(w~) - the
  * selection is that of dsalt_quantize_windows followed by this call without w_out.
  * w_out may equal w (in place).
+ * w_logit (optional, NULL allowed; needs w_out): the window gate's logits [T] (the
+ * win_gate output of DSALTAttention._window_continuous, dsalt/modules/dsalt_attention.py:
+ * 270-276) in w_logit_dtype. The windows are then computed in the launch as the module
+ * computes them, w~ = n_min + sigmoid(logit) * (n_max - n_min), with every intermediate
+ * (the sigmoid 1 / (1 + exp(-x)) in fp32, the product, the sum) rounded to w_logit_dtype
+ * as torch's 16-bit elementwise ops round them - bit for bit torch's windows for every
+ * bf16 and fp16 logit value; w is not read (may be NULL) and w_out receives q(w~) as
+ * above. fp32 logits are not taken (DSALT_ERR_UNSUPPORTED): torch's fp32 sigmoid can
+ * differ from this formula in the last bit.
  */
 typedef struct dsalt_select_args {
     int32_t total_len, num_seqs, n_heads, k_lmk;
@@ -244,6 +253,10 @@ typedef struct dsalt_select_args {
     int64_t workspace_bytes;
     int32_t max_seqlen; /* 0 (unknown) or an upper bound on the sequence lengths */
     float *w_out;       /* NULL, or [T] fp32: quantised windows (w is then w~) */
+    const void *w_logit;    /* NULL, or [T] window-gate logits (then w is not read) */
+    int64_t w_logit_stride;
+    int32_t w_logit_dtype;  /* DSALT_DTYPE_BF16 or _F16 */
+    float n_min, n_max;     /* the module's window bounds */
 } dsalt_select_args;
 
 int64_t dsalt_select_workspace_size(int32_t total_len, int32_t num_seqs, int32_t n_heads, int32_t k_lmk);

@@ -371,6 +371,35 @@ def test_select_with_quantize_bit_exact(lens, H, k):
     np.testing.assert_array_equal(out.cpu().numpy(), got.cpu().numpy())
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("n_min,n_max", [(32, 512), (64, 1024), (7, 1000)])
+def test_select_windows_from_gate_logits_bit_exact(dtype, n_min, n_max):
+    """Windows formed in the selection launch from the window gate's 16-bit logits equal
+    torch's own n_min + sigmoid(logits) * (n_max - n_min) in the logits' dtype, then
+    max(1, floor(.)), bit for bit, for every logit value (65536 bit patterns, NaN and
+    infinities included). (7, 1000): a span that bf16 cannot hold exactly. The selection
+    on those windows equals the selection on torch's windows. (fp32 logits are refused:
+    torch's fp32 sigmoid differs from 1 / (1 + exp(-x)) in the last bit for about one
+    value in 10^6.)"""
+    print(f"gate windows dtype={dtype} n_min={n_min} n_max={n_max}", flush=True)
+    dev = torch.device("cuda", 0)
+    logit = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(dtype).to(dev)
+    T = logit.numel()
+    with torch.no_grad():
+        w_torch = n_min + torch.sigmoid(logit) * (n_max - n_min)   # the module's _window_continuous
+        wq_ref = hip.quantize_windows(w_torch)
+    lens = [T // 3, T - T // 3]
+    cu = torch.tensor([0, lens[0], T], dtype=torch.int32, device=dev)
+    scores = torch.randn(T, 2, device=dev)
+    wq, lmk = hip.select_landmarks_quantize(scores, None, cu, 8, gate=(logit, n_min, n_max))
+    same = (wq == wq_ref) | (torch.isnan(wq) & torch.isnan(wq_ref))
+    assert bool(same.all()), f"{int((~same).sum())} windows differ from torch's, e.g. logit " \
+                             f"{logit[~same][:4].tolist()}: {wq[~same][:4].tolist()} vs {wq_ref[~same][:4].tolist()}"
+    assert torch.equal(lmk, hip.select_landmarks(scores, wq_ref, cu, 8))
+    with pytest.raises(hip.DsaltError):
+        hip.select_landmarks_quantize(scores, None, cu, 8, gate=(logit.float(), n_min, n_max))
+
+
 def test_quantize_bit_exact():
     rng = np.random.default_rng(1)
     w = np.concatenate([rng.random(10000).astype(np.float32) * 600 - 50,

@@ -65,6 +65,10 @@ def test_default_selection_equals_gemm_route(cfg, dtype_mode):
     w_h, lmk_h = _run_route(mod, x, cu, fused=True, hip_scores=True, autocast=ac)
     mod._fused_selector, mod._hip_scores = True, True
     assert torch.equal(w_g, w_t) and torch.equal(w_g, w_h)
+    # the windows the selection launch formed from the gate logits are torch's own
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=ac):
+        w_torch = mod._window_sizes(x, floor=True)
+    assert torch.equal(w_g, w_torch), f"{int((w_g != w_torch).sum())} windows differ from _window_sizes"
     # slots are emitted in ascending position order, so equal sets are equal rows
     for name, lmk in (("torch route on v", lmk_t), ("HIP score kernel (default)", lmk_h)):
         same = (lmk_g == lmk).all(-1)
