@@ -265,6 +265,21 @@ int dsalt_scores_check(const dsalt_scores_args *a) {
         return fail(DSALT_ERR_INVALID, "workspace too small: %lld < %lld bytes", (long long)a->workspace_bytes,
                     (long long)need);
     if (!aligned(a->workspace, 256)) return fail(DSALT_ERR_INVALID, "workspace must be 256-byte aligned");
+    if (a->k) {  // RoPE of k riding along: dsalt_rope's rules for k alone
+        if (!a->k_out || !a->rope_cos || !a->rope_sin)
+            return fail(DSALT_ERR_INVALID, "k needs k_out, rope_cos and rope_sin");
+        if (a->head_dim % 2) return fail(DSALT_ERR_INVALID, "head_dim must be even for RoPE (got %d)", a->head_dim);
+        if (a->rope_rows < 1 || a->rope_stride < a->head_dim)
+            return fail(DSALT_ERR_INVALID, "rope tables need >= 1 row of >= head_dim entries");
+        if (a->cu_seqlens && a->num_seqs < 1) return fail(DSALT_ERR_INVALID, "num_seqs must be >= 1 with cu_seqlens");
+        const int ev = a->v_dtype == DSALT_DTYPE_F32 ? 4 : 8;
+        if (!aligned(a->k, 16) || !aligned(a->k_out, 16) || a->k_stride_t % ev || a->k_stride_h % ev ||
+            a->k_out_stride_t % ev || a->k_out_stride_h % ev || (a->head_dim / 2) % ev)
+            return fail(DSALT_ERR_INVALID, "k / k_out must be 16-byte aligned with strides and head_dim / 2 multiples of %d",
+                        ev);
+        if (!aligned(a->rope_cos, 16) || !aligned(a->rope_sin, 16) || a->rope_stride % 4)
+            return fail(DSALT_ERR_INVALID, "rope tables must be 16-byte aligned with a row stride multiple of 4");
+    }
     return DSALT_OK;
 }
 

@@ -220,7 +220,8 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     // With RoPE tables, Q is rotated here exactly as dsalt_rope does it: the lane holds
     // both halves of every rotated pair (chunk s and s + KS/2 are head dims c and c + D/2),
     // cos/sin of the query's position are rounded to the element type, products and
-    // difference / sum in fp32 without contraction, one rounding of the result.
+    // difference / sum in fp32 without contraction, the fp32 result rounded to the
+    // element type.
     if (p.rope_cos) {
         const int pos = qvalid ? i : seq_len - 1;
         const bool in_table = pos < p.rope_rows;
@@ -262,6 +263,8 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
                     const float ss0 = in_table ? DT::round(s0[c]) : NAN, ss1 = in_table ? DT::round(s1[c]) : NAN;
                     lo[h2] = __fsub_rn(__fmul_rn(a, cc0), __fmul_rn(b, ss0));
                     hi[h2] = __fadd_rn(__fmul_rn(b, cc1), __fmul_rn(a, ss1));
+                    // rounded to fp32 first: no fp16 fma_mix folding of the sum and the conversion
+                    asm volatile("" : "+v"(lo[h2]), "+v"(hi[h2]));
                 }
                 oa[e] = DT::pack2(lo[0], lo[1]);
                 ob[e] = DT::pack2(hi[0], hi[1]);

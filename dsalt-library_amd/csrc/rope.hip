@@ -15,6 +15,7 @@
 // per-token tables (the module's rope_cs argument) row t is token t.
 #include "common.h"
 #include "launch.h"
+#include "rotary.h"
 
 namespace dsalt {
 namespace {
@@ -30,100 +31,11 @@ struct RopeParams {
     int T, D, S, transpose, rows;
 };
 
-template <typename DT>
-struct Elem;
-template <>
-struct Elem<BF16> {
-    static __device__ __forceinline__ float ld(const void *p, int64_t i) {
-        return __uint_as_float((uint32_t)static_cast<const uint16_t *>(p)[i] << 16);
-    }
-    static __device__ __forceinline__ float round(float x) {
-        uint32_t u = __float_as_uint(x);
-        if ((u & 0x7fffffffu) > 0x7f800000u) return x;
-        u += 0x7fffu + ((u >> 16) & 1u);
-        return __uint_as_float(u & 0xffff0000u);
-    }
-    static __device__ __forceinline__ void st(void *p, int64_t i, float x) {
-        static_cast<uint16_t *>(p)[i] = (uint16_t)(__float_as_uint(round(x)) >> 16);
-    }
-    template <int VW>
-    static __device__ __forceinline__ void ldv(const void *p, int64_t i, float *x) {
-        if constexpr (VW == 8) {
-            const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p) + i);
-            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                x[2 * e] = __uint_as_float(w[e] << 16);
-                x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < VW; ++e) x[e] = ld(p, i + e);
-        }
-    }
-    template <int VW>
-    static __device__ __forceinline__ void stv(void *p, int64_t i, const float *x) {
-        if constexpr (VW == 8) {
-            uint32_t w[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                w[e] = (__float_as_uint(round(x[2 * e])) >> 16) | (__float_as_uint(round(x[2 * e + 1])) & 0xffff0000u);
-            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(p) + i) = make_uint4(w[0], w[1], w[2], w[3]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < VW; ++e) st(p, i + e, x[e]);
-        }
-    }
-};
-template <>
-struct Elem<F16> {
-    static __device__ __forceinline__ float ld(const void *p, int64_t i) {
-        return (float)static_cast<const _Float16 *>(p)[i];
-    }
-    static __device__ __forceinline__ float round(float x) { return (float)(_Float16)x; }
-    static __device__ __forceinline__ void st(void *p, int64_t i, float x) { static_cast<_Float16 *>(p)[i] = (_Float16)x; }
-    template <int VW>
-    static __device__ __forceinline__ void ldv(const void *p, int64_t i, float *x) {
-#pragma unroll
-        for (int e = 0; e < VW; ++e) x[e] = ld(p, i + e);
-    }
-    template <int VW>
-    static __device__ __forceinline__ void stv(void *p, int64_t i, const float *x) {
-#pragma unroll
-        for (int e = 0; e < VW; ++e) st(p, i + e, x[e]);
-    }
-};
-struct F32 {};
-template <>
-struct Elem<F32> {
-    static __device__ __forceinline__ float ld(const void *p, int64_t i) { return static_cast<const float *>(p)[i]; }
-    static __device__ __forceinline__ float round(float x) { return x; }
-    static __device__ __forceinline__ void st(void *p, int64_t i, float x) { static_cast<float *>(p)[i] = x; }
-    template <int VW>
-    static __device__ __forceinline__ void ldv(const void *p, int64_t i, float *x) {
-#pragma unroll
-        for (int e = 0; e < VW; ++e) x[e] = ld(p, i + e);
-    }
-    template <int VW>
-    static __device__ __forceinline__ void stv(void *p, int64_t i, const float *x) {
-#pragma unroll
-        for (int e = 0; e < VW; ++e) st(p, i + e, x[e]);
-    }
-};
-
-template <int VW>
-__device__ __forceinline__ void ldv_f32(const float *p, float *x) {
-#pragma unroll
-    for (int e = 0; e < VW; ++e) x[e] = p[e];
-}
-
 // One thread per (token, head, VW consecutive j < D/2) of q then k: both elements of
 // each rotated pair. Reads and writes of a pair happen in the same thread, so out may
 // alias in. VW = 8 moves 16-byte (16-bit types) or 32-byte (fp32) vectors per half.
 template <typename DT, int VW>
 __global__ void __launch_bounds__(256) rope_kernel(const RopeParams p) {
-#pragma clang fp contract(off)
-    typedef Elem<DT> E;
     const int half = p.D >> 1;
     const int nj = half / VW;  // vectors per half-row
     const int64_t per_tok = (int64_t)(p.heads[0] + p.heads[1]) * nj;
@@ -135,42 +47,13 @@ __global__ void __launch_bounds__(256) rope_kernel(const RopeParams p) {
         const int which = r >= p.heads[0] * nj;  // 0: q, 1: k
         if (which) r -= p.heads[0] * nj;
         const int h = r / nj, j0 = (r - h * nj) * VW;
-        int pos = t;
-        if (p.cu) {  // offset inside the sequence: binary search over cu_seqlens
-            int lo = 0, hi = p.S;  // cu[lo] <= t < cu[hi]
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (p.cu[mid] <= t) lo = mid;
-                else hi = mid;
-            }
-            pos = t - p.cu[lo];
-        }
+        const int pos = p.cu ? seq_offset(p.cu, p.S, t) : t;
         const bool in_table = pos < p.rows;  // a row past the table: NaN outputs
         const float *cr = p.cos + (int64_t)(in_table ? pos : 0) * p.cs_st;
         const float *sr = p.sin + (int64_t)(in_table ? pos : 0) * p.cs_st;
         const int64_t ib = (int64_t)t * p.in_st[which] + (int64_t)h * p.in_sh[which];
         const int64_t ob = (int64_t)t * p.out_st[which] + (int64_t)h * p.out_sh[which];
-        float a[VW], b[VW], c0[VW], c1[VW], s0[VW], s1[VW], o0[VW], o1[VW];
-        E::template ldv<VW>(p.in[which], ib + j0, a);
-        E::template ldv<VW>(p.in[which], ib + j0 + half, b);
-        ldv_f32<VW>(cr + j0, c0);
-        ldv_f32<VW>(cr + j0 + half, c1);
-        ldv_f32<VW>(sr + j0, s0);
-        ldv_f32<VW>(sr + j0 + half, s1);
-#pragma unroll
-        for (int e = 0; e < VW; ++e) {
-            const float cc0 = in_table ? E::round(c0[e]) : NAN, cc1 = in_table ? E::round(c1[e]) : NAN;
-            const float ss0 = in_table ? E::round(s0[e]) : NAN, ss1 = in_table ? E::round(s1[e]) : NAN;
-            if (!p.transpose) {
-                o0[e] = a[e] * cc0 - b[e] * ss0;
-                o1[e] = b[e] * cc1 + a[e] * ss1;
-            } else {
-                o0[e] = a[e] * cc0 + b[e] * ss1;
-                o1[e] = b[e] * cc1 - a[e] * ss0;
-            }
-        }
-        E::template stv<VW>(p.out[which], ob + j0, o0);
-        E::template stv<VW>(p.out[which], ob + j0 + half, o1);
+        rotate_vec<DT, VW>(p.in[which], ib, p.out[which], ob, cr, sr, half, j0, in_table, p.transpose != 0);
     }
 }
 

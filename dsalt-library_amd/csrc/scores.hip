@@ -18,8 +18,12 @@
 //     rounded to fp32, the std clamped at 1e-6 with NaN kept.
 //  3. standardize_kernel: z_x, z_v and the scores, elementwise, with the reference's
 //     fp32 operation order (no FMA contraction).
+// With k given, norms_kernel also applies RoPE to the token's k row (dsalt_rope's
+// arithmetic, rotary.h): the module's k rotation rides on the pass that reads x and v
+// anyway instead of taking a launch of its own.
 #include "common.h"
 #include "launch.h"
+#include "rotary.h"
 
 namespace dsalt {
 namespace {
@@ -37,6 +41,13 @@ struct ScoreParams {
     float *stats;     // workspace: [1 + n_kv][2] (mean, std)
     int64_t x_st, v_st, v_sh, s_st, s_sh, zv_st, zv_sh;
     int T, d, n_kv, D, H, nblk, norms_f32;
+    // optional RoPE of k: null k, or k / k_out [T, n_kv, D] in v's dtype
+    const void *k;
+    void *k_out;
+    int64_t k_st, k_sh, ko_st, ko_sh, cs_st;
+    const float *cos, *sin;
+    const int32_t *cu;
+    int rows, S;
 };
 
 // Element loads and the dtype rounding of a norm, per storage type.
@@ -91,6 +102,12 @@ struct LdF32 {
     static __device__ __forceinline__ float round(float x) { return x; }
 };
 
+// Element tag (rotary.h) of each load type.
+template <typename L> struct ElemOf;
+template <> struct ElemOf<LdBF16> { typedef BF16 T; };
+template <> struct ElemOf<LdF16> { typedef F16 T; };
+template <> struct ElemOf<LdF32> { typedef F32 T; };
+
 // Sum over the `width` lanes of each aligned lane group (width a power of two <= 64);
 // every lane of the group receives it.
 __device__ __forceinline__ float group_sum(float x, int width) {
@@ -130,6 +147,21 @@ __global__ void __launch_bounds__(64 * kNormTokens) norms_kernel(const ScorePara
             if (g < p.n_kv && lane % G == 0) {
                 p.vn[(int64_t)t * p.n_kv + g] = vn;
                 s_n[j][1 + g] = vn;
+            }
+        }
+        if (p.k) {
+            // RoPE of the token's k row: lane r takes pair vector r (16 bytes of each half)
+            constexpr int VW = EV;
+            const int half = p.D >> 1, nj = half / VW;
+            const int pos = p.cu ? seq_offset(p.cu, p.S, t) : t;
+            const bool in_table = pos < p.rows;
+            const float *cr = p.cos + (int64_t)(in_table ? pos : 0) * p.cs_st;
+            const float *sr = p.sin + (int64_t)(in_table ? pos : 0) * p.cs_st;
+            for (int r = lane; r < p.n_kv * nj; r += 64) {
+                const int h = r / nj, j0 = (r - h * nj) * VW;
+                rotate_vec<typename ElemOf<LV>::T, VW>(p.k, (int64_t)t * p.k_st + (int64_t)h * p.k_sh, p.k_out,
+                                                       (int64_t)t * p.ko_st + (int64_t)h * p.ko_sh, cr, sr, half, j0,
+                                                       in_table, false);
             }
         }
     }
@@ -257,6 +289,18 @@ hipError_t launch_scores(const dsalt_scores_args &a, hipStream_t stream) {
     p.s_sh = a.scores_stride_h;
     p.zv_st = a.z_v_stride_t;
     p.zv_sh = a.z_v_stride_h;
+    p.k = a.k;
+    p.k_out = a.k_out;
+    p.k_st = a.k_stride_t;
+    p.k_sh = a.k_stride_h;
+    p.ko_st = a.k_out_stride_t;
+    p.ko_sh = a.k_out_stride_h;
+    p.cos = a.rope_cos;
+    p.sin = a.rope_sin;
+    p.cs_st = a.rope_stride;
+    p.cu = a.cu_seqlens;
+    p.rows = a.rope_rows;
+    p.S = a.num_seqs;
     launch_norms(a.x_dtype, a.v_dtype, p, stream);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -107,6 +107,11 @@ class ScoresArgs(ctypes.Structure):
         ("z_x", c_void_p),
         ("z_v", c_void_p), ("z_v_stride_t", c_int64), ("z_v_stride_h", c_int64),
         ("workspace", c_void_p), ("workspace_bytes", c_int64),
+        ("k", c_void_p), ("k_stride_t", c_int64), ("k_stride_h", c_int64),
+        ("k_out", c_void_p), ("k_out_stride_t", c_int64), ("k_out_stride_h", c_int64),
+        ("rope_cos", c_void_p), ("rope_sin", c_void_p), ("rope_stride", c_int64),
+        ("rope_rows", c_int32), ("num_seqs", c_int32),
+        ("cu_seqlens", c_void_p),
     ]
 
 
@@ -764,12 +769,14 @@ def scores_supported(x: torch.Tensor, v: torch.Tensor) -> bool:
 
 
 def hybrid_scores(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int,
-                  norms_f32: bool | None = None):
+                  norms_f32: bool | None = None, rope_k=None):
     """``(scores [T, H], z_x [T], z_v [T, H])`` fp32 of the hybrid landmark score from the
     hidden states x [T, d] and their value projection v = x W_V^T [T, n_kv, D]
     (pre-RoPE), without the GEMM; no gradient (the selection is detached).
     ``norms_f32`` (default: whether autocast is on) keeps the norms of 16-bit inputs in
-    fp32 instead of rounding them to the input dtype."""
+    fp32 instead of rounding them to the input dtype. ``rope_k = (k, cos, sin,
+    cu_seqlens)`` also rotates k [T, n_kv, D] (v's dtype) in the same pass, exactly as
+    ``rope`` rotates k alone, and returns the rotated k as a fourth value."""
     if norms_f32 is None:
         norms_f32 = autocast_norms()
     dev = require_gpu(x, v, alpha)
@@ -789,7 +796,27 @@ def hybrid_scores(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads
     z_v = torch.empty((T, n_heads), device=dev, dtype=torch.float32)
     ws = torch.empty((scores_workspace_size(T, v.shape[1]),), device=dev, dtype=torch.uint8)
     a = scores_args(x, v, alpha, n_heads, scores, z_x, z_v, ws, norms_f32)
+    keep = None
+    if rope_k is not None:
+        k, cos, sin, cu = rope_k
+        if k.dtype != v.dtype or k.shape != v.shape:
+            raise DsaltError(f"k must match v's shape and dtype (got {tuple(k.shape)} {k.dtype}, "
+                             f"{tuple(v.shape)} {v.dtype})")
+        k = k if k.stride(2) == 1 else k.contiguous()
+        k_out = torch.empty_like(k)
+        cos = cos.to(torch.float32).contiguous()
+        sin = sin.to(torch.float32).contiguous()
+        cu = _cu_i32(cu) if cu is not None else None
+        a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
+        a.k_out, a.k_out_stride_t, a.k_out_stride_h = k_out.data_ptr(), k_out.stride(0), k_out.stride(1)
+        a.rope_cos, a.rope_sin, a.rope_stride, a.rope_rows = cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0]
+        a.cu_seqlens = _ptr(cu)
+        a.num_seqs = cu.shape[0] - 1 if cu is not None else 1
+        keep = (k, cos, sin, cu)
     _raise(lib().dsalt_hybrid_scores(ctypes.byref(a), stream_handle(dev)), "dsalt_hybrid_scores")
+    del keep
+    if rope_k is not None:
+        return scores, z_x, z_v, k_out
     return scores, z_x, z_v
 
 

@@ -70,6 +70,7 @@ class DSALTAttention(nn.Module):
 
     _fused_selector = True
     _hip_scores = True
+    _fuse_rope_k = True  # inference: k rotated by the score launch (when that route is taken)
 
     def __init__(
         self,
@@ -273,8 +274,13 @@ class DSALTAttention(nn.Module):
         # inference without autograd only k is rotated here: the attention kernel rotates
         # q as it loads it (the same arithmetic), so q is never written back rotated.
         fuse_q = not self.training and rope_cs is None and not torch.is_grad_enabled()
+        # ... and k is rotated by the launch that computes the selector norms from x and v,
+        # when the selection takes that route (the HIP score kernels)
+        fuse_k = (fuse_q and self._fuse_rope_k and self._hip_scores and self._fused_selector and v_sel is not None
+                  and k.shape == v_sel.shape and _hip.scores_supported(x, v_sel))
         if fuse_q:
-            k = rotate_packed(k, self.rope_cos, self.rope_sin, cu_seqlens)
+            if not fuse_k:
+                k = rotate_packed(k, self.rope_cos, self.rope_sin, cu_seqlens)
         elif rope_cs is None:
             q, k = apply_rotary_emb_packed(q, k, self.rope_cos, self.rope_sin, cu_seqlens)
         else:
@@ -303,10 +309,20 @@ class DSALTAttention(nn.Module):
             # reproduced bit for bit, so fp32 logits take torch's window ops)
             gate = (logit, self.n_min, self.n_max) if logit.dtype in (torch.bfloat16, torch.float16) else None
             w_cont = None if gate is not None else self.n_min + torch.sigmoid(logit) * (self.n_max - self.n_min)
-            w_sizes, lmk_indices = _landmarks_and_windows(
-                x.detach(), self.v_proj.weight.detach(), alpha.detach().float(), w_cont,
-                cu_seqlens, self.k_lmk, cu_list, head_dim=self.head_dim,
-                v=None if route_v is None else route_v.detach(), hip_scores=self._hip_scores, gate=gate)
+        if fuse_k:
+            with torch.no_grad():
+                scores, _, _, k = _hip.hybrid_scores(x.detach(), v_sel.detach(), alpha.detach().float(), self.n_heads,
+                                                     rope_k=(k, self.rope_cos, self.rope_sin, cu_seqlens))
+                max_len = None if cu_list is None else max((b - a for a, b in zip(cu_list[:-1], cu_list[1:])),
+                                                           default=0)
+                w_sizes, lmk_indices = _hip.select_landmarks_quantize(scores, w_cont, cu_seqlens, self.k_lmk,
+                                                                      max_seqlen=max_len, gate=gate)
+        else:
+            with torch.no_grad():
+                w_sizes, lmk_indices = _landmarks_and_windows(
+                    x.detach(), self.v_proj.weight.detach(), alpha.detach().float(), w_cont,
+                    cu_seqlens, self.k_lmk, cu_list, head_dim=self.head_dim,
+                    v=None if route_v is None else route_v.detach(), hip_scores=self._hip_scores, gate=gate)
         self._last_selection = (w_sizes, lmk_indices)
         # Hard A(i) = W(i) ∪ L(i): the score only selects (zero landmark bias).
         out = sparse_attention(_hip.MODE_HARD, q, k, v, lmk_indices, None, w_sizes, cu_seqlens,

@@ -294,6 +294,18 @@ typedef struct dsalt_scores_args {
     int64_t z_v_stride_t, z_v_stride_h;
     void *workspace; /* >= dsalt_scores_workspace_size(...) bytes, 256-byte aligned */
     int64_t workspace_bytes;
+    /* Optional: the RoPE of k in the same pass (what dsalt_rope does for k alone, same
+     * arithmetic and table rules): k [T, n_kv_heads, head_dim] in v_dtype, rotated into
+     * k_out (may alias k); the rows of cos/sin are positions inside the sequence given by
+     * cu_seqlens (NULL: token t reads row t). k = NULL: no rotation. */
+    const void *k;
+    int64_t k_stride_t, k_stride_h;
+    void *k_out;
+    int64_t k_out_stride_t, k_out_stride_h;
+    const float *rope_cos, *rope_sin;
+    int64_t rope_stride;
+    int32_t rope_rows, num_seqs;
+    const int32_t *cu_seqlens;
 } dsalt_scores_args;
 
 int64_t dsalt_scores_workspace_size(int32_t total_len, int32_t n_kv_heads);

@@ -127,3 +127,31 @@ def test_rope_k_only_matches_pair():
     q2, k2 = _hip.rope(q, k, cos, sin, cu)
     assert torch.equal(rotate_packed(k, cos, sin, cu), k2)
     assert torch.equal(_hip.rope(q, None, cos, sin, cu)[0], q2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("n_kv,D", [(16, 64), (2, 128), (4, 64)])
+def test_scores_pass_rotates_k_like_rope(dtype, n_kv, D):
+    """The score pass with k given (the module's inference route) rotates k exactly as
+    dsalt_rope rotates it alone - packed positions from cu_seqlens, the module's tables
+    and arbitrary ones, a sequence longer than the table (NaN rows) - and its scores are
+    those of the pass without k."""
+    from dsalt.kernels.window_utils import build_rope_cache
+    print(f"scores pass rotates k {dtype} n_kv={n_kv} D={D}", flush=True)
+    g = torch.Generator().manual_seed(n_kv * D)
+    lens = [300, 70, 230]
+    T, d, H = sum(lens), 256, 16
+    cu = torch.tensor([0, 300, 370, 600], dtype=torch.int32, device=DEV)
+    x = torch.randn(T, d, generator=g).to(DEV, dtype)
+    v = torch.randn(T, n_kv, D, generator=g).to(DEV, dtype)
+    k = torch.randn(T, n_kv, D, generator=g).to(DEV, dtype)
+    alpha = torch.rand(H, generator=g).to(DEV)
+    for cos, sin in (build_rope_cache(512, D, DEV),
+                     (torch.randn(280, D, generator=g).to(DEV), torch.randn(280, D, generator=g).to(DEV))):
+        s0, zx0, zv0 = _hip.hybrid_scores(x, v, alpha, H)
+        s1, zx1, zv1, k1 = _hip.hybrid_scores(x, v, alpha, H, rope_k=(k, cos, sin, cu))
+        _, k_ref = _hip.rope(None, k, cos, sin, cu)
+        torch.cuda.synchronize()
+        assert torch.equal(s0, s1) and torch.equal(zx0, zx1) and torch.equal(zv0, zv1)
+        assert torch.equal(torch.nan_to_num(k1.float(), 7.0), torch.nan_to_num(k_ref.float(), 7.0))
+        assert bool(torch.isnan(k1).any()) == (cos.shape[0] < max(lens))
