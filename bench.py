@@ -377,11 +377,22 @@ def measure_front_end(wl, w, cu, sel) -> dict:
         s, _, _ = hybrid_scores_from_v(xb, vb, alpha, H)
         _hip.select_landmarks(s, w, cu, k, max_seqlen=wl["L"])
 
+    # the scores formed inside the selection launch (norms pass + selection: 2 launches
+    # instead of 4); w is already quantised, so its quantisation is the identity
+    hyb = _hip.SelectHybridLauncher(xb, vb, alpha, H, w, cu, k, max_seqlen=wl["L"], norms_f32=False)
     with torch.no_grad():
+        hip_scores_path()
+        hyb()
+        torch.cuda.synchronize()
+        if not (torch.equal(hyb.out, sel_f.out) and torch.equal(hyb.w_out, w.float())):
+            raise RuntimeError("dsalt_select_hybrid differs from dsalt_hybrid_scores + dsalt_select_landmarks")
         gemm_ms = time_launches(gemm_path, 50, 10)
         v_route_ms = time_launches(v_route_path, 50, 10)
         hip_ms = time_launches(hip_scores_path, 50, 10)
+        hyb_ms = time_launches(hyb, 50, 10)
         scores_graph_ms = time_graph(scores)
+        two_step_graph_ms = time_graph(hip_scores_path)
+        hyb_graph_ms = time_graph(hyb)
     d = xb.shape[1]
     bytes_scores = 2 * T * d + 2 * T * H * D + 4 * T * (1 + H) * 2 + 4 * T * H * 3
     return {
@@ -389,12 +400,17 @@ def measure_front_end(wl, w, cu, sel) -> dict:
         "gemm_path_us": gemm_ms * 1e3,
         "torch_v_route_us": v_route_ms * 1e3,
         "hip_scores_path_us": hip_ms * 1e3,
+        "select_hybrid_path_us": hyb_ms * 1e3,
         "hip_scores_graph_us": scores_graph_ms * 1e3,
+        "hip_scores_then_select_graph_us": two_step_graph_ms * 1e3,
+        "select_hybrid_graph_us": hyb_graph_ms * 1e3,
         "hip_scores_GB/s": bytes_scores / (scores_graph_ms * 1e-3) / 1e9,
         "gemm_flops_saved": 2.0 * T * d * H * D,
         "note": "gemm_path: the reference's x @ W_V^T route; torch_v_route: the same torch norms on the "
                 "module's own value projection (no second GEMM, DSALTAttention._hip_scores = False); "
-                "hip_scores_path: the module's default, the one-pass HIP score kernel on x and v",
+                "hip_scores_path: dsalt_hybrid_scores on x and v then dsalt_select_landmarks (4 launches); "
+                "select_hybrid_path: the module's default, dsalt_select_hybrid (norms pass, then the selection "
+                "forming each score itself: 2 launches, same sets, checked)",
     }
 
 
@@ -430,11 +446,12 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
     """The c2 inference forward as DSALTAttention runs it by default, in bf16 (module cast to
     bf16, _collect_last_P off, packed with cu_seqlens and its host copy): the whole
     module call, and each of its stages eager, launch costs included: q/k/v projections,
-    RoPE of k (q is rotated inside the attention kernel), the window gate's GEMV, the
-    landmark scores (HIP score kernel on x and the module's value projection; the torch
-    route's cost beside it, not in the sum), the top-k selection with the windows formed
-    from the gate logits and quantised in the same launch, the HARD attention forward
-    rotating q on load, out_proj."""
+    the window gate's GEMV, the selection (dsalt_select_hybrid: the norms pass over x and
+    the module's value projection, which also applies RoPE to k, then the selection
+    launch forming the scores, the windows from the gate logits and the top-k), the HARD
+    attention forward rotating q on load, out_proj. Beside them, not in the sum: the
+    routes the default replaces (k RoPE alone, the score kernels then the selection on
+    their scores, the torch score route)."""
     import copy
     from dsalt import _hip
     from dsalt.kernels._sparse import sparse_attention
@@ -462,8 +479,11 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
         out = sparse_attention(_hip.MODE_HARD, q, kr, v, lmk, None, w, cu, rope=(cos, sin))
     stages = {
         "qkv_proj": lambda: (mod.q_proj(x), mod.k_proj(x), mod.v_proj(x)),
-        "rope_k": lambda: rotate_packed(k, cos, sin, cu),
         "window_gate_gemv": lambda: mod.win_gate(x),
+        "norms_rope_k_and_select": lambda: _hip.select_hybrid(x, v, alpha, H, None, cu, kl, max_seqlen=L,
+                                                              gate=(gl, mod.n_min, mod.n_max),
+                                                              rope_k=(k, cos, sin, cu)),
+        "rope_k_alone": lambda: rotate_packed(k, cos, sin, cu),
         "landmark_scores": lambda: selection_scores(x, mod.v_proj.weight, alpha, H, D, v=v, hip_scores=True),
         "landmark_scores_torch_route": lambda: selection_scores(x, mod.v_proj.weight, alpha, H, D, v=v),
         "select_topk_and_windows": lambda: _hip.select_landmarks_quantize(sc, None, cu, kl, max_seqlen=L,
@@ -473,15 +493,16 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
         "out_proj": lambda: mod._apply_out_proj(out.reshape(T, H * D)),
     }
     res = {"workload": "c2 DSALTAttention(1024, 16, 32, 512, 64) inference forward, bf16, packed 4 x 2048, "
-                       "default routes (HIP scores on x and v, k RoPE pass, windows from the gate logits in the selection, "
-                       "q rotated in the attention kernel)"}
+                       "default routes (norms pass over x and v rotating k, selection forming scores and windows "
+                       "from the gate logits, q rotated in the attention kernel)"}
     with torch.no_grad():
         res["module_forward_us"] = time_launches(lambda: mod(x, cu_seqlens=cu, cu_list=cu_list), steps,
                                                  warmup) * 1e3
         for name, fn in stages.items():
             res[name + "_us"] = time_launches(fn, steps, warmup) * 1e3
-    res["stages_sum_us"] = sum(v for kk, v in res.items()
-                               if kk.endswith("_us") and kk not in ("module_forward_us", "landmark_scores_torch_route_us"))
+    beside = ("module_forward_us", "rope_k_alone_us", "landmark_scores_us", "landmark_scores_torch_route_us",
+              "select_topk_and_windows_us")
+    res["stages_sum_us"] = sum(v for kk, v in res.items() if kk.endswith("_us") and kk not in beside)
     return res
 
 

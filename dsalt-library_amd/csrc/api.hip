@@ -178,14 +178,17 @@ int dsalt_fwd(const dsalt_fwd_args *a, void *stream) {
     return DSALT_OK;
 }
 
-int dsalt_select_check(const dsalt_select_args *a) {
+namespace {
+
+// hybrid: the scores are formed in the launch (dsalt_select_hybrid), so none are read
+int check_select(const dsalt_select_args *a, bool hybrid) {
     if (!a) return fail(DSALT_ERR_INVALID, "args is NULL");
     if (a->total_len < 0) return fail(DSALT_ERR_INVALID, "total_len must be >= 0");
     if (a->num_seqs < 1) return fail(DSALT_ERR_INVALID, "num_seqs must be >= 1");
     if (a->n_heads < 1) return fail(DSALT_ERR_INVALID, "n_heads must be >= 1");
     if (a->k_lmk < 0 || a->k_lmk > DSALT_MAX_K_LMK)
         return fail(DSALT_ERR_UNSUPPORTED, "k_lmk must be in [0, %d] (got %d)", DSALT_MAX_K_LMK, a->k_lmk);
-    if (!a->scores || (!a->w && !a->w_logit) || !a->cu_seqlens || (!a->lmk_pos && a->k_lmk > 0))
+    if ((!a->scores && !hybrid) || (!a->w && !a->w_logit) || !a->cu_seqlens || (!a->lmk_pos && a->k_lmk > 0))
         return fail(DSALT_ERR_INVALID, "scores, w (or w_logit), cu_seqlens and lmk_pos must be non-NULL");
     if (a->w_logit) {
         if (!a->w_out) return fail(DSALT_ERR_INVALID, "w_logit needs w_out (the quantised windows are returned there)");
@@ -207,6 +210,10 @@ int dsalt_select_check(const dsalt_select_args *a) {
     return DSALT_OK;
 }
 
+}  // namespace
+
+int dsalt_select_check(const dsalt_select_args *a) { return check_select(a, false); }
+
 int64_t dsalt_select_workspace_size(int32_t total_len, int32_t num_seqs, int32_t n_heads, int32_t k_lmk) {
     if (total_len < 0 || num_seqs < 1 || n_heads < 1 || k_lmk < 0 || k_lmk > DSALT_MAX_K_LMK) return -1;
     return dsalt::select_workspace_bytes(total_len, num_seqs, n_heads, k_lmk);
@@ -226,7 +233,10 @@ int64_t dsalt_scores_workspace_size(int32_t total_len, int32_t n_kv_heads) {
     return dsalt::scores_workspace_bytes(total_len, n_kv_heads);
 }
 
-int dsalt_scores_check(const dsalt_scores_args *a) {
+namespace {
+
+// hybrid: dsalt_select_hybrid, which writes no scores (scores, z_x and z_v must be NULL)
+int check_scores(const dsalt_scores_args *a, bool hybrid) {
     if (!a) return fail(DSALT_ERR_INVALID, "args is NULL");
     if (a->total_len < 0) return fail(DSALT_ERR_INVALID, "total_len must be >= 0");
     if (a->d_model < 1 || a->head_dim < 1 || a->n_heads < 1 || a->n_kv_heads < 1)
@@ -247,8 +257,11 @@ int dsalt_scores_check(const dsalt_scores_args *a) {
     const int g = a->head_dim / ev;
     if (g > 64 || (g & (g - 1)))
         return fail(DSALT_ERR_UNSUPPORTED, "head_dim / %d must be a power of two <= 64 (head_dim %d)", ev, a->head_dim);
+    if (hybrid && (a->scores || a->z_x || a->z_v))
+        return fail(DSALT_ERR_INVALID, "dsalt_select_hybrid writes no scores: scores, z_x and z_v must be NULL");
+    if (hybrid && !a->alpha) return fail(DSALT_ERR_INVALID, "alpha must be non-NULL");
     if (a->total_len == 0) return DSALT_OK;
-    if (!a->x || !a->v || !a->alpha || !a->scores)
+    if (!a->x || !a->v || !a->alpha || (!a->scores && !hybrid))
         return fail(DSALT_ERR_INVALID, "x, v, alpha and scores must be non-NULL");
     if (!aligned(a->x, 16) || !aligned(a->v, 16)) return fail(DSALT_ERR_INVALID, "x and v must be 16-byte aligned");
     if (a->x_stride_t < a->d_model || a->x_stride_t % ex)
@@ -283,12 +296,31 @@ int dsalt_scores_check(const dsalt_scores_args *a) {
     return DSALT_OK;
 }
 
+}  // namespace
+
+int dsalt_scores_check(const dsalt_scores_args *a) { return check_scores(a, false); }
+
 int dsalt_hybrid_scores(const dsalt_scores_args *a, void *stream) {
     int rc = dsalt_scores_check(a);
     if (rc) return rc;
     hipError_t e = dsalt::launch_scores(*a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess)
         return fail(DSALT_ERR_LAUNCH, "dsalt_hybrid_scores launch failed: %s", hipGetErrorString(e));
+    return DSALT_OK;
+}
+
+int dsalt_select_hybrid(const dsalt_scores_args *sa, const dsalt_select_args *a, void *stream) {
+    int rc = check_scores(sa, true);
+    if (rc) return rc;
+    if ((rc = check_select(a, true))) return rc;
+    if (sa->total_len != a->total_len || sa->n_heads != a->n_heads)
+        return fail(DSALT_ERR_INVALID, "score and selection arguments disagree: total_len %d / %d, n_heads %d / %d",
+                    sa->total_len, a->total_len, sa->n_heads, a->n_heads);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    dsalt::HybridSrc src;
+    hipError_t e = dsalt::launch_norms_for_select(*sa, src, st);
+    if (e == hipSuccess) e = dsalt::launch_select(*a, st, &src);
+    if (e != hipSuccess) return fail(DSALT_ERR_LAUNCH, "dsalt_select_hybrid launch failed: %s", hipGetErrorString(e));
     return DSALT_OK;
 }
 

@@ -30,7 +30,16 @@ constexpr int fwd_ring(int) { return 2; }  // K / V ring depth
 
 hipError_t launch_fwd(const dsalt_fwd_args &a, hipStream_t stream);
 hipError_t launch_bwd(const dsalt_bwd_args &a, hipStream_t stream);
-hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream);
+// Selection scores formed on the fly from the norms pass's outputs (scores workspace):
+// per-token norms, per-block fp64 partial sums, and the per-head balance alpha.
+struct HybridSrc {
+    const float *xn, *vn;
+    const double *part;
+    const float *alpha;
+    int nblk, n_kv, n_heads, total_len;
+};
+hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream, const HybridSrc *hy = nullptr);
+hipError_t launch_norms_for_select(const dsalt_scores_args &a, HybridSrc &src, hipStream_t stream);
 int64_t select_workspace_bytes(int total_len, int num_seqs, int n_heads, int k);
 hipError_t launch_rope(const dsalt_rope_args &a, hipStream_t stream);
 hipError_t launch_scores(const dsalt_scores_args &a, hipStream_t stream);

@@ -23,6 +23,7 @@
 // anyway instead of taking a launch of its own.
 #include "common.h"
 #include "launch.h"
+#include "hybrid.h"
 #include "rotary.h"
 
 namespace dsalt {
@@ -184,24 +185,11 @@ __global__ void __launch_bounds__(64 * kNormTokens) norms_kernel(const ScorePara
 __global__ void __launch_bounds__(1024) stats_kernel(const ScoreParams p) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int q = wave; q <= p.n_kv; q += 16) {  // wave-uniform
-        double s = 0.0, s2 = 0.0;
-        for (int b = lane; b < p.nblk; b += 64) {
-            const double *o = p.part + ((int64_t)b * (1 + p.n_kv) + q) * 2;
-            s += o[0];
-            s2 += o[1];
-        }
-        for (int off = 1; off < 64; off <<= 1) {
-            s += __shfl_xor(s, off);
-            s2 += __shfl_xor(s2, off);
-        }
+        float mean, sd;
+        hybrid_stat(p.part, p.nblk, 1 + p.n_kv, q, (double)p.T, lane, mean, sd);
         if (lane == 0) {
-            const double n = (double)p.T;
-            const double mean = s / n;
-            // unbiased variance; T = 1 gives 0/0 = NaN, as torch.std does
-            const double var = fmax(s2 - s * mean, 0.0) / (n - 1.0);
-            const float sd = (float)sqrt(var);
-            p.stats[2 * q] = (float)mean;
-            p.stats[2 * q + 1] = (sd != sd) ? sd : fmaxf(sd, 1e-6f);  // clamp(min=1e-6) keeps NaN
+            p.stats[2 * q] = mean;
+            p.stats[2 * q + 1] = sd;
         }
     }
 }
@@ -219,12 +207,9 @@ __global__ void __launch_bounds__(256) standardize_kernel(const ScoreParams p) {
     const int nt = min(kStdTokens, p.T - t0);
     for (int e = threadIdx.x; e < nt * p.H; e += blockDim.x) {
         const int t = t0 + e / p.H, h = e % p.H, g = h / rep;
-        const float zx = (p.xn[t] - s_mean[0]) / s_std[0];
-        const float zv = (p.vn[(int64_t)t * p.n_kv + g] - s_mean[1 + g]) / s_std[1 + g];
-        const float a = p.alpha[h];
-        const float t1 = a * zv;
-        const float t2 = (1.0f - a) * zx;
-        p.scores[(int64_t)t * p.s_st + (int64_t)h * p.s_sh] = t1 + t2;
+        const float zx = hybrid_z(p.xn[t], s_mean[0], s_std[0]);
+        const float zv = hybrid_z(p.vn[(int64_t)t * p.n_kv + g], s_mean[1 + g], s_std[1 + g]);
+        p.scores[(int64_t)t * p.s_st + (int64_t)h * p.s_sh] = hybrid_mix(zx, zv, p.alpha[h]);
         if (p.z_v) p.z_v[(int64_t)t * p.zv_st + (int64_t)h * p.zv_sh] = zv;
         if (p.z_x && h == 0) p.z_x[t] = zx;
     }
@@ -258,8 +243,9 @@ int64_t scores_workspace_bytes(int total_len, int n_kv) {
 
 int scores_max_kv() { return kMaxKvScores; }
 
-hipError_t launch_scores(const dsalt_scores_args &a, hipStream_t stream) {
-    if (a.total_len == 0) return hipSuccess;
+namespace {
+
+ScoreParams make_params(const dsalt_scores_args &a) {
     ScoreParams p;
     p.x = a.x;
     p.v = a.v;
@@ -301,12 +287,35 @@ hipError_t launch_scores(const dsalt_scores_args &a, hipStream_t stream) {
     p.cu = a.cu_seqlens;
     p.rows = a.rope_rows;
     p.S = a.num_seqs;
+    return p;
+}
+
+}  // namespace
+
+hipError_t launch_scores(const dsalt_scores_args &a, hipStream_t stream) {
+    if (a.total_len == 0) return hipSuccess;
+    const ScoreParams p = make_params(a);
     launch_norms(a.x_dtype, a.v_dtype, p, stream);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(stats_kernel, dim3(1), dim3(1024), 0, stream, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(standardize_kernel, dim3((p.T + kStdTokens - 1) / kStdTokens), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_norms_for_select(const dsalt_scores_args &a, HybridSrc &src, hipStream_t stream) {
+    const ScoreParams p = make_params(a);
+    src.xn = p.xn;
+    src.vn = p.vn;
+    src.part = p.part;
+    src.alpha = a.alpha;
+    src.nblk = p.nblk;
+    src.n_kv = p.n_kv;
+    src.n_heads = p.H;
+    src.total_len = p.T;
+    if (a.total_len == 0) return hipSuccess;
+    launch_norms(a.x_dtype, a.v_dtype, p, stream);
     return hipGetLastError();
 }
 

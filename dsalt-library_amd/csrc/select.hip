@@ -35,12 +35,19 @@
 // from the candidates, concatenated in chunk order (hence in position order).
 // Fully deterministic; integer-exact with respect to the fp32 scores.
 //
+// Scores formed in the launch (dsalt_select_hybrid): instead of reading fp32 scores, each
+// workgroup takes the norms pass's per-token norms and per-block partial sums, derives
+// the mean / std of x's norms and of its head group's value norms with the score kernels'
+// own arithmetic (hybrid.h: one wave each, the same fixed order), and forms every score
+// as standardize_kernel would - the same bits, without the stats and standardise launches.
+//
 // Window quantisation can ride along (w_out): the windows are then the continuous w~,
 // a token is covered when its offset o satisfies o + 1 <= q(w~) with q(w) = max(1,
 // floor(w)) (NaN kept, so never covered) - exactly the test on the quantised windows,
 // since q is idempotent - and the workgroups of head 0 write q(w~) for the tokens they
 // read, which saves the quantisation its own launch.
 #include "common.h"
+#include "hybrid.h"
 #include "launch.h"
 
 namespace dsalt {
@@ -78,6 +85,11 @@ struct SelParams {
     int64_t w_logit_st;
     int w_logit_dt;
     float n_min, span;    // w~ = n_min + sigmoid(logit) * span
+    // hybrid scores (non-null xn): norms [T] / [T, n_kv], fp64 partials [nblk][1 + n_kv][2]
+    const float *xn, *vn;
+    const double *part;
+    const float *alpha;
+    int nblk, n_kv, rep, total_len;
     int num_seqs, n_heads, k;
     // chunked selection of long sequences (null ws_key: one workgroup per (head, sequence))
     uint32_t *ws_key;  // [H][n_chunk_ub][chunk_slots(k)] candidate keys, 0 in unused slots
@@ -163,7 +175,36 @@ struct SelShared {
     int w[kSelWaves][2];
     int cnt[kSelWaves];  // written once: its readers need no trailing barrier
     uint32_t mm[kSelWaves][2];
+    float st[4];  // hybrid scores: mean / std of x's norms, then of the head group's value norms
 };
+
+// The standardisation of one workgroup's head (hybrid scores): waves 0 and 1 derive the
+// two (mean, std) pairs, shared through LDS. Every thread of the workgroup calls it.
+struct HybridStats {
+    float mx, sx, mv, sv, alpha;
+    int g;
+};
+__device__ __forceinline__ HybridStats hybrid_stats(const SelParams &p, SelShared &sh, int head) {
+    HybridStats h{};
+    if (!p.xn) return h;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    h.g = head / p.rep;
+    if (wave < 2) {
+        float m, sd;
+        hybrid_stat(p.part, p.nblk, 1 + p.n_kv, wave == 0 ? 0 : 1 + h.g, (double)p.total_len, lane, m, sd);
+        if (lane == 0) {
+            sh.st[2 * wave] = m;
+            sh.st[2 * wave + 1] = sd;
+        }
+    }
+    __syncthreads();
+    h.mx = sh.st[0];
+    h.sx = sh.st[1];
+    h.mv = sh.st[2];
+    h.sv = sh.st[3];
+    h.alpha = p.alpha[head];
+    return h;
+}
 
 // The top k_eff of items 0 .. n-1 of key key_of(j, first) (0: not a candidate; `first`
 // is true on the first of possibly several calls per item), emitted as emit(slot, j, key)
@@ -316,9 +357,16 @@ __device__ __forceinline__ int select_block(SelShared &sh, int n, int k_eff, int
 // Key of token `tok` at offset `pos` of its sequence for `head`: 0 when covered
 // (pos < trunc(w), i.e. pos + 1 <= w for the integer pos + 1; with w_out the test is on
 // q(w~) and, on the first visit by a head-0 workgroup, q(w~) is stored).
-__device__ __forceinline__ uint32_t cand_key(const SelParams &p, int head, int pos, int64_t tok, bool first) {
+__device__ __forceinline__ uint32_t cand_key(const SelParams &p, const HybridStats &hs, int head, int pos,
+                                             int64_t tok, bool first) {
     float wv = window_of(p.w, p.w_st, p.w_logit, p.w_logit_st, p.w_logit_dt, p.n_min, p.span, tok);
-    const uint32_t key = order_key(p.scores[tok * p.sc_st + (int64_t)head * p.sc_sh]);
+    float sc;
+    if (p.xn)
+        sc = hybrid_mix(hybrid_z(p.xn[tok], hs.mx, hs.sx), hybrid_z(p.vn[tok * p.n_kv + hs.g], hs.mv, hs.sv),
+                        hs.alpha);
+    else
+        sc = p.scores[tok * p.sc_st + (int64_t)head * p.sc_sh];
+    const uint32_t key = order_key(sc);
     if (p.w_out) {
         wv = quantize_window(wv);
         if (first && head == 0) p.w_out[tok] = wv;
@@ -344,10 +392,11 @@ __global__ void __launch_bounds__(kSelThreads) select_chunk_kernel(const SelPara
     const int cs = chunk_slots(p.k);
     uint32_t *ck = p.ws_key + ((int64_t)head * p.n_chunk_ub + cid) * cs;
     int32_t *cp = p.ws_pos + ((int64_t)head * p.n_chunk_ub + cid) * cs;
+    const HybridStats hs = hybrid_stats(p, sh, head);
     auto key_of = [&](int j, bool first) -> uint32_t {
         const int pos = c0 + j;
         const int64_t tok = (int64_t)start + pos;
-        return cand_key(p, head, pos, tok, first);
+        return cand_key(p, hs, head, pos, tok, first);
     };
     auto emit = [&](int slot, int j, uint32_t key) {
         if (slot < cs) {
@@ -389,8 +438,9 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
         };
         total = select_block(sh, n, k_eff, k_eff, false, key_of, emit);
     } else {
+        const HybridStats hs = hybrid_stats(p, sh, head);
         auto key_of = [&](int j, bool first) -> uint32_t {
-            return cand_key(p, head, j, (int64_t)start + j, first);
+            return cand_key(p, hs, head, j, (int64_t)start + j, first);
         };
         auto emit = [&](int slot, int j, uint32_t) {
             if (slot < p.k) out[slot] = j;
@@ -422,7 +472,7 @@ int64_t select_workspace_bytes(int total_len, int num_seqs, int n_heads, int k) 
     return 2 * al(n * chunk_slots(k) * 4);
 }
 
-hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream) {
+hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream, const HybridSrc *hy) {
     if (a.k_lmk == 0) {  // nothing to select; the windows are still quantised
         if (!a.w_out || a.total_len == 0) return hipSuccess;
         const int64_t blocks = ((int64_t)a.total_len + 255) / 256;
@@ -445,6 +495,14 @@ hipError_t launch_select(const dsalt_select_args &a, hipStream_t stream) {
     p.w_logit_dt = a.w_logit_dtype;
     p.n_min = a.n_min;
     p.span = a.n_max - a.n_min;
+    p.xn = hy ? hy->xn : nullptr;
+    p.vn = hy ? hy->vn : nullptr;
+    p.part = hy ? hy->part : nullptr;
+    p.alpha = hy ? hy->alpha : nullptr;
+    p.nblk = hy ? hy->nblk : 0;
+    p.n_kv = hy ? hy->n_kv : 1;
+    p.rep = hy ? hy->n_heads / hy->n_kv : 1;
+    p.total_len = a.total_len;
     p.num_seqs = a.num_seqs;
     p.n_heads = a.n_heads;
     p.k = a.k_lmk;

@@ -134,9 +134,9 @@ EXPORTED_SYMBOLS = (
     "dsalt_abi_version", "dsalt_last_error", "dsalt_fwd_args_size", "dsalt_bwd_args_size",
     "dsalt_select_args_size", "dsalt_hybrid_scores", "dsalt_scores_check", "dsalt_scores_workspace_size",
     "dsalt_scores_args_size", "dsalt_rope", "dsalt_rope_check", "dsalt_rope_args_size",
-    "dsalt_bwd_noalloc", "dsalt_select_workspace_size",
+    "dsalt_bwd_noalloc", "dsalt_select_workspace_size", "dsalt_select_hybrid",
 )
-NOALLOC_SCRATCH_BYTES = 128 << 20  # DSALT_NOALLOC_SCRATCH_BYTES
+NOALLOC_SCRATCH_BYTES = 76 << 20  # DSALT_NOALLOC_SCRATCH_BYTES
 SELECT_SPLIT_MIN = 4096  # longer sequences can be selected chunk-wise
 
 _lib = None
@@ -162,6 +162,7 @@ def lib() -> ctypes.CDLL:
         ("dsalt_select_check", [ctypes.POINTER(SelectArgs)]),
         ("dsalt_hybrid_scores", [ctypes.POINTER(ScoresArgs), c_void_p]),
         ("dsalt_scores_check", [ctypes.POINTER(ScoresArgs)]),
+        ("dsalt_select_hybrid", [ctypes.POINTER(ScoresArgs), ctypes.POINTER(SelectArgs), c_void_p]),
         ("dsalt_rope", [ctypes.POINTER(RopeArgs), c_void_p]),
         ("dsalt_rope_check", [ctypes.POINTER(RopeArgs)]),
         ("dsalt_quantize_windows", [c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
@@ -622,20 +623,22 @@ class DenseBwdLauncher:
         _raise(self._fn(self._ref, stream_handle(self.device)), "dsalt_bwd (dense)")
 
 
-def _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen=None, w_out=None, gate=None):
-    """The argument block of one selection and the tensors it points into. chunked:
+def _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen=None, w_out=None, gate=None, shape=None):
+    """The argument block of one selection and the tensors it points into. scores: fp32
+    [T, H], or None with shape = (T, H) (dsalt_select_hybrid forms the scores). chunked:
     pass the workspace, so that long sequences are selected chunk-wise; max_seqlen (a
     bound on the sequence lengths, None: unknown) lets the library skip the chunk stage
     when no sequence is long; w_out (fp32 [T], contiguous): w is the continuous w~ and
     the kernel also writes the quantised windows there; gate = (logits [T], n_min, n_max):
     the windows are formed from the window gate's logits in the launch (w unused)."""
-    if scores.dtype != torch.float32:
+    if scores is not None and scores.dtype != torch.float32:
         raise DsaltError(f"scores must be float32, got {scores.dtype}")
-    T, H = scores.shape
+    T, H = scores.shape if scores is not None else shape
     S = cu.shape[0] - 1
     a = SelectArgs()
     a.total_len, a.num_seqs, a.n_heads, a.k_lmk = T, S, H, k_lmk
-    a.scores, a.scores_stride_t, a.scores_stride_h = scores.data_ptr(), scores.stride(0), scores.stride(1)
+    if scores is not None:
+        a.scores, a.scores_stride_t, a.scores_stride_h = scores.data_ptr(), scores.stride(0), scores.stride(1)
     if w is not None:
         a.w, a.w_stride = w.data_ptr(), w.stride(0)
     if gate is not None:
@@ -658,7 +661,7 @@ def _select_args(scores, w, cu, k_lmk, out, chunked, max_seqlen=None, w_out=None
         if ws_bytes < 0:
             raise DsaltError(f"dsalt_select_workspace_size: invalid shape (T={T}, S={S}, H={H}, k={k_lmk})")
         if ws_bytes > 0:
-            ws = torch.empty(ws_bytes, device=scores.device, dtype=torch.uint8)
+            ws = torch.empty(ws_bytes, device=out.device, dtype=torch.uint8)
             a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
     return a, (scores, w, cu, out, ws, w_out, gate)
 
@@ -688,20 +691,66 @@ def select_landmarks_quantize(scores: torch.Tensor, w_cont: torch.Tensor | None,
     16-bit dtype (``w_cont`` is then unused and may be None)."""
     dev = require_gpu(scores, cu_seqlens, w_cont if gate is None else gate[0])
     cu = _cu_i32(cu_seqlens)
-    T = scores.shape[0]
-    if gate is None:
-        w_cont = _f32_vec(w_cont)
-    else:
-        w_cont = None
-        logit = gate[0]
-        if logit.dim() == 2 and logit.shape[1] == 1:
-            logit = logit[:, 0]
-        gate = (logit, gate[1], gate[2])
+    w_cont, gate = _window_source(w_cont, gate)
     out = torch.empty((scores.shape[1], cu.shape[0] - 1, k_lmk), device=dev, dtype=torch.int64)
-    w_out = torch.empty(T, device=dev, dtype=torch.float32)
+    w_out = torch.empty(scores.shape[0], device=dev, dtype=torch.float32)
     a, _keep = _select_args(scores, w_cont, cu, k_lmk, out, chunked, max_seqlen, w_out, gate)
     _raise(lib().dsalt_select_landmarks(ctypes.byref(a), stream_handle(dev)), "dsalt_select_landmarks")
     return w_out, out
+
+
+def _window_source(w_cont, gate):
+    """(w_cont as an fp32 vector or None, gate with [T] logits or None)."""
+    if gate is None:
+        return _f32_vec(w_cont), None
+    logit = gate[0]
+    if logit.dim() == 2 and logit.shape[1] == 1:
+        logit = logit[:, 0]
+    return None, (logit, gate[1], gate[2])
+
+
+def select_hybrid(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int,
+                  w_cont: torch.Tensor | None, cu_seqlens: torch.Tensor, k_lmk: int, chunked: bool = True,
+                  max_seqlen: int | None = None, gate=None, norms_f32: bool | None = None, rope_k=None):
+    """hybrid_scores followed by select_landmarks_quantize in two launches
+    (dsalt_select_hybrid): the selection forms each score from the norms pass's outputs
+    instead of reading a [T, H] score tensor, with the same bits. Arguments as for those
+    two calls; returns (w [T] fp32 quantised windows, landmark positions [H, S, k],
+    rotated k or None when rope_k is None)."""
+    f = SelectHybridLauncher(x, v, alpha, n_heads, w_cont, cu_seqlens, k_lmk, chunked, max_seqlen, gate, norms_f32,
+                             rope_k)
+    f()
+    return f.w_out, f.out, f.k_out
+
+
+class SelectHybridLauncher:
+    """select_hybrid with its argument blocks, outputs and workspaces built once: each call
+    launches the norms pass and the selection on the current stream (for timing loops
+    and graph capture); `w_out`, `out` and `k_out` (None without rope_k) hold the result."""
+
+    def __init__(self, x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int,
+                 w_cont: torch.Tensor | None, cu_seqlens: torch.Tensor, k_lmk: int, chunked: bool = True,
+                 max_seqlen: int | None = None, gate=None, norms_f32: bool | None = None, rope_k=None):
+        if norms_f32 is None:
+            norms_f32 = autocast_norms()
+        self.device = require_gpu(x, v, alpha, cu_seqlens, w_cont if gate is None else gate[0])
+        x, v, alpha = _score_operands(x, v, alpha, n_heads)
+        cu = _cu_i32(cu_seqlens)
+        w_cont, gate = _window_source(w_cont, gate)
+        T = x.shape[0]
+        ws = torch.empty((scores_workspace_size(T, v.shape[1]),), device=self.device, dtype=torch.uint8)
+        self._sa = scores_args(x, v, alpha, n_heads, None, None, None, ws, norms_f32)
+        self.k_out, keep_k = _rope_k_args(self._sa, v, rope_k)
+        self.out = torch.empty((n_heads, cu.shape[0] - 1, k_lmk), device=self.device, dtype=torch.int64)
+        self.w_out = torch.empty(T, device=self.device, dtype=torch.float32)
+        self._a, keep_s = _select_args(None, w_cont, cu, k_lmk, self.out, chunked, max_seqlen, self.w_out, gate,
+                                       shape=(T, n_heads))
+        self._keep = (x, v, alpha, cu, ws, keep_k, keep_s)
+        self._refs = (ctypes.byref(self._sa), ctypes.byref(self._a))
+        self._fn = lib().dsalt_select_hybrid
+
+    def __call__(self) -> None:
+        _raise(self._fn(*self._refs, stream_handle(self.device)), "dsalt_select_hybrid")
 
 
 _SCORE_DTYPES = {torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16, torch.float32: DTYPE_F32}
@@ -717,7 +766,7 @@ def autocast_norms() -> bool:
 
 
 def scores_args(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int,
-                scores: torch.Tensor, z_x: torch.Tensor | None, z_v: torch.Tensor | None,
+                scores: torch.Tensor | None, z_x: torch.Tensor | None, z_v: torch.Tensor | None,
                 ws: torch.Tensor | None, norms_f32: bool = False) -> ScoresArgs:
     """Argument block of dsalt_hybrid_scores (x [T, d], v [T, n_kv, D], alpha [H] fp32)."""
     T, d = x.shape
@@ -730,7 +779,8 @@ def scores_args(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: 
     a.x, a.x_stride_t = x.data_ptr(), x.stride(0)
     a.v, a.v_stride_t, a.v_stride_h = v.data_ptr(), v.stride(0), v.stride(1)
     a.alpha = alpha.data_ptr()
-    a.scores, a.scores_stride_t, a.scores_stride_h = scores.data_ptr(), scores.stride(0), scores.stride(1)
+    if scores is not None:
+        a.scores, a.scores_stride_t, a.scores_stride_h = scores.data_ptr(), scores.stride(0), scores.stride(1)
     a.z_x = _ptr(z_x)
     if z_v is not None:
         a.z_v, a.z_v_stride_t, a.z_v_stride_h = z_v.data_ptr(), z_v.stride(0), z_v.stride(1)
@@ -780,6 +830,23 @@ def hybrid_scores(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads
     if norms_f32 is None:
         norms_f32 = autocast_norms()
     dev = require_gpu(x, v, alpha)
+    x, v, alpha = _score_operands(x, v, alpha, n_heads)
+    T = x.shape[0]
+    scores = torch.empty((T, n_heads), device=dev, dtype=torch.float32)
+    z_x = torch.empty((T,), device=dev, dtype=torch.float32)
+    z_v = torch.empty((T, n_heads), device=dev, dtype=torch.float32)
+    ws = torch.empty((scores_workspace_size(T, v.shape[1]),), device=dev, dtype=torch.uint8)
+    a = scores_args(x, v, alpha, n_heads, scores, z_x, z_v, ws, norms_f32)
+    k_out, keep = _rope_k_args(a, v, rope_k)
+    _raise(lib().dsalt_hybrid_scores(ctypes.byref(a), stream_handle(dev)), "dsalt_hybrid_scores")
+    del keep
+    if rope_k is not None:
+        return scores, z_x, z_v, k_out
+    return scores, z_x, z_v
+
+
+def _score_operands(x, v, alpha, n_heads):
+    """x [T, d] and v [T, n_kv, D] with unit inner strides, alpha as a contiguous fp32 [H]."""
     if x.dim() != 2 or v.dim() != 3 or v.shape[0] != x.shape[0]:
         raise DsaltError(f"x must be [T, d] and v [T, n_kv, D] with the same T (got {tuple(x.shape)}, "
                          f"{tuple(v.shape)})")
@@ -790,34 +857,30 @@ def hybrid_scores(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads
     alpha = alpha.detach().to(torch.float32).contiguous()
     if alpha.shape != (n_heads,):
         raise DsaltError(f"alpha must be [{n_heads}] (got {tuple(alpha.shape)})")
-    T = x.shape[0]
-    scores = torch.empty((T, n_heads), device=dev, dtype=torch.float32)
-    z_x = torch.empty((T,), device=dev, dtype=torch.float32)
-    z_v = torch.empty((T, n_heads), device=dev, dtype=torch.float32)
-    ws = torch.empty((scores_workspace_size(T, v.shape[1]),), device=dev, dtype=torch.uint8)
-    a = scores_args(x, v, alpha, n_heads, scores, z_x, z_v, ws, norms_f32)
-    keep = None
-    if rope_k is not None:
-        k, cos, sin, cu = rope_k
-        if k.dtype != v.dtype or k.shape != v.shape:
-            raise DsaltError(f"k must match v's shape and dtype (got {tuple(k.shape)} {k.dtype}, "
-                             f"{tuple(v.shape)} {v.dtype})")
-        k = k if k.stride(2) == 1 else k.contiguous()
-        k_out = torch.empty_like(k)
-        cos = cos.to(torch.float32).contiguous()
-        sin = sin.to(torch.float32).contiguous()
-        cu = _cu_i32(cu) if cu is not None else None
-        a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
-        a.k_out, a.k_out_stride_t, a.k_out_stride_h = k_out.data_ptr(), k_out.stride(0), k_out.stride(1)
-        a.rope_cos, a.rope_sin, a.rope_stride, a.rope_rows = cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0]
-        a.cu_seqlens = _ptr(cu)
-        a.num_seqs = cu.shape[0] - 1 if cu is not None else 1
-        keep = (k, cos, sin, cu)
-    _raise(lib().dsalt_hybrid_scores(ctypes.byref(a), stream_handle(dev)), "dsalt_hybrid_scores")
-    del keep
-    if rope_k is not None:
-        return scores, z_x, z_v, k_out
-    return scores, z_x, z_v
+    return x, v, alpha
+
+
+def _rope_k_args(a: ScoresArgs, v: torch.Tensor, rope_k):
+    """Fill the k-rotation fields of a score argument block from rope_k = (k, cos, sin,
+    cu_seqlens) or leave them empty (rope_k None); returns (k_out or None, tensors to keep
+    alive until the launch)."""
+    if rope_k is None:
+        return None, None
+    k, cos, sin, cu = rope_k
+    if k.dtype != v.dtype or k.shape != v.shape:
+        raise DsaltError(f"k must match v's shape and dtype (got {tuple(k.shape)} {k.dtype}, "
+                         f"{tuple(v.shape)} {v.dtype})")
+    k = k if k.stride(2) == 1 else k.contiguous()
+    k_out = torch.empty_like(k)
+    cos = cos.to(torch.float32).contiguous()
+    sin = sin.to(torch.float32).contiguous()
+    cu = _cu_i32(cu) if cu is not None else None
+    a.k, a.k_stride_t, a.k_stride_h = k.data_ptr(), k.stride(0), k.stride(1)
+    a.k_out, a.k_out_stride_t, a.k_out_stride_h = k_out.data_ptr(), k_out.stride(0), k_out.stride(1)
+    a.rope_cos, a.rope_sin, a.rope_stride, a.rope_rows = cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.shape[0]
+    a.cu_seqlens = _ptr(cu)
+    a.num_seqs = cu.shape[0] - 1 if cu is not None else 1
+    return k_out, (k, cos, sin, cu)
 
 
 def rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,

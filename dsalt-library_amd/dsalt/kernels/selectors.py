@@ -142,12 +142,19 @@ def _landmarks_and_windows(x: torch.Tensor, W_V: torch.Tensor, alpha: torch.Tens
     reference) and :func:`_compute_landmark_indices` on those windows, with the
     quantisation done by the selection launch itself (``w_cont`` is the continuous
     ``w~``; or ``gate = (window-gate logits [T], n_min, n_max)``, from which the launch
-    also forms ``w~`` with torch's roundings). Same results as the steps apart."""
+    also forms ``w~`` with torch's roundings). Same results as the steps apart. On the HIP
+    score route the scores are formed inside the selection launch (``_hip.select_hybrid``:
+    the norms pass, then the selection; no [T, H] score tensor), with the same bits."""
     n_heads = alpha.shape[0]
     dh = head_dim if head_dim is not None else W_V.shape[0] // n_heads
     with torch.no_grad():
-        scores, _, _ = selection_scores(x, W_V, alpha, n_heads, dh, v, hip_scores)
         max_len = None if cu_list is None else max((b - a for a, b in zip(cu_list[:-1], cu_list[1:])), default=0)
+        if v is not None and hip_scores and _hip.scores_supported(x, v):
+            w_sizes, lmk, _ = _hip.select_hybrid(x.detach(), v.detach(), alpha, n_heads,
+                                                 None if w_cont is None else w_cont.detach(), cu_seqlens, int(k_lmk),
+                                                 max_seqlen=max_len, gate=gate)
+            return w_sizes, lmk
+        scores, _, _ = selection_scores(x, W_V, alpha, n_heads, dh, v, hip_scores)
         return _hip.select_landmarks_quantize(scores.float(), None if w_cont is None else w_cont.detach(),
                                               cu_seqlens, int(k_lmk), max_seqlen=max_len, gate=gate)
 

@@ -310,13 +310,14 @@ class DSALTAttention(nn.Module):
             gate = (logit, self.n_min, self.n_max) if logit.dtype in (torch.bfloat16, torch.float16) else None
             w_cont = None if gate is not None else self.n_min + torch.sigmoid(logit) * (self.n_max - self.n_min)
         if fuse_k:
+            # two launches: the norms pass (which also rotates k), then the selection,
+            # which forms the scores, the windows and the top-k
             with torch.no_grad():
-                scores, _, _, k = _hip.hybrid_scores(x.detach(), v_sel.detach(), alpha.detach().float(), self.n_heads,
-                                                     rope_k=(k, self.rope_cos, self.rope_sin, cu_seqlens))
                 max_len = None if cu_list is None else max((b - a for a, b in zip(cu_list[:-1], cu_list[1:])),
                                                            default=0)
-                w_sizes, lmk_indices = _hip.select_landmarks_quantize(scores, w_cont, cu_seqlens, self.k_lmk,
-                                                                      max_seqlen=max_len, gate=gate)
+                w_sizes, lmk_indices, k = _hip.select_hybrid(
+                    x.detach(), v_sel.detach(), alpha.detach().float(), self.n_heads, w_cont, cu_seqlens, self.k_lmk,
+                    max_seqlen=max_len, gate=gate, rope_k=(k, self.rope_cos, self.rope_sin, cu_seqlens))
         else:
             with torch.no_grad():
                 w_sizes, lmk_indices = _landmarks_and_windows(

@@ -313,6 +313,23 @@ int dsalt_hybrid_scores(const dsalt_scores_args *args, void *stream);
 int dsalt_scores_check(const dsalt_scores_args *args);
 
 /*
+ * Landmark selection with the hybrid scores formed inside the selection launch.
+ * Replaces, in one call, hybrid_scores_per_head (dsalt/kernels/landmark_tokens_ker.py:
+ * 19-61) and the selection of _compute_landmark_indices (dsalt/kernels/selectors.py:
+ * 105-134) as DSALTAttention._packed chains them (dsalt/modules/dsalt_attention.py:
+ * 655-666): the result is that of dsalt_hybrid_scores followed by dsalt_select_landmarks
+ * on its scores, bit for bit (the same norms, the same fp64 statistics in the same order,
+ * the same fp32 standardisation), with two launches instead of four: the norms pass
+ * (which also rotates k when scores->k is set), then the selection, whose workgroups
+ * derive the statistics of their head and score each candidate as they read it.
+ * scores: as for dsalt_hybrid_scores, except that scores, z_x and z_v must be NULL (no
+ * scores are written) and alpha is always required; its workspace must stay untouched
+ * until the selection has run (same stream). select: as for dsalt_select_landmarks,
+ * except that select->scores is not read (may be NULL). total_len and n_heads must agree.
+ */
+int dsalt_select_hybrid(const dsalt_scores_args *scores, const dsalt_select_args *select, void *stream);
+
+/*
  * Rotary position embedding of q and k (half-split convention) in one pass.
  * Replaces apply_rotary_emb (dsalt/kernels/window_utils.py:73-88) as called by
  * DSALTAttention._packed (dsalt/modules/dsalt_attention.py:570-585): cos/sin rows are

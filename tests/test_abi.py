@@ -300,3 +300,32 @@ def test_dense_mode_checks():
                        (dict(num_seqs=1, k_lmk=0, lmk_pos=None, scale=-0.125), "scale > 0")):
         rc, msg = _check(_fake_fwd(mode=hip.MODE_DENSE, **kw))
         assert rc != 0 and needle in msg, (kw, rc, msg)
+
+
+def test_select_hybrid_rejects_before_launching():
+    """dsalt_select_hybrid validates both argument blocks and their agreement on the host
+    and returns before any launch when they are wrong."""
+    lib = hip.lib()
+    sel = hip.SelectArgs()
+    sel.total_len, sel.num_seqs, sel.n_heads, sel.k_lmk = 100, 1, 8, 16
+    sel.w, sel.cu_seqlens, sel.lmk_pos = 0x2000, 0x3000, 0x4000  # scores NULL: formed in the launch
+    fn = lib.dsalt_select_hybrid
+    assert fn(ctypes.byref(_scores_args()), ctypes.byref(sel), None) == 1
+    assert "writes no scores" in lib.dsalt_last_error().decode()
+    assert fn(ctypes.byref(_scores_args(scores=0, alpha=0)), ctypes.byref(sel), None) == 1
+    assert "alpha" in lib.dsalt_last_error().decode()
+    sel.n_heads = 4
+    assert fn(ctypes.byref(_scores_args(scores=0)), ctypes.byref(sel), None) == 1
+    assert "disagree" in lib.dsalt_last_error().decode()
+    sel.n_heads, sel.w = 8, 0
+    assert fn(ctypes.byref(_scores_args(scores=0)), ctypes.byref(sel), None) == 1
+    assert "w_logit" in lib.dsalt_last_error().decode()
+    # the plain selection still needs its scores
+    sel.w = 0x2000
+    assert lib.dsalt_select_check(ctypes.byref(sel)) == 1
+
+
+def test_noalloc_scratch_size_matches_header():
+    text = open(HEADER).read()
+    m = re.search(r"#define DSALT_NOALLOC_SCRATCH_BYTES \(\(int64_t\)(\d+) << (\d+)\)", text)
+    assert m and hip.NOALLOC_SCRATCH_BYTES == int(m.group(1)) << int(m.group(2))

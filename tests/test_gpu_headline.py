@@ -76,6 +76,41 @@ def test_default_selection_equals_gemm_route(cfg, dtype_mode):
         assert bool(same.all()), f"{name}: {int((~same).sum())} landmark sets differ from the x @ W_V.T route"
 
 
+@pytest.mark.parametrize("dtype_mode", ["fp32", "bf16", "autocast"])
+def test_c3_training_selection_equals_gemm_route(dtype_mode):
+    """Config 3's training selection (the module's _train_selectors on its eight packed
+    sequences): the default HIP score route and the torch route on v pick the landmark
+    sets of the reference's x @ W_V.T route, and all three quantise the same windows."""
+    import numpy as np
+    from dsalt.modules import DSALTAttention
+    print(f"c3 training selection routes {dtype_mode}", flush=True)
+    np.random.seed(2)
+    lens = [int(v) for v in np.random.randint(256, 2049, 8)]
+    torch.manual_seed(2)
+    mod = DSALTAttention(1024, 16, 32, 512, 64, max_seq_len=2048).to(DEV).train()
+    T = sum(lens)
+    x = torch.randn(T, 1024).to(DEV)
+    if dtype_mode == "bf16":
+        mod, x = mod.to(torch.bfloat16), x.to(torch.bfloat16)
+    cu_list = [0]
+    for L in lens:
+        cu_list.append(cu_list[-1] + L)
+    cu = torch.tensor(cu_list, dtype=torch.int32, device=DEV)
+    res = {}
+    for name, fused, hip_scores in (("gemm", False, False), ("torch_v", True, False), ("hip", True, True)):
+        mod._fused_selector, mod._hip_scores = fused, hip_scores
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16, enabled=dtype_mode == "autocast"):
+            v = mod.v_proj(x).view(T, 16, 64)  # as the module forms it (in bf16 under autocast)
+            w, lmk, _ = mod._train_selectors(x, cu, T, DEV, cu_list, v if fused else None)
+        res[name] = (mod._last_selection[0].clone(), lmk.clone())
+    mod._fused_selector, mod._hip_scores = True, True
+    for name in ("torch_v", "hip"):
+        assert torch.equal(res[name][0], res["gemm"][0])
+        same = (res[name][1] == res["gemm"][1]).all(-1)
+        print(f"  {name}: {int(same.sum())}/{same.numel()} (head, sequence) sets equal", flush=True)
+        assert bool(same.all()), f"{name}: {int((~same).sum())} landmark sets differ from the x @ W_V.T route"
+
+
 @pytest.mark.parametrize("cfg,windows", [("c2", [(0, 256), (1024, 1280), (1536, 1792)]),
                                          ("c4", [(0, 256), (8192, 8448), (15872, 16128)])])
 @pytest.mark.parametrize("mode", ["hard", "soft"])

@@ -160,3 +160,55 @@ def test_module_fused_selector(training):
     assert torch.equal(sels[2], sels[1])
     err = (outs[2] - outs[1]).abs().max().item()
     assert err < 2e-2, f"HIP-score selector output differs by {err}"
+
+
+SELECT_HYBRID_CASES = {
+    # lens, d, H, n_kv, D, dtype, k, window source, norms_f32, rotate k
+    "mha-bf16-gate": ([700, 0, 333, 1100], 512, 16, 16, 64, torch.bfloat16, 32, "gate", False, True),
+    "gqa-f16-long-chunked": ([9000, 3000, 17], 256, 8, 2, 64, torch.float16, 128, "cont", False, False),
+    "fp32-d128": ([600, 1500], 256, 8, 4, 128, torch.float32, 64, "cont", False, True),
+    "bf16-autocast-norms": ([4096, 200], 1024, 16, 16, 64, torch.bfloat16, 64, "gate", True, True),
+    "one-token-nan-std": ([1], 256, 4, 4, 64, torch.bfloat16, 8, "cont", False, False),
+    "empty-seq-k0": ([50, 0, 80], 256, 4, 2, 64, torch.bfloat16, 0, "gate", False, False),
+}
+
+
+@pytest.mark.parametrize("case", list(SELECT_HYBRID_CASES), ids=list(SELECT_HYBRID_CASES))
+def test_select_hybrid_equals_scores_then_select(case):
+    """dsalt_select_hybrid (norms pass, then the selection forming each score itself) gives
+    the windows, landmark sets and rotated k of dsalt_hybrid_scores followed by the
+    selection on its scores, bit for bit: long chunked sequences, GQA, fp32 and 16-bit
+    inputs, autocast's fp32 norms, a single token (NaN std), an empty sequence and k = 0."""
+    from dsalt.kernels.window_utils import build_rope_cache
+    lens, d, H, n_kv, D, dtype, k_lmk, src, nf32, rot = SELECT_HYBRID_CASES[case]
+    print(f"select_hybrid {case}", flush=True)
+    g = torch.Generator().manual_seed(len(case))
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=DEV)
+    T = int(cu[-1])
+    x = (torch.randn(T, d, generator=g) * (1 + torch.rand(T, 1, generator=g))).to(DEV, dtype)
+    v = torch.randn(T, n_kv, D, generator=g).to(DEV, dtype)
+    alpha = torch.rand(H, generator=g).to(DEV)
+    if src == "gate":
+        gdt = torch.float16 if dtype == torch.float16 else torch.bfloat16
+        w_cont, gate = None, ((torch.randn(T, generator=g) * 3).to(DEV, gdt), 8.0, 700.0)
+    else:
+        w_cont, gate = (torch.rand(T, generator=g) * 300 + 0.5).to(DEV), None
+    rope_k = None
+    if rot:
+        k = torch.randn(T, n_kv, D, generator=g).to(DEV, dtype)
+        cos, sin = build_rope_cache(max(lens) + 1, D, DEV)
+        rope_k = (k, cos, sin, cu)
+    for chunked in (True, False):
+        ref = _hip.hybrid_scores(x, v, alpha, H, norms_f32=nf32, rope_k=rope_k)
+        w_ref, lmk_ref = _hip.select_landmarks_quantize(ref[0], w_cont, cu, k_lmk, chunked=chunked, gate=gate)
+        w_got, lmk_got, k_got = _hip.select_hybrid(x, v, alpha, H, w_cont, cu, k_lmk, chunked=chunked, gate=gate,
+                                                   norms_f32=nf32, rope_k=rope_k)
+        torch.cuda.synchronize()
+        assert torch.equal(torch.nan_to_num(w_got, 7.0), torch.nan_to_num(w_ref, 7.0))
+        assert torch.equal(lmk_got, lmk_ref), f"chunked={chunked}: landmark sets differ"
+        if rot:
+            assert torch.equal(k_got, ref[3])
+        else:
+            assert k_got is None
+    if case == "one-token-nan-std":
+        assert bool((lmk_got == -1).all())  # a NaN score is never a landmark
