@@ -14,14 +14,28 @@ namespace dsalt {
 // Mean and unbiased std (clamped at 1e-6, NaN kept) of quantity q from the norms pass's
 // fp64 partial sums part[b][nq][2] (sum, sum of squares) over b < nblk blocks and T tokens.
 // One wave, fixed order: lane l adds blocks l, l + 64, ..., then a shuffle tree; products
-// and differences rounded separately (no FMA). The result is valid in every lane.
+// and differences rounded separately (no FMA). The result is valid in every lane. The
+// partials are loaded kStatBatch blocks per lane at a time, ahead of their adds (the
+// order of the adds is unchanged), so that the loads' latencies overlap.
+constexpr int kStatBatch = 8;
 __device__ __forceinline__ void hybrid_stat(const double *part, int nblk, int nq, int q, double T, int lane,
                                             float &mean, float &sd) {
     double s = 0.0, s2 = 0.0;
-    for (int b = lane; b < nblk; b += 64) {
-        const double *o = part + ((int64_t)b * nq + q) * 2;
-        s = __dadd_rn(s, o[0]);
-        s2 = __dadd_rn(s2, o[1]);
+    for (int b0 = lane; b0 < nblk; b0 += 64 * kStatBatch) {
+        double a[kStatBatch], a2[kStatBatch];
+#pragma unroll
+        for (int u = 0; u < kStatBatch; ++u) {
+            const int b = min(b0 + 64 * u, nblk - 1);  // past the end: a valid block, not added
+            const double *o = part + ((int64_t)b * nq + q) * 2;
+            a[u] = o[0];
+            a2[u] = o[1];
+        }
+#pragma unroll
+        for (int u = 0; u < kStatBatch; ++u)
+            if (b0 + 64 * u < nblk) {
+                s = __dadd_rn(s, a[u]);
+                s2 = __dadd_rn(s2, a2[u]);
+            }
     }
     for (int off = 1; off < 64; off <<= 1) {
         s = __dadd_rn(s, __shfl_xor(s, off));
