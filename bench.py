@@ -442,6 +442,53 @@ def measure_host_launch(device: torch.device, calls: int = 4000) -> dict:
     return res
 
 
+def measure_peaks(device: torch.device) -> dict:
+    """What the box reaches of the published peaks, for context (the roofline fractions
+    use the published 2.5 PFLOP/s and 8 TB/s): a large square bf16 GEMM through torch
+    (hipBLASLt, MFMA), a 2 GiB device copy (bytes read + written) and a 2 GiB bf16 sum
+    (bytes read)."""
+    n = 8192
+    a = torch.randn(n, n, device=device, dtype=torch.bfloat16)
+    b = torch.randn(n, n, device=device, dtype=torch.bfloat16)
+    gemm_ms = time_launches(lambda: torch.matmul(a, b), 20, 5)
+    del a, b
+    nbytes = 2 << 30
+    src = torch.empty(nbytes // 2, device=device, dtype=torch.bfloat16).normal_()
+    dst = torch.empty_like(src)
+    copy_ms = time_launches(lambda: dst.copy_(src), 20, 5)
+    sum_ms = time_launches(lambda: src.sum(dtype=torch.float32), 20, 5)
+    res = {
+        "gemm_bf16_TFLOP/s": 2.0 * n ** 3 / (gemm_ms * 1e-3) / 1e12,
+        "copy_GB/s": 2 * nbytes / (copy_ms * 1e-3) / 1e9,
+        "sum_read_GB/s": nbytes / (sum_ms * 1e-3) / 1e9,
+    }
+    # the probe kernels of libdsalt_peaks.so: MFMA alone, and a plain streaming read
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.abspath(__file__)), "dsalt-library_amd", "dsalt",
+                                   "libdsalt_peaks.so"))
+    lib.dsalt_bench_mfma.restype = ctypes.c_float
+    lib.dsalt_bench_mfma.argtypes = [ctypes.c_int, ctypes.c_int]
+    lib.dsalt_bench_read.restype = ctypes.c_float
+    lib.dsalt_bench_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int]
+    torch.cuda.synchronize()
+    blocks, iters = 256 * 8, 32768  # 8 waves per SIMD; ~20 ms per launch, so the clock has ramped
+    mfma_ms = lib.dsalt_bench_mfma(blocks, iters)
+    read_ms = lib.dsalt_bench_read(src.data_ptr(), nbytes, 256 * 16)
+    if mfma_ms <= 0 or read_ms <= 0:
+        raise RuntimeError("peak probes failed")
+    mfma_tf = blocks * 4 * iters * 4 * (32 * 32 * 16 * 2) / (mfma_ms * 1e-3) / 1e12
+    res["mfma_loop_TFLOP/s"] = mfma_tf
+    res["read_kernel_GB/s"] = nbytes / (read_ms * 1e-3) / 1e9
+    res["mfma_loop_frac_of_published"] = mfma_tf / MFMA_BF16_PEAK_TFLOPS
+    res["read_kernel_frac_of_published"] = res["read_kernel_GB/s"] / HBM_PEAK_GBS
+    res["note"] = (f"torch.matmul {n}^3 bf16 (hipBLASLt); dst.copy_(src) and src.sum() over 2 GiB; "
+                   f"mfma_loop: {blocks} x 4 waves, {iters} rounds of 4 independent 32x32x16 bf16 MFMAs; "
+                   "read_kernel: one grid-stride 16-byte read of the 2 GiB")
+    del src, dst
+    torch.cuda.empty_cache()
+    return res
+
+
 def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
     """The c2 inference forward as DSALTAttention runs it by default, in bf16 (module cast to
     bf16, _collect_last_P off, packed with cu_seqlens and its host copy): the whole
@@ -665,7 +712,7 @@ def main():
                     help="skip the config-4, dense-variant and config-5 LM measurements")
     ap.add_argument("--only-fwd", action="store_true",
                     help="time only the headline forward of --config and exit (for profiling)")
-    ap.add_argument("--only", choices=("lm", "dense", "backward", "c4"), default=None,
+    ap.add_argument("--only", choices=("lm", "dense", "backward", "c4", "peaks"), default=None,
                     help="run only that measurement and print its JSON (for profiling)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (counter calibration)")
@@ -687,7 +734,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if args.only is not None:
-        fn = {"lm": measure_lm, "dense": measure_dense, "backward": measure_backward, "c4": measure_c4}[args.only]
+        fn = {"lm": measure_lm, "dense": measure_dense, "backward": measure_backward, "c4": measure_c4,
+              "peaks": measure_peaks}[args.only]
         print(json.dumps(fn(dev)))
         return
     wl = make_workload(args.config, dev)
@@ -802,6 +850,7 @@ def main():
         "rope": measure_rope(wl, cu, ms),
         "module_path_c2": measure_module_path(wl),
         "host_launch": measure_host_launch(dev),
+        "peaks_measured": measure_peaks(dev),
     }
     if not args.no_extras and args.config == "c2":
         res["c4"] = measure_c4(dev)

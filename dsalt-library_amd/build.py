@@ -3,6 +3,8 @@
 Usage: python dsalt-library_amd/build.py [--jobs N]
 The library lands in dsalt-library_amd/dsalt/libdsalt_hip.so, next to the Python
 package that loads it. Objects are compiled in parallel into _build/ and linked once.
+bench_kernels/peaks.hip (bench.py's peak probes, not part of the DSALT ABI) becomes
+libdsalt_peaks.so beside it.
 """
 from __future__ import annotations
 
@@ -18,6 +20,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "dsalt", "libdsalt_hip.so")
+PEAKS_SRC = os.path.join(HERE, "bench_kernels", "peaks.hip")
+PEAKS_OUT = os.path.join(HERE, "dsalt", "libdsalt_peaks.so")
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32.
@@ -97,18 +101,23 @@ def compile_one(src: str) -> str:
     return obj
 
 
-def build(jobs: int | None = None) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    srcs = sources()
-    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2) // 2))
-    with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(compile_one, srcs))
-    tmp = OUT + ".tmp"
+def link(objs: list[str], out: str) -> None:
+    tmp = out + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
+
+
+def build(jobs: int | None = None) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    srcs = sources() + [PEAKS_SRC]
+    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2) // 2))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(compile_one, srcs))
+    link(objs[:-1], OUT)
+    link(objs[-1:], PEAKS_OUT)
     return OUT
 
 

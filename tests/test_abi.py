@@ -329,3 +329,13 @@ def test_noalloc_scratch_size_matches_header():
     text = open(HEADER).read()
     m = re.search(r"#define DSALT_NOALLOC_SCRATCH_BYTES \(\(int64_t\)(\d+) << (\d+)\)", text)
     assert m and hip.NOALLOC_SCRATCH_BYTES == int(m.group(1)) << int(m.group(2))
+
+
+def test_peak_probe_library_is_built_apart_from_the_abi():
+    """bench.py's peak probes live in their own library: built next to the product, not
+    exported by libdsalt_hip.so."""
+    path = os.path.join(os.path.dirname(hip.LIB_PATH), "libdsalt_peaks.so")
+    assert os.path.exists(path), "run dsalt-library_amd/build.py"
+    peaks = ctypes.CDLL(path)
+    assert hasattr(peaks, "dsalt_bench_mfma") and hasattr(peaks, "dsalt_bench_read")
+    assert not hasattr(ctypes.CDLL(hip.LIB_PATH), "dsalt_bench_mfma")
