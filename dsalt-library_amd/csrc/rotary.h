@@ -71,8 +71,18 @@ struct Elem<F16> {
     static __device__ __forceinline__ void st(void *p, int64_t i, float x) { static_cast<_Float16 *>(p)[i] = (_Float16)x; }
     template <int VW>
     static __device__ __forceinline__ void ldv(const void *p, int64_t i, float *x) {
+        if constexpr (VW == 8) {  // one 16-byte load
+            const uint4 u = *reinterpret_cast<const uint4 *>(static_cast<const _Float16 *>(p) + i);
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-        for (int e = 0; e < VW; ++e) x[e] = ld(p, i + e);
+            for (int e = 0; e < 4; ++e) {
+                x[2 * e] = F16::lo_f32(w[e]);
+                x[2 * e + 1] = F16::hi_f32(w[e]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < VW; ++e) x[e] = ld(p, i + e);
+        }
     }
     template <int VW>
     static __device__ __forceinline__ void stv(void *p, int64_t i, const float *x) {
