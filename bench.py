@@ -545,9 +545,15 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
     with torch.no_grad():
         res["module_forward_us"] = time_launches(lambda: mod(x, cu_seqlens=cu, cu_list=cu_list), steps,
                                                  warmup) * 1e3
+        # the same call captured whole in a HIP graph and replayed: GPU time without the
+        # host's per-call work
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            mod(x, cu_seqlens=cu, cu_list=cu_list)
+        res["module_forward_graph_us"] = time_launches(graph.replay, steps, warmup) * 1e3
         for name, fn in stages.items():
             res[name + "_us"] = time_launches(fn, steps, warmup) * 1e3
-    beside = ("module_forward_us", "rope_k_alone_us", "landmark_scores_us", "landmark_scores_torch_route_us",
+    beside = ("module_forward_us", "module_forward_graph_us", "rope_k_alone_us", "landmark_scores_us", "landmark_scores_torch_route_us",
               "select_topk_and_windows_us")
     res["stages_sum_us"] = sum(v for kk, v in res.items() if kk.endswith("_us") and kk not in beside)
     return res

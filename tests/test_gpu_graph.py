@@ -90,3 +90,31 @@ def test_soft_backward_replays_match_eager():
         torch.cuda.synchronize()
         for got, want in zip(bwd.results, ref):
             assert torch.equal(torch.nan_to_num(got), torch.nan_to_num(want))
+
+
+def test_module_eval_forward_replays_match_eager():
+    """DSALTAttention's packed inference forward (bf16, host cu_list, _last_P off) captured
+    whole - projections, the two-launch selection, the forward, out_proj - and replayed."""
+    print("graph module eval forward", flush=True)
+    from dsalt.modules import DSALTAttention
+    torch.manual_seed(7)
+    mod = DSALTAttention(512, 8, 16, 300, 32, max_seq_len=1024).to(DEV).to(torch.bfloat16).eval()
+    mod._collect_last_P = False
+    lens = [600, 424, 1000]
+    cu_list = [0] + np.cumsum(lens).tolist()
+    cu = torch.tensor(cu_list, dtype=torch.int32, device=DEV)
+    x = torch.randn(cu_list[-1], 512, device=DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        mod(x, cu_seqlens=cu, cu_list=cu_list)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out_g, _ = mod(x, cu_seqlens=cu, cu_list=cu_list)
+        for seed in (1, 2, 3):
+            gen = torch.Generator(device="cpu").manual_seed(seed)
+            x.copy_(torch.randn(x.shape, generator=gen).to(DEV, x.dtype))
+            out_e, _ = mod(x, cu_seqlens=cu, cu_list=cu_list)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out_g, out_e)
