@@ -342,14 +342,14 @@ def time_launches(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
-def measure_front_end(wl, w, cu, sel) -> dict:
+def measure_front_end(wl, w, cu) -> dict:
     """The inference selection path in bf16 at the workload's shape: hybrid scores + top-k,
     by the reference's route (x @ W_V^T GEMM, norms and standardisation in torch,
-    landmark_tokens_ker.py:45-61), by the torch ops on the module's value projection, and
-    by the module's default (dsalt_hybrid_scores on the module's value projection). All
-    eager, launch costs included; the HIP scores also
-    from a HIP graph (GPU time alone). HBM bytes of the fused score kernels: x and v read
-    once (bf16), norms and scores written and read back (fp32)."""
+    landmark_tokens_ker.py:45-61), by the torch ops on the module's value projection, by
+    dsalt_hybrid_scores followed by the selection, and by the module's default,
+    dsalt_select_hybrid. All eager, launch costs included; the HIP routes also from a HIP
+    graph (GPU time alone). HBM bytes of the score kernels: x and v read once (bf16), norms
+    and scores written and read back (fp32)."""
     from dsalt import _hip
     from dsalt.kernels.landmark_tokens_ker import hybrid_scores_per_head
     mod, T, H, D = wl["mod"], wl["T"], wl["H"], wl["D"]
@@ -412,6 +412,12 @@ def measure_front_end(wl, w, cu, sel) -> dict:
                 "select_hybrid_path: the module's default, dsalt_select_hybrid (norms pass, then the selection "
                 "forming each score itself: 2 launches, same sets, checked)",
     }
+
+
+def measure_selection(device: torch.device) -> dict:
+    """measure_front_end alone on the c2 workload (for kernel traces of the selection)."""
+    wl = make_workload("c2", device)
+    return measure_front_end(wl, wl["w"], wl["cu"])
 
 
 def measure_host_launch(device: torch.device, calls: int = 4000) -> dict:
@@ -718,7 +724,7 @@ def main():
                     help="skip the config-4, dense-variant and config-5 LM measurements")
     ap.add_argument("--only-fwd", action="store_true",
                     help="time only the headline forward of --config and exit (for profiling)")
-    ap.add_argument("--only", choices=("lm", "dense", "backward", "c4", "peaks"), default=None,
+    ap.add_argument("--only", choices=("lm", "dense", "backward", "c4", "peaks", "selection"), default=None,
                     help="run only that measurement and print its JSON (for profiling)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (counter calibration)")
@@ -741,7 +747,7 @@ def main():
         del src, dst
     if args.only is not None:
         fn = {"lm": measure_lm, "dense": measure_dense, "backward": measure_backward, "c4": measure_c4,
-              "peaks": measure_peaks}[args.only]
+              "peaks": measure_peaks, "selection": measure_selection}[args.only]
         print(json.dumps(fn(dev)))
         return
     wl = make_workload(args.config, dev)
@@ -772,7 +778,7 @@ def main():
     if not (torch.equal(selq.out, sel.out) and torch.equal(selq.w_out, w.float())):
         raise RuntimeError("fused selection + quantisation differs from the separate launches")
     bytes_sel = 4 * T * H + 4 * T + 4 * (wl["B"] + 1) + 8 * H * wl["B"] * wl["k_lmk"]
-    front = measure_front_end(wl, w, cu, sel)
+    front = measure_front_end(wl, w, cu)
 
     # cold HBM: launches rotate over input sets whose total (> 512 MB) exceeds the
     # 256 MB last-level cache, so every launch reads Q, K and V from HBM
