@@ -181,7 +181,7 @@ __global__ void __launch_bounds__(64 * kDqW, D == 64 ? 3 : 2) bwd_dq_kernel(cons
     head_rank(blockIdx.x, p.grid_dq, p.n_heads, p.n_dqblk, head, rank);
     if (head >= p.n_heads) return;
     int seq, blk, seq_start, seq_len;
-    if (!find_block_desc(p.cu, p.num_seqs, rank, p.n_dqblk, BM, lane, seq, blk, seq_start, seq_len)) return;
+    if (!find_block_desc(p.cu, p.num_seqs, p.total_len, rank, p.n_dqblk, BM, lane, seq, blk, seq_start, seq_len)) return;
     const int target = seq_start / BM + seq + blk;  // the block's find_block id (ws_minlo index)
     const int wq0 = blk * BM + wave * 32;
     const int i = wq0 + ql;
@@ -610,7 +610,9 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
         // chunk partials summed in chunk order (zero for an empty sequence)
         const int id = blockIdx.x - p.grid_q;
         const int h = id / p.num_seqs, sq = id - h * p.num_seqs;
-        const int st0 = p.cu[sq], len = p.cu[sq + 1] - st0;
+        int st0, en0;
+        seq_bounds(p.cu, sq, p.total_len, st0, en0);
+        const int len = en0 - st0;
         const int n_ch = (len + kLC - 1) / kLC;
         const size_t base = (size_t)h * p.n_lchunk + st0 / kLC + sq;  // the sequence's first chunk row
         for (int sl = threadIdx.x; sl < p.k_lmk; sl += NT) {
@@ -630,7 +632,7 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
         int rank, bdesc;
         head_rank(blockIdx.x, p.grid_q, p.n_heads, p.n_qblk, head, rank);
         if (head >= p.n_heads) return;
-        if (!find_block_desc(p.cu, p.num_seqs, rank, p.n_qblk, kBM, lane, seq, bdesc, seq_start, seq_len)) return;
+        if (!find_block_desc(p.cu, p.num_seqs, p.total_len, rank, p.n_qblk, kBM, lane, seq, bdesc, seq_start, seq_len)) return;
         kblk = (seq_len + kBM - 1) / kBM - 1 - bdesc;
     } else {
         // workgroup = (head, 64-slot group, query chunk); chunk ids follow find_block
@@ -640,7 +642,7 @@ __global__ void __launch_bounds__(LMK ? 256 : 64 * kv_waves(D), D == 64 ? 2 : 1)
         const int gp = rem / p.n_lchunk;
         lcid = rem - gp * p.n_lchunk;
         int lchunk;
-        if (!find_block(p.cu, p.num_seqs, lcid, kLC, lane, seq, lchunk, seq_start, seq_len)) return;
+        if (!find_block(p.cu, p.num_seqs, p.total_len, lcid, kLC, lane, seq, lchunk, seq_start, seq_len)) return;
         sbw = wave & 1;
         slot = gp * 64 + (wave >> 1) * 32 + ql;
         q_begin = lchunk * kLC;  // refined below

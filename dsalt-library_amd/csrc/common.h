@@ -131,6 +131,15 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
+// Bounds of sequence s as the kernels use them: cu_seqlens entries clamped to [0, T] and
+// the end to at least the start. For every packing with 0 <= cu[0] <= ... <= cu[S] <= T
+// this is (cu[s], cu[s+1]); for any other content of cu_seqlens it still keeps every row
+// a kernel reads or writes inside the T rows of its tensors.
+__device__ __forceinline__ void seq_bounds(const int32_t *__restrict__ cu, int s, int total_len, int &c0, int &c1) {
+    c0 = min(max(cu[s], 0), total_len);
+    c1 = max(min(cu[s + 1], total_len), c0);
+}
+
 // Workgroup ids over the query (or key) blocks of a packed batch. Sequence s (start
 // cu[s], length L_s) owns the ceil(L_s / bm) consecutive ids starting at
 // first(s) = floor(cu[s] / bm) + s. first() is strictly increasing and the ranges are
@@ -140,16 +149,15 @@ __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_lo
 // entries and a ballot per 64 sequences - no prefix sum and no host-side block map,
 // so launches need no device-to-host synchronisation. Every lane returns the same
 // (wave-uniform) answer, with the sequence's start and length.
-__device__ __forceinline__ bool find_block(const int32_t *__restrict__ cu, int num_seqs, int target,
-                                           int bm, int lane, int &seq, int &blk, int &seq_start,
+__device__ __forceinline__ bool find_block(const int32_t *__restrict__ cu, int num_seqs, int total_len,
+                                           int target, int bm, int lane, int &seq, int &blk, int &seq_start,
                                            int &seq_len) {
     int cand = -1, cand_first = 0, cand_start = 0, cand_end = 0;
     for (int base = 0; base < num_seqs; base += 64) {
         const int s = base + lane;
         int c0 = 0, c1 = 0, first = INT_MAX;
         if (s < num_seqs) {
-            c0 = cu[s];
-            c1 = cu[s + 1];
+            seq_bounds(cu, s, total_len, c0, c1);
             first = c0 / bm + s;
         }
         const unsigned long long m = __ballot(first <= target);  // a prefix of the lanes
@@ -170,10 +178,10 @@ __device__ __forceinline__ bool find_block(const int32_t *__restrict__ cu, int n
     seq_len = len;
     return true;
 }
-__device__ __forceinline__ bool find_block(const int32_t *__restrict__ cu, int num_seqs, int target,
-                                           int bm, int lane, int &seq, int &blk) {
+__device__ __forceinline__ bool find_block(const int32_t *__restrict__ cu, int num_seqs, int total_len,
+                                           int target, int bm, int lane, int &seq, int &blk) {
     int start, len;
-    return find_block(cu, num_seqs, target, bm, lane, seq, blk, start, len);
+    return find_block(cu, num_seqs, total_len, target, bm, lane, seq, blk, start, len);
 }
 
 // Wave-uniform reductions over all 64 lanes without LDS: DPP quad/row permutations
@@ -289,16 +297,15 @@ __device__ __forceinline__ int wave_sum_u(int x) { return wave_reduce_dpp(x, Add
 // >= b, so the level of `rank` is the largest b with C(b) > rank (binary search over
 // DPP wave sums) and its sequence is the (rank - C(b+1))-th of that level. One lane per
 // sequence: more than 64 sequences use find_block over reversed ids instead.
-__device__ __forceinline__ bool find_block_desc(const int32_t *__restrict__ cu, int num_seqs, int rank, int n_rank,
-                                                int bm, int lane, int &seq, int &blk, int &seq_start,
-                                                int &seq_len) {
+__device__ __forceinline__ bool find_block_desc(const int32_t *__restrict__ cu, int num_seqs, int total_len,
+                                                int rank, int n_rank, int bm, int lane, int &seq, int &blk,
+                                                int &seq_start, int &seq_len) {
     if (num_seqs > 64)
-        return find_block(cu, num_seqs, n_rank - 1 - rank, bm, lane, seq, blk, seq_start, seq_len);
+        return find_block(cu, num_seqs, total_len, n_rank - 1 - rank, bm, lane, seq, blk, seq_start, seq_len);
     int c0 = 0, c1 = 0, nblk = 0;
     if (lane < num_seqs) {
-        c0 = cu[lane];
-        c1 = cu[lane + 1];
-        nblk = max(c1 - c0 + bm - 1, 0) / bm;
+        seq_bounds(cu, lane, total_len, c0, c1);
+        nblk = (c1 - c0 + bm - 1) / bm;
     }
     if (rank >= wave_sum_u(nblk)) return false;
     int lo = 0, hi = wave_max_u(nblk);  // C(lo) > rank >= C(hi) = 0

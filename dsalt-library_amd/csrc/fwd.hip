@@ -134,7 +134,7 @@ __global__ void __launch_bounds__(64 * fwd_waves(D), fwd_waves_per_simd(D, MODE 
     head_rank(blockIdx.x, p.grid, p.n_heads, p.n_qblk, head, rank);
     if (head >= p.n_heads) return;
     int seq, blk, seq_start, seq_len;
-    if (!find_block_desc(p.cu, p.num_seqs, rank, p.n_qblk, BM, lane, seq, blk, seq_start, seq_len)) return;
+    if (!find_block_desc(p.cu, p.num_seqs, p.total_len, rank, p.n_qblk, BM, lane, seq, blk, seq_start, seq_len)) return;
     const int wq0 = blk * BM + wave * 32;      // first query of this wave
     const int i = wq0 + ql;                    // query offset inside the sequence
     const bool qvalid = i < seq_len;

@@ -47,8 +47,8 @@ __global__ void __launch_bounds__(256) rope_kernel(const RopeParams p) {
         const int which = r >= p.heads[0] * nj;  // 0: q, 1: k
         if (which) r -= p.heads[0] * nj;
         const int h = r / nj, j0 = (r - h * nj) * VW;
-        const int pos = p.cu ? seq_offset(p.cu, p.S, t) : t;
-        const bool in_table = pos < p.rows;  // a row past the table: NaN outputs
+        const int pos = p.cu ? seq_offset(p.cu, p.S, p.T, t) : t;
+        const bool in_table = pos >= 0 && pos < p.rows;  // no table row (past it, or a token before cu[0]): NaN outputs
         const float *cr = p.cos + (int64_t)(in_table ? pos : 0) * p.cs_st;
         const float *sr = p.sin + (int64_t)(in_table ? pos : 0) * p.cs_st;
         const int64_t ib = (int64_t)t * p.in_st[which] + (int64_t)h * p.in_sh[which];

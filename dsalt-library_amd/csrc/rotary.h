@@ -114,15 +114,18 @@ __device__ __forceinline__ void ldv_f32(const float *p, float *x) {
 }
 
 
-// Offset of token t inside its sequence (binary search over cu_seqlens[0 .. S]).
-__device__ __forceinline__ int seq_offset(const int32_t *cu, int S, int t) {
+// Offset of token t inside its sequence (binary search over cu_seqlens[0 .. S], its
+// entries clamped to [0, T] as seq_bounds clamps them). Negative for a token before the
+// first sequence.
+__device__ __forceinline__ int seq_offset(const int32_t *cu, int S, int T, int t) {
+    auto at = [&](int s) { return min(max(cu[s], 0), T); };
     int lo = 0, hi = S;  // cu[lo] <= t < cu[hi]
     while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
-        if (cu[mid] <= t) lo = mid;
+        if (at(mid) <= t) lo = mid;
         else hi = mid;
     }
-    return t - cu[lo];
+    return t - at(lo);
 }
 
 // Rotate the VW pairs (j0 + e, j0 + e + half) of one head row: reads in[ib + ...], writes

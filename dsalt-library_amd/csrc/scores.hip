@@ -154,8 +154,8 @@ __global__ void __launch_bounds__(64 * kNormTokens) norms_kernel(const ScorePara
             // RoPE of the token's k row: lane r takes pair vector r (16 bytes of each half)
             constexpr int VW = EV;
             const int half = p.D >> 1, nj = half / VW;
-            const int pos = p.cu ? seq_offset(p.cu, p.S, t) : t;
-            const bool in_table = pos < p.rows;
+            const int pos = p.cu ? seq_offset(p.cu, p.S, p.T, t) : t;
+            const bool in_table = pos >= 0 && pos < p.rows;
             const float *cr = p.cos + (int64_t)(in_table ? pos : 0) * p.cs_st;
             const float *sr = p.sin + (int64_t)(in_table ? pos : 0) * p.cs_st;
             for (int r = lane; r < p.n_kv * nj; r += 64) {

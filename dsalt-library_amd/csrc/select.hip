@@ -384,7 +384,7 @@ __global__ void __launch_bounds__(kSelThreads) select_chunk_kernel(const SelPara
     const int head = blockIdx.x / p.n_chunk_ub;
     const int cid = blockIdx.x - head * p.n_chunk_ub;
     int seq, chunk, start, L;
-    if (!find_block(p.cu, p.num_seqs, cid, kSelChunk, lane, seq, chunk, start, L)) return;
+    if (!find_block(p.cu, p.num_seqs, p.total_len, cid, kSelChunk, lane, seq, chunk, start, L)) return;
     if (!split_sequence(L, p.k)) return;  // selected from the scores by select_kernel
     const int c0 = chunk * kSelChunk;
     const int n = min(kSelChunk, L - c0);
@@ -415,8 +415,9 @@ __global__ void __launch_bounds__(kSelThreads) select_kernel(const SelParams p) 
     const int tid = threadIdx.x;
     const int head = blockIdx.x / p.num_seqs;
     const int seq = blockIdx.x - head * p.num_seqs;
-    const int start = p.cu[seq];
-    const int L = max(p.cu[seq + 1] - start, 0);
+    int start, end;
+    seq_bounds(p.cu, seq, p.total_len, start, end);
+    const int L = end - start;
     int64_t *out = p.out + ((int64_t)head * p.num_seqs + seq) * p.k;
     const int k_eff = min(p.k, L);
     int total;

@@ -28,6 +28,11 @@
  *   - Landmark positions are int64 [H, S, k], relative to the sequence start; -1 (or any
  *     value outside [0, L_s)) marks an empty slot.
  *   - cu_seqlens is int32 [S + 1], non-decreasing, cu_seqlens[0] = 0, cu_seqlens[S] = T.
+ *     It lives on the device, so the host-side checks cannot read it; the kernels take
+ *     sequence s as rows [clamp(cu[s], 0, T), max(clamp(cu[s+1], 0, T), that start)), so
+ *     that no content of cu_seqlens makes them read or write outside the T rows (a packing
+ *     that breaks the rule above gives results for those clamped sequences, and RoPE gives
+ *     NaN to a token before cu_seqlens[0]).
  *   - `stream` is a hipStream_t (NULL = default stream). Calls are asynchronous on that
  *     stream, never synchronise and never allocate memory; the backward takes its scratch
  *     memory from a caller-provided workspace.

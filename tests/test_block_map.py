@@ -8,19 +8,38 @@ import numpy as np
 import pytest
 
 
-def first_ids(cu, bm):
-    return [int(cu[s]) // bm + s for s in range(len(cu) - 1)]
+def bounds(cu, s, T):
+    """seq_bounds: the entries clamped to [0, T], the end to at least the start."""
+    c0 = min(max(int(cu[s]), 0), T)
+    return c0, max(min(int(cu[s + 1]), T), c0)
 
 
-def lookup(cu, bm, target):
-    """Device algorithm: the last sequence with first(s) <= target, then a range check."""
-    f = first_ids(cu, bm)
-    cand = max((s for s in range(len(f)) if f[s] <= target), default=-1)
+def first_ids(cu, bm, T=None):
+    T = int(cu[-1]) if T is None else T
+    return [bounds(cu, s, T)[0] // bm + s for s in range(len(cu) - 1)]
+
+
+def lookup(cu, bm, target, T=None, with_bounds=False):
+    """Device algorithm of find_block: per group of 64 sequences, the last one whose
+    first(s) <= target (the next group only when the group's last one qualifies), then a
+    range check."""
+    T = int(cu[-1]) if T is None else T
+    f = first_ids(cu, bm, T)
+    cand = -1
+    for base in range(0, len(f), 64):
+        lanes = [l for l in range(min(64, len(f) - base)) if f[base + l] <= target]
+        if not lanes:
+            break
+        cand = base + lanes[-1]
+        if lanes[-1] < 63:
+            break
     if cand < 0:
         return None
-    L = int(cu[cand + 1] - cu[cand])
+    c0, c1 = bounds(cu, cand, T)
     blk = target - f[cand]
-    return (cand, blk) if blk < (L + bm - 1) // bm else None
+    if blk >= (c1 - c0 + bm - 1) // bm:
+        return None
+    return (cand, blk, c0, c1 - c0) if with_bounds else (cand, blk)
 
 
 @pytest.mark.parametrize("bm", [64, 128])
@@ -46,13 +65,15 @@ def test_block_ids_cover_every_block_once(bm, seed):
         assert ids == list(range(ids[0], ids[0] + len(ids))) if ids else True
 
 
-def lookup_desc(cu, bm, rank, n_rank):
+def lookup_desc(cu, bm, rank, n_rank, T=None, with_bounds=False):
     """Device algorithm of find_block_desc: blocks in decreasing block index (ties in
     increasing sequence), through the binary search over C(b) = sum_s max(0, n_s - b)."""
+    T = int(cu[-1]) if T is None else T
     S = len(cu) - 1
     if S > 64:
-        return lookup(cu, bm, n_rank - 1 - rank)
-    n = [max(int(cu[s + 1] - cu[s]) + bm - 1, 0) // bm for s in range(S)]
+        return lookup(cu, bm, n_rank - 1 - rank, T, with_bounds)
+    bnd = [bounds(cu, s, T) for s in range(S)]
+    n = [(c1 - c0 + bm - 1) // bm for c0, c1 in bnd]
     if rank >= sum(n):
         return None
     C = lambda b: sum(max(x - b, 0) for x in n)  # noqa: E731
@@ -65,7 +86,8 @@ def lookup_desc(cu, bm, rank, n_rank):
             hi = mid
     j = rank - C(lo + 1)
     level = [s for s in range(S) if n[s] > lo]
-    return (level[j], lo)
+    s = level[j]
+    return (s, lo, bnd[s][0], bnd[s][1] - bnd[s][0]) if with_bounds else (s, lo)
 
 
 def head_rank(bid, grid, n_heads, n_rank):
@@ -110,3 +132,30 @@ def test_head_rank_covers_grid(n_heads):
         for x in range(8):
             ranks = [seen[b][1] for b in range(x, grid, 8)]
             assert ranks == sorted(ranks)
+
+
+@pytest.mark.parametrize("desc", [False, True], ids=["find_block", "find_block_desc"])
+@pytest.mark.parametrize("seed", range(12))
+def test_any_cu_seqlens_content_stays_inside_the_rows(desc, seed):
+    """Whatever cu_seqlens holds (negative entries, entries past T, decreasing runs, a
+    first entry above 0), every block the lookup returns lies inside the T rows: start >= 0,
+    start + length <= T and block * bm < length, for every id of the launch's grid. For
+    valid packings the clamps change nothing (the tests above)."""
+    rng = np.random.default_rng(500 + seed)
+    bm = 64
+    S = int(rng.integers(1, 70)) if seed % 3 else int(rng.integers(65, 140))
+    T = int(rng.integers(1, 40 * bm))
+    cu = rng.integers(-3 * bm, T + 3 * bm, size=S + 1)
+    if seed % 2:  # mostly increasing with a few disorders
+        cu = np.sort(cu)
+        for _ in range(3):
+            i, j = rng.integers(0, S + 1, size=2)
+            cu[i], cu[j] = cu[j], cu[i]
+    n_rank = (T + bm - 1) // bm + S
+    for r in range(n_rank):
+        got = lookup_desc(cu, bm, r, n_rank, T, True) if desc else lookup(cu, bm, r, T, True)
+        if got is None:
+            continue
+        s, blk, start, length = got
+        assert 0 <= s < S and blk >= 0
+        assert 0 <= start and start + length <= T and blk * bm < length
