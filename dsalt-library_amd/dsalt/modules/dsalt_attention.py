@@ -9,8 +9,10 @@ Packed input (``cu_seqlens`` given) runs the sparse path:
   * training: ``_train_selectors`` (continuous window, HIP landmark top-k, soft landmark
     weight log sigmoid(s/tau_lmk)) then the SOFT HIP kernels (forward + deterministic
     backward carrying d_w~ to win_gate and d_logw to alpha_w), dsalt_attention.py:440-487;
-  * inference: floor-quantised windows (HIP), hybrid scores from the value projection
-    and HIP landmark top-k, the HARD HIP kernel, dsalt_attention.py:610-625; then the
+  * inference: two HIP launches select (dsalt_select_hybrid: a norms pass over x and the
+    value projection that also rotates k, then one launch forming the hybrid scores, the
+    floor-quantised windows from the gate logits and the landmark top-k), then the HARD
+    HIP kernel rotating q as it loads it, dsalt_attention.py:610-625; then the
     ``_last_P`` diagnostic of sequence 0 unless ``_collect_last_P`` is set to False
     (dsalt_attention.py:636-702).
 The attention output stays in the compute dtype on the module path (the reference
@@ -57,12 +59,12 @@ class DSALTAttention(nn.Module):
 
     ``_fused_selector`` (default True): without a projection bias the landmark scores are
     formed from the module's own value projection ``v = x W_V^T`` instead of a second
-    ``x @ W_V.T`` GEMM. ``_hip_scores`` (default True) forms the selection's scores with
-    the one-pass HIP score kernel over x and v (norms, standardisation and the hybrid
-    combination in two launches, no torch passes); it rounds its fp32 norm sums in another
+    ``x @ W_V.T`` GEMM. ``_hip_scores`` (default True) selects with the HIP norms pass over
+    x and v, whose statistics, standardisation and hybrid combination the selection launch
+    forms itself (no torch passes, no score tensor); it rounds its fp32 norm sums in another
     order than torch, so a score can differ in its last bits from the reference's route -
-    the landmark sets of configs 2 and 4 (fp32, bf16, autocast) are the reference route's,
-    set for set, but a near-tie could move. ``_hip_scores = False`` keeps torch's own norm
+    the landmark sets of configs 2, 3 and 4 (fp32, bf16, autocast) are the reference
+    route's, set for set, but a near-tie could move. ``_hip_scores = False`` keeps torch's own norm
     and standardisation ops on v, whose fp32 scores are bit-identical to the reference's
     route. The differentiable landmark weights of training always use the torch ops.
     ``_last_selection`` holds the ``(windows, landmark positions)`` of the last forward.
@@ -70,7 +72,7 @@ class DSALTAttention(nn.Module):
 
     _fused_selector = True
     _hip_scores = True
-    _fuse_rope_k = True  # inference: k rotated by the score launch (when that route is taken)
+    _fuse_rope_k = True  # inference: k rotated by the selection's norms pass (when that route is taken)
 
     def __init__(
         self,
