@@ -130,6 +130,31 @@ class DSALTAttention(nn.Module):
     def _alpha(self) -> torch.Tensor:
         return torch.sigmoid(self.alpha_w)
 
+    def _alpha_selection(self) -> torch.Tensor:
+        """``sigmoid(alpha_w)`` detached, in fp32 (rounded to ``alpha_w``'s dtype first, as
+        the selection's scores see it): the per-head balance of the inference selection,
+        which takes no gradient. Computed once per parameter storage and version."""
+        p = self.alpha_w
+        key = (p.data_ptr(), p._version, p.dtype)
+        hit = getattr(self, "_alpha_sel_cache", None)
+        if hit is None or hit[0] != key:
+            with torch.no_grad():
+                hit = (key, torch.sigmoid(p.detach()).float())
+            self._alpha_sel_cache = hit
+        return hit[1]
+
+    def _rope_tables(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """``rope_cos`` / ``rope_sin`` as the contiguous fp32 tables the HIP kernels read
+        (they round each entry to the tensor dtype, so the values used are unchanged),
+        converted once per buffer storage and version instead of on every call."""
+        c, s = self.rope_cos, self.rope_sin
+        key = (c.data_ptr(), s.data_ptr(), c._version, s._version, c.dtype)
+        hit = getattr(self, "_rope_tables_cache", None)
+        if hit is None or hit[0] != key:
+            hit = (key, c.to(torch.float32).contiguous(), s.to(torch.float32).contiguous())
+            self._rope_tables_cache = hit
+        return hit[1], hit[2]
+
     def _apply_out_proj(self, out: torch.Tensor) -> torch.Tensor:
         """out_proj in its weight's dtype (the attention output may be fp32 or 16-bit)."""
         wdt = self.out_proj.weight.dtype
@@ -191,7 +216,7 @@ class DSALTAttention(nn.Module):
         v = self.v_proj(xs).view(T, self.n_kv_heads, self.head_dim)
         v_sel = v if (self.v_proj.bias is None and self._fused_selector) else None
         cu = torch.tensor([0, T], dtype=torch.int32, device=device)
-        q, k = apply_rotary_emb_packed(q, k, self.rope_cos, self.rope_sin, cu)
+        q, k = apply_rotary_emb_packed(q, k, *self._rope_tables(), cu)
 
         # grouped K/V heads go to the kernels as they are (query head h reads K/V head
         # h // n_rep); no repeated copy
@@ -282,9 +307,9 @@ class DSALTAttention(nn.Module):
                   and k.shape == v_sel.shape and _hip.scores_supported(x, v_sel))
         if fuse_q:
             if not fuse_k:
-                k = rotate_packed(k, self.rope_cos, self.rope_sin, cu_seqlens)
+                k = rotate_packed(k, *self._rope_tables(), cu_seqlens)
         elif rope_cs is None:
-            q, k = apply_rotary_emb_packed(q, k, self.rope_cos, self.rope_sin, cu_seqlens)
+            q, k = apply_rotary_emb_packed(q, k, *self._rope_tables(), cu_seqlens)
         else:
             cos, sin = rope_cs
             q, k = apply_rotary_emb_packed(q, k, cos.reshape(total_len, -1), sin.reshape(total_len, -1))
@@ -300,7 +325,7 @@ class DSALTAttention(nn.Module):
                                    self.tau_win, float(self.win_edge))
             return self._apply_out_proj(out.reshape(total_len, self.d_model)), aux
 
-        alpha = self._alpha()
+        alpha = self._alpha_selection()  # the HARD output takes no gradient from the scores
         route_v = v_sel if self._fused_selector else None
         # the windows are formed from the gate's logits and quantised by the selection
         # launch itself (same values as _window_sizes(floor=True) followed by
@@ -319,7 +344,7 @@ class DSALTAttention(nn.Module):
                                                            default=0)
                 w_sizes, lmk_indices, k = _hip.select_hybrid(
                     x.detach(), v_sel.detach(), alpha.detach().float(), self.n_heads, w_cont, cu_seqlens, self.k_lmk,
-                    max_seqlen=max_len, gate=gate, rope_k=(k, self.rope_cos, self.rope_sin, cu_seqlens))
+                    max_seqlen=max_len, gate=gate, rope_k=(k, *self._rope_tables(), cu_seqlens))
         else:
             with torch.no_grad():
                 w_sizes, lmk_indices = _landmarks_and_windows(
@@ -329,12 +354,12 @@ class DSALTAttention(nn.Module):
         self._last_selection = (w_sizes, lmk_indices)
         # Hard A(i) = W(i) ∪ L(i): the score only selects (zero landmark bias).
         out = sparse_attention(_hip.MODE_HARD, q, k, v, lmk_indices, None, w_sizes, cu_seqlens,
-                               rope=(self.rope_cos, self.rope_sin) if fuse_q else None)
+                               rope=self._rope_tables() if fuse_q else None)
 
         if getattr(self, "_collect_last_P", True):
             if fuse_q:  # the diagnostic needs the rotated q of the first sequence
                 n0 = int(cu_list[1]) if cu_list is not None else int(cu_seqlens[1])
-                q = rotate_packed(q[:n0].contiguous(), self.rope_cos, self.rope_sin, cu_seqlens[:2])
+                q = rotate_packed(q[:n0].contiguous(), *self._rope_tables(), cu_seqlens[:2])
             self._last_P = self._first_sequence_probs(x, q, k, w_sizes, alpha, cu_seqlens, cu_list)
         else:
             self._last_P = None
