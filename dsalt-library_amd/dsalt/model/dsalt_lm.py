@@ -116,7 +116,8 @@ class DSALTLMHeadModel(nn.Module):
         for layer in self.layers:
             x, a = layer(x, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen,
                          gradient_checkpointing=gradient_checkpointing, cu_list=cu_list)
-            aux = aux + a
+            if labels is not None:  # the layers' auxiliary losses are only returned with a loss
+                aux = aux + a
         x = self.final_norm(x)
         if labels is None:
             return {"loss": None, "logits": self.lm_head(x), "aux_loss": None}
