@@ -324,6 +324,21 @@ int dsalt_select_hybrid(const dsalt_scores_args *sa, const dsalt_select_args *a,
     return DSALT_OK;
 }
 
+int dsalt_swiglu(const void *gate, const void *up, void *out, int64_t n, int32_t dtype, void *stream) {
+    if (n < 0) return fail(DSALT_ERR_INVALID, "n must be >= 0 (got %lld)", (long long)n);
+    if (dtype != DSALT_DTYPE_BF16 && dtype != DSALT_DTYPE_F16 && dtype != DSALT_DTYPE_F32)
+        return fail(DSALT_ERR_INVALID, "dtype must be DSALT_DTYPE_BF16, _F16 or _F32 (got %d)", dtype);
+    const int per = dtype == DSALT_DTYPE_F32 ? 4 : 8;  // elements per 16-byte access
+    if (n % per) return fail(DSALT_ERR_UNSUPPORTED, "n must be a multiple of %d (got %lld)", per, (long long)n);
+    if (n == 0) return DSALT_OK;
+    if (!gate || !up || !out) return fail(DSALT_ERR_INVALID, "gate, up and out must be non-NULL");
+    if (!aligned(gate, 16) || !aligned(up, 16) || !aligned(out, 16))
+        return fail(DSALT_ERR_INVALID, "gate, up and out must be 16-byte aligned");
+    hipError_t e = dsalt::launch_swiglu(gate, up, out, n, dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(DSALT_ERR_LAUNCH, "dsalt_swiglu launch failed: %s", hipGetErrorString(e));
+    return DSALT_OK;
+}
+
 int dsalt_rope_check(const dsalt_rope_args *a) {
     if (!a) return fail(DSALT_ERR_INVALID, "args is NULL");
     if (a->total_len < 0 || a->n_q_heads < 0 || a->n_k_heads < 0)

@@ -86,8 +86,15 @@ struct Elem<F16> {
     }
     template <int VW>
     static __device__ __forceinline__ void stv(void *p, int64_t i, const float *x) {
+        if constexpr (VW == 8) {  // one 16-byte store
+            uint32_t w[4];
 #pragma unroll
-        for (int e = 0; e < VW; ++e) st(p, i + e, x[e]);
+            for (int e = 0; e < 4; ++e) w[e] = F16::pack2(x[2 * e], x[2 * e + 1]);
+            *reinterpret_cast<uint4 *>(static_cast<_Float16 *>(p) + i) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < VW; ++e) st(p, i + e, x[e]);
+        }
     }
 };
 template <>
@@ -97,13 +104,22 @@ struct Elem<F32> {
     static __device__ __forceinline__ void st(void *p, int64_t i, float x) { static_cast<float *>(p)[i] = x; }
     template <int VW>
     static __device__ __forceinline__ void ldv(const void *p, int64_t i, float *x) {
+        if constexpr (VW == 4) {  // one 16-byte load
+            const float4 v = *reinterpret_cast<const float4 *>(static_cast<const float *>(p) + i);
+            x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+        } else {
 #pragma unroll
-        for (int e = 0; e < VW; ++e) x[e] = ld(p, i + e);
+            for (int e = 0; e < VW; ++e) x[e] = ld(p, i + e);
+        }
     }
     template <int VW>
     static __device__ __forceinline__ void stv(void *p, int64_t i, const float *x) {
+        if constexpr (VW == 4) {  // one 16-byte store
+            *reinterpret_cast<float4 *>(static_cast<float *>(p) + i) = make_float4(x[0], x[1], x[2], x[3]);
+        } else {
 #pragma unroll
-        for (int e = 0; e < VW; ++e) st(p, i + e, x[e]);
+            for (int e = 0; e < VW; ++e) st(p, i + e, x[e]);
+        }
     }
 };
 

@@ -134,7 +134,7 @@ EXPORTED_SYMBOLS = (
     "dsalt_abi_version", "dsalt_last_error", "dsalt_fwd_args_size", "dsalt_bwd_args_size",
     "dsalt_select_args_size", "dsalt_hybrid_scores", "dsalt_scores_check", "dsalt_scores_workspace_size",
     "dsalt_scores_args_size", "dsalt_rope", "dsalt_rope_check", "dsalt_rope_args_size",
-    "dsalt_bwd_noalloc", "dsalt_select_workspace_size", "dsalt_select_hybrid",
+    "dsalt_bwd_noalloc", "dsalt_select_workspace_size", "dsalt_select_hybrid", "dsalt_swiglu",
 )
 NOALLOC_SCRATCH_BYTES = 76 << 20  # DSALT_NOALLOC_SCRATCH_BYTES
 SELECT_SPLIT_MIN = 4096  # longer sequences can be selected chunk-wise
@@ -166,6 +166,7 @@ def lib() -> ctypes.CDLL:
         ("dsalt_rope", [ctypes.POINTER(RopeArgs), c_void_p]),
         ("dsalt_rope_check", [ctypes.POINTER(RopeArgs)]),
         ("dsalt_quantize_windows", [c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
+        ("dsalt_swiglu", [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
     ):
         fn = getattr(h, name)
         fn.argtypes = argtypes
@@ -991,3 +992,28 @@ def quantize_windows(w_cont: torch.Tensor, want_int: bool = False):
     _raise(lib().dsalt_quantize_windows(w_cont.data_ptr(), n, wq.data_ptr(), _ptr(wi), stream_handle(dev)),
            "dsalt_quantize_windows")
     return (wq, wi) if want_int else wq
+
+
+def swiglu_supported(gate: torch.Tensor, up: torch.Tensor) -> bool:
+    """Whether dsalt_swiglu takes these operands: GPU tensors of one shape and dtype (bf16,
+    fp16 or fp32), contiguous and 16-byte aligned, with a multiple of 8 (4 for fp32)
+    elements."""
+    if gate.device.type != "cuda" or up.device != gate.device or gate.dtype not in _SCORE_DTYPES:
+        return False
+    if up.dtype != gate.dtype or up.shape != gate.shape or not (gate.is_contiguous() and up.is_contiguous()):
+        return False
+    per = 4 if gate.dtype == torch.float32 else 8
+    return gate.numel() % per == 0 and gate.data_ptr() % 16 == 0 and up.data_ptr() % 16 == 0
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """``F.silu(gate) * up`` in one HIP pass, bit for bit torch's two ops (no autograd)."""
+    dev = require_gpu(gate, up)
+    if not swiglu_supported(gate, up):
+        raise DsaltError(f"dsalt_swiglu needs contiguous, 16-byte aligned gate and up of one shape and "
+                         f"dtype with a multiple of 8 (4 for fp32) elements (got {tuple(gate.shape)} "
+                         f"{gate.dtype}, {tuple(up.shape)} {up.dtype})")
+    out = torch.empty_like(gate)
+    _raise(lib().dsalt_swiglu(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(),
+                              _SCORE_DTYPES[gate.dtype], stream_handle(dev)), "dsalt_swiglu")
+    return out

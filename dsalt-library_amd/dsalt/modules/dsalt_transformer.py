@@ -13,12 +13,15 @@ import torch.nn as nn
 import torch.nn.functional as F
 import torch.utils.checkpoint
 
+from .. import _hip
 from ..kernels.RMSENorm import RMSENorm
 from .dsalt_attention import DSALTAttention
 
 
 class SwiGLUFFN(nn.Module):
-    """``down_proj(silu(gate_proj(x)) * up_proj(x))`` (dsalt_transformer.py:10-21)."""
+    """``down_proj(silu(gate_proj(x)) * up_proj(x))`` (dsalt_transformer.py:10-21). Without
+    autograd, on the GPU, the gated product is one HIP pass (``dsalt_swiglu``) with torch's
+    roundings, instead of torch's silu and product passes."""
 
     def __init__(self, d_model: int, d_ff: int, dropout: float = 0.0):
         super().__init__()
@@ -28,8 +31,11 @@ class SwiGLUFFN(nn.Module):
         self.drop = nn.Dropout(dropout)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        h = F.silu(self.gate_proj(x))
-        h = h * self.up_proj(x)
+        g, u = self.gate_proj(x), self.up_proj(x)
+        if not torch.is_grad_enabled() and _hip.swiglu_supported(g, u):
+            h = _hip.swiglu(g, u)  # one pass, the same bits as the two torch ops below
+        else:
+            h = F.silu(g) * u
         return self.drop(self.down_proj(h))
 
 

@@ -378,6 +378,17 @@ int dsalt_rope_check(const dsalt_rope_args *args);
 int dsalt_quantize_windows(const float *w_cont, int64_t n, float *w_out, int32_t *w_int_out,
                            void *stream);
 
+/*
+ * Gated SwiGLU product of the LM's feed-forward blocks: out = silu(gate) * up over n
+ * elements of one dtype (DSALT_DTYPE_BF16, _F16 or _F32).
+ * Replaces F.silu(gate_proj(x)) * up_proj(x) of SwiGLUFFN.forward
+ * (dsalt/modules/dsalt_transformer.py:20-21) in one pass, with torch's two roundings:
+ * silu(g) = g / (1 + exp(-g)) in fp32 rounded to the dtype, then the product in fp32
+ * rounded again (bit for bit the two torch ops). gate, up, out: contiguous, 16-byte
+ * aligned; n a multiple of 8 (16-bit) or 4 (fp32), else DSALT_ERR_UNSUPPORTED.
+ */
+int dsalt_swiglu(const void *gate, const void *up, void *out, int64_t n, int32_t dtype, void *stream);
+
 int dsalt_abi_version(void);
 const char *dsalt_last_error(void);
 /* sizeof of the argument structs as compiled into the library (ABI layout check). */

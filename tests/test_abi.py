@@ -339,3 +339,16 @@ def test_peak_probe_library_is_built_apart_from_the_abi():
     peaks = ctypes.CDLL(path)
     assert hasattr(peaks, "dsalt_bench_mfma") and hasattr(peaks, "dsalt_bench_read")
     assert not hasattr(ctypes.CDLL(hip.LIB_PATH), "dsalt_bench_mfma")
+
+
+def test_swiglu_rejects_before_launching():
+    lib = hip.lib()
+    fn = lib.dsalt_swiglu
+    assert fn(0x1000, 0x2000, 0x3000, -1, hip.DTYPE_BF16, None) == 1
+    assert fn(0x1000, 0x2000, 0x3000, 64, 9, None) == 1
+    assert fn(0x1000, 0x2000, 0x3000, 12, hip.DTYPE_BF16, None) == 2  # not a multiple of 8
+    assert fn(0x1000, 0x2000, 0x3000, 6, hip.DTYPE_F32, None) == 2    # not a multiple of 4
+    assert fn(0x1008, 0x2000, 0x3000, 64, hip.DTYPE_BF16, None) == 1  # misaligned
+    assert "aligned" in lib.dsalt_last_error().decode()
+    assert fn(0, 0x2000, 0x3000, 64, hip.DTYPE_BF16, None) == 1
+    assert fn(0, 0, 0, 0, hip.DTYPE_BF16, None) == 0  # nothing to do
