@@ -499,12 +499,13 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
     """The c2 inference forward as DSALTAttention runs it by default, in bf16 (module cast to
     bf16, _collect_last_P off, packed with cu_seqlens and its host copy): the whole
     module call, and each of its stages eager, launch costs included: q/k/v projections,
-    the window gate's GEMV, the selection (dsalt_select_hybrid: the norms pass over x and
-    the module's value projection, which also applies RoPE to k, then the selection
-    launch forming the scores, the windows from the gate logits and the top-k), the HARD
-    attention forward rotating q on load, out_proj. Beside them, not in the sum: the
-    routes the default replaces (k RoPE alone, the score kernels then the selection on
-    their scores, the torch score route)."""
+    the selection (dsalt_select_hybrid: the norms pass over x and the module's value
+    projection, which also forms the window gate's logits and applies RoPE to k, then the
+    selection launch forming the scores, the windows from the gate logits and the top-k),
+    the HARD attention forward rotating q on load, out_proj. Beside them, not in the sum:
+    the routes the default replaces (the window gate's GEMV and the selection taking its
+    logits, k RoPE alone, the score kernels then the selection on their scores, the torch
+    score route)."""
     import copy
     from dsalt import _hip
     from dsalt.kernels._sparse import sparse_attention
@@ -530,8 +531,11 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
         sc = sc.float()
         lmk = _hip.select_landmarks(sc, w, cu, kl, max_seqlen=L)
         out = sparse_attention(_hip.MODE_HARD, q, kr, v, lmk, None, w, cu, rope=(cos, sin))
+    gate_linear = (mod.win_gate.weight, mod.win_gate.bias, mod.n_min, mod.n_max)
     stages = {
         "qkv_proj": lambda: (mod.q_proj(x), mod.k_proj(x), mod.v_proj(x)),
+        "norms_gate_rope_k_and_select": lambda: _hip.select_hybrid(x, v, alpha, H, None, cu, kl, max_seqlen=L,
+                                                                   rope_k=(k, cos, sin, cu), gate_linear=gate_linear),
         "window_gate_gemv": lambda: mod.win_gate(x),
         "norms_rope_k_and_select": lambda: _hip.select_hybrid(x, v, alpha, H, None, cu, kl, max_seqlen=L,
                                                               gate=(gl, mod.n_min, mod.n_max),
@@ -546,8 +550,8 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
         "out_proj": lambda: mod._apply_out_proj(out.reshape(T, H * D)),
     }
     res = {"workload": "c2 DSALTAttention(1024, 16, 32, 512, 64) inference forward, bf16, packed 4 x 2048, "
-                       "default routes (norms pass over x and v rotating k, selection forming scores and windows "
-                       "from the gate logits, q rotated in the attention kernel)"}
+                       "default routes (norms pass over x and v forming the window gate's logits and rotating k, "
+                       "selection forming scores and windows from those logits, q rotated in the attention kernel)"}
     with torch.no_grad():
         res["module_forward_us"] = time_launches(lambda: mod(x, cu_seqlens=cu, cu_list=cu_list), steps,
                                                  warmup) * 1e3
@@ -559,8 +563,8 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
         res["module_forward_graph_us"] = time_launches(graph.replay, steps, warmup) * 1e3
         for name, fn in stages.items():
             res[name + "_us"] = time_launches(fn, steps, warmup) * 1e3
-    beside = ("module_forward_us", "module_forward_graph_us", "rope_k_alone_us", "landmark_scores_us", "landmark_scores_torch_route_us",
-              "select_topk_and_windows_us")
+    beside = ("module_forward_us", "module_forward_graph_us", "window_gate_gemv_us", "norms_rope_k_and_select_us",
+              "rope_k_alone_us", "landmark_scores_us", "landmark_scores_torch_route_us", "select_topk_and_windows_us")
     res["stages_sum_us"] = sum(v for kk, v in res.items() if kk.endswith("_us") and kk not in beside)
     return res
 
@@ -724,7 +728,7 @@ def main():
                     help="skip the config-4, dense-variant and config-5 LM measurements")
     ap.add_argument("--only-fwd", action="store_true",
                     help="time only the headline forward of --config and exit (for profiling)")
-    ap.add_argument("--only", choices=("lm", "dense", "backward", "c4", "peaks", "selection"), default=None,
+    ap.add_argument("--only", choices=("lm", "dense", "backward", "c4", "peaks", "selection", "module"), default=None,
                     help="run only that measurement and print its JSON (for profiling)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (counter calibration)")
@@ -746,6 +750,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if args.only is not None:
+        if args.only == "module":
+            print(json.dumps(measure_module_path(make_workload("c2", dev))))
+            return
         fn = {"lm": measure_lm, "dense": measure_dense, "backward": measure_backward, "c4": measure_c4,
               "peaks": measure_peaks, "selection": measure_selection}[args.only]
         print(json.dumps(fn(dev)))

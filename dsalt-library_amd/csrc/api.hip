@@ -260,6 +260,10 @@ int check_scores(const dsalt_scores_args *a, bool hybrid) {
     if (hybrid && (a->scores || a->z_x || a->z_v))
         return fail(DSALT_ERR_INVALID, "dsalt_select_hybrid writes no scores: scores, z_x and z_v must be NULL");
     if (hybrid && !a->alpha) return fail(DSALT_ERR_INVALID, "alpha must be non-NULL");
+    if (!a->gate_w && (a->gate_b || a->gate_out))
+        return fail(DSALT_ERR_INVALID, "gate_b and gate_out need gate_w");
+    if (a->gate_w && a->x_dtype == DSALT_DTYPE_F32)
+        return fail(DSALT_ERR_UNSUPPORTED, "the window-gate logit needs 16-bit x (x_dtype BF16 or F16)");
     if (a->total_len == 0) return DSALT_OK;
     if (!a->x || !a->v || !a->alpha || (!a->scores && !hybrid))
         return fail(DSALT_ERR_INVALID, "x, v, alpha and scores must be non-NULL");
@@ -292,6 +296,11 @@ int check_scores(const dsalt_scores_args *a, bool hybrid) {
                         ev);
         if (!aligned(a->rope_cos, 16) || !aligned(a->rope_sin, 16) || a->rope_stride % 4)
             return fail(DSALT_ERR_INVALID, "rope tables must be 16-byte aligned with a row stride multiple of 4");
+    }
+    if (a->gate_w) {
+        if (!a->gate_out) return fail(DSALT_ERR_INVALID, "gate_w needs gate_out");
+        if (!aligned(a->gate_w, 16) || !aligned(a->gate_out, 2) || !aligned(a->gate_b, 2))
+            return fail(DSALT_ERR_INVALID, "gate_w must be 16-byte aligned, gate_b and gate_out 2-byte aligned");
     }
     return DSALT_OK;
 }

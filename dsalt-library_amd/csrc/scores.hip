@@ -20,7 +20,10 @@
 //     fp32 operation order (no FMA contraction).
 // With k given, norms_kernel also applies RoPE to the token's k row (dsalt_rope's
 // arithmetic, rotary.h): the module's k rotation rides on the pass that reads x and v
-// anyway instead of taking a launch of its own.
+// anyway instead of taking a launch of its own. With gate_w given (16-bit x), it also
+// forms the window gate's logit x_t . w + b (win_gate, dsalt_attention.py:270-276) from
+// the x chunks it loads: fp32 products and sums in a fixed order, the bias added, one
+// rounding to x's dtype; this replaces the module's GEMV and its bias copy.
 #include "common.h"
 #include "launch.h"
 #include "hybrid.h"
@@ -49,13 +52,16 @@ struct ScoreParams {
     const float *cos, *sin;
     const int32_t *cu;
     int rows, S;
+    // optional window-gate logit: x_t . gate_w + gate_b[0], rounded to x's dtype
+    const void *gate_w, *gate_b;
+    void *gate_out;
 };
 
 // Element loads and the dtype rounding of a norm, per storage type.
 struct LdBF16 {
     static constexpr int E = 8;  // elements per 16 bytes
-    static __device__ __forceinline__ float sumsq16(const void *p) {
-        const uint4 u = *reinterpret_cast<const uint4 *>(p);
+    static __device__ __forceinline__ float sumsq16(const void *p) { return sumsq(*reinterpret_cast<const uint4 *>(p)); }
+    static __device__ __forceinline__ float sumsq(const uint4 u) {
         const uint32_t w[4] = {u.x, u.y, u.z, u.w};
         float s = 0.f;
 #pragma unroll
@@ -73,11 +79,28 @@ struct LdBF16 {
         u += 0x7fffu + ((u >> 16) & 1u);
         return __uint_as_float(u & 0xffff0000u);
     }
+    // acc + the 8 products of a chunk with the gate weights, in element order (each
+    // product of two 16-bit values is exact in fp32)
+    static __device__ __forceinline__ float dot(const uint4 x, const uint4 g, float acc) {
+        const uint32_t a[4] = {x.x, x.y, x.z, x.w}, b[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc = fmaf(__uint_as_float(a[i] << 16), __uint_as_float(b[i] << 16), acc);
+            acc = fmaf(__uint_as_float(a[i] & 0xffff0000u), __uint_as_float(b[i] & 0xffff0000u), acc);
+        }
+        return acc;
+    }
+    static __device__ __forceinline__ float ld1(const void *p) {
+        return __uint_as_float((uint32_t)*static_cast<const uint16_t *>(p) << 16);
+    }
+    static __device__ __forceinline__ void st1(void *p, float rounded) {
+        *static_cast<uint16_t *>(p) = (uint16_t)(__float_as_uint(rounded) >> 16);
+    }
 };
 struct LdF16 {
     static constexpr int E = 8;
-    static __device__ __forceinline__ float sumsq16(const void *p) {
-        const uint4 u = *reinterpret_cast<const uint4 *>(p);
+    static __device__ __forceinline__ float sumsq16(const void *p) { return sumsq(*reinterpret_cast<const uint4 *>(p)); }
+    static __device__ __forceinline__ float sumsq(const uint4 u) {
         const uint32_t w[4] = {u.x, u.y, u.z, u.w};
         float s = 0.f;
 #pragma unroll
@@ -89,6 +112,17 @@ struct LdF16 {
         return s;
     }
     static __device__ __forceinline__ float round(float x) { return (float)(_Float16)x; }
+    static __device__ __forceinline__ float dot(const uint4 x, const uint4 g, float acc) {
+        const uint32_t a[4] = {x.x, x.y, x.z, x.w}, b[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc = fmaf(F16::lo_f32(a[i]), F16::lo_f32(b[i]), acc);
+            acc = fmaf(F16::hi_f32(a[i]), F16::hi_f32(b[i]), acc);
+        }
+        return acc;
+    }
+    static __device__ __forceinline__ float ld1(const void *p) { return (float)*static_cast<const _Float16 *>(p); }
+    static __device__ __forceinline__ void st1(void *p, float rounded) { *static_cast<_Float16 *>(p) = (_Float16)rounded; }
 };
 struct LdF32 {
     static constexpr int E = 4;
@@ -130,7 +164,30 @@ __global__ void __launch_bounds__(64 * kNormTokens) norms_kernel(const ScorePara
         // ||x_t||: lanes stride the row in 16-byte chunks
         const char *xr = static_cast<const char *>(p.x) + (int64_t)t * p.x_st * BX;
         float sx = 0.f;
-        for (int c = lane * EX; c < p.d; c += 64 * EX) sx += LX::sumsq16(xr + (int64_t)c * BX);
+        if constexpr (EX == 8) {
+            if (p.gate_w) {
+                // the window gate's logit from the same chunks: each lane sums its chunks'
+                // products in order, then the lanes' sums are added by a fixed butterfly
+                const char *gw = static_cast<const char *>(p.gate_w);
+                float gd = 0.f;
+                for (int c = lane * EX; c < p.d; c += 64 * EX) {
+                    const uint4 xv = *reinterpret_cast<const uint4 *>(xr + (int64_t)c * BX);
+                    sx += LX::sumsq(xv);
+                    gd = LX::dot(xv, *reinterpret_cast<const uint4 *>(gw + (int64_t)c * BX), gd);
+                }
+                gd = group_sum(gd, 64);
+                if (lane == 0) {
+                    float logit = p.gate_b ? gd + LX::ld1(p.gate_b) : gd;
+                    // rounded to fp32 first: no mixed-precision fold of the sum and the conversion
+                    asm volatile("" : "+v"(logit));
+                    LX::st1(static_cast<char *>(p.gate_out) + (int64_t)t * BX, LX::round(logit));
+                }
+            } else {
+                for (int c = lane * EX; c < p.d; c += 64 * EX) sx += LX::sumsq16(xr + (int64_t)c * BX);
+            }
+        } else {
+            for (int c = lane * EX; c < p.d; c += 64 * EX) sx += LX::sumsq16(xr + (int64_t)c * BX);
+        }
         sx = group_sum(sx, 64);
         const float xn = p.norms_f32 ? sqrtf(sx) : LX::round(sqrtf(sx));
         if (lane == 0) {
@@ -287,6 +344,9 @@ ScoreParams make_params(const dsalt_scores_args &a) {
     p.cu = a.cu_seqlens;
     p.rows = a.rope_rows;
     p.S = a.num_seqs;
+    p.gate_w = a.gate_w;
+    p.gate_b = a.gate_b;
+    p.gate_out = a.gate_out;
     return p;
 }
 

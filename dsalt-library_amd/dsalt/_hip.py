@@ -25,7 +25,7 @@ DTYPE_BF16 = 0
 DTYPE_F16 = 1
 DTYPE_F32 = 2
 MAX_K_LMK = 1024
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _DTYPES = {torch.bfloat16: DTYPE_BF16, torch.float16: DTYPE_F16}
 
@@ -112,6 +112,7 @@ class ScoresArgs(ctypes.Structure):
         ("rope_cos", c_void_p), ("rope_sin", c_void_p), ("rope_stride", c_int64),
         ("rope_rows", c_int32), ("num_seqs", c_int32),
         ("cu_seqlens", c_void_p),
+        ("gate_w", c_void_p), ("gate_b", c_void_p), ("gate_out", c_void_p),
     ]
 
 
@@ -712,16 +713,32 @@ def _window_source(w_cont, gate):
 
 def select_hybrid(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int,
                   w_cont: torch.Tensor | None, cu_seqlens: torch.Tensor, k_lmk: int, chunked: bool = True,
-                  max_seqlen: int | None = None, gate=None, norms_f32: bool | None = None, rope_k=None):
+                  max_seqlen: int | None = None, gate=None, norms_f32: bool | None = None, rope_k=None,
+                  gate_linear=None):
     """hybrid_scores followed by select_landmarks_quantize in two launches
     (dsalt_select_hybrid): the selection forms each score from the norms pass's outputs
     instead of reading a [T, H] score tensor, with the same bits. Arguments as for those
     two calls; returns (w [T] fp32 quantised windows, landmark positions [H, S, k],
-    rotated k or None when rope_k is None)."""
+    rotated k or None when rope_k is None). ``gate_linear = (weight, bias, n_min, n_max)``
+    (the window gate's [1, d] weight and [1] bias or None, in x's 16-bit dtype) forms the
+    gate's logits in the norms pass (dsalt_scores_args.gate_w) instead of taking them
+    from ``gate``; the windows then come from those logits as with ``gate``."""
     f = SelectHybridLauncher(x, v, alpha, n_heads, w_cont, cu_seqlens, k_lmk, chunked, max_seqlen, gate, norms_f32,
-                             rope_k)
+                             rope_k, gate_linear)
     f()
     return f.w_out, f.out, f.k_out
+
+
+def gate_linear_supported(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> bool:
+    """Whether the norms pass can form win_gate(x) = x @ weight.T + bias for these operands:
+    16-bit x, weight [1, d] (or [d]) and bias [1] (or None) in x's dtype, weight contiguous
+    and 16-byte aligned."""
+    if x.dtype not in (torch.bfloat16, torch.float16) or x.dim() != 2:
+        return False
+    w = weight.reshape(-1) if weight.dim() == 2 and weight.shape[0] == 1 else weight
+    if w.dim() != 1 or w.shape[0] != x.shape[1] or w.dtype != x.dtype or w.stride(0) != 1 or w.data_ptr() % 16:
+        return False
+    return bias is None or (bias.dtype == x.dtype and bias.numel() == 1)
 
 
 class SelectHybridLauncher:
@@ -731,22 +748,41 @@ class SelectHybridLauncher:
 
     def __init__(self, x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads: int,
                  w_cont: torch.Tensor | None, cu_seqlens: torch.Tensor, k_lmk: int, chunked: bool = True,
-                 max_seqlen: int | None = None, gate=None, norms_f32: bool | None = None, rope_k=None):
+                 max_seqlen: int | None = None, gate=None, norms_f32: bool | None = None, rope_k=None,
+                 gate_linear=None):
         if norms_f32 is None:
             norms_f32 = autocast_norms()
-        self.device = require_gpu(x, v, alpha, cu_seqlens, w_cont if gate is None else gate[0])
+        if gate_linear is not None and (gate is not None or w_cont is not None):
+            raise DsaltError("gate_linear replaces gate and w_cont: pass neither with it")
+        self.device = require_gpu(x, v, alpha, cu_seqlens,
+                                  gate_linear[0] if gate_linear is not None else w_cont if gate is None else gate[0])
         x, v, alpha = _score_operands(x, v, alpha, n_heads)
         cu = _cu_i32(cu_seqlens)
-        w_cont, gate = _window_source(w_cont, gate)
         T = x.shape[0]
+        self.logit = None  # the window gate's logits [T] when gate_linear forms them
+        keep_g = None
+        if gate_linear is not None:
+            weight, bias, n_min, n_max = gate_linear
+            if not gate_linear_supported(x, weight, bias):
+                raise DsaltError(f"gate_linear needs 16-bit x with a contiguous, 16-byte aligned [1, d] weight and a "
+                                 f"[1] bias (or None) of x's dtype (x {x.dtype}, weight {weight.dtype} "
+                                 f"{tuple(weight.shape)})")
+            self.logit = torch.empty(T, device=self.device, dtype=x.dtype)
+            gate = (self.logit, n_min, n_max)
+            keep_g = (weight, bias)
+        w_cont, gate = _window_source(w_cont, gate)
         ws = torch.empty((scores_workspace_size(T, v.shape[1]),), device=self.device, dtype=torch.uint8)
         self._sa = scores_args(x, v, alpha, n_heads, None, None, None, ws, norms_f32)
+        if keep_g is not None:
+            self._sa.gate_w = keep_g[0].data_ptr()
+            self._sa.gate_b = _ptr(keep_g[1])
+            self._sa.gate_out = self.logit.data_ptr()
         self.k_out, keep_k = _rope_k_args(self._sa, v, rope_k)
         self.out = torch.empty((n_heads, cu.shape[0] - 1, k_lmk), device=self.device, dtype=torch.int64)
         self.w_out = torch.empty(T, device=self.device, dtype=torch.float32)
         self._a, keep_s = _select_args(None, w_cont, cu, k_lmk, self.out, chunked, max_seqlen, self.w_out, gate,
                                        shape=(T, n_heads))
-        self._keep = (x, v, alpha, cu, ws, keep_k, keep_s)
+        self._keep = (x, v, alpha, cu, ws, keep_k, keep_s, keep_g)
         self._refs = (ctypes.byref(self._sa), ctypes.byref(self._a))
         self._fn = lib().dsalt_select_hybrid
 

@@ -67,12 +67,18 @@ class DSALTAttention(nn.Module):
     route's, set for set, but a near-tie could move. ``_hip_scores = False`` keeps torch's own norm
     and standardisation ops on v, whose fp32 scores are bit-identical to the reference's
     route. The differentiable landmark weights of training always use the torch ops.
+    ``_fuse_gate`` (default True): on that route's inference path, with 16-bit x and
+    ``win_gate`` parameters of x's dtype, the norms pass also forms the window gate's
+    logits (an fp32 dot product in its own fixed order, rounded once) instead of torch's
+    GEMV; a logit can then differ from torch's in its last bit and move a window by one
+    key - the windows of configs 2 and 5 are torch's, token for token.
     ``_last_selection`` holds the ``(windows, landmark positions)`` of the last forward.
     """
 
     _fused_selector = True
     _hip_scores = True
     _fuse_rope_k = True  # inference: k rotated by the selection's norms pass (when that route is taken)
+    _fuse_gate = True    # inference: the window gate's logits formed by the same norms pass
 
     def __init__(
         self,
@@ -330,12 +336,20 @@ class DSALTAttention(nn.Module):
         # the windows are formed from the gate's logits and quantised by the selection
         # launch itself (same values as _window_sizes(floor=True) followed by
         # _compute_landmark_indices)
-        with torch.no_grad():
-            logit = self.win_gate(x).squeeze(-1)
-            # 16-bit logits: the launch forms the windows (torch's fp32 sigmoid is not
-            # reproduced bit for bit, so fp32 logits take torch's window ops)
-            gate = (logit, self.n_min, self.n_max) if logit.dtype in (torch.bfloat16, torch.float16) else None
-            w_cont = None if gate is not None else self.n_min + torch.sigmoid(logit) * (self.n_max - self.n_min)
+        gate_linear = None
+        if fuse_k and self._fuse_gate and _hip.gate_linear_supported(x, self.win_gate.weight, self.win_gate.bias):
+            # the norms pass forms the gate's logits: no GEMV
+            bias = self.win_gate.bias
+            gate_linear = (self.win_gate.weight.detach(), None if bias is None else bias.detach(), self.n_min,
+                           self.n_max)
+            gate = w_cont = None
+        else:
+            with torch.no_grad():
+                logit = self.win_gate(x).squeeze(-1)
+                # 16-bit logits: the launch forms the windows (torch's fp32 sigmoid is not
+                # reproduced bit for bit, so fp32 logits take torch's window ops)
+                gate = (logit, self.n_min, self.n_max) if logit.dtype in (torch.bfloat16, torch.float16) else None
+                w_cont = None if gate is not None else self.n_min + torch.sigmoid(logit) * (self.n_max - self.n_min)
         if fuse_k:
             # two launches: the norms pass (which also rotates k), then the selection,
             # which forms the scores, the windows and the top-k
@@ -344,7 +358,8 @@ class DSALTAttention(nn.Module):
                                                            default=0)
                 w_sizes, lmk_indices, k = _hip.select_hybrid(
                     x.detach(), v_sel.detach(), alpha.detach().float(), self.n_heads, w_cont, cu_seqlens, self.k_lmk,
-                    max_seqlen=max_len, gate=gate, rope_k=(k, *self._rope_tables(), cu_seqlens))
+                    max_seqlen=max_len, gate=gate, rope_k=(k, *self._rope_tables(), cu_seqlens),
+                    gate_linear=gate_linear)
         else:
             with torch.no_grad():
                 w_sizes, lmk_indices = _landmarks_and_windows(

@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define DSALT_ABI_VERSION 2
+#define DSALT_ABI_VERSION 3
 
 enum {
     DSALT_OK = 0,
@@ -311,6 +311,16 @@ typedef struct dsalt_scores_args {
     int64_t rope_stride;
     int32_t rope_rows, num_seqs;
     const int32_t *cu_seqlens;
+    /* Optional: the window gate's logit in the same pass, which replaces the GEMV of
+     * DSALTAttention._window_continuous (win_gate(x), dsalt/modules/dsalt_attention.py:
+     * 270-276): gate_out[t] = x_t . gate_w + gate_b[0], the products summed in fp32 in a
+     * fixed order (per lane over its 16-byte chunks, then a butterfly over the 64 lanes),
+     * the bias added, rounded once to x_dtype. 16-bit x only. gate_w [d_model] and gate_b
+     * [1] in x_dtype, 16-byte aligned (gate_b may be NULL: no bias); gate_out [T]
+     * contiguous in x_dtype, e.g. the w_logit of the selection that follows.
+     * gate_w = NULL: no logit (gate_b and gate_out must then be NULL). */
+    const void *gate_w, *gate_b;
+    void *gate_out;
 } dsalt_scores_args;
 
 int64_t dsalt_scores_workspace_size(int32_t total_len, int32_t n_kv_heads);

@@ -249,6 +249,25 @@ def test_scores_check_fp32_and_gqa():
     assert lib.dsalt_scores_check(ctypes.byref(_scores_args(n_kv_heads=256, n_heads=256))) == 2
 
 
+def test_scores_check_gate_fields():
+    """The window-gate logit of the norms pass: 16-bit x only, weights 16-byte aligned, an
+    output with every gate, and neither bias nor output without weights."""
+    lib = hip.lib()
+    gate = dict(gate_w=0x60000, gate_b=0x70000, gate_out=0x80000)
+    assert lib.dsalt_scores_check(ctypes.byref(_scores_args(**gate))) == 0
+    assert lib.dsalt_scores_check(ctypes.byref(_scores_args(**dict(gate, gate_b=0)))) == 0  # no bias
+    assert lib.dsalt_scores_check(ctypes.byref(_scores_args(**dict(gate, x_dtype=hip.DTYPE_F16)))) == 0
+    for kw, code, needle in ((dict(gate, x_dtype=hip.DTYPE_F32), 2, "16-bit x"),
+                             (dict(gate, gate_out=0), 1, "gate_out"),
+                             (dict(gate, gate_w=0x60008), 1, "16-byte aligned"),
+                             (dict(gate, gate_out=0x80001), 1, "2-byte aligned"),
+                             (dict(gate_b=0x70000), 1, "need gate_w"),
+                             (dict(gate_out=0x80000), 1, "need gate_w"),
+                             (dict(gate, x_dtype=hip.DTYPE_F32, total_len=0), 2, "16-bit x")):
+        assert lib.dsalt_scores_check(ctypes.byref(_scores_args(**kw))) == code, kw
+        assert needle in lib.dsalt_last_error().decode()
+
+
 def test_rope_check():
     lib = hip.lib()
     a = hip.RopeArgs()

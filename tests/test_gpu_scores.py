@@ -10,9 +10,12 @@ fraction of such tokens instead of requiring equality. Under autocast torch keep
 norms in fp32 (``norms_f32``), and the kernel matches the float64 oracle to fp32
 rounding again.
 
-The module's default selection route does not use this kernel: it applies torch's own
-norm ops to v, which is bit-identical to the reference's x @ W_V.T route
-(tests/test_gpu_headline.py)."""
+The module's default inference selection takes this route in two launches
+(dsalt_select_hybrid: the norms pass, which also rotates k and can form the window
+gate's logits, then the selection forming the scores); its landmark sets equal the
+reference's x @ W_V.T route at configs 2 to 4 (tests/test_gpu_headline.py)."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -212,3 +215,63 @@ def test_select_hybrid_equals_scores_then_select(case):
             assert k_got is None
     if case == "one-token-nan-std":
         assert bool((lmk_got == -1).all())  # a NaN score is never a landmark
+
+
+def _ulp(r: torch.Tensor, dtype) -> torch.Tensor:
+    """Spacing of the 16-bit values around each float64 value r."""
+    mant, emin = (7, -126) if dtype == torch.bfloat16 else (10, -14)
+    e = torch.floor(torch.log2(r.abs().clamp(min=2.0 ** (emin - mant)))).clamp(min=emin)
+    return torch.exp2(e - mant)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("lens,d,bias", [([2048] * 4, 1024, True), ([300, 1, 777], 512, False),
+                                         ([5000], 2048, True)], ids=["c2-shape", "ragged-no-bias", "long"])
+def test_select_hybrid_window_gate_in_norms_pass(dtype, lens, d, bias):
+    """The window gate's logits formed by the norms pass (gate_linear): each is x.w + b
+    rounded once to the dtype from an fp32 sum, so it lies within half an ulp of the exact
+    (float64) value plus the fp32 summation bound, and equals the correctly rounded value in
+    all but a few tokens; the windows and landmark sets are those the selection forms from
+    the same logits passed as `gate`, bit for bit; against torch's GEMV (win_gate), the
+    logits differ in at most 0.5 % of the tokens, by one ulp."""
+    from dsalt.kernels.window_utils import build_rope_cache
+    print(f"gate in norms pass {dtype} lens={lens[:3]} d={d}", flush=True)
+    g = torch.Generator().manual_seed(d + len(lens))
+    H, n_kv, D, k_lmk, n_min, n_max = 16, 16, 64, 64, 32.0, 512.0
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=DEV)
+    T = int(cu[-1])
+    x = torch.randn(T, d, generator=g).to(DEV, dtype)
+    v = torch.randn(T, n_kv, D, generator=g).to(DEV, dtype)
+    k = torch.randn(T, n_kv, D, generator=g).to(DEV, dtype)
+    alpha = torch.rand(H, generator=g).to(DEV)
+    # nn.Linear(d, 1)'s initialisation range, scaled up so that the logits span the sigmoid
+    lin = torch.nn.Linear(d, 1).to(DEV, dtype)
+    with torch.no_grad():
+        lin.weight.copy_(((torch.rand(1, d, generator=g) * 2 - 1) * 4 / math.sqrt(d)).to(DEV, dtype))
+        lin.bias.copy_(torch.tensor([0.3]).to(DEV, dtype))
+    b = lin.bias if bias else None
+    cos, sin = build_rope_cache(max(lens) + 1, D, DEV)
+    f = _hip.SelectHybridLauncher(x, v, alpha, H, None, cu, k_lmk, gate_linear=(lin.weight, b, n_min, n_max),
+                                  rope_k=(k, cos, sin, cu))
+    f()
+    with torch.no_grad():
+        torch_logit = torch.nn.functional.linear(x, lin.weight, b).squeeze(-1)
+    torch.cuda.synchronize()
+    got = f.logit.double()
+    exact = x.double() @ lin.weight.double()[0] + (b.double() if bias else 0.0)
+    bound = 0.5 * _ulp(exact, dtype) + (d + 1) * 2.0 ** -24 * ((x.double().abs() @ lin.weight.double().abs()[0]) +
+                                                                (b.double().abs() if bias else 0.0))
+    assert bool(((got - exact).abs() <= bound).all()), "a logit is farther from x.w + b than its rounding allows"
+    rounded = exact.float().to(dtype).double()
+    off = int((got != rounded).sum())
+    print(f"  {off}/{T} logits differ from the correctly rounded value", flush=True)
+    assert off <= max(1, T // 500)
+    n_torch = int((f.logit != torch_logit).sum())
+    print(f"  {n_torch}/{T} logits differ from torch's GEMV", flush=True)
+    assert n_torch <= max(2, T // 200)
+    assert bool(((f.logit.double() - torch_logit.double()).abs() <= _ulp(torch_logit.double(), dtype)).all())
+    # the selection on those logits, given explicitly
+    w_ref, lmk_ref, k_ref = _hip.select_hybrid(x, v, alpha, H, None, cu, k_lmk, gate=(f.logit.clone(), n_min, n_max),
+                                               rope_k=(k, cos, sin, cu))
+    torch.cuda.synchronize()
+    assert torch.equal(f.w_out, w_ref) and torch.equal(f.out, lmk_ref) and torch.equal(f.k_out, k_ref)
