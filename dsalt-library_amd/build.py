@@ -38,7 +38,7 @@ HIPCC_FLAGS = [
 # operation contractible). -ffp-contract=fast lets the backend fuse any multiply-add, among
 # them the range reduction inside the device library's expf (x*log2e - round(x*log2e)
 # becomes one fma), which changes exp's last bit against torch's build.
-TORCH_ROUNDING_SOURCES = {"swiglu.hip"}
+TORCH_ROUNDING_SOURCES = {"swiglu.hip", "rmsnorm.hip"}
 
 
 def flags_for(src: str) -> list[str]:

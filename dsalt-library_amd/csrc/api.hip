@@ -348,6 +348,27 @@ int dsalt_swiglu(const void *gate, const void *up, void *out, int64_t n, int32_t
     return DSALT_OK;
 }
 
+int dsalt_add_rms_norm(const void *x, const void *h, void *x_out, void *y, const void *weight, int64_t rows,
+                       int32_t d, float eps, int32_t dtype, void *stream) {
+    if (rows < 0) return fail(DSALT_ERR_INVALID, "rows must be >= 0 (got %lld)", (long long)rows);
+    if (dtype != DSALT_DTYPE_BF16 && dtype != DSALT_DTYPE_F16)
+        return fail(DSALT_ERR_INVALID, "dtype must be DSALT_DTYPE_BF16 or _F16 (got %d)", dtype);
+    if (d < 8 || d % 8 || d > dsalt::rms_norm_max_dim())
+        return fail(DSALT_ERR_UNSUPPORTED, "d must be a multiple of 8 in [8, %d] (got %d)", dsalt::rms_norm_max_dim(), d);
+    if (!(eps >= 0.f)) return fail(DSALT_ERR_INVALID, "eps must be >= 0");
+    if (h && !x_out) return fail(DSALT_ERR_INVALID, "h needs x_out");
+    if (rows == 0) return DSALT_OK;
+    if (!x || !y || !weight) return fail(DSALT_ERR_INVALID, "x, y and weight must be non-NULL");
+    if (!aligned(x, 16) || !aligned(h, 16) || !aligned(x_out, 16) || !aligned(y, 16) || !aligned(weight, 16))
+        return fail(DSALT_ERR_INVALID, "x, h, x_out, y and weight must be 16-byte aligned");
+    if (y == x || y == h || (h && y == x_out))
+        return fail(DSALT_ERR_INVALID, "y must not alias x, h or x_out");
+    hipError_t e = dsalt::launch_add_rms_norm(x, h, h ? x_out : nullptr, y, weight, rows, d, eps, dtype,
+                                              static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(DSALT_ERR_LAUNCH, "dsalt_add_rms_norm launch failed: %s", hipGetErrorString(e));
+    return DSALT_OK;
+}
+
 int dsalt_rope_check(const dsalt_rope_args *a) {
     if (!a) return fail(DSALT_ERR_INVALID, "args is NULL");
     if (a->total_len < 0 || a->n_q_heads < 0 || a->n_k_heads < 0)

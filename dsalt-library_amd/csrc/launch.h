@@ -48,6 +48,9 @@ int scores_max_kv();
 hipError_t launch_quantize(const float *w_cont, int64_t n, float *w_out, int32_t *w_int,
                            hipStream_t stream);
 hipError_t launch_swiglu(const void *gate, const void *up, void *out, int64_t n, int dtype, hipStream_t stream);
+hipError_t launch_add_rms_norm(const void *x, const void *h, void *x_out, void *y, const void *weight, int64_t rows,
+                               int d, float eps, int dtype, hipStream_t stream);
+int rms_norm_max_dim();
 
 // Number of query blocks of `bm` tokens over a packed batch, as an upper bound that is
 // computable without reading cu_seqlens: sum_s ceil(L_s/bm) <= ceil(T/bm) + S.

@@ -136,6 +136,7 @@ EXPORTED_SYMBOLS = (
     "dsalt_select_args_size", "dsalt_hybrid_scores", "dsalt_scores_check", "dsalt_scores_workspace_size",
     "dsalt_scores_args_size", "dsalt_rope", "dsalt_rope_check", "dsalt_rope_args_size",
     "dsalt_bwd_noalloc", "dsalt_select_workspace_size", "dsalt_select_hybrid", "dsalt_swiglu",
+    "dsalt_add_rms_norm",
 )
 NOALLOC_SCRATCH_BYTES = 76 << 20  # DSALT_NOALLOC_SCRATCH_BYTES
 SELECT_SPLIT_MIN = 4096  # longer sequences can be selected chunk-wise
@@ -168,6 +169,8 @@ def lib() -> ctypes.CDLL:
         ("dsalt_rope_check", [ctypes.POINTER(RopeArgs)]),
         ("dsalt_quantize_windows", [c_void_p, c_int64, c_void_p, c_void_p, c_void_p]),
         ("dsalt_swiglu", [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p]),
+        ("dsalt_add_rms_norm", [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_float, c_int32,
+                                c_void_p]),
     ):
         fn = getattr(h, name)
         fn.argtypes = argtypes
@@ -1053,3 +1056,39 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     _raise(lib().dsalt_swiglu(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(),
                               _SCORE_DTYPES[gate.dtype], stream_handle(dev)), "dsalt_swiglu")
     return out
+
+
+RMS_NORM_MAX_DIM = 4096  # largest row length of dsalt_add_rms_norm
+
+
+def add_rms_norm_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Whether dsalt_add_rms_norm takes rows of x [..., d] with this weight [d]: a GPU
+    tensor in bf16 or fp16, contiguous and 16-byte aligned, d a multiple of 8 up to 4096,
+    the weight of the same dtype, contiguous and aligned."""
+    if x.device.type != "cuda" or x.dtype not in (torch.bfloat16, torch.float16) or x.dim() < 1:
+        return False
+    d = x.shape[-1]
+    if not (8 <= d <= RMS_NORM_MAX_DIM and d % 8 == 0 and x.is_contiguous() and x.data_ptr() % 16 == 0):
+        return False
+    return (weight.device == x.device and weight.dtype == x.dtype and weight.shape == (d,) and weight.is_contiguous()
+            and weight.data_ptr() % 16 == 0)
+
+
+def add_rms_norm(x: torch.Tensor, h: torch.Tensor | None, weight: torch.Tensor, eps: float):
+    """``x_out = x + h`` (torch's add, bit for bit) and ``y = F.rms_norm(x_out, (d,), weight,
+    eps)`` in one HIP pass over the rows (no autograd); h = None normalises x alone.
+    Returns (x_out, y), x_out None without h. y can differ from F.rms_norm in an output's
+    last bit (the sum of squares runs in another order)."""
+    dev = require_gpu(x, weight, h)
+    if not add_rms_norm_supported(x, weight) or (h is not None and (h.shape != x.shape or h.dtype != x.dtype or
+                                                                    not h.is_contiguous() or h.data_ptr() % 16)):
+        raise DsaltError(f"dsalt_add_rms_norm needs contiguous, 16-byte aligned bf16/fp16 rows of d = 8k <= "
+                         f"{RMS_NORM_MAX_DIM} with a weight [d] of the same dtype (got x {tuple(x.shape)} {x.dtype}, "
+                         f"weight {tuple(weight.shape)} {weight.dtype})")
+    d = x.shape[-1]
+    x_out = torch.empty_like(x) if h is not None else None
+    y = torch.empty_like(x)
+    _raise(lib().dsalt_add_rms_norm(x.data_ptr(), _ptr(h), _ptr(x_out), y.data_ptr(), weight.data_ptr(),
+                                    x.numel() // d, d, float(eps), _SCORE_DTYPES[x.dtype], stream_handle(dev)),
+           "dsalt_add_rms_norm")
+    return x_out, y

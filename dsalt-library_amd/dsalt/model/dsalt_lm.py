@@ -24,6 +24,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .. import _hip
 from ..kernels.RMSENorm import RMSENorm
 from ..modules.dsalt_transformer import DSALTTransformerBlock
 
@@ -112,6 +113,14 @@ class DSALTLMHeadModel(nn.Module):
             max_seqlen = input_ids.shape[-1]
         x = self._to_autocast_dtype(self.embed_dropout(self.embed_tokens(input_ids)))
         cu_list = None if cu_seqlens is None else cu_seqlens.detach().cpu().tolist()
+        if labels is None and self._norms_fusable(x):
+            # inference: each residual add runs in the pass of the norm that follows it
+            delta = None
+            for layer in self.layers:
+                x, delta, _ = layer._forward_fused(x, delta, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen,
+                                                   cu_list=cu_list)
+            _, x = _hip.add_rms_norm(x, delta, self.final_norm.weight, self.final_norm.eps)
+            return {"loss": None, "logits": self.lm_head(x), "aux_loss": None}
         aux = torch.zeros((), device=input_ids.device, dtype=x.dtype)
         for layer in self.layers:
             x, a = layer(x, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen,
@@ -124,6 +133,14 @@ class DSALTLMHeadModel(nn.Module):
         loss = _chunked_cross_entropy(x.reshape(-1, self.d_model), self.lm_head.weight,
                                       labels.reshape(-1).long(), self.lm_head_chunk_size)
         return {"loss": loss + self.aux_loss_weight * aux, "logits": None, "aux_loss": aux.detach()}
+
+    def _norms_fusable(self, x: torch.Tensor) -> bool:
+        """Whether every residual add and norm of the forward can run as dsalt_add_rms_norm
+        passes (inference without autograd, 16-bit rows, norm weights of x's dtype)."""
+        if not self.layers or not _hip.add_rms_norm_supported(x, self.final_norm.weight):
+            return False
+        return all(layer._norms_fusable(x, None, layer.attn_norm) and layer._norms_fusable(x, None, layer.ffn_norm)
+                   for layer in self.layers)
 
     def num_parameters(self, trainable_only: bool = True) -> int:
         return sum(p.numel() for p in self.parameters() if p.requires_grad or not trainable_only)

@@ -42,7 +42,12 @@ class SwiGLUFFN(nn.Module):
 class DSALTTransformerBlock(nn.Module):
     """RMSNorm -> DSALTAttention -> residual, RMSNorm -> SwiGLU -> residual
     (dsalt_transformer.py:24-88); ``gradient_checkpointing`` recomputes the attention and
-    the FFN in the backward when training."""
+    the FFN in the backward when training. ``_fuse_norms`` (default True): at inference
+    without autograd, with 16-bit rows, a residual add and the norm after it run as one
+    HIP pass (``dsalt_add_rms_norm``: the sum is torch's add bit for bit, the norm can
+    differ from F.rms_norm in an output's last bit)."""
+
+    _fuse_norms = True
 
     def __init__(self, d_model: int, n_heads: int, n_min: int, n_max: int, k_lmk: int, max_seq_len: int,
                  d_ff: int, dropout: float = 0.0, yarn_scale: float = 1.0, layer_idx: int = 0,
@@ -69,7 +74,38 @@ class DSALTTransformerBlock(nn.Module):
 
         recompute = gradient_checkpointing and self.training
         h = self.attn_norm(x)
-        x = x + (torch.utils.checkpoint.checkpoint(attend, h, use_reentrant=False) if recompute else attend(h))
-        h = self.ffn_norm(x)
+        x_attn = torch.utils.checkpoint.checkpoint(attend, h, use_reentrant=False) if recompute else attend(h)
+        if self._norms_fusable(x, x_attn, self.ffn_norm):
+            # the residual add and the FFN's norm in one HIP pass (inference)
+            x, h = _hip.add_rms_norm(x, x_attn, self.ffn_norm.weight, self.ffn_norm.eps)
+        else:
+            x = x + x_attn
+            h = self.ffn_norm(x)
         x = x + (torch.utils.checkpoint.checkpoint(self.ffn, h, use_reentrant=False) if recompute else self.ffn(h))
         return x, aux_box[0]
+
+    def _norms_fusable(self, x: torch.Tensor, h: torch.Tensor | None, norm: nn.Module) -> bool:
+        """Whether x (+ h) and the RMSENorm `norm` can run as one dsalt_add_rms_norm pass:
+        inference without autograd, 16-bit rows on the GPU, a weight of x's dtype."""
+        if self.training or torch.is_grad_enabled() or not self._fuse_norms:
+            return False
+        if h is not None and (h.shape != x.shape or h.dtype != x.dtype or not h.is_contiguous()):
+            return False
+        return _hip.add_rms_norm_supported(x, norm.weight)
+
+    def _forward_fused(self, x: torch.Tensor, delta: torch.Tensor | None, cu_seqlens=None, max_seqlen=None,
+                       rope_cs=None, cu_list=None):
+        """Inference forward that leaves its last residual add to the caller: returns
+        (x + attention, the FFN output, aux), so that the next block's norm (or the final
+        norm) takes that add in its own pass. `delta` is the previous block's pending FFN
+        output (None for the first block). The caller checks `_norms_fusable` first."""
+        x_sum, h = _hip.add_rms_norm(x, delta, self.attn_norm.weight, self.attn_norm.eps)
+        if x_sum is not None:
+            x = x_sum
+        x_attn, aux = self.attn(h, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen, rope_cs=rope_cs, cu_list=cu_list)
+        if self._norms_fusable(x, x_attn, self.ffn_norm):
+            x, h = _hip.add_rms_norm(x, x_attn, self.ffn_norm.weight, self.ffn_norm.eps)
+        else:
+            x = x + x_attn
+            h = self.ffn_norm(x)
+        return x, self.ffn(h), aux

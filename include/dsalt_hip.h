@@ -399,6 +399,23 @@ int dsalt_quantize_windows(const float *w_cont, int64_t n, float *w_out, int32_t
  */
 int dsalt_swiglu(const void *gate, const void *up, void *out, int64_t n, int32_t dtype, void *stream);
 
+/*
+ * Residual add and RMSNorm of the LM's pre-norm blocks in one pass, per row of d elements:
+ * x_out = x + h (each sum in fp32 rounded to the dtype, as torch's add), then
+ * y = (x_out * rstd) * weight with rstd = rsqrt(sum(x_out^2) / d + eps) in fp32, rounded
+ * to the dtype. h = NULL: y = RMSNorm(x) alone (x_out not written, may be NULL).
+ * Replaces x = x + x_attn / x = x + x_ffn followed by the next RMSENorm
+ * (dsalt/modules/dsalt_transformer.py:81-84; RMSENorm.forward, dsalt/kernels/RMSENorm.py:
+ * 21-23) and the LM's final norm (dsalt/model/dsalt_lm.py:273). The sum of squares runs in
+ * this pass's fixed order, so an output can differ from F.rms_norm's in its last bit
+ * (a few in 10^6 in the tests); x_out is torch's sum exactly.
+ * dtype BF16 or F16 for x, h, x_out, y and weight [d]; rows contiguous with row stride d;
+ * d a multiple of 8, at most 4096; 16-byte aligned pointers; x_out may alias x or h, y
+ * may alias none of them.
+ */
+int dsalt_add_rms_norm(const void *x, const void *h, void *x_out, void *y, const void *weight, int64_t rows,
+                       int32_t d, float eps, int32_t dtype, void *stream);
+
 int dsalt_abi_version(void);
 const char *dsalt_last_error(void);
 /* sizeof of the argument structs as compiled into the library (ABI layout check). */

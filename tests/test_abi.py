@@ -371,3 +371,23 @@ def test_swiglu_rejects_before_launching():
     assert "aligned" in lib.dsalt_last_error().decode()
     assert fn(0, 0x2000, 0x3000, 64, hip.DTYPE_BF16, None) == 1
     assert fn(0, 0, 0, 0, hip.DTYPE_BF16, None) == 0  # nothing to do
+
+
+def test_add_rms_norm_rejects_before_launching():
+    lib = hip.lib()
+    fn = lib.dsalt_add_rms_norm
+    x, h, xo, y, w = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
+    bf = hip.DTYPE_BF16
+    for args, code, needle in (((x, h, xo, y, w, -1, 1024, 1e-6, bf), 1, "rows"),
+                               ((x, h, xo, y, w, 4, 1024, 1e-6, hip.DTYPE_F32), 1, "dtype"),
+                               ((x, h, xo, y, w, 4, 12, 1e-6, bf), 2, "multiple of 8"),
+                               ((x, h, xo, y, w, 4, 8192, 1e-6, bf), 2, "4096"),
+                               ((x, h, xo, y, w, 4, 1024, -1.0, bf), 1, "eps"),
+                               ((x, h, 0, y, w, 4, 1024, 1e-6, bf), 1, "x_out"),
+                               ((x, h, xo, 0, w, 4, 1024, 1e-6, bf), 1, "non-NULL"),
+                               ((x + 8, h, xo, y, w, 4, 1024, 1e-6, bf), 1, "aligned"),
+                               ((x, h, xo, x, w, 4, 1024, 1e-6, bf), 1, "alias"),
+                               ((x, h, xo, xo, w, 4, 1024, 1e-6, bf), 1, "alias")):
+        assert fn(*args, None) == code, args
+        assert needle in lib.dsalt_last_error().decode(), (args, lib.dsalt_last_error())
+    assert fn(0, 0, 0, 0, 0, 0, 1024, 1e-6, bf, None) == 0  # no rows: nothing to do
