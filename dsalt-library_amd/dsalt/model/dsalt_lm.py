@@ -15,6 +15,11 @@ the host copy of cu_seqlens is taken once per forward and shared by every layer.
 ``labels`` gives the mean token cross-entropy (ignore index -100), computed over
 ``lm_head_chunk_size``-token chunks so that at most [chunk, vocab] logits exist at once.
 The Triton-only "liger" loss is not available (as in the reference without Triton).
+
+Inference without autograd in bf16/fp16 runs every residual add in the pass of the
+RMSNorm after it (dsalt_add_rms_norm: each block hands its FFN output to the next
+block's norm, the last one to the final norm); the FFN's gated product and the window
+gate run as HIP passes too (SwiGLUFFN, DSALTAttention).
 """
 from __future__ import annotations
 
