@@ -48,3 +48,36 @@ def test_hard_pairs(seed):
 def test_soft_pairs(seed):
     w, pos, cu, H = _case(seed, soft=True)
     assert bench.effective_pairs_soft(w, pos, cu) == orc.effective_pairs("soft", w, pos, cu, H)
+
+
+@pytest.mark.parametrize("mode", ["hard", "soft"])
+@pytest.mark.parametrize("seed", range(4))
+def test_pair_counts_equal_the_attention_masks(mode, seed, monkeypatch):
+    """The counted pairs are the pairs the oracle's attention actually admits: wrap the
+    oracle's per-sequence softmax, record the band and landmark masks that
+    attention_hard / attention_soft build (NaN and sub-1 windows, holes and out-of-range
+    landmark slots included) and count their entries, one per head and landmark slot."""
+    import torch
+    w, pos, cu, H = _case(seed, soft=mode == "soft")
+    T, k = int(cu[-1]), pos.shape[-1]
+    g = torch.Generator().manual_seed(seed)
+    q, kk, v = (torch.randn(T, H, 4, generator=g, dtype=torch.float64) for _ in range(3))
+    counted = [0]
+    inner = orc._seq_attention
+
+    def recording(qs, ks, vs, band_bias, band_ok, lk, lv, lmk_logit_bias, lmk_ok, scale):
+        counted[0] += int(band_ok.sum()) * qs.shape[0]  # band_ok [R, L] is shared by the heads
+        if lmk_ok is not None:
+            counted[0] += int(lmk_ok.sum())  # [H, R, k]: one entry per admitted slot
+        return inner(qs, ks, vs, band_bias, band_ok, lk, lv, lmk_logit_bias, lmk_ok, scale)
+
+    monkeypatch.setattr(orc, "_seq_attention", recording)
+    pos_t = torch.from_numpy(pos)
+    if mode == "hard":
+        orc.attention_hard(q, kk, v, torch.from_numpy(w), pos_t, None, cu)
+        want = bench.effective_pairs_hard(w, pos, cu)
+    else:
+        logw = torch.zeros(pos.shape, dtype=torch.float64)  # finite weights: every valid slot counts
+        orc.attention_soft(q, kk, v, torch.from_numpy(w), pos_t, logw, cu)
+        want = bench.effective_pairs_soft(w, pos, cu)
+    assert counted[0] == want == orc.effective_pairs(mode, w, pos, cu, H)
