@@ -19,7 +19,16 @@ path. It restates, on the CPU, the reference algorithm of LeonardoCofone/dsalt-l
                          (dsalt/modules/dsalt_attention.py:286-329, :371-438): soft window
                          tail on every causal key, landmarks admitted at d >= max(1, floor(w~)),
                          union = elementwise max of the two log-biases
+  rope, seq_positions    dsalt/kernels/window_utils.py:73-88 as dsalt_attention.py:570-585
+                         calls it (positions inside each packed sequence)
+  hybrid_scores_from_v   hybrid_scores on the module's value projection v = x W_V^T
+  module_train_forward   the packed training forward of DSALTAttention (dsalt_attention.py:
+                         440-487, :565-609): projections, RoPE, SOFT selectors, attention
+  module_eval_forward    the packed inference forward (dsalt_attention.py:610-625): the
+                         same projections and RoPE, floor windows, top-k, HARD attention
   module_batched_forward dsalt_attention.py:371-401 (B = 1) from the module parameters
+  effective_pairs,       the pair counts of F = 4 D P (band keys plus admitted landmark
+  hard_mask              slots) and the dense HARD mask
   lm_forward             DSALTLMHeadModel eval logits (dsalt/model/dsalt_lm.py:237-280):
                          embedding, pre-norm blocks (RMSNorm, attention, SwiGLU), final
                          RMSNorm, tied head; lm_train_loss the packed training loss
@@ -33,7 +42,11 @@ sequence; O_i = V_i for w = 1, k = 0; the constant-landmark-bias reweighting clo
 form; the soft edge against F.logsigmoid; selection against a brute-force Python sort
 and against torch.topk as sets; scores against numpy's mean/std(ddof=1); gradients
 against finite differences (torch.autograd.gradcheck) - and the committed golden
-fixtures of tests/golden/. The reference ships no golden vectors of its own.
+fixtures of tests/golden/ (module_train_forward, module_batched_forward, lm_forward,
+lm_train_loss). module_eval_forward has no golden of its own: it composes the pinned
+pieces above with module_train_forward's golden-pinned projections and RoPE. The pair
+counts equal the entries of the masks attention_hard / attention_soft build
+(tests/test_bench_counts.py). The reference ships no golden vectors of its own.
 """
 from __future__ import annotations
 
