@@ -202,9 +202,11 @@ class DSALTAttention(nn.Module):
     # ---- forward -----------------------------------------------------------------------
     def forward(self, x: torch.Tensor, cu_seqlens: torch.Tensor | None = None,
                 max_seqlen: int | None = None, rope_cs: tuple | None = None,
-                cu_list: list | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+                cu_list: list | None = None, *, _need_aux: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+        # _need_aux=False (internal, packed path): return None instead of the zero aux loss,
+        # so that a caller that discards it launches no fill for it
         if cu_seqlens is not None:
-            return self._packed(x, cu_seqlens, x.shape[0], x.device, rope_cs, cu_list)
+            return self._packed(x, cu_seqlens, x.shape[0], x.device, rope_cs, cu_list, need_aux=_need_aux)
         B, T, _ = x.shape
         return self._batched(x, B, T, x.device)
 
@@ -293,7 +295,7 @@ class DSALTAttention(nn.Module):
         return w_cont, lmk_pos, lmk_logw
 
     def _packed(self, x: torch.Tensor, cu_seqlens: torch.Tensor, total_len: int, device: torch.device,
-                rope_cs: tuple | None = None, cu_list: list | None = None):
+                rope_cs: tuple | None = None, cu_list: list | None = None, need_aux: bool = True):
         _hip.require_gpu(x, cu_seqlens)
         q = self.q_proj(x).view(total_len, self.n_heads, self.head_dim)
         k = self.k_proj(x).view(total_len, self.n_kv_heads, self.head_dim)
@@ -322,7 +324,7 @@ class DSALTAttention(nn.Module):
         # grouped K/V heads go to the kernels as they are (query head h reads K/V head
         # h // n_rep); no repeated copy
 
-        aux = x.new_zeros(())
+        aux = x.new_zeros(()) if need_aux else None
 
         if self.training:
             self._last_P = None

@@ -96,13 +96,15 @@ class DSALTTransformerBlock(nn.Module):
     def _forward_fused(self, x: torch.Tensor, delta: torch.Tensor | None, cu_seqlens=None, max_seqlen=None,
                        rope_cs=None, cu_list=None):
         """Inference forward that leaves its last residual add to the caller: returns
-        (x + attention, the FFN output, aux), so that the next block's norm (or the final
-        norm) takes that add in its own pass. `delta` is the previous block's pending FFN
+        (x + attention, the FFN output, aux - None on the packed path, where the attention
+        makes no zero aux tensor), so that the next block's norm (or the final norm) takes
+        that add in its own pass. `delta` is the previous block's pending FFN
         output (None for the first block). The caller checks `_norms_fusable` first."""
         x_sum, h = _hip.add_rms_norm(x, delta, self.attn_norm.weight, self.attn_norm.eps)
         if x_sum is not None:
             x = x_sum
-        x_attn, aux = self.attn(h, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen, rope_cs=rope_cs, cu_list=cu_list)
+        x_attn, aux = self.attn(h, cu_seqlens=cu_seqlens, max_seqlen=max_seqlen, rope_cs=rope_cs, cu_list=cu_list,
+                                _need_aux=False)
         if self._norms_fusable(x, x_attn, self.ffn_norm):
             x, h = _hip.add_rms_norm(x, x_attn, self.ffn_norm.weight, self.ffn_norm.eps)
         else:
