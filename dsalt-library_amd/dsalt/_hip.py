@@ -734,14 +734,15 @@ def select_hybrid(x: torch.Tensor, v: torch.Tensor, alpha: torch.Tensor, n_heads
 
 def gate_linear_supported(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None) -> bool:
     """Whether the norms pass can form win_gate(x) = x @ weight.T + bias for these operands:
-    16-bit x, weight [1, d] (or [d]) and bias [1] (or None) in x's dtype, weight contiguous
-    and 16-byte aligned."""
-    if x.dtype not in (torch.bfloat16, torch.float16) or x.dim() != 2:
+    16-bit x on the GPU, weight [1, d] (or [d]) and bias [1] (or None) in x's dtype on x's
+    device, weight contiguous and 16-byte aligned."""
+    if x.dtype not in (torch.bfloat16, torch.float16) or x.dim() != 2 or x.device.type != "cuda":
         return False
     w = weight.reshape(-1) if weight.dim() == 2 and weight.shape[0] == 1 else weight
-    if w.dim() != 1 or w.shape[0] != x.shape[1] or w.dtype != x.dtype or w.stride(0) != 1 or w.data_ptr() % 16:
+    if (w.dim() != 1 or w.shape[0] != x.shape[1] or w.dtype != x.dtype or w.device != x.device or w.stride(0) != 1
+            or w.data_ptr() % 16):
         return False
-    return bias is None or (bias.dtype == x.dtype and bias.numel() == 1)
+    return bias is None or (bias.dtype == x.dtype and bias.numel() == 1 and bias.device == x.device)
 
 
 class SelectHybridLauncher:

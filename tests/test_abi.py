@@ -391,3 +391,14 @@ def test_add_rms_norm_rejects_before_launching():
         assert fn(*args, None) == code, args
         assert needle in lib.dsalt_last_error().decode(), (args, lib.dsalt_last_error())
     assert fn(0, 0, 0, 0, 0, 0, 1024, 1e-6, bf, None) == 0  # no rows: nothing to do
+
+
+def test_gate_linear_supported_rejects_cpu_operands():
+    """The window gate's operands must all live on the GPU with x: a CPU weight or bias (or
+    x) is refused before any pointer reaches the library."""
+    import torch
+    x = torch.zeros(4, 16, dtype=torch.bfloat16)
+    w = torch.zeros(1, 16, dtype=torch.bfloat16)
+    b = torch.zeros(1, dtype=torch.bfloat16)
+    assert not hip.gate_linear_supported(x, w, b)  # CPU x
+    assert not hip.gate_linear_supported(x, w, None)
