@@ -4,7 +4,7 @@
   route (the HIP score kernel over x and its own value projection v = x W_V^T) and the
   torch route on v must both pick exactly the landmark sets of the reference's route
   (x @ W_V.T, then torch's norms), per (head, sequence), for an fp32 module, a bf16
-  module and an fp32 module under bf16 autocast; the torch route on v also gives the
+  module, an fp16 module (c2) and an fp32 module under bf16 autocast; the torch route on v also gives the
   same fp32 scores bit for bit.
 * Forward parity at configs 2 and 4, HARD and SOFT, on the windows and landmarks the
   module produces (built as bench.py builds them: seed 1 / seed 3, x ~ N(0, 1)), against
@@ -39,9 +39,10 @@ def _c2_module(dtype_mode, cfg="c2"):
     mod = mod.to(DEV).eval()
     mod._collect_last_P = False
     x = x.to(DEV)
-    if dtype_mode == "bf16":
-        mod = mod.to(torch.bfloat16)
-        x = x.to(torch.bfloat16)
+    if dtype_mode in ("bf16", "fp16"):
+        dt = torch.bfloat16 if dtype_mode == "bf16" else torch.float16
+        mod = mod.to(dt)
+        x = x.to(dt)
     cu = torch.arange(0, B * L + 1, L, dtype=torch.int32, device=DEV)
     return mod, x, cu
 
@@ -54,7 +55,7 @@ def _run_route(mod, x, cu, fused, hip_scores, autocast):
     return w.clone(), lmk.clone()
 
 
-@pytest.mark.parametrize("cfg,dtype_mode", [("c2", "fp32"), ("c2", "bf16"), ("c2", "autocast"),
+@pytest.mark.parametrize("cfg,dtype_mode", [("c2", "fp32"), ("c2", "bf16"), ("c2", "fp16"), ("c2", "autocast"),
                                             ("c4", "bf16"), ("c4", "autocast")])
 def test_default_selection_equals_gemm_route(cfg, dtype_mode):
     print(f"{cfg} selection routes {dtype_mode}", flush=True)
