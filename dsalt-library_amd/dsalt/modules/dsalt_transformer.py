@@ -3,8 +3,9 @@
 The LM consumer of the attention path: x + attn(norm(x)), then x + ffn(norm(x)), with a
 SwiGLU feed-forward. Parameter names and creation order follow the reference
 (attn_norm, ffn_norm, attn, ffn; gate_proj, up_proj, down_proj) so state dicts load and
-seeded initialisations agree. Only the attention runs on the HIP kernels; the norms,
-projections and FFN are torch (hipBLASLt GEMMs).
+seeded initialisations agree. The attention runs on the HIP kernels; the projections are
+torch (hipBLASLt GEMMs). Without autograd on the GPU, the FFN's gated product and each
+residual add with the norm after it are HIP passes too; with autograd they are torch ops.
 """
 from __future__ import annotations
 
@@ -89,7 +90,8 @@ class DSALTTransformerBlock(nn.Module):
         inference without autograd, 16-bit rows on the GPU, a weight of x's dtype."""
         if self.training or torch.is_grad_enabled() or not self._fuse_norms:
             return False
-        if h is not None and (h.shape != x.shape or h.dtype != x.dtype or not h.is_contiguous()):
+        if h is not None and (h.shape != x.shape or h.dtype != x.dtype or not h.is_contiguous()
+                              or h.data_ptr() % 16):
             return False
         return _hip.add_rms_norm_supported(x, norm.weight)
 

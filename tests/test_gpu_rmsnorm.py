@@ -91,3 +91,20 @@ def test_lm_fused_norms_against_unfused():
     rel = float((fused - plain).norm() / plain.norm())
     print(f"  fused vs unfused logits rel-L2 {rel:.2e}", flush=True)
     assert torch.isfinite(fused).all() and rel < 2e-2
+
+
+def test_block_declines_unaligned_residual():
+    """A residual that is contiguous but not 16-byte aligned turns the block's fused pass
+    off (torch's add and norm run), rather than reaching the C ABI, which rejects it."""
+    from dsalt.modules.dsalt_transformer import DSALTTransformerBlock
+    with torch.device(DEV):
+        block = DSALTTransformerBlock(256, 4, 16, 128, 16, 512, 512)
+    block = block.to(DEV, torch.bfloat16).eval()
+    x = torch.randn(10, 256, device=DEV, dtype=torch.bfloat16)
+    h = torch.randn(10 * 256 + 1, device=DEV, dtype=torch.bfloat16)[1:].view(10, 256)
+    assert h.is_contiguous() and h.data_ptr() % 16
+    with torch.no_grad():
+        assert block._norms_fusable(x, h.clone(), block.ffn_norm)
+        assert not block._norms_fusable(x, h, block.ffn_norm)
+        with pytest.raises(_hip.DsaltError):
+            _hip.add_rms_norm(x, h, block.ffn_norm.weight, block.ffn_norm.eps)
