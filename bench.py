@@ -507,14 +507,14 @@ def measure_peaks(device: torch.device) -> dict:
 def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
     """The c2 inference forward as DSALTAttention runs it by default, in bf16 (module cast to
     bf16, _collect_last_P off, packed with cu_seqlens and its host copy): the whole
-    module call, and each of its stages eager, launch costs included: q/k/v projections,
-    the selection (dsalt_select_hybrid: the norms pass over x and the module's value
+    module call, and each of its stages eager, launch costs included: the q/k/v projections
+    (one GEMM over the concatenated weights, as the module runs them), the selection (dsalt_select_hybrid: the norms pass over x and the module's value
     projection, which also forms the window gate's logits and applies RoPE to k, then the
     selection launch forming the scores, the windows from the gate logits and the top-k),
     the HARD attention forward rotating q on load, out_proj. Beside them, not in the sum:
-    the routes the default replaces (the window gate's GEMV and the selection taking its
-    logits, k RoPE alone, the score kernels then the selection on their scores, the torch
-    score route)."""
+    the routes the default replaces (three separate projection GEMMs, the window gate's GEMV
+    and the selection taking its logits, k RoPE alone, the score kernels then the selection
+    on their scores, the torch score route)."""
     import copy
     from dsalt import _hip
     from dsalt.kernels._sparse import sparse_attention
@@ -529,9 +529,7 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
     cu_list = cu.tolist()
     cos, sin = mod.rope_cos, mod.rope_sin
     with torch.no_grad():
-        q = mod.q_proj(x).view(T, H, D)
-        k = mod.k_proj(x).view(T, H, D)
-        v = mod.v_proj(x).view(T, H, D)
+        q, k, v = (t.view(T, H, D) for t in mod._project_qkv(x))
         kr = rotate_packed(k, cos, sin, cu)
         w = mod._window_sizes(x, floor=True)
         gl = mod.win_gate(x).squeeze(-1)
@@ -542,7 +540,8 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
         out = sparse_attention(_hip.MODE_HARD, q, kr, v, lmk, None, w, cu, rope=(cos, sin))
     gate_linear = (mod.win_gate.weight, mod.win_gate.bias, mod.n_min, mod.n_max)
     stages = {
-        "qkv_proj": lambda: (mod.q_proj(x), mod.k_proj(x), mod.v_proj(x)),
+        "qkv_proj": lambda: mod._project_qkv(x),
+        "qkv_proj_separate": lambda: (mod.q_proj(x), mod.k_proj(x), mod.v_proj(x)),
         "norms_gate_rope_k_and_select": lambda: _hip.select_hybrid(x, v, alpha, H, None, cu, kl, max_seqlen=L,
                                                                    rope_k=(k, cos, sin, cu), gate_linear=gate_linear),
         "window_gate_gemv": lambda: mod.win_gate(x),
@@ -572,7 +571,8 @@ def measure_module_path(wl, steps: int = 50, warmup: int = 10) -> dict:
         res["module_forward_graph_us"] = time_launches(graph.replay, steps, warmup) * 1e3
         for name, fn in stages.items():
             res[name + "_us"] = time_launches(fn, steps, warmup) * 1e3
-    beside = ("module_forward_us", "module_forward_graph_us", "window_gate_gemv_us", "norms_rope_k_and_select_us",
+    beside = ("module_forward_us", "module_forward_graph_us", "qkv_proj_separate_us", "window_gate_gemv_us",
+              "norms_rope_k_and_select_us",
               "rope_k_alone_us", "landmark_scores_us", "landmark_scores_torch_route_us", "select_topk_and_windows_us")
     res["stages_sum_us"] = sum(v for kk, v in res.items() if kk.endswith("_us") and kk not in beside)
     return res

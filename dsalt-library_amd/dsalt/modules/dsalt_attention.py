@@ -35,6 +35,7 @@ import math
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from .. import _hip
 from ..kernels._dense import dense_attention, dense_probabilities
@@ -72,6 +73,12 @@ class DSALTAttention(nn.Module):
     logits (an fp32 dot product in its own fixed order, rounded once) instead of torch's
     GEMV; a logit can then differ from torch's in its last bit and move a window by one
     key - the windows of configs 2 and 5 are torch's, token for token.
+    ``_fuse_qkv`` (default True): at inference without autograd or autocast, without
+    projection biases, q, k and v come from one GEMM against the three weights concatenated
+    (cached until a weight changes; one extra copy of them in device memory) and are column
+    views of its output - the kernels take their strides as they are. At configs 2 and 5 the
+    columns equal the three separate projections bit for bit (hipBLASLt runs the same
+    reduction order), and the one GEMM of 3x the width fills more of the chip.
     ``_last_selection`` holds the ``(windows, landmark positions)`` of the last forward.
     """
 
@@ -79,6 +86,7 @@ class DSALTAttention(nn.Module):
     _hip_scores = True
     _fuse_rope_k = True  # inference: k rotated by the selection's norms pass (when that route is taken)
     _fuse_gate = True    # inference: the window gate's logits formed by the same norms pass
+    _fuse_qkv = True     # inference: q, k and v from one GEMM over the concatenated weights
 
     def __init__(
         self,
@@ -133,6 +141,24 @@ class DSALTAttention(nn.Module):
         self.register_buffer("rope_sin", sin, persistent=False)
 
     # ---- small pieces (dsalt_attention.py:243-284) ---------------------------------------
+    def _project_qkv(self, x: torch.Tensor):
+        """``(q_proj(x), k_proj(x), v_proj(x))`` as [T, d_model], [T, kv_dim], [T, kv_dim]; with
+        ``_fuse_qkv`` at inference one GEMM whose output columns the three are views of."""
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
+        if not (self._fuse_qkv and not self.training and not torch.is_grad_enabled() and x.is_cuda
+                and not torch.is_autocast_enabled() and self.q_proj.bias is None and self.k_proj.bias is None
+                and self.v_proj.bias is None and all(w.dtype == x.dtype and w.device == x.device for w in ws)
+                and self.d_model % 8 == 0 and self.kv_dim % 8 == 0):
+            return self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
+        cache = getattr(self, "_qkv_weight_cache", None)
+        if cache is None or cache[0] != key:
+            cache = (key, torch.cat([w.detach() for w in ws], 0))
+            self._qkv_weight_cache = cache
+        qkv = F.linear(x, cache[1])
+        d, kv = self.d_model, self.kv_dim
+        return qkv[:, :d], qkv[:, d:d + kv], qkv[:, d + kv:]
+
     def _alpha(self) -> torch.Tensor:
         return torch.sigmoid(self.alpha_w)
 
@@ -297,9 +323,10 @@ class DSALTAttention(nn.Module):
     def _packed(self, x: torch.Tensor, cu_seqlens: torch.Tensor, total_len: int, device: torch.device,
                 rope_cs: tuple | None = None, cu_list: list | None = None, need_aux: bool = True):
         _hip.require_gpu(x, cu_seqlens)
-        q = self.q_proj(x).view(total_len, self.n_heads, self.head_dim)
-        k = self.k_proj(x).view(total_len, self.n_kv_heads, self.head_dim)
-        v = self.v_proj(x).view(total_len, self.n_kv_heads, self.head_dim)
+        q, k, v = self._project_qkv(x)
+        q = q.view(total_len, self.n_heads, self.head_dim)
+        k = k.view(total_len, self.n_kv_heads, self.head_dim)
+        v = v.view(total_len, self.n_kv_heads, self.head_dim)
         # x W_V^T before RoPE and the kv repeat: the selector's value norms come from it
         # (only without a projection bias, where v is exactly x W_V^T)
         v_sel = v if self.v_proj.bias is None else None

@@ -128,3 +128,57 @@ def test_module_bf16_autocast_train_step():
     for name, p in mod.named_parameters():
         assert p.grad is not None and torch.isfinite(p.grad).all(), name
     assert mod.win_gate.weight.grad.abs().sum() > 0 and mod.alpha_w.grad.abs().sum() > 0
+
+
+@pytest.mark.parametrize("T", [8192, 16384], ids=["c2", "c5"])
+def test_fused_qkv_projection_equals_separate_at_headline_shapes(T):
+    """At inference the module forms q, k and v with one GEMM over the concatenated weights
+    (_fuse_qkv). At the d_model 1024 / 16-head shapes of configs 2 and 5 its columns are
+    the three separate projections bit for bit, and so is the module's whole output."""
+    print(f"fused qkv T={T}", flush=True)
+    torch.manual_seed(11)
+    mod = DSALTAttention(1024, 16, 32, 512, 64, 2048).to(DEV, torch.bfloat16).eval()
+    mod._collect_last_P = False
+    x = torch.randn(T, 1024, device=DEV).to(torch.bfloat16)
+    L = 2048
+    cu = torch.arange(0, T + 1, L, dtype=torch.int32, device=DEV)
+    with torch.no_grad():
+        q, k, v = mod._project_qkv(x)
+        assert q.data_ptr() + 1024 * 2 == k.data_ptr() and q.stride(0) == 3 * 1024  # one GEMM's columns
+        assert torch.equal(q, mod.q_proj(x)) and torch.equal(k, mod.k_proj(x)) and torch.equal(v, mod.v_proj(x))
+        fused, _ = mod(x, cu_seqlens=cu, cu_list=cu.tolist())
+        try:
+            DSALTAttention._fuse_qkv = False
+            plain, _ = mod(x, cu_seqlens=cu, cu_list=cu.tolist())
+        finally:
+            DSALTAttention._fuse_qkv = True
+    torch.cuda.synchronize()
+    assert torch.equal(fused, plain)
+
+
+def test_fused_qkv_projection_gqa_and_weight_updates():
+    """The fused projection with grouped K/V heads (kv_dim < d_model) against the separate
+    projections, before and after an in-place weight update (the cached concatenation is
+    rebuilt), and the module's output with and without it."""
+    print("fused qkv GQA", flush=True)
+    torch.manual_seed(12)
+    mod = DSALTAttention(512, 8, 16, 128, 16, 1024, n_kv_heads=2).to(DEV, torch.bfloat16).eval()
+    mod._collect_last_P = False
+    x = torch.randn(700, 512, device=DEV).to(torch.bfloat16)
+    cu = torch.tensor([0, 300, 700], dtype=torch.int32, device=DEV)
+    with torch.no_grad():
+        for step in range(2):
+            q, k, v = mod._project_qkv(x)
+            assert q.shape == (700, 512) and k.shape == (700, 128) and v.shape == (700, 128)
+            for got, lin in ((q, mod.q_proj), (k, mod.k_proj), (v, mod.v_proj)):
+                torch.testing.assert_close(got.float(), lin(x).float(), rtol=1e-2, atol=1e-2)
+            mod.k_proj.weight.mul_(1.5)  # in place: the next call must see it
+        fused, _ = mod(x, cu_seqlens=cu, cu_list=cu.tolist())
+        try:
+            DSALTAttention._fuse_qkv = False
+            plain, _ = mod(x, cu_seqlens=cu, cu_list=cu.tolist())
+        finally:
+            DSALTAttention._fuse_qkv = True
+    torch.cuda.synchronize()
+    rel = float((fused.float() - plain.float()).norm() / plain.float().norm())
+    assert rel < 1e-2, rel
