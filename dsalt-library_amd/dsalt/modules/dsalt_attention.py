@@ -78,7 +78,10 @@ class DSALTAttention(nn.Module):
     (cached until a weight changes; one extra copy of them in device memory) and are column
     views of its output - the kernels take their strides as they are. At configs 2 and 5 the
     columns equal the three separate projections bit for bit (hipBLASLt runs the same
-    reduction order), and the one GEMM of 3x the width fills more of the chip.
+    reduction order), and the one GEMM of 3x the width fills more of the chip. The cache
+    follows each weight's pointer and version counter: in-place updates (optimizer steps,
+    ``load_state_dict``, ``copy_`` under no_grad) are seen, but a change made through
+    ``weight.data`` does not bump the counter - call ``invalidate_qkv_cache()`` after one.
     ``_last_selection`` holds the ``(windows, landmark positions)`` of the last forward.
     """
 
@@ -141,6 +144,10 @@ class DSALTAttention(nn.Module):
         self.register_buffer("rope_sin", sin, persistent=False)
 
     # ---- small pieces (dsalt_attention.py:243-284) ---------------------------------------
+    def invalidate_qkv_cache(self) -> None:
+        """Drop the cached concatenation of the q/k/v weights (``_fuse_qkv``)."""
+        self._qkv_weight_cache = None
+
     def _project_qkv(self, x: torch.Tensor):
         """``(q_proj(x), k_proj(x), v_proj(x))`` as [T, d_model], [T, kv_dim], [T, kv_dim]; with
         ``_fuse_qkv`` at inference one GEMM whose output columns the three are views of."""

@@ -173,6 +173,10 @@ def test_fused_qkv_projection_gqa_and_weight_updates():
             for got, lin in ((q, mod.q_proj), (k, mod.k_proj), (v, mod.v_proj)):
                 torch.testing.assert_close(got.float(), lin(x).float(), rtol=1e-2, atol=1e-2)
             mod.k_proj.weight.mul_(1.5)  # in place: the next call must see it
+        mod.v_proj.weight.data.mul_(0.5)  # through .data: no version bump, so invalidate
+        mod.invalidate_qkv_cache()
+        _, _, v = mod._project_qkv(x)
+        torch.testing.assert_close(v.float(), mod.v_proj(x).float(), rtol=1e-2, atol=1e-2)  # stale: 2x off
         fused, _ = mod(x, cu_seqlens=cu, cu_list=cu.tolist())
         try:
             DSALTAttention._fuse_qkv = False
