@@ -74,7 +74,8 @@ class DSALTAttention(nn.Module):
     GEMV; a logit can then differ from torch's in its last bit and move a window by one
     key - the windows of configs 2 and 5 are torch's, token for token.
     ``_fuse_qkv`` (default True): at inference without autograd or autocast, without
-    projection biases, q, k and v come from one GEMM against the three weights concatenated
+    projection biases and with ``_hip_scores`` (the reference-exact score route keeps the
+    separate projections), q, k and v come from one GEMM against the three weights concatenated
     (cached until a weight changes; one extra copy of them in device memory) and are column
     views of its output - the kernels take their strides as they are. At configs 2 and 5 the
     columns equal the three separate projections bit for bit (hipBLASLt runs the same
@@ -152,7 +153,7 @@ class DSALTAttention(nn.Module):
         """``(q_proj(x), k_proj(x), v_proj(x))`` as [T, d_model], [T, kv_dim], [T, kv_dim]; with
         ``_fuse_qkv`` at inference one GEMM whose output columns the three are views of."""
         ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
-        if not (self._fuse_qkv and not self.training and not torch.is_grad_enabled() and x.is_cuda
+        if not (self._fuse_qkv and self._hip_scores and not self.training and not torch.is_grad_enabled() and x.is_cuda
                 and not torch.is_autocast_enabled() and self.q_proj.bias is None and self.k_proj.bias is None
                 and self.v_proj.bias is None and all(w.dtype == x.dtype and w.device == x.device for w in ws)
                 and self.d_model % 8 == 0 and self.kv_dim % 8 == 0):
