@@ -38,29 +38,41 @@ __device__ __forceinline__ float opaque(float v) {
     return v;
 }
 
-template <typename DT, bool ADD>
+// NCH: 16-byte chunks per lane (d <= 512 NCH). Every load of the row (x, h and the
+// weight chunks) is issued before any arithmetic; the arithmetic order is that of one
+// chunk after the other.
+template <typename DT, bool ADD, int NCH>
 __global__ void __launch_bounds__(64 * kRowsPerBlock) add_rms_norm_kernel(const RmsParams p) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     if (row >= p.rows) return;  // wave-uniform
     const int64_t base = row * p.nch;
     // chunk c of the lane holds elements (64 c + lane) * 8 .. + 7 (coalesced per chunk)
-    uint4 s[kMaxChunks];
-    float ss = 0.f;
+    uint4 s[NCH], hv[NCH], wv[NCH];
 #pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c) {
+    for (int c = 0; c < NCH; ++c) {
         const int ch = c * 64 + lane;
         if (ch < p.nch) {
-            uint4 v = p.x[base + ch];
+            s[c] = p.x[base + ch];
+            if constexpr (ADD) hv[c] = p.h[base + ch];
+            wv[c] = p.w[ch];
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int ch = c * 64 + lane;
+        if (ch < p.nch) {
+            uint4 v = s[c];
             if constexpr (ADD) {
-                const uint4 hv = p.h[base + ch];
-                const uint32_t a[4] = {v.x, v.y, v.z, v.w}, b[4] = {hv.x, hv.y, hv.z, hv.w};
+                const uint32_t a[4] = {v.x, v.y, v.z, v.w}, b[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
                 uint32_t o[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     o[e] = DT::pack2(opaque(DT::lo_f32(a[e]) + DT::lo_f32(b[e])),
                                      opaque(DT::hi_f32(a[e]) + DT::hi_f32(b[e])));
                 v = make_uint4(o[0], o[1], o[2], o[3]);
+                p.x_out[base + ch] = v;
             }
             s[c] = v;
             const uint32_t a[4] = {v.x, v.y, v.z, v.w};
@@ -75,12 +87,11 @@ __global__ void __launch_bounds__(64 * kRowsPerBlock) add_rms_norm_kernel(const 
     ss = wave_sumf(ss);
     const float rstd = rsqrtf(ss / p.d + p.eps);
 #pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c) {
+    for (int c = 0; c < NCH; ++c) {
         const int ch = c * 64 + lane;
         if (ch < p.nch) {
-            const uint4 v = s[c], wv = p.w[ch];
-            if constexpr (ADD) p.x_out[base + ch] = v;
-            const uint32_t a[4] = {v.x, v.y, v.z, v.w}, b[4] = {wv.x, wv.y, wv.z, wv.w};
+            const uint4 v = s[c];
+            const uint32_t a[4] = {v.x, v.y, v.z, v.w}, b[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
             uint32_t o[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -91,11 +102,23 @@ __global__ void __launch_bounds__(64 * kRowsPerBlock) add_rms_norm_kernel(const 
     }
 }
 
+template <typename DT, bool ADD>
+void launch_add(const RmsParams &p, const dim3 grid, const dim3 block, hipStream_t stream) {
+    if (p.nch <= 64)
+        hipLaunchKernelGGL((add_rms_norm_kernel<DT, ADD, 1>), grid, block, 0, stream, p);
+    else if (p.nch <= 128)
+        hipLaunchKernelGGL((add_rms_norm_kernel<DT, ADD, 2>), grid, block, 0, stream, p);
+    else if (p.nch <= 256)
+        hipLaunchKernelGGL((add_rms_norm_kernel<DT, ADD, 4>), grid, block, 0, stream, p);
+    else
+        hipLaunchKernelGGL((add_rms_norm_kernel<DT, ADD, kMaxChunks>), grid, block, 0, stream, p);
+}
+
 template <typename DT>
 void launch_dt(const RmsParams &p, bool add, hipStream_t stream) {
     const dim3 grid((unsigned)((p.rows + kRowsPerBlock - 1) / kRowsPerBlock)), block(64 * kRowsPerBlock);
-    if (add) hipLaunchKernelGGL((add_rms_norm_kernel<DT, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((add_rms_norm_kernel<DT, false>), grid, block, 0, stream, p);
+    if (add) launch_add<DT, true>(p, grid, block, stream);
+    else launch_add<DT, false>(p, grid, block, stream);
 }
 
 }  // namespace
